@@ -1,0 +1,197 @@
+/*
+ * qa_hip.h -- C ABI of libqa_hip.so, the MI355X (gfx950) integer inference
+ * library for QuantAnything's quantized Conv / Gemm / MatMul path.
+ *
+ * Part 1 replaces, symbol for symbol, the C ABI that QuantAnything's loader
+ * binds through ctypes (reference: quantization/native.py:104-128, selected
+ * with QA_LIB at native.py:137). Signatures, argument meaning and results are
+ * those of quantization/kernels/qa_kernels.cpp; results are bit-identical.
+ * These entries take host (or device) pointers, run on the GPU and return
+ * when the output is written. Like the reference they return void; a failure
+ * is reported through qa_last_error() and printed to stderr once.
+ *
+ * Part 2 is additional surface the reference's loader ignores: backend
+ * identification and errors, weight packing, and device-pointer entries used
+ * by the device-resident executor (asynchronous on a caller stream).
+ */
+#ifndef QA_HIP_H
+#define QA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===================== Part 1: the reference ABI (17 symbols) ========== */
+
+/* qa_kernels.cpp:233-249. The GPU library reports the compute-unit count of
+ * the current device, ignores set_num_threads and has no OpenMP. */
+int qa_num_threads(void);
+void qa_set_num_threads(int n);
+int qa_has_openmp(void);
+
+/* C[M,N] = A[M,K] B[K,N], row-major (qa_kernels.cpp:252-263). The narrow
+ * integer form sums int16 products modulo 2^32 (an int32 accumulator), the
+ * wide form int32 products in int64. */
+void qa_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A,
+                 const float* B, float* C);
+void qa_gemm_i16_i32(int64_t M, int64_t N, int64_t K, const int16_t* A,
+                     const int16_t* B, int32_t* C);
+void qa_gemm_i32_i64(int64_t M, int64_t N, int64_t K, const int32_t* A,
+                     const int32_t* B, int64_t* C);
+
+/* y[N,Cout,OH,OW] = conv(x[N,C,H,W], w[Cout,C/G,KH,KW]) with strides,
+ * top/left pads, dilations and groups; taps outside the image contribute 0
+ * (qa_kernels.cpp:273-284). The narrow form wraps activations to int16
+ * before the product, like the reference's int16 im2col buffer. */
+void qa_conv_f32(const float* x, const float* w, float* y, int64_t N,
+                 int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t KH,
+                 int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                 int64_t DH, int64_t DW, int64_t G, int64_t OH, int64_t OW);
+void qa_conv_i32_i16_i32(const int32_t* x, const int16_t* w, int32_t* y,
+                         int64_t N, int64_t C, int64_t H, int64_t W,
+                         int64_t Cout, int64_t KH, int64_t KW, int64_t SH,
+                         int64_t SW, int64_t PH, int64_t PW, int64_t DH,
+                         int64_t DW, int64_t G, int64_t OH, int64_t OW);
+void qa_conv_i32_i32_i64(const int32_t* x, const int32_t* w, int64_t* y,
+                         int64_t N, int64_t C, int64_t H, int64_t W,
+                         int64_t Cout, int64_t KH, int64_t KW, int64_t SH,
+                         int64_t SW, int64_t PH, int64_t PW, int64_t DH,
+                         int64_t DW, int64_t G, int64_t OH, int64_t OW);
+
+/* out[o,c,i] = clip(mbqm(acc + pre[c], mult[c], shift[c]) + post[c] + zp)
+ * over the [outer, C, inner] view; pre/post may be NULL
+ * (qa_kernels.cpp:287-302). mbqm(x,m,s) = round(x*m*2^-(31+s)) with a
+ * 128-bit product, rounding half up. */
+void qa_requantize_i32(const int32_t* acc, int32_t* out, int64_t outer,
+                       int64_t C, int64_t inner, const int64_t* mult,
+                       const int64_t* shift, const int64_t* pre_bias,
+                       const int64_t* post_bias, int64_t zp, int64_t qmin,
+                       int64_t qmax);
+void qa_requantize_i64(const int64_t* acc, int32_t* out, int64_t outer,
+                       int64_t C, int64_t inner, const int64_t* mult,
+                       const int64_t* shift, const int64_t* pre_bias,
+                       const int64_t* post_bias, int64_t zp, int64_t qmin,
+                       int64_t qmax);
+
+/* Element-wise integer kernels (qa_kernels.cpp:307-358). */
+void qa_rescale(const int32_t* x, int32_t* out, int64_t n, int64_t zp_in,
+                int64_t m, int64_t s, int64_t zp_out, int64_t qmin,
+                int64_t qmax);
+void qa_add(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
+            int64_t za, int64_t ma, int64_t sa, int64_t zb, int64_t mb,
+            int64_t sb, int64_t sign, int64_t zp_out, int64_t qmin,
+            int64_t qmax);
+void qa_mul(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
+            int64_t za, int64_t zb, int64_t m, int64_t s, int64_t zp_out,
+            int64_t qmin, int64_t qmax);
+void qa_lut(const int32_t* x, int32_t* out, int64_t n, int64_t offset,
+            const int32_t* lut, int64_t lut_len);
+
+/* Per-tensor float <-> integer (qa_kernels.cpp:363-386): q = clip(
+ * nearbyint(double(x)/scale) + zp), x = float(double(q - zp) * scale). */
+void qa_quantize_f32(const float* x, int32_t* q, int64_t n, double scale,
+                     int64_t zp, int64_t qmin, int64_t qmax);
+void qa_dequantize_f32(const int32_t* q, float* x, int64_t n, double scale,
+                       int64_t zp);
+
+/* ===================== Part 2: additional surface ====================== */
+/* No counterpart in the reference: its loader ignores these symbols. */
+
+const char* qa_backend(void);       /* "hip-gfx950" */
+const char* qa_last_error(void);    /* NULL when no error on this thread */
+void qa_clear_error(void);
+int qa_device_count(void);
+int qa_device_arch(char* buf, int64_t len);
+void* qa_stream(void);              /* library stream (hipStream_t) */
+int qa_synchronize(void);
+
+/* Storage codes of device tensors: 1 int8, 2 int16, 4 int32, 8 int64.
+ * A quantized value q is stored as q - so (so: storage offset). */
+
+/* Packs centred OIHW weights (w - w_zp, int32) for the int8 MFMA path:
+ * per output channel an offset b_off makes every value int8; K is laid out
+ * in 16-byte groups (tap-major, 16 input channels each) padded to 64 bytes,
+ * rows padded to a multiple of 128 per group. Writes wp (see
+ * qa_pack_weights_i8_size), corr[c] = a_off*colsum_c + K*a_off*b_off[c]
+ * and boff. Returns 0 on success, 1 when a channel spans more than 255
+ * values (use the VALU path), -1 on bad arguments; *needs_rowsum is set
+ * when some b_off is non-zero. */
+int64_t qa_pack_weights_i8_size(int64_t Cout, int64_t Cg, int64_t KH,
+                                int64_t KW, int64_t G, int64_t* kgp,
+                                int64_t* rows_per_group);
+int qa_pack_weights_i8(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
+                       int64_t KW, int64_t G, int64_t a_off, int8_t* wp,
+                       int64_t* corr, int32_t* boff, int32_t* needs_rowsum);
+
+/* Fused integer convolution / GEMM on device tensors:
+ *   acc = sum (x_stored + x_add) * w         (exact, int32 or int64)
+ *   q   = clip(mbqm(acc + pre_bias[c], mult[c], shift[c]) + zp)
+ *   q   = lut[clip(q - lut_offset)]                      (if lut)
+ *   q   = clip(mbqm(r - za) + sign*mbqm(q - zb) + add_zp) (if res; the
+ *         residual r is the first Add operand when res_first)
+ *   y   = q - y_so
+ * w_code 1: packed int8 weights (MFMA); 2/4: OIHW int16/int32 (VALU, int64
+ * accumulation when wide). rowmajor 1: x is an [N][lda] matrix (GEMM with
+ * K = C, H = W = KH = KW = 1). Pointers may be pre-offset to address channel
+ * slices; *_nstride are elements between images. */
+typedef struct qa_conv_desc {
+    const void* x;
+    int64_t x_code, x_nstride, x_add, rowmajor;
+    int64_t N, C, H, W, Cout, KH, KW, SH, SW, PH, PW, DH, DW, G, OH, OW;
+    const void* w;
+    int64_t w_code, w_kgp, w_rows, wide, needs_rowsum;
+    const int64_t* corr;
+    const int32_t* boff;
+    const int64_t* pre_bias;
+    const int64_t* mult;
+    const int64_t* shift;
+    int64_t zp, qmin, qmax;
+    const int32_t* lut;
+    int64_t lut_offset, lut_len;
+    const void* res;
+    int64_t res_nstride, res_so, res_first;
+    int64_t za, ma, sa, zb, mb, sb, add_sign, add_zp, add_qmin, add_qmax;
+    void* y;
+    int64_t y_code, y_nstride, y_so;
+} qa_conv_desc;
+
+int qa_d_conv(const qa_conv_desc* d, void* stream);
+
+/* Element-wise device entries (storage codes as above; `*_so` storage
+ * offsets; `sub` is subtracted from the accumulator before the bias). */
+int qa_d_requantize(const void* acc, int acc_code, void* out, int out_code,
+                    int64_t outer, int64_t C, int64_t inner,
+                    const int64_t* mult, const int64_t* shift,
+                    const int64_t* pre_bias, const int64_t* post_bias,
+                    int64_t zp, int64_t qmin, int64_t qmax, int64_t sub,
+                    int64_t out_so, void* stream);
+int qa_d_rescale(const void* x, int in_code, void* out, int out_code,
+                 int64_t n, int64_t zp_in, int64_t m, int64_t s,
+                 int64_t zp_out, int64_t qmin, int64_t qmax, int64_t in_so,
+                 int64_t out_so, void* stream);
+int qa_d_add(const void* a, const void* b, int in_code, void* out,
+             int out_code, int64_t n, int64_t za, int64_t ma, int64_t sa,
+             int64_t zb, int64_t mb, int64_t sb, int64_t sign, int64_t zp_out,
+             int64_t qmin, int64_t qmax, int64_t a_so, int64_t b_so,
+             int64_t out_so, void* stream);
+int qa_d_mul(const void* a, const void* b, int in_code, void* out,
+             int out_code, int64_t n, int64_t za, int64_t zb, int64_t m,
+             int64_t s, int64_t zp_out, int64_t qmin, int64_t qmax,
+             int64_t a_so, int64_t b_so, int64_t out_so, void* stream);
+int qa_d_lut(const void* x, int in_code, void* out, int out_code, int64_t n,
+             int64_t offset, const int32_t* lut, int64_t lut_len,
+             int64_t in_so, int64_t out_so, void* stream);
+int qa_d_quantize_f32(const float* x, void* q, int out_code, int64_t n,
+                      double scale, int64_t zp, int64_t qmin, int64_t qmax,
+                      int64_t out_so, void* stream);
+int qa_d_dequantize_f32(const void* q, int in_code, float* x, int64_t n,
+                        double scale, int64_t zp, int64_t in_so,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QA_HIP_H */

@@ -1,0 +1,112 @@
+// Shared definitions of the MI355X (gfx950) integer inference library.
+//
+// Conventions used by every kernel:
+//  * NCHW activations, OIHW weights, row-major GEMM operands (the layouts of
+//    the reference ABI, quantization/kernels/qa_kernels.cpp:51-185).
+//  * Device-resident quantized tensors are stored as int8 (types of <= 8
+//    bits) or int16 (9..16 bits) holding  stored = q - storage_offset,
+//    storage_offset = 0 for signed types and 2^(bits-1) for unsigned ones
+//    (uint8 q in [0,255] is stored as q-128 in [-128,127]).
+//  * Every fixed-point multiply is the reference's exact one: a 128-bit
+//    product rounded half up, right shifts clamped to 120 and left shifts to
+//    60, clamps applied to the 128-bit value (qa_kernels.cpp:188-205).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __int128 qa_i128;
+
+#define QA_API extern "C" __attribute__((visibility("default")))
+
+// ---------------------------------------------------------------- mbqm ----
+// round(x * mult * 2^-(31+shift)) with a wrapping 128-bit product.
+__host__ __device__ __forceinline__ qa_i128 qa_mbqm(int64_t x, int64_t mult,
+                                                   int64_t shift) {
+    const qa_i128 p = (qa_i128)x * (qa_i128)mult;
+    int64_t ts = 31 + shift;
+    if (ts > 0) {
+        if (ts > 120) ts = 120;
+        return (p + ((qa_i128)1 << (ts - 1))) >> ts;
+    }
+    int64_t ls = -ts;
+    if (ls > 60) ls = 60;
+    return p * ((qa_i128)1 << ls);
+}
+
+// Fast path of qa_mbqm for |x| < 2^32 and |mult| < 2^31 (the product is
+// exact in int64), which covers every 8-bit-model accumulator; falls back to
+// the 128-bit form otherwise. Bit-identical to qa_mbqm for all inputs:
+// floor((p + 2^(t-1)) / 2^t) == (p >> t) + bit (t-1) of p, with no overflow,
+// and for t >= 64 the rounded value of |p| < 2^63 is 0.
+__device__ __forceinline__ qa_i128 qa_mbqm_fast(int64_t x, int64_t mult,
+                                               int64_t shift) {
+    const uint64_t ax = x < 0 ? 0ull - (uint64_t)x : (uint64_t)x;
+    const uint64_t am = mult < 0 ? 0ull - (uint64_t)mult : (uint64_t)mult;
+    const int64_t ts = 31 + shift;
+    if ((ax >> 32) == 0 && (am >> 31) == 0 && ts > 0) {
+        if (ts >= 64) return 0;
+        const int64_t p = x * mult;
+        return (qa_i128)((p >> ts) + ((p >> (ts - 1)) & 1));
+    }
+    return qa_mbqm(x, mult, shift);
+}
+
+__host__ __device__ __forceinline__ int64_t qa_clip128(qa_i128 v, int64_t lo,
+                                                      int64_t hi) {
+    if (v < (qa_i128)lo) return lo;
+    if (v > (qa_i128)hi) return hi;
+    return (int64_t)v;
+}
+
+// --------------------------------------------------------------- errors ---
+namespace qa {
+
+// Records the first failure of the calling thread (see qa_last_error) and
+// prints it to stderr once, so that a caller that never checks still sees it.
+void set_error(const char* where, const char* what);
+void set_hip_error(const char* where, hipError_t e);
+bool ok();
+
+#define QA_HIP(call)                                        \
+    do {                                                    \
+        hipError_t qa_e_ = (call);                          \
+        if (qa_e_ != hipSuccess) {                          \
+            ::qa::set_hip_error(#call, qa_e_);              \
+            return;                                         \
+        }                                                   \
+    } while (0)
+
+#define QA_HIP_RET(call, ret)                               \
+    do {                                                    \
+        hipError_t qa_e_ = (call);                          \
+        if (qa_e_ != hipSuccess) {                          \
+            ::qa::set_hip_error(#call, qa_e_);              \
+            return ret;                                     \
+        }                                                   \
+    } while (0)
+
+// Library stream of the current device (default priority, non-blocking).
+hipStream_t stream();
+
+// A device scratch buffer of at least `bytes`, owned by the library and
+// reused across host-pointer ABI calls (which serialise on a mutex).
+void* scratch(int slot, size_t bytes);
+
+// Serialises host-pointer ABI calls (they share the scratch buffers).
+struct AbiLock {
+    AbiLock();
+    ~AbiLock();
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+inline unsigned grid_1d(int64_t n, int threads, int64_t cap = 1 << 16) {
+    int64_t g = ceil_div(n, threads);
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (unsigned)g;
+}
+
+}  // namespace qa

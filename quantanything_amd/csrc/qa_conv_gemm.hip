@@ -1,0 +1,602 @@
+// Convolution / GEMM entry points: the reference ABI (host pointers,
+// qa_kernels.cpp:233-284) and the device-resident qa_d_conv.
+//
+// ABI integer path: the operands are centred integers of any width. The
+// library measures the activation range on the device and the per-channel
+// weight ranges on the host; when every range spans at most 256 values it
+// offsets both into int8 and runs the MFMA kernel with the exact correction
+// terms (qa_igemm.h), otherwise it runs the exact VALU kernel. Either way
+// the result equals the reference's int32 (modulo 2^32) or int64 sums.
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/qa_hip.h"
+#include "qa_igemm.h"
+#include "qa_valu.h"
+
+namespace qa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int64_t kRowPad = 128;  // packed weight rows per group: x128
+
+// ------------------------------------------------------------- kernels --
+template <class T>
+__global__ __launch_bounds__(kThreads) void k_range(const T* x, int64_t n,
+                                                    int narrow16, int* mm) {
+    int lo = INT32_MAX, hi = INT32_MIN;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step) {
+        int v = (int)x[i];
+        if (narrow16) v = (int16_t)v;
+        lo = min(lo, v);
+        hi = max(hi, v);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        lo = min(lo, __shfl_xor(lo, off));
+        hi = max(hi, __shfl_xor(hi, off));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        atomicMin(&mm[0], lo);
+        atomicMax(&mm[1], hi);
+    }
+}
+
+// y[i] = int8(v - a_off) with v optionally wrapped to int16 first.
+template <class T>
+__global__ __launch_bounds__(kThreads) void k_pack_i8(const T* x, int8_t* y,
+                                                      int64_t n, int narrow16,
+                                                      int a_off) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step) {
+        int v = (int)x[i];
+        if (narrow16) v = (int16_t)v;
+        y[i] = (int8_t)(v - a_off);
+    }
+}
+
+// Row-major A[M][K] -> int8 [M][Kp] with zero K-padding.
+template <class T>
+__global__ __launch_bounds__(kThreads) void k_pack_rows_i8(
+    const T* a, int8_t* y, int64_t M, int64_t K, int64_t Kp, int a_off) {
+    const int64_t n = M * Kp;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step) {
+        const int64_t m = i / Kp, k = i - m * Kp;
+        y[i] = k < K ? (int8_t)((int)a[m * K + k] - a_off) : (int8_t)0;
+    }
+}
+
+// ------------------------------------------------------------- helpers --
+bool fits_i32(int64_t v) { return v >= 0 && v < ((int64_t)1 << 31); }
+
+template <class T>
+bool host_copy(const T* src, int64_t n, std::vector<T>& dst) {
+    dst.resize((size_t)std::max<int64_t>(n, 1));
+    if (n <= 0) return true;
+    hipError_t e = hipMemcpy(dst.data(), src, (size_t)n * sizeof(T),
+                             hipMemcpyDefault);
+    if (e != hipSuccess) {
+        set_hip_error("hipMemcpy(host copy)", e);
+        return false;
+    }
+    return true;
+}
+
+template <class T>
+T* upload(int slot, const T* h, int64_t n, hipStream_t st) {
+    T* d = (T*)scratch(slot, (size_t)std::max<int64_t>(n, 1) * sizeof(T));
+    if (!d) return nullptr;
+    if (n <= 0) return d;
+    hipError_t e =
+        hipMemcpyAsync(d, h, (size_t)n * sizeof(T), hipMemcpyDefault, st);
+    if (e != hipSuccess) {
+        set_hip_error("hipMemcpyAsync(upload)", e);
+        return nullptr;
+    }
+    return d;
+}
+
+bool download(void* h, const void* d, size_t bytes, hipStream_t st) {
+    hipError_t e = hipMemcpyAsync(h, d, bytes, hipMemcpyDefault, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        set_hip_error("download", e);
+        return false;
+    }
+    return true;
+}
+
+// Device min/max of n values (wrapped to int16 when narrow16).
+template <class T>
+bool device_range(const T* d, int64_t n, bool narrow16, hipStream_t st,
+                  int* lo, int* hi) {
+    int* mm = (int*)scratch(7, 2 * sizeof(int));
+    if (!mm) return false;
+    const int init[2] = {INT32_MAX, INT32_MIN};
+    QA_HIP_RET(hipMemcpyAsync(mm, init, sizeof(init), hipMemcpyHostToDevice,
+                              st), false);
+    k_range<T><<<grid_1d(n, kThreads, 4096), kThreads, 0, st>>>(
+        d, n, narrow16 ? 1 : 0, mm);
+    QA_HIP_RET(hipGetLastError(), false);
+    int out[2];
+    if (!download(out, mm, sizeof(out), st)) return false;
+    *lo = out[0];
+    *hi = out[1];
+    return true;
+}
+
+// Activation offset making [lo, hi] (0 included for padding) int8, or false.
+bool activation_offset(int lo, int hi, int* a_off) {
+    lo = std::min(lo, 0);
+    hi = std::max(hi, 0);
+    if ((int64_t)hi - lo > 255) return false;
+    *a_off = (lo >= -128 && hi <= 127) ? 0 : lo + 128;
+    return true;
+}
+
+void fill_geometry(IgemmArgs& a, int64_t N, int64_t C, int64_t H, int64_t W,
+                   int64_t Cout, int64_t KH, int64_t KW, int64_t SH,
+                   int64_t SW, int64_t PH, int64_t PW, int64_t DH, int64_t DW,
+                   int64_t G, int64_t OH, int64_t OW) {
+    a.C = (int32_t)C;
+    a.H = (int32_t)H;
+    a.W = (int32_t)W;
+    a.Cg = (int32_t)(C / G);
+    a.G = (int32_t)G;
+    a.Cog = (int32_t)(Cout / G);
+    a.KH = (int32_t)KH;
+    a.KW = (int32_t)KW;
+    a.SH = (int32_t)SH;
+    a.SW = (int32_t)SW;
+    a.PH = (int32_t)PH;
+    a.PW = (int32_t)PW;
+    a.DH = (int32_t)DH;
+    a.DW = (int32_t)DW;
+    a.OH = (int32_t)OH;
+    a.OW = (int32_t)OW;
+    a.CB = (int32_t)ceil_div(a.Cg, 16);
+    a.KG = a.KH * a.KW * a.CB;
+    a.KGp = (int32_t)round_up(std::max(a.KG, 1), 4);
+    a.M = N * OH * OW;
+    a.Kreal = a.Cg * a.KH * a.KW;
+    a.Cout = (int32_t)Cout;
+}
+
+ValuConv valu_geometry(int64_t N, int64_t C, int64_t H, int64_t W,
+                       int64_t Cout, int64_t KH, int64_t KW, int64_t SH,
+                       int64_t SW, int64_t PH, int64_t PW, int64_t DH,
+                       int64_t DW, int64_t G, int64_t OH, int64_t OW) {
+    ValuConv c;
+    memset(&c, 0, sizeof(c));
+    c.N = (int32_t)N;
+    c.C = (int32_t)C;
+    c.H = (int32_t)H;
+    c.W = (int32_t)W;
+    c.Cout = (int32_t)Cout;
+    c.KH = (int32_t)KH;
+    c.KW = (int32_t)KW;
+    c.SH = (int32_t)SH;
+    c.SW = (int32_t)SW;
+    c.PH = (int32_t)PH;
+    c.PW = (int32_t)PW;
+    c.DH = (int32_t)DH;
+    c.DW = (int32_t)DW;
+    c.G = (int32_t)G;
+    c.OH = (int32_t)OH;
+    c.OW = (int32_t)OW;
+    c.x_nstride = C * H * W;
+    return c;
+}
+
+bool conv_shape_ok(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
+                   int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t DH,
+                   int64_t DW, int64_t G, int64_t OH, int64_t OW) {
+    if (G <= 0 || C % G || Cout % G || SH <= 0 || SW <= 0 || DH <= 0 ||
+        DW <= 0 || KH < 0 || KW < 0) {
+        set_error("conv", "invalid geometry (groups, strides or dilations)");
+        return false;
+    }
+    const int64_t dims[] = {N, C, H, W, Cout, KH, KW, OH, OW, N * OH * OW,
+                            C * H * W};
+    for (int64_t d : dims)
+        if (!fits_i32(d)) {
+            set_error("conv", "dimension outside [0, 2^31)");
+            return false;
+        }
+    if (Cout > 65535 || N > 65535) {
+        set_error("conv", "Cout and N must be at most 65535");
+        return false;
+    }
+    return true;
+}
+
+// Packs weights host-side; see qa_pack_weights_i8 in qa_hip.h.
+int pack_weights(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
+                 int64_t KW, int64_t G, int64_t a_off, int8_t* wp,
+                 int64_t* corr, int32_t* boff, int32_t* needs_rowsum) {
+    if (G <= 0 || Cout % G || Cg < 0) return -1;
+    const int64_t Cog = Cout / G;
+    const int64_t CB = ceil_div(Cg, 16);
+    const int64_t KG = KH * KW * CB;
+    const int64_t KGp = round_up(std::max<int64_t>(KG, 1), 4);
+    const int64_t rows = round_up(std::max<int64_t>(Cog, 1), kRowPad);
+    const int64_t K = Cg * KH * KW;
+    memset(wp, 0, (size_t)(G * rows * KGp * 16));
+    int32_t any = 0;
+    for (int64_t co = 0; co < Cout; ++co) {
+        const int32_t* row = w + co * K;
+        int lo = INT32_MAX, hi = INT32_MIN;
+        for (int64_t k = 0; k < K; ++k) {
+            lo = std::min(lo, row[k]);
+            hi = std::max(hi, row[k]);
+        }
+        if (K == 0) lo = hi = 0;
+        if ((int64_t)hi - lo > 255) return 1;
+        const int b = (lo >= -128 && hi <= 127) ? 0 : lo + 128;
+        if (b) any = 1;
+        int64_t colsum = 0;
+        const int64_t g = co / Cog, r = co % Cog;
+        int8_t* dst = wp + (g * rows + r) * KGp * 16;
+        for (int64_t c = 0; c < Cg; ++c)
+            for (int64_t ky = 0; ky < KH; ++ky)
+                for (int64_t kx = 0; kx < KW; ++kx) {
+                    const int v = row[(c * KH + ky) * KW + kx] - b;
+                    colsum += v;
+                    const int64_t kg = (ky * KW + kx) * CB + c / 16;
+                    dst[kg * 16 + c % 16] = (int8_t)v;
+                }
+        corr[co] = a_off * colsum + K * a_off * (int64_t)b;
+        boff[co] = b;
+    }
+    *needs_rowsum = any;
+    return 0;
+}
+
+// ------------------------------------------------------------ ABI conv --
+template <bool WIDE, class TW>
+void conv_abi(const int32_t* x, const TW* w, void* y, int64_t N, int64_t C,
+              int64_t H, int64_t W, int64_t Cout, int64_t KH, int64_t KW,
+              int64_t SH, int64_t SW, int64_t PH, int64_t PW, int64_t DH,
+              int64_t DW, int64_t G, int64_t OH, int64_t OW) {
+    const int64_t nout = N * Cout * OH * OW;
+    if (nout <= 0) return;
+    if (!conv_shape_ok(N, C, H, W, Cout, KH, KW, SH, SW, DH, DW, G, OH, OW))
+        return;
+    AbiLock lk;
+    hipStream_t st = stream();
+    if (!st) return;
+    const size_t ybytes = (size_t)nout * (WIDE ? 8 : 4);
+    void* dy = scratch(1, ybytes);
+    if (!dy) return;
+    const int64_t Cg = C / G;
+    const int64_t K = Cg * KH * KW;
+    if (K == 0 || N * C * H * W == 0) {
+        QA_HIP(hipMemsetAsync(dy, 0, ybytes, st));
+        download(y, dy, ybytes, st);
+        return;
+    }
+    const int64_t nx = N * C * H * W;
+    const int32_t* dx = upload(0, x, nx, st);
+    if (!dx) return;
+    std::vector<TW> hw;
+    if (!host_copy(w, Cout * K, hw)) return;
+
+    int lo, hi, a_off = 0;
+    if (!device_range(dx, nx, !WIDE, st, &lo, &hi)) return;
+    bool mfma = K < 131072 && activation_offset(lo, hi, &a_off);
+    std::vector<int32_t> w32;
+    int64_t kgp = 0, rows = 0;
+    const int64_t wpbytes =
+        qa_pack_weights_i8_size(Cout, Cg, KH, KW, G, &kgp, &rows);
+    std::vector<int8_t> wp;
+    std::vector<int64_t> corr;
+    std::vector<int32_t> boff;
+    int32_t rowsum = 0;
+    if (mfma) {
+        w32.assign(hw.begin(), hw.begin() + Cout * K);
+        wp.resize((size_t)wpbytes);
+        corr.resize((size_t)Cout);
+        boff.resize((size_t)Cout);
+        mfma = pack_weights(w32.data(), Cout, Cg, KH, KW, G, a_off, wp.data(),
+                            corr.data(), boff.data(), &rowsum) == 0;
+    }
+    IgemmArgs a;
+    memset(&a, 0, sizeof(a));
+    fill_geometry(a, N, C, H, W, Cout, KH, KW, SH, SW, PH, PW, DH, DW, G, OH,
+                  OW);
+    a.y = dy;
+    a.y_nstride = Cout * OH * OW;
+    if (mfma) {
+        int8_t* dxs = (int8_t*)scratch(6, (size_t)nx);
+        const int8_t* dwp = upload(2, wp.data(), wpbytes, st);
+        const int64_t* dcorr = upload(3, corr.data(), Cout, st);
+        const int32_t* dboff = upload(4, boff.data(), Cout, st);
+        if (!dxs || !dwp || !dcorr || !dboff) return;
+        k_pack_i8<int32_t><<<grid_1d(nx, kThreads, 1 << 20), kThreads, 0,
+                             st>>>(dx, dxs, nx, WIDE ? 0 : 1, a_off);
+        QA_HIP(hipGetLastError());
+        a.x = dxs;
+        a.x_nstride = C * H * W;
+        a.x_cstride = H * W;
+        a.pad_value = -a_off;
+        a.wp = dwp;
+        a.wp_rstride = kgp * 16;
+        a.wp_gstride = rows * kgp * 16;
+        a.corr = dcorr;
+        a.boff = dboff;
+        if (!launch_igemm(a, WIDE ? EPI_RAW64 : EPI_RAW32, rowsum != 0, st))
+            return;
+    } else {
+        const TW* dw = upload(2, hw.data(), Cout * K, st);
+        if (!dw) return;
+        ValuConv c = valu_geometry(N, C, H, W, Cout, KH, KW, SH, SW, PH, PW,
+                                   DH, DW, G, OH, OW);
+        c.x = dx;
+        c.x_code = 4;
+        c.narrow16 = WIDE ? 0 : 1;
+        c.w = dw;
+        c.w_code = sizeof(TW);
+        c.wide = WIDE ? 1 : 0;
+        if (!launch_conv_valu(c, a, WIDE ? EPI_RAW64 : EPI_RAW32, st)) return;
+    }
+    download(y, dy, ybytes, st);
+}
+
+// ------------------------------------------------------------ ABI GEMM --
+template <bool WIDE, class T>
+void gemm_abi(int64_t M, int64_t N, int64_t K, const T* A, const T* B,
+              void* C) {
+    if (M <= 0 || N <= 0) return;
+    if (!fits_i32(M) || !fits_i32(N) || !fits_i32(K)) {
+        set_error("gemm", "dimension outside [0, 2^31)");
+        return;
+    }
+    AbiLock lk;
+    hipStream_t st = stream();
+    if (!st) return;
+    const size_t cbytes = (size_t)(M * N) * (WIDE ? 8 : 4);
+    void* dc = scratch(1, cbytes);
+    if (!dc) return;
+    if (K == 0) {
+        QA_HIP(hipMemsetAsync(dc, 0, cbytes, st));
+        download(C, dc, cbytes, st);
+        return;
+    }
+    const T* da = upload(0, A, M * K, st);
+    if (!da) return;
+    std::vector<T> hb;
+    if (!host_copy(B, K * N, hb)) return;
+    int lo, hi, a_off = 0;
+    if (!device_range(da, M * K, false, st, &lo, &hi)) return;
+    bool mfma = K < 131072 && activation_offset(lo, hi, &a_off);
+    // B^T as "weights" [N][K] (Cout = N, Cg = K, 1x1)
+    int64_t kgp = 0, rows = 0;
+    const int64_t wpbytes = qa_pack_weights_i8_size(N, K, 1, 1, 1, &kgp, &rows);
+    std::vector<int8_t> wp;
+    std::vector<int64_t> corr;
+    std::vector<int32_t> boff;
+    int32_t rowsum = 0;
+    if (mfma) {
+        std::vector<int32_t> bt((size_t)(N * K));
+        for (int64_t k = 0; k < K; ++k)
+            for (int64_t n = 0; n < N; ++n) bt[n * K + k] = (int32_t)hb[k * N + n];
+        wp.resize((size_t)wpbytes);
+        corr.resize((size_t)N);
+        boff.resize((size_t)N);
+        mfma = pack_weights(bt.data(), N, K, 1, 1, 1, a_off, wp.data(),
+                            corr.data(), boff.data(), &rowsum) == 0;
+    }
+    if (mfma) {
+        const int64_t Kp = kgp * 16;
+        int8_t* das = (int8_t*)scratch(6, (size_t)(M * Kp));
+        const int8_t* dwp = upload(2, wp.data(), wpbytes, st);
+        const int64_t* dcorr = upload(3, corr.data(), N, st);
+        const int32_t* dboff = upload(4, boff.data(), N, st);
+        if (!das || !dwp || !dcorr || !dboff) return;
+        k_pack_rows_i8<T><<<grid_1d(M * Kp, kThreads, 1 << 20), kThreads, 0,
+                            st>>>(da, das, M, K, Kp, a_off);
+        QA_HIP(hipGetLastError());
+        IgemmArgs a;
+        memset(&a, 0, sizeof(a));
+        fill_geometry(a, M, K, 1, 1, N, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 1);
+        a.x = das;
+        a.rowmajor = 1;
+        a.lda = Kp;
+        a.x_nstride = Kp;
+        a.x_cstride = 1;
+        a.wp = dwp;
+        a.wp_rstride = kgp * 16;
+        a.wp_gstride = rows * kgp * 16;
+        a.corr = dcorr;
+        a.boff = dboff;
+        a.y = dc;
+        a.y_nstride = N;
+        if (!launch_igemm(a, WIDE ? EPI_RAW64 : EPI_RAW32, rowsum != 0, st))
+            return;
+    } else {
+        const T* db = upload(2, hb.data(), K * N, st);
+        if (!db) return;
+        if (!launch_gemm_valu(da, sizeof(T), db, sizeof(T), dc, M, N, K, WIDE,
+                              st))
+            return;
+    }
+    download(C, dc, cbytes, st);
+}
+
+}  // namespace
+}  // namespace qa
+
+using namespace qa;
+
+// ================================================== reference ABI exports ==
+QA_API int qa_num_threads(void) {
+    int d = 0, n = 0;
+    if (hipGetDevice(&d) != hipSuccess) return 1;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) !=
+        hipSuccess)
+        return 1;
+    return n;
+}
+
+QA_API void qa_set_num_threads(int n) { (void)n; }
+
+QA_API int qa_has_openmp(void) { return 0; }
+
+QA_API void qa_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A,
+                        const float* B, float* C) {
+    if (M <= 0 || N <= 0) return;
+    AbiLock lk;
+    hipStream_t st = stream();
+    if (!st) return;
+    const float* da = upload(0, A, M * K, st);
+    const float* db = upload(2, B, K * N, st);
+    float* dc = (float*)scratch(1, (size_t)(M * N) * 4);
+    if (!da || !db || !dc) return;
+    if (!launch_gemm_f32(da, db, dc, M, N, K, st)) return;
+    download(C, dc, (size_t)(M * N) * 4, st);
+}
+
+QA_API void qa_gemm_i16_i32(int64_t M, int64_t N, int64_t K, const int16_t* A,
+                            const int16_t* B, int32_t* C) {
+    gemm_abi<false, int16_t>(M, N, K, A, B, C);
+}
+
+QA_API void qa_gemm_i32_i64(int64_t M, int64_t N, int64_t K, const int32_t* A,
+                            const int32_t* B, int64_t* C) {
+    gemm_abi<true, int32_t>(M, N, K, A, B, C);
+}
+
+#define QA_CONV_PARAMS                                                       \
+    int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t KH,    \
+        int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,          \
+        int64_t DH, int64_t DW, int64_t G, int64_t OH, int64_t OW
+#define QA_CONV_FWD N, C, H, W, Cout, KH, KW, SH, SW, PH, PW, DH, DW, G, OH, OW
+
+QA_API void qa_conv_f32(const float* x, const float* w, float* y,
+                        QA_CONV_PARAMS) {
+    const int64_t nout = N * Cout * OH * OW;
+    if (nout <= 0) return;
+    if (!conv_shape_ok(N, C, H, W, Cout, KH, KW, SH, SW, DH, DW, G, OH, OW))
+        return;
+    AbiLock lk;
+    hipStream_t st = stream();
+    if (!st) return;
+    const float* dx = upload(0, x, N * C * H * W, st);
+    const float* dw = upload(2, w, Cout * (C / G) * KH * KW, st);
+    float* dy = (float*)scratch(1, (size_t)nout * 4);
+    if (!dx || !dw || !dy) return;
+    ValuConv c = valu_geometry(QA_CONV_FWD);
+    if (!launch_conv_f32(dx, dw, dy, c, st)) return;
+    download(y, dy, (size_t)nout * 4, st);
+}
+
+QA_API void qa_conv_i32_i16_i32(const int32_t* x, const int16_t* w,
+                                int32_t* y, QA_CONV_PARAMS) {
+    conv_abi<false, int16_t>(x, w, y, QA_CONV_FWD);
+}
+
+QA_API void qa_conv_i32_i32_i64(const int32_t* x, const int32_t* w,
+                                int64_t* y, QA_CONV_PARAMS) {
+    conv_abi<true, int32_t>(x, w, y, QA_CONV_FWD);
+}
+
+// ============================================== additional surface ==
+QA_API int64_t qa_pack_weights_i8_size(int64_t Cout, int64_t Cg, int64_t KH,
+                                       int64_t KW, int64_t G, int64_t* kgp,
+                                       int64_t* rows_per_group) {
+    if (G <= 0 || Cout < 0 || Cout % G) return -1;
+    const int64_t KG = KH * KW * ceil_div(Cg, 16);
+    const int64_t KGp = round_up(std::max<int64_t>(KG, 1), 4);
+    const int64_t rows = round_up(std::max<int64_t>(Cout / G, 1), kRowPad);
+    if (kgp) *kgp = KGp;
+    if (rows_per_group) *rows_per_group = rows;
+    return G * rows * KGp * 16;
+}
+
+QA_API int qa_pack_weights_i8(const int32_t* w, int64_t Cout, int64_t Cg,
+                              int64_t KH, int64_t KW, int64_t G, int64_t a_off,
+                              int8_t* wp, int64_t* corr, int32_t* boff,
+                              int32_t* needs_rowsum) {
+    return pack_weights(w, Cout, Cg, KH, KW, G, a_off, wp, corr, boff,
+                        needs_rowsum);
+}
+
+QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
+    hipStream_t st = stream_ ? (hipStream_t)stream_ : stream();
+    if (!d || !st) return -1;
+    if (!conv_shape_ok(d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW, d->SH,
+                       d->SW, d->DH, d->DW, d->G, d->OH, d->OW))
+        return -1;
+    if (d->N * d->Cout * d->OH * d->OW == 0) return 0;
+    IgemmArgs a;
+    memset(&a, 0, sizeof(a));
+    fill_geometry(a, d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW, d->SH,
+                  d->SW, d->PH, d->PW, d->DH, d->DW, d->G, d->OH, d->OW);
+    a.corr = d->corr;
+    a.boff = d->boff;
+    a.pre = d->pre_bias;
+    a.y = d->y;
+    a.y_nstride = d->y_nstride;
+    a.out_code = (int32_t)d->y_code;
+    a.out_so = d->y_so;
+    a.mult = d->mult;
+    a.shift = d->shift;
+    a.zp = d->zp;
+    a.qmin = d->qmin;
+    a.qmax = d->qmax;
+    a.lut = d->lut;
+    a.lut_off = d->lut_offset;
+    a.lut_len = d->lut_len;
+    a.res = d->res;
+    a.res_nstride = d->res_nstride;
+    a.res_so = d->res_so;
+    a.res_first = (int32_t)d->res_first;
+    a.za = d->za;
+    a.ma = d->ma;
+    a.sa = d->sa;
+    a.zb = d->zb;
+    a.mb = d->mb;
+    a.sb = d->sb;
+    a.add_sign = d->add_sign;
+    a.add_zp = d->add_zp;
+    a.add_qmin = d->add_qmin;
+    a.add_qmax = d->add_qmax;
+    if (d->y_code != 1 && d->y_code != 2) {
+        set_error("qa_d_conv", "output storage must be int8 or int16");
+        return -1;
+    }
+    if (d->w_code == 1) {
+        if (d->x_code != 1 || d->x_add < -127 || d->x_add > 128 ||
+            d->w_kgp != a.KGp || a.Kreal >= 131072) {
+            set_error("qa_d_conv", "int8 MFMA path: bad operands");
+            return -1;
+        }
+        a.x = (const int8_t*)d->x;
+        a.x_nstride = d->x_nstride;
+        a.x_cstride = d->rowmajor ? 1 : d->H * d->W;
+        a.rowmajor = (int32_t)d->rowmajor;
+        a.lda = d->x_nstride;
+        a.pad_value = (int32_t)(-d->x_add);
+        a.wp = (const int8_t*)d->w;
+        a.wp_rstride = d->w_kgp * 16;
+        a.wp_gstride = d->w_rows * d->w_kgp * 16;
+        return launch_igemm(a, EPI_QUANT, d->needs_rowsum != 0, st) ? 0 : -1;
+    }
+    ValuConv c = valu_geometry(d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW,
+                               d->SH, d->SW, d->PH, d->PW, d->DH, d->DW, d->G,
+                               d->OH, d->OW);
+    c.x = d->x;
+    c.x_code = (int32_t)d->x_code;
+    c.x_nstride = d->x_nstride;
+    c.x_add = d->x_add;
+    c.w = d->w;
+    c.w_code = (int32_t)d->w_code;
+    c.wide = (int32_t)d->wide;
+    return launch_conv_valu(c, a, EPI_QUANT, st) ? 0 : -1;
+}

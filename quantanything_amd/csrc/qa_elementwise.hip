@@ -1,0 +1,475 @@
+// Element-wise integer kernels: requantize, rescale, add, mul, LUT,
+// float <-> integer conversion. HBM-bound; one element per thread per
+// grid-stride step, 64-bit indices.
+//
+// Host-pointer exports replace the reference's (qa_kernels.cpp:287-386) with
+// identical signatures and results; qa_d_* exports take device pointers, a
+// stream, and the int8/int16 storage form used by the resident executor.
+#include "qa_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// Element index -> channel of a [outer, C, inner] view.
+__device__ __forceinline__ int64_t chan_of(int64_t i, int64_t C, int64_t inner,
+                                           bool small) {
+    if (small) return (int64_t)(((uint32_t)i / (uint32_t)inner) % (uint32_t)C);
+    return (i / inner) % C;
+}
+
+// out = clip(mbqm(acc - sub + pre[c], m[c], s[c]) + post[c] + zp) - out_so
+template <class TAcc, class TOut>
+__global__ __launch_bounds__(kThreads) void k_requant(
+    const TAcc* __restrict__ acc, TOut* __restrict__ out, int64_t n,
+    int64_t C, int64_t inner, const int64_t* __restrict__ mult,
+    const int64_t* __restrict__ shift, const int64_t* __restrict__ pre,
+    const int64_t* __restrict__ post, int64_t zp, int64_t qmin, int64_t qmax,
+    int64_t sub, int64_t out_so) {
+    const bool small = n < (int64_t)0x7fffffff && inner < (int64_t)0x7fffffff;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step) {
+        const int64_t c = chan_of(i, C, inner, small);
+        const int64_t pb = pre ? pre[c] : 0;
+        const int64_t qb = (post ? post[c] : 0) + zp;
+        const qa_i128 v = qa_mbqm_fast((int64_t)acc[i] - sub + pb, mult[c],
+                                       shift[c]) + qb;
+        out[i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
+    }
+}
+
+template <class TIn, class TOut>
+__global__ __launch_bounds__(kThreads) void k_rescale(
+    const TIn* __restrict__ x, TOut* __restrict__ out, int64_t n,
+    int64_t zp_in, int64_t m, int64_t s, int64_t zp_out, int64_t qmin,
+    int64_t qmax, int64_t in_so, int64_t out_so) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step) {
+        const qa_i128 v =
+            qa_mbqm_fast((int64_t)x[i] + in_so - zp_in, m, s) + zp_out;
+        out[i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
+    }
+}
+
+template <class TIn, class TOut>
+__global__ __launch_bounds__(kThreads) void k_add(
+    const TIn* __restrict__ a, const TIn* __restrict__ b,
+    TOut* __restrict__ out, int64_t n, int64_t za, int64_t ma, int64_t sa,
+    int64_t zb, int64_t mb, int64_t sb, int64_t sign, int64_t zp_out,
+    int64_t qmin, int64_t qmax, int64_t a_so, int64_t b_so, int64_t out_so) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step) {
+        const qa_i128 v = qa_mbqm_fast((int64_t)a[i] + a_so - za, ma, sa) +
+                          (qa_i128)sign *
+                              qa_mbqm_fast((int64_t)b[i] + b_so - zb, mb, sb) +
+                          zp_out;
+        out[i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
+    }
+}
+
+template <class TIn, class TOut>
+__global__ __launch_bounds__(kThreads) void k_mul(
+    const TIn* __restrict__ a, const TIn* __restrict__ b,
+    TOut* __restrict__ out, int64_t n, int64_t za, int64_t zb, int64_t m,
+    int64_t s, int64_t zp_out, int64_t qmin, int64_t qmax, int64_t a_so,
+    int64_t b_so, int64_t out_so) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step) {
+        const int64_t p =
+            ((int64_t)a[i] + a_so - za) * ((int64_t)b[i] + b_so - zb);
+        const qa_i128 v = qa_mbqm_fast(p, m, s) + zp_out;
+        out[i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
+    }
+}
+
+template <class TIn, class TOut>
+__global__ __launch_bounds__(kThreads) void k_lut(
+    const TIn* __restrict__ x, TOut* __restrict__ out, int64_t n,
+    int64_t offset, const int32_t* __restrict__ lut, int64_t len,
+    int64_t in_so, int64_t out_so) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step) {
+        int64_t idx = (int64_t)x[i] + in_so - offset;
+        idx = idx < 0 ? 0 : (idx >= len ? len - 1 : idx);
+        out[i] = (TOut)((int64_t)lut[idx] - out_so);
+    }
+}
+
+// q = clip(rint(double(x) / scale) + zp); NaN -> INT32_MIN (what the
+// reference's double -> int32 conversion yields on x86-64).
+__device__ __forceinline__ int64_t quantize_one(float x, double scale,
+                                                int64_t zp, int64_t qmin,
+                                                int64_t qmax) {
+    double v = rint((double)x / scale) + (double)zp;
+    if (v != v) return INT32_MIN;
+    if (v < (double)qmin) v = (double)qmin;
+    if (v > (double)qmax) v = (double)qmax;
+    return (int64_t)(int32_t)v;
+}
+
+template <class TOut>
+__global__ __launch_bounds__(kThreads) void k_quantize(
+    const float* __restrict__ x, TOut* __restrict__ q, int64_t n,
+    double scale, int64_t zp, int64_t qmin, int64_t qmax, int64_t out_so) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step)
+        q[i] = (TOut)(quantize_one(x[i], scale, zp, qmin, qmax) - out_so);
+}
+
+// 16 float32 -> 16 int8 per thread (graph-input quantization).
+__global__ __launch_bounds__(kThreads) void k_quantize_v16_i8(
+    const float4* __restrict__ x, int4* __restrict__ q, int64_t n16,
+    double scale, int64_t zp, int64_t qmin, int64_t qmax, int64_t out_so) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+         i += step) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 f = x[i * 4 + j];
+            const uint32_t b0 = (uint8_t)(int8_t)(
+                quantize_one(f.x, scale, zp, qmin, qmax) - out_so);
+            const uint32_t b1 = (uint8_t)(int8_t)(
+                quantize_one(f.y, scale, zp, qmin, qmax) - out_so);
+            const uint32_t b2 = (uint8_t)(int8_t)(
+                quantize_one(f.z, scale, zp, qmin, qmax) - out_so);
+            const uint32_t b3 = (uint8_t)(int8_t)(
+                quantize_one(f.w, scale, zp, qmin, qmax) - out_so);
+            w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+        q[i] = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+    }
+}
+
+template <class TIn>
+__global__ __launch_bounds__(kThreads) void k_dequantize(
+    const TIn* __restrict__ q, float* __restrict__ x, int64_t n, double scale,
+    int64_t zp, int64_t in_so) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += step)
+        x[i] = (float)((double)((int64_t)q[i] + in_so - zp) * scale);
+}
+
+hipStream_t pick(void* s) {
+    return s ? (hipStream_t)s : qa::stream();
+}
+
+template <class T>
+T* upload(int slot, const T* h, int64_t n, hipStream_t st) {
+    T* d = (T*)qa::scratch(slot, (size_t)n * sizeof(T));
+    if (!d) return nullptr;
+    hipError_t e = hipMemcpyAsync(d, h, (size_t)n * sizeof(T),
+                                  hipMemcpyDefault, st);
+    if (e != hipSuccess) {
+        qa::set_hip_error("hipMemcpyAsync(upload)", e);
+        return nullptr;
+    }
+    return d;
+}
+
+bool download(void* h, const void* d, size_t bytes, hipStream_t st) {
+    hipError_t e = hipMemcpyAsync(h, d, bytes, hipMemcpyDefault, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        qa::set_hip_error("download", e);
+        return false;
+    }
+    return true;
+}
+
+bool launched(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        qa::set_hip_error(what, e);
+        return false;
+    }
+    return true;
+}
+
+template <class TAcc>
+void requantize_abi(const TAcc* acc, int32_t* out, int64_t outer, int64_t C,
+                    int64_t inner, const int64_t* mult, const int64_t* shift,
+                    const int64_t* pre, const int64_t* post, int64_t zp,
+                    int64_t qmin, int64_t qmax) {
+    const int64_t n = outer * C * inner;
+    if (n <= 0) return;
+    qa::AbiLock lk;
+    hipStream_t st = qa::stream();
+    if (!st) return;
+    const TAcc* da = upload(0, acc, n, st);
+    const int64_t* dm = upload(2, mult, C, st);
+    const int64_t* ds = upload(3, shift, C, st);
+    const int64_t* dpre = pre ? upload(4, pre, C, st) : nullptr;
+    const int64_t* dpost = post ? upload(5, post, C, st) : nullptr;
+    int32_t* dout = (int32_t*)qa::scratch(1, (size_t)n * 4);
+    if (!da || !dm || !ds || !dout || (pre && !dpre) || (post && !dpost))
+        return;
+    k_requant<TAcc, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
+        da, dout, n, C, inner, dm, ds, dpre, dpost, zp, qmin, qmax, 0, 0);
+    if (!launched("k_requant")) return;
+    download(out, dout, (size_t)n * 4, st);
+}
+
+}  // namespace
+
+// ===================================================== host-pointer ABI ===
+// Every entry accepts host (or device) pointers, runs on the GPU and returns
+// once the result is in `out`. Errors: see qa_last_error.
+
+QA_API void qa_requantize_i32(const int32_t* acc, int32_t* out, int64_t outer,
+                              int64_t C, int64_t inner, const int64_t* mult,
+                              const int64_t* shift, const int64_t* pre_bias,
+                              const int64_t* post_bias, int64_t zp,
+                              int64_t qmin, int64_t qmax) {
+    requantize_abi<int32_t>(acc, out, outer, C, inner, mult, shift, pre_bias,
+                            post_bias, zp, qmin, qmax);
+}
+
+QA_API void qa_requantize_i64(const int64_t* acc, int32_t* out, int64_t outer,
+                              int64_t C, int64_t inner, const int64_t* mult,
+                              const int64_t* shift, const int64_t* pre_bias,
+                              const int64_t* post_bias, int64_t zp,
+                              int64_t qmin, int64_t qmax) {
+    requantize_abi<int64_t>(acc, out, outer, C, inner, mult, shift, pre_bias,
+                            post_bias, zp, qmin, qmax);
+}
+
+QA_API void qa_rescale(const int32_t* x, int32_t* out, int64_t n,
+                       int64_t zp_in, int64_t m, int64_t s, int64_t zp_out,
+                       int64_t qmin, int64_t qmax) {
+    if (n <= 0) return;
+    qa::AbiLock lk;
+    hipStream_t st = qa::stream();
+    if (!st) return;
+    const int32_t* dx = upload(0, x, n, st);
+    int32_t* dy = (int32_t*)qa::scratch(1, (size_t)n * 4);
+    if (!dx || !dy) return;
+    k_rescale<int32_t, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
+        dx, dy, n, zp_in, m, s, zp_out, qmin, qmax, 0, 0);
+    if (!launched("k_rescale")) return;
+    download(out, dy, (size_t)n * 4, st);
+}
+
+QA_API void qa_add(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
+                   int64_t za, int64_t ma, int64_t sa, int64_t zb, int64_t mb,
+                   int64_t sb, int64_t sign, int64_t zp_out, int64_t qmin,
+                   int64_t qmax) {
+    if (n <= 0) return;
+    qa::AbiLock lk;
+    hipStream_t st = qa::stream();
+    if (!st) return;
+    const int32_t* da = upload(0, a, n, st);
+    const int32_t* db = upload(2, b, n, st);
+    int32_t* dy = (int32_t*)qa::scratch(1, (size_t)n * 4);
+    if (!da || !db || !dy) return;
+    k_add<int32_t, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
+        da, db, dy, n, za, ma, sa, zb, mb, sb, sign, zp_out, qmin, qmax, 0, 0,
+        0);
+    if (!launched("k_add")) return;
+    download(out, dy, (size_t)n * 4, st);
+}
+
+QA_API void qa_mul(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
+                   int64_t za, int64_t zb, int64_t m, int64_t s, int64_t zp_out,
+                   int64_t qmin, int64_t qmax) {
+    if (n <= 0) return;
+    qa::AbiLock lk;
+    hipStream_t st = qa::stream();
+    if (!st) return;
+    const int32_t* da = upload(0, a, n, st);
+    const int32_t* db = upload(2, b, n, st);
+    int32_t* dy = (int32_t*)qa::scratch(1, (size_t)n * 4);
+    if (!da || !db || !dy) return;
+    k_mul<int32_t, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
+        da, db, dy, n, za, zb, m, s, zp_out, qmin, qmax, 0, 0, 0);
+    if (!launched("k_mul")) return;
+    download(out, dy, (size_t)n * 4, st);
+}
+
+QA_API void qa_lut(const int32_t* x, int32_t* out, int64_t n, int64_t offset,
+                   const int32_t* lut, int64_t lut_len) {
+    if (n <= 0 || lut_len <= 0) return;
+    qa::AbiLock lk;
+    hipStream_t st = qa::stream();
+    if (!st) return;
+    const int32_t* dx = upload(0, x, n, st);
+    const int32_t* dl = upload(2, lut, lut_len, st);
+    int32_t* dy = (int32_t*)qa::scratch(1, (size_t)n * 4);
+    if (!dx || !dl || !dy) return;
+    k_lut<int32_t, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
+        dx, dy, n, offset, dl, lut_len, 0, 0);
+    if (!launched("k_lut")) return;
+    download(out, dy, (size_t)n * 4, st);
+}
+
+QA_API void qa_quantize_f32(const float* x, int32_t* q, int64_t n,
+                            double scale, int64_t zp, int64_t qmin,
+                            int64_t qmax) {
+    if (n <= 0) return;
+    qa::AbiLock lk;
+    hipStream_t st = qa::stream();
+    if (!st) return;
+    const float* dx = upload(0, x, n, st);
+    int32_t* dq = (int32_t*)qa::scratch(1, (size_t)n * 4);
+    if (!dx || !dq) return;
+    k_quantize<int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
+        dx, dq, n, scale, zp, qmin, qmax, 0);
+    if (!launched("k_quantize")) return;
+    download(q, dq, (size_t)n * 4, st);
+}
+
+QA_API void qa_dequantize_f32(const int32_t* q, float* x, int64_t n,
+                              double scale, int64_t zp) {
+    if (n <= 0) return;
+    qa::AbiLock lk;
+    hipStream_t st = qa::stream();
+    if (!st) return;
+    const int32_t* dq = upload(0, q, n, st);
+    float* dx = (float*)qa::scratch(1, (size_t)n * 4);
+    if (!dq || !dx) return;
+    k_dequantize<int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
+        dq, dx, n, scale, zp, 0);
+    if (!launched("k_dequantize")) return;
+    download(x, dx, (size_t)n * 4, st);
+}
+
+// =================================================== device-pointer API ===
+// Storage codes: 1 = int8, 2 = int16, 4 = int32 (element size in bytes).
+// `*_so` are storage offsets (q = stored + so). All calls are asynchronous
+// on `stream` (NULL: the library stream) and return 0 on success.
+
+#define QA_DISPATCH_STORAGE(code, T, ...)          \
+    switch (code) {                                \
+        case 1: { typedef int8_t T; __VA_ARGS__; break; }  \
+        case 2: { typedef int16_t T; __VA_ARGS__; break; } \
+        case 4: { typedef int32_t T; __VA_ARGS__; break; } \
+        default: qa::set_error("storage", "unsupported storage code"); \
+            return -1;                             \
+    }
+
+QA_API int qa_d_requantize(const void* acc, int acc_code, void* out,
+                           int out_code, int64_t outer, int64_t C,
+                           int64_t inner, const int64_t* mult,
+                           const int64_t* shift, const int64_t* pre_bias,
+                           const int64_t* post_bias, int64_t zp, int64_t qmin,
+                           int64_t qmax, int64_t sub, int64_t out_so,
+                           void* stream) {
+    const int64_t n = outer * C * inner;
+    if (n <= 0) return 0;
+    hipStream_t st = pick(stream);
+    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    if (acc_code == 8) {
+        QA_DISPATCH_STORAGE(out_code, TO,
+            k_requant<int64_t, TO><<<g, kThreads, 0, st>>>(
+                (const int64_t*)acc, (TO*)out, n, C, inner, mult, shift,
+                pre_bias, post_bias, zp, qmin, qmax, sub, out_so))
+    } else {
+        QA_DISPATCH_STORAGE(acc_code, TA,
+            QA_DISPATCH_STORAGE(out_code, TO,
+                k_requant<TA, TO><<<g, kThreads, 0, st>>>(
+                    (const TA*)acc, (TO*)out, n, C, inner, mult, shift,
+                    pre_bias, post_bias, zp, qmin, qmax, sub, out_so)))
+    }
+    return launched("qa_d_requantize") ? 0 : -1;
+}
+
+QA_API int qa_d_rescale(const void* x, int in_code, void* out, int out_code,
+                        int64_t n, int64_t zp_in, int64_t m, int64_t s,
+                        int64_t zp_out, int64_t qmin, int64_t qmax,
+                        int64_t in_so, int64_t out_so, void* stream) {
+    if (n <= 0) return 0;
+    hipStream_t st = pick(stream);
+    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    QA_DISPATCH_STORAGE(in_code, TI,
+        QA_DISPATCH_STORAGE(out_code, TO,
+            k_rescale<TI, TO><<<g, kThreads, 0, st>>>(
+                (const TI*)x, (TO*)out, n, zp_in, m, s, zp_out, qmin, qmax,
+                in_so, out_so)))
+    return launched("qa_d_rescale") ? 0 : -1;
+}
+
+QA_API int qa_d_add(const void* a, const void* b, int in_code, void* out,
+                    int out_code, int64_t n, int64_t za, int64_t ma,
+                    int64_t sa, int64_t zb, int64_t mb, int64_t sb,
+                    int64_t sign, int64_t zp_out, int64_t qmin, int64_t qmax,
+                    int64_t a_so, int64_t b_so, int64_t out_so, void* stream) {
+    if (n <= 0) return 0;
+    hipStream_t st = pick(stream);
+    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    QA_DISPATCH_STORAGE(in_code, TI,
+        QA_DISPATCH_STORAGE(out_code, TO,
+            k_add<TI, TO><<<g, kThreads, 0, st>>>(
+                (const TI*)a, (const TI*)b, (TO*)out, n, za, ma, sa, zb, mb,
+                sb, sign, zp_out, qmin, qmax, a_so, b_so, out_so)))
+    return launched("qa_d_add") ? 0 : -1;
+}
+
+QA_API int qa_d_mul(const void* a, const void* b, int in_code, void* out,
+                    int out_code, int64_t n, int64_t za, int64_t zb,
+                    int64_t m, int64_t s, int64_t zp_out, int64_t qmin,
+                    int64_t qmax, int64_t a_so, int64_t b_so, int64_t out_so,
+                    void* stream) {
+    if (n <= 0) return 0;
+    hipStream_t st = pick(stream);
+    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    QA_DISPATCH_STORAGE(in_code, TI,
+        QA_DISPATCH_STORAGE(out_code, TO,
+            k_mul<TI, TO><<<g, kThreads, 0, st>>>(
+                (const TI*)a, (const TI*)b, (TO*)out, n, za, zb, m, s, zp_out,
+                qmin, qmax, a_so, b_so, out_so)))
+    return launched("qa_d_mul") ? 0 : -1;
+}
+
+QA_API int qa_d_lut(const void* x, int in_code, void* out, int out_code,
+                    int64_t n, int64_t offset, const int32_t* lut,
+                    int64_t lut_len, int64_t in_so, int64_t out_so,
+                    void* stream) {
+    if (n <= 0) return 0;
+    hipStream_t st = pick(stream);
+    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    QA_DISPATCH_STORAGE(in_code, TI,
+        QA_DISPATCH_STORAGE(out_code, TO,
+            k_lut<TI, TO><<<g, kThreads, 0, st>>>(
+                (const TI*)x, (TO*)out, n, offset, lut, lut_len, in_so,
+                out_so)))
+    return launched("qa_d_lut") ? 0 : -1;
+}
+
+QA_API int qa_d_quantize_f32(const float* x, void* q, int out_code, int64_t n,
+                             double scale, int64_t zp, int64_t qmin,
+                             int64_t qmax, int64_t out_so, void* stream) {
+    if (n <= 0) return 0;
+    hipStream_t st = pick(stream);
+    if (out_code == 1 && n % 16 == 0 && ((uintptr_t)x & 15) == 0 &&
+        ((uintptr_t)q & 15) == 0) {
+        const int64_t n16 = n / 16;
+        k_quantize_v16_i8<<<qa::grid_1d(n16, kThreads, 1 << 20), kThreads, 0,
+                            st>>>((const float4*)x, (int4*)q, n16, scale, zp,
+                                  qmin, qmax, out_so);
+        return launched("qa_d_quantize_f32") ? 0 : -1;
+    }
+    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    QA_DISPATCH_STORAGE(out_code, TO,
+        k_quantize<TO><<<g, kThreads, 0, st>>>(x, (TO*)q, n, scale, zp, qmin,
+                                               qmax, out_so))
+    return launched("qa_d_quantize_f32") ? 0 : -1;
+}
+
+QA_API int qa_d_dequantize_f32(const void* q, int in_code, float* x,
+                               int64_t n, double scale, int64_t zp,
+                               int64_t in_so, void* stream) {
+    if (n <= 0) return 0;
+    hipStream_t st = pick(stream);
+    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    QA_DISPATCH_STORAGE(in_code, TI,
+        k_dequantize<TI><<<g, kThreads, 0, st>>>((const TI*)q, x, n, scale,
+                                                 zp, in_so))
+    return launched("qa_d_dequantize_f32") ? 0 : -1;
+}

@@ -1,0 +1,153 @@
+// Library runtime: error reporting, the per-device stream, scratch buffers
+// and the diagnostic exports (qa_backend, qa_last_error, ...).
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "qa_common.h"
+
+namespace qa {
+
+namespace {
+
+constexpr int kMaxDevices = 16;
+constexpr int kSlots = 8;
+
+struct DeviceState {
+    hipStream_t stream = nullptr;
+    void* buf[kSlots] = {};
+    size_t cap[kSlots] = {};
+};
+
+DeviceState g_dev[kMaxDevices];
+std::mutex g_init_mutex;
+std::recursive_mutex g_abi_mutex;
+
+thread_local char t_error[512] = {0};
+thread_local bool t_failed = false;
+
+int current_device() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= kMaxDevices) d = 0;
+    return d;
+}
+
+}  // namespace
+
+void set_error(const char* where, const char* what) {
+    if (!t_failed) {
+        snprintf(t_error, sizeof(t_error), "%s: %s", where, what);
+        fprintf(stderr, "[qa_hip] error: %s\n", t_error);
+    }
+    t_failed = true;
+}
+
+void set_hip_error(const char* where, hipError_t e) {
+    set_error(where, hipGetErrorString(e));
+}
+
+bool ok() { return !t_failed; }
+
+hipStream_t stream() {
+    const int d = current_device();
+    DeviceState& s = g_dev[d];
+    if (!s.stream) {
+        std::lock_guard<std::mutex> lk(g_init_mutex);
+        if (!s.stream) {
+            hipStream_t st = nullptr;
+            // Default priority on purpose: streams of different priorities
+            // are not used anywhere in this library.
+            hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+            if (e != hipSuccess) {
+                set_hip_error("hipStreamCreateWithFlags", e);
+                return nullptr;
+            }
+            s.stream = st;
+        }
+    }
+    return s.stream;
+}
+
+void* scratch(int slot, size_t bytes) {
+    DeviceState& s = g_dev[current_device()];
+    if (bytes == 0) bytes = 256;
+    if (s.cap[slot] < bytes) {
+        if (s.buf[slot]) {
+            // Freed only once the stream has drained (the buffer may still be
+            // read by the previous call's kernels).
+            hipStreamSynchronize(stream());
+            hipFree(s.buf[slot]);
+            s.buf[slot] = nullptr;
+            s.cap[slot] = 0;
+        }
+        size_t want = bytes + bytes / 4;
+        want = (want + 4095) & ~(size_t)4095;
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess) {
+            set_hip_error("hipMalloc(scratch)", e);
+            return nullptr;
+        }
+        s.buf[slot] = p;
+        s.cap[slot] = want;
+    }
+    return s.buf[slot];
+}
+
+AbiLock::AbiLock() { g_abi_mutex.lock(); }
+AbiLock::~AbiLock() { g_abi_mutex.unlock(); }
+
+}  // namespace qa
+
+// ------------------------------------------------------------ exports ---
+
+// Identifies the backend so a caller can assert that the GPU library (and
+// not a CPU build) is the one loaded.
+QA_API const char* qa_backend(void) { return "hip-gfx950"; }
+
+// First error recorded on the calling thread since the last qa_clear_error,
+// or NULL. Host-pointer ABI entries return void like the reference's, so
+// this is how a caller learns that a call failed.
+QA_API const char* qa_last_error(void) {
+    return qa::t_failed ? qa::t_error : nullptr;
+}
+
+QA_API void qa_clear_error(void) {
+    qa::t_failed = false;
+    qa::t_error[0] = 0;
+}
+
+// Number of visible GPUs (0 when the HIP runtime finds none).
+QA_API int qa_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+// gfx architecture name of the current device into `buf` (NUL-terminated);
+// returns 0 on success.
+QA_API int qa_device_arch(char* buf, int64_t len) {
+    hipDeviceProp_t prop;
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess) return -1;
+    if (hipGetDeviceProperties(&prop, d) != hipSuccess) return -1;
+    if (len > 0) {
+        strncpy(buf, prop.gcnArchName, (size_t)len - 1);
+        buf[len - 1] = 0;
+    }
+    return 0;
+}
+
+// The library's stream on the current device (hipStream_t as a pointer).
+QA_API void* qa_stream(void) { return (void*)qa::stream(); }
+
+// Waits for all work the library queued on the current device.
+QA_API int qa_synchronize(void) {
+    hipError_t e = hipStreamSynchronize(qa::stream());
+    if (e != hipSuccess) {
+        qa::set_hip_error("hipStreamSynchronize", e);
+        return -1;
+    }
+    return 0;
+}
