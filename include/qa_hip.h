@@ -159,28 +159,36 @@ typedef struct qa_conv_desc {
 
 int qa_d_conv(const qa_conv_desc* d, void* stream);
 
-/* Element-wise device entries (storage codes as above; `*_so` storage
- * offsets; `sub` is subtracted from the accumulator before the bias). */
+/* Element-wise device entries (storage codes as above, `*_so` storage
+ * offsets). The row forms process `rows` rows of `cols` elements with one
+ * row stride per operand (a channel slice of an NCHW tensor: rows = N,
+ * cols = C_slice*H*W, stride = C*H*W). In qa_d_requantize, `sub` is
+ * subtracted from the stored accumulator before the bias. */
 int qa_d_requantize(const void* acc, int acc_code, void* out, int out_code,
                     int64_t outer, int64_t C, int64_t inner,
                     const int64_t* mult, const int64_t* shift,
                     const int64_t* pre_bias, const int64_t* post_bias,
                     int64_t zp, int64_t qmin, int64_t qmax, int64_t sub,
                     int64_t out_so, void* stream);
-int qa_d_rescale(const void* x, int in_code, void* out, int out_code,
-                 int64_t n, int64_t zp_in, int64_t m, int64_t s,
+int qa_d_rescale(const void* x, int in_code, int64_t x_rstride, void* out,
+                 int out_code, int64_t out_rstride, int64_t rows,
+                 int64_t cols, int64_t zp_in, int64_t m, int64_t s,
                  int64_t zp_out, int64_t qmin, int64_t qmax, int64_t in_so,
                  int64_t out_so, void* stream);
-int qa_d_add(const void* a, const void* b, int in_code, void* out,
-             int out_code, int64_t n, int64_t za, int64_t ma, int64_t sa,
-             int64_t zb, int64_t mb, int64_t sb, int64_t sign, int64_t zp_out,
-             int64_t qmin, int64_t qmax, int64_t a_so, int64_t b_so,
-             int64_t out_so, void* stream);
-int qa_d_mul(const void* a, const void* b, int in_code, void* out,
-             int out_code, int64_t n, int64_t za, int64_t zb, int64_t m,
-             int64_t s, int64_t zp_out, int64_t qmin, int64_t qmax,
+int qa_d_add(const void* a, int64_t a_rstride, const void* b,
+             int64_t b_rstride, int in_code, void* out, int out_code,
+             int64_t out_rstride, int64_t rows, int64_t cols, int64_t za,
+             int64_t ma, int64_t sa, int64_t zb, int64_t mb, int64_t sb,
+             int64_t sign, int64_t zp_out, int64_t qmin, int64_t qmax,
              int64_t a_so, int64_t b_so, int64_t out_so, void* stream);
-int qa_d_lut(const void* x, int in_code, void* out, int out_code, int64_t n,
+int qa_d_mul(const void* a, int64_t a_rstride, const void* b,
+             int64_t b_rstride, int in_code, void* out, int out_code,
+             int64_t out_rstride, int64_t rows, int64_t cols, int64_t za,
+             int64_t zb, int64_t m, int64_t s, int64_t zp_out, int64_t qmin,
+             int64_t qmax, int64_t a_so, int64_t b_so, int64_t out_so,
+             void* stream);
+int qa_d_lut(const void* x, int in_code, int64_t x_rstride, void* out,
+             int out_code, int64_t out_rstride, int64_t rows, int64_t cols,
              int64_t offset, const int32_t* lut, int64_t lut_len,
              int64_t in_so, int64_t out_so, void* stream);
 int qa_d_quantize_f32(const float* x, void* q, int out_code, int64_t n,
@@ -189,6 +197,23 @@ int qa_d_quantize_f32(const float* x, void* q, int out_code, int64_t n,
 int qa_d_dequantize_f32(const void* q, int in_code, float* x, int64_t n,
                         double scale, int64_t zp, int64_t in_so,
                         void* stream);
+
+/* GlobalAveragePool of x [N, C, HW] (image stride x_nstride) into out
+ * [N, C]: clip(mbqm(sum(q - zp_in), mult, shift) + zp_out)
+ * (quant_layers.py:563-590). */
+int qa_d_gap(const void* x, int in_code, int64_t x_nstride, int64_t N,
+             int64_t C, int64_t HW, int64_t zp_in, int64_t in_so,
+             int64_t mult, int64_t shift, int64_t zp_out, int64_t qmin,
+             int64_t qmax, void* out, int out_code, int64_t out_so,
+             void* stream);
+
+/* Float fallback of Softmax over the last axis of [rows, cols]:
+ * dequantize to float32, softmax in float64, float32, quantize
+ * (quant_layers.py:195-205, float_ops.py:380-385). */
+int qa_d_softmax(const void* x, int in_code, int64_t rows, int64_t cols,
+                 double in_scale, int64_t in_zp, int64_t in_so, void* out,
+                 int out_code, double out_scale, int64_t out_zp, int64_t qmin,
+                 int64_t qmax, int64_t out_so, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,159 @@
+"""Float operator semantics needed by the oracle pipeline (test only).
+
+Restated from the reference's ``quantization/float_ops.py`` for the ops that
+feed integer parameters (lookup tables are built by evaluating these on every
+quantized input value) or run as float fallbacks:
+Sigmoid / Exp / Softplus in float64 cast to float32 (``float_ops.py:225-227``
+and neighbours), HardSwish / HardSigmoid / LeakyRelu / Elu / Tanh / Relu,
+Abramowitz-Stegun erf and Gelu (``:289-320``), binary element-wise ops in
+NumPy's promotion, Softmax and LayerNorm in float64 (``:336-347``,
+``:380-385``), and the integer-safe shaping ops.
+"""
+
+import numpy as np
+from numpy.lib.stride_tricks import sliding_window_view
+
+
+def _f32(a):
+    return np.asarray(a).astype(np.float32)
+
+
+def _erf(x):
+    x = x.astype(np.float64)
+    a = np.abs(x)
+    t = 1.0 / (1.0 + 0.3275911 * a)
+    p = t * (0.254829592 + t * (-0.284496736 + t * (1.421413741 + t * (
+        -1.453152027 + t * 1.061405429))))
+    return np.sign(x) * (1.0 - p * np.exp(-a * a))
+
+
+UNARY = {
+    "Sigmoid": lambda n, x: _f32(1.0 / (1.0 + np.exp(-x.astype(np.float64)))),
+    "Relu": lambda n, x: np.maximum(x, 0),
+    "LeakyRelu": lambda n, x: _f32(np.where(x >= 0, x,
+                                            n.attr("alpha", 0.01) * x)),
+    "Tanh": lambda n, x: _f32(np.tanh(x)),
+    "HardSigmoid": lambda n, x: _f32(np.clip(
+        n.attr("alpha", 0.2) * x + n.attr("beta", 0.5), 0, 1)),
+    "HardSwish": lambda n, x: _f32(x * np.clip(x / 6.0 + 0.5, 0, 1)),
+    "Elu": lambda n, x: _f32(np.where(
+        x > 0, x, n.attr("alpha", 1.0) * np.expm1(np.minimum(x, 0)))),
+    "Softplus": lambda n, x: _f32(np.logaddexp(0, x.astype(np.float64))),
+    "Abs": lambda n, x: np.abs(x),
+    "Neg": lambda n, x: -x,
+    "Sqrt": lambda n, x: _f32(np.sqrt(x)),
+    "Exp": lambda n, x: _f32(np.exp(x.astype(np.float64))),
+    "Erf": lambda n, x: _f32(_erf(x)),
+}
+
+
+def _gelu(node, x):
+    x = x.astype(np.float64)
+    if node.attr("approximate", "none") == "tanh":
+        return _f32(0.5 * x * (1 + np.tanh(np.sqrt(2 / np.pi) * (
+            x + 0.044715 * x**3))))
+    return _f32(0.5 * x * (1 + _erf(x / np.sqrt(2))))
+
+
+UNARY["Gelu"] = _gelu
+
+BINARY = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply,
+          "Div": np.divide, "Max": np.maximum, "Min": np.minimum}
+
+
+def softmax(x, axis):
+    x = x.astype(np.float64)
+    e = np.exp(x - x.max(axis=axis, keepdims=True))
+    return _f32(e / e.sum(axis=axis, keepdims=True))
+
+
+def layer_norm(x, gamma, beta, axis, eps):
+    x = x.astype(np.float64)
+    axes = tuple(range(axis, x.ndim))
+    m = x.mean(axis=axes, keepdims=True)
+    v = ((x - m) ** 2).mean(axis=axes, keepdims=True)
+    y = (x - m) / np.sqrt(v + eps) * gamma
+    return _f32(y + beta if beta is not None else y)
+
+
+def eval_node(node, args, opset=13, pad_value=None):
+    """Evaluates one node on NumPy arrays; returns the list of outputs."""
+    op = node.op_type
+    if op in UNARY:
+        return [UNARY[op](node, args[0])]
+    if op in BINARY:
+        return [BINARY[op](args[0], args[1])]
+    if op == "Pow":
+        return [_f32(np.power(args[0].astype(np.float64),
+                              np.asarray(args[1]).astype(np.float64)))]
+    if op == "Clip":
+        lo = args[1] if len(args) > 1 and args[1] is not None \
+            else node.attr("min")
+        hi = args[2] if len(args) > 2 and args[2] is not None \
+            else node.attr("max")
+        return [np.clip(args[0], lo, hi)]
+    if op == "FusedElementwise":
+        env = dict(node.attrs["consts"])
+        env[node.inputs[0]] = args[0]
+        for sub in node.attrs["nodes"]:
+            env[sub.outputs[0]] = eval_node(
+                sub, [env[i] if i else None for i in sub.inputs], opset)[0]
+        return [env[node.outputs[0]]]
+    if op == "Softmax":
+        ax = node.attr("axis", -1 if opset >= 13 else 1)
+        return [softmax(args[0], ax + args[0].ndim if ax < 0 else ax)]
+    if op == "LayerNormalization":
+        ax = node.attr("axis", -1)
+        return [layer_norm(args[0], args[1], args[2] if len(args) > 2
+                           else None, ax + args[0].ndim if ax < 0 else ax,
+                           node.attr("epsilon", 1e-5))]
+    if op == "Split":
+        x = args[0]
+        ax = node.attr("axis", 0)
+        ax = ax + x.ndim if ax < 0 else ax
+        sizes = (np.asarray(args[1]).astype(np.int64).tolist()
+                 if len(args) > 1 and args[1] is not None
+                 else node.attr("split"))
+        if not sizes:
+            sizes = [x.shape[ax] // len(node.outputs)] * len(node.outputs)
+        return list(np.split(x, np.cumsum(sizes)[:-1], axis=ax))
+    if op == "Flatten":
+        x = args[0]
+        ax = node.attr("axis", 1)
+        ax = ax + x.ndim if ax < 0 else ax
+        return [x.reshape(int(np.prod(x.shape[:ax])), -1)]
+    if op == "Reshape":
+        shape = [int(s) for s in np.asarray(args[1]).reshape(-1)]
+        if not node.attr("allowzero", 0):
+            shape = [args[0].shape[i] if s == 0 else s
+                     for i, s in enumerate(shape)]
+        return [args[0].reshape(shape)]
+    if op == "Transpose":
+        perm = node.attr("perm")
+        return [np.transpose(args[0], perm if perm else None)]
+    if op == "Concat":
+        return [np.concatenate(args, axis=node.attr("axis"))]
+    if op == "GlobalAveragePool":
+        x = args[0]
+        return [_f32(x.mean(axis=tuple(range(2, x.ndim)), keepdims=True))]
+    if op == "Pad":
+        x = args[0]
+        pads = (np.asarray(args[1]).astype(np.int64).tolist()
+                if len(args) > 1 and args[1] is not None
+                else node.attr("pads"))
+        value = pad_value if pad_value is not None else node.attr("value", 0)
+        n = x.ndim
+        return [np.pad(x, [(pads[i], pads[i + n]) for i in range(n)],
+                       constant_values=value)]
+    if op == "MaxPool":
+        x = args[0]
+        k = tuple(node.attr("kernel_shape"))
+        s = tuple(node.attr("strides", [1, 1]))
+        p = node.attr("pads", [0, 0, 0, 0])
+        value = pad_value if pad_value is not None else (
+            -np.inf if x.dtype.kind == "f" else np.iinfo(x.dtype).min)
+        xp = np.pad(x, ((0, 0), (0, 0), (p[0], p[2]), (p[1], p[3])),
+                    constant_values=value)
+        win = sliding_window_view(xp, k, axis=(2, 3))[:, :, ::s[0], ::s[1]]
+        return [win.max(axis=(4, 5))]
+    raise NotImplementedError(f"oracle has no float semantics for {op}")

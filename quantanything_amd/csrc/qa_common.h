@@ -59,6 +59,19 @@ __host__ __device__ __forceinline__ int64_t qa_clip128(qa_i128 v, int64_t lo,
     return (int64_t)v;
 }
 
+// q = clip(nearbyint(double(x) / scale) + zp) with IEEE double division and
+// round-half-even; NaN -> INT32_MIN, which is what the reference's
+// double -> int32 conversion yields on x86-64 (qa_kernels.cpp:363-376).
+__device__ __forceinline__ int64_t qa_quantize_one(float x, double scale,
+                                                   int64_t zp, int64_t qmin,
+                                                   int64_t qmax) {
+    double v = rint((double)x / scale) + (double)zp;
+    if (v != v) return INT32_MIN;
+    if (v < (double)qmin) v = (double)qmin;
+    if (v > (double)qmax) v = (double)qmax;
+    return (int64_t)(int32_t)v;
+}
+
 // --------------------------------------------------------------- errors ---
 namespace qa {
 

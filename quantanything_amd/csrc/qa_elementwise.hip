@@ -5,6 +5,8 @@
 // Host-pointer exports replace the reference's (qa_kernels.cpp:287-386) with
 // identical signatures and results; qa_d_* exports take device pointers, a
 // stream, and the int8/int16 storage form used by the resident executor.
+#include <algorithm>
+
 #include "qa_common.h"
 
 namespace {
@@ -39,77 +41,77 @@ __global__ __launch_bounds__(kThreads) void k_requant(
     }
 }
 
+// Row-strided element-wise kernels: `rows` rows of `cols` elements, each
+// operand with its own row stride (a channel slice of an NCHW tensor is
+// rows = N, cols = C_slice*H*W, stride = C*H*W). grid.y walks the rows.
+#define QA_ROW_LOOP                                                         \
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y)                  \
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;    \
+             i < cols; i += (int64_t)gridDim.x * blockDim.x)
+
 template <class TIn, class TOut>
 __global__ __launch_bounds__(kThreads) void k_rescale(
-    const TIn* __restrict__ x, TOut* __restrict__ out, int64_t n,
-    int64_t zp_in, int64_t m, int64_t s, int64_t zp_out, int64_t qmin,
-    int64_t qmax, int64_t in_so, int64_t out_so) {
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += step) {
+    const TIn* __restrict__ x, int64_t xs, TOut* __restrict__ out,
+    int64_t os, int64_t rows, int64_t cols, int64_t zp_in, int64_t m,
+    int64_t s, int64_t zp_out, int64_t qmin, int64_t qmax, int64_t in_so,
+    int64_t out_so) {
+    QA_ROW_LOOP {
         const qa_i128 v =
-            qa_mbqm_fast((int64_t)x[i] + in_so - zp_in, m, s) + zp_out;
-        out[i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
+            qa_mbqm_fast((int64_t)x[r * xs + i] + in_so - zp_in, m, s) +
+            zp_out;
+        out[r * os + i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
     }
 }
 
 template <class TIn, class TOut>
 __global__ __launch_bounds__(kThreads) void k_add(
-    const TIn* __restrict__ a, const TIn* __restrict__ b,
-    TOut* __restrict__ out, int64_t n, int64_t za, int64_t ma, int64_t sa,
-    int64_t zb, int64_t mb, int64_t sb, int64_t sign, int64_t zp_out,
-    int64_t qmin, int64_t qmax, int64_t a_so, int64_t b_so, int64_t out_so) {
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += step) {
-        const qa_i128 v = qa_mbqm_fast((int64_t)a[i] + a_so - za, ma, sa) +
-                          (qa_i128)sign *
-                              qa_mbqm_fast((int64_t)b[i] + b_so - zb, mb, sb) +
-                          zp_out;
-        out[i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
+    const TIn* __restrict__ a, int64_t as, const TIn* __restrict__ b,
+    int64_t bs, TOut* __restrict__ out, int64_t os, int64_t rows,
+    int64_t cols, int64_t za, int64_t ma, int64_t sa, int64_t zb, int64_t mb,
+    int64_t sb, int64_t sign, int64_t zp_out, int64_t qmin, int64_t qmax,
+    int64_t a_so, int64_t b_so, int64_t out_so) {
+    QA_ROW_LOOP {
+        const qa_i128 v =
+            qa_mbqm_fast((int64_t)a[r * as + i] + a_so - za, ma, sa) +
+            (qa_i128)sign *
+                qa_mbqm_fast((int64_t)b[r * bs + i] + b_so - zb, mb, sb) +
+            zp_out;
+        out[r * os + i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
     }
 }
 
 template <class TIn, class TOut>
 __global__ __launch_bounds__(kThreads) void k_mul(
-    const TIn* __restrict__ a, const TIn* __restrict__ b,
-    TOut* __restrict__ out, int64_t n, int64_t za, int64_t zb, int64_t m,
-    int64_t s, int64_t zp_out, int64_t qmin, int64_t qmax, int64_t a_so,
-    int64_t b_so, int64_t out_so) {
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += step) {
-        const int64_t p =
-            ((int64_t)a[i] + a_so - za) * ((int64_t)b[i] + b_so - zb);
+    const TIn* __restrict__ a, int64_t as, const TIn* __restrict__ b,
+    int64_t bs, TOut* __restrict__ out, int64_t os, int64_t rows,
+    int64_t cols, int64_t za, int64_t zb, int64_t m, int64_t s,
+    int64_t zp_out, int64_t qmin, int64_t qmax, int64_t a_so, int64_t b_so,
+    int64_t out_so) {
+    QA_ROW_LOOP {
+        const int64_t p = ((int64_t)a[r * as + i] + a_so - za) *
+                          ((int64_t)b[r * bs + i] + b_so - zb);
         const qa_i128 v = qa_mbqm_fast(p, m, s) + zp_out;
-        out[i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
+        out[r * os + i] = (TOut)(qa_clip128(v, qmin, qmax) - out_so);
     }
 }
 
 template <class TIn, class TOut>
 __global__ __launch_bounds__(kThreads) void k_lut(
-    const TIn* __restrict__ x, TOut* __restrict__ out, int64_t n,
-    int64_t offset, const int32_t* __restrict__ lut, int64_t len,
-    int64_t in_so, int64_t out_so) {
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += step) {
-        int64_t idx = (int64_t)x[i] + in_so - offset;
+    const TIn* __restrict__ x, int64_t xs, TOut* __restrict__ out,
+    int64_t os, int64_t rows, int64_t cols, int64_t offset,
+    const int32_t* __restrict__ lut, int64_t len, int64_t in_so,
+    int64_t out_so) {
+    QA_ROW_LOOP {
+        int64_t idx = (int64_t)x[r * xs + i] + in_so - offset;
         idx = idx < 0 ? 0 : (idx >= len ? len - 1 : idx);
-        out[i] = (TOut)((int64_t)lut[idx] - out_so);
+        out[r * os + i] = (TOut)((int64_t)lut[idx] - out_so);
     }
 }
 
-// q = clip(rint(double(x) / scale) + zp); NaN -> INT32_MIN (what the
-// reference's double -> int32 conversion yields on x86-64).
 __device__ __forceinline__ int64_t quantize_one(float x, double scale,
                                                 int64_t zp, int64_t qmin,
                                                 int64_t qmax) {
-    double v = rint((double)x / scale) + (double)zp;
-    if (v != v) return INT32_MIN;
-    if (v < (double)qmin) v = (double)qmin;
-    if (v > (double)qmax) v = (double)qmax;
-    return (int64_t)(int32_t)v;
+    return qa_quantize_one(x, scale, zp, qmin, qmax);
 }
 
 template <class TOut>
@@ -252,7 +254,7 @@ QA_API void qa_rescale(const int32_t* x, int32_t* out, int64_t n,
     int32_t* dy = (int32_t*)qa::scratch(1, (size_t)n * 4);
     if (!dx || !dy) return;
     k_rescale<int32_t, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
-        dx, dy, n, zp_in, m, s, zp_out, qmin, qmax, 0, 0);
+        dx, n, dy, n, 1, n, zp_in, m, s, zp_out, qmin, qmax, 0, 0);
     if (!launched("k_rescale")) return;
     download(out, dy, (size_t)n * 4, st);
 }
@@ -270,8 +272,8 @@ QA_API void qa_add(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
     int32_t* dy = (int32_t*)qa::scratch(1, (size_t)n * 4);
     if (!da || !db || !dy) return;
     k_add<int32_t, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
-        da, db, dy, n, za, ma, sa, zb, mb, sb, sign, zp_out, qmin, qmax, 0, 0,
-        0);
+        da, n, db, n, dy, n, 1, n, za, ma, sa, zb, mb, sb, sign, zp_out, qmin,
+        qmax, 0, 0, 0);
     if (!launched("k_add")) return;
     download(out, dy, (size_t)n * 4, st);
 }
@@ -288,7 +290,7 @@ QA_API void qa_mul(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
     int32_t* dy = (int32_t*)qa::scratch(1, (size_t)n * 4);
     if (!da || !db || !dy) return;
     k_mul<int32_t, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
-        da, db, dy, n, za, zb, m, s, zp_out, qmin, qmax, 0, 0, 0);
+        da, n, db, n, dy, n, 1, n, za, zb, m, s, zp_out, qmin, qmax, 0, 0, 0);
     if (!launched("k_mul")) return;
     download(out, dy, (size_t)n * 4, st);
 }
@@ -304,7 +306,7 @@ QA_API void qa_lut(const int32_t* x, int32_t* out, int64_t n, int64_t offset,
     int32_t* dy = (int32_t*)qa::scratch(1, (size_t)n * 4);
     if (!dx || !dl || !dy) return;
     k_lut<int32_t, int32_t><<<qa::grid_1d(n, kThreads), kThreads, 0, st>>>(
-        dx, dy, n, offset, dl, lut_len, 0, 0);
+        dx, n, dy, n, 1, n, offset, dl, lut_len, 0, 0);
     if (!launched("k_lut")) return;
     download(out, dy, (size_t)n * 4, st);
 }
@@ -380,65 +382,77 @@ QA_API int qa_d_requantize(const void* acc, int acc_code, void* out,
     return launched("qa_d_requantize") ? 0 : -1;
 }
 
-QA_API int qa_d_rescale(const void* x, int in_code, void* out, int out_code,
-                        int64_t n, int64_t zp_in, int64_t m, int64_t s,
-                        int64_t zp_out, int64_t qmin, int64_t qmax,
+static dim3 grid_rows(int64_t rows, int64_t cols) {
+    return dim3(qa::grid_1d(cols, kThreads, 1 << 16),
+                (unsigned)std::min<int64_t>(std::max<int64_t>(rows, 1), 65535));
+}
+
+QA_API int qa_d_rescale(const void* x, int in_code, int64_t x_rstride,
+                        void* out, int out_code, int64_t out_rstride,
+                        int64_t rows, int64_t cols, int64_t zp_in, int64_t m,
+                        int64_t s, int64_t zp_out, int64_t qmin, int64_t qmax,
                         int64_t in_so, int64_t out_so, void* stream) {
-    if (n <= 0) return 0;
+    if (rows <= 0 || cols <= 0) return 0;
     hipStream_t st = pick(stream);
-    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    const dim3 g = grid_rows(rows, cols);
     QA_DISPATCH_STORAGE(in_code, TI,
         QA_DISPATCH_STORAGE(out_code, TO,
             k_rescale<TI, TO><<<g, kThreads, 0, st>>>(
-                (const TI*)x, (TO*)out, n, zp_in, m, s, zp_out, qmin, qmax,
-                in_so, out_so)))
+                (const TI*)x, x_rstride, (TO*)out, out_rstride, rows, cols,
+                zp_in, m, s, zp_out, qmin, qmax, in_so, out_so)))
     return launched("qa_d_rescale") ? 0 : -1;
 }
 
-QA_API int qa_d_add(const void* a, const void* b, int in_code, void* out,
-                    int out_code, int64_t n, int64_t za, int64_t ma,
-                    int64_t sa, int64_t zb, int64_t mb, int64_t sb,
-                    int64_t sign, int64_t zp_out, int64_t qmin, int64_t qmax,
-                    int64_t a_so, int64_t b_so, int64_t out_so, void* stream) {
-    if (n <= 0) return 0;
+QA_API int qa_d_add(const void* a, int64_t a_rstride, const void* b,
+                    int64_t b_rstride, int in_code, void* out, int out_code,
+                    int64_t out_rstride, int64_t rows, int64_t cols,
+                    int64_t za, int64_t ma, int64_t sa, int64_t zb,
+                    int64_t mb, int64_t sb, int64_t sign, int64_t zp_out,
+                    int64_t qmin, int64_t qmax, int64_t a_so, int64_t b_so,
+                    int64_t out_so, void* stream) {
+    if (rows <= 0 || cols <= 0) return 0;
     hipStream_t st = pick(stream);
-    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    const dim3 g = grid_rows(rows, cols);
     QA_DISPATCH_STORAGE(in_code, TI,
         QA_DISPATCH_STORAGE(out_code, TO,
             k_add<TI, TO><<<g, kThreads, 0, st>>>(
-                (const TI*)a, (const TI*)b, (TO*)out, n, za, ma, sa, zb, mb,
-                sb, sign, zp_out, qmin, qmax, a_so, b_so, out_so)))
+                (const TI*)a, a_rstride, (const TI*)b, b_rstride, (TO*)out,
+                out_rstride, rows, cols, za, ma, sa, zb, mb, sb, sign, zp_out,
+                qmin, qmax, a_so, b_so, out_so)))
     return launched("qa_d_add") ? 0 : -1;
 }
 
-QA_API int qa_d_mul(const void* a, const void* b, int in_code, void* out,
-                    int out_code, int64_t n, int64_t za, int64_t zb,
-                    int64_t m, int64_t s, int64_t zp_out, int64_t qmin,
-                    int64_t qmax, int64_t a_so, int64_t b_so, int64_t out_so,
-                    void* stream) {
-    if (n <= 0) return 0;
+QA_API int qa_d_mul(const void* a, int64_t a_rstride, const void* b,
+                    int64_t b_rstride, int in_code, void* out, int out_code,
+                    int64_t out_rstride, int64_t rows, int64_t cols,
+                    int64_t za, int64_t zb, int64_t m, int64_t s,
+                    int64_t zp_out, int64_t qmin, int64_t qmax, int64_t a_so,
+                    int64_t b_so, int64_t out_so, void* stream) {
+    if (rows <= 0 || cols <= 0) return 0;
     hipStream_t st = pick(stream);
-    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    const dim3 g = grid_rows(rows, cols);
     QA_DISPATCH_STORAGE(in_code, TI,
         QA_DISPATCH_STORAGE(out_code, TO,
             k_mul<TI, TO><<<g, kThreads, 0, st>>>(
-                (const TI*)a, (const TI*)b, (TO*)out, n, za, zb, m, s, zp_out,
-                qmin, qmax, a_so, b_so, out_so)))
+                (const TI*)a, a_rstride, (const TI*)b, b_rstride, (TO*)out,
+                out_rstride, rows, cols, za, zb, m, s, zp_out, qmin, qmax,
+                a_so, b_so, out_so)))
     return launched("qa_d_mul") ? 0 : -1;
 }
 
-QA_API int qa_d_lut(const void* x, int in_code, void* out, int out_code,
-                    int64_t n, int64_t offset, const int32_t* lut,
+QA_API int qa_d_lut(const void* x, int in_code, int64_t x_rstride, void* out,
+                    int out_code, int64_t out_rstride, int64_t rows,
+                    int64_t cols, int64_t offset, const int32_t* lut,
                     int64_t lut_len, int64_t in_so, int64_t out_so,
                     void* stream) {
-    if (n <= 0) return 0;
+    if (rows <= 0 || cols <= 0) return 0;
     hipStream_t st = pick(stream);
-    const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
+    const dim3 g = grid_rows(rows, cols);
     QA_DISPATCH_STORAGE(in_code, TI,
         QA_DISPATCH_STORAGE(out_code, TO,
             k_lut<TI, TO><<<g, kThreads, 0, st>>>(
-                (const TI*)x, (TO*)out, n, offset, lut, lut_len, in_so,
-                out_so)))
+                (const TI*)x, x_rstride, (TO*)out, out_rstride, rows, cols,
+                offset, lut, lut_len, in_so, out_so)))
     return launched("qa_d_lut") ? 0 : -1;
 }
 

@@ -207,7 +207,8 @@ __global__ __launch_bounds__(256) void k_igemm(IgemmArgs a) {
             if (MODE == EPI_QUANT) {
                 const bool has_res = a.res != nullptr;
                 const bool vec4 = a.out_code == 1 && (OHW & 3) == 0 &&
-                                  pb + 3 < a.M;
+                                  pb + 3 < a.M && (a.y_nstride & 3) == 0 &&
+                                  (((uintptr_t)a.y) & 3) == 0;
                 int64_t q[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {

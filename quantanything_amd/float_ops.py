@@ -1,0 +1,382 @@
+"""Float semantics of the graph's operators (reference: ``float_ops.py``).
+
+Used for calibration (min/max of every tensor), for building activation
+lookup tables (``prepare`` of LUT layers evaluates the op on every quantized
+input value) and by the float fallback of the integer path. The element-wise
+numerics follow the reference exactly where they feed integer parameters:
+Sigmoid / Exp / Softplus in float64 cast to float32 (``float_ops.py:225-227``
+and around), HardSwish / HardSigmoid / LeakyRelu / Elu formulas, the
+Abramowitz-Stegun ``erf`` (``float_ops.py:289-304``), float64 Softmax and
+LayerNorm (``:336-347``, ``:380-385``).
+
+Conv and Gemm run on the GPU through ``native.conv2d_f32`` /
+``native.gemm_f32`` (the float entries of the same library).
+"""
+
+import numpy as np
+from numpy.lib.stride_tricks import sliding_window_view
+
+from quantanything_amd import native
+
+OPS = {}
+UNARY = {}
+
+
+class UnsupportedOp(NotImplementedError):
+    """An operator without a float implementation here."""
+
+
+def _reg(*names):
+    def deco(fn):
+        for n in names:
+            OPS[n] = fn
+        return fn
+    return deco
+
+
+def _unary(name):
+    def deco(fn):
+        UNARY[name] = fn
+        OPS[name] = lambda node, ins, opset, **kw: fn(node, ins[0])
+        return fn
+    return deco
+
+
+def run_node(node, inputs, opset=13, **kw):
+    fn = OPS.get(node.op_type)
+    if fn is None:
+        raise UnsupportedOp(f"operator {node.op_type} ({node.name}) has no "
+                            "float implementation")
+    out = fn(node, inputs, opset, **kw)
+    return list(out) if isinstance(out, (list, tuple)) else [out]
+
+
+def normalize_feeds(graph, feeds):
+    if not isinstance(feeds, dict):
+        names = graph.input_names
+        if len(names) != 1:
+            raise ValueError(f"model has {len(names)} inputs; pass a dict "
+                             f"keyed by {names}")
+        feeds = {names[0]: feeds}
+    return {k: np.asarray(v, dtype=np.float32) for k, v in feeds.items()}
+
+
+def run_float(graph, feeds, keep_all=False):
+    env = dict(graph.initializers)
+    env.update(normalize_feeds(graph, feeds))
+    for node in graph.nodes:
+        outs = run_node(node, [env[i] if i else None for i in node.inputs],
+                        graph.opset)
+        env.update(zip(node.outputs, outs))
+    if keep_all:
+        return env
+    res = [env[o] for o in graph.outputs]
+    return res[0] if len(res) == 1 else res
+
+
+def conv_pads(node, in_hw, kernel, strides, dilations):
+    """``pads`` / ``auto_pad`` -> ``(top, left, bottom, right)``
+    (``float_ops.py:132-146``)."""
+    auto = node.attr("auto_pad", "NOTSET")
+    if auto in ("SAME_UPPER", "SAME_LOWER"):
+        res = []
+        for size, k, s, d in zip(in_hw, kernel, strides, dilations):
+            out = -(-size // s)
+            total = max((out - 1) * s + d * (k - 1) + 1 - size, 0)
+            lo, hi = total // 2, total - total // 2
+            res.append((lo, hi) if auto == "SAME_UPPER" else (hi, lo))
+        return (res[0][0], res[1][0], res[0][1], res[1][1])
+    if auto == "VALID":
+        return (0, 0, 0, 0)
+    p = node.attr("pads", [0] * 4)
+    return (p[0], p[1], p[2], p[3])
+
+
+def conv_geometry(node, x_shape, w_shape):
+    strides = tuple(node.attr("strides", [1, 1]))
+    dilations = tuple(node.attr("dilations", [1, 1]))
+    pads = conv_pads(node, x_shape[2:], w_shape[2:], strides, dilations)
+    return strides, pads, dilations, node.attr("group", 1)
+
+
+# ------------------------------------------------------------- linear ----
+@_reg("Conv")
+def _conv(node, ins, opset, **kw):
+    x, w = ins[0], ins[1]
+    if x.ndim != 4:
+        raise UnsupportedOp("only 2-D convolution is supported")
+    y = native.conv2d_f32(x, w, *conv_geometry(node, x.shape, w.shape))
+    if len(ins) > 2 and ins[2] is not None:
+        y = y + ins[2].reshape(1, -1, 1, 1)
+    return y
+
+
+@_reg("Gemm")
+def _gemm(node, ins, opset, **kw):
+    a, b = ins[0], ins[1]
+    if node.attr("transA", 0):
+        a = a.T
+    if node.attr("transB", 0):
+        b = b.T
+    y = np.float32(node.attr("alpha", 1.0)) * native.gemm_f32(a, b)
+    if len(ins) > 2 and ins[2] is not None:
+        y = y + np.float32(node.attr("beta", 1.0)) * ins[2]
+    return y.astype(np.float32)
+
+
+@_reg("MatMul")
+def _matmul(node, ins, opset, **kw):
+    y = np.matmul(ins[0], ins[1]).astype(np.float32)
+    if len(ins) > 2 and ins[2] is not None:
+        y = y + ins[2]
+    return y
+
+
+@_reg("FusedElementwise")
+def _fused(node, ins, opset, **kw):
+    env = dict(node.attrs["consts"])
+    env[node.inputs[0]] = ins[0]
+    for sub in node.attrs["nodes"]:
+        env[sub.outputs[0]] = run_node(
+            sub, [env[i] if i else None for i in sub.inputs], opset)[0]
+    return env[node.outputs[0]]
+
+
+@_reg("BatchNormalization")
+def _bn(node, ins, opset, **kw):
+    x, gamma, beta, mean, var = ins[:5]
+    shape = [1, -1] + [1] * (x.ndim - 2)
+    a = gamma / np.sqrt(var + node.attr("epsilon", 1e-5))
+    return (x * a.reshape(shape) + (beta - a * mean).reshape(shape)).astype(
+        np.float32)
+
+
+# ------------------------------------------------------- element-wise ----
+for _name, _fn in (("Add", np.add), ("Sub", np.subtract),
+                   ("Mul", np.multiply), ("Div", np.divide),
+                   ("Max", np.maximum), ("Min", np.minimum)):
+    OPS[_name] = (lambda f: lambda node, ins, opset, **kw: f(ins[0], ins[1]))(
+        _fn)
+
+
+@_unary("Sigmoid")
+def _sigmoid(node, x):
+    return (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+
+
+@_unary("Relu")
+def _relu(node, x):
+    return np.maximum(x, 0)
+
+
+@_unary("LeakyRelu")
+def _leaky(node, x):
+    return np.where(x >= 0, x, node.attr("alpha", 0.01) * x).astype(
+        np.float32)
+
+
+@_unary("Tanh")
+def _tanh(node, x):
+    return np.tanh(x).astype(np.float32)
+
+
+@_unary("HardSigmoid")
+def _hsig(node, x):
+    a, b = node.attr("alpha", 0.2), node.attr("beta", 0.5)
+    return np.clip(a * x + b, 0, 1).astype(np.float32)
+
+
+@_unary("HardSwish")
+def _hswish(node, x):
+    return (x * np.clip(x / 6.0 + 0.5, 0, 1)).astype(np.float32)
+
+
+@_unary("Elu")
+def _elu(node, x):
+    a = node.attr("alpha", 1.0)
+    return np.where(x > 0, x, a * np.expm1(np.minimum(x, 0))).astype(
+        np.float32)
+
+
+@_unary("Softplus")
+def _softplus(node, x):
+    return np.logaddexp(0, x.astype(np.float64)).astype(np.float32)
+
+
+@_unary("Abs")
+def _abs(node, x):
+    return np.abs(x)
+
+
+@_unary("Neg")
+def _neg(node, x):
+    return -x
+
+
+@_unary("Sqrt")
+def _sqrt(node, x):
+    return np.sqrt(x).astype(np.float32)
+
+
+@_unary("Exp")
+def _exp(node, x):
+    return np.exp(x.astype(np.float64)).astype(np.float32)
+
+
+def erf(x):
+    """Abramowitz-Stegun 7.1.26 in float64 (the reference's ``_erf``)."""
+    x = x.astype(np.float64)
+    ax = np.abs(x)
+    t = 1.0 / (1.0 + 0.3275911 * ax)
+    poly = t * (0.254829592 + t * (-0.284496736 + t * (
+        1.421413741 + t * (-1.453152027 + t * 1.061405429))))
+    return np.sign(x) * (1.0 - poly * np.exp(-ax * ax))
+
+
+@_unary("Erf")
+def _erf(node, x):
+    return erf(x).astype(np.float32)
+
+
+@_unary("Gelu")
+def _gelu(node, x):
+    x64 = x.astype(np.float64)
+    if node.attr("approximate", "none") == "tanh":
+        inner = np.sqrt(2 / np.pi) * (x64 + 0.044715 * x64**3)
+        return (0.5 * x64 * (1 + np.tanh(inner))).astype(np.float32)
+    return (0.5 * x64 * (1 + erf(x64 / np.sqrt(2)))).astype(np.float32)
+
+
+@_reg("Pow")
+def _pow(node, ins, opset, **kw):
+    return np.power(ins[0].astype(np.float64),
+                    np.asarray(ins[1]).astype(np.float64)).astype(np.float32)
+
+
+@_reg("Clip")
+def _clip(node, ins, opset, **kw):
+    lo = ins[1] if len(ins) > 1 and ins[1] is not None else node.attr("min")
+    hi = ins[2] if len(ins) > 2 and ins[2] is not None else node.attr("max")
+    return np.clip(ins[0], lo, hi)
+
+
+def _axis(axis, ndim):
+    return axis + ndim if axis < 0 else axis
+
+
+@_reg("Softmax")
+def _softmax(node, ins, opset, **kw):
+    x = ins[0].astype(np.float64)
+    ax = _axis(node.attr("axis", -1 if opset >= 13 else 1), x.ndim)
+    e = np.exp(x - x.max(axis=ax, keepdims=True))
+    return (e / e.sum(axis=ax, keepdims=True)).astype(np.float32)
+
+
+@_reg("LayerNormalization")
+def _layer_norm(node, ins, opset, **kw):
+    x = ins[0].astype(np.float64)
+    axes = tuple(range(_axis(node.attr("axis", -1), x.ndim), x.ndim))
+    mean = x.mean(axis=axes, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=axes, keepdims=True)
+    y = (x - mean) / np.sqrt(var + node.attr("epsilon", 1e-5)) * ins[1]
+    if len(ins) > 2 and ins[2] is not None:
+        y = y + ins[2]
+    return y.astype(np.float32)
+
+
+# ------------------------------------------------------------- shapes ----
+@_reg("Identity", "Dropout")
+def _identity(node, ins, opset, **kw):
+    return ins[0]
+
+
+@_reg("Flatten")
+def _flatten(node, ins, opset, **kw):
+    x = ins[0]
+    ax = _axis(node.attr("axis", 1), x.ndim)
+    return x.reshape(int(np.prod(x.shape[:ax])), -1)
+
+
+@_reg("Reshape")
+def _reshape(node, ins, opset, **kw):
+    x = ins[0]
+    shape = [int(s) for s in np.asarray(ins[1]).reshape(-1)]
+    if not node.attr("allowzero", 0):
+        shape = [x.shape[i] if s == 0 else s for i, s in enumerate(shape)]
+    return x.reshape(shape)
+
+
+@_reg("Transpose")
+def _transpose(node, ins, opset, **kw):
+    perm = node.attr("perm")
+    return np.transpose(ins[0], perm if perm else None)
+
+
+@_reg("Concat")
+def _concat(node, ins, opset, **kw):
+    return np.concatenate(ins, axis=node.attr("axis"))
+
+
+@_reg("Split")
+def _split(node, ins, opset, **kw):
+    x = ins[0]
+    ax = _axis(node.attr("axis", 0), x.ndim)
+    if len(ins) > 1 and ins[1] is not None:
+        sizes = np.asarray(ins[1]).astype(np.int64).tolist()
+    else:
+        sizes = node.attr("split")
+    n_out = len(node.outputs)
+    if not sizes:
+        sizes = [x.shape[ax] // n_out] * n_out
+    return list(np.split(x, np.cumsum(sizes)[:-1], axis=ax))
+
+
+@_reg("GlobalAveragePool")
+def _gap(node, ins, opset, **kw):
+    x = ins[0]
+    return x.mean(axis=tuple(range(2, x.ndim)), keepdims=True).astype(
+        np.float32)
+
+
+@_reg("GlobalMaxPool")
+def _gmp(node, ins, opset, **kw):
+    x = ins[0]
+    return x.max(axis=tuple(range(2, x.ndim)), keepdims=True)
+
+
+@_reg("Pad")
+def _pad(node, ins, opset, pad_value=None, **kw):
+    x = ins[0]
+    pads = (np.asarray(ins[1]).astype(np.int64).tolist()
+            if len(ins) > 1 and ins[1] is not None else node.attr("pads"))
+    if pad_value is None:
+        pad_value = (np.asarray(ins[2]).reshape(()).item()
+                     if len(ins) > 2 and ins[2] is not None
+                     else node.attr("value", 0))
+    n = x.ndim
+    width = [(pads[i], pads[i + n]) for i in range(n)]
+    return np.pad(x, width, mode="constant", constant_values=pad_value)
+
+
+@_reg("MaxPool")
+def _maxpool(node, ins, opset, pad_value=None, **kw):
+    x = ins[0]
+    kernel = tuple(node.attr("kernel_shape"))
+    strides = tuple(node.attr("strides", [1] * len(kernel)))
+    dil = tuple(node.attr("dilations", [1] * len(kernel)))
+    pads = list(conv_pads(node, x.shape[2:], kernel, strides, dil))
+    if node.attr("ceil_mode", 0):
+        for ax in range(2):
+            size = x.shape[2 + ax] + pads[ax] + pads[ax + 2]
+            ek = dil[ax] * (kernel[ax] - 1) + 1
+            out = -(-(size - ek) // strides[ax]) + 1
+            pads[ax + 2] += max((out - 1) * strides[ax] + ek - size, 0)
+    if pad_value is None:
+        pad_value = (-np.inf if np.issubdtype(x.dtype, np.floating)
+                     else np.iinfo(x.dtype).min)
+    xp = np.pad(x, ((0, 0), (0, 0), (pads[0], pads[2]), (pads[1], pads[3])),
+                constant_values=pad_value)
+    ek = [d * (k - 1) + 1 for k, d in zip(kernel, dil)]
+    win = sliding_window_view(xp, tuple(ek), axis=(2, 3))
+    win = win[:, :, ::strides[0], ::strides[1], ::dil[0], ::dil[1]]
+    return win.max(axis=(4, 5))

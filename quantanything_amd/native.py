@@ -65,10 +65,14 @@ def _declare(lib):
         "qa_d_conv": (i32, [p, p]),
         "qa_d_requantize": (i32, [p, i32, p, i32] + [i64] * 3 + [p] * 4
                             + [i64] * 5 + [p]),
-        "qa_d_rescale": (i32, [p, i32, p, i32] + [i64] * 9 + [p]),
-        "qa_d_add": (i32, [p, p, i32, p, i32] + [i64] * 14 + [p]),
-        "qa_d_mul": (i32, [p, p, i32, p, i32] + [i64] * 11 + [p]),
-        "qa_d_lut": (i32, [p, i32, p, i32, i64, i64, p, i64, i64, i64, p]),
+        "qa_d_rescale": (i32, [p, i32, i64, p, i32] + [i64] * 11 + [p]),
+        "qa_d_add": (i32, [p, i64, p, i64, i32, p, i32] + [i64] * 16 + [p]),
+        "qa_d_mul": (i32, [p, i64, p, i64, i32, p, i32] + [i64] * 13 + [p]),
+        "qa_d_lut": (i32, [p, i32, i64, p, i32, i64, i64, i64, i64, p, i64,
+                           i64, i64, p]),
+        "qa_d_gap": (i32, [p, i32] + [i64] * 11 + [p, i32, i64, p]),
+        "qa_d_softmax": (i32, [p, i32, i64, i64, f64, i64, i64, p, i32, f64]
+                         + [i64] * 4 + [p]),
         "qa_d_quantize_f32": (i32, [p, p, i32, i64, f64, i64, i64, i64, i64,
                                     p]),
         "qa_d_dequantize_f32": (i32, [p, i32, p, i64, f64, i64, i64, p]),
@@ -85,9 +89,23 @@ def _declare(lib):
 SYMBOLS = None
 
 
+def _single_hip_runtime():
+    """PyTorch-ROCm ships its own ``libamdhip64.so`` with the same soname
+    (``libamdhip64.so.7``) as the system one the library was linked against.
+    Loading torch first makes the library bind to that already-loaded
+    runtime, so the process has ONE HIP runtime (device pointers and streams
+    are shared with torch); loading the library first would pull in a second
+    runtime that then fails to see the GPU."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def _load():
     global _lib, _load_error, SYMBOLS
     path = os.environ.get("QA_LIB") or str(DEFAULT_LIB)
+    _single_hip_runtime()
     try:
         lib = ctypes.CDLL(path)
         SYMBOLS = _declare(lib)
@@ -156,29 +174,12 @@ def _as_i64(v):
 
 # --------------------------------------------------- fixed-point multiply ----
 def mbqm_np(x, mult, shift):
-    """``round(x * mult * 2**-(31+shift))`` on the host with Python integers
-    beyond the int64-safe range (reference: ``native.py:177-203``). Host-side
-    parameter maths only; tensors go through the GPU kernels."""
-    x = _as_i64(x)
-    mult = _as_i64(mult)
-    ts = 31 + _as_i64(shift)
-    xm = int(np.max(np.abs(x))) if x.size else 0
-    mm = int(np.max(np.abs(mult))) if mult.size else 0
-    if xm * mm < (1 << 62):
-        product = x * mult
-        right = ts > 0
-        ts_r = np.where(right, ts, 1)
-        rounded = (product + (np.int64(1) << (ts_r - 1))) >> ts_r
-        left = product << np.where(right, 0, np.minimum(-ts, 60))
-        return np.where(right, rounded, left).astype(np.int64)
-    xb, mb, tb = np.broadcast_arrays(x, mult, ts)
-    out = np.empty(xb.shape, dtype=object)
-    res = out.ravel()
-    for i, (xi, mi, ti) in enumerate(zip(xb.ravel(), mb.ravel(), tb.ravel())):
-        p = int(xi) * int(mi)
-        t = int(ti)
-        res[i] = ((p + (1 << (t - 1))) >> t) if t > 0 else (p << -t)
-    return np.clip(out, -(1 << 62), 1 << 62).astype(np.int64)
+    """Host ``round(x * mult * 2**-(31+shift))`` (reference name kept; the
+    implementation is :func:`quantanything_amd.utils.
+    multiply_by_quantized_multiplier`)."""
+    from quantanything_amd.utils import multiply_by_quantized_multiplier
+
+    return multiply_by_quantized_multiplier(x, mult, shift)
 
 
 # ------------------------------------------------------------------ GEMM ----

@@ -1,0 +1,114 @@
+"""End-to-end integer inference on the GPU (device-resident executor) vs the
+oracle pipeline on the same graph, q.json and input. Integer outputs must be
+bit-exact; the float Softmax fallback may differ by one quantization step
+(float64 exp / summation order)."""
+
+import numpy as np
+import pytest
+
+from oracle.pipeline import OraclePipeline
+from quantanything_amd import graph as G
+from quantanything_amd.container import QuantContainer
+from quantanything_amd.synth import Stream
+
+pytestmark = pytest.mark.gpu
+
+
+def _images(seed, n, size, lo=0.0, hi=1.0):
+    return Stream(seed).uniform((n, 3, size, size), lo, hi).astype(np.float32)
+
+
+def _calibrated(g, quant_type, per_channel, batches):
+    c = QuantContainer(g, quant_type, per_channel)
+    c.calibrate(batches)
+    return c
+
+
+def _qjson(c, tmp_path):
+    path = tmp_path / "q.json"
+    c.save(path)
+    return path
+
+
+@pytest.mark.parametrize("per_channel", [True, False])
+@pytest.mark.parametrize("quant_type", ["int8", "uint8", "int16"])
+def test_mini_yolo_integer_bit_exact(hip, tmp_path, quant_type, per_channel):
+    g = G.mini_yolo(seed=0, softmax=False)
+    calib = [_images(1 + i, 4, 32) for i in range(3)]
+    c = _calibrated(g, quant_type, per_channel, calib)
+    x = calib[0]
+    got = c.integer_outputs(x)
+    ints, _ = OraclePipeline(g, _qjson(c, tmp_path)).run(x)
+    for name in g.outputs:
+        np.testing.assert_array_equal(got[name], ints[name])
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8", "int16"])
+def test_mini_yolo_with_softmax_within_one_step(hip, tmp_path, quant_type):
+    g = G.mini_yolo(seed=0)
+    calib = [_images(1 + i, 4, 32) for i in range(3)]
+    c = _calibrated(g, quant_type, True, calib)
+    got = c.integer_outputs(calib[1])[g.outputs[0]]
+    ints, floats = OraclePipeline(g, _qjson(c, tmp_path)).run(calib[1])
+    assert np.abs(got.astype(np.int64) - ints[g.outputs[0]]).max() <= 1
+    out = c.run_graph(calib[1], "integer")
+    step = c.qparams[g.outputs[0]].scale
+    assert np.abs(out - floats[0]).max() <= step * 1.0001
+    assert out.dtype == np.float32 and out.shape == (4, 10)
+
+
+def test_yolov8n_cls_int8_bit_exact(hip, tmp_path):
+    g = G.yolov8n_cls(seed=3, softmax=False)
+    calib = [Stream(40 + i).normal((2, 3, 224, 224)).astype(np.float32)
+             for i in range(2)]
+    c = _calibrated(g, "int8", True, calib)
+    x = Stream(50).normal((2, 3, 224, 224)).astype(np.float32)
+    got = c.integer_outputs(x)[g.outputs[0]]
+    ints, _ = OraclePipeline(g, _qjson(c, tmp_path)).run(x)
+    np.testing.assert_array_equal(got, ints[g.outputs[0]])
+
+
+def test_saved_qparams_reload_to_identical_results(hip, tmp_path):
+    g = G.mini_yolo(seed=0)
+    calib = [_images(1 + i, 4, 32) for i in range(3)]
+    c = _calibrated(g, "int16", True, calib)
+    path = _qjson(c, tmp_path)
+    loaded = QuantContainer.load(g, path)
+    assert loaded.quant_type == "int16" and loaded.calibrated
+    np.testing.assert_array_equal(c.run_graph(calib[2], "integer"),
+                                  loaded.run_graph(calib[2], "integer"))
+
+
+def test_batch_size_can_change_after_calibration(hip):
+    g = G.mini_yolo(seed=0)
+    calib = [_images(1 + i, 4, 32) for i in range(3)]
+    c = _calibrated(g, "int8", True, calib)
+    one = c.run_graph(calib[0][:1], "integer")
+    many = c.run_graph(np.concatenate(calib), "integer")
+    np.testing.assert_array_equal(one, many[:1])
+
+
+def test_graph_replay_matches_eager(hip):
+    """A captured HIP graph replayed several times (with eager work and
+    synchronisation in between) gives the eager result every time."""
+    import torch
+
+    g = G.mini_yolo(seed=0)
+    calib = [_images(1 + i, 4, 32) for i in range(3)]
+    c = _calibrated(g, "int8", True, calib)
+    ex = c.executor({"images": (4, 3, 32, 32)})
+    eager = ex.run({"images": calib[0]})
+    for _ in range(3):
+        replay = ex.run({"images": calib[0]}, use_graph=True)
+        for k in eager:
+            np.testing.assert_array_equal(replay[k], eager[k])
+        torch.zeros(1024, device="cuda").sum().item()
+    other = ex.run({"images": calib[1]}, use_graph=True)
+    eager_other = ex.run({"images": calib[1]})
+    for k in other:
+        np.testing.assert_array_equal(other[k], eager_other[k])
+
+
+def test_uncalibrated_container_refuses(hip):
+    with pytest.raises(ValueError, match="not calibrated"):
+        QuantContainer(G.mini_yolo()).run_graph(_images(0, 1, 32), "integer")
