@@ -110,38 +110,47 @@ int qa_synchronize(void);
 /* Storage codes of device tensors: 1 int8, 2 int16, 4 int32, 8 int64.
  * A quantized value q is stored as q - so (so: storage offset). */
 
-/* Packs centred OIHW weights (w - w_zp, int32) for the int8 MFMA path:
- * per output channel an offset b_off makes every value int8; K is laid out
- * in 16-byte groups (tap-major, 16 input channels each) padded to 64 bytes,
- * rows padded to a multiple of 128 per group. Writes wp (see
- * qa_pack_weights_i8_size), corr[c] = a_off*colsum_c + K*a_off*b_off[c]
- * and boff. Returns 0 on success, 1 when a channel spans more than 255
- * values (use the VALU path), -1 on bad arguments; *needs_rowsum is set
- * when some b_off is non-zero. */
+/* Packs centred OIHW weights (w - w_zp, int32) for the int8 MFMA path.
+ * Per output channel an offset b_off makes every value int8; K is laid out
+ * in 16-byte groups padded to a multiple of 64 bytes, rows padded to a
+ * multiple of 128 per group. layout 0: group kg = tap kg/CB, input channels
+ * [16*(kg%CB), +16), CB = ceil(Cg/16). layout 1 (Cg <= 4, KW <= 4; inputs
+ * stored 4 bytes per pixel): group ky = kernel row, byte 4*kx + c. Writes wp
+ * (qa_pack_weights_i8_size bytes), corr[c] = a_off*colsum_c +
+ * K*a_off*b_off[c] and boff. Returns 0 on success, 1 when a channel spans
+ * more than 255 values (use the VALU path), -1 on bad arguments;
+ * *needs_rowsum is set when some b_off is non-zero. */
 int64_t qa_pack_weights_i8_size(int64_t Cout, int64_t Cg, int64_t KH,
-                                int64_t KW, int64_t G, int64_t* kgp,
-                                int64_t* rows_per_group);
+                                int64_t KW, int64_t G, int64_t layout,
+                                int64_t* kgp, int64_t* rows_per_group);
 int qa_pack_weights_i8(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
-                       int64_t KW, int64_t G, int64_t a_off, int8_t* wp,
-                       int64_t* corr, int32_t* boff, int32_t* needs_rowsum);
+                       int64_t KW, int64_t G, int64_t a_off, int64_t layout,
+                       int8_t* wp, int64_t* corr, int32_t* boff,
+                       int32_t* needs_rowsum);
 
 /* Fused integer convolution / GEMM on device tensors:
- *   acc = sum (x_stored + x_add) * w         (exact, int32 or int64)
+ *   acc = sum (x_stored + x_add) * w         (exact)
  *   q   = clip(mbqm(acc + pre_bias[c], mult[c], shift[c]) + zp)
- *   q   = lut[clip(q - lut_offset)]                      (if lut)
- *   q   = clip(mbqm(r - za) + sign*mbqm(q - zb) + add_zp) (if res; the
+ *   q   = lut[clip(q - lut_offset)]                        (if lut)
+ *   q   = clip(mbqm(r - za) + sign*mbqm(q - zb) + add_zp)    (if res; the
  *         residual r is the first Add operand when res_first)
- *   y   = q - y_so
- * w_code 1: packed int8 weights (MFMA); 2/4: OIHW int16/int32 (VALU, int64
- * accumulation when wide). rowmajor 1: x is an [N][lda] matrix (GEMM with
- * K = C, H = W = KH = KW = 1). Pointers may be pre-offset to address channel
- * slices; *_nstride are elements between images. */
+ *   y   = q - y_so;  y2 = clip(mbqm(q - r2_zp_in, r2_m, r2_s) + r2_zp_out)
+ *         - y_so  (if y2: a rescaled copy, e.g. into a Concat buffer)
+ * Input element (n, c, iy, ix) at x + n*x_sn + c*x_sc + (iy*W+ix)*x_sp;
+ * output / residual / y2 element (n, c, pix) at p + n*sn + c*sc + pix*sp.
+ * w_code 1: weights from qa_pack_weights_i8 (int8 MFMA; needs int8 input
+ * with x_sc == 1 and 16-byte aligned channel groups, 4-byte for layout 1);
+ * w_code 2/4: OIHW int16/int32 weights (VALU; int64 accumulation when wide).
+ * A GEMM is the case H = W = KH = KW = 1 with row m as image m. */
 typedef struct qa_conv_desc {
     const void* x;
-    int64_t x_code, x_nstride, x_add, rowmajor;
+    int64_t x_code, x_sn, x_sc, x_sp, x_add;
     int64_t N, C, H, W, Cout, KH, KW, SH, SW, PH, PW, DH, DW, G, OH, OW;
     const void* w;
-    int64_t w_code, w_kgp, w_rows, wide, needs_rowsum;
+    int64_t w_code, w_layout, w_kgp, w_rows, wide, needs_rowsum;
+    int64_t fast_epilogue; /* caller asserts: every channel has |mult| <
+                              2^31, 1 <= 31+shift <= 62, |pre_bias| < 2^31
+                              (int64-only requantization, MFMA path) */
     const int64_t* corr;
     const int32_t* boff;
     const int64_t* pre_bias;
@@ -151,12 +160,18 @@ typedef struct qa_conv_desc {
     const int32_t* lut;
     int64_t lut_offset, lut_len;
     const void* res;
-    int64_t res_nstride, res_so, res_first;
+    int64_t res_sn, res_sc, res_sp, res_so, res_first;
     int64_t za, ma, sa, zb, mb, sb, add_sign, add_zp, add_qmin, add_qmax;
     void* y;
-    int64_t y_code, y_nstride, y_so;
+    int64_t y_code, y_sn, y_sc, y_sp, y_so;
+    void* y2;
+    int64_t y2_sn, y2_sc, y2_sp, r2_zp_in, r2_m, r2_s, r2_zp_out, r2_qmin,
+        r2_qmax;
 } qa_conv_desc;
 
+/* `stream` of every qa_d_* entry is the hipStream_t to launch on, used as
+ * given (NULL: the null stream). The entries are asynchronous and return 0
+ * on success, -1 on an error (see qa_last_error). */
 int qa_d_conv(const qa_conv_desc* d, void* stream);
 
 /* Element-wise device entries (storage codes as above, `*_so` storage
@@ -198,14 +213,23 @@ int qa_d_dequantize_f32(const void* q, int in_code, float* x, int64_t n,
                         double scale, int64_t zp, int64_t in_so,
                         void* stream);
 
-/* GlobalAveragePool of x [N, C, HW] (image stride x_nstride) into out
- * [N, C]: clip(mbqm(sum(q - zp_in), mult, shift) + zp_out)
+/* GlobalAveragePool of x [N, C, HW] (element (n, c, p) at x + n*x_sn +
+ * c*x_sc + p*x_sp; needs x_sc == 1 or x_sp == 1) into out [N, C] (row
+ * stride out_sn): clip(mbqm(sum(q - zp_in), mult, shift) + zp_out)
  * (quant_layers.py:563-590). */
-int qa_d_gap(const void* x, int in_code, int64_t x_nstride, int64_t N,
-             int64_t C, int64_t HW, int64_t zp_in, int64_t in_so,
-             int64_t mult, int64_t shift, int64_t zp_out, int64_t qmin,
-             int64_t qmax, void* out, int out_code, int64_t out_so,
-             void* stream);
+int qa_d_gap(const void* x, int in_code, int64_t x_sn, int64_t x_sc,
+             int64_t x_sp, int64_t N, int64_t C, int64_t HW, int64_t zp_in,
+             int64_t in_so, int64_t mult, int64_t shift, int64_t zp_out,
+             int64_t qmin, int64_t qmax, void* out, int out_code,
+             int64_t out_sn, int64_t out_so, void* stream);
+
+/* Quantizes float32 NCHW input into channels-last int8/int16 storage with
+ * pixel stride y_sp >= C (padding channels 0), half-to-even like
+ * qa_quantize_f32. */
+int qa_d_quantize_nhwc(const float* x, int64_t N, int64_t C, int64_t HW,
+                       void* y, int y_code, int64_t y_sp, double scale,
+                       int64_t zp, int64_t qmin, int64_t qmax, int64_t so,
+                       void* stream);
 
 /* Float fallback of Softmax over the last axis of [rows, cols]:
  * dequantize to float32, softmax in float64, float32, quantize

@@ -1,0 +1,138 @@
+// Convolution / GEMM on gfx950: shared argument block and epilogue.
+//
+// Activations are channels-last ("NHWC"): element (n, c, iy, ix) of the
+// input lives at x + n*x_sn + (iy*W + ix)*x_sp + c*x_sc, with x_sc == 1 on
+// the int8 MFMA path, so 16 consecutive input channels of one pixel are one
+// aligned 16-byte load. A GEMM is the 1x1 case with H = W = 1 (row m is
+// "image" m, x_sn = lda). Outputs use general strides: element (n, co, pix)
+// (pix = oy*OW + ox) at y + n*y_sn + co*y_sc + pix*y_sp, so the same kernel
+// writes NHWC tensors, NCHW ABI results or row-major GEMM results.
+//
+// int8 MFMA path (v_mfma_i32_16x16x64_i8): the GEMM is
+//   C[Cout x P] = W[Cout x K] * X[K x P],  P = N*OH*OW pixels (batch folded)
+// with K in 16-byte "k-groups": k-group kg covers tap kg / CB and input
+// channels [16*(kg % CB), +16), CB = ceil(Cg/16) (layout 0). For inputs of at
+// most 4 channels stored 4 bytes per pixel (layout 1, the 3-channel stem),
+// k-group ky covers kernel row ky: bytes [4*kx + c] for kx < KW. Lane l
+// supplies row / column (l & 15) and k-group (l >> 4) of its fragments; the
+// accumulator lane l holds output channels 4*(l >> 4) + i, i = 0..3, of pixel
+// (l & 15). Operands are int8 after offsets: x = x_s + a_off,
+// w = w_s + b_off[co]:
+//   sum x w = MFMA(w_s, x_s) + a_off*colsum(w_s)[co]
+//           + b_off[co]*(pixsum(x_s)[p] + K*a_off)
+// corr[co] holds the first and last terms; image padding is x = 0, so it is
+// filled with x_s = -a_off ("pad_value"); K-padding has zero weights and is
+// left out of pixsum.
+#pragma once
+
+#include "qa_common.h"
+
+namespace qa {
+
+enum EpiMode {
+    EPI_RAW32 = 0,  // int32 accumulator (wraps modulo 2^32): ABI narrow path
+    EPI_RAW64 = 1,  // exact int64 accumulator: ABI wide path
+    EPI_QUANT = 2,  // requantize (+LUT) (+residual Add) -> int8/int16
+};
+
+struct ConvArgs {
+    // ---- input ----
+    const void* x;
+    int32_t x_code;                 // 1 int8, 2 int16, 4 int32
+    int64_t x_sn, x_sc, x_sp;       // strides (elements)
+    int64_t x_add;                  // x_centred = stored + x_add
+    int32_t narrow16;               // wrap activations to int16 (ABI narrow)
+    // ---- geometry ----
+    int32_t N, H, W, Cg, G, Cog, KH, KW, SH, SW, PH, PW, DH, DW, OH, OW;
+    int32_t Cout;
+    int64_t M;                      // N*OH*OW
+    // ---- packed int8 weights (MFMA path) ----
+    const int8_t* wp;
+    int32_t layout;                 // 0 tap-major 16-channel groups, 1 stem
+    int32_t CB, KG, KGp, Kreal;
+    int64_t wp_gstride, wp_rstride; // bytes
+    int32_t pad_value;
+    int32_t rowsum;                 // some b_off != 0
+    int32_t fast_hint;              // every channel: |mult| < 2^31,
+                                    // 1 <= 31+shift <= 62, |bias| < 2^31
+    // ---- plain weights (VALU path): OIHW ----
+    const void* w;
+    int32_t w_code;                 // 2 int16, 4 int32
+    int32_t wide;                   // int64 accumulation
+    // ---- per output channel ----
+    const int64_t* corr;
+    const int32_t* boff;
+    const int64_t* pre;             // bias added after the int32 wrap
+    const int64_t* mult;
+    const int64_t* shift;
+    // ---- epilogue ----
+    int32_t mode;
+    int64_t zp, qmin, qmax;
+    const int32_t* lut;
+    int64_t lut_off, lut_len;
+    const void* res;
+    int64_t res_sn, res_sc, res_sp, res_so;
+    int32_t res_first;
+    int64_t za, ma, sa, zb, mb, sb, add_sign, add_zp, add_qmin, add_qmax;
+    void* y;
+    int32_t y_code;                 // 1 int8, 2 int16, 4 int32, 8 int64
+    int64_t y_sn, y_sc, y_sp, y_so;
+    void* y2;                       // optional rescaled copy (same code)
+    int64_t y2_sn, y2_sc, y2_sp;
+    int64_t r2_zp_in, r2_m, r2_s, r2_zp_out, r2_qmin, r2_qmax;
+};
+
+// Requantize, table and residual Add of one accumulator (mode EPI_QUANT):
+// returns the quantized value q (before the storage offset).
+__device__ __forceinline__ int64_t quant_one(const ConvArgs& a, int64_t v,
+                                             int64_t m, int64_t s,
+                                             int64_t res_q) {
+    int64_t q = qa_clip128(qa_mbqm_fast(v, m, s) + a.zp, a.qmin, a.qmax);
+    if (a.lut) {
+        int64_t idx = q - a.lut_off;
+        idx = idx < 0 ? 0 : (idx >= a.lut_len ? a.lut_len - 1 : idx);
+        q = a.lut[idx];
+    }
+    if (a.res) {
+        const int64_t first = a.res_first ? res_q : q;
+        const int64_t second = a.res_first ? q : res_q;
+        const qa_i128 t = qa_mbqm_fast(first - a.za, a.ma, a.sa) +
+                          (qa_i128)a.add_sign *
+                              qa_mbqm_fast(second - a.zb, a.mb, a.sb) +
+                          a.add_zp;
+        q = qa_clip128(t, a.add_qmin, a.add_qmax);
+    }
+    return q;
+}
+
+__device__ __forceinline__ int64_t rescale2(const ConvArgs& a, int64_t q) {
+    return qa_clip128(qa_mbqm_fast(q - a.r2_zp_in, a.r2_m, a.r2_s) +
+                          a.r2_zp_out,
+                      a.r2_qmin, a.r2_qmax);
+}
+
+__device__ __forceinline__ int64_t load_any(const void* p, int code,
+                                            int64_t i) {
+    switch (code) {
+        case 1: return ((const int8_t*)p)[i];
+        case 2: return ((const int16_t*)p)[i];
+        case 4: return ((const int32_t*)p)[i];
+        default: return ((const int64_t*)p)[i];
+    }
+}
+
+__device__ __forceinline__ void store_any(void* p, int code, int64_t i,
+                                          int64_t v) {
+    switch (code) {
+        case 1: ((int8_t*)p)[i] = (int8_t)v; break;
+        case 2: ((int16_t*)p)[i] = (int16_t)v; break;
+        case 4: ((int32_t*)p)[i] = (int32_t)v; break;
+        default: ((int64_t*)p)[i] = v; break;
+    }
+}
+
+// Launchers; false on launch failure (recorded with set_error).
+bool launch_conv_mfma(const ConvArgs& a, hipStream_t st);
+bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
+
+}  // namespace qa

@@ -1,19 +1,20 @@
 // Convolution / GEMM entry points: the reference ABI (host pointers,
-// qa_kernels.cpp:233-284) and the device-resident qa_d_conv.
+// qa_kernels.cpp:252-284) and the device-resident qa_d_conv.
 //
-// ABI integer path: the operands are centred integers of any width. The
-// library measures the activation range on the device and the per-channel
-// weight ranges on the host; when every range spans at most 256 values it
-// offsets both into int8 and runs the MFMA kernel with the exact correction
-// terms (qa_igemm.h), otherwise it runs the exact VALU kernel. Either way
-// the result equals the reference's int32 (modulo 2^32) or int64 sums.
+// ABI integer path: operands are centred integers of any width. The library
+// measures the activation range on the device and the per-channel weight
+// ranges on the host; when every range spans at most 256 values it offsets
+// both into int8, repacks the activations channels-last and runs the MFMA
+// kernel with the exact correction terms (qa_conv.h); otherwise it runs the
+// exact VALU kernel on the original data. Either way the result equals the
+// reference's int32 (modulo 2^32) or int64 sums.
 #include <string.h>
 
 #include <algorithm>
 #include <vector>
 
 #include "../../include/qa_hip.h"
-#include "qa_igemm.h"
+#include "qa_conv.h"
 #include "qa_valu.h"
 
 namespace qa {
@@ -21,6 +22,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int64_t kRowPad = 128;  // packed weight rows per group: x128
+constexpr int64_t kTail = 64;     // slack after packed activations
 
 // ------------------------------------------------------------- kernels --
 template <class T>
@@ -45,23 +47,31 @@ __global__ __launch_bounds__(kThreads) void k_range(const T* x, int64_t n,
     }
 }
 
-// y[i] = int8(v - a_off) with v optionally wrapped to int16 first.
-template <class T>
-__global__ __launch_bounds__(kThreads) void k_pack_i8(const T* x, int8_t* y,
-                                                      int64_t n, int narrow16,
-                                                      int a_off) {
+// NCHW int32 -> channels-last int8 x_s = v - a_off with pixel stride Cs;
+// padding channels are 0.
+__global__ __launch_bounds__(kThreads) void k_pack_nhwc(
+    const int32_t* x, int8_t* y, int64_t N, int64_t C, int64_t HW,
+    int64_t Cs, int narrow16, int a_off) {
+    const int64_t total = N * HW * Cs;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += step) {
-        int v = (int)x[i];
-        if (narrow16) v = (int16_t)v;
-        y[i] = (int8_t)(v - a_off);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+         i < total; i += step) {
+        const int64_t c = i % Cs;
+        const int64_t np = i / Cs;
+        const int64_t n = np / HW, p = np - n * HW;
+        int8_t v = 0;
+        if (c < C) {
+            int x0 = x[(n * C + c) * HW + p];
+            if (narrow16) x0 = (int16_t)x0;
+            v = (int8_t)(x0 - a_off);
+        }
+        y[i] = v;
     }
 }
 
 // Row-major A[M][K] -> int8 [M][Kp] with zero K-padding.
 template <class T>
-__global__ __launch_bounds__(kThreads) void k_pack_rows_i8(
+__global__ __launch_bounds__(kThreads) void k_pack_rows(
     const T* a, int8_t* y, int64_t M, int64_t K, int64_t Kp, int a_off) {
     const int64_t n = M * Kp;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
@@ -79,8 +89,8 @@ template <class T>
 bool host_copy(const T* src, int64_t n, std::vector<T>& dst) {
     dst.resize((size_t)std::max<int64_t>(n, 1));
     if (n <= 0) return true;
-    hipError_t e = hipMemcpy(dst.data(), src, (size_t)n * sizeof(T),
-                             hipMemcpyDefault);
+    hipError_t e =
+        hipMemcpy(dst.data(), src, (size_t)n * sizeof(T), hipMemcpyDefault);
     if (e != hipSuccess) {
         set_hip_error("hipMemcpy(host copy)", e);
         return false;
@@ -112,7 +122,6 @@ bool download(void* h, const void* d, size_t bytes, hipStream_t st) {
     return true;
 }
 
-// Device min/max of n values (wrapped to int16 when narrow16).
 template <class T>
 bool device_range(const T* d, int64_t n, bool narrow16, hipStream_t st,
                   int* lo, int* hi) {
@@ -131,7 +140,7 @@ bool device_range(const T* d, int64_t n, bool narrow16, hipStream_t st,
     return true;
 }
 
-// Activation offset making [lo, hi] (0 included for padding) int8, or false.
+// Activation offset making [lo, hi] (0 included, for padding) int8.
 bool activation_offset(int lo, int hi, int* a_off) {
     lo = std::min(lo, 0);
     hi = std::max(hi, 0);
@@ -140,16 +149,17 @@ bool activation_offset(int lo, int hi, int* a_off) {
     return true;
 }
 
-void fill_geometry(IgemmArgs& a, int64_t N, int64_t C, int64_t H, int64_t W,
-                   int64_t Cout, int64_t KH, int64_t KW, int64_t SH,
-                   int64_t SW, int64_t PH, int64_t PW, int64_t DH, int64_t DW,
-                   int64_t G, int64_t OH, int64_t OW) {
-    a.C = (int32_t)C;
+void set_geometry(ConvArgs& a, int64_t N, int64_t C, int64_t H, int64_t W,
+                  int64_t Cout, int64_t KH, int64_t KW, int64_t SH, int64_t SW,
+                  int64_t PH, int64_t PW, int64_t DH, int64_t DW, int64_t G,
+                  int64_t OH, int64_t OW) {
+    a.N = (int32_t)N;
     a.H = (int32_t)H;
     a.W = (int32_t)W;
     a.Cg = (int32_t)(C / G);
     a.G = (int32_t)G;
     a.Cog = (int32_t)(Cout / G);
+    a.Cout = (int32_t)Cout;
     a.KH = (int32_t)KH;
     a.KW = (int32_t)KW;
     a.SH = (int32_t)SH;
@@ -160,38 +170,18 @@ void fill_geometry(IgemmArgs& a, int64_t N, int64_t C, int64_t H, int64_t W,
     a.DW = (int32_t)DW;
     a.OH = (int32_t)OH;
     a.OW = (int32_t)OW;
-    a.CB = (int32_t)ceil_div(a.Cg, 16);
-    a.KG = a.KH * a.KW * a.CB;
-    a.KGp = (int32_t)round_up(std::max(a.KG, 1), 4);
     a.M = N * OH * OW;
     a.Kreal = a.Cg * a.KH * a.KW;
-    a.Cout = (int32_t)Cout;
 }
 
-ValuConv valu_geometry(int64_t N, int64_t C, int64_t H, int64_t W,
-                       int64_t Cout, int64_t KH, int64_t KW, int64_t SH,
-                       int64_t SW, int64_t PH, int64_t PW, int64_t DH,
-                       int64_t DW, int64_t G, int64_t OH, int64_t OW) {
-    ValuConv c;
-    memset(&c, 0, sizeof(c));
-    c.N = (int32_t)N;
-    c.C = (int32_t)C;
-    c.H = (int32_t)H;
-    c.W = (int32_t)W;
-    c.Cout = (int32_t)Cout;
-    c.KH = (int32_t)KH;
-    c.KW = (int32_t)KW;
-    c.SH = (int32_t)SH;
-    c.SW = (int32_t)SW;
-    c.PH = (int32_t)PH;
-    c.PW = (int32_t)PW;
-    c.DH = (int32_t)DH;
-    c.DW = (int32_t)DW;
-    c.G = (int32_t)G;
-    c.OH = (int32_t)OH;
-    c.OW = (int32_t)OW;
-    c.x_nstride = C * H * W;
-    return c;
+// Packed-weight geometry of a layout (see qa_pack_weights_i8).
+void pack_geometry(int64_t Cout, int64_t Cg, int64_t KH, int64_t KW,
+                   int64_t G, int layout, int64_t* CB, int64_t* KG,
+                   int64_t* KGp, int64_t* rows) {
+    *CB = layout == 1 ? 1 : ceil_div(Cg, 16);
+    *KG = layout == 1 ? KH : KH * KW * *CB;
+    *KGp = round_up(std::max<int64_t>(*KG, 1), 4);
+    *rows = round_up(std::max<int64_t>(Cout / G, 1), kRowPad);
 }
 
 bool conv_shape_ok(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
@@ -216,16 +206,14 @@ bool conv_shape_ok(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
     return true;
 }
 
-// Packs weights host-side; see qa_pack_weights_i8 in qa_hip.h.
 int pack_weights(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
-                 int64_t KW, int64_t G, int64_t a_off, int8_t* wp,
+                 int64_t KW, int64_t G, int64_t a_off, int layout, int8_t* wp,
                  int64_t* corr, int32_t* boff, int32_t* needs_rowsum) {
-    if (G <= 0 || Cout % G || Cg < 0) return -1;
+    if (G <= 0 || Cout % G || Cg < 0 || (layout == 1 && (Cg > 4 || KW > 4)))
+        return -1;
     const int64_t Cog = Cout / G;
-    const int64_t CB = ceil_div(Cg, 16);
-    const int64_t KG = KH * KW * CB;
-    const int64_t KGp = round_up(std::max<int64_t>(KG, 1), 4);
-    const int64_t rows = round_up(std::max<int64_t>(Cog, 1), kRowPad);
+    int64_t CB, KG, KGp, rows;
+    pack_geometry(Cout, Cg, KH, KW, G, layout, &CB, &KG, &KGp, &rows);
     const int64_t K = Cg * KH * KW;
     memset(wp, 0, (size_t)(G * rows * KGp * 16));
     int32_t any = 0;
@@ -248,14 +236,45 @@ int pack_weights(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
                 for (int64_t kx = 0; kx < KW; ++kx) {
                     const int v = row[(c * KH + ky) * KW + kx] - b;
                     colsum += v;
-                    const int64_t kg = (ky * KW + kx) * CB + c / 16;
-                    dst[kg * 16 + c % 16] = (int8_t)v;
+                    const int64_t at =
+                        layout == 1 ? ky * 16 + kx * 4 + c
+                                    : ((ky * KW + kx) * CB + c / 16) * 16 +
+                                          c % 16;
+                    dst[at] = (int8_t)v;
                 }
         corr[co] = a_off * colsum + K * a_off * (int64_t)b;
         boff[co] = b;
     }
     *needs_rowsum = any;
     return 0;
+}
+
+// Packs host weights and uploads them; fills the weight part of `a`.
+bool upload_weights(const std::vector<int32_t>& w32, int64_t Cout, int64_t Cg,
+                    int64_t KH, int64_t KW, int64_t G, int a_off, int layout,
+                    ConvArgs& a, hipStream_t st) {
+    int64_t CB, KG, KGp, rows;
+    pack_geometry(Cout, Cg, KH, KW, G, layout, &CB, &KG, &KGp, &rows);
+    std::vector<int8_t> wp((size_t)(G * rows * KGp * 16));
+    std::vector<int64_t> corr((size_t)std::max<int64_t>(Cout, 1));
+    std::vector<int32_t> boff((size_t)std::max<int64_t>(Cout, 1));
+    int32_t rowsum = 0;
+    if (pack_weights(w32.data(), Cout, Cg, KH, KW, G, a_off, layout,
+                     wp.data(), corr.data(), boff.data(), &rowsum) != 0)
+        return false;
+    a.wp = upload(2, wp.data(), (int64_t)wp.size(), st);
+    a.corr = upload(3, corr.data(), Cout, st);
+    a.boff = upload(4, boff.data(), Cout, st);
+    if (!a.wp || !a.corr || !a.boff) return false;
+    a.layout = layout;
+    a.CB = (int32_t)CB;
+    a.KG = (int32_t)KG;
+    a.KGp = (int32_t)KGp;
+    a.wp_rstride = KGp * 16;
+    a.wp_gstride = rows * KGp * 16;
+    a.rowsum = rowsum;
+    a.pad_value = -a_off;
+    return true;
 }
 
 // ------------------------------------------------------------ ABI conv --
@@ -276,74 +295,65 @@ void conv_abi(const int32_t* x, const TW* w, void* y, int64_t N, int64_t C,
     if (!dy) return;
     const int64_t Cg = C / G;
     const int64_t K = Cg * KH * KW;
-    if (K == 0 || N * C * H * W == 0) {
+    const int64_t nx = N * C * H * W;
+    if (K == 0 || nx == 0) {
         QA_HIP(hipMemsetAsync(dy, 0, ybytes, st));
         download(y, dy, ybytes, st);
         return;
     }
-    const int64_t nx = N * C * H * W;
     const int32_t* dx = upload(0, x, nx, st);
     if (!dx) return;
     std::vector<TW> hw;
     if (!host_copy(w, Cout * K, hw)) return;
+    std::vector<int32_t> w32(hw.begin(), hw.begin() + Cout * K);
+
+    ConvArgs a;
+    memset(&a, 0, sizeof(a));
+    set_geometry(a, N, C, H, W, Cout, KH, KW, SH, SW, PH, PW, DH, DW, G, OH,
+                 OW);
+    a.mode = WIDE ? EPI_RAW64 : EPI_RAW32;
+    a.y = dy;
+    a.y_code = WIDE ? 8 : 4;
+    a.y_sn = Cout * OH * OW;
+    a.y_sc = OH * OW;
+    a.y_sp = 1;
 
     int lo, hi, a_off = 0;
     if (!device_range(dx, nx, !WIDE, st, &lo, &hi)) return;
-    bool mfma = K < 131072 && activation_offset(lo, hi, &a_off);
-    std::vector<int32_t> w32;
-    int64_t kgp = 0, rows = 0;
-    const int64_t wpbytes =
-        qa_pack_weights_i8_size(Cout, Cg, KH, KW, G, &kgp, &rows);
-    std::vector<int8_t> wp;
-    std::vector<int64_t> corr;
-    std::vector<int32_t> boff;
-    int32_t rowsum = 0;
+    const int layout = (G == 1 && Cg <= 4 && KW <= 4) ? 1 : 0;
+    bool mfma = K < 131072 && activation_offset(lo, hi, &a_off) &&
+                (layout == 1 || G == 1 || Cg % 16 == 0);
+    if (mfma)
+        mfma = upload_weights(w32, Cout, Cg, KH, KW, G, a_off, layout, a, st);
+    if (!ok()) return;
     if (mfma) {
-        w32.assign(hw.begin(), hw.begin() + Cout * K);
-        wp.resize((size_t)wpbytes);
-        corr.resize((size_t)Cout);
-        boff.resize((size_t)Cout);
-        mfma = pack_weights(w32.data(), Cout, Cg, KH, KW, G, a_off, wp.data(),
-                            corr.data(), boff.data(), &rowsum) == 0;
-    }
-    IgemmArgs a;
-    memset(&a, 0, sizeof(a));
-    fill_geometry(a, N, C, H, W, Cout, KH, KW, SH, SW, PH, PW, DH, DW, G, OH,
-                  OW);
-    a.y = dy;
-    a.y_nstride = Cout * OH * OW;
-    if (mfma) {
-        int8_t* dxs = (int8_t*)scratch(6, (size_t)nx);
-        const int8_t* dwp = upload(2, wp.data(), wpbytes, st);
-        const int64_t* dcorr = upload(3, corr.data(), Cout, st);
-        const int32_t* dboff = upload(4, boff.data(), Cout, st);
-        if (!dxs || !dwp || !dcorr || !dboff) return;
-        k_pack_i8<int32_t><<<grid_1d(nx, kThreads, 1 << 20), kThreads, 0,
-                             st>>>(dx, dxs, nx, WIDE ? 0 : 1, a_off);
+        const int64_t Cs = layout == 1 ? 4 : (G == 1 ? round_up(C, 16) : C);
+        const int64_t HW = H * W;
+        const int64_t nb = N * HW * Cs;
+        int8_t* dxs = (int8_t*)scratch(6, (size_t)(nb + kTail));
+        if (!dxs) return;
+        k_pack_nhwc<<<grid_1d(nb, kThreads, 1 << 20), kThreads, 0, st>>>(
+            dx, dxs, N, C, HW, Cs, WIDE ? 0 : 1, a_off);
         QA_HIP(hipGetLastError());
         a.x = dxs;
-        a.x_nstride = C * H * W;
-        a.x_cstride = H * W;
-        a.pad_value = -a_off;
-        a.wp = dwp;
-        a.wp_rstride = kgp * 16;
-        a.wp_gstride = rows * kgp * 16;
-        a.corr = dcorr;
-        a.boff = dboff;
-        if (!launch_igemm(a, WIDE ? EPI_RAW64 : EPI_RAW32, rowsum != 0, st))
-            return;
+        a.x_code = 1;
+        a.x_sn = HW * Cs;
+        a.x_sc = 1;
+        a.x_sp = Cs;
+        if (!launch_conv_mfma(a, st)) return;
     } else {
         const TW* dw = upload(2, hw.data(), Cout * K, st);
         if (!dw) return;
-        ValuConv c = valu_geometry(N, C, H, W, Cout, KH, KW, SH, SW, PH, PW,
-                                   DH, DW, G, OH, OW);
-        c.x = dx;
-        c.x_code = 4;
-        c.narrow16 = WIDE ? 0 : 1;
-        c.w = dw;
-        c.w_code = sizeof(TW);
-        c.wide = WIDE ? 1 : 0;
-        if (!launch_conv_valu(c, a, WIDE ? EPI_RAW64 : EPI_RAW32, st)) return;
+        a.x = dx;
+        a.x_code = 4;
+        a.x_sn = C * H * W;
+        a.x_sc = H * W;
+        a.x_sp = 1;
+        a.narrow16 = WIDE ? 0 : 1;
+        a.w = dw;
+        a.w_code = sizeof(TW);
+        a.wide = WIDE ? 1 : 0;
+        if (!launch_conv_valu(a, st)) return;
     }
     download(y, dy, ybytes, st);
 }
@@ -351,10 +361,10 @@ void conv_abi(const int32_t* x, const TW* w, void* y, int64_t N, int64_t C,
 // ------------------------------------------------------------ ABI GEMM --
 template <bool WIDE, class T>
 void gemm_abi(int64_t M, int64_t N, int64_t K, const T* A, const T* B,
-              void* C) {
+              void* Cm) {
     if (M <= 0 || N <= 0) return;
-    if (!fits_i32(M) || !fits_i32(N) || !fits_i32(K)) {
-        set_error("gemm", "dimension outside [0, 2^31)");
+    if (!fits_i32(M) || !fits_i32(N) || !fits_i32(K) || N > 65535) {
+        set_error("gemm", "dimension outside the supported range");
         return;
     }
     AbiLock lk;
@@ -365,7 +375,7 @@ void gemm_abi(int64_t M, int64_t N, int64_t K, const T* A, const T* B,
     if (!dc) return;
     if (K == 0) {
         QA_HIP(hipMemsetAsync(dc, 0, cbytes, st));
-        download(C, dc, cbytes, st);
+        download(Cm, dc, cbytes, st);
         return;
     }
     const T* da = upload(0, A, M * K, st);
@@ -375,50 +385,37 @@ void gemm_abi(int64_t M, int64_t N, int64_t K, const T* A, const T* B,
     int lo, hi, a_off = 0;
     if (!device_range(da, M * K, false, st, &lo, &hi)) return;
     bool mfma = K < 131072 && activation_offset(lo, hi, &a_off);
-    // B^T as "weights" [N][K] (Cout = N, Cg = K, 1x1)
-    int64_t kgp = 0, rows = 0;
-    const int64_t wpbytes = qa_pack_weights_i8_size(N, K, 1, 1, 1, &kgp, &rows);
-    std::vector<int8_t> wp;
-    std::vector<int64_t> corr;
-    std::vector<int32_t> boff;
-    int32_t rowsum = 0;
+    ConvArgs a;
+    memset(&a, 0, sizeof(a));
+    // A GEMM is a 1x1 convolution of M one-pixel "images" with K channels.
+    set_geometry(a, M, K, 1, 1, N, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 1);
+    a.mode = WIDE ? EPI_RAW64 : EPI_RAW32;
+    a.y = dc;
+    a.y_code = WIDE ? 8 : 4;
+    a.y_sn = N;
+    a.y_sc = 1;
+    a.y_sp = 0;
     if (mfma) {
-        std::vector<int32_t> bt((size_t)(N * K));
+        std::vector<int32_t> bt((size_t)(N * K));  // B^T: [N][K]
         for (int64_t k = 0; k < K; ++k)
-            for (int64_t n = 0; n < N; ++n) bt[n * K + k] = (int32_t)hb[k * N + n];
-        wp.resize((size_t)wpbytes);
-        corr.resize((size_t)N);
-        boff.resize((size_t)N);
-        mfma = pack_weights(bt.data(), N, K, 1, 1, 1, a_off, wp.data(),
-                            corr.data(), boff.data(), &rowsum) == 0;
+            for (int64_t n = 0; n < N; ++n)
+                bt[n * K + k] = (int32_t)hb[k * N + n];
+        mfma = upload_weights(bt, N, K, 1, 1, 1, a_off, 0, a, st);
     }
+    if (!ok()) return;
     if (mfma) {
-        const int64_t Kp = kgp * 16;
-        int8_t* das = (int8_t*)scratch(6, (size_t)(M * Kp));
-        const int8_t* dwp = upload(2, wp.data(), wpbytes, st);
-        const int64_t* dcorr = upload(3, corr.data(), N, st);
-        const int32_t* dboff = upload(4, boff.data(), N, st);
-        if (!das || !dwp || !dcorr || !dboff) return;
-        k_pack_rows_i8<T><<<grid_1d(M * Kp, kThreads, 1 << 20), kThreads, 0,
-                            st>>>(da, das, M, K, Kp, a_off);
+        const int64_t Kp = round_up(K, 16);
+        int8_t* das = (int8_t*)scratch(6, (size_t)(M * Kp + kTail));
+        if (!das) return;
+        k_pack_rows<T><<<grid_1d(M * Kp, kThreads, 1 << 20), kThreads, 0,
+                         st>>>(da, das, M, K, Kp, a_off);
         QA_HIP(hipGetLastError());
-        IgemmArgs a;
-        memset(&a, 0, sizeof(a));
-        fill_geometry(a, M, K, 1, 1, N, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 1);
         a.x = das;
-        a.rowmajor = 1;
-        a.lda = Kp;
-        a.x_nstride = Kp;
-        a.x_cstride = 1;
-        a.wp = dwp;
-        a.wp_rstride = kgp * 16;
-        a.wp_gstride = rows * kgp * 16;
-        a.corr = dcorr;
-        a.boff = dboff;
-        a.y = dc;
-        a.y_nstride = N;
-        if (!launch_igemm(a, WIDE ? EPI_RAW64 : EPI_RAW32, rowsum != 0, st))
-            return;
+        a.x_code = 1;
+        a.x_sn = Kp;
+        a.x_sc = 1;
+        a.x_sp = 0;
+        if (!launch_conv_mfma(a, st)) return;
     } else {
         const T* db = upload(2, hb.data(), K * N, st);
         if (!db) return;
@@ -426,7 +423,7 @@ void gemm_abi(int64_t M, int64_t N, int64_t K, const T* A, const T* B,
                               st))
             return;
     }
-    download(C, dc, cbytes, st);
+    download(Cm, dc, cbytes, st);
 }
 
 }  // namespace
@@ -491,8 +488,10 @@ QA_API void qa_conv_f32(const float* x, const float* w, float* y,
     const float* dw = upload(2, w, Cout * (C / G) * KH * KW, st);
     float* dy = (float*)scratch(1, (size_t)nout * 4);
     if (!dx || !dw || !dy) return;
-    ValuConv c = valu_geometry(QA_CONV_FWD);
-    if (!launch_conv_f32(dx, dw, dy, c, st)) return;
+    ConvArgs a;
+    memset(&a, 0, sizeof(a));
+    set_geometry(a, QA_CONV_FWD);
+    if (!launch_conv_f32(dx, dw, dy, a, st)) return;
     download(y, dy, (size_t)nout * 4, st);
 }
 
@@ -508,12 +507,11 @@ QA_API void qa_conv_i32_i32_i64(const int32_t* x, const int32_t* w,
 
 // ============================================== additional surface ==
 QA_API int64_t qa_pack_weights_i8_size(int64_t Cout, int64_t Cg, int64_t KH,
-                                       int64_t KW, int64_t G, int64_t* kgp,
-                                       int64_t* rows_per_group) {
-    if (G <= 0 || Cout < 0 || Cout % G) return -1;
-    const int64_t KG = KH * KW * ceil_div(Cg, 16);
-    const int64_t KGp = round_up(std::max<int64_t>(KG, 1), 4);
-    const int64_t rows = round_up(std::max<int64_t>(Cout / G, 1), kRowPad);
+                                       int64_t KW, int64_t G, int64_t layout,
+                                       int64_t* kgp, int64_t* rows_per_group) {
+    if (G <= 0 || Cout < 0 || Cout % G || layout < 0 || layout > 1) return -1;
+    int64_t CB, KG, KGp, rows;
+    pack_geometry(Cout, Cg, KH, KW, G, (int)layout, &CB, &KG, &KGp, &rows);
     if (kgp) *kgp = KGp;
     if (rows_per_group) *rows_per_group = rows;
     return G * rows * KGp * 16;
@@ -521,32 +519,39 @@ QA_API int64_t qa_pack_weights_i8_size(int64_t Cout, int64_t Cg, int64_t KH,
 
 QA_API int qa_pack_weights_i8(const int32_t* w, int64_t Cout, int64_t Cg,
                               int64_t KH, int64_t KW, int64_t G, int64_t a_off,
-                              int8_t* wp, int64_t* corr, int32_t* boff,
-                              int32_t* needs_rowsum) {
-    return pack_weights(w, Cout, Cg, KH, KW, G, a_off, wp, corr, boff,
-                        needs_rowsum);
+                              int64_t layout, int8_t* wp, int64_t* corr,
+                              int32_t* boff, int32_t* needs_rowsum) {
+    return pack_weights(w, Cout, Cg, KH, KW, G, a_off, (int)layout, wp, corr,
+                        boff, needs_rowsum);
 }
 
 QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
-    hipStream_t st = stream_ ? (hipStream_t)stream_ : stream();
-    if (!d || !st) return -1;
+    hipStream_t st = (hipStream_t)stream_;
+    if (!d) return -1;
     if (!conv_shape_ok(d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW, d->SH,
                        d->SW, d->DH, d->DW, d->G, d->OH, d->OW))
         return -1;
     if (d->N * d->Cout * d->OH * d->OW == 0) return 0;
-    IgemmArgs a;
+    if (d->y_code != 1 && d->y_code != 2) {
+        set_error("qa_d_conv", "output storage must be int8 or int16");
+        return -1;
+    }
+    ConvArgs a;
     memset(&a, 0, sizeof(a));
-    fill_geometry(a, d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW, d->SH,
-                  d->SW, d->PH, d->PW, d->DH, d->DW, d->G, d->OH, d->OW);
+    set_geometry(a, d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW, d->SH,
+                 d->SW, d->PH, d->PW, d->DH, d->DW, d->G, d->OH, d->OW);
+    a.x = d->x;
+    a.x_code = (int32_t)d->x_code;
+    a.x_sn = d->x_sn;
+    a.x_sc = d->x_sc;
+    a.x_sp = d->x_sp;
+    a.x_add = d->x_add;
     a.corr = d->corr;
     a.boff = d->boff;
     a.pre = d->pre_bias;
-    a.y = d->y;
-    a.y_nstride = d->y_nstride;
-    a.out_code = (int32_t)d->y_code;
-    a.out_so = d->y_so;
     a.mult = d->mult;
     a.shift = d->shift;
+    a.mode = EPI_QUANT;
     a.zp = d->zp;
     a.qmin = d->qmin;
     a.qmax = d->qmax;
@@ -554,7 +559,9 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
     a.lut_off = d->lut_offset;
     a.lut_len = d->lut_len;
     a.res = d->res;
-    a.res_nstride = d->res_nstride;
+    a.res_sn = d->res_sn;
+    a.res_sc = d->res_sc;
+    a.res_sp = d->res_sp;
     a.res_so = d->res_so;
     a.res_first = (int32_t)d->res_first;
     a.za = d->za;
@@ -567,36 +574,54 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
     a.add_zp = d->add_zp;
     a.add_qmin = d->add_qmin;
     a.add_qmax = d->add_qmax;
-    if (d->y_code != 1 && d->y_code != 2) {
-        set_error("qa_d_conv", "output storage must be int8 or int16");
-        return -1;
-    }
+    a.y = d->y;
+    a.y_code = (int32_t)d->y_code;
+    a.y_sn = d->y_sn;
+    a.y_sc = d->y_sc;
+    a.y_sp = d->y_sp;
+    a.y_so = d->y_so;
+    a.y2 = d->y2;
+    a.y2_sn = d->y2_sn;
+    a.y2_sc = d->y2_sc;
+    a.y2_sp = d->y2_sp;
+    a.r2_zp_in = d->r2_zp_in;
+    a.r2_m = d->r2_m;
+    a.r2_s = d->r2_s;
+    a.r2_zp_out = d->r2_zp_out;
+    a.r2_qmin = d->r2_qmin;
+    a.r2_qmax = d->r2_qmax;
     if (d->w_code == 1) {
-        if (d->x_code != 1 || d->x_add < -127 || d->x_add > 128 ||
-            d->w_kgp != a.KGp || a.Kreal >= 131072) {
-            set_error("qa_d_conv", "int8 MFMA path: bad operands");
+        int64_t CB, KG, KGp, rows;
+        pack_geometry(d->Cout, d->C / d->G, d->KH, d->KW, d->G,
+                      (int)d->w_layout, &CB, &KG, &KGp, &rows);
+        const uintptr_t xa = (uintptr_t)d->x;
+        const bool aligned =
+            d->w_layout == 1
+                ? (d->x_sp % 4 == 0 && d->x_sn % 4 == 0 && xa % 4 == 0 &&
+                   d->G == 1)
+                : (xa % 16 == 0 && d->x_sn % 16 == 0 &&
+                   (d->H * d->W == 1 || d->x_sp % 16 == 0) &&
+                   (d->G == 1 || (d->C / d->G) % 16 == 0));
+        if (d->x_code != 1 || d->x_sc != 1 || d->x_add < -127 ||
+            d->x_add > 128 || d->w_kgp != KGp || d->w_rows != rows ||
+            a.Kreal >= 131072 || !aligned) {
+            set_error("qa_d_conv", "int8 MFMA path: operands do not match");
             return -1;
         }
-        a.x = (const int8_t*)d->x;
-        a.x_nstride = d->x_nstride;
-        a.x_cstride = d->rowmajor ? 1 : d->H * d->W;
-        a.rowmajor = (int32_t)d->rowmajor;
-        a.lda = d->x_nstride;
-        a.pad_value = (int32_t)(-d->x_add);
         a.wp = (const int8_t*)d->w;
-        a.wp_rstride = d->w_kgp * 16;
-        a.wp_gstride = d->w_rows * d->w_kgp * 16;
-        return launch_igemm(a, EPI_QUANT, d->needs_rowsum != 0, st) ? 0 : -1;
+        a.layout = (int32_t)d->w_layout;
+        a.CB = (int32_t)CB;
+        a.KG = (int32_t)KG;
+        a.KGp = (int32_t)KGp;
+        a.wp_rstride = KGp * 16;
+        a.wp_gstride = rows * KGp * 16;
+        a.pad_value = (int32_t)(-d->x_add);
+        a.rowsum = (int32_t)d->needs_rowsum;
+        a.fast_hint = (int32_t)d->fast_epilogue;
+        return launch_conv_mfma(a, st) ? 0 : -1;
     }
-    ValuConv c = valu_geometry(d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW,
-                               d->SH, d->SW, d->PH, d->PW, d->DH, d->DW, d->G,
-                               d->OH, d->OW);
-    c.x = d->x;
-    c.x_code = (int32_t)d->x_code;
-    c.x_nstride = d->x_nstride;
-    c.x_add = d->x_add;
-    c.w = d->w;
-    c.w_code = (int32_t)d->w_code;
-    c.wide = (int32_t)d->wide;
-    return launch_conv_valu(c, a, EPI_QUANT, st) ? 0 : -1;
+    a.w = d->w;
+    a.w_code = (int32_t)d->w_code;
+    a.wide = (int32_t)d->wide;
+    return launch_conv_valu(a, st) ? 0 : -1;
 }

@@ -42,12 +42,17 @@ __global__ __launch_bounds__(kThreads) void k_requant(
 }
 
 // Row-strided element-wise kernels: `rows` rows of `cols` elements, each
-// operand with its own row stride (a channel slice of an NCHW tensor is
-// rows = N, cols = C_slice*H*W, stride = C*H*W). grid.y walks the rows.
+// operand with its own row stride (a channel slice of a channels-last tensor
+// is rows = N*H*W pixels, cols = C_slice, stride = the buffer's channel
+// count). One flat index per element, so narrow rows still fill the GPU.
 #define QA_ROW_LOOP                                                         \
-    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y)                  \
-        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;    \
-             i < cols; i += (int64_t)gridDim.x * blockDim.x)
+    const bool small_ = rows * cols < ((int64_t)1 << 32);                   \
+    for (int64_t i_ = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;       \
+         i_ < rows * cols; i_ += (int64_t)gridDim.x * blockDim.x)           \
+        for (int64_t r = small_ ? (int64_t)((uint32_t)i_ / (uint32_t)cols)  \
+                                : i_ / cols,                                \
+                     i = i_ - r * cols, once_ = 1;                          \
+             once_; once_ = 0)
 
 template <class TIn, class TOut>
 __global__ __launch_bounds__(kThreads) void k_rescale(
@@ -159,9 +164,9 @@ __global__ __launch_bounds__(kThreads) void k_dequantize(
         x[i] = (float)((double)((int64_t)q[i] + in_so - zp) * scale);
 }
 
-hipStream_t pick(void* s) {
-    return s ? (hipStream_t)s : qa::stream();
-}
+// Device entries launch on the caller's stream as given (NULL: the null
+// stream, which is also what torch's default stream handle is).
+hipStream_t pick(void* s) { return (hipStream_t)s; }
 
 template <class T>
 T* upload(int slot, const T* h, int64_t n, hipStream_t st) {
@@ -383,8 +388,7 @@ QA_API int qa_d_requantize(const void* acc, int acc_code, void* out,
 }
 
 static dim3 grid_rows(int64_t rows, int64_t cols) {
-    return dim3(qa::grid_1d(cols, kThreads, 1 << 16),
-                (unsigned)std::min<int64_t>(std::max<int64_t>(rows, 1), 65535));
+    return dim3(qa::grid_1d(rows * cols, kThreads, 1 << 20));
 }
 
 QA_API int qa_d_rescale(const void* x, int in_code, int64_t x_rstride,

@@ -30,19 +30,39 @@ __device__ __forceinline__ int64_t wave_sum(int64_t v) {
     return v;
 }
 
-// One wave per (n, c) plane: acc = sum(q - zp_in) in int64, then
-// out = clip(mbqm(acc, mult, shift) + zp_out) - out_so.
-__global__ __launch_bounds__(kThreads) void k_gap(
-    const void* __restrict__ x, int in_code, int64_t x_nstride, int64_t N,
-    int64_t C, int64_t HW, int64_t zp_in, int64_t in_so, int64_t mult,
-    int64_t shift, int64_t zp_out, int64_t qmin, int64_t qmax, void* out,
-    int out_code, int64_t out_so) {
+// GlobalAveragePool: acc = sum over the HW pixels of (q - zp_in) in int64,
+// out = clip(mbqm(acc, mult, shift) + zp_out) - out_so. Element (n, c, p) of
+// x at x + n*x_sn + c*x_sc + p*x_sp. Channels-last inputs (x_sc == 1) use one
+// thread per (n, c), so neighbouring threads read neighbouring bytes.
+__global__ __launch_bounds__(kThreads) void k_gap_cl(
+    const void* __restrict__ x, int in_code, int64_t x_sn, int64_t x_sp,
+    int64_t N, int64_t C, int64_t HW, int64_t zp_in, int64_t in_so,
+    int64_t mult, int64_t shift, int64_t zp_out, int64_t qmin, int64_t qmax,
+    void* out, int out_code, int64_t out_sn, int64_t out_so) {
+    const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t n = blockIdx.y;
+    if (c >= C) return;
+    const int64_t base = n * x_sn + c;
+    int64_t s = 0;
+    for (int64_t p = 0; p < HW; ++p) s += load_s(x, in_code, base + p * x_sp);
+    const int64_t acc = s + HW * (in_so - zp_in);
+    const int64_t q =
+        qa_clip128(qa_mbqm(acc, mult, shift) + zp_out, qmin, qmax);
+    store_s(out, out_code, n * out_sn + c, q - out_so);
+}
+
+// Planar inputs: one wave per (n, c) plane.
+__global__ __launch_bounds__(kThreads) void k_gap_planar(
+    const void* __restrict__ x, int in_code, int64_t x_sn, int64_t x_sc,
+    int64_t N, int64_t C, int64_t HW, int64_t zp_in, int64_t in_so,
+    int64_t mult, int64_t shift, int64_t zp_out, int64_t qmin, int64_t qmax,
+    void* out, int out_code, int64_t out_sn, int64_t out_so) {
     const int64_t plane = (int64_t)blockIdx.x * (kThreads / 64) +
                           (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (plane >= N * C) return;
     const int64_t n = plane / C, c = plane - n * C;
-    const int64_t base = n * x_nstride + c * HW;
+    const int64_t base = n * x_sn + c * x_sc;
     int64_t s = 0;
     for (int64_t i = lane; i < HW; i += 64) s += load_s(x, in_code, base + i);
     s = wave_sum(s);
@@ -50,7 +70,29 @@ __global__ __launch_bounds__(kThreads) void k_gap(
         const int64_t acc = s + HW * (in_so - zp_in);
         const int64_t q =
             qa_clip128(qa_mbqm(acc, mult, shift) + zp_out, qmin, qmax);
-        store_s(out, out_code, plane, q - out_so);
+        store_s(out, out_code, n * out_sn + c, q - out_so);
+    }
+}
+
+// Graph input: float32 NCHW -> quantized channels-last with pixel stride
+// y_sp >= C (padding channels written as 0), one thread per pixel.
+template <class TOut>
+__global__ __launch_bounds__(kThreads) void k_quantize_cl(
+    const float* __restrict__ x, int64_t N, int64_t C, int64_t HW,
+    TOut* __restrict__ y, int64_t y_sp, double scale, int64_t zp,
+    int64_t qmin, int64_t qmax, int64_t so) {
+    const int64_t total = N * HW;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t n = i / HW, p = i - n * HW;
+        TOut* dst = y + i * y_sp;
+        for (int64_t c = 0; c < y_sp; ++c) {
+            int64_t v = 0;
+            if (c < C)
+                v = qa_quantize_one(x[(n * C + c) * HW + p], scale, zp, qmin,
+                                    qmax) - so;
+            dst[c] = (TOut)v;
+        }
     }
 }
 
@@ -113,20 +155,63 @@ bool launched(const char* what) {
 
 }  // namespace
 
-// GlobalAveragePool of device tensor x [N, C, HW] (image stride x_nstride)
-// into out [N, C] with a scalar multiplier (in_scale / (out_scale * HW)).
-QA_API int qa_d_gap(const void* x, int in_code, int64_t x_nstride, int64_t N,
-                    int64_t C, int64_t HW, int64_t zp_in, int64_t in_so,
-                    int64_t mult, int64_t shift, int64_t zp_out, int64_t qmin,
-                    int64_t qmax, void* out, int out_code, int64_t out_so,
+// GlobalAveragePool of x [N, C, HW] (strides x_sn, x_sc, x_sp) into out
+// [N, C] (row stride out_sn) with a scalar multiplier.
+QA_API int qa_d_gap(const void* x, int in_code, int64_t x_sn, int64_t x_sc,
+                    int64_t x_sp, int64_t N, int64_t C, int64_t HW,
+                    int64_t zp_in, int64_t in_so, int64_t mult, int64_t shift,
+                    int64_t zp_out, int64_t qmin, int64_t qmax, void* out,
+                    int out_code, int64_t out_sn, int64_t out_so,
                     void* stream) {
     if (N * C <= 0) return 0;
-    hipStream_t st = stream ? (hipStream_t)stream : qa::stream();
-    const int64_t blocks = qa::ceil_div(N * C, kThreads / 64);
-    k_gap<<<(unsigned)blocks, kThreads, 0, st>>>(
-        x, in_code, x_nstride, N, C, HW, zp_in, in_so, mult, shift, zp_out,
-        qmin, qmax, out, out_code, out_so);
+    hipStream_t st = (hipStream_t)stream;
+    if (x_sc == 1) {
+        if (N > 65535) {
+            qa::set_error("qa_d_gap", "N above 65535");
+            return -1;
+        }
+        dim3 grid((unsigned)qa::ceil_div(C, kThreads), (unsigned)N);
+        k_gap_cl<<<grid, kThreads, 0, st>>>(x, in_code, x_sn, x_sp, N, C, HW,
+                                           zp_in, in_so, mult, shift, zp_out,
+                                           qmin, qmax, out, out_code, out_sn,
+                                           out_so);
+    } else {
+        if (x_sp != 1) {
+            qa::set_error("qa_d_gap", "needs x_sc == 1 or x_sp == 1");
+            return -1;
+        }
+        const int64_t blocks = qa::ceil_div(N * C, kThreads / 64);
+        k_gap_planar<<<(unsigned)blocks, kThreads, 0, st>>>(
+            x, in_code, x_sn, x_sc, N, C, HW, zp_in, in_so, mult, shift,
+            zp_out, qmin, qmax, out, out_code, out_sn, out_so);
+    }
     return launched("qa_d_gap") ? 0 : -1;
+}
+
+// Quantizes a float32 NCHW tensor into channels-last storage (int8 or int16)
+// with pixel stride y_sp (>= C; padding channels are 0).
+QA_API int qa_d_quantize_nhwc(const float* x, int64_t N, int64_t C,
+                              int64_t HW, void* y, int y_code, int64_t y_sp,
+                              double scale, int64_t zp, int64_t qmin,
+                              int64_t qmax, int64_t so, void* stream) {
+    if (N * HW <= 0) return 0;
+    if (y_sp < C) {
+        qa::set_error("qa_d_quantize_nhwc", "pixel stride below C");
+        return -1;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned g = qa::grid_1d(N * HW, kThreads, 1 << 20);
+    if (y_code == 1)
+        k_quantize_cl<int8_t><<<g, kThreads, 0, st>>>(
+            x, N, C, HW, (int8_t*)y, y_sp, scale, zp, qmin, qmax, so);
+    else if (y_code == 2)
+        k_quantize_cl<int16_t><<<g, kThreads, 0, st>>>(
+            x, N, C, HW, (int16_t*)y, y_sp, scale, zp, qmin, qmax, so);
+    else {
+        qa::set_error("qa_d_quantize_nhwc", "storage must be int8 or int16");
+        return -1;
+    }
+    return launched("qa_d_quantize_nhwc") ? 0 : -1;
 }
 
 // Softmax over the last axis of a [rows, cols] device tensor through float:
@@ -137,7 +222,7 @@ QA_API int qa_d_softmax(const void* x, int in_code, int64_t rows, int64_t cols,
                         int64_t out_zp, int64_t qmin, int64_t qmax,
                         int64_t out_so, void* stream) {
     if (rows <= 0 || cols <= 0) return 0;
-    hipStream_t st = stream ? (hipStream_t)stream : qa::stream();
+    hipStream_t st = (hipStream_t)stream;
     const unsigned blocks = (unsigned)(rows < 65535 ? rows : 65535);
     k_softmax<<<blocks, kThreads, 0, st>>>(x, in_code, rows, cols, in_scale,
                                            in_zp, in_so, out, out_code,

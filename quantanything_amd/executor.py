@@ -8,15 +8,19 @@ once into a HIP graph and replayed.
 
 Storage: every quantized tensor lives on the device as int8 (types of at most
 8 bits) or int16 (9-16 bits) holding ``q - so``, ``so`` = 0 for signed types
-and 2^(bits-1) for unsigned ones. Layouts are NCHW; a tensor may be a view
-(``offset`` into a buffer, ``nstride`` elements between images), which is how
-``Split`` outputs are produced without a copy.
+and 2^(bits-1) for unsigned ones. 4-D tensors are channels-last: element
+(n, c, pix) at ``offset + n*sn + c*sc + pix*sp`` with ``sc = 1`` and a pixel
+stride ``sp`` of the channel count rounded up to 16 for int8 (4 for tensors
+of at most 4 channels), which keeps every 16-channel group of a pixel one
+aligned 16-byte load for the MFMA kernel. ``Split`` outputs are channel views
+into their input's buffer (no copy).
 
 Fusion: a Conv / Gemm whose output feeds only a lookup-table activation runs
 the table in its epilogue; if that result feeds only an Add whose other
-operand already exists, the Add (rescale of both operands, sum, clip) runs in
-the same epilogue. Every fused step applies the same integer operations, in
-the same order, as the separate layers would.
+operand already exists, the Add runs in the same epilogue; if the final
+result (or the Split views of it) is a Concat input, the epilogue also writes
+the rescaled copy straight into the Concat buffer. Every fused step applies
+the same integer operations, in the same order, as the separate layers.
 
 torch is used for device memory, the stream and graph capture only; all
 arithmetic is in ``libqa_hip.so``.
@@ -32,44 +36,55 @@ from quantanything_amd import native
 _I64 = ctypes.c_int64
 _P = ctypes.c_void_p
 IDENTITY = (1 << 30, -1)  # multiplier exactly 1.0
+TAIL = 64  # slack bytes after every buffer (16-byte group over-reads)
 
 
 class ConvDesc(ctypes.Structure):
     """``qa_conv_desc`` of ``include/qa_hip.h`` (all fields 8 bytes)."""
 
     _fields_ = (
-        [("x", _P)] + [(n, _I64) for n in ("x_code", "x_nstride", "x_add",
-                                          "rowmajor")]
+        [("x", _P)] + [(n, _I64) for n in ("x_code", "x_sn", "x_sc", "x_sp",
+                                          "x_add")]
         + [(n, _I64) for n in ("N", "C", "H", "W", "Cout", "KH", "KW", "SH",
                                "SW", "PH", "PW", "DH", "DW", "G", "OH", "OW")]
-        + [("w", _P)] + [(n, _I64) for n in ("w_code", "w_kgp", "w_rows",
-                                            "wide", "needs_rowsum")]
+        + [("w", _P)] + [(n, _I64) for n in ("w_code", "w_layout", "w_kgp",
+                                            "w_rows", "wide", "needs_rowsum",
+                                            "fast_epilogue")]
         + [(n, _P) for n in ("corr", "boff", "pre_bias", "mult", "shift")]
         + [(n, _I64) for n in ("zp", "qmin", "qmax")]
         + [("lut", _P), ("lut_offset", _I64), ("lut_len", _I64)]
-        + [("res", _P)] + [(n, _I64) for n in ("res_nstride", "res_so",
-                                              "res_first")]
+        + [("res", _P)] + [(n, _I64) for n in ("res_sn", "res_sc", "res_sp",
+                                              "res_so", "res_first")]
         + [(n, _I64) for n in ("za", "ma", "sa", "zb", "mb", "sb", "add_sign",
                                "add_zp", "add_qmin", "add_qmax")]
-        + [("y", _P)] + [(n, _I64) for n in ("y_code", "y_nstride", "y_so")])
+        + [("y", _P)] + [(n, _I64) for n in ("y_code", "y_sn", "y_sc", "y_sp",
+                                            "y_so")]
+        + [("y2", _P)] + [(n, _I64) for n in ("y2_sn", "y2_sc", "y2_sp",
+                                             "r2_zp_in", "r2_m", "r2_s",
+                                             "r2_zp_out", "r2_qmin",
+                                             "r2_qmax")])
 
 
-def storage_of(quant_type_bits, signed):
+def storage_of(bits, signed):
     """``(code, torch dtype, storage offset)`` of a quantization type."""
-    if quant_type_bits <= 8:
+    if bits <= 8:
         return 1, torch.int8, 0 if signed else 128
-    if quant_type_bits <= 16:
+    if bits <= 16:
         return 2, torch.int16, 0 if signed else 32768
-    raise NotImplementedError(
-        f"{quant_type_bits}-bit tensors are not supported on the device")
+    raise NotImplementedError(f"{bits}-bit tensors are not supported on the "
+                              "device")
 
 
 class DeviceTensor:
-    """A quantized tensor (or view) resident in device memory."""
+    """A quantized tensor (or view) resident in device memory.
 
-    def __init__(self, buf, offset, shape, nstride, code, so, qp):
+    ``shape`` is the logical (NCHW / [N, F]) shape; element (n, c, pix) is at
+    element offset ``offset + n*sn + c*sc + pix*sp``."""
+
+    def __init__(self, buf, offset, shape, sn, sc, sp, code, so, qp):
         self.buf, self.offset = buf, int(offset)
-        self.shape, self.nstride = tuple(int(s) for s in shape), int(nstride)
+        self.shape = tuple(int(s) for s in shape)
+        self.sn, self.sc, self.sp = int(sn), int(sc), int(sp)
         self.code, self.so, self.qp = code, int(so), qp
 
     @property
@@ -77,27 +92,54 @@ class DeviceTensor:
         return self.buf.data_ptr() + self.offset * self.buf.element_size()
 
     @property
-    def per_image(self):
-        return int(np.prod(self.shape[1:], dtype=np.int64))
+    def channels(self):
+        return self.shape[1]
 
     @property
-    def contiguous(self):
-        return self.nstride == self.per_image
+    def pixels(self):
+        return int(np.prod(self.shape[2:], dtype=np.int64))
+
+    def rows_view(self):
+        """``(rows, cols, row_stride)`` of the tensor as a strided matrix
+        (rows = N*pixels, cols = channels), or None when not expressible."""
+        if len(self.shape) == 2:
+            return self.shape[0], self.shape[1], self.sn
+        if self.sc == 1 and self.sn == self.pixels * self.sp:
+            return self.shape[0] * self.pixels, self.channels, self.sp
+        return None
+
+    def contiguous_2d(self):
+        return len(self.shape) == 2 and self.sn == self.shape[1] and \
+            self.sc == 1
 
     def to_host(self):
-        """Quantized values ``q`` as an int32 NumPy array."""
-        n = self.shape[0]
-        flat = self.buf[self.offset:self.offset + max(n - 1, 0) * self.nstride
-                        + self.per_image]
-        rows = [flat[i * self.nstride:i * self.nstride + self.per_image]
-                for i in range(n)]
-        data = torch.stack(rows) if rows else flat[:0]
-        return (data.to(torch.int32).cpu().numpy().reshape(self.shape)
-                + self.so)
+        """Quantized values ``q`` as an int32 NumPy array (NCHW / [N, F])."""
+        if len(self.shape) == 4:
+            n, c, h, w = self.shape
+            v = torch.as_strided(self.buf, (n, c, h, w),
+                                 (self.sn, self.sc, w * self.sp, self.sp),
+                                 self.offset)
+        else:
+            v = torch.as_strided(self.buf, self.shape, (self.sn, self.sc),
+                                 self.offset)
+        return v.to(torch.int32).cpu().numpy() + self.so
+
+
+def fast_epilogue_ok(mult, shift, bias):
+    """Whether every channel allows the library's int64-only requantization
+    (|mult| < 2^31, 1 <= 31+shift <= 62, |bias| < 2^31)."""
+    mult = np.asarray(mult, np.int64)
+    shift = np.asarray(shift, np.int64)
+    ok = bool(np.all(np.abs(mult) < (1 << 31)) and
+              np.all((31 + shift >= 1) & (31 + shift <= 62)))
+    if bias is not None:
+        ok = ok and bool(np.all(np.abs(np.asarray(bias, np.int64))
+                                < (1 << 31)))
+    return ok
 
 
 def _dev(a, dtype):
-    return torch.from_numpy(np.ascontiguousarray(a, dtype=dtype)).cuda()
+    return torch.from_numpy(np.array(a, dtype=dtype, copy=True)).cuda()
 
 
 def _ok(rc, what):
@@ -120,6 +162,7 @@ class DeviceExecutor:
         self.launches = []  # (name, fn(stream))
         self.keep = []  # host objects that launches point into
         self.tensors = {}
+        self.epi = {}  # tensor -> (desc, first channel) written by an epilogue
         self.inputs_f32 = {}
         self.outputs_f32 = {}
         self.cuda_graph = None
@@ -127,16 +170,32 @@ class DeviceExecutor:
 
     # -------------------------------------------------------------- utils --
     def _new(self, shape, qp):
-        n = int(np.prod(shape, dtype=np.int64))
-        buf = torch.empty(max(n, 1), dtype=self.dtype, device="cuda")
-        per = int(np.prod(shape[1:], dtype=np.int64))
-        return DeviceTensor(buf, 0, shape, per, self.code, self.so, qp)
+        """Fresh channels-last (4-D) or row-major (2-D) tensor."""
+        shape = tuple(int(s) for s in shape)
+        if len(shape) == 4:
+            n, c, h, w = shape
+            if c <= 4:
+                cs = 4
+            elif self.code == 1:
+                cs = -(-c // 16) * 16
+            else:
+                cs = c
+            numel = n * h * w * cs
+            buf = torch.empty(numel + TAIL, dtype=self.dtype, device="cuda")
+            return DeviceTensor(buf, 0, shape, h * w * cs, 1, cs, self.code,
+                                self.so, qp)
+        if len(shape) == 2:
+            numel = shape[0] * shape[1]
+            buf = torch.empty(numel + TAIL, dtype=self.dtype, device="cuda")
+            return DeviceTensor(buf, 0, shape, shape[1], 1, 0, self.code,
+                                self.so, qp)
+        raise NotImplementedError(f"{len(shape)}-D tensors on the device")
 
     def _add(self, name, fn):
         self.launches.append((name, fn))
 
-    def _params(self, layer):
-        """Device copies of a layer's integer parameters (cached on it)."""
+    @staticmethod
+    def _params(layer):
         if getattr(layer, "_dev_params", None) is None:
             layer._dev_params = {}
         return layer._dev_params
@@ -146,23 +205,32 @@ class DeviceExecutor:
         c, g = self.c, self.graph
         for name, shape in input_shapes.items():
             qp = c.qparams[name]
-            xf = torch.empty(tuple(shape), dtype=torch.float32, device="cuda")
-            t = self._new(tuple(shape), qp)
+            shape = tuple(shape)
+            xf = torch.empty(shape, dtype=torch.float32, device="cuda")
             self.inputs_f32[name] = xf
+            if len(shape) == 4:
+                t = self._new(shape, qp)
+                n, ch, h, w = shape
+                self._add(f"quantize:{name}", lambda s, xf=xf, t=t, n=n,
+                          ch=ch, hw=h * w, qp=qp: _ok(
+                              self.lib.qa_d_quantize_nhwc(
+                                  xf.data_ptr(), n, ch, hw, t.ptr, t.code,
+                                  t.sp, qp.scale, qp.zp, qp.qmin, qp.qmax,
+                                  t.so, s), "quantize"))
+            else:
+                t = self._new(shape if len(shape) == 2 else
+                              (shape[0], int(np.prod(shape[1:]))), qp)
+                numel = xf.numel()
+                self._add(f"quantize:{name}", lambda s, xf=xf, t=t,
+                          numel=numel, qp=qp: _ok(
+                              self.lib.qa_d_quantize_f32(
+                                  xf.data_ptr(), t.ptr, t.code, numel,
+                                  qp.scale, qp.zp, qp.qmin, qp.qmax, t.so, s),
+                              "quantize"))
             self.tensors[name] = t
-            n = xf.numel()
-            self._add(f"quantize:{name}", lambda s, xf=xf, t=t, n=n, qp=qp:
-                      _ok(self.lib.qa_d_quantize_f32(
-                          xf.data_ptr(), t.ptr, t.code, n, qp.scale, qp.zp,
-                          qp.qmin, qp.qmax, t.so, s), "quantize"))
         for name in c.const_names:
-            qp = c.qparams[name]
-            q = c.const_q[name]
-            t = self._new(q.shape if q.ndim else (1,), qp)
-            t.buf.copy_(torch.from_numpy(
-                (q.astype(np.int64) - t.so).astype(
-                    np.int8 if self.code == 1 else np.int16).reshape(-1)))
-            self.tensors[name] = t
+            raise NotImplementedError(
+                f"constant operand {name} consumed as an activation")
 
         layers = c.layers
         producer = g.producer_index()
@@ -171,13 +239,13 @@ class DeviceExecutor:
             for i in l.data_inputs:
                 cons.setdefault(i, []).append(l)
         absorbed = set()
-        for k, layer in enumerate(layers):
+        for layer in layers:
             if layer.name in absorbed:
                 continue
             layer.check_ready()
             ins = [self.tensors[n] for n in layer.data_inputs]
             if layer.kind in ("conv", "gemm"):
-                lut_layer = add_layer = None
+                lut_layer = add_layer = res = None
                 out_name = layer.node.outputs[0]
                 users = cons.get(out_name, [])
                 if out_name not in g.outputs and len(users) == 1 and \
@@ -185,7 +253,6 @@ class DeviceExecutor:
                     lut_layer = users[0]
                     out_name = lut_layer.node.outputs[0]
                     users = cons.get(out_name, [])
-                res = None
                 if out_name not in g.outputs and len(users) == 1 and \
                         users[0].kind == "add" and \
                         len(users[0].data_inputs) == 2:
@@ -196,21 +263,21 @@ class DeviceExecutor:
                             producer.get(layer.node.outputs[0], 0):
                         add_layer = a
                         res = (others[0], a.data_inputs[0] == others[0])
-                outs = self._plan_weighted(layer, ins[0], lut_layer,
-                                           add_layer, res)
                 final = add_layer or lut_layer or layer
+                y = self._plan_weighted(layer, ins[0], lut_layer, add_layer,
+                                        res)
                 for l in (lut_layer, add_layer):
                     if l is not None:
                         absorbed.add(l.name)
-                self.tensors[final.node.outputs[0]] = outs
+                self.tensors[final.node.outputs[0]] = y
                 continue
             outs = getattr(self, "_plan_" + layer.kind)(layer, ins)
             for name, t in zip(layer.node.outputs, outs):
                 self.tensors[name] = t
         for name in g.outputs:
             t = self.tensors[name]
-            if not t.contiguous:
-                raise NotImplementedError("graph output must be contiguous")
+            if not t.contiguous_2d():
+                raise NotImplementedError("graph outputs must be 2-D")
             yf = torch.empty(t.shape, dtype=torch.float32, device="cuda")
             self.outputs_f32[name] = yf
             n = yf.numel()
@@ -219,51 +286,62 @@ class DeviceExecutor:
                           t.ptr, t.code, yf.data_ptr(), n, t.qp.scale,
                           t.qp.zp, t.so, s), "dequantize"))
 
-    def _weights_dev(self, layer, x, rowmajor):
-        """Packs (once) the layer's weights for the MFMA or VALU path."""
+    # ---------------------------------------------------- conv and gemm --
+    def _mfma_ok(self, layer, x, layout, groups, cg, k_real):
+        if self.code != 1 or layer.wide or k_real >= 131072:
+            return False
+        off_bytes = x.offset  # int8 elements are bytes
+        if layout == 1:
+            return groups == 1 and x.sp % 4 == 0 and x.sn % 4 == 0 and \
+                off_bytes % 4 == 0
+        pix = x.pixels if len(x.shape) == 4 else 1
+        return off_bytes % 16 == 0 and x.sn % 16 == 0 and \
+            (pix == 1 or x.sp % 16 == 0) and (groups == 1 or cg % 16 == 0)
+
+    def _weights_dev(self, layer, x, layout, use_mfma):
         p = self._params(layer)
         a_off = x.so - layer.in_zp
-        key = ("w", a_off, self.code)
+        key = ("w", a_off, self.code, layout, use_mfma)
         if key in p:
             return p[key]
         if layer.kind == "gemm":
-            w = np.ascontiguousarray(layer.w_centered.T)  # [N, K]
-            cout, cg, kh, kw, groups = w.shape[0], w.shape[1], 1, 1, 1
+            w = np.ascontiguousarray(layer.w_centered.T)[:, :, None, None]
+            groups = 1
         else:
             w = layer.w_centered
-            cout, cg, kh, kw = w.shape
             groups = layer.geometry(x.shape)[3]
+        cout, cg, kh, kw = w.shape
         w32 = np.ascontiguousarray(w, dtype=np.int32)
         info = None
-        if self.code == 1 and not layer.wide and cg * kh * kw < 131072:
+        if use_mfma:
             kgp, rows = _I64(0), _I64(0)
             size = self.lib.qa_pack_weights_i8_size(
-                cout, cg, kh, kw, groups, ctypes.byref(kgp),
+                cout, cg, kh, kw, groups, layout, ctypes.byref(kgp),
                 ctypes.byref(rows))
             wp = np.empty(size, np.int8)
             corr = np.empty(cout, np.int64)
             boff = np.empty(cout, np.int32)
             need = ctypes.c_int32(0)
             rc = self.lib.qa_pack_weights_i8(
-                w32.ctypes.data, cout, cg, kh, kw, groups, a_off,
+                w32.ctypes.data, cout, cg, kh, kw, groups, a_off, layout,
                 wp.ctypes.data, corr.ctypes.data, boff.ctypes.data,
                 ctypes.byref(need))
             if rc == 0:
-                info = dict(w=_dev(wp, np.int8), w_code=1, kgp=kgp.value,
-                            rows=rows.value, corr=_dev(corr, np.int64),
+                info = dict(w=_dev(wp, np.int8), w_code=1, layout=layout,
+                            kgp=kgp.value, rows=rows.value,
+                            corr=_dev(corr, np.int64),
                             boff=_dev(boff, np.int32), rowsum=need.value,
                             wide=0)
-        if info is None:  # exact VALU path with int64 accumulation
-            info = dict(w=_dev(w32.reshape(cout, cg, kh, kw), np.int32),
-                        w_code=4, kgp=0, rows=0, corr=None, boff=None,
-                        rowsum=0, wide=1)
-        cout_all = cout
-        info["mult"] = _dev(np.broadcast_to(layer.q_mult, (cout_all,)),
-                            np.int64)
-        info["shift"] = _dev(np.broadcast_to(layer.shift, (cout_all,)),
-                             np.int64)
+        if info is None:  # exact VALU path, int64 accumulation
+            info = dict(w=_dev(w32, np.int32), w_code=4, layout=0, kgp=0,
+                        rows=0, corr=None, boff=None, rowsum=0, wide=1)
+        mult = np.broadcast_to(layer.q_mult, (cout,)).astype(np.int64)
+        shift = np.broadcast_to(layer.shift, (cout,)).astype(np.int64)
+        info["mult"] = _dev(mult, np.int64)
+        info["shift"] = _dev(shift, np.int64)
         info["pre"] = (None if layer.bias_int is None
                        else _dev(layer.bias_int, np.int64))
+        info["fast"] = int(fast_epilogue_ok(mult, shift, layer.bias_int))
         p[key] = info
         return info
 
@@ -286,33 +364,30 @@ class DeviceExecutor:
             out_shape = (n, cout, oh, ow)
             geo = (n, cin, h, w, cout, kh, kw, strides[0], strides[1],
                    pads[0], pads[1], dil[0], dil[1], groups, oh, ow)
-            d.rowmajor = 0
-            d.x_nstride = x.nstride
+            layout = 1 if (groups == 1 and cg <= 4 and kw <= 4 and
+                           x.sp == 4) else 0
         else:
-            k = layer.w_centered.shape[0]
-            if x.shape[-1] != k:
-                raise ValueError(f"gemm shape mismatch: {x.shape} x "
-                                 f"{layer.w_centered.shape}")
-            m = int(np.prod(x.shape[:-1]))
-            if not (x.contiguous or len(x.shape) == 2):
-                raise NotImplementedError("gemm input must be contiguous")
-            ncol = layer.w_centered.shape[1]
+            k, ncol = layer.w_centered.shape
+            if x.shape[-1] != k or len(x.shape) != 2:
+                raise NotImplementedError(
+                    f"gemm input {x.shape} x {layer.w_centered.shape}")
+            m = x.shape[0]
             out_shape = layer.out_shape(x.shape)
             geo = (m, k, 1, 1, ncol, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 1)
-            d.rowmajor = 1
-            d.x_nstride = x.nstride if len(x.shape) == 2 else k
-        info = self._weights_dev(layer, x, d.rowmajor)
+            groups, cg, kh, kw, cout = 1, k, 1, 1, ncol
+            layout = 0
+        use_mfma = self._mfma_ok(layer, x, layout, groups, cg, cg * kh * kw)
+        info = self._weights_dev(layer, x, layout, use_mfma)
         (d.N, d.C, d.H, d.W, d.Cout, d.KH, d.KW, d.SH, d.SW, d.PH, d.PW,
          d.DH, d.DW, d.G, d.OH, d.OW) = geo
-        d.x = x.ptr
-        d.x_code = x.code
+        d.x, d.x_code = x.ptr, x.code
+        d.x_sn, d.x_sc, d.x_sp = x.sn, x.sc, x.sp
         d.x_add = x.so - layer.in_zp
         d.w = info["w"].data_ptr()
-        d.w_code = info["w_code"]
-        d.w_kgp = info["kgp"]
-        d.w_rows = info["rows"]
-        d.wide = info["wide"]
-        d.needs_rowsum = info["rowsum"]
+        d.w_code, d.w_layout = info["w_code"], info["layout"]
+        d.w_kgp, d.w_rows = info["kgp"], info["rows"]
+        d.wide, d.needs_rowsum = info["wide"], info["rowsum"]
+        d.fast_epilogue = info["fast"]
         d.corr = info["corr"].data_ptr() if info["corr"] is not None else None
         d.boff = info["boff"].data_ptr() if info["boff"] is not None else None
         d.pre_bias = info["pre"].data_ptr() if info["pre"] is not None \
@@ -338,66 +413,70 @@ class DeviceExecutor:
             (ma, sa), (mb, sb) = add_layer.mults
             qa_, qb_ = add_layer.in_qp
             o = add_layer.out_qp[0]
-            if layer.kind == "gemm" and not r.contiguous:
-                raise NotImplementedError("strided Gemm residual")
             d.res = r.ptr
-            d.res_nstride = r.nstride if layer.kind == "conv" else d.Cout
-            d.res_so = r.so
+            d.res_sn, d.res_sc, d.res_sp, d.res_so = r.sn, r.sc, r.sp, r.so
             d.res_first = 1 if first else 0
             d.za, d.ma, d.sa = qa_.zp, ma, sa
             d.zb, d.mb, d.sb = qb_.zp, mb, sb
             d.add_sign = add_layer.sign
             d.add_zp, d.add_qmin, d.add_qmax = o.zp, o.qmin, o.qmax
             y.qp = o
-        d.y = y.ptr
-        d.y_code = y.code
-        d.y_nstride = y.nstride if layer.kind == "conv" else d.Cout
-        d.y_so = y.so
+        d.y, d.y_code = y.ptr, y.code
+        d.y_sn, d.y_sc, d.y_sp, d.y_so = y.sn, y.sc, y.sp, y.so
         self.keep.append(d)
+        name = add_layer or lut_layer or layer
+        self.epi[name.node.outputs[0]] = (d, 0, cout)
         self._add(f"conv:{layer.name}", lambda s, d=d:
                   _ok(self.lib.qa_d_conv(ctypes.byref(d), s), "qa_d_conv"))
         return y
 
+    # ------------------------------------------------------- element-wise --
     def _plan_lut(self, layer, ins):
         x = ins[0]
         p = self._params(layer)
         if "lut" not in p:
             p["lut"] = _dev(layer.lut, np.int32)
         y = self._new(x.shape, layer.out_qp[0])
+        xv, yv = x.rows_view(), y.rows_view()
+        if xv is None or yv is None:
+            raise NotImplementedError("table on a non-matrix view")
+        rows, cols, xs = xv
         lut = p["lut"]
         self._add(f"lut:{layer.name}", lambda s: _ok(self.lib.qa_d_lut(
-            x.ptr, x.code, x.nstride, y.ptr, y.code, y.nstride, x.shape[0],
-            x.per_image, layer.lut_offset, lut.data_ptr(), len(layer.lut),
-            x.so, y.so, s), "qa_d_lut"))
+            x.ptr, x.code, xs, y.ptr, y.code, yv[2], rows, cols,
+            layer.lut_offset, lut.data_ptr(), len(layer.lut), x.so, y.so, s),
+            "qa_d_lut"))
         return [y]
+
+    def _binary_views(self, a, b, y):
+        av, bv, yv = a.rows_view(), b.rows_view(), y.rows_view()
+        if a.shape != b.shape or None in (av, bv, yv):
+            raise NotImplementedError("broadcasting element-wise op")
+        return av, bv, yv
 
     def _plan_add(self, layer, ins):
         a, b = ins
-        if a.shape != b.shape:
-            raise NotImplementedError("broadcasting Add on the device")
-        (ma, sa), (mb, sb) = layer.mults
-        qa_, qb_ = layer.in_qp
         o = layer.out_qp[0]
         y = self._new(a.shape, o)
+        av, bv, yv = self._binary_views(a, b, y)
+        (ma, sa), (mb, sb) = layer.mults
+        qa_, qb_ = layer.in_qp
         self._add(f"add:{layer.name}", lambda s: _ok(self.lib.qa_d_add(
-            a.ptr, a.nstride, b.ptr, b.nstride, a.code, y.ptr, y.code,
-            y.nstride, a.shape[0], a.per_image, qa_.zp, ma, sa, qb_.zp, mb,
-            sb, layer.sign, o.zp, o.qmin, o.qmax, a.so, b.so, y.so, s),
-            "qa_d_add"))
+            a.ptr, av[2], b.ptr, bv[2], a.code, y.ptr, y.code, yv[2], av[0],
+            av[1], qa_.zp, ma, sa, qb_.zp, mb, sb, layer.sign, o.zp, o.qmin,
+            o.qmax, a.so, b.so, y.so, s), "qa_d_add"))
         return [y]
 
     def _plan_mul(self, layer, ins):
         a, b = ins
-        if a.shape != b.shape:
-            raise NotImplementedError("broadcasting Mul on the device")
-        qa_, qb_ = layer.in_qp
         o = layer.out_qp[0]
         y = self._new(a.shape, o)
+        av, bv, yv = self._binary_views(a, b, y)
+        qa_, qb_ = layer.in_qp
         self._add(f"mul:{layer.name}", lambda s: _ok(self.lib.qa_d_mul(
-            a.ptr, a.nstride, b.ptr, b.nstride, a.code, y.ptr, y.code,
-            y.nstride, a.shape[0], a.per_image, qa_.zp, qb_.zp, layer.mult,
-            layer.shift, o.zp, o.qmin, o.qmax, a.so, b.so, y.so, s),
-            "qa_d_mul"))
+            a.ptr, av[2], b.ptr, bv[2], a.code, y.ptr, y.code, yv[2], av[0],
+            av[1], qa_.zp, qb_.zp, layer.mult, layer.shift, o.zp, o.qmin,
+            o.qmax, a.so, b.so, y.so, s), "qa_d_mul"))
         return [y]
 
     def _plan_concat(self, layer, ins):
@@ -410,38 +489,68 @@ class DeviceExecutor:
         shape = list(ins[0].shape)
         shape[1] = sum(t.shape[1] for t in ins)
         y = self._new(tuple(shape), o)
-        inner = int(np.prod(shape[2:], dtype=np.int64))
-        off = 0
-        for t, qp, (m, s_) in zip(ins, layer.in_qp, layer.mults):
+        names = layer.data_inputs
+        k, off = 0, 0
+        while k < len(ins):
+            t, qp, (m, s_) = ins[k], layer.in_qp[k], layer.mults[k]
             if qp.scale == o.scale and qp.zp == o.zp:
                 m, s_ = IDENTITY
-            dst = y.ptr + off * inner * y.buf.element_size()
-            self._add(f"concat:{layer.name}", lambda st, t=t, qp=qp, m=m,
-                      s_=s_, dst=dst: _ok(self.lib.qa_d_rescale(
-                          t.ptr, t.code, t.nstride, dst, y.code, y.nstride,
-                          t.shape[0], t.per_image, qp.zp, m, s_, o.zp, o.qmin,
-                          o.qmax, t.so, y.so, st), "qa_d_rescale"))
+            # Parts written by one epilogue (its whole output, possibly as
+            # consecutive Split views) get the copy from that epilogue.
+            e = self.epi.get(names[k])
+            if e is not None and e[1] == 0:
+                d, _, cout = e
+                span, j = 0, k
+                while j < len(ins) and span < cout:
+                    ej = self.epi.get(names[j])
+                    if ej is None or ej[0] is not d or ej[1] != span or \
+                            layer.in_qp[j] != qp:
+                        break
+                    span += ins[j].shape[1]
+                    j += 1
+                if span == cout and not d.y2:
+                    d.y2 = y.ptr + off * y.buf.element_size()
+                    d.y2_sn, d.y2_sc, d.y2_sp = y.sn, y.sc, y.sp
+                    d.r2_zp_in, d.r2_m, d.r2_s = qp.zp, m, s_
+                    d.r2_zp_out, d.r2_qmin, d.r2_qmax = o.zp, o.qmin, o.qmax
+                    off += span
+                    k = j
+                    continue
+            tv = t.rows_view()
+            yv = (y.shape[0] * y.pixels, t.shape[1], y.sp) \
+                if len(y.shape) == 4 else (y.shape[0], t.shape[1], y.sn)
+            if tv is None:
+                raise NotImplementedError("Concat of a non-matrix view")
+            dst = y.ptr + off * y.buf.element_size()
+            self._add(f"concat:{layer.name}", lambda st, t=t, tv=tv, qp=qp,
+                      m=m, s_=s_, dst=dst, yv=yv: _ok(self.lib.qa_d_rescale(
+                          t.ptr, t.code, tv[2], dst, y.code, yv[2], tv[0],
+                          tv[1], qp.zp, m, s_, o.zp, o.qmin, o.qmax, t.so,
+                          y.so, st), "qa_d_rescale"))
             off += t.shape[1]
+            k += 1
         return [y]
 
     def _plan_gap(self, layer, ins):
         x = ins[0]
         n, ch = x.shape[:2]
-        area = int(np.prod(x.shape[2:], dtype=np.int64))
+        area = x.pixels
         mult, shift = layer.multiplier(area)
         o = layer.out_qp[0]
-        y = self._new((n, ch) + (1,) * (len(x.shape) - 2), o)
+        y = self._new((n, ch), o)
         self._add(f"gap:{layer.name}", lambda s: _ok(self.lib.qa_d_gap(
-            x.ptr, x.code, x.nstride, n, ch, area, layer.in_zp, x.so, mult,
-            shift, o.zp, o.qmin, o.qmax, y.ptr, y.code, y.so, s), "qa_d_gap"))
-        return [y]
+            x.ptr, x.code, x.sn, x.sc, x.sp, n, ch, area, layer.in_zp, x.so,
+            mult, shift, o.zp, o.qmin, o.qmax, y.ptr, y.code, y.sn, y.so, s),
+            "qa_d_gap"))
+        # keep the ONNX shape [N, C, 1, 1] as a view of the [N, C] buffer
+        return [DeviceTensor(y.buf, 0, (n, ch) + (1,) * (len(x.shape) - 2),
+                             y.sn, 1, 0, y.code, y.so, o)]
 
     def _plan_bn(self, layer, ins):
         x = ins[0]
-        if not x.contiguous:
-            raise NotImplementedError("BatchNorm on a strided view")
-        n, ch = x.shape[:2]
-        inner = int(np.prod(x.shape[2:], dtype=np.int64))
+        xv = x.rows_view()
+        if xv is None or xv[2] != xv[1]:
+            raise NotImplementedError("BatchNorm on a padded or strided view")
         p = self._params(layer)
         if "mult" not in p:
             p["mult"] = _dev(layer.q_mult, np.int64)
@@ -449,8 +558,9 @@ class DeviceExecutor:
             p["post"] = _dev(layer.q_B, np.int64)
         o = layer.out_qp[0]
         y = self._new(x.shape, o)
+        rows, ch = xv[0], xv[1]
         self._add(f"bn:{layer.name}", lambda s: _ok(self.lib.qa_d_requantize(
-            x.ptr, x.code, y.ptr, y.code, n, ch, inner, p["mult"].data_ptr(),
+            x.ptr, x.code, y.ptr, y.code, rows, ch, 1, p["mult"].data_ptr(),
             p["shift"].data_ptr(), None, p["post"].data_ptr(), o.zp, o.qmin,
             o.qmax, layer.in_zp - x.so, y.so, s), "qa_d_requantize"))
         return [y]
@@ -470,20 +580,22 @@ class DeviceExecutor:
             else:
                 sizes = node.attr("split") or \
                     [x.shape[1] // len(node.outputs)] * len(node.outputs)
-            inner = int(np.prod(x.shape[2:], dtype=np.int64))
             outs, c0 = [], 0
-            for sz in sizes:
+            src = self.epi.get(node.inputs[0])
+            for name, sz in zip(node.outputs, sizes):
                 shape = (x.shape[0], sz) + x.shape[2:]
-                outs.append(DeviceTensor(x.buf, x.offset + c0 * inner, shape,
-                                         x.nstride, x.code, x.so, x.qp))
+                outs.append(DeviceTensor(x.buf, x.offset + c0 * x.sc, shape,
+                                         x.sn, x.sc, x.sp, x.code, x.so,
+                                         x.qp))
+                if src is not None:
+                    self.epi[name] = (src[0], src[1] + c0, src[2])
                 c0 += sz
             return outs
         if op == "Flatten":
-            axis = layer.node.attr("axis", 1)
-            if axis != 1:
-                raise NotImplementedError("Flatten on the device needs axis 1")
-            return [DeviceTensor(x.buf, x.offset, (x.shape[0], x.per_image),
-                                 x.nstride, x.code, x.so, x.qp)]
+            if layer.node.attr("axis", 1) != 1 or x.pixels != 1:
+                raise NotImplementedError("Flatten of a spatial tensor")
+            return [DeviceTensor(x.buf, x.offset, (x.shape[0], x.channels),
+                                 x.sn, x.sc, 0, x.code, x.so, x.qp)]
         raise NotImplementedError(f"{op} on the device")
 
     def _plan_fallback(self, layer, ins):
@@ -492,12 +604,11 @@ class DeviceExecutor:
         if op == "Softmax":
             ax = layer.node.attr("axis", -1 if self.graph.opset >= 13 else 1)
             ax = ax + len(x.shape) if ax < 0 else ax
-            if ax != len(x.shape) - 1 or not x.contiguous:
+            if ax != len(x.shape) - 1 or not x.contiguous_2d():
                 raise NotImplementedError("Softmax over a non-last axis")
             o = layer.out_qp[0]
             y = self._new(x.shape, o)
-            cols = x.shape[-1]
-            rows = int(np.prod(x.shape[:-1], dtype=np.int64))
+            rows, cols = x.shape
             iq = layer.in_qp[0]
             self._add(f"softmax:{layer.name}", lambda s: _ok(
                 self.lib.qa_d_softmax(x.ptr, x.code, rows, cols, iq.scale,

@@ -60,8 +60,8 @@ def _declare(lib):
         "qa_device_arch": (i32, [c.c_char_p, i64]),
         "qa_stream": (p, []),
         "qa_synchronize": (i32, []),
-        "qa_pack_weights_i8_size": (i64, [i64] * 5 + [p, p]),
-        "qa_pack_weights_i8": (i32, [p] + [i64] * 6 + [p, p, p, p]),
+        "qa_pack_weights_i8_size": (i64, [i64] * 6 + [p, p]),
+        "qa_pack_weights_i8": (i32, [p] + [i64] * 7 + [p, p, p, p]),
         "qa_d_conv": (i32, [p, p]),
         "qa_d_requantize": (i32, [p, i32, p, i32] + [i64] * 3 + [p] * 4
                             + [i64] * 5 + [p]),
@@ -70,7 +70,9 @@ def _declare(lib):
         "qa_d_mul": (i32, [p, i64, p, i64, i32, p, i32] + [i64] * 13 + [p]),
         "qa_d_lut": (i32, [p, i32, i64, p, i32, i64, i64, i64, i64, p, i64,
                            i64, i64, p]),
-        "qa_d_gap": (i32, [p, i32] + [i64] * 11 + [p, i32, i64, p]),
+        "qa_d_gap": (i32, [p, i32] + [i64] * 13 + [p, i32, i64, i64, p]),
+        "qa_d_quantize_nhwc": (i32, [p, i64, i64, i64, p, i32, i64, f64, i64,
+                                     i64, i64, i64, p]),
         "qa_d_softmax": (i32, [p, i32, i64, i64, f64, i64, i64, p, i32, f64]
                          + [i64] * 4 + [p]),
         "qa_d_quantize_f32": (i32, [p, p, i32, i64, f64, i64, i64, i64, i64,
