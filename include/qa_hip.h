@@ -148,9 +148,9 @@ typedef struct qa_conv_desc {
     int64_t N, C, H, W, Cout, KH, KW, SH, SW, PH, PW, DH, DW, G, OH, OW;
     const void* w;
     int64_t w_code, w_layout, w_kgp, w_rows, wide, needs_rowsum;
-    int64_t fast_epilogue; /* caller asserts: every channel has |mult| <
-                              2^31, 1 <= 31+shift <= 62, |pre_bias| < 2^31
-                              (int64-only requantization, MFMA path) */
+    const void* epi_plan;  /* device copy of a qa_plan_epilogue_i8 plan for
+                              exactly these parameters, or NULL (MFMA path;
+                              the 128-bit epilogue then runs) */
     const int64_t* corr;
     const int32_t* boff;
     const int64_t* pre_bias;
@@ -168,6 +168,33 @@ typedef struct qa_conv_desc {
     int64_t y2_sn, y2_sc, y2_sp, r2_zp_in, r2_m, r2_s, r2_zp_out, r2_qmin,
         r2_qmax;
 } qa_conv_desc;
+
+/* Host-side planner of the int8 table epilogue of qa_d_conv. From the
+ * per-channel mult / shift / pre_bias and the clip, table, residual Add and
+ * rescaled-copy parameters of a qa_conv_desc (host copies), writes a plan of
+ * qa_epi_plan_bytes(cout) bytes; the caller copies it to the device and sets
+ * epi_plan. Within it the requantization is one 32x32+64-bit multiply-add and
+ * shift, and the table, residual Add and rescale are 256-entry lookups
+ * computed here with the 128-bit arithmetic, so results equal the 128-bit
+ * epilogue's. Returns 1 when planned, 0 when the parameters fall outside the
+ * plan's exact range (|mult| < 2^31, 1 <= 31+shift <= 62, int64 headroom,
+ * at most 256 output levels, residual terms below 2^28), -1 on bad
+ * arguments. */
+typedef struct qa_epi_params {
+    int64_t cout;
+    const int64_t* mult;
+    const int64_t* shift;
+    const int64_t* pre_bias;   /* NULL: 0 */
+    int64_t zp, qmin, qmax;
+    const int32_t* lut;        /* NULL: no table */
+    int64_t lut_offset, lut_len;
+    int64_t has_res, res_first, res_so;
+    int64_t za, ma, sa, zb, mb, sb, add_sign, add_zp, add_qmin, add_qmax;
+    int64_t has_y2, r2_zp_in, r2_m, r2_s, r2_zp_out, r2_qmin, r2_qmax;
+    int64_t y_so;
+} qa_epi_params;
+int64_t qa_epi_plan_bytes(int64_t cout);
+int qa_plan_epilogue_i8(const qa_epi_params* p, void* plan);
 
 /* `stream` of every qa_d_* entry is the hipStream_t to launch on, used as
  * given (NULL: the null stream). The entries are asynchronous and return 0

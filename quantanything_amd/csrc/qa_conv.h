@@ -53,8 +53,7 @@ struct ConvArgs {
     int64_t wp_gstride, wp_rstride; // bytes
     int32_t pad_value;
     int32_t rowsum;                 // some b_off != 0
-    int32_t fast_hint;              // every channel: |mult| < 2^31,
-                                    // 1 <= 31+shift <= 62, |bias| < 2^31
+    const void* plan;               // table epilogue plan (int8 output)
     // ---- plain weights (VALU path): OIHW ----
     const void* w;
     int32_t w_code;                 // 2 int16, 4 int32
@@ -81,6 +80,23 @@ struct ConvArgs {
     int64_t y2_sn, y2_sc, y2_sp;
     int64_t r2_zp_in, r2_m, r2_s, r2_zp_out, r2_qmin, r2_qmax;
 };
+
+// Table epilogue plan for int8 outputs (device buffer written by
+// qa_plan_epilogue_i8). With per-channel constants m (int32), t (1..62) and
+// c = pre_bias*m + 2^(t-1), the requantized value of the int32 accumulator w
+// is q0 = (w*m + c) >> t, exact in int64 and within int32 (the planner checks
+// both). Everything after it is a function of i = clip(q0, A, B) - A, at most
+// 256 values, or, with a residual Add, of the stored residual byte u:
+//   no residual: e = E[i]
+//   residual:    e = E[clip(TC[i] + TR[u], 0, SH)]
+// e holds the stored output byte in bits 0..7 and the stored byte of the
+// rescaled second output in bits 8..15.
+constexpr int PLAN_E = 64;             // int32 E[256]
+constexpr int PLAN_TC = PLAN_E + 1024;  // int32 TC[256]
+constexpr int PLAN_TR = PLAN_TC + 1024; // int32 TR[256]
+constexpr int PLAN_CH = PLAN_TR + 1024; // int32x4 {m, t, c_lo, c_hi} per channel
+// header (int32): [0] A, [1] B, [2] SH, [3] flags
+constexpr int PLAN_RES = 1, PLAN_Y2 = 2;
 
 // Requantize, table and residual Add of one accumulator (mode EPI_QUANT):
 // returns the quantized value q (before the storage offset).

@@ -617,7 +617,7 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
         a.wp_gstride = rows * KGp * 16;
         a.pad_value = (int32_t)(-d->x_add);
         a.rowsum = (int32_t)d->needs_rowsum;
-        a.fast_hint = (int32_t)d->fast_epilogue;
+        a.plan = d->epi_plan;
         return launch_conv_mfma(a, st) ? 0 : -1;
     }
     a.w = d->w;

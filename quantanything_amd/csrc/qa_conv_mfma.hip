@@ -12,11 +12,9 @@
 //
 // Epilogue variants (template EPI):
 //   EPI_RAW32 / EPI_RAW64  accumulators for the reference ABI,
-//   Q8_FAST   int64-only requantization, used when the host has checked
-//             that every multiplier has |M| < 2^31, 1 <= 31+shift <= 62 and
-//             every bias fits int32, so |acc + bias| <= 2^32 and the product
-//             is exact in int64; then round(p * 2^-t) half up equals
-//             (p >> t) + bit (t-1) of p, the reference's 128-bit result;
+//   Q8_TABLE  int8 output through a host-built plan (qa_conv.h): one int64
+//             multiply-add and shift per element, then 256-entry LDS tables
+//             for clip, activation table, residual Add and rescaled copy,
 //   Q8_GENERAL the 128-bit form for any parameters.
 #include "qa_conv.h"
 
@@ -25,7 +23,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int Q8_FAST = 3;
+constexpr int Q8_TABLE = 3;
 constexpr int Q8_GENERAL = 4;
 
 struct PixCtx {
@@ -104,64 +102,37 @@ __device__ __forceinline__ uint32_t pack4(int64_t b0, int64_t b1, int64_t b2,
            ((uint32_t)(uint8_t)b2 << 16) | ((uint32_t)(uint8_t)b3 << 24);
 }
 
-// round(x * m * 2^-t) for 1 <= t <= 62 and an exact int64 product x*m
-__device__ __forceinline__ int64_t mbqm64(int64_t x, int64_t m, int t) {
-    const int64_t p = x * m;
-    return (p >> t) + ((p >> (t - 1)) & 1);
-}
-
-__device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo,
-                                           int64_t hi) {
-    return v < lo ? lo : (v > hi ? hi : v);
-}
-
-template <int EPI>
-__device__ __forceinline__ int64_t quant8(const ConvArgs& a,
-                                          const int* __restrict__ s_lut,
-                                          int64_t v, int64_t m, int t,
-                                          int64_t res_q) {
-    if (EPI == Q8_GENERAL) {
-        int64_t q = qa_clip128(qa_mbqm(v, m, t - 31) + a.zp, a.qmin, a.qmax);
-        if (a.lut) {
-            int64_t idx = q - a.lut_off;
-            idx = idx < 0 ? 0 : (idx >= a.lut_len ? a.lut_len - 1 : idx);
-            q = s_lut ? s_lut[idx] : a.lut[idx];
-        }
-        if (a.res) {
-            const int64_t f = a.res_first ? res_q : q;
-            const int64_t s = a.res_first ? q : res_q;
-            q = qa_clip128(qa_mbqm(f - a.za, a.ma, a.sa) +
-                               (qa_i128)a.add_sign *
-                                   qa_mbqm(s - a.zb, a.mb, a.sb) +
-                               a.add_zp,
-                           a.add_qmin, a.add_qmax);
-        }
-        return q;
-    }
-    int64_t q = clamp64(mbqm64(v, m, t) + a.zp, a.qmin, a.qmax);
+// The 128-bit epilogue of one accumulator (Q8_GENERAL).
+__device__ __forceinline__ int64_t quant_general(const ConvArgs& a,
+                                                 const int* __restrict__ s_lut,
+                                                 int64_t v, int64_t m,
+                                                 int64_t shift, int64_t res_q) {
+    int64_t q = qa_clip128(qa_mbqm(v, m, shift) + a.zp, a.qmin, a.qmax);
     if (a.lut) {
         int64_t idx = q - a.lut_off;
         idx = idx < 0 ? 0 : (idx >= a.lut_len ? a.lut_len - 1 : idx);
-        q = s_lut[idx];
+        q = s_lut ? s_lut[idx] : a.lut[idx];
     }
     if (a.res) {
         const int64_t f = a.res_first ? res_q : q;
         const int64_t s = a.res_first ? q : res_q;
-        q = clamp64(mbqm64(f - a.za, a.ma, (int)(31 + a.sa)) +
-                        a.add_sign *
-                            mbqm64(s - a.zb, a.mb, (int)(31 + a.sb)) +
-                        a.add_zp,
-                    a.add_qmin, a.add_qmax);
+        q = qa_clip128(qa_mbqm(f - a.za, a.ma, a.sa) +
+                           (qa_i128)a.add_sign * qa_mbqm(s - a.zb, a.mb, a.sb) +
+                           a.add_zp,
+                       a.add_qmin, a.add_qmax);
     }
     return q;
 }
 
-template <int EPI>
-__device__ __forceinline__ int64_t rescale8(const ConvArgs& a, int64_t q) {
-    if (EPI == Q8_GENERAL) return rescale2(a, q);
-    return clamp64(mbqm64(q - a.r2_zp_in, a.r2_m, (int)(31 + a.r2_s)) +
-                       a.r2_zp_out,
-                   a.r2_qmin, a.r2_qmax);
+// Low bytes of four table entries packed into one word (byte = 0), or their
+// second bytes (byte = 1).
+__device__ __forceinline__ uint32_t pack_entries(const int e[4], int byte) {
+    const uint32_t sel_lo = byte ? 0x0c0c0501u : 0x0c0c0400u;
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)e[1], (uint32_t)e[0],
+                                              sel_lo);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)e[3], (uint32_t)e[2],
+                                              sel_lo);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 // KSPLIT: the 4 waves share the block's WN*16 pixels and split the K-steps
@@ -170,9 +141,11 @@ __device__ __forceinline__ int64_t rescale8(const ConvArgs& a, int64_t q) {
 // few pixels to give every CU work otherwise.
 template <int WM, int WN, int LAYOUT, int EPI, bool KSPLIT>
 __global__ __launch_bounds__(256) void k_conv_mfma(ConvArgs a) {
-    constexpr bool QUANT = EPI == Q8_FAST || EPI == Q8_GENERAL;
+    constexpr bool QUANT = EPI == Q8_TABLE || EPI == Q8_GENERAL;
+    constexpr bool TABLE = EPI == Q8_TABLE;
     constexpr int KSTRIDE = KSPLIT ? 4 : 1;
-    __shared__ int s_lut[QUANT ? 256 : 1];
+    // Q8_GENERAL: activation table; Q8_TABLE: E, TC, TR of the plan
+    __shared__ int s_tab[TABLE ? 768 : (QUANT ? 256 : 1)];
     __shared__ int s_red[KSPLIT ? 3 * WM * WN * 4 * 64 + 3 * WN * 64 : 1];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -184,9 +157,14 @@ __global__ __launch_bounds__(256) void k_conv_mfma(ConvArgs a) {
     const int kgl = lane >> 4;
     const int col = lane & 15;
     const uint32_t OHW = (uint32_t)(a.OH * a.OW);
-    const bool lds_lut = QUANT && a.lut && a.lut_len <= 256;
-    if (lds_lut) {
-        for (int i = threadIdx.x; i < a.lut_len; i += 256) s_lut[i] = a.lut[i];
+    const bool lds_tab =
+        TABLE || (QUANT && a.lut && a.lut_len <= 256);
+    if (TABLE) {
+        const int* tab = (const int*)((const char*)a.plan + PLAN_E);
+        const int n = (((const int*)a.plan)[3] & PLAN_RES) ? 768 : 256;
+        for (int i = threadIdx.x; i < n; i += 256) s_tab[i] = tab[i];
+    } else if (lds_tab) {
+        for (int i = threadIdx.x; i < a.lut_len; i += 256) s_tab[i] = a.lut[i];
     }
 
     PixCtx px[WN];
@@ -323,16 +301,110 @@ __global__ __launch_bounds__(256) void k_conv_mfma(ConvArgs a) {
             psum[j] = s;
         }
     }
-    if (lds_lut && !KSPLIT) __syncthreads();  // KSPLIT synced above
-    const int* lut = lds_lut ? s_lut : nullptr;
+    if (lds_tab && !KSPLIT) __syncthreads();  // KSPLIT synced above
 
     // ---- epilogue ----
+    if (TABLE) {
+        const int* hd = (const int*)a.plan;
+        const int A = hd[0], B = hd[1], SH = hd[2];
+        const bool res = a.res != nullptr, two = a.y2 != nullptr;
+        const int4* pch = (const int4*)((const char*)a.plan + PLAN_CH);
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int cl = co0 + i * 16 + kgl * 4;  // first of 4 channels
+            const int64_t cg0 = (int64_t)g * a.Cog + cl;
+            uint32_t corr[4], bo[4];
+            int mlt[4], tsh[4];
+            int64_t cst[4];
+            bool cv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                cv[r] = cl + r < a.Cog;
+                const int64_t co = cv[r] ? cg0 + r : cg0 - cl;
+                const int4 pc = pch[co];
+                mlt[r] = pc.x;
+                tsh[r] = pc.y;
+                cst[r] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                                   (uint32_t)pc.z);
+                corr[r] = a.corr ? (uint32_t)a.corr[co] : 0u;
+                bo[r] = a.rowsum ? (uint32_t)a.boff[co] : 0u;
+            }
+            const bool all4 = cv[0] && cv[1] && cv[2] && cv[3];
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                if (!px[j].ok) continue;
+                const uint32_t rs = (uint32_t)psum[j];
+                int e[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    // int32 accumulator (wraps like the reference's)
+                    const int w = (int)((uint32_t)acc[i][j][r] + corr[r] +
+                                        bo[r] * rs);
+                    const int q0 =
+                        (int)(((int64_t)w * mlt[r] + cst[r]) >> tsh[r]);
+                    e[r] = min(max(q0, A), B) - A;
+                }
+                if (res) {
+                    const int64_t rb = (int64_t)px[j].n * a.res_sn +
+                                       (int64_t)px[j].pix * a.res_sp + cg0;
+                    uint32_t u[4];
+                    if (all4 && a.res_sc == 1 && (rb & 3) == 0) {
+                        const uint32_t wv =
+                            *(const uint32_t*)((const int8_t*)a.res + rb);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) u[r] = (wv >> (8 * r)) & 255u;
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            u[r] = cv[r] ? ((const uint8_t*)
+                                                a.res)[rb + r * a.res_sc]
+                                         : 0u;
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int t = s_tab[256 + e[r]] + s_tab[512 + u[r]];
+                        e[r] = min(max(t, 0), SH);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) e[r] = s_tab[e[r]];
+                const int64_t ybase = (int64_t)px[j].n * a.y_sn +
+                                      (int64_t)px[j].pix * a.y_sp;
+                const int64_t yo = ybase + cg0;
+                if (all4 && a.y_sc == 1 && (yo & 3) == 0) {
+                    *(uint32_t*)((int8_t*)a.y + yo) = pack_entries(e, 0);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (cv[r])
+                            ((int8_t*)a.y)[ybase + (cg0 + r) * a.y_sc] =
+                                (int8_t)e[r];
+                }
+                if (two) {
+                    const int64_t b2 = (int64_t)px[j].n * a.y2_sn +
+                                       (int64_t)px[j].pix * a.y2_sp;
+                    const int64_t o2 = b2 + cg0;
+                    if (all4 && a.y2_sc == 1 && (o2 & 3) == 0) {
+                        *(uint32_t*)((int8_t*)a.y2 + o2) = pack_entries(e, 1);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (cv[r])
+                                ((int8_t*)a.y2)[b2 + (cg0 + r) * a.y2_sc] =
+                                    (int8_t)(e[r] >> 8);
+                    }
+                }
+            }
+        }
+        return;
+    }
+    const int* lut = lds_tab ? s_tab : nullptr;
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
         const int cl = co0 + i * 16 + kgl * 4;  // first of 4 channels
         const int64_t cg0 = (int64_t)g * a.Cog + cl;
-        int64_t corr[4], pre[4], mlt[4];
-        int bo[4], tsh[4];
+        int64_t corr[4], pre[4], mlt[4], shf[4];
+        int bo[4];
         bool cv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -342,91 +414,47 @@ __global__ __launch_bounds__(256) void k_conv_mfma(ConvArgs a) {
             bo[r] = a.rowsum ? a.boff[co] : 0;
             pre[r] = (QUANT && a.pre) ? a.pre[co] : 0;
             mlt[r] = QUANT ? a.mult[co] : 0;
-            tsh[r] = QUANT ? (int)(31 + a.shift[co]) : 0;
+            shf[r] = QUANT ? a.shift[co] : 0;
         }
-        const bool all4 = cv[0] && cv[1] && cv[2] && cv[3];
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
             if (!px[j].ok) continue;
             const int64_t rs = psum[j];
             const int64_t ybase = (int64_t)px[j].n * a.y_sn +
                                   (int64_t)px[j].pix * a.y_sp;
-            if (!QUANT) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (!cv[r]) continue;
-                    const int64_t o = ybase + (cg0 + r) * a.y_sc;
-                    if (EPI == EPI_RAW64)
-                        ((int64_t*)a.y)[o] = (int64_t)acc[i][j][r] + corr[r] +
-                                             (int64_t)bo[r] * rs;
-                    else
-                        ((int32_t*)a.y)[o] =
-                            (int32_t)((uint32_t)acc[i][j][r] +
-                                      (uint32_t)corr[r] +
-                                      (uint32_t)bo[r] * (uint32_t)rs);
-                }
-                continue;
-            }
-            int64_t rq[4] = {0, 0, 0, 0};
-            if (a.res) {
-                const int64_t rb = (int64_t)px[j].n * a.res_sn +
-                                   (int64_t)px[j].pix * a.res_sp + cg0;
-                if (all4 && a.res_sc == 1 && (rb & 3) == 0) {
-                    const uint32_t w = *(const uint32_t*)((const int8_t*)a.res +
-                                                          rb);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        rq[r] = (int64_t)(int8_t)(w >> (8 * r)) + a.res_so;
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (cv[r])
-                            rq[r] = (int64_t)((const int8_t*)
-                                                  a.res)[rb + r * a.res_sc] +
-                                    a.res_so;
-                }
-            }
-            int64_t q[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                // the reference adds the bias to the int32 accumulator
-                const int64_t v =
-                    (int64_t)(int32_t)((uint32_t)acc[i][j][r] +
-                                       (uint32_t)corr[r] +
-                                       (uint32_t)bo[r] * (uint32_t)rs) +
-                    pre[r];
-                q[r] = quant8<EPI>(a, lut, v, mlt[r], tsh[r], rq[r]);
-            }
-            const int64_t yo = ybase + cg0;
-            if (all4 && a.y_sc == 1 && (yo & 3) == 0) {
-                *(uint32_t*)((int8_t*)a.y + yo) =
-                    pack4(q[0] - a.y_so, q[1] - a.y_so, q[2] - a.y_so,
-                          q[3] - a.y_so);
-            } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (cv[r])
-                        ((int8_t*)a.y)[ybase + (cg0 + r) * a.y_sc] =
-                            (int8_t)(q[r] - a.y_so);
-            }
-            if (a.y2) {
-                const int64_t b2 = (int64_t)px[j].n * a.y2_sn +
-                                   (int64_t)px[j].pix * a.y2_sp;
-                int64_t q2[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    q2[r] = rescale8<EPI>(a, q[r]) - a.y_so;
-                const int64_t o2 = b2 + cg0;
-                if (all4 && a.y2_sc == 1 && (o2 & 3) == 0) {
-                    *(uint32_t*)((int8_t*)a.y2 + o2) =
-                        pack4(q2[0], q2[1], q2[2], q2[3]);
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (cv[r])
-                            ((int8_t*)a.y2)[b2 + (cg0 + r) * a.y2_sc] =
-                                (int8_t)q2[r];
+                if (!cv[r]) continue;
+                const int64_t o = ybase + (cg0 + r) * a.y_sc;
+                if (EPI == EPI_RAW64) {
+                    ((int64_t*)a.y)[o] = (int64_t)acc[i][j][r] + corr[r] +
+                                         (int64_t)bo[r] * rs;
+                    continue;
                 }
+                const int32_t w = (int32_t)((uint32_t)acc[i][j][r] +
+                                            (uint32_t)corr[r] +
+                                            (uint32_t)bo[r] * (uint32_t)rs);
+                if (EPI == EPI_RAW32) {
+                    ((int32_t*)a.y)[o] = w;
+                    continue;
+                }
+                int64_t rq = 0;
+                if (a.res)
+                    rq = (int64_t)((const int8_t*)a.res)
+                             [(int64_t)px[j].n * a.res_sn +
+                              (int64_t)px[j].pix * a.res_sp +
+                              (cg0 + r) * a.res_sc] +
+                         a.res_so;
+                // the reference adds the bias to the int32 accumulator
+                const int64_t q =
+                    quant_general(a, lut, (int64_t)w + pre[r], mlt[r], shf[r],
+                                  rq);
+                ((int8_t*)a.y)[o] = (int8_t)(q - a.y_so);
+                if (a.y2)
+                    ((int8_t*)a.y2)[(int64_t)px[j].n * a.y2_sn +
+                                    (int64_t)px[j].pix * a.y2_sp +
+                                    (cg0 + r) * a.y2_sc] =
+                        (int8_t)(rescale2(a, q) - a.y_so);
             }
         }
     }
@@ -445,8 +473,8 @@ bool launch_cfg(const ConvArgs& a, int epi, hipStream_t st) {
             k_conv_mfma<WM, WN, LAYOUT, EPI_RAW64, KSPLIT>
                 <<<grid, 256, 0, st>>>(a);
             break;
-        case Q8_FAST:
-            k_conv_mfma<WM, WN, LAYOUT, Q8_FAST, KSPLIT>
+        case Q8_TABLE:
+            k_conv_mfma<WM, WN, LAYOUT, Q8_TABLE, KSPLIT>
                 <<<grid, 256, 0, st>>>(a);
             break;
         default:
@@ -475,12 +503,6 @@ bool launch_wm(const ConvArgs& a, int epi, hipStream_t st) {
     return launch_cfg<WM, 1, LAYOUT, true>(a, epi, st);
 }
 
-// True when a multiplier allows the int64 epilogue.
-bool fast_ok(int64_t m, int64_t shift) {
-    const int64_t am = m < 0 ? -m : m;
-    return am < ((int64_t)1 << 31) && 31 + shift >= 1 && 31 + shift <= 62;
-}
-
 }  // namespace
 
 bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
@@ -495,11 +517,7 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
             set_error("launch_conv_mfma", "int8 output expected");
             return false;
         }
-        // parameters are read back from the host-visible descriptor copies
-        bool fast = a.fast_hint != 0;
-        if (a.res) fast = fast && fast_ok(a.ma, a.sa) && fast_ok(a.mb, a.sb);
-        if (a.y2) fast = fast && fast_ok(a.r2_m, a.r2_s);
-        epi = fast ? Q8_FAST : Q8_GENERAL;
+        epi = a.plan ? Q8_TABLE : Q8_GENERAL;
     }
     if (a.layout == 1) {
         if (a.Cog <= 16) return launch_wm<1, 1>(a, epi, st);

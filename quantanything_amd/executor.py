@@ -48,9 +48,9 @@ class ConvDesc(ctypes.Structure):
         + [(n, _I64) for n in ("N", "C", "H", "W", "Cout", "KH", "KW", "SH",
                                "SW", "PH", "PW", "DH", "DW", "G", "OH", "OW")]
         + [("w", _P)] + [(n, _I64) for n in ("w_code", "w_layout", "w_kgp",
-                                            "w_rows", "wide", "needs_rowsum",
-                                            "fast_epilogue")]
-        + [(n, _P) for n in ("corr", "boff", "pre_bias", "mult", "shift")]
+                                            "w_rows", "wide", "needs_rowsum")]
+        + [(n, _P) for n in ("epi_plan", "corr", "boff", "pre_bias", "mult",
+                             "shift")]
         + [(n, _I64) for n in ("zp", "qmin", "qmax")]
         + [("lut", _P), ("lut_offset", _I64), ("lut_len", _I64)]
         + [("res", _P)] + [(n, _I64) for n in ("res_sn", "res_sc", "res_sp",
@@ -125,17 +125,57 @@ class DeviceTensor:
         return v.to(torch.int32).cpu().numpy() + self.so
 
 
-def fast_epilogue_ok(mult, shift, bias):
-    """Whether every channel allows the library's int64-only requantization
-    (|mult| < 2^31, 1 <= 31+shift <= 62, |bias| < 2^31)."""
-    mult = np.asarray(mult, np.int64)
-    shift = np.asarray(shift, np.int64)
-    ok = bool(np.all(np.abs(mult) < (1 << 31)) and
-              np.all((31 + shift >= 1) & (31 + shift <= 62)))
-    if bias is not None:
-        ok = ok and bool(np.all(np.abs(np.asarray(bias, np.int64))
-                                < (1 << 31)))
-    return ok
+class EpiParams(ctypes.Structure):
+    """``qa_epi_params`` of ``include/qa_hip.h`` (all fields 8 bytes)."""
+
+    _fields_ = (
+        [("cout", _I64)] + [(n, _P) for n in ("mult", "shift", "pre_bias")]
+        + [(n, _I64) for n in ("zp", "qmin", "qmax")]
+        + [("lut", _P), ("lut_offset", _I64), ("lut_len", _I64)]
+        + [(n, _I64) for n in ("has_res", "res_first", "res_so", "za", "ma",
+                               "sa", "zb", "mb", "sb", "add_sign", "add_zp",
+                               "add_qmin", "add_qmax", "has_y2", "r2_zp_in",
+                               "r2_m", "r2_s", "r2_zp_out", "r2_qmin",
+                               "r2_qmax", "y_so")])
+
+
+def plan_epilogue(lib, d, mult, shift, pre=None, lut=None):
+    """Host plan of the int8 table epilogue for the parameters held in the
+    conv descriptor ``d`` (per-channel ``mult`` / ``shift`` / ``pre`` and the
+    activation table ``lut`` as host arrays). Returns the plan bytes (NumPy
+    uint8) or None when the parameters need the 128-bit epilogue."""
+    cout = int(d.Cout)
+    mult = np.ascontiguousarray(np.broadcast_to(mult, (cout,)), np.int64)
+    shift = np.ascontiguousarray(np.broadcast_to(shift, (cout,)), np.int64)
+    e = EpiParams()
+    e.cout, e.mult, e.shift = cout, mult.ctypes.data, shift.ctypes.data
+    keep = [mult, shift]
+    if pre is not None:
+        pre = np.ascontiguousarray(np.broadcast_to(pre, (cout,)), np.int64)
+        keep.append(pre)
+        e.pre_bias = pre.ctypes.data
+    e.zp, e.qmin, e.qmax = d.zp, d.qmin, d.qmax
+    if lut is not None:
+        lut = np.ascontiguousarray(lut, np.int32)
+        keep.append(lut)
+        e.lut, e.lut_offset, e.lut_len = lut.ctypes.data, d.lut_offset, \
+            len(lut)
+    if d.res:
+        e.has_res, e.res_first, e.res_so = 1, d.res_first, d.res_so
+        (e.za, e.ma, e.sa, e.zb, e.mb, e.sb, e.add_sign, e.add_zp,
+         e.add_qmin, e.add_qmax) = (d.za, d.ma, d.sa, d.zb, d.mb, d.sb,
+                                    d.add_sign, d.add_zp, d.add_qmin,
+                                    d.add_qmax)
+    if d.y2:
+        e.has_y2 = 1
+        (e.r2_zp_in, e.r2_m, e.r2_s, e.r2_zp_out, e.r2_qmin, e.r2_qmax) = (
+            d.r2_zp_in, d.r2_m, d.r2_s, d.r2_zp_out, d.r2_qmin, d.r2_qmax)
+    e.y_so = d.y_so
+    plan = np.zeros(lib.qa_epi_plan_bytes(cout), np.uint8)
+    rc = lib.qa_plan_epilogue_i8(ctypes.byref(e), plan.ctypes.data)
+    if rc < 0:
+        raise ValueError("qa_plan_epilogue_i8: bad arguments")
+    return plan if rc == 1 else None
 
 
 def _dev(a, dtype):
@@ -163,6 +203,7 @@ class DeviceExecutor:
         self.keep = []  # host objects that launches point into
         self.tensors = {}
         self.epi = {}  # tensor -> (desc, first channel) written by an epilogue
+        self.mfma_descs = []  # (desc, host params, host table) to plan
         self.inputs_f32 = {}
         self.outputs_f32 = {}
         self.cuda_graph = None
@@ -274,6 +315,7 @@ class DeviceExecutor:
             outs = getattr(self, "_plan_" + layer.kind)(layer, ins)
             for name, t in zip(layer.node.outputs, outs):
                 self.tensors[name] = t
+        self._plan_epilogues()
         for name in g.outputs:
             t = self.tensors[name]
             if not t.contiguous_2d():
@@ -341,7 +383,7 @@ class DeviceExecutor:
         info["shift"] = _dev(shift, np.int64)
         info["pre"] = (None if layer.bias_int is None
                        else _dev(layer.bias_int, np.int64))
-        info["fast"] = int(fast_epilogue_ok(mult, shift, layer.bias_int))
+        info["host"] = (mult, shift, layer.bias_int)
         p[key] = info
         return info
 
@@ -387,7 +429,6 @@ class DeviceExecutor:
         d.w_code, d.w_layout = info["w_code"], info["layout"]
         d.w_kgp, d.w_rows = info["kgp"], info["rows"]
         d.wide, d.needs_rowsum = info["wide"], info["rowsum"]
-        d.fast_epilogue = info["fast"]
         d.corr = info["corr"].data_ptr() if info["corr"] is not None else None
         d.boff = info["boff"].data_ptr() if info["boff"] is not None else None
         d.pre_bias = info["pre"].data_ptr() if info["pre"] is not None \
@@ -424,11 +465,25 @@ class DeviceExecutor:
         d.y, d.y_code = y.ptr, y.code
         d.y_sn, d.y_sc, d.y_sp, d.y_so = y.sn, y.sc, y.sp, y.so
         self.keep.append(d)
+        if d.w_code == 1 and d.y_code == 1:
+            self.mfma_descs.append(
+                (d, info["host"],
+                 None if lut_layer is None else lut_layer.lut))
         name = add_layer or lut_layer or layer
         self.epi[name.node.outputs[0]] = (d, 0, cout)
         self._add(f"conv:{layer.name}", lambda s, d=d:
                   _ok(self.lib.qa_d_conv(ctypes.byref(d), s), "qa_d_conv"))
         return y
+
+    def _plan_epilogues(self):
+        """Table-epilogue plans of the int8 MFMA convolutions, built once the
+        descriptors are final (a later Concat may add the rescaled copy)."""
+        for d, (mult, shift, pre), lut in self.mfma_descs:
+            plan = plan_epilogue(self.lib, d, mult, shift, pre, lut)
+            if plan is not None:
+                dev = _dev(plan, np.uint8)
+                self.keep.append(dev)
+                d.epi_plan = dev.data_ptr()
 
     # ------------------------------------------------------- element-wise --
     def _plan_lut(self, layer, ins):

@@ -63,6 +63,8 @@ def _declare(lib):
         "qa_pack_weights_i8_size": (i64, [i64] * 6 + [p, p]),
         "qa_pack_weights_i8": (i32, [p] + [i64] * 7 + [p, p, p, p]),
         "qa_d_conv": (i32, [p, p]),
+        "qa_epi_plan_bytes": (i64, [i64]),
+        "qa_plan_epilogue_i8": (i32, [p, p]),
         "qa_d_requantize": (i32, [p, i32, p, i32] + [i64] * 3 + [p] * 4
                             + [i64] * 5 + [p]),
         "qa_d_rescale": (i32, [p, i32, i64, p, i32] + [i64] * 11 + [p]),

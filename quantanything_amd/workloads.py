@@ -19,7 +19,7 @@ import numpy as np
 import torch
 
 from quantanything_amd import native, synth
-from quantanything_amd.executor import ConvDesc, _dev, _ok, fast_epilogue_ok
+from quantanything_amd.executor import ConvDesc, _dev, _ok, plan_epilogue
 
 
 class _Workload:
@@ -47,6 +47,15 @@ class _Workload:
         self.corr = _dev(corr, np.int64)
         self.boff = _dev(boff, np.int32)
         return kgp.value, rows.value, need.value
+
+    def _plan(self, d, mult, shift, bias, lut=None):
+        plan = plan_epilogue(self.lib, d, mult, shift, bias, lut)
+        if plan is None:
+            raise RuntimeError("workload parameters need the 128-bit "
+                               "epilogue")
+        self.plan = _dev(plan, np.uint8)
+        d.epi_plan = self.plan.data_ptr()
+        self.d = d
 
     def launch(self, stream=None):
         s = stream if stream is not None else \
@@ -95,11 +104,9 @@ class GemmWorkload(_Workload):
         d.corr, d.boff = self.corr.data_ptr(), self.boff.data_ptr()
         d.pre_bias, d.mult, d.shift = (p.data_ptr() for p in self.params)
         d.zp, d.qmin, d.qmax = g["zp_out"], g["qmin"], g["qmax"]
-        d.fast_epilogue = int(fast_epilogue_ok(g["mult"], g["shift"],
-                                               g["bias"]))
         d.y, d.y_code, d.y_sn, d.y_sc, d.y_sp, d.y_so = (
             self.y.data_ptr(), 1, n, 1, 0, 128)
-        self.d = d
+        self._plan(d, g["mult"], g["shift"], g["bias"])
         self.out_shape = (m, n)
         self.ops = 2 * m * n * k
         self.bytes = m * k + k * n + m * n + n * 24
@@ -141,13 +148,11 @@ class ConvWorkload(_Workload):
         d.corr, d.boff = self.corr.data_ptr(), self.boff.data_ptr()
         d.pre_bias, d.mult, d.shift = (p_.data_ptr() for p_ in self.params[:3])
         d.zp, d.qmin, d.qmax = c["zp_out"], c["qmin"], c["qmax"]
-        d.fast_epilogue = int(fast_epilogue_ok(c["mult"], c["shift"],
-                                               c["bias"]))
         d.lut, d.lut_offset, d.lut_len = (self.params[3].data_ptr(),
                                           c["lut_offset"], len(c["lut"]))
         d.y, d.y_code, d.y_sn, d.y_sc, d.y_sp, d.y_so = (
             self.y.data_ptr(), 1, oh * ow * cout, 1, cout, 128)
-        self.d = d
+        self._plan(d, c["mult"], c["shift"], c["bias"], c["lut"])
         self.out_shape = (n, cout, oh, ow)
         self.ops = 2 * n * cout * oh * ow * cin * kh * kw
         self.bytes = x.size + w.size + n * cout * oh * ow + cout * 24 + 1024
