@@ -72,6 +72,27 @@ __device__ __forceinline__ int64_t qa_quantize_one(float x, double scale,
     return (int64_t)(int32_t)v;
 }
 
+// qa_quantize_one with a multiplication by inv = 1/scale (double) instead
+// of the division. The product is within 2^-51 relative of the correctly
+// rounded quotient, so both round to the same integer unless the product
+// lies within 2^-48 * |y| of a half-integer (or is huge, infinite or NaN);
+// those take the division. Bit-identical to qa_quantize_one.
+__device__ __forceinline__ int64_t qa_quantize_one_fast(float x, double scale,
+                                                        double inv, int64_t zp,
+                                                        int64_t qmin,
+                                                        int64_t qmax) {
+    const double y = (double)x * inv;
+    const double r = rint(y);
+    const double ay = fabs(y);
+    if (!(ay < 2147483648.0) ||
+        fabs(fabs(y - r) - 0.5) <= ay * 0x1p-48)
+        return qa_quantize_one(x, scale, zp, qmin, qmax);
+    double v = r + (double)zp;
+    if (v < (double)qmin) v = (double)qmin;
+    if (v > (double)qmax) v = (double)qmax;
+    return (int64_t)(int32_t)v;
+}
+
 // --------------------------------------------------------------- errors ---
 namespace qa {
 

@@ -50,6 +50,8 @@ struct ConvArgs {
     const int8_t* wp;
     int32_t layout;                 // 0 tap-major 16-channel groups, 1 stem
     int32_t CB, KG, KGp, Kreal;
+    uint64_t mg_cb, mg_kw;          // ceil(2^32 / CB), ceil(2^32 / KW)
+    int32_t st_dn, st_doy, st_dox;  // a wave's pixel stride as (n, oy, ox)
     int64_t wp_gstride, wp_rstride; // bytes
     int32_t pad_value;
     int32_t rowsum;                 // some b_off != 0

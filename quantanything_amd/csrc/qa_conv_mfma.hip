@@ -1,20 +1,25 @@
 // int8 MFMA convolution / GEMM (data layout: qa_conv.h).
 //
-// Work-group = 4 wave64s, each owning the same WM*16 output channels and its
-// own WN*16 consecutive output pixels (batch folded in), so every activation
-// byte a wave loads is used only by that wave and the weight fragments are
-// shared through L1/L2 by all waves and work-groups. Fragments are loaded
-// straight from global memory into registers (16 contiguous bytes per lane),
-// one K-step ahead of the MFMAs that consume them; there is no barrier in
-// the main loop. The epilogue requantizes, applies the table (held in LDS),
-// the residual Add and an optional rescaled second output, and stores 4
-// consecutive output channels of a pixel as one 32-bit word.
+// Persistent tiles. A tile is 16 consecutive output pixels (batch folded
+// in) times the WM*16 output channels of the work-group's channel block
+// (blockIdx.y). Each wave64 walks its own sequence of tiles (tile, tile +
+// stride, ...); with KSPLIT the 4 waves of a work-group share each tile and
+// split its K-steps. Fragments come straight from global memory into
+// registers (16 contiguous bytes per lane) through a ring of D K-steps that
+// runs across tile boundaries, so the loads of the next tile are in flight
+// while the current tile's MFMAs and epilogue execute; there is no barrier
+// in the main loop (KSPLIT: two per tile, for the reduction).
+//
+// Everything the epilogue needs besides the accumulators is ready before
+// the loop: the tables and the block's per-channel records sit in LDS, and
+// the residual words of the next tile are fetched one tile ahead.
 //
 // Epilogue variants (template EPI):
 //   EPI_RAW32 / EPI_RAW64  accumulators for the reference ABI,
 //   Q8_TABLE  int8 output through a host-built plan (qa_conv.h): one int64
 //             multiply-add and shift per element, then 256-entry LDS tables
-//             for clip, activation table, residual Add and rescaled copy,
+//             for clip, activation table, residual Add and rescaled copy;
+//             4 consecutive channels of a pixel are stored as one word,
 //   Q8_GENERAL the 128-bit form for any parameters.
 #include "qa_conv.h"
 
@@ -26,18 +31,64 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int Q8_TABLE = 3;
 constexpr int Q8_GENERAL = 4;
 
-struct PixCtx {
-    const int8_t* base;  // image base + group channel offset
-    int iy0, ix0;
-    int ok;
-    uint32_t n, pix;
+// Output pixel of one lane, walked through the tiles by a constant stride
+// (st_dn, st_doy, st_dox) with one carry per coordinate instead of a
+// division per tile.
+struct PixPos {
+    int n, oy, ox;
 };
+
+__device__ __forceinline__ PixPos pix_decode(const ConvArgs& a, int64_t p) {
+    const uint32_t pp = (uint32_t)p;  // < 2^31
+    const uint32_t ohw = (uint32_t)(a.OH * a.OW);
+    PixPos q;
+    q.n = (int)(pp / ohw);
+    const uint32_t pix = pp - (uint32_t)q.n * ohw;
+    q.oy = (int)(pix / (uint32_t)a.OW);
+    q.ox = (int)pix - q.oy * a.OW;
+    return q;
+}
+
+__device__ __forceinline__ void pix_step(const ConvArgs& a, PixPos& q) {
+    q.ox += a.st_dox;
+    const int cx = q.ox >= a.OW;
+    q.ox -= cx ? a.OW : 0;
+    q.oy += a.st_doy + cx;
+    const int cy = q.oy >= a.OH;
+    q.oy -= cy ? a.OH : 0;
+    q.n += a.st_dn + cy;
+}
+
+// Fetch side of one lane's pixel: image base (+ group channel offset) and
+// the top-left input coordinate of its receptive field.
+struct FetchPix {
+    const int8_t* base;  // image base (+ group channel offset)
+    const int8_t* org;   // base + offset of input position (iy0, ix0)
+    int iy0, ix0;
+};
+
+__device__ __forceinline__ FetchPix fetch_pix(const ConvArgs& a, PixPos q,
+                                              int g) {
+    FetchPix f;
+    const int n = q.n < a.N ? q.n : 0;  // past the end: read image 0
+    f.iy0 = q.oy * a.SH - a.PH;
+    f.ix0 = q.ox * a.SW - a.PW;
+    f.base = (const int8_t*)a.x + (int64_t)n * a.x_sn + (int64_t)g * a.Cg;
+    f.org = f.base + ((int64_t)f.iy0 * a.W + f.ix0) * a.x_sp;
+    return f;
+}
+
+// floor(n / d) for n < 2^16 with m = ceil(2^32 / d) (d < 2^16): the error
+// of m*d - 2^32 < d stays below one step for such n.
+__device__ __forceinline__ int div_magic(int n, uint64_t m) {
+    return (int)(((uint64_t)(uint32_t)n * m) >> 32);
+}
 
 __device__ __forceinline__ int splat4(int b) {
     return (int)((uint32_t)(uint8_t)b * 0x01010101u);
 }
 
-// sum of the first nreal signed bytes of v (nreal in 1..16)
+// sum of the first nreal signed bytes of v (nreal in 0..16)
 __device__ __forceinline__ int bytes_sum(v4i v, int nreal) {
     int s = 0;
 #pragma unroll
@@ -51,55 +102,89 @@ __device__ __forceinline__ int bytes_sum(v4i v, int nreal) {
     return s;
 }
 
-// B fragment: 16 bytes of K for one pixel.
-template <int LAYOUT>
-__device__ __forceinline__ v4i load_b(const ConvArgs& a, const PixCtx& P,
-                                      bool kvalid, int ky, int kx, int cb,
-                                      int kg, int* psum) {
-    v4i v = {0, 0, 0, 0};
-    if (!P.ok || !kvalid) return v;
-    if (LAYOUT == 0) {
-        const int iy = P.iy0 + ky * a.DH;
-        const int ix = P.ix0 + kx * a.DW;
-        if (iy < 0 || iy >= a.H || ix < 0 || ix >= a.W) {
-            const int pv = splat4(a.pad_value);
-            v = v4i{pv, pv, pv, pv};
-            if (a.rowsum) *psum += min(16, a.Cg - cb * 16) * a.pad_value;
-        } else {
-            v = *(const v4i*)(P.base + ((int64_t)iy * a.W + ix) * a.x_sp +
-                              cb * 16);
-            if (a.rowsum) *psum += bytes_sum(v, min(16, a.Cg - cb * 16));
-        }
-        return v;
-    }
-    // LAYOUT 1: k-group kg = kernel row; 4 bytes (channels) per kx
-    const int iy = P.iy0 + kg * a.DH;
-    const bool row_ok = iy >= 0 && iy < a.H;
-    const int mask = a.Cg >= 4 ? 0x01010101
-                               : (int)((1u << (8 * a.Cg)) - 1) & 0x01010101;
+// sum of the real bytes of a layout-1 fragment: the first nreal bytes of
+// each of the first KW words
+__device__ __forceinline__ int bytes_sum_l1(v4i v, int nreal, int KW) {
+    const int mask = nreal >= 4 ? 0x01010101
+                                : (int)((1u << (8 * nreal)) - 1) & 0x01010101;
+    int s = 0;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        if (t < a.KW) {
-            const int ix = P.ix0 + t * a.DW;
-            int w;
-            if (row_ok && ix >= 0 && ix < a.W) {
-                w = *(const int*)(P.base + ((int64_t)iy * a.W + ix) * a.x_sp);
-                if (a.rowsum) *psum = __builtin_amdgcn_sdot4(w, mask, *psum,
-                                                             false);
-            } else {
-                w = splat4(a.pad_value);
-                if (a.rowsum) *psum += a.Cg * a.pad_value;
-            }
-            v[t] = w;
-        }
+    for (int w = 0; w < 4; ++w)
+        if (w < KW) s = __builtin_amdgcn_sdot4(v[w], mask, s, false);
+    return s;
+}
+
+
+// Where k-group kg of one lane reads (layout 0: tap kg / CB, channel block
+// kg % CB; layout 1: kernel row kg): input offsets (dy, dx) from the
+// pixel's receptive-field origin and the byte offset of that position.
+struct KTap {
+    int dy, dx;
+    int64_t off;
+      int nreal;  // real bytes: layout 0 of the 16, layout 1 of each word
+};
+
+template <int LAYOUT>
+__device__ __forceinline__ KTap ktap(const ConvArgs& a, int kg) {
+    KTap t;
+    if (LAYOUT == 0) {
+        const int tap = div_magic(kg, a.mg_cb);
+        const int cb = kg - tap * a.CB;
+        const int ky = div_magic(tap, a.mg_kw);
+        const int kx = tap - ky * a.KW;
+        t.dy = ky * a.DH;
+        t.dx = kx * a.DW;
+        t.off = ((int64_t)t.dy * a.W + t.dx) * a.x_sp + cb * 16;
+        t.nreal = kg < a.KG ? min(16, a.Cg - cb * 16) : 0;
+    } else {
+        t.dy = kg * a.DH;
+        t.dx = 0;
+        t.off = (int64_t)t.dy * a.W * a.x_sp;
+        t.nreal = kg < a.KG ? a.Cg : 0;
     }
+    return t;
+}
+
+// B fragment of one pixel, loaded from an address that is always inside
+// the input (image padding and pixels past the end read the image origin);
+// *pad receives the lanes that must read pad_value instead (layout 0: a
+// flag; layout 1: one bit per kx word), applied when the fragment is used.
+template <int LAYOUT>
+__device__ __forceinline__ v4i load_b(const ConvArgs& a, const FetchPix& P,
+                                      const KTap& t, int* pad) {
+    const int iy = P.iy0 + t.dy;
+    const bool row_ok = (unsigned)iy < (unsigned)a.H;
+    if (LAYOUT == 0) {
+        const int ix = P.ix0 + t.dx;
+        const bool in = row_ok && (unsigned)ix < (unsigned)a.W;
+        *pad = !in;
+        return *(const v4i*)(in ? P.org + t.off : P.base);
+    }
+    v4i v;
+    int m = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int ix = P.ix0 + k * a.DW;
+        const bool in = row_ok && (unsigned)ix < (unsigned)a.W;
+        if (!in) m |= 1 << k;
+        v[k] = *(const int*)(in ? P.org + t.off + (int64_t)k * a.DW * a.x_sp
+                                : P.base);
+    }
+    *pad = m;
     return v;
 }
 
-__device__ __forceinline__ uint32_t pack4(int64_t b0, int64_t b1, int64_t b2,
-                                          int64_t b3) {
-    return (uint32_t)(uint8_t)b0 | ((uint32_t)(uint8_t)b1 << 8) |
-           ((uint32_t)(uint8_t)b2 << 16) | ((uint32_t)(uint8_t)b3 << 24);
+// The fragment as the MFMA consumes it: pad_value where the image is padded.
+template <int LAYOUT>
+__device__ __forceinline__ v4i apply_pad(v4i v, int pad, int pv) {
+    if (LAYOUT == 0) {
+        if (pad) v = v4i{pv, pv, pv, pv};
+        return v;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (pad & (1 << k)) v[k] = pv;
+    return v;
 }
 
 // The 128-bit epilogue of one accumulator (Q8_GENERAL).
@@ -135,353 +220,411 @@ __device__ __forceinline__ uint32_t pack_entries(const int e[4], int byte) {
     return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
-// KSPLIT: the 4 waves share the block's WN*16 pixels and split the K-steps
-// (wave w takes steps w, w+4, ...); the partial accumulators are summed
-// through LDS and wave 0 runs the epilogue. Used when the output has too
-// few pixels to give every CU work otherwise.
-template <int WM, int WN, int LAYOUT, int EPI, bool KSPLIT>
-__global__ __launch_bounds__(256) void k_conv_mfma(ConvArgs a) {
+
+// Waves per SIMD the register allocation must allow (occupancy target).
+template <int WM>
+constexpr int waves_per_simd() {
+    return WM >= 8 ? 2 : (WM >= 2 ? 3 : 4);
+}
+
+// K-steps in flight per wave (ring of fragment registers), within the
+// register budget of the tile.
+template <int WM>
+constexpr int ring_depth() {
+    return WM <= 1 ? 4 : (WM <= 2 ? 3 : 2);
+}
+
+template <int WM, int LAYOUT, int EPI, bool KSPLIT>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
+    ConvArgs a) {
     constexpr bool QUANT = EPI == Q8_TABLE || EPI == Q8_GENERAL;
     constexpr bool TABLE = EPI == Q8_TABLE;
     constexpr int KSTRIDE = KSPLIT ? 4 : 1;
+    constexpr int D = ring_depth<WM>();
     // Q8_GENERAL: activation table; Q8_TABLE: E, TC, TR of the plan
     __shared__ int s_tab[TABLE ? 768 : (QUANT ? 256 : 1)];
-    __shared__ int s_red[KSPLIT ? 3 * WM * WN * 4 * 64 + 3 * WN * 64 : 1];
+    // Q8_TABLE: the block's channel records {m, t, c_lo, c_hi}, {corr, boff}
+    __shared__ int4 s_pc[TABLE ? WM * 16 : 1];
+    __shared__ int2 s_cb[TABLE ? WM * 16 : 1];
+    __shared__ int s_red[KSPLIT ? 3 * (WM * 4 + 1) * 64 : 1];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave index in a scalar register: the tile walk below is wave-uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = blockIdx.z;
-    const int co0 = blockIdx.y * (WM * 16);
-    const int64_t pw0 =
-        KSPLIT ? (int64_t)blockIdx.x * (WN * 16)
-               : (int64_t)blockIdx.x * (4 * WN * 16) + (int64_t)wave * (WN * 16);
     const int kgl = lane >> 4;
     const int col = lane & 15;
-    const uint32_t OHW = (uint32_t)(a.OH * a.OW);
-    const bool lds_tab =
-        TABLE || (QUANT && a.lut && a.lut_len <= 256);
+    const bool res = TABLE && a.res != nullptr;
+    const bool lds_tab = TABLE || (QUANT && a.lut && a.lut_len <= 256);
+
+    // Tiles of 16 consecutive output pixels; the work-groups that run on
+    // one XCD (consecutive block ids go round-robin over the 8 XCDs) take a
+    // contiguous range. A wave's tiles are tile, tile + tstride, ...
+    const uint32_t nb = gridDim.x;
+    // block b runs on XCD b % 8 as that XCD's (b / 8)-th block; XCD x holds
+    // q + (x < r) blocks (nb = 8q + r) and takes the x-th contiguous range
+    const uint32_t xcd = blockIdx.x & 7, q8 = nb >> 3, r8 = nb & 7;
+    const uint32_t bx = xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3);
+    const int64_t ntiles = (a.M + 15) >> 4;
+    const int64_t tstride = KSPLIT ? (int64_t)nb : (int64_t)nb * 4;
+    int64_t tile = KSPLIT ? (int64_t)bx : (int64_t)bx * 4 + wave;
+    const bool has_tile = tile < ntiles;  // uniform within a KSPLIT group
+
+    const int KS = a.KGp >> 2;                   // K-steps of 64 bytes
+    const int L = KSPLIT ? (KS + 3) >> 2 : KS;   // steps per wave and tile
+    const int st0 = KSPLIT ? wave : 0;
+
+    const int8_t* wrow = a.wp + (int64_t)g * a.wp_gstride +
+                         (int64_t)(blockIdx.y * (WM * 16) + col) *
+                             a.wp_rstride +
+                         kgl * 16;
+    const int64_t wstep = 16 * a.wp_rstride;  // next 16 rows
+
+    // ---- fetch side: (ftile, fi) is the next K-step to load; the stream
+    // of (tile, step) runs through the D ring slots without gaps ----
+    const PixPos p0 = pix_decode(a, tile * 16 + col);
+    int64_t ftile = tile;
+    int fi = 0;
+    PixPos fpos = p0;
+    FetchPix fp = fetch_pix(a, fpos, g);
+    v4i af[D][WM], bf[D];
+    int pd[D];  // pad flags of the slot's B fragment
+    int nr[D];  // real bytes of the slot's B fragment (row sums)
+    auto fetch = [&](v4i* fa, v4i& fb, int& pds, int& nrs)
+                     __attribute__((always_inline)) {
+        const int step = st0 + fi * KSTRIDE;
+        if (ftile < ntiles && step < KS) {
+            const KTap t = ktap<LAYOUT>(a, 4 * step + kgl);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+                fa[i] = *(const v4i*)(wrow + i * wstep + step * 64);
+            fb = load_b<LAYOUT>(a, fp, t, &pds);
+            nrs = t.nreal;
+        }
+        if (ftile < ntiles) {
+            if (++fi == L) {
+                fi = 0;
+                ftile += tstride;
+                pix_step(a, fpos);
+                fp = fetch_pix(a, fpos, g);
+            }
+        }
+    };
+    // plan header (clip bounds of the requantized value, residual range)
+    int pA = 0, pB = 0, pSH = 0;
     if (TABLE) {
-        const int* tab = (const int*)((const char*)a.plan + PLAN_E);
-        const int n = (((const int*)a.plan)[3] & PLAN_RES) ? 768 : 256;
-        for (int i = threadIdx.x; i < n; i += 256) s_tab[i] = tab[i];
-    } else if (lds_tab) {
-        for (int i = threadIdx.x; i < a.lut_len; i += 256) s_tab[i] = a.lut[i];
+        const int4 h = *(const int4*)a.plan;
+        pA = h.x;
+        pB = h.y;
+        pSH = h.z;
     }
-
-    PixCtx px[WN];
+    // first loads of the ring, then the tables: their latencies overlap
+    if (has_tile) {
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
-        const int64_t p = pw0 + j * 16 + col;
-        px[j].ok = p < a.M;
-        const uint32_t pp = px[j].ok ? (uint32_t)p : 0u;
-        const uint32_t n = pp / OHW;
-        const uint32_t pix = pp - n * OHW;
-        const int oy = (int)(pix / (uint32_t)a.OW);
-        const int ox = (int)pix - oy * a.OW;
-        px[j].n = n;
-        px[j].pix = pix;
-        px[j].iy0 = oy * a.SH - a.PH;
-        px[j].ix0 = ox * a.SW - a.PW;
-        px[j].base = (const int8_t*)a.x + (int64_t)n * a.x_sn +
-                     (int64_t)g * a.Cg;
+        for (int s = 0; s < D; ++s) fetch(af[s], bf[s], pd[s], nr[s]);
     }
-    const int8_t* wrow[WM];
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-        wrow[i] = a.wp + (int64_t)g * a.wp_gstride +
-                  (int64_t)(co0 + i * 16 + col) * a.wp_rstride + kgl * 16;
-
-    v4i acc[WM][WN];
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-    int psum[WN];
-#pragma unroll
-    for (int j = 0; j < WN; ++j) psum[j] = 0;
-
-    // k-group of this lane: kg = 4*ks + kgl -> (tap, cb), tap -> (ky, kx);
-    // advanced incrementally by 4*KSTRIDE groups per step.
-    const int ks0 = KSPLIT ? wave : 0;
-    int cb = 4 * ks0 + kgl, ky = 0, kx = 0;
-    if (LAYOUT == 0) {
-        while (cb >= a.CB) {
-            cb -= a.CB;
-            if (++kx == a.KW) {
-                kx = 0;
-                ++ky;
+    {
+        const int co0 = blockIdx.y * (WM * 16);
+        if (TABLE) {
+            const int* tab = (const int*)((const char*)a.plan + PLAN_E);
+            const int n = res ? 768 : 256;
+            for (int i = threadIdx.x; i < n; i += 256) s_tab[i] = tab[i];
+            if (threadIdx.x < WM * 16) {
+                const int c = min(co0 + (int)threadIdx.x, a.Cog - 1);
+                const int64_t co = (int64_t)g * a.Cog + c;
+                s_pc[threadIdx.x] =
+                    ((const int4*)((const char*)a.plan + PLAN_CH))[co];
+                s_cb[threadIdx.x] = int2{a.corr ? (int)a.corr[co] : 0,
+                                         a.rowsum ? a.boff[co] : 0};
             }
+        } else if (lds_tab) {
+            for (int i = threadIdx.x; i < a.lut_len; i += 256)
+                s_tab[i] = a.lut[i];
         }
     }
-    const int KS = a.KGp >> 2;
-    v4i af[WM], bf[WN];
-    if (ks0 < KS) {
-        const int kg = 4 * ks0 + kgl;
-#pragma unroll
-        for (int i = 0; i < WM; ++i) af[i] = *(const v4i*)(wrow[i] + ks0 * 64);
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-            bf[j] = load_b<LAYOUT>(a, px[j], kg < a.KG, ky, kx, cb, kg,
-                                   &psum[j]);
-    }
-    for (int ks = ks0; ks < KS; ks += KSTRIDE) {
-        v4i an[WM], bn[WN];
-        const bool more = ks + KSTRIDE < KS;
-        if (more) {
-            const int kg = 4 * (ks + KSTRIDE) + kgl;
-            if (LAYOUT == 0) {
-                cb += 4 * KSTRIDE;
-                while (cb >= a.CB) {
-                    cb -= a.CB;
-                    if (++kx == a.KW) {
-                        kx = 0;
-                        ++ky;
-                    }
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-                an[i] = *(const v4i*)(wrow[i] + (ks + KSTRIDE) * 64);
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-                bn[j] = load_b<LAYOUT>(a, px[j], kg < a.KG, ky, kx, cb, kg,
-                                       &psum[j]);
-        }
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                    af[i], bf[j], acc[i][j], 0, 0, 0);
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < WM; ++i) af[i] = an[i];
-#pragma unroll
-            for (int j = 0; j < WN; ++j) bf[j] = bn[j];
-        }
-    }
+    __syncthreads();
+    if (!has_tile) return;
+    const int* lut = lds_tab ? s_tab : nullptr;
+    const int pv = splat4(a.pad_value);
 
-    if (KSPLIT) {  // sum the 4 waves' partial results into wave 0
-        if (wave > 0) {
-            int* dst = s_red + (wave - 1) * (WM * WN * 4 + WN) * 64;
+    // ---- residual words (4 channels of a pixel), one tile ahead ----
+    const bool res_wave = res && (!KSPLIT || wave == 0);
+    constexpr int RM = TABLE ? WM : 1;
+    uint32_t rwn[RM], rwc[RM];
+    PixPos rpos = p0;
+    auto load_res = [&](int co0) __attribute__((always_inline)) {
+        const bool ok = rpos.n < a.N;
+        const int64_t pbase = (int64_t)rpos.n * a.res_sn +
+                              (int64_t)(rpos.oy * a.OW + rpos.ox) * a.res_sp +
+                              (int64_t)g * a.Cog;
 #pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-                for (int j = 0; j < WN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        dst[((i * WN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-                dst[(WM * WN * 4 + j) * 64 + lane] = psum[j];
-        }
-        __syncthreads();
-        if (wave > 0) return;
-#pragma unroll
-        for (int w = 0; w < 3; ++w) {
-            const int* src = s_red + w * (WM * WN * 4 + WN) * 64;
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-                for (int j = 0; j < WN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[i][j][r] += src[((i * WN + j) * 4 + r) * 64 + lane];
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-                psum[j] += src[(WM * WN * 4 + j) * 64 + lane];
-        }
-    }
-
-    if (a.rowsum) {  // lanes col, col+16, col+32, col+48 hold partial sums
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            int s = psum[j];
-            s += __shfl_xor(s, 16);
-            s += __shfl_xor(s, 32);
-            psum[j] = s;
-        }
-    }
-    if (lds_tab && !KSPLIT) __syncthreads();  // KSPLIT synced above
-
-    // ---- epilogue ----
-    if (TABLE) {
-        const int* hd = (const int*)a.plan;
-        const int A = hd[0], B = hd[1], SH = hd[2];
-        const bool res = a.res != nullptr, two = a.y2 != nullptr;
-        const int4* pch = (const int4*)((const char*)a.plan + PLAN_CH);
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            const int cl = co0 + i * 16 + kgl * 4;  // first of 4 channels
-            const int64_t cg0 = (int64_t)g * a.Cog + cl;
-            uint32_t corr[4], bo[4];
-            int mlt[4], tsh[4];
-            int64_t cst[4];
-            bool cv[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                cv[r] = cl + r < a.Cog;
-                const int64_t co = cv[r] ? cg0 + r : cg0 - cl;
-                const int4 pc = pch[co];
-                mlt[r] = pc.x;
-                tsh[r] = pc.y;
-                cst[r] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
-                                   (uint32_t)pc.z);
-                corr[r] = a.corr ? (uint32_t)a.corr[co] : 0u;
-                bo[r] = a.rowsum ? (uint32_t)a.boff[co] : 0u;
-            }
-            const bool all4 = cv[0] && cv[1] && cv[2] && cv[3];
-#pragma unroll
-            for (int j = 0; j < WN; ++j) {
-                if (!px[j].ok) continue;
-                const uint32_t rs = (uint32_t)psum[j];
-                int e[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    // int32 accumulator (wraps like the reference's)
-                    const int w = (int)((uint32_t)acc[i][j][r] + corr[r] +
-                                        bo[r] * rs);
-                    const int q0 =
-                        (int)(((int64_t)w * mlt[r] + cst[r]) >> tsh[r]);
-                    e[r] = min(max(q0, A), B) - A;
-                }
-                if (res) {
-                    const int64_t rb = (int64_t)px[j].n * a.res_sn +
-                                       (int64_t)px[j].pix * a.res_sp + cg0;
-                    uint32_t u[4];
-                    if (all4 && a.res_sc == 1 && (rb & 3) == 0) {
-                        const uint32_t wv =
-                            *(const uint32_t*)((const int8_t*)a.res + rb);
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) u[r] = (wv >> (8 * r)) & 255u;
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            u[r] = cv[r] ? ((const uint8_t*)
-                                                a.res)[rb + r * a.res_sc]
-                                         : 0u;
-                    }
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int t = s_tab[256 + e[r]] + s_tab[512 + u[r]];
-                        e[r] = min(max(t, 0), SH);
-                    }
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) e[r] = s_tab[e[r]];
-                const int64_t ybase = (int64_t)px[j].n * a.y_sn +
-                                      (int64_t)px[j].pix * a.y_sp;
-                const int64_t yo = ybase + cg0;
-                if (all4 && a.y_sc == 1 && (yo & 3) == 0) {
-                    *(uint32_t*)((int8_t*)a.y + yo) = pack_entries(e, 0);
+        for (int i = 0; i < RM; ++i) {
+            const int cl = co0 + i * 16 + kgl * 4;
+            const int64_t rb = pbase + cl;
+            uint32_t w = 0;
+            if (ok) {
+                if (cl + 3 < a.Cog && a.res_sc == 1 && (rb & 3) == 0) {
+                    w = *(const uint32_t*)((const int8_t*)a.res + rb);
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (cv[r])
-                            ((int8_t*)a.y)[ybase + (cg0 + r) * a.y_sc] =
-                                (int8_t)e[r];
+                        if (cl + r < a.Cog)
+                            w |= (uint32_t)((const uint8_t*)
+                                                a.res)[rb + r * a.res_sc]
+                                 << (8 * r);
                 }
-                if (two) {
-                    const int64_t b2 = (int64_t)px[j].n * a.y2_sn +
-                                       (int64_t)px[j].pix * a.y2_sp;
-                    const int64_t o2 = b2 + cg0;
-                    if (all4 && a.y2_sc == 1 && (o2 & 3) == 0) {
-                        *(uint32_t*)((int8_t*)a.y2 + o2) = pack_entries(e, 1);
+            }
+            rwn[i] = w;
+        }
+    };
+    if (res_wave) {
+        load_res(blockIdx.y * (WM * 16));
+#pragma unroll
+        for (int i = 0; i < RM; ++i) rwc[i] = rwn[i];
+        pix_step(a, rpos);
+        if (tile + tstride < ntiles) load_res(blockIdx.y * (WM * 16));
+    }
+
+    PixPos cpos = p0;
+    v4i acc[WM];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) acc[i] = v4i{0, 0, 0, 0};
+    int psum = 0;
+
+    // Epilogue of the finished tile, then move to the next one.
+    auto finish_tile = [&]() __attribute__((always_inline)) {
+        // The channel base, opaque to the compiler here, so that the
+        // epilogue's per-channel offsets are recomputed per tile rather than
+        // held in registers across the loop.
+        int co0 = blockIdx.y * (WM * 16);
+        asm volatile("" : "+s"(co0));
+        bool store = true;
+        if (KSPLIT) {  // sum the 4 waves' partial results into wave 0
+            if (wave > 0) {
+                int* dst = s_red + (wave - 1) * (WM * 4 + 1) * 64;
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        dst[(i * 4 + r) * 64 + lane] = acc[i][r];
+                dst[WM * 4 * 64 + lane] = psum;
+            }
+            __syncthreads();
+            if (wave == 0) {
+#pragma unroll
+                for (int w = 0; w < 3; ++w) {
+                    const int* src = s_red + w * (WM * 4 + 1) * 64;
+#pragma unroll
+                    for (int i = 0; i < WM; ++i)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[i][r] += src[(i * 4 + r) * 64 + lane];
+                    psum += src[WM * 4 * 64 + lane];
+                }
+            }
+            __syncthreads();
+            store = wave == 0;
+        }
+        const PixPos op = cpos;
+        if (store && op.n < a.N) {
+            if (a.rowsum) {  // lanes col, col+16, col+32, col+48 hold parts
+                psum += __shfl_xor(psum, 16);
+                psum += __shfl_xor(psum, 32);
+            }
+            const int64_t pixo = op.oy * a.OW + op.ox;
+            if (TABLE) {
+                const int A = pA, B = pB, SH = pSH;
+                const bool two = a.y2 != nullptr;
+                const int64_t ybase = (int64_t)op.n * a.y_sn + pixo * a.y_sp;
+                const int64_t b2 =
+                    two ? (int64_t)op.n * a.y2_sn + pixo * a.y2_sp : 0;
+                // re-read the channel records from LDS for every tile
+                int rec = kgl * 4;
+                asm volatile("" : "+v"(rec));
+#pragma unroll
+                for (int i = 0; i < WM; ++i) {
+                    const int cl = co0 + i * 16 + kgl * 4;  // first channel
+                    const int64_t cg0 = (int64_t)g * a.Cog + cl;
+                    const bool all4 = cl + 3 < a.Cog;
+                    int e[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int4 pc = s_pc[i * 16 + rec + r];
+                        const int2 cb2 = s_cb[i * 16 + rec + r];
+                        const int64_t cst =
+                            (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                                      (uint32_t)pc.z);
+                        // int32 accumulator (wraps like the reference's)
+                        uint32_t wu = (uint32_t)acc[i][r] + (uint32_t)cb2.x;
+                        if (a.rowsum) wu += (uint32_t)cb2.y * (uint32_t)psum;
+                        const int w = (int)wu;
+                        const int q0 =
+                            (int)(((int64_t)w * pc.x + cst) >> pc.y);
+                        e[r] = min(max(q0, A), B) - A;
+                    }
+                    if (res) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int t =
+                                s_tab[256 + e[r]] +
+                                s_tab[512 + ((rwc[i] >> (8 * r)) & 255)];
+                            e[r] = min(max(t, 0), SH);
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) e[r] = s_tab[e[r]];
+                    const int64_t yo = ybase + cg0;
+                    if (all4 && a.y_sc == 1 && (yo & 3) == 0) {
+                        *(uint32_t*)((int8_t*)a.y + yo) = pack_entries(e, 0);
                     } else {
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            if (cv[r])
-                                ((int8_t*)a.y2)[b2 + (cg0 + r) * a.y2_sc] =
-                                    (int8_t)(e[r] >> 8);
+                            if (cl + r < a.Cog)
+                                ((int8_t*)a.y)[ybase + (cg0 + r) * a.y_sc] =
+                                    (int8_t)e[r];
+                    }
+                    if (two) {
+                        const int64_t o2 = b2 + cg0;
+                        if (all4 && a.y2_sc == 1 && (o2 & 3) == 0) {
+                            *(uint32_t*)((int8_t*)a.y2 + o2) =
+                                pack_entries(e, 1);
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (cl + r < a.Cog)
+                                    ((int8_t*)a.y2)[b2 + (cg0 + r) * a.y2_sc] =
+                                        (int8_t)(e[r] >> 8);
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < WM; ++i) {
+                    const int cl = co0 + i * 16 + kgl * 4;  // first channel
+                    const int64_t cg0 = (int64_t)g * a.Cog + cl;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (cl + r >= a.Cog) continue;
+                        const int64_t co = cg0 + r;
+                        const int64_t corr = a.corr ? a.corr[co] : 0;
+                        const int64_t bo = a.rowsum ? a.boff[co] : 0;
+                        const int64_t o = (int64_t)op.n * a.y_sn +
+                                          pixo * a.y_sp + co * a.y_sc;
+                        if (EPI == EPI_RAW64) {
+                            ((int64_t*)a.y)[o] =
+                                (int64_t)acc[i][r] + corr + bo * psum;
+                            continue;
+                        }
+                        const int32_t w =
+                            (int32_t)((uint32_t)acc[i][r] + (uint32_t)corr +
+                                      (uint32_t)bo * (uint32_t)psum);
+                        if (EPI == EPI_RAW32) {
+                            ((int32_t*)a.y)[o] = w;
+                            continue;
+                        }
+                        int64_t rq = 0;
+                        if (a.res)
+                            rq = (int64_t)((const int8_t*)a.res)
+                                     [(int64_t)op.n * a.res_sn +
+                                      pixo * a.res_sp + co * a.res_sc] +
+                                 a.res_so;
+                        // the reference adds the bias to the int32 sum
+                        const int64_t q = quant_general(
+                            a, lut, (int64_t)w + (a.pre ? a.pre[co] : 0),
+                            a.mult[co], a.shift[co], rq);
+                        ((int8_t*)a.y)[o] = (int8_t)(q - a.y_so);
+                        if (a.y2)
+                            ((int8_t*)a.y2)[(int64_t)op.n * a.y2_sn +
+                                            pixo * a.y2_sp + co * a.y2_sc] =
+                                (int8_t)(rescale2(a, q) - a.y_so);
                     }
                 }
             }
         }
-        return;
-    }
-    const int* lut = lds_tab ? s_tab : nullptr;
+        // next tile
+        pix_step(a, cpos);
+        tile += tstride;
+        if (res_wave) {
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
-        const int cl = co0 + i * 16 + kgl * 4;  // first of 4 channels
-        const int64_t cg0 = (int64_t)g * a.Cog + cl;
-        int64_t corr[4], pre[4], mlt[4], shf[4];
-        int bo[4];
-        bool cv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            cv[r] = cl + r < a.Cog;
-            const int64_t co = cv[r] ? cg0 + r : cg0 - cl;
-            corr[r] = a.corr ? a.corr[co] : 0;
-            bo[r] = a.rowsum ? a.boff[co] : 0;
-            pre[r] = (QUANT && a.pre) ? a.pre[co] : 0;
-            mlt[r] = QUANT ? a.mult[co] : 0;
-            shf[r] = QUANT ? a.shift[co] : 0;
+            for (int i = 0; i < RM; ++i) rwc[i] = rwn[i];
+            pix_step(a, rpos);
+            if (tile + tstride < ntiles) load_res(co0);
         }
 #pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            if (!px[j].ok) continue;
-            const int64_t rs = psum[j];
-            const int64_t ybase = (int64_t)px[j].n * a.y_sn +
-                                  (int64_t)px[j].pix * a.y_sp;
+        for (int i = 0; i < WM; ++i) acc[i] = v4i{0, 0, 0, 0};
+        psum = 0;
+    };
+
+    // ---- main loop: one ring slot per step; a tile ends at any slot ----
+    int ci = 0;  // consumer's step within the tile
+    while (true) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (!cv[r]) continue;
-                const int64_t o = ybase + (cg0 + r) * a.y_sc;
-                if (EPI == EPI_RAW64) {
-                    ((int64_t*)a.y)[o] = (int64_t)acc[i][j][r] + corr[r] +
-                                         (int64_t)bo[r] * rs;
-                    continue;
-                }
-                const int32_t w = (int32_t)((uint32_t)acc[i][j][r] +
-                                            (uint32_t)corr[r] +
-                                            (uint32_t)bo[r] * (uint32_t)rs);
-                if (EPI == EPI_RAW32) {
-                    ((int32_t*)a.y)[o] = w;
-                    continue;
-                }
-                int64_t rq = 0;
-                if (a.res)
-                    rq = (int64_t)((const int8_t*)a.res)
-                             [(int64_t)px[j].n * a.res_sn +
-                              (int64_t)px[j].pix * a.res_sp +
-                              (cg0 + r) * a.res_sc] +
-                         a.res_so;
-                // the reference adds the bias to the int32 accumulator
-                const int64_t q =
-                    quant_general(a, lut, (int64_t)w + pre[r], mlt[r], shf[r],
-                                  rq);
-                ((int8_t*)a.y)[o] = (int8_t)(q - a.y_so);
-                if (a.y2)
-                    ((int8_t*)a.y2)[(int64_t)px[j].n * a.y2_sn +
-                                    (int64_t)px[j].pix * a.y2_sp +
-                                    (cg0 + r) * a.y2_sc] =
-                        (int8_t)(rescale2(a, q) - a.y_so);
+        for (int s = 0; s < D; ++s) {
+            if (st0 + ci * KSTRIDE < KS) {
+                const v4i b = apply_pad<LAYOUT>(bf[s], pd[s], pv);
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        af[s][i], b, acc[i], 0, 0, 0);
+                if (a.rowsum)
+                    psum += LAYOUT == 0 ? bytes_sum(b, nr[s])
+                                        : bytes_sum_l1(b, nr[s], a.KW);
+            }
+            fetch(af[s], bf[s], pd[s], nr[s]);
+            if (++ci == L) {
+                ci = 0;
+                finish_tile();
+                if (tile >= ntiles) return;
             }
         }
     }
 }
 
-template <int WM, int WN, int LAYOUT, bool KSPLIT>
-bool launch_cfg(const ConvArgs& a, int epi, hipStream_t st) {
-    dim3 grid((unsigned)ceil_div(a.M, (KSPLIT ? 1 : 4) * WN * 16),
-              (unsigned)ceil_div(a.Cog, WM * 16), (unsigned)a.G);
-    switch (epi) {
-        case EPI_RAW32:
-            k_conv_mfma<WM, WN, LAYOUT, EPI_RAW32, KSPLIT>
-                <<<grid, 256, 0, st>>>(a);
-            break;
-        case EPI_RAW64:
-            k_conv_mfma<WM, WN, LAYOUT, EPI_RAW64, KSPLIT>
-                <<<grid, 256, 0, st>>>(a);
-            break;
-        case Q8_TABLE:
-            k_conv_mfma<WM, WN, LAYOUT, Q8_TABLE, KSPLIT>
-                <<<grid, 256, 0, st>>>(a);
-            break;
-        default:
-            k_conv_mfma<WM, WN, LAYOUT, Q8_GENERAL, KSPLIT>
-                <<<grid, 256, 0, st>>>(a);
-            break;
+// Compute units of the current device (cached per device).
+int cu_count() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                                  dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
     }
+    return cus[dev];
+}
+
+// Launches one instantiation with a persistent grid: as many work-groups as
+// are resident at once (occupancy of this kernel), at most one per 4 tiles.
+template <int WM, int LAYOUT, int EPI, bool KSPLIT>
+bool launch_kernel(const ConvArgs& a0, hipStream_t st) {
+    auto* kern = &k_conv_mfma<WM, LAYOUT, EPI, KSPLIT>;
+    static int resident = 0;  // work-groups per CU (same for every device)
+    if (resident == 0) {
+        int nbk = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nbk, (const void*)kern, 256, 0) != hipSuccess ||
+            nbk <= 0)
+            nbk = 1;
+        resident = nbk;
+    }
+    const int64_t cblocks = ceil_div(a0.Cog, WM * 16);
+    const int64_t ntiles = ceil_div(a0.M, 16);
+    const int64_t need = KSPLIT ? ntiles : ceil_div(ntiles, 4);
+    int64_t cap = (int64_t)resident * cu_count() / (cblocks * a0.G);
+    if (cap < 1) cap = 1;
+    const int64_t gx = need < cap ? need : cap;
+    // a wave's pixel stride (16 pixels per tile) as (n, oy, ox) offsets
+    ConvArgs a = a0;
+    const int64_t stride = 16 * gx * (KSPLIT ? 1 : 4);
+    const int64_t ohw = (int64_t)a.OH * a.OW;
+    a.st_dn = (int32_t)(stride / ohw);
+    a.st_doy = (int32_t)((stride % ohw) / a.OW);
+    a.st_dox = (int32_t)((stride % ohw) % a.OW);
+    dim3 grid((unsigned)gx, (unsigned)cblocks, (unsigned)a.G);
+    kern<<<grid, 256, 0, st>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("k_conv_mfma launch", e);
@@ -490,24 +633,40 @@ bool launch_cfg(const ConvArgs& a, int epi, hipStream_t st) {
     return true;
 }
 
-// Tile choice: the widest pixel tile that still gives >= 2 work-groups per
-// CU; when even 64-pixel tiles do not, the waves split K instead.
-template <int WM, int LAYOUT>
-bool launch_wm(const ConvArgs& a, int epi, hipStream_t st) {
-    constexpr int WN_WIDE = WM <= 4 ? 4 : 2;
-    const int64_t cblocks = ceil_div(a.Cog, WM * 16) * (int64_t)a.G;
-    if (LAYOUT == 1 || ceil_div(a.M, 4 * WN_WIDE * 16) * cblocks >= 512)
-        return launch_cfg<WM, WN_WIDE, LAYOUT, false>(a, epi, st);
-    if (ceil_div(a.M, 4 * 16) * cblocks >= 512 || a.KGp < 16)
-        return launch_cfg<WM, 1, LAYOUT, false>(a, epi, st);
-    return launch_cfg<WM, 1, LAYOUT, true>(a, epi, st);
+template <int WM, int LAYOUT, bool KSPLIT>
+bool launch_epi(const ConvArgs& a, int epi, hipStream_t st) {
+    switch (epi) {
+        case EPI_RAW32:
+            return launch_kernel<WM, LAYOUT, EPI_RAW32, KSPLIT>(a, st);
+        case EPI_RAW64:
+            return launch_kernel<WM, LAYOUT, EPI_RAW64, KSPLIT>(a, st);
+        case Q8_TABLE:
+            return launch_kernel<WM, LAYOUT, Q8_TABLE, KSPLIT>(a, st);
+        default:
+            return launch_kernel<WM, LAYOUT, Q8_GENERAL, KSPLIT>(a, st);
+    }
+}
+
+template <int LAYOUT, bool KSPLIT>
+bool launch_wm(const ConvArgs& a, int wm, int epi, hipStream_t st) {
+    switch (wm) {
+        case 1: return launch_epi<1, LAYOUT, KSPLIT>(a, epi, st);
+        case 2: return launch_epi<2, LAYOUT, KSPLIT>(a, epi, st);
+        case 4: return launch_epi<4, LAYOUT, KSPLIT>(a, epi, st);
+        default: return launch_epi<8, LAYOUT, KSPLIT>(a, epi, st);
+    }
 }
 
 }  // namespace
 
+// Tile choice: 16-pixel tiles; the widest channel block (up to 128) that
+// still gives every SIMD two waves, else narrower blocks, and for long K
+// (>= 8 steps) the 4 waves of a work-group split K when that is what it
+// takes to reach that parallelism.
 bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     if (a.M <= 0 || a.Cog <= 0 || a.G <= 0) return true;
-    if (a.M >= ((int64_t)1 << 31) || a.KGp < 4 || (a.KGp & 3)) {
+    if (a.M >= ((int64_t)1 << 31) || a.KGp < 4 || (a.KGp & 3) ||
+        a.KGp >= (1 << 16) || a.CB < 1 || a.KW < 1) {
         set_error("launch_conv_mfma", "unsupported problem size");
         return false;
     }
@@ -519,16 +678,27 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
         }
         epi = a.plan ? Q8_TABLE : Q8_GENERAL;
     }
-    if (a.layout == 1) {
-        if (a.Cog <= 16) return launch_wm<1, 1>(a, epi, st);
-        if (a.Cog <= 32) return launch_wm<2, 1>(a, epi, st);
-        if (a.Cog <= 64) return launch_wm<4, 1>(a, epi, st);
-        return launch_wm<8, 1>(a, epi, st);
+    ConvArgs b = a;
+    b.mg_cb = (((uint64_t)1 << 32) + a.CB - 1) / (uint64_t)a.CB;
+    b.mg_kw = (((uint64_t)1 << 32) + a.KW - 1) / (uint64_t)a.KW;
+    const int64_t ntiles = ceil_div(a.M, 16);
+    const int64_t want = 2 * 4 * (int64_t)cu_count();
+    auto waves = [&](int wm, bool split) {
+        return ntiles * ceil_div(a.Cog, 16 * wm) * a.G * (split ? 4 : 1);
+    };
+    const int wm_max =
+        a.Cog <= 16 ? 1 : (a.Cog <= 32 ? 2 : (a.Cog <= 64 ? 4 : 8));
+    int wm = wm_max;
+    while (wm > 1 && waves(wm, false) < want) wm >>= 1;
+    bool split = false;
+    if (a.layout == 0 && waves(wm, false) < want && (a.KGp >> 2) >= 8) {
+        split = true;
+        wm = wm_max;
+        while (wm > 1 && waves(wm, true) < want) wm >>= 1;
     }
-    if (a.Cog <= 16) return launch_wm<1, 0>(a, epi, st);
-    if (a.Cog <= 32) return launch_wm<2, 0>(a, epi, st);
-    if (a.Cog <= 64) return launch_wm<4, 0>(a, epi, st);
-    return launch_wm<8, 0>(a, epi, st);
+    if (a.layout == 1) return launch_wm<1, false>(b, wm, epi, st);
+    return split ? launch_wm<0, true>(b, wm, epi, st)
+                 : launch_wm<0, false>(b, wm, epi, st);
 }
 
 }  // namespace qa

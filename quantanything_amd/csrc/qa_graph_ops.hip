@@ -51,6 +51,49 @@ __global__ __launch_bounds__(kThreads) void k_gap_cl(
     store_s(out, out_code, n * out_sn + c, q - out_so);
 }
 
+// Channels-last int8 input with C, the strides and the base multiples of 4:
+// a thread sums 4 channels (one word per pixel) over a quarter of the
+// pixels (the 4 waves of a work-group take pixels w, w+4, ...); the
+// partial sums meet in LDS and wave 0 requantizes and stores.
+__global__ __launch_bounds__(kThreads) void k_gap_cl4(
+    const int8_t* __restrict__ x, int64_t x_sn, int64_t x_sp, int64_t C,
+    int64_t HW, int64_t zp_in, int64_t in_so, int64_t mult, int64_t shift,
+    int64_t zp_out, int64_t qmin, int64_t qmax, void* out, int out_code,
+    int64_t out_sn, int64_t out_so) {
+    __shared__ int part[3][4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t c = ((int64_t)blockIdx.x * 64 + lane) * 4;
+    const int64_t n = blockIdx.y;
+    int s[4] = {0, 0, 0, 0};
+    if (c < C) {
+        const int8_t* p = x + n * x_sn + c;
+#pragma unroll 4
+        for (int64_t q = wave; q < HW; q += 4) {
+            const uint32_t w = *(const uint32_t*)(p + q * x_sp);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] += (int)(int8_t)(w >> (8 * r));
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[wave - 1][r][lane] = s[r];
+    }
+    __syncthreads();
+    if (wave > 0 || c >= C) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        s[r] += part[0][r][lane] + part[1][r][lane] + part[2][r][lane];
+    int64_t q[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t acc = (int64_t)s[r] + HW * (in_so - zp_in);
+        q[r] = qa_clip128(qa_mbqm(acc, mult, shift) + zp_out, qmin, qmax) -
+               out_so;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) store_s(out, out_code, n * out_sn + c + r, q[r]);
+}
+
 // Planar inputs: one wave per (n, c) plane.
 __global__ __launch_bounds__(kThreads) void k_gap_planar(
     const void* __restrict__ x, int in_code, int64_t x_sn, int64_t x_sc,
@@ -74,23 +117,62 @@ __global__ __launch_bounds__(kThreads) void k_gap_planar(
     }
 }
 
+// Graph input, int8 storage with 4 bytes a pixel (C <= 4) and HW a
+// multiple of 4: a thread quantizes 4 consecutive pixels (one 16-byte load
+// per input plane, one 16-byte store), over a grid-strided range.
+__global__ __launch_bounds__(kThreads) void k_quantize_cl4x4(
+    const float* __restrict__ x, int64_t N, int64_t C, int64_t HW,
+    int8_t* __restrict__ y, double scale, double inv, int64_t zp,
+    int64_t qmin, int64_t qmax, int64_t so) {
+    const int64_t groups = N * HW / 4;
+    for (int64_t gi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+         gi < groups; gi += (int64_t)gridDim.x * kThreads) {
+        const int64_t i = gi * 4;  // first pixel
+        const int64_t n = i / HW, p = i - n * HW;
+        uint32_t w[4] = {0, 0, 0, 0};
+        for (int64_t c = 0; c < C; ++c) {
+            const float4 v = *(const float4*)(x + (n * C + c) * HW + p);
+            const float f[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                w[k] |= (uint32_t)(uint8_t)(qa_quantize_one_fast(
+                                                f[k], scale, inv, zp, qmin,
+                                                qmax) -
+                                            so)
+                        << (8 * c);
+        }
+        *(uint4*)(y + i * 4) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 // Graph input: float32 NCHW -> quantized channels-last with pixel stride
 // y_sp >= C (padding channels written as 0), one thread per pixel.
 template <class TOut>
 __global__ __launch_bounds__(kThreads) void k_quantize_cl(
     const float* __restrict__ x, int64_t N, int64_t C, int64_t HW,
-    TOut* __restrict__ y, int64_t y_sp, double scale, int64_t zp,
-    int64_t qmin, int64_t qmax, int64_t so) {
+    TOut* __restrict__ y, int64_t y_sp, double scale, double inv, int64_t zp,
+    int64_t qmin, int64_t qmax, int64_t so, int word) {
     const int64_t total = N * HW;
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * kThreads) {
         const int64_t n = i / HW, p = i - n * HW;
         TOut* dst = y + i * y_sp;
+        if (word) {  // int8, 4 bytes a pixel, aligned: one word store
+            uint32_t w = 0;
+            for (int64_t c = 0; c < C; ++c)
+                w |= (uint32_t)(uint8_t)(qa_quantize_one_fast(
+                                             x[(n * C + c) * HW + p], scale,
+                                             inv, zp, qmin, qmax) -
+                                         so)
+                     << (8 * c);
+            *(uint32_t*)dst = w;
+            continue;
+        }
         for (int64_t c = 0; c < y_sp; ++c) {
             int64_t v = 0;
             if (c < C)
-                v = qa_quantize_one(x[(n * C + c) * HW + p], scale, zp, qmin,
-                                    qmax) - so;
+                v = qa_quantize_one_fast(x[(n * C + c) * HW + p], scale, inv,
+                                         zp, qmin, qmax) - so;
             dst[c] = (TOut)v;
         }
     }
@@ -165,7 +247,17 @@ QA_API int qa_d_gap(const void* x, int in_code, int64_t x_sn, int64_t x_sc,
                     void* stream) {
     if (N * C <= 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    if (x_sc == 1) {
+    if (x_sc == 1 && in_code == 1 && C % 4 == 0 && x_sp % 4 == 0 &&
+        x_sn % 4 == 0 && (uintptr_t)x % 4 == 0 && HW < (1 << 23)) {
+        if (N > 65535) {
+            qa::set_error("qa_d_gap", "N above 65535");
+            return -1;
+        }
+        dim3 grid((unsigned)qa::ceil_div(C, 256), (unsigned)N);
+        k_gap_cl4<<<grid, kThreads, 0, st>>>(
+            (const int8_t*)x, x_sn, x_sp, C, HW, zp_in, in_so, mult, shift,
+            zp_out, qmin, qmax, out, out_code, out_sn, out_so);
+    } else if (x_sc == 1) {
         if (N > 65535) {
             qa::set_error("qa_d_gap", "N above 65535");
             return -1;
@@ -201,12 +293,21 @@ QA_API int qa_d_quantize_nhwc(const float* x, int64_t N, int64_t C,
     }
     hipStream_t st = (hipStream_t)stream;
     const unsigned g = qa::grid_1d(N * HW, kThreads, 1 << 20);
-    if (y_code == 1)
+    const double inv = 1.0 / scale;
+    const int word = y_code == 1 && y_sp == 4 && (uintptr_t)y % 4 == 0;
+    if (word && C <= 4 && HW % 4 == 0 && (uintptr_t)y % 16 == 0 &&
+        (uintptr_t)x % 16 == 0) {
+        const unsigned g4 = qa::grid_1d(N * HW / 4, kThreads, 2048);
+        k_quantize_cl4x4<<<g4, kThreads, 0, st>>>(
+            x, N, C, HW, (int8_t*)y, scale, inv, zp, qmin, qmax, so);
+    } else if (y_code == 1)
         k_quantize_cl<int8_t><<<g, kThreads, 0, st>>>(
-            x, N, C, HW, (int8_t*)y, y_sp, scale, zp, qmin, qmax, so);
+            x, N, C, HW, (int8_t*)y, y_sp, scale, inv, zp, qmin, qmax, so,
+            word);
     else if (y_code == 2)
         k_quantize_cl<int16_t><<<g, kThreads, 0, st>>>(
-            x, N, C, HW, (int16_t*)y, y_sp, scale, zp, qmin, qmax, so);
+            x, N, C, HW, (int16_t*)y, y_sp, scale, inv, zp, qmin, qmax, so,
+            0);
     else {
         qa::set_error("qa_d_quantize_nhwc", "storage must be int8 or int16");
         return -1;
