@@ -45,6 +45,12 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--profile-only", action="store_true",
                    help="skip the CPU baseline and the correctness gate")
+    p.add_argument("--eager", action="store_true",
+                   help="time eager launches instead of graph replays (for "
+                        "per-dispatch counter collection)")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                   help="finish with one device copy of MIB MiB (a plain "
+                        "copy kernel that calibrates byte counters)")
     return p.parse_args()
 
 
@@ -168,13 +174,15 @@ def main():
                              "compiled kernels, OpenMP"}
 
     # ---- timed region: captured graph replays ----------------------------
-    ex.capture()
+    step = ex.launch if args.eager else ex.replay
+    if not args.eager:
+        ex.capture()
     for _ in range(args.warmup):
-        ex.replay()
+        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        ex.replay()
+        step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = dt * 1e3 / args.steps
@@ -187,6 +195,14 @@ def main():
         shapes[name] = t.shape
     for name, fn in ex.launches:
         per.append((time_launch(fn, 20, torch), name, fn))
+    by_name = {f"conv:{l.name}": l for l in c.layers}
+    in_order = []
+    for t, n, _ in per:
+        row = [n, round(t, 5)]
+        if n in by_name:  # algorithmic ops and bytes of a fused conv launch
+            row += list(layer_work(by_name[n],
+                                   shapes[by_name[n].data_inputs[0]]))
+        in_order.append(row)
     per.sort(reverse=True, key=lambda r: r[0])
     top_ms, top_name, _ = per[0]
     top = None
@@ -239,7 +255,16 @@ def main():
         "gate": gate,
         "launches_per_step": len(ex.launches),
         "top_launches_ms": [[n, round(t, 5)] for t, n, _ in per[:6]],
+        "launches_ms": in_order,
     }
+    if args.copy_probe > 0:
+        src = torch.empty(args.copy_probe << 20, dtype=torch.uint8,
+                          device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(line))
     return 0
 
