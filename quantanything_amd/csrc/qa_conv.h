@@ -52,6 +52,9 @@ struct ConvArgs {
     int32_t CB, KG, KGp, Kreal;
     uint64_t mg_cb, mg_kw;          // ceil(2^32 / CB), ceil(2^32 / KW)
     int32_t st_dn, st_doy, st_dox;  // a wave's pixel stride as (n, oy, ox)
+    int32_t fastio;                 // y (res, y2): dense channels-last, 4-byte
+                                    // aligned 4-channel words
+    int64_t y_pst, res_pst, y2_pst; // their pixel strides when fastio
     int64_t wp_gstride, wp_rstride; // bytes
     int32_t pad_value;
     int32_t rowsum;                 // some b_off != 0

@@ -221,17 +221,66 @@ __device__ __forceinline__ uint32_t pack_entries(const int e[4], int byte) {
 }
 
 
+// One output element on the general path: the ABI results (raw int32 /
+// int64 sums in any layout) and the 128-bit requantization for parameters
+// or layouts outside the table epilogue (rare: its loops stay rolled).
+template <int EPI>
+__device__ __forceinline__ void store_general(
+    const ConvArgs& a, const int* lut, int accv, int64_t p, int64_t co,
+    int rs) {
+    const PixPos op = pix_decode(a, p);
+    const int64_t pixo = op.oy * a.OW + op.ox;
+    const int64_t corr = a.corr ? a.corr[co] : 0;
+    const int64_t bo = a.rowsum ? a.boff[co] : 0;
+    const int64_t o = (int64_t)op.n * a.y_sn + pixo * a.y_sp + co * a.y_sc;
+    if (EPI == EPI_RAW64) {
+        ((int64_t*)a.y)[o] = (int64_t)accv + corr + bo * rs;
+        return;
+    }
+    const int32_t w = (int32_t)((uint32_t)accv + (uint32_t)corr +
+                                (uint32_t)bo * (uint32_t)rs);
+    if (EPI == EPI_RAW32) {
+        ((int32_t*)a.y)[o] = w;
+        return;
+    }
+    int64_t rq = 0;
+    if (a.res)
+        rq = (int64_t)((const int8_t*)a.res)[(int64_t)op.n * a.res_sn +
+                                             pixo * a.res_sp + co * a.res_sc] +
+             a.res_so;
+    // the reference adds the bias to the int32 sum
+    const int64_t qv = quant_general(a, lut, (int64_t)w + (a.pre ? a.pre[co] : 0),
+                                     a.mult[co], a.shift[co], rq);
+    ((int8_t*)a.y)[o] = (int8_t)(qv - a.y_so);
+    if (a.y2)
+        ((int8_t*)a.y2)[(int64_t)op.n * a.y2_sn + pixo * a.y2_sp +
+                        co * a.y2_sc] = (int8_t)(rescale2(a, qv) - a.y_so);
+}
+
+// 4x4 byte transpose across the 4 lanes of a quad (q = lane & 3): lane q
+// holds bytes (x[q][0], .., x[q][3]) and ends with (x[0][q], .., x[3][q]).
+// s1/s2 are the lane's byte selectors (quad_selectors).
+__device__ __forceinline__ uint32_t quad_transpose(uint32_t w, uint32_t s1,
+                                                   uint32_t s2) {
+    // partner lane q ^ 2 (quad_perm 2,3,0,1), then q ^ 1 (1,0,3,2)
+    uint32_t p = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x4E, 0xF, 0xF,
+                                                    true);
+    const uint32_t t = __builtin_amdgcn_perm(p, w, s1);
+    p = (uint32_t)__builtin_amdgcn_mov_dpp((int)t, 0xB1, 0xF, 0xF, true);
+    return __builtin_amdgcn_perm(p, t, s2);
+}
+
 // Waves per SIMD the register allocation must allow (occupancy target).
 template <int WM>
 constexpr int waves_per_simd() {
-    return WM >= 8 ? 2 : (WM >= 2 ? 3 : 4);
+    return WM >= 8 ? 2 : 3;
 }
 
 // K-steps in flight per wave (ring of fragment registers), within the
 // register budget of the tile.
 template <int WM>
 constexpr int ring_depth() {
-    return WM <= 1 ? 4 : (WM <= 2 ? 3 : 2);
+    return WM <= 1 ? 8 : (WM <= 2 ? 4 : (WM <= 4 ? 3 : 2));
 }
 
 template <int WM, int LAYOUT, int EPI, bool KSPLIT>
@@ -244,9 +293,6 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
     constexpr int D = ring_depth<WM>();
     // Q8_GENERAL: activation table; Q8_TABLE: E, TC, TR of the plan
     __shared__ int s_tab[TABLE ? 768 : (QUANT ? 256 : 1)];
-    // Q8_TABLE: the block's channel records {m, t, c_lo, c_hi}, {corr, boff}
-    __shared__ int4 s_pc[TABLE ? WM * 16 : 1];
-    __shared__ int2 s_cb[TABLE ? WM * 16 : 1];
     __shared__ int s_red[KSPLIT ? 3 * (WM * 4 + 1) * 64 : 1];
     const int lane = threadIdx.x & 63;
     // wave index in a scalar register: the tile walk below is wave-uniform
@@ -254,6 +300,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
     const int g = blockIdx.z;
     const int kgl = lane >> 4;
     const int col = lane & 15;
+    const int co0 = blockIdx.y * (WM * 16);
     const bool res = TABLE && a.res != nullptr;
     const bool lds_tab = TABLE || (QUANT && a.lut && a.lut_len <= 256);
 
@@ -275,21 +322,18 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
     const int st0 = KSPLIT ? wave : 0;
 
     const int8_t* wrow = a.wp + (int64_t)g * a.wp_gstride +
-                         (int64_t)(blockIdx.y * (WM * 16) + col) *
-                             a.wp_rstride +
-                         kgl * 16;
+                         (int64_t)(co0 + col) * a.wp_rstride + kgl * 16;
     const int64_t wstep = 16 * a.wp_rstride;  // next 16 rows
 
     // ---- fetch side: (ftile, fi) is the next K-step to load; the stream
     // of (tile, step) runs through the D ring slots without gaps ----
-    const PixPos p0 = pix_decode(a, tile * 16 + col);
     int64_t ftile = tile;
     int fi = 0;
-    PixPos fpos = p0;
+    PixPos fpos = pix_decode(a, tile * 16 + col);
     FetchPix fp = fetch_pix(a, fpos, g);
     v4i af[D][WM], bf[D];
-    int pd[D];  // pad flags of the slot's B fragment
-    int nr[D];  // real bytes of the slot's B fragment (row sums)
+    int pd[D];  // pad flags of the slot's activation fragment
+    int nr[D];  // real bytes of the slot's activation fragment (row sums)
     auto fetch = [&](v4i* fa, v4i& fb, int& pds, int& nrs)
                      __attribute__((always_inline)) {
         const int step = st0 + fi * KSTRIDE;
@@ -310,7 +354,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
             }
         }
     };
-    // plan header (clip bounds of the requantized value, residual range)
+    // plan header: clip bounds of the requantized value, residual range
     int pA = 0, pB = 0, pSH = 0;
     if (TABLE) {
         const int4 h = *(const int4*)a.plan;
@@ -323,54 +367,65 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
 #pragma unroll
         for (int s = 0; s < D; ++s) fetch(af[s], bf[s], pd[s], nr[s]);
     }
-    {
-        const int co0 = blockIdx.y * (WM * 16);
-        if (TABLE) {
-            const int* tab = (const int*)((const char*)a.plan + PLAN_E);
-            const int n = res ? 768 : 256;
-            for (int i = threadIdx.x; i < n; i += 256) s_tab[i] = tab[i];
-            if (threadIdx.x < WM * 16) {
-                const int c = min(co0 + (int)threadIdx.x, a.Cog - 1);
-                const int64_t co = (int64_t)g * a.Cog + c;
-                s_pc[threadIdx.x] =
-                    ((const int4*)((const char*)a.plan + PLAN_CH))[co];
-                s_cb[threadIdx.x] = int2{a.corr ? (int)a.corr[co] : 0,
-                                         a.rowsum ? a.boff[co] : 0};
-            }
-        } else if (lds_tab) {
-            for (int i = threadIdx.x; i < a.lut_len; i += 256)
-                s_tab[i] = a.lut[i];
-        }
+    if (TABLE) {
+        const int* tab = (const int*)((const char*)a.plan + PLAN_E);
+        const int n = res ? 768 : 256;
+        for (int i = threadIdx.x; i < n; i += 256) s_tab[i] = tab[i];
+    } else if (lds_tab) {
+        for (int i = threadIdx.x; i < a.lut_len; i += 256) s_tab[i] = a.lut[i];
     }
     __syncthreads();
     if (!has_tile) return;
-    const int* lut = lds_tab ? s_tab : nullptr;
+    // the activation table in LDS (Q8_TABLE's LDS holds the plan's tables)
+    const int* lut = (lds_tab && !TABLE) ? s_tab : nullptr;
     const int pv = splat4(a.pad_value);
 
-    // ---- residual words (4 channels of a pixel), one tile ahead ----
+    // ---- this lane's output channel (co0 + i*16 + col) and its constants
+    int cm[TABLE ? WM : 1], ct[TABLE ? WM : 1];
+    int64_t cc[TABLE ? WM : 1];
+    uint32_t ccorr[TABLE ? WM : 1], cbo[TABLE ? WM : 1];
+    if (TABLE) {
+        const int4* pch = (const int4*)((const char*)a.plan + PLAN_CH);
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int c = min(co0 + i * 16 + col, a.Cog - 1);
+            const int64_t co = (int64_t)g * a.Cog + c;
+            const int4 pc = pch[co];
+            cm[i] = pc.x;
+            ct[i] = pc.y;
+            cc[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                              (uint32_t)pc.z);
+            ccorr[i] = a.corr ? (uint32_t)a.corr[co] : 0u;
+            cbo[i] = a.rowsum ? (uint32_t)a.boff[co] : 0u;
+        }
+    }
+    const int q = lane & 3;  // lane within its quad
+    const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
+    const uint32_t sel2 = (q & 1) ? 0x03070105u : 0x06020400u;
+    // channel-quad of this lane: channels co0 + i*16 + (col & ~3) .. +3
+    const int cq = col & ~3;
+
+    // ---- residual words, one tile ahead (fast layout): lane q loads the 4
+    // channels of pixel 4*kgl + q of its channel quad, transposed on use
     const bool res_wave = res && (!KSPLIT || wave == 0);
     constexpr int RM = TABLE ? WM : 1;
     uint32_t rwn[RM], rwc[RM];
-    PixPos rpos = p0;
-    auto load_res = [&](int co0) __attribute__((always_inline)) {
-        const bool ok = rpos.n < a.N;
-        const int64_t pbase = (int64_t)rpos.n * a.res_sn +
-                              (int64_t)(rpos.oy * a.OW + rpos.ox) * a.res_sp +
-                              (int64_t)g * a.Cog;
+    auto load_res = [&](int64_t t) __attribute__((always_inline)) {
+        const int64_t p = t * 16 + 4 * kgl + q;
+        const bool ok = p < a.M;
 #pragma unroll
         for (int i = 0; i < RM; ++i) {
-            const int cl = co0 + i * 16 + kgl * 4;
-            const int64_t rb = pbase + cl;
+            const int c0 = co0 + i * 16 + cq;
             uint32_t w = 0;
-            if (ok) {
-                if (cl + 3 < a.Cog && a.res_sc == 1 && (rb & 3) == 0) {
+            if (ok && a.fastio) {
+                const int64_t rb = p * a.res_pst + (int64_t)g * a.Cog + c0;
+                if (c0 + 3 < a.Cog) {
                     w = *(const uint32_t*)((const int8_t*)a.res + rb);
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (cl + r < a.Cog)
-                            w |= (uint32_t)((const uint8_t*)
-                                                a.res)[rb + r * a.res_sc]
+                        if (c0 + r < a.Cog)
+                            w |= (uint32_t)((const uint8_t*)a.res)[rb + r]
                                  << (8 * r);
                 }
             }
@@ -378,26 +433,21 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
         }
     };
     if (res_wave) {
-        load_res(blockIdx.y * (WM * 16));
+        load_res(tile);
 #pragma unroll
         for (int i = 0; i < RM; ++i) rwc[i] = rwn[i];
-        pix_step(a, rpos);
-        if (tile + tstride < ntiles) load_res(blockIdx.y * (WM * 16));
+        if (tile + tstride < ntiles) load_res(tile + tstride);
     }
 
-    PixPos cpos = p0;
     v4i acc[WM];
 #pragma unroll
     for (int i = 0; i < WM; ++i) acc[i] = v4i{0, 0, 0, 0};
     int psum = 0;
 
-    // Epilogue of the finished tile, then move to the next one.
+    // Epilogue of the finished tile, then move to the next one. The lane
+    // holds, per channel group i, output channel co0 + i*16 + col for the
+    // 4 pixels 4*kgl + r of the tile.
     auto finish_tile = [&]() __attribute__((always_inline)) {
-        // The channel base, opaque to the compiler here, so that the
-        // epilogue's per-channel offsets are recomputed per tile rather than
-        // held in registers across the loop.
-        int co0 = blockIdx.y * (WM * 16);
-        asm volatile("" : "+s"(co0));
         bool store = true;
         if (KSPLIT) {  // sum the 4 waves' partial results into wave 0
             if (wave > 0) {
@@ -425,130 +475,95 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
             __syncthreads();
             store = wave == 0;
         }
-        const PixPos op = cpos;
-        if (store && op.n < a.N) {
-            if (a.rowsum) {  // lanes col, col+16, col+32, col+48 hold parts
+        if (store) {
+            // row sums of the lane's 4 pixels (held by lanes 4*kgl + r)
+            int ps[4] = {0, 0, 0, 0};
+            if (a.rowsum) {
                 psum += __shfl_xor(psum, 16);
                 psum += __shfl_xor(psum, 32);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ps[r] = __shfl(psum, 4 * kgl + r);
             }
-            const int64_t pixo = op.oy * a.OW + op.ox;
-            if (TABLE) {
-                const int A = pA, B = pB, SH = pSH;
-                const bool two = a.y2 != nullptr;
-                const int64_t ybase = (int64_t)op.n * a.y_sn + pixo * a.y_sp;
-                const int64_t b2 =
-                    two ? (int64_t)op.n * a.y2_sn + pixo * a.y2_sp : 0;
-                // re-read the channel records from LDS for every tile
-                int rec = kgl * 4;
-                asm volatile("" : "+v"(rec));
+            const int64_t p0 = tile * 16 + 4 * kgl;  // first of the 4 pixels
+            if (TABLE) {  // launched only with the fast output layout
+                const int64_t pq = p0 + q;  // pixel this lane stores
+                const bool pok = pq < a.M;
 #pragma unroll
                 for (int i = 0; i < WM; ++i) {
-                    const int cl = co0 + i * 16 + kgl * 4;  // first channel
-                    const int64_t cg0 = (int64_t)g * a.Cog + cl;
-                    const bool all4 = cl + 3 < a.Cog;
                     int e[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int4 pc = s_pc[i * 16 + rec + r];
-                        const int2 cb2 = s_cb[i * 16 + rec + r];
-                        const int64_t cst =
-                            (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
-                                      (uint32_t)pc.z);
                         // int32 accumulator (wraps like the reference's)
-                        uint32_t wu = (uint32_t)acc[i][r] + (uint32_t)cb2.x;
-                        if (a.rowsum) wu += (uint32_t)cb2.y * (uint32_t)psum;
-                        const int w = (int)wu;
-                        const int q0 =
-                            (int)(((int64_t)w * pc.x + cst) >> pc.y);
-                        e[r] = min(max(q0, A), B) - A;
+                        uint32_t wu = (uint32_t)acc[i][r] + ccorr[i];
+                        if (a.rowsum) wu += cbo[i] * (uint32_t)ps[r];
+                        const int q0 = (int)(((int64_t)(int)wu * cm[i] +
+                                              cc[i]) >> ct[i]);
+                        e[r] = min(max(q0, pA), pB) - pA;
                     }
                     if (res) {
+                        const uint32_t rv =
+                            quad_transpose(rwc[i], sel1, sel2);
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int t =
-                                s_tab[256 + e[r]] +
-                                s_tab[512 + ((rwc[i] >> (8 * r)) & 255)];
-                            e[r] = min(max(t, 0), SH);
+                            const int t = s_tab[256 + e[r]] +
+                                          s_tab[512 + ((rv >> (8 * r)) & 255)];
+                            e[r] = min(max(t, 0), pSH);
                         }
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) e[r] = s_tab[e[r]];
-                    const int64_t yo = ybase + cg0;
-                    if (all4 && a.y_sc == 1 && (yo & 3) == 0) {
-                        *(uint32_t*)((int8_t*)a.y + yo) = pack_entries(e, 0);
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            if (cl + r < a.Cog)
-                                ((int8_t*)a.y)[ybase + (cg0 + r) * a.y_sc] =
-                                    (int8_t)e[r];
-                    }
-                    if (two) {
-                        const int64_t o2 = b2 + cg0;
-                        if (all4 && a.y2_sc == 1 && (o2 & 3) == 0) {
-                            *(uint32_t*)((int8_t*)a.y2 + o2) =
-                                pack_entries(e, 1);
+                    const int c0 = co0 + i * 16 + cq;
+                    const int64_t cofs = (int64_t)g * a.Cog + c0;
+                    const uint32_t wy =
+                        quad_transpose(pack_entries(e, 0), sel1, sel2);
+                    if (pok) {
+                        int8_t* py = (int8_t*)a.y + pq * a.y_pst + cofs;
+                        if (c0 + 3 < a.Cog) {
+                            *(uint32_t*)py = wy;
                         } else {
 #pragma unroll
                             for (int r = 0; r < 4; ++r)
-                                if (cl + r < a.Cog)
-                                    ((int8_t*)a.y2)[b2 + (cg0 + r) * a.y2_sc] =
-                                        (int8_t)(e[r] >> 8);
+                                if (c0 + r < a.Cog) py[r] = (int8_t)(wy >> (8 * r));
+                        }
+                    }
+                    if (a.y2) {
+                        const uint32_t w2 =
+                            quad_transpose(pack_entries(e, 1), sel1, sel2);
+                        if (pok) {
+                            int8_t* p2 = (int8_t*)a.y2 + pq * a.y2_pst + cofs;
+                            if (c0 + 3 < a.Cog) {
+                                *(uint32_t*)p2 = w2;
+                            } else {
+#pragma unroll
+                                for (int r = 0; r < 4; ++r)
+                                    if (c0 + r < a.Cog)
+                                        p2[r] = (int8_t)(w2 >> (8 * r));
+                            }
                         }
                     }
                 }
             } else {
-#pragma unroll
-                for (int i = 0; i < WM; ++i) {
-                    const int cl = co0 + i * 16 + kgl * 4;  // first channel
-                    const int64_t cg0 = (int64_t)g * a.Cog + cl;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (cl + r >= a.Cog) continue;
-                        const int64_t co = cg0 + r;
-                        const int64_t corr = a.corr ? a.corr[co] : 0;
-                        const int64_t bo = a.rowsum ? a.boff[co] : 0;
-                        const int64_t o = (int64_t)op.n * a.y_sn +
-                                          pixo * a.y_sp + co * a.y_sc;
-                        if (EPI == EPI_RAW64) {
-                            ((int64_t*)a.y)[o] =
-                                (int64_t)acc[i][r] + corr + bo * psum;
-                            continue;
-                        }
-                        const int32_t w =
-                            (int32_t)((uint32_t)acc[i][r] + (uint32_t)corr +
-                                      (uint32_t)bo * (uint32_t)psum);
-                        if (EPI == EPI_RAW32) {
-                            ((int32_t*)a.y)[o] = w;
-                            continue;
-                        }
-                        int64_t rq = 0;
-                        if (a.res)
-                            rq = (int64_t)((const int8_t*)a.res)
-                                     [(int64_t)op.n * a.res_sn +
-                                      pixo * a.res_sp + co * a.res_sc] +
-                                 a.res_so;
-                        // the reference adds the bias to the int32 sum
-                        const int64_t q = quant_general(
-                            a, lut, (int64_t)w + (a.pre ? a.pre[co] : 0),
-                            a.mult[co], a.shift[co], rq);
-                        ((int8_t*)a.y)[o] = (int8_t)(q - a.y_so);
-                        if (a.y2)
-                            ((int8_t*)a.y2)[(int64_t)op.n * a.y2_sn +
-                                            pixo * a.y2_sp + co * a.y2_sc] =
-                                (int8_t)(rescale2(a, q) - a.y_so);
+                // general layouts: one element at a time
+#pragma unroll 1
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t p = p0 + r;
+                    if (p >= a.M) continue;
+#pragma unroll 1
+                    for (int i = 0; i < WM; ++i) {
+                        const int c = co0 + i * 16 + col;
+                        if (c < a.Cog)
+                            store_general<EPI>(a, lut, acc[i][r], p,
+                                               (int64_t)g * a.Cog + c, ps[r]);
                     }
                 }
             }
         }
         // next tile
-        pix_step(a, cpos);
         tile += tstride;
         if (res_wave) {
 #pragma unroll
             for (int i = 0; i < RM; ++i) rwc[i] = rwn[i];
-            pix_step(a, rpos);
-            if (tile + tstride < ntiles) load_res(co0);
+            if (tile + tstride < ntiles) load_res(tile + tstride);
         }
 #pragma unroll
         for (int i = 0; i < WM; ++i) acc[i] = v4i{0, 0, 0, 0};
@@ -562,10 +577,11 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
         for (int s = 0; s < D; ++s) {
             if (st0 + ci * KSTRIDE < KS) {
                 const v4i b = apply_pad<LAYOUT>(bf[s], pd[s], pv);
+                // rows = the 16 pixels, columns = 16 output channels
 #pragma unroll
                 for (int i = 0; i < WM; ++i)
                     acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        af[s][i], b, acc[i], 0, 0, 0);
+                        b, af[s][i], acc[i], 0, 0, 0);
                 if (a.rowsum)
                     psum += LAYOUT == 0 ? bytes_sum(b, nr[s])
                                         : bytes_sum_l1(b, nr[s], a.KW);
@@ -676,9 +692,29 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
             set_error("launch_conv_mfma", "int8 output expected");
             return false;
         }
-        epi = a.plan ? Q8_TABLE : Q8_GENERAL;
+        epi = Q8_GENERAL;  // chosen below, once the layout is known
     }
     ConvArgs b = a;
+    // dense channels-last int8 output (and residual / copy): 4-channel
+    // words of a pixel at pixel * sp + channel, 4-byte aligned
+    {
+        const int64_t ohw = (int64_t)a.OH * a.OW;
+        // pixel stride: sp, or the row stride sn of a GEMM (one pixel a row)
+        auto pst = [&](int64_t sn, int64_t sp) { return ohw == 1 ? sn : sp; };
+        auto dense = [&](const void* p, int64_t sn, int64_t sc, int64_t sp) {
+            return p == nullptr ||
+                   (sc == 1 && (ohw == 1 || sn == ohw * sp) &&
+                    pst(sn, sp) % 4 == 0 && (uintptr_t)p % 4 == 0);
+        };
+        b.fastio = a.mode == EPI_QUANT && (a.G == 1 || a.Cog % 4 == 0) &&
+                   dense(a.y, a.y_sn, a.y_sc, a.y_sp) &&
+                   dense(a.res, a.res_sn, a.res_sc, a.res_sp) &&
+                   dense(a.y2, a.y2_sn, a.y2_sc, a.y2_sp);
+        b.y_pst = pst(a.y_sn, a.y_sp);
+        b.res_pst = pst(a.res_sn, a.res_sp);
+        b.y2_pst = pst(a.y2_sn, a.y2_sp);
+    }
+    if (a.mode == EPI_QUANT && a.plan && b.fastio) epi = Q8_TABLE;
     b.mg_cb = (((uint64_t)1 << 32) + a.CB - 1) / (uint64_t)a.CB;
     b.mg_kw = (((uint64_t)1 << 32) + a.KW - 1) / (uint64_t)a.KW;
     const int64_t ntiles = ceil_div(a.M, 16);
