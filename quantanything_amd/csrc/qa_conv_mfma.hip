@@ -21,6 +21,9 @@
 //             for clip, activation table, residual Add and rescaled copy;
 //             4 consecutive channels of a pixel are stored as one word,
 //   Q8_GENERAL the 128-bit form for any parameters.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "qa_conv.h"
 
 namespace qa {
@@ -362,29 +365,11 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
         pB = h.y;
         pSH = h.z;
     }
-    // first loads of the ring, then the tables: their latencies overlap
-    if (has_tile) {
-#pragma unroll
-        for (int s = 0; s < D; ++s) fetch(af[s], bf[s], pd[s], nr[s]);
-    }
-    if (TABLE) {
-        const int* tab = (const int*)((const char*)a.plan + PLAN_E);
-        const int n = res ? 768 : 256;
-        for (int i = threadIdx.x; i < n; i += 256) s_tab[i] = tab[i];
-    } else if (lds_tab) {
-        for (int i = threadIdx.x; i < a.lut_len; i += 256) s_tab[i] = a.lut[i];
-    }
-    __syncthreads();
-    if (!has_tile) return;
-    // the activation table in LDS (Q8_TABLE's LDS holds the plan's tables)
-    const int* lut = (lds_tab && !TABLE) ? s_tab : nullptr;
-    const int pv = splat4(a.pad_value);
-
     // ---- this lane's output channel (co0 + i*16 + col) and its constants
     int cm[TABLE ? WM : 1], ct[TABLE ? WM : 1];
     int64_t cc[TABLE ? WM : 1];
     uint32_t ccorr[TABLE ? WM : 1], cbo[TABLE ? WM : 1];
-    if (TABLE) {
+    if (TABLE && has_tile) {
         const int4* pch = (const int4*)((const char*)a.plan + PLAN_CH);
 #pragma unroll
         for (int i = 0; i < WM; ++i) {
@@ -432,12 +417,30 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
             rwn[i] = w;
         }
     };
-    if (res_wave) {
+    if (res_wave && has_tile) {
         load_res(tile);
 #pragma unroll
         for (int i = 0; i < RM; ++i) rwc[i] = rwn[i];
         if (tile + tstride < ntiles) load_res(tile + tstride);
     }
+
+    // first loads of the ring, then the tables: their latencies overlap
+    if (has_tile) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) fetch(af[s], bf[s], pd[s], nr[s]);
+    }
+    if (TABLE) {
+        const int* tab = (const int*)((const char*)a.plan + PLAN_E);
+        const int n = res ? 768 : 256;
+        for (int i = threadIdx.x; i < n; i += 256) s_tab[i] = tab[i];
+    } else if (lds_tab) {
+        for (int i = threadIdx.x; i < a.lut_len; i += 256) s_tab[i] = a.lut[i];
+    }
+    __syncthreads();
+    if (!has_tile) return;
+    // the activation table in LDS (Q8_TABLE's LDS holds the plan's tables)
+    const int* lut = (lds_tab && !TABLE) ? s_tab : nullptr;
+    const int pv = splat4(a.pad_value);
 
     v4i acc[WM];
 #pragma unroll
@@ -675,10 +678,11 @@ bool launch_wm(const ConvArgs& a, int wm, int epi, hipStream_t st) {
 
 }  // namespace
 
-// Tile choice: 16-pixel tiles; the widest channel block (up to 128) that
-// still gives every SIMD two waves, else narrower blocks, and for long K
-// (>= 8 steps) the 4 waves of a work-group split K when that is what it
-// takes to reach that parallelism.
+// Tile choice (from measured sweeps over the channel-block width WM and
+// K-splitting on MI355X): the widest channel block that still gives about
+// 1.5 waves per SIMD (0.75 when K is long, >= 9 steps: those waves are long
+// enough on their own), and the 4 waves of a work-group split K only when
+// even 16-channel blocks leave most SIMDs idle.
 bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     if (a.M <= 0 || a.Cog <= 0 || a.G <= 0) return true;
     if (a.M >= ((int64_t)1 << 31) || a.KGp < 4 || (a.KGp & 3) ||
@@ -718,20 +722,28 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     b.mg_cb = (((uint64_t)1 << 32) + a.CB - 1) / (uint64_t)a.CB;
     b.mg_kw = (((uint64_t)1 << 32) + a.KW - 1) / (uint64_t)a.KW;
     const int64_t ntiles = ceil_div(a.M, 16);
-    const int64_t want = 2 * 4 * (int64_t)cu_count();
+    const int64_t simds = 4 * (int64_t)cu_count();
     auto waves = [&](int wm, bool split) {
         return ntiles * ceil_div(a.Cog, 16 * wm) * a.G * (split ? 4 : 1);
     };
+    const int KS = a.KGp >> 2;
     const int wm_max =
         a.Cog <= 16 ? 1 : (a.Cog <= 32 ? 2 : (a.Cog <= 64 ? 4 : 8));
+    const int64_t want = KS >= 9 ? simds * 3 / 4 : simds * 3 / 2;
     int wm = wm_max;
     while (wm > 1 && waves(wm, false) < want) wm >>= 1;
-    bool split = false;
-    if (a.layout == 0 && waves(wm, false) < want && (a.KGp >> 2) >= 8) {
-        split = true;
-        wm = wm_max;
-        while (wm > 1 && waves(wm, true) < want) wm >>= 1;
+    bool split = a.layout == 0 && KS >= 4 && waves(wm, false) < simds / 2;
+#ifdef QA_CONV_TUNING
+    // tuning builds only: QA_CONV_FORCE="wm,split" overrides the choice
+    if (const char* f = getenv("QA_CONV_FORCE")) {
+        int fw = 0, fs = 0;
+        if (sscanf(f, "%d,%d", &fw, &fs) == 2 && fw >= 1 && fw <= wm_max &&
+            (fw & (fw - 1)) == 0) {
+            wm = fw;
+            split = fs && a.layout == 0;
+        }
     }
+#endif
     if (a.layout == 1) return launch_wm<1, false>(b, wm, epi, st);
     return split ? launch_wm<0, true>(b, wm, epi, st)
                  : launch_wm<0, false>(b, wm, epi, st);
