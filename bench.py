@@ -48,6 +48,9 @@ def parse():
     p.add_argument("--eager", action="store_true",
                    help="time eager launches instead of graph replays (for "
                         "per-dispatch counter collection)")
+    p.add_argument("--no-tune", action="store_true",
+                   help="keep the library's own conv tiling (no plan-time "
+                        "timing of the tile variants)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="finish with one device copy of MIB MiB (a plain "
                         "copy kernel that calibrates byte counters)")
@@ -125,6 +128,11 @@ def main():
     ex.inputs_f32["images"].copy_(torch.from_numpy(x))
     ex.launch()
     torch.cuda.synchronize()
+    tiles = {}
+    if not args.no_tune:  # plan time: per-layer tile variants, fastest kept
+        tiles = ex.tune()
+        ex.launch()
+        torch.cuda.synchronize()
 
     # ---- correctness gate + CPU baseline (reference kernels on the host) --
     cpu = None
@@ -256,6 +264,8 @@ def main():
         "launches_per_step": len(ex.launches),
         "top_launches_ms": [[n, round(t, 5)] for t, n, _ in per[:6]],
         "launches_ms": in_order,
+        "tiles": {n: [hex(code), round(best, 5), round(lib, 5)]
+                  for n, (code, best, lib) in tiles.items()},
     }
     if args.copy_probe > 0:
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8,

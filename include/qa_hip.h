@@ -167,6 +167,12 @@ typedef struct qa_conv_desc {
     void* y2;
     int64_t y2_sn, y2_sc, y2_sp, r2_zp_in, r2_m, r2_s, r2_zp_out, r2_qmin,
         r2_qmax;
+    int64_t tile;  /* 0: the library picks the MFMA tiling; otherwise
+                      0x10000 | wm | split << 8 | lds << 9 with wm = 16-channel
+                      groups per tile (1, 2, 4, 8), split = the 4 waves of a
+                      work-group split K, lds = weights staged in LDS (a
+                      caller's measured choice; ignored where it does not
+                      apply). Results do not depend on it. */
 } qa_conv_desc;
 
 /* Host-side planner of the int8 table epilogue of qa_d_conv. From the

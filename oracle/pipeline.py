@@ -320,9 +320,10 @@ class OraclePipeline:
         outs = eval_node(node, full, self.g.opset)
         return [L.quantize_f32(y, *q) for y, q in zip(outs, st["out_qp"])]
 
-    def run(self, x):
+    def run(self, x, keep=False):
         """Returns ``{output name: int32 quantized array}`` and the
-        dequantized float32 outputs in graph-output order."""
+        dequantized float32 outputs in graph-output order; ``keep`` leaves
+        every tensor of the pass in ``self.env``."""
         feeds = x if isinstance(x, dict) else {self.g.input_names[0]: x}
         env = {}
         for name, v in feeds.items():
@@ -332,6 +333,8 @@ class OraclePipeline:
         for st in self.plan:
             args = [env[n] if n in env else self._const(n) for n in st["ins"]]
             env.update(zip(st["node"].outputs, self._run_step(st, args)))
+        if keep:
+            self.env = env
         ints = {o: env[o] for o in self.g.outputs}
         floats = [self.lib.dequantize_f32(env[o], *self.qp[o][:2])
                   for o in self.g.outputs]

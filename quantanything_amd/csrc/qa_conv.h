@@ -29,6 +29,8 @@
 
 namespace qa {
 
+constexpr int32_t TILE_VALID = 1 << 16;
+
 enum EpiMode {
     EPI_RAW32 = 0,  // int32 accumulator (wraps modulo 2^32): ABI narrow path
     EPI_RAW64 = 1,  // exact int64 accumulator: ABI wide path
@@ -55,6 +57,8 @@ struct ConvArgs {
     int32_t fastio;                 // y (res, y2): dense channels-last, 4-byte
                                     // aligned 4-channel words
     int64_t y_pst, res_pst, y2_pst; // their pixel strides when fastio
+    int32_t tile_hint;              // 0, or TILE_VALID | wm | split << 8 |
+                                    // lds << 9 (MFMA tile choice)
     int64_t wp_gstride, wp_rstride; // bytes
     int32_t pad_value;
     int32_t rowsum;                 // some b_off != 0
@@ -154,6 +158,12 @@ __device__ __forceinline__ void store_any(void* p, int code, int64_t i,
 
 // Launchers; false on launch failure (recorded with set_error).
 bool launch_conv_mfma(const ConvArgs& a, hipStream_t st);
+// The int8 MFMA variants with weights staged in LDS / read from L2 (wm: 16
+// channel groups per tile, 1/2/4/8; split: the 4 waves split K).
+bool mfma_launch_lds(const ConvArgs& b, int wm, bool split, int epi,
+                     hipStream_t st);
+bool mfma_launch_l2(const ConvArgs& b, int wm, bool split, int epi,
+                    hipStream_t st);
 bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
 
 }  // namespace qa

@@ -618,6 +618,7 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
         a.pad_value = (int32_t)(-d->x_add);
         a.rowsum = (int32_t)d->needs_rowsum;
         a.plan = d->epi_plan;
+        a.tile_hint = (int32_t)d->tile;
         return launch_conv_mfma(a, st) ? 0 : -1;
     }
     a.w = d->w;

@@ -62,7 +62,8 @@ class ConvDesc(ctypes.Structure):
         + [("y2", _P)] + [(n, _I64) for n in ("y2_sn", "y2_sc", "y2_sp",
                                              "r2_zp_in", "r2_m", "r2_s",
                                              "r2_zp_out", "r2_qmin",
-                                             "r2_qmax")])
+                                             "r2_qmax")]
+        + [("tile", _I64)])
 
 
 def storage_of(bits, signed):
@@ -203,7 +204,7 @@ class DeviceExecutor:
         self.keep = []  # host objects that launches point into
         self.tensors = {}
         self.epi = {}  # tensor -> (desc, first channel) written by an epilogue
-        self.mfma_descs = []  # (desc, host params, host table) to plan
+        self.mfma_descs = []  # (desc, host params, host table, launch name)
         self.inputs_f32 = {}
         self.outputs_f32 = {}
         self.cuda_graph = None
@@ -468,7 +469,8 @@ class DeviceExecutor:
         if d.w_code == 1 and d.y_code == 1:
             self.mfma_descs.append(
                 (d, info["host"],
-                 None if lut_layer is None else lut_layer.lut))
+                 None if lut_layer is None else lut_layer.lut,
+                 f"conv:{layer.name}"))
         name = add_layer or lut_layer or layer
         self.epi[name.node.outputs[0]] = (d, 0, cout)
         self._add(f"conv:{layer.name}", lambda s, d=d:
@@ -478,7 +480,7 @@ class DeviceExecutor:
     def _plan_epilogues(self):
         """Table-epilogue plans of the int8 MFMA convolutions, built once the
         descriptors are final (a later Concat may add the rescaled copy)."""
-        for d, (mult, shift, pre), lut in self.mfma_descs:
+        for d, (mult, shift, pre), lut, _ in self.mfma_descs:
             plan = plan_epilogue(self.lib, d, mult, shift, pre, lut)
             if plan is not None:
                 dev = _dev(plan, np.uint8)
@@ -672,6 +674,65 @@ class DeviceExecutor:
                 "qa_d_softmax"))
             return [y]
         raise NotImplementedError(f"float fallback of {op} on the device")
+
+    # ------------------------------------------------------------ tiling --
+    @staticmethod
+    def tile_candidates(d):
+        """``qa_conv_desc.tile`` codes worth timing for one int8 MFMA
+        convolution: 0 (the library's own choice), then every channel-block
+        width up to the output channels per group, K-split (channel-blocked
+        weight layout only) and weights in LDS (where 16 rows per channel
+        group of K bytes fit in the 3 KiB-chunk staging budget; the library
+        re-checks the LDS size)."""
+        cog = d.Cout // d.G
+        wm_max = 1 if cog <= 16 else 2 if cog <= 32 else 4 if cog <= 64 else 8
+        out = [0]
+        for wm in (1, 2, 4, 8):
+            if wm > wm_max:
+                break
+            for split in ((0, 1) if d.w_layout == 0 else (0,)):
+                for lds in ((0, 1) if wm * d.w_kgp <= 192 else (0,)):
+                    out.append(0x10000 | wm | split << 8 | lds << 9)
+        return out
+
+    def tune(self, launches=8, reps=3):
+        """Times every tile code of every int8 MFMA convolution in place
+        (captured graphs of ``launches`` back-to-back launches, HIP events
+        over ``reps`` replays) and keeps the fastest per layer. Inputs must
+        hold a pass's data (call once after ``launch``); results do not
+        depend on the tiles. Returns ``{launch name: (code, best ms,
+        library-choice ms)}``."""
+        if self.cuda_graph is not None:
+            raise RuntimeError("tune() before the pass is captured")
+        report = {}
+        torch.cuda.synchronize()
+        for d, _, _, name in self.mfma_descs:
+            times = {}
+            for code in self.tile_candidates(d):
+                d.tile = code
+                times[code] = self._time_conv(d, launches, reps)
+            best = min(times, key=times.get)
+            d.tile = best
+            report[name] = (best, times[best], times[0])
+        return report
+
+    def _time_conv(self, d, launches, reps):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            s = torch.cuda.current_stream().cuda_stream
+            for _ in range(launches):
+                _ok(self.lib.qa_d_conv(ctypes.byref(d), s), "qa_d_conv")
+        g.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / (reps * launches)
+        del g
+        return ms
 
     # ------------------------------------------------------------ running --
     def launch(self, stream=None):

@@ -68,6 +68,58 @@ def test_yolov8n_cls_int8_bit_exact(hip, tmp_path):
     np.testing.assert_array_equal(got, ints[g.outputs[0]])
 
 
+@pytest.mark.parametrize("model,quant_type", [("yolov8n_cls", "int8"),
+                                              ("mini_yolo", "uint8")])
+def test_every_conv_tile_is_bit_exact(hip, tmp_path, model, quant_type):
+    """Every int8 MFMA conv forced through each tile code it accepts
+    (channel-block width, K-split, weights in LDS): every tensor the device
+    pass keeps equals the oracle's."""
+    if model == "yolov8n_cls":
+        g = G.yolov8n_cls(seed=3, softmax=False)
+        x = Stream(51).normal((2, 3, 224, 224)).astype(np.float32)
+        calib = [Stream(40).normal((2, 3, 224, 224)).astype(np.float32)]
+    else:
+        g = G.mini_yolo(seed=0, softmax=False)
+        calib = [_images(1 + i, 4, 32) for i in range(3)]
+        x = _images(9, 3, 32)
+    c = _calibrated(g, quant_type, True, calib)
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    oracle.run(x, keep=True)
+    ex = c.executor({"images": x.shape})
+    descs = [m[0] for m in ex.mfma_descs]
+    assert descs, "no MFMA convolutions planned"
+    cands = [ex.tile_candidates(d) for d in descs]
+    for r in range(max(len(cc) for cc in cands)):
+        for d, cc in zip(descs, cands):
+            d.tile = cc[r % len(cc)]
+        ex.run({"images": x})
+        checked = 0
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, tiles {[hex(d.tile) for d in descs]}")
+                checked += 1
+        assert checked > len(descs) // 2
+
+
+def test_tuned_tiles_keep_results(hip):
+    g = G.mini_yolo(seed=0)
+    calib = [_images(1 + i, 4, 32) for i in range(3)]
+    c = _calibrated(g, "int8", True, calib)
+    ex = c.executor({"images": (4, 3, 32, 32)})
+    before = ex.run({"images": calib[0]})
+    report = ex.tune(launches=2, reps=1)
+    assert set(report) == {m[3] for m in ex.mfma_descs}
+    for code, best, lib in report.values():
+        assert best <= lib
+        assert code == 0 or code & 0x10000
+    after = ex.run({"images": calib[0]}, use_graph=True)
+    for k in before:
+        np.testing.assert_array_equal(after[k], before[k])
+
+
 def test_saved_qparams_reload_to_identical_results(hip, tmp_path):
     g = G.mini_yolo(seed=0)
     calib = [_images(1 + i, 4, 32) for i in range(3)]
