@@ -57,8 +57,9 @@ def parse():
     return p.parse_args()
 
 
-def layer_work(layer, x_shape):
-    """Algorithmic ops and HBM bytes of one fused conv launch (int8)."""
+def layer_work(layer, x_shape, in_bytes=1):
+    """Algorithmic ops and HBM bytes of one fused conv launch (int8; the
+    input is float32, ``in_bytes`` 4, when its quantization is fused in)."""
     if layer.kind == "conv":
         n, cin, h, w = x_shape
         cout, cg, kh, kw = layer.w_centered.shape
@@ -66,7 +67,8 @@ def layer_work(layer, x_shape):
         oh = (h + pads[0] + pads[2] - dil[0] * (kh - 1) - 1) // strides[0] + 1
         ow = (w + pads[1] + pads[3] - dil[1] * (kw - 1) - 1) // strides[1] + 1
         ops = 2 * n * cout * oh * ow * cg * kh * kw
-        byts = n * cin * h * w + cout * cg * kh * kw + n * cout * oh * ow
+        byts = n * cin * h * w * in_bytes + cout * cg * kh * kw + \
+            n * cout * oh * ow
     else:
         m = int(np.prod(x_shape[:-1]))
         k, ncol = layer.w_centered.shape
@@ -198,29 +200,39 @@ def main():
 
     # ---- per-launch durations (HIP events on the launch stream) ----------
     per = []
-    shapes = {}
+    shapes = {"images": x.shape}
     for name, t in ex.tensors.items():
         shapes[name] = t.shape
     for name, fn in ex.launches:
         per.append((time_launch(fn, 20, torch), name, fn))
-    by_name = {f"conv:{l.name}": l for l in c.layers}
+    layers = {l.name: l for l in c.layers}
+
+    def work(name):
+        """(layer, ops, bytes) of a conv launch ("qconv:": float input)."""
+        kind, _, lname = name.partition(":")
+        if kind not in ("conv", "qconv") or lname not in layers:
+            return None
+        layer = layers[lname]
+        ops, byts = layer_work(layer, shapes[layer.data_inputs[0]],
+                               4 if kind == "qconv" else 1)
+        return layer, ops, byts
+
     in_order = []
     for t, n, _ in per:
         row = [n, round(t, 5)]
-        if n in by_name:  # algorithmic ops and bytes of a fused conv launch
-            row += list(layer_work(by_name[n],
-                                   shapes[by_name[n].data_inputs[0]]))
+        w = work(n)
+        if w is not None:  # algorithmic ops and bytes of a fused conv launch
+            row += [w[1], w[2]]
         in_order.append(row)
     per.sort(reverse=True, key=lambda r: r[0])
     top_ms, top_name, _ = per[0]
-    top = None
-    for layer in c.layers:
-        if top_name == f"conv:{layer.name}":
-            top = layer
-    if top is not None:
-        ops, byts = layer_work(top, shapes[top.data_inputs[0]])
+    w = work(top_name)
+    if w is not None:
+        top, ops, byts = w
         roof = roofline(ops, byts, top_ms)
-        roof["kernel"] = f"fused conv {top.name} (int8 MFMA)"
+        roof["kernel"] = (f"fused conv {top.name} (int8 MFMA"
+                          + (", float input quantized in" if
+                             top_name.startswith("qconv:") else "") + ")")
         roof["ops_per_launch"] = ops
         roof["bytes_per_launch"] = byts
     else:

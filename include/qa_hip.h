@@ -207,6 +207,21 @@ int qa_plan_epilogue_i8(const qa_epi_params* p, void* plan);
  * on success, -1 on an error (see qa_last_error). */
 int qa_d_conv(const qa_conv_desc* d, void* stream);
 
+/* Graph-input quantization fused into the first convolution: x is the
+ * float32 NCHW input [N, C, H, W]; it is quantized exactly as
+ * qa_d_quantize_nhwc would (scale, zp, clip; storage offset
+ * d->x_add + in_zp) and convolved as qa_d_conv would convolve that int8
+ * tensor, which is never written (d->x is not read). Requires the int8
+ * weights of packed layout 1 (C <= 4, KH <= 4, KW <= 4, one group), an
+ * epilogue plan, no residual and no rescaled copy, and a dense channels-last
+ * output; anything else returns -1. d->tile: 0, or 0x10000 | R for R output
+ * rows per work-group. The reference runs the two steps separately
+ * (quant_container.py:150-155 quantizes the input, quant_layers.py:320-335
+ * convolves it). */
+int qa_d_quantize_conv(const qa_conv_desc* d, const float* x, double in_scale,
+                       int64_t in_zp, int64_t in_qmin, int64_t in_qmax,
+                       void* stream);
+
 /* Element-wise device entries (storage codes as above, `*_so` storage
  * offsets). The row forms process `rows` rows of `cols` elements with one
  * row stride per operand (a channel slice of an NCHW tensor: rows = N,

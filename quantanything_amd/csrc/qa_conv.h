@@ -166,4 +166,13 @@ bool mfma_launch_l2(const ConvArgs& b, int wm, bool split, int epi,
                     hipStream_t st);
 bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
 
+// Input quantization fused into a layout-1 convolution (qa_conv_qin.hip):
+// float32 NCHW graph input, quantized exactly like qa_d_quantize_nhwc.
+struct QinArgs {
+    const float* xf;
+    double scale, inv;
+    int64_t zp, qmin, qmax, so;
+};
+bool launch_conv_qin(const ConvArgs& a, const QinArgs& q, hipStream_t st);
+
 }  // namespace qa

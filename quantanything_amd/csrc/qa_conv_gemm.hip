@@ -525,18 +525,20 @@ QA_API int qa_pack_weights_i8(const int32_t* w, int64_t Cout, int64_t Cg,
                         boff, needs_rowsum);
 }
 
-QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
-    hipStream_t st = (hipStream_t)stream_;
+namespace {
+
+// Kernel arguments of a device descriptor: 1 for the int8 MFMA path, 0 for
+// the VALU path, 2 for an empty problem, -1 on error (recorded for `who`).
+int desc_args(const qa_conv_desc* d, ConvArgs& a, const char* who) {
     if (!d) return -1;
     if (!conv_shape_ok(d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW, d->SH,
                        d->SW, d->DH, d->DW, d->G, d->OH, d->OW))
         return -1;
-    if (d->N * d->Cout * d->OH * d->OW == 0) return 0;
+    if (d->N * d->Cout * d->OH * d->OW == 0) return 2;
     if (d->y_code != 1 && d->y_code != 2) {
-        set_error("qa_d_conv", "output storage must be int8 or int16");
+        set_error(who, "output storage must be int8 or int16");
         return -1;
     }
-    ConvArgs a;
     memset(&a, 0, sizeof(a));
     set_geometry(a, d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW, d->SH,
                  d->SW, d->PH, d->PW, d->DH, d->DW, d->G, d->OH, d->OW);
@@ -605,7 +607,7 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
         if (d->x_code != 1 || d->x_sc != 1 || d->x_add < -127 ||
             d->x_add > 128 || d->w_kgp != KGp || d->w_rows != rows ||
             a.Kreal >= 131072 || !aligned) {
-            set_error("qa_d_conv", "int8 MFMA path: operands do not match");
+            set_error(who, "int8 MFMA path: operands do not match");
             return -1;
         }
         a.wp = (const int8_t*)d->w;
@@ -619,10 +621,46 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
         a.rowsum = (int32_t)d->needs_rowsum;
         a.plan = d->epi_plan;
         a.tile_hint = (int32_t)d->tile;
-        return launch_conv_mfma(a, st) ? 0 : -1;
+        return 1;
     }
     a.w = d->w;
     a.w_code = (int32_t)d->w_code;
     a.wide = (int32_t)d->wide;
+    return 0;
+}
+
+}  // namespace
+
+QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
+    hipStream_t st = (hipStream_t)stream_;
+    ConvArgs a;
+    const int r = desc_args(d, a, "qa_d_conv");
+    if (r < 0) return -1;
+    if (r == 2) return 0;
+    if (r == 1) return launch_conv_mfma(a, st) ? 0 : -1;
     return launch_conv_valu(a, st) ? 0 : -1;
+}
+
+QA_API int qa_d_quantize_conv(const qa_conv_desc* d, const float* x,
+                              double in_scale, int64_t in_zp, int64_t in_qmin,
+                              int64_t in_qmax, void* stream_) {
+    hipStream_t st = (hipStream_t)stream_;
+    ConvArgs a;
+    const int r = desc_args(d, a, "qa_d_quantize_conv");
+    if (r < 0) return -1;
+    if (r == 2) return 0;
+    if (r != 1 || !x || !(in_scale > 0.0)) {
+        set_error("qa_d_quantize_conv",
+                  "needs int8 packed weights, an input and a positive scale");
+        return -1;
+    }
+    QinArgs q;
+    q.xf = x;
+    q.scale = in_scale;
+    q.inv = 1.0 / in_scale;
+    q.zp = in_zp;
+    q.qmin = in_qmin;
+    q.qmax = in_qmax;
+    q.so = d->x_add + in_zp;  // stored = q - so, x_add = so - zp
+    return launch_conv_qin(a, q, st) ? 0 : -1;
 }

@@ -1,0 +1,261 @@
+// Graph-input quantization fused into a layout-1 convolution (inputs of at
+// most 4 channels, the image stem): float32 NCHW -> int8 -> conv -> int8
+// table epilogue in one launch, so the int8 input tensor never goes through
+// HBM (it would be written once and read back by the conv).
+//
+// A work-group owns a band of R output rows of one image. Phase 1 reads the
+// band's input rows (R-1)*SH + (KH-1)*DH + 1 of all channels as float4
+// (coalesced rows of each plane), quantizes them exactly like
+// qa_d_quantize_nhwc (qa_quantize_one_fast) and writes them to LDS as one
+// 4-byte word per pixel, channels in bytes 0..C-1 (0 above), with image
+// padding pre-filled with the zero point's stored byte on every side, so
+// phase 2 needs no bounds checks. Phase 2: the 4 waves take 16-pixel tiles
+// of the band in turn; a lane's fragment (pixel col, kernel row kgl) is the
+// 4 words at kernel taps kx = 0..3 of its LDS row, the same bytes the
+// unfused kernel loads from the int8 tensor, then one MFMA per 16 output
+// channels and the table epilogue of k_conv_mfma (Q8_TABLE).
+#include "qa_conv_mfma.h"
+
+namespace qa {
+namespace {
+
+constexpr int QIN_THREADS = 256;
+
+struct QinGeom {
+    int R;           // output rows per band
+    int IR, RW;      // LDS rows and row width (words) of a band
+    int bands;       // ceil(OH / R)
+    int CBK;         // 16-channel output blocks
+    uint64_t mg_ow;  // ceil(2^32 / OW)
+    uint64_t mg_gw;  // ceil(2^32 / (W / 4)) (vector fill)
+    uint64_t mg_w;   // ceil(2^32 / W) (scalar fill)
+    uint64_t mg_pw;  // ceil(2^32 / (RW - W)) (pad columns)
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
+                                                          QinArgs q,
+                                                          QinGeom g) {
+    extern __shared__ int s_raw[];  // IR x RW words
+    __shared__ int s_tab[256];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // consecutive bands of an image on one XCD (blocks are dealt to the 8
+    // XCDs round-robin): their halo rows meet in that XCD's L2
+    const uint32_t nb = gridDim.x, xcd = blockIdx.x & 7;
+    const uint32_t q8 = nb >> 3, r8 = nb & 7;
+    const uint32_t bid = xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3);
+    const int n = (int)(bid / (uint32_t)g.bands);
+    const int band = (int)bid - n * g.bands;
+    const int oy0 = band * g.R;
+    const int iy_base = oy0 * a.SH - a.PH;
+    const int pv = splat4(a.pad_value);
+
+    // ---- phase 1: input rows -> LDS (quantized words, padding filled) --
+    for (int i = tid; i < 256; i += QIN_THREADS)
+        s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
+    const int HW = a.H * a.W;
+    const float* xn = q.xf + (int64_t)n * a.Cg * HW;
+    const int so = (int)q.so;
+    auto qword = [&](const float* f, int stride) -> int {
+        uint32_t w = 0;
+        for (int c = 0; c < a.Cg; ++c)
+            w |= (uint32_t)(uint8_t)(qa_quantize_one_fast(
+                                         f[c * stride], q.scale, q.inv, q.zp,
+                                         q.qmin, q.qmax) -
+                                     so)
+                 << (8 * c);
+        return (int)w;
+    };
+    if (VEC) {  // 4 pixels a thread: one float4 per channel plane
+        const int GW = a.W >> 2;
+        const int items = g.IR * GW;
+        for (int i = tid; i < items; i += QIN_THREADS) {
+            const int r = div_magic(i, g.mg_gw);
+            const int u = i - r * GW;
+            const int iy = iy_base + r;
+            int* dst = s_raw + r * g.RW + a.PW + 4 * u;
+            if ((unsigned)iy < (unsigned)a.H) {
+                const float* src = xn + iy * a.W + 4 * u;
+                float4 v[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (c < a.Cg) v[c] = *(const float4*)(src + c * HW);
+                uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (c < a.Cg) {
+                        const float f[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            w[k] |= (uint32_t)(uint8_t)(qa_quantize_one_fast(
+                                                            f[k], q.scale,
+                                                            q.inv, q.zp,
+                                                            q.qmin, q.qmax) -
+                                                        so)
+                                    << (8 * c);
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) dst[k] = (int)w[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) dst[k] = pv;
+            }
+        }
+    } else {  // one pixel a thread
+        const int items = g.IR * a.W;
+        for (int i = tid; i < items; i += QIN_THREADS) {
+            const int r = div_magic(i, g.mg_w);
+            const int ix = i - r * a.W;
+            const int iy = iy_base + r;
+            s_raw[r * g.RW + a.PW + ix] =
+                (unsigned)iy < (unsigned)a.H ? qword(xn + iy * a.W + ix, HW)
+                                             : pv;
+        }
+    }
+    {  // pad columns: left PW, right RW - W - PW
+        const int PC = g.RW - a.W;
+        for (int i = tid; i < g.IR * PC; i += QIN_THREADS) {
+            const int r = div_magic(i, g.mg_pw);
+            const int k = i - r * PC;
+            s_raw[r * g.RW + (k < a.PW ? k : a.W + k)] = pv;
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 2: 16-pixel tiles of the band, one MFMA per 16 channels --
+    const int col = lane & 15, kgl = lane >> 4, qd = lane & 3;
+    const int Rv = min(g.R, a.OH - oy0);  // valid rows of this band
+    const int bpix = Rv * a.OW;
+    const int ntile = (bpix + 15) >> 4;
+    const int64_t pix0 = ((int64_t)n * a.OH + oy0) * a.OW;  // band's first
+    const uint32_t sel1 = qd < 2 ? 0x05040100u : 0x03020706u;
+    const uint32_t sel2 = (qd & 1) ? 0x03070105u : 0x06020400u;
+    const int cq = col & ~3;
+    const bool krow = kgl < a.KH;  // k-group kgl is kernel row kgl
+    const int nreal = krow ? a.Cg : 0;
+    const int4 hdr = *(const int4*)a.plan;
+    for (int cb = 0; cb < g.CBK; ++cb) {
+        const int co0 = cb * 16;
+        const v4i wf =
+            *(const v4i*)(a.wp + (int64_t)(co0 + col) * a.wp_rstride + kgl * 16);
+        const int c = min(co0 + col, a.Cout - 1);
+        const int4 pc = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
+        const int64_t cc = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                                     (uint32_t)pc.z);
+        const uint32_t ccorr = a.corr ? (uint32_t)a.corr[c] : 0u;
+        const uint32_t cbo = a.rowsum ? (uint32_t)a.boff[c] : 0u;
+        for (int t = wave; t < ntile; t += 4) {
+            // fetch pixel of this lane (clamped into the band)
+            const int pb = min(t * 16 + col, bpix - 1);
+            const int oyl = div_magic(pb, g.mg_ow);
+            const int ox = pb - oyl * a.OW;
+            const int base =
+                krow ? (oyl * a.SH + kgl * a.DH) * g.RW + ox * a.SW : 0;
+            v4i b;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) b[k] = krow ? s_raw[base + k * a.DW] : 0;
+            const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                b, wf, v4i{0, 0, 0, 0}, 0, 0, 0);
+            int ps[4] = {0, 0, 0, 0};
+            if (a.rowsum) {
+                int psum = bytes_sum_l1(b, nreal, a.KW);
+                psum += __shfl_xor(psum, 16);
+                psum += __shfl_xor(psum, 32);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ps[r] = __shfl(psum, 4 * kgl + r);
+            }
+            int e[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                uint32_t wu = (uint32_t)acc[r] + ccorr;
+                if (a.rowsum) wu += cbo * (uint32_t)ps[r];
+                const int q0 = (int)(((int64_t)(int)wu * pc.x + cc) >> pc.y);
+                e[r] = s_tab[min(max(q0, hdr.x), hdr.y) - hdr.x];
+            }
+            const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
+            const int pq = t * 16 + 4 * kgl + qd;  // pixel this lane stores
+            const int c0 = co0 + cq;
+            if (pq < bpix && c0 < a.Cout) {
+                int8_t* py = (int8_t*)a.y + (pix0 + pq) * a.y_pst + c0;
+                if (c0 + 3 < a.Cout) {
+                    *(uint32_t*)py = wy;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (c0 + r < a.Cout) py[r] = (int8_t)(wy >> (8 * r));
+                }
+            }
+        }
+    }
+}
+
+uint64_t magic(int d) { return (((uint64_t)1 << 32) + d - 1) / (uint64_t)d; }
+
+}  // namespace
+
+bool launch_conv_qin(const ConvArgs& a0, const QinArgs& q, hipStream_t st) {
+    ConvArgs a = a0;
+    const int64_t ohw = (int64_t)a.OH * a.OW;
+    const bool dense = a.y_sc == 1 && (a.N == 1 || a.y_sn == ohw * a.y_sp) &&
+                       a.y_sp % 4 == 0 && (uintptr_t)a.y % 4 == 0;
+    if (a.layout != 1 || a.G != 1 || a.KGp != 4 || a.KH < 1 || a.KH > 4 ||
+        a.KW < 1 || a.KW > 4 ||
+        a.Cg > 4 || !a.plan || a.mode != EPI_QUANT || a.y_code != 1 ||
+        a.res || a.y2 || !dense || a.M >= ((int64_t)1 << 31)) {
+        set_error("qa_d_quantize_conv",
+                  "needs layout-1 int8 weights (C, KH, KW <= 4, one group), "
+                  "an epilogue plan, no residual or second output and a "
+                  "dense channels-last int8 output");
+        return false;
+    }
+    a.y_pst = a.y_sp;
+    QinGeom g;
+    // LDS row: input columns -PW .. (OW-1)*SW - PW + 3*DW (kx up to 3)
+    g.RW = (a.OW - 1) * a.SW + 3 * a.DW + 1;
+    if (g.RW < a.W + a.PW) g.RW = a.W + a.PW;
+    g.CBK = (a.Cout + 15) / 16;
+    auto in_rows = [&](int R) { return (R - 1) * a.SH + (a.KH - 1) * a.DH + 1; };
+    auto lds = [&](int R) { return (int64_t)in_rows(R) * g.RW * 4; };
+    int R = 0;
+    const int hint = a.tile_hint & TILE_VALID ? (a.tile_hint & 0xffff) : 0;
+    if (hint >= 1 && hint <= a.OH && lds(hint) <= 60 * 1024) R = hint;
+    if (R == 0) {  // the most rows that still give 4 work-groups per CU
+        const int64_t want = 4 * (int64_t)cu_count();
+        for (int r : {16, 8, 4, 2, 1}) {
+            if (r > a.OH || lds(r) > 32 * 1024) continue;
+            R = r;
+            if ((int64_t)a.N * ((a.OH + r - 1) / r) >= want) break;
+        }
+        if (R == 0) R = 1;
+    }
+    g.R = R;
+    g.IR = in_rows(R);
+    g.bands = (a.OH + R - 1) / R;
+    const int64_t shm = lds(R);
+    const int64_t blocks = (int64_t)a.N * g.bands;
+    if (shm > 60 * 1024 || (int64_t)R * a.OW >= (1 << 16) ||
+        (int64_t)g.IR * g.RW >= (1 << 16) || blocks >= ((int64_t)1 << 31)) {
+        set_error("qa_d_quantize_conv", "image rows too wide for one band");
+        return false;
+    }
+    g.mg_ow = magic(a.OW);
+    g.mg_w = magic(a.W);
+    g.mg_pw = magic(std::max(g.RW - a.W, 1));
+    const bool vec = a.W % 4 == 0 && (uintptr_t)q.xf % 16 == 0;
+    g.mg_gw = magic(vec ? a.W / 4 : 1);
+    if (vec)
+        k_conv_qin<true><<<(unsigned)blocks, QIN_THREADS, shm, st>>>(a, q, g);
+    else
+        k_conv_qin<false><<<(unsigned)blocks, QIN_THREADS, shm, st>>>(a, q, g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_hip_error("qa_d_quantize_conv", e);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace qa

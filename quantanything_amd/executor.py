@@ -206,6 +206,8 @@ class DeviceExecutor:
         self.epi = {}  # tensor -> (desc, first channel) written by an epilogue
         self.mfma_descs = []  # (desc, host params, host table, launch name)
         self.inputs_f32 = {}
+        self.input_q = {}  # graph input -> (float buffer, int8 tensor, qp)
+        self.tunables = []  # (launch name, desc, tile codes, fn(stream))
         self.outputs_f32 = {}
         self.cuda_graph = None
         self._plan(input_shapes)
@@ -252,6 +254,7 @@ class DeviceExecutor:
             self.inputs_f32[name] = xf
             if len(shape) == 4:
                 t = self._new(shape, qp)
+                self.input_q[name] = (xf, t, qp)
                 n, ch, h, w = shape
                 self._add(f"quantize:{name}", lambda s, xf=xf, t=t, n=n,
                           ch=ch, hw=h * w, qp=qp: _ok(
@@ -317,6 +320,13 @@ class DeviceExecutor:
             for name, t in zip(layer.node.outputs, outs):
                 self.tensors[name] = t
         self._plan_epilogues()
+        self._fuse_input_quantization(cons)
+        for d, _, _, name in self.mfma_descs:
+            if name in dict(self.launches):
+                self.tunables.append(
+                    (name, d, self.tile_candidates(d),
+                     lambda s, d=d: _ok(self.lib.qa_d_conv(ctypes.byref(d), s),
+                                        "qa_d_conv")))
         for name in g.outputs:
             t = self.tensors[name]
             if not t.contiguous_2d():
@@ -486,6 +496,39 @@ class DeviceExecutor:
                 dev = _dev(plan, np.uint8)
                 self.keep.append(dev)
                 d.epi_plan = dev.data_ptr()
+
+    def _fuse_input_quantization(self, cons):
+        """A 4-D graph input read only by a layout-1 (<= 4 channel) int8
+        convolution with a table plan is quantized inside that convolution
+        (``qa_d_quantize_conv``): the int8 input tensor is never written."""
+        for name, (xf, t, qp) in self.input_q.items():
+            users = cons.get(name, [])
+            if name in self.graph.outputs or len(users) != 1:
+                continue
+            hits = [(d, ln) for d, _, _, ln in self.mfma_descs
+                    if d.x == t.ptr and ln == f"conv:{users[0].name}"]
+            if len(hits) != 1:
+                continue
+            d, ln = hits[0]
+            if not (d.w_layout == 1 and d.G == 1 and d.epi_plan and
+                    1 <= d.KH <= 4 and 1 <= d.KW <= 4 and not d.res and
+                    not d.y2 and d.y_sc == 1 and d.y_sp % 4 == 0):
+                continue
+            qname = f"quantize:{name}"
+            fused = f"qconv:{users[0].name}"
+
+            def fn(s, d=d, xf=xf, qp=qp):
+                _ok(self.lib.qa_d_quantize_conv(
+                    ctypes.byref(d), xf.data_ptr(), qp.scale, qp.zp, qp.qmin,
+                    qp.qmax, s), "qa_d_quantize_conv")
+
+            self.launches = [(fused, fn) if n == ln else (n, f)
+                             for n, f in self.launches if n != qname]
+            self.keep.append(t)
+            del self.tensors[name]  # never materialized
+            rows = [0] + [0x10000 | r for r in (1, 2, 4, 8, 16)
+                          if r <= d.OH]
+            self.tunables.append((fused, d, rows, fn))
 
     # ------------------------------------------------------- element-wise --
     def _plan_lut(self, layer, ins):
@@ -706,22 +749,23 @@ class DeviceExecutor:
             raise RuntimeError("tune() before the pass is captured")
         report = {}
         torch.cuda.synchronize()
-        for d, _, _, name in self.mfma_descs:
+        for name, d, codes, fn in self.tunables:
             times = {}
-            for code in self.tile_candidates(d):
+            for code in codes:
                 d.tile = code
-                times[code] = self._time_conv(d, launches, reps)
+                times[code] = self._time_launch(fn, launches, reps)
             best = min(times, key=times.get)
             d.tile = best
             report[name] = (best, times[best], times[0])
         return report
 
-    def _time_conv(self, d, launches, reps):
+    @staticmethod
+    def _time_launch(fn, launches, reps):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             s = torch.cuda.current_stream().cuda_stream
             for _ in range(launches):
-                _ok(self.lib.qa_d_conv(ctypes.byref(d), s), "qa_d_conv")
+                fn(s)
         g.replay()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)

@@ -86,9 +86,11 @@ def test_every_conv_tile_is_bit_exact(hip, tmp_path, model, quant_type):
     oracle = OraclePipeline(g, _qjson(c, tmp_path))
     oracle.run(x, keep=True)
     ex = c.executor({"images": x.shape})
-    descs = [m[0] for m in ex.mfma_descs]
-    assert descs, "no MFMA convolutions planned"
-    cands = [ex.tile_candidates(d) for d in descs]
+    assert any(n.startswith("qconv:") for n, _ in ex.launches), \
+        "input quantization not fused into the stem"
+    descs = [t[1] for t in ex.tunables]
+    assert len(descs) == len(ex.mfma_descs)
+    cands = [t[2] for t in ex.tunables]
     for r in range(max(len(cc) for cc in cands)):
         for d, cc in zip(descs, cands):
             d.tile = cc[r % len(cc)]
@@ -104,6 +106,48 @@ def test_every_conv_tile_is_bit_exact(hip, tmp_path, model, quant_type):
         assert checked > len(descs) // 2
 
 
+def _stem_graph(cin, cout, k, stride, pad, dil, size):
+    b = G.GraphBuilder(7)
+    y = b.silu(b.conv("images", cin, cout, k, stride, pad=pad, dilation=dil))
+    y = b.op("Flatten", [b.op("GlobalAveragePool", [y])], axis=1)
+    return b.build("images", [None, cin, size, size], y)
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+@pytest.mark.parametrize("cin,cout,k,stride,pad,dil,size", [
+    (3, 16, 3, 2, 1, 1, 32),   # the image stem, float4 rows
+    (1, 8, 3, 1, 1, 1, 30),    # one channel, rows not a multiple of 4
+    (4, 20, 4, 2, 2, 1, 36),   # 4 channels, 4x4 taps, a partial channel block
+    (2, 16, 2, 1, 0, 2, 29),   # dilation 2, no padding, odd width
+    (3, 32, 1, 1, 0, 1, 16),   # 1x1
+])
+def test_input_quantization_fused_into_stem(hip, tmp_path, quant_type, cin,
+                                            cout, k, stride, pad, dil, size):
+    """qa_d_quantize_conv (float input quantized inside the layout-1 conv)
+    gives the oracle's conv output for every band height it accepts."""
+    g = _stem_graph(cin, cout, k, stride, pad, dil, size)
+    calib = [Stream(20 + i).uniform((3, cin, size, size), -1.0, 1.0)
+             .astype(np.float32) for i in range(2)]
+    c = _calibrated(g, quant_type, True, calib)
+    # beyond the calibrated range
+    x = Stream(30).uniform((3, cin, size, size), -1.2, 1.2).astype(np.float32)
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    oracle.run(x, keep=True)
+    ex = c.executor({"images": x.shape})
+    fused = [t for t in ex.tunables if t[0].startswith("qconv:")]
+    assert len(fused) == 1 and "images" not in ex.tensors
+    _, d, codes, _ = fused[0]
+    for code in codes:
+        d.tile = code
+        ex.run({"images": x})
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, band code {code:#x}")
+
+
 def test_tuned_tiles_keep_results(hip):
     g = G.mini_yolo(seed=0)
     calib = [_images(1 + i, 4, 32) for i in range(3)]
@@ -111,7 +155,7 @@ def test_tuned_tiles_keep_results(hip):
     ex = c.executor({"images": (4, 3, 32, 32)})
     before = ex.run({"images": calib[0]})
     report = ex.tune(launches=2, reps=1)
-    assert set(report) == {m[3] for m in ex.mfma_descs}
+    assert set(report) == {t[0] for t in ex.tunables}
     for code, best, lib in report.values():
         assert best <= lib
         assert code == 0 or code & 0x10000
