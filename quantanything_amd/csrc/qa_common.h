@@ -93,6 +93,29 @@ __device__ __forceinline__ int64_t qa_quantize_one_fast(float x, double scale,
     return (int64_t)(int32_t)v;
 }
 
+// float32 form of qa_quantize_one for scales in [2^-60, 2^60] and clip
+// ranges narrower than 2^20, with invf = float(1 / scale). y = x * invf is
+// within 2^-22.8 * |y| of x / scale (two float roundings), and the
+// reference's double quotient within 2^-53 of it, so when y is farther than
+// 2^-20 * |y| from every half-integer all three round to the same integer
+// (|y| < 2^21, where rintf and the int conversion are exact); when
+// |y| >= 2^21 the clip decides by the sign alone (+-2^21 + zp lies outside
+// the clip range). Otherwise (a near-tie, NaN) *slow is set and the caller
+// must use qa_quantize_one_fast.
+__device__ __forceinline__ int qa_quantize_f32(float x, float invf, int zp,
+                                               int qmin, int qmax,
+                                               bool* slow) {
+    const float y = x * invf;
+    const float ay = fabsf(y);
+    const float r = rintf(y);
+    // no short-circuit: one select-free test (false for NaN)
+    const bool ok = (ay >= 0x1p21f) | (0.5f - fabsf(y - r) > ay * 0x1p-20f);
+    *slow |= !ok;
+    // |r| >= 2^21 saturates to +-2^21, which the clip takes to qmin / qmax
+    const int q = (int)fminf(fmaxf(r, -0x1p21f), 0x1p21f) + zp;
+    return min(max(q, qmin), qmax);
+}
+
 // --------------------------------------------------------------- errors ---
 namespace qa {
 

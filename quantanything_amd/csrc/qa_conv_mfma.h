@@ -314,6 +314,17 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
     const int col = lane & 15;
     const int co0 = blockIdx.y * (WM * 16);
     const bool res = TABLE && a.res != nullptr;
+    // the epilogue tables first: their loads overlap everything below
+    const int ntab = res ? 768 : 256;
+    int tabv[TABLE ? 3 : 1];
+    if (TABLE) {
+        const int* tab = (const int*)((const char*)a.plan + PLAN_E);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int i = threadIdx.x + 256 * j;
+            tabv[j] = i < ntab ? tab[i] : 0;
+        }
+    }
 
     // Tiles of 16 consecutive output pixels; the work-groups that run on
     // one XCD (consecutive block ids go round-robin over the 8 XCDs) take a
@@ -454,7 +465,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
             }
         }
     }
-    // first loads of the ring, then the tables: their latencies overlap
+    // first loads of the ring (in flight with the weight and table loads)
     if (has_tile) {
 #pragma unroll
         for (int s = 0; s < D; ++s)
@@ -471,9 +482,11 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
         }
     }
     if (TABLE) {
-        const int* tab = (const int*)((const char*)a.plan + PLAN_E);
-        const int n = res ? 768 : 256;
-        for (int i = threadIdx.x; i < n; i += 256) s_tab[i] = tab[i];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int i = threadIdx.x + 256 * j;
+            if (i < ntab) s_tab[i] = tabv[j];
+        }
     }
     __syncthreads();
     if (!has_tile) return;

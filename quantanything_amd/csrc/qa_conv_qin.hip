@@ -24,15 +24,45 @@ constexpr int QIN_THREADS = 256;
 struct QinGeom {
     int R;           // output rows per band
     int IR, RW;      // LDS rows and row width (words) of a band
+    int c0;          // LDS column of input column 0 (>= PW; 4-aligned: VEC)
     int bands;       // ceil(OH / R)
     int CBK;         // 16-channel output blocks
+    int f32;         // the float32 quantization form applies
     uint64_t mg_ow;  // ceil(2^32 / OW)
-    uint64_t mg_gw;  // ceil(2^32 / (W / 4)) (vector fill)
-    uint64_t mg_w;   // ceil(2^32 / W) (scalar fill)
-    uint64_t mg_pw;  // ceil(2^32 / (RW - W)) (pad columns)
+    uint64_t mg_pw;  // ceil(2^32 / pad columns per row)
 };
 
-template <bool VEC>
+// Quantized word of one pixel: channel c in byte c (storage offset so
+// subtracted), bytes above CIN zero, exactly qa_quantize_one per value.
+template <int CIN>
+__device__ __forceinline__ uint32_t pixel_word(const float (&f)[CIN],
+                                               const QinArgs& q, float invf,
+                                               bool f32) {
+    uint32_t w = 0;
+    bool slow = !f32;
+    if (f32) {  // clip(r + zp) - so == clip(r + zp - so) with shifted bounds
+        const int so = (int)q.so;
+#pragma unroll
+        for (int c = 0; c < CIN; ++c)
+            w |= (uint32_t)(uint8_t)qa_quantize_f32(
+                     f[c], invf, (int)q.zp - so, (int)q.qmin - so,
+                     (int)q.qmax - so, &slow)
+                 << (8 * c);
+    }
+    if (slow) {  // near a rounding tie, NaN, or scales outside the f32 form
+        w = 0;
+#pragma unroll
+        for (int c = 0; c < CIN; ++c)
+            w |= (uint32_t)(uint8_t)(qa_quantize_one_fast(f[c], q.scale, q.inv,
+                                                          q.zp, q.qmin,
+                                                          q.qmax) -
+                                     q.so)
+                 << (8 * c);
+    }
+    return w;
+}
+
+template <int CIN, bool VEC>
 __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
                                                           QinArgs q,
                                                           QinGeom g) {
@@ -56,71 +86,64 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
     for (int i = tid; i < 256; i += QIN_THREADS)
         s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
     const int HW = a.H * a.W;
-    const float* xn = q.xf + (int64_t)n * a.Cg * HW;
-    const int so = (int)q.so;
-    auto qword = [&](const float* f, int stride) -> int {
-        uint32_t w = 0;
-        for (int c = 0; c < a.Cg; ++c)
-            w |= (uint32_t)(uint8_t)(qa_quantize_one_fast(
-                                         f[c * stride], q.scale, q.inv, q.zp,
-                                         q.qmin, q.qmax) -
-                                     so)
-                 << (8 * c);
-        return (int)w;
-    };
-    if (VEC) {  // 4 pixels a thread: one float4 per channel plane
-        const int GW = a.W >> 2;
-        const int items = g.IR * GW;
-        for (int i = tid; i < items; i += QIN_THREADS) {
-            const int r = div_magic(i, g.mg_gw);
-            const int u = i - r * GW;
-            const int iy = iy_base + r;
-            int* dst = s_raw + r * g.RW + a.PW + 4 * u;
-            if ((unsigned)iy < (unsigned)a.H) {
-                const float* src = xn + iy * a.W + 4 * u;
-                float4 v[4];
+    const float* xn = q.xf + (int64_t)n * CIN * HW;
+    const float invf = (float)q.inv;
+    const bool f32 = g.f32;
+    constexpr int PX = VEC ? 4 : 1;  // pixels per item
+    const int GW = a.W / PX;          // items per input row
+    // wave w fills rows w, w + 4, ..., two rows at a time (loads of both
+    // in flight); lane = item of the row
+    for (int r0 = wave; r0 < g.IR; r0 += 8) {
+        for (int u = lane; u < GW; u += 64) {
+            float v[2][CIN][PX];
+            bool in[2];
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (c < a.Cg) v[c] = *(const float4*)(src + c * HW);
-                uint32_t w[4] = {0, 0, 0, 0};
+            for (int k = 0; k < 2; ++k) {
+                const int iy = iy_base + min(r0 + 4 * k, g.IR - 1);
+                in[k] = (unsigned)iy < (unsigned)a.H;
+                const float* src = xn + (in[k] ? iy : 0) * a.W + PX * u;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    if (c < a.Cg) {
-                        const float f[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            w[k] |= (uint32_t)(uint8_t)(qa_quantize_one_fast(
-                                                            f[k], q.scale,
-                                                            q.inv, q.zp,
-                                                            q.qmin, q.qmax) -
-                                                        so)
-                                    << (8 * c);
+                for (int c = 0; c < CIN; ++c) {
+                    if (VEC) {
+                        const float4 t = *(const float4*)(src + c * HW);
+                        v[k][c][0] = t.x;
+                        v[k][c][PX > 1 ? 1 : 0] = t.y;
+                        v[k][c][PX > 2 ? 2 : 0] = t.z;
+                        v[k][c][PX > 3 ? 3 : 0] = t.w;
+                    } else {
+                        v[k][c][0] = src[c * HW];
                     }
                 }
+            }
 #pragma unroll
-                for (int k = 0; k < 4; ++k) dst[k] = (int)w[k];
-            } else {
+            for (int k = 0; k < 2; ++k) {
+                const int r = r0 + 4 * k;
+                if (r >= g.IR) break;
+                uint32_t w[PX];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) dst[k] = pv;
+                for (int p = 0; p < PX; ++p) {
+                    float f[CIN];
+#pragma unroll
+                    for (int c = 0; c < CIN; ++c) f[c] = v[k][c][p];
+                    w[p] = pixel_word<CIN>(f, q, invf, f32);
+                    if (!in[k]) w[p] = (uint32_t)pv;
+                }
+                int* dst = s_raw + r * g.RW + g.c0 + PX * u;
+                if (VEC)
+                    *(uint4*)dst = make_uint4(w[0], w[PX > 1 ? 1 : 0],
+                                              w[PX > 2 ? 2 : 0],
+                                              w[PX > 3 ? 3 : 0]);
+                else
+                    *dst = (int)w[0];
             }
         }
-    } else {  // one pixel a thread
-        const int items = g.IR * a.W;
-        for (int i = tid; i < items; i += QIN_THREADS) {
-            const int r = div_magic(i, g.mg_w);
-            const int ix = i - r * a.W;
-            const int iy = iy_base + r;
-            s_raw[r * g.RW + a.PW + ix] =
-                (unsigned)iy < (unsigned)a.H ? qword(xn + iy * a.W + ix, HW)
-                                             : pv;
-        }
     }
-    {  // pad columns: left PW, right RW - W - PW
-        const int PC = g.RW - a.W;
+    {  // pad columns: c0 - PW .. c0 - 1 and c0 + W .. RW - 1
+        const int lo = g.c0 - a.PW, PC = g.RW - lo - a.W;
         for (int i = tid; i < g.IR * PC; i += QIN_THREADS) {
             const int r = div_magic(i, g.mg_pw);
             const int k = i - r * PC;
-            s_raw[r * g.RW + (k < a.PW ? k : a.W + k)] = pv;
+            s_raw[r * g.RW + lo + (k < a.PW ? k : a.W + k)] = pv;
         }
     }
     __syncthreads();
@@ -134,8 +157,12 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
     const uint32_t sel1 = qd < 2 ? 0x05040100u : 0x03020706u;
     const uint32_t sel2 = (qd & 1) ? 0x03070105u : 0x06020400u;
     const int cq = col & ~3;
-    const bool krow = kgl < a.KH;  // k-group kgl is kernel row kgl
-    const int nreal = krow ? a.Cg : 0;
+    // k-group kgl is kernel row kgl; past the kernel rows the weights are
+    // zero: those lanes read row KH - 1 (any bytes do), left out of the
+    // row sums
+    const int kbase = min(kgl, a.KH - 1) * a.DH * g.RW + g.c0 - a.PW;
+    const int shrw = a.SH * g.RW;
+    const int nreal = kgl < a.KH ? a.Cg : 0;
     const int4 hdr = *(const int4*)a.plan;
     for (int cb = 0; cb < g.CBK; ++cb) {
         const int co0 = cb * 16;
@@ -147,16 +174,28 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
                                      (uint32_t)pc.z);
         const uint32_t ccorr = a.corr ? (uint32_t)a.corr[c] : 0u;
         const uint32_t cbo = a.rowsum ? (uint32_t)a.boff[c] : 0u;
+        // this lane's fetch pixel walks the band 64 pixels a step
+        int fp = min(wave * 16 + col, bpix - 1);
+        int oyl = div_magic(fp, g.mg_ow);
+        int ox = fp - oyl * a.OW;
         for (int t = wave; t < ntile; t += 4) {
-            // fetch pixel of this lane (clamped into the band)
-            const int pb = min(t * 16 + col, bpix - 1);
-            const int oyl = div_magic(pb, g.mg_ow);
-            const int ox = pb - oyl * a.OW;
-            const int base =
-                krow ? (oyl * a.SH + kgl * a.DH) * g.RW + ox * a.SW : 0;
+            const int base = __mul24(oyl, shrw) + kbase + __mul24(ox, a.SW);
             v4i b;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) b[k] = krow ? s_raw[base + k * a.DW] : 0;
+            for (int k = 0; k < 4; ++k) b[k] = s_raw[base + k * a.DW];
+            // next tile of this wave (pixels past the band stay clamped)
+            if (fp + 64 < bpix) {
+                fp += 64;
+                ox += 64;
+                while (ox >= a.OW) {
+                    ox -= a.OW;
+                    ++oyl;
+                }
+            } else {
+                fp = bpix - 1;
+                oyl = div_magic(fp, g.mg_ow);
+                ox = fp - oyl * a.OW;
+            }
             const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                 b, wf, v4i{0, 0, 0, 0}, 0, 0, 0);
             int ps[4] = {0, 0, 0, 0};
@@ -203,7 +242,7 @@ bool launch_conv_qin(const ConvArgs& a0, const QinArgs& q, hipStream_t st) {
                        a.y_sp % 4 == 0 && (uintptr_t)a.y % 4 == 0;
     if (a.layout != 1 || a.G != 1 || a.KGp != 4 || a.KH < 1 || a.KH > 4 ||
         a.KW < 1 || a.KW > 4 ||
-        a.Cg > 4 || !a.plan || a.mode != EPI_QUANT || a.y_code != 1 ||
+        a.Cg < 1 || a.Cg > 4 || !a.plan || a.mode != EPI_QUANT || a.y_code != 1 ||
         a.res || a.y2 || !dense || a.M >= ((int64_t)1 << 31)) {
         set_error("qa_d_quantize_conv",
                   "needs layout-1 int8 weights (C, KH, KW <= 4, one group), "
@@ -213,10 +252,19 @@ bool launch_conv_qin(const ConvArgs& a0, const QinArgs& q, hipStream_t st) {
     }
     a.y_pst = a.y_sp;
     QinGeom g;
-    // LDS row: input columns -PW .. (OW-1)*SW - PW + 3*DW (kx up to 3)
-    g.RW = (a.OW - 1) * a.SW + 3 * a.DW + 1;
-    if (g.RW < a.W + a.PW) g.RW = a.W + a.PW;
+    const bool vec = a.W % 4 == 0 && (uintptr_t)q.xf % 16 == 0;
+    // LDS row: input columns -PW .. (OW-1)*SW - PW + 3*DW (taps kx <= 3)
+    // and the whole image row, column ix at c0 + ix
+    g.c0 = vec ? (a.PW + 3) / 4 * 4 : a.PW;
+    {
+        const int last = std::max(g.c0 - a.PW + (a.OW - 1) * a.SW + 3 * a.DW,
+                                  g.c0 + a.W - 1);
+        g.RW = (last + 1 + 3) / 4 * 4;
+    }
     g.CBK = (a.Cout + 15) / 16;
+    g.f32 = q.scale >= 0x1p-60 && q.scale <= 0x1p60 &&
+            q.qmax - q.qmin < (1 << 20) && q.qmin >= INT32_MIN &&
+            q.qmax <= INT32_MAX && q.zp >= q.qmin && q.zp <= q.qmax;
     auto in_rows = [&](int R) { return (R - 1) * a.SH + (a.KH - 1) * a.DH + 1; };
     auto lds = [&](int R) { return (int64_t)in_rows(R) * g.RW * 4; };
     int R = 0;
@@ -242,14 +290,20 @@ bool launch_conv_qin(const ConvArgs& a0, const QinArgs& q, hipStream_t st) {
         return false;
     }
     g.mg_ow = magic(a.OW);
-    g.mg_w = magic(a.W);
-    g.mg_pw = magic(std::max(g.RW - a.W, 1));
-    const bool vec = a.W % 4 == 0 && (uintptr_t)q.xf % 16 == 0;
-    g.mg_gw = magic(vec ? a.W / 4 : 1);
-    if (vec)
-        k_conv_qin<true><<<(unsigned)blocks, QIN_THREADS, shm, st>>>(a, q, g);
-    else
-        k_conv_qin<false><<<(unsigned)blocks, QIN_THREADS, shm, st>>>(a, q, g);
+    g.mg_pw = magic(std::max(g.RW - (g.c0 - a.PW) - a.W, 1));
+    auto go = [&](auto kern) {
+        kern<<<(unsigned)blocks, QIN_THREADS, shm, st>>>(a, q, g);
+    };
+    switch (a.Cg * 2 + (vec ? 1 : 0)) {
+        case 2: go(k_conv_qin<1, false>); break;
+        case 3: go(k_conv_qin<1, true>); break;
+        case 4: go(k_conv_qin<2, false>); break;
+        case 5: go(k_conv_qin<2, true>); break;
+        case 6: go(k_conv_qin<3, false>); break;
+        case 7: go(k_conv_qin<3, true>); break;
+        case 8: go(k_conv_qin<4, false>); break;
+        default: go(k_conv_qin<4, true>); break;
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("qa_d_quantize_conv", e);
