@@ -287,6 +287,16 @@ int qa_d_softmax(const void* x, int in_code, int64_t rows, int64_t cols,
                  int out_code, double out_scale, int64_t out_zp, int64_t qmin,
                  int64_t qmax, int64_t out_so, void* stream);
 
+/* qa_d_softmax that also writes the dequantized result to out_f32
+ * ([rows, cols] float32, (q - out_zp) * out_scale as qa_d_dequantize_f32
+ * computes it) when the Softmax output is a graph output (the reference
+ * dequantizes graph outputs after the pass, quant_container.py:186-192). */
+int qa_d_softmax_f32(const void* x, int in_code, int64_t rows, int64_t cols,
+                     double in_scale, int64_t in_zp, int64_t in_so, void* out,
+                     int out_code, double out_scale, int64_t out_zp,
+                     int64_t qmin, int64_t qmax, int64_t out_so,
+                     float* out_f32, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -192,35 +192,70 @@ __device__ double block_reduce(double v, bool is_max, double* sh) {
     return r;
 }
 
-// One work-group per row of `cols` values.
+// One work-group per row of `cols` values. Rows of at most kThreads * PER
+// values are read once and their exponentials kept in registers; longer
+// rows take three passes. Summation order is the same either way (thread
+// t adds its values t, t + kThreads, ... in order, then the block
+// reduction). outf (optional) receives the dequantized output,
+// (q - out_zp) * out_scale, as qa_d_dequantize_f32 computes it.
+constexpr int SOFTMAX_PER = 8;
+
 __global__ __launch_bounds__(kThreads) void k_softmax(
     const void* __restrict__ x, int in_code, int64_t rows, int64_t cols,
     double in_scale, int64_t in_zp, int64_t in_so, void* out, int out_code,
     double out_scale, int64_t out_zp, int64_t qmin, int64_t qmax,
-    int64_t out_so) {
+    int64_t out_so, float* __restrict__ outf) {
     __shared__ double sh[kThreads / 64];
+    const bool held = cols <= (int64_t)kThreads * SOFTMAX_PER;
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const int64_t base = r * cols;
-        double mx = -INFINITY;
-        for (int64_t i = threadIdx.x; i < cols; i += kThreads) {
-            const float xf = (float)((double)(load_s(x, in_code, base + i) +
-                                              in_so - in_zp) * in_scale);
-            mx = fmax(mx, (double)xf);
-        }
-        mx = block_reduce(mx, true, sh);
-        double sum = 0.0;
-        for (int64_t i = threadIdx.x; i < cols; i += kThreads) {
-            const float xf = (float)((double)(load_s(x, in_code, base + i) +
-                                              in_so - in_zp) * in_scale);
-            sum += exp((double)xf - mx);
-        }
-        sum = block_reduce(sum, false, sh);
-        for (int64_t i = threadIdx.x; i < cols; i += kThreads) {
-            const float xf = (float)((double)(load_s(x, in_code, base + i) +
-                                              in_so - in_zp) * in_scale);
-            const float y = (float)(exp((double)xf - mx) / sum);
-            store_s(out, out_code, base + i,
-                    qa_quantize_one(y, out_scale, out_zp, qmin, qmax) - out_so);
+        auto value = [&](int64_t i) {
+            return (float)((double)(load_s(x, in_code, base + i) + in_so -
+                                    in_zp) *
+                           in_scale);
+        };
+        auto emit = [&](int64_t i, double e, double sum) {
+            const float y = (float)(e / sum);
+            const int64_t q = qa_quantize_one(y, out_scale, out_zp, qmin, qmax);
+            store_s(out, out_code, base + i, q - out_so);
+            if (outf)
+                outf[base + i] =
+                    (float)((double)(q - out_zp) * out_scale);
+        };
+        if (held) {
+            float xf[SOFTMAX_PER];
+            double mx = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < SOFTMAX_PER; ++k) {
+                const int64_t i = threadIdx.x + (int64_t)k * kThreads;
+                xf[k] = i < cols ? value(i) : 0.0f;
+                if (i < cols) mx = fmax(mx, (double)xf[k]);
+            }
+            mx = block_reduce(mx, true, sh);
+            double e[SOFTMAX_PER], sum = 0.0;
+#pragma unroll
+            for (int k = 0; k < SOFTMAX_PER; ++k) {
+                const int64_t i = threadIdx.x + (int64_t)k * kThreads;
+                e[k] = i < cols ? exp((double)xf[k] - mx) : 0.0;
+                sum += e[k];
+            }
+            sum = block_reduce(sum, false, sh);
+#pragma unroll
+            for (int k = 0; k < SOFTMAX_PER; ++k) {
+                const int64_t i = threadIdx.x + (int64_t)k * kThreads;
+                if (i < cols) emit(i, e[k], sum);
+            }
+        } else {
+            double mx = -INFINITY;
+            for (int64_t i = threadIdx.x; i < cols; i += kThreads)
+                mx = fmax(mx, (double)value(i));
+            mx = block_reduce(mx, true, sh);
+            double sum = 0.0;
+            for (int64_t i = threadIdx.x; i < cols; i += kThreads)
+                sum += exp((double)value(i) - mx);
+            sum = block_reduce(sum, false, sh);
+            for (int64_t i = threadIdx.x; i < cols; i += kThreads)
+                emit(i, exp((double)value(i) - mx), sum);
         }
         __syncthreads();
     }
@@ -328,6 +363,28 @@ QA_API int qa_d_softmax(const void* x, int in_code, int64_t rows, int64_t cols,
     k_softmax<<<blocks, kThreads, 0, st>>>(x, in_code, rows, cols, in_scale,
                                            in_zp, in_so, out, out_code,
                                            out_scale, out_zp, qmin, qmax,
-                                           out_so);
+                                           out_so, nullptr);
     return launched("qa_d_softmax") ? 0 : -1;
+}
+
+// qa_d_softmax that also writes the dequantized output (float32, same
+// [rows, cols] layout) for a graph output.
+QA_API int qa_d_softmax_f32(const void* x, int in_code, int64_t rows,
+                            int64_t cols, double in_scale, int64_t in_zp,
+                            int64_t in_so, void* out, int out_code,
+                            double out_scale, int64_t out_zp, int64_t qmin,
+                            int64_t qmax, int64_t out_so, float* out_f32,
+                            void* stream) {
+    if (rows <= 0 || cols <= 0) return 0;
+    if (!out_f32) {
+        qa::set_error("qa_d_softmax_f32", "no float output");
+        return -1;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned blocks = (unsigned)(rows < 65535 ? rows : 65535);
+    k_softmax<<<blocks, kThreads, 0, st>>>(x, in_code, rows, cols, in_scale,
+                                           in_zp, in_so, out, out_code,
+                                           out_scale, out_zp, qmin, qmax,
+                                           out_so, out_f32);
+    return launched("qa_d_softmax_f32") ? 0 : -1;
 }

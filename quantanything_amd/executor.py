@@ -207,6 +207,7 @@ class DeviceExecutor:
         self.mfma_descs = []  # (desc, host params, host table, launch name)
         self.inputs_f32 = {}
         self.input_q = {}  # graph input -> (float buffer, int8 tensor, qp)
+        self.softmax_of = {}  # Softmax output -> (launch name, arguments)
         self.tunables = []  # (launch name, desc, tile codes, fn(stream))
         self.outputs_f32 = {}
         self.cuda_graph = None
@@ -333,6 +334,15 @@ class DeviceExecutor:
                 raise NotImplementedError("graph outputs must be 2-D")
             yf = torch.empty(t.shape, dtype=torch.float32, device="cuda")
             self.outputs_f32[name] = yf
+            sm = self.softmax_of.get(name)
+            if sm is not None:  # the Softmax writes the float copy too
+                lname, args = sm
+                fused = (lname, lambda s, args=args, yf=yf: _ok(
+                    self.lib.qa_d_softmax_f32(*args, yf.data_ptr(), s),
+                    "qa_d_softmax_f32"))
+                self.launches = [fused if n == lname else (n, f)
+                                 for n, f in self.launches]
+                continue
             n = yf.numel()
             self._add(f"dequantize:{name}", lambda s, t=t, yf=yf, n=n:
                       _ok(self.lib.qa_d_dequantize_f32(
@@ -710,11 +720,12 @@ class DeviceExecutor:
             y = self._new(x.shape, o)
             rows, cols = x.shape
             iq = layer.in_qp[0]
-            self._add(f"softmax:{layer.name}", lambda s: _ok(
-                self.lib.qa_d_softmax(x.ptr, x.code, rows, cols, iq.scale,
-                                      iq.zp, x.so, y.ptr, y.code, o.scale,
-                                      o.zp, o.qmin, o.qmax, y.so, s),
-                "qa_d_softmax"))
+            args = (x.ptr, x.code, rows, cols, iq.scale, iq.zp, x.so, y.ptr,
+                    y.code, o.scale, o.zp, o.qmin, o.qmax, y.so)
+            lname = f"softmax:{layer.name}"
+            self.softmax_of[layer.node.outputs[0]] = (lname, args)
+            self._add(lname, lambda s: _ok(self.lib.qa_d_softmax(*args, s),
+                                           "qa_d_softmax"))
             return [y]
         raise NotImplementedError(f"float fallback of {op} on the device")
 
