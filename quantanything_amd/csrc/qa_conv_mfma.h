@@ -387,25 +387,23 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
         pB = h.y;
         pSH = h.z;
     }
-    // ---- this lane's output channel (co0 + i*16 + col) and its constants
+    // ---- the block's per-channel constants, loaded once per work-group
+    // (thread t < WM*16: channel co0 + t) and read from LDS after the
+    // barrier into the lane's registers (channels co0 + i*16 + col)
+    __shared__ int4 s_pc[TABLE ? WM * 16 : 1];
+    __shared__ uint2 s_cb[TABLE ? WM * 16 : 1];
+    int4 cst_pc = int4{0, 0, 0, 0};
+    uint2 cst_cb = uint2{0u, 0u};
+    if (TABLE && threadIdx.x < WM * 16) {
+        const int c = min(co0 + (int)threadIdx.x, a.Cog - 1);
+        const int64_t co = (int64_t)g * a.Cog + c;
+        cst_pc = ((const int4*)((const char*)a.plan + PLAN_CH))[co];
+        cst_cb.x = a.corr ? (uint32_t)a.corr[co] : 0u;
+        cst_cb.y = a.rowsum ? (uint32_t)a.boff[co] : 0u;
+    }
     int cm[TABLE ? WM : 1], ct[TABLE ? WM : 1];
     int64_t cc[TABLE ? WM : 1];
     uint32_t ccorr[TABLE ? WM : 1], cbo[TABLE ? WM : 1];
-    if (TABLE && has_tile) {
-        const int4* pch = (const int4*)((const char*)a.plan + PLAN_CH);
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            const int c = min(co0 + i * 16 + col, a.Cog - 1);
-            const int64_t co = (int64_t)g * a.Cog + c;
-            const int4 pc = pch[co];
-            cm[i] = pc.x;
-            ct[i] = pc.y;
-            cc[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
-                              (uint32_t)pc.z);
-            ccorr[i] = a.corr ? (uint32_t)a.corr[co] : 0u;
-            cbo[i] = a.rowsum ? (uint32_t)a.boff[co] : 0u;
-        }
-    }
     const int q = lane & 3;  // lane within its quad
     const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
     const uint32_t sel2 = (q & 1) ? 0x03070105u : 0x06020400u;
@@ -487,8 +485,25 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
             const int i = threadIdx.x + 256 * j;
             if (i < ntab) s_tab[i] = tabv[j];
         }
+        if (threadIdx.x < WM * 16) {
+            s_pc[threadIdx.x] = cst_pc;
+            s_cb[threadIdx.x] = cst_cb;
+        }
     }
     __syncthreads();
+    if (TABLE) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int4 pc = s_pc[i * 16 + col];
+            const uint2 cb = s_cb[i * 16 + col];
+            cm[i] = pc.x;
+            ct[i] = pc.y;
+            cc[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                              (uint32_t)pc.z);
+            ccorr[i] = cb.x;
+            cbo[i] = cb.y;
+        }
+    }
     if (!has_tile) return;
     const int pv = splat4(a.pad_value);
 
