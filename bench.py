@@ -51,6 +51,9 @@ def parse():
     p.add_argument("--no-tune", action="store_true",
                    help="keep the library's own conv tiling (no plan-time "
                         "timing of the tile variants)")
+    p.add_argument("--tiles", metavar="JSON",
+                   help="fixed tile codes instead of timing them: a bench "
+                        "line's \"tiles\" object, or that object alone")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="finish with one device copy of MIB MiB (a plain "
                         "copy kernel that calibrates byte counters)")
@@ -131,7 +134,17 @@ def main():
     ex.launch()
     torch.cuda.synchronize()
     tiles = {}
-    if not args.no_tune:  # plan time: per-layer tile variants, fastest kept
+    if args.tiles:  # a recorded choice (reproducible profiles)
+        with open(args.tiles) as f:
+            fixed = json.load(f)
+        fixed = fixed.get("tiles", fixed)
+        for name, d, codes, _ in ex.tunables:
+            if name in fixed:
+                d.tile = int(fixed[name][0], 16)
+                tiles[name] = (d.tile, float("nan"), float("nan"))
+        ex.launch()
+        torch.cuda.synchronize()
+    elif not args.no_tune:  # plan time: per-layer tile variants, fastest kept
         tiles = ex.tune()
         ex.launch()
         torch.cuda.synchronize()
@@ -240,6 +253,15 @@ def main():
                 "unit": "GB/s", "frac": None, "traffic": None,
                 "kernel": top_name}
     roof["avg_ms"] = round(top_ms, 5)
+    # HBM bytes of that launch from the committed counter profile (rocprofv3
+    # FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), when it has it
+    prof = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "yolov8n_cls_b64_int8_traffic.json")
+    if os.path.exists(prof):
+        with open(prof) as f:
+            measured = json.load(f).get("traffic", {})
+        if top_name in measured:
+            roof["traffic"] = measured[top_name]
 
     kernels = []
     for wl in (GemmWorkload(), ConvWorkload()):
@@ -276,7 +298,8 @@ def main():
         "launches_per_step": len(ex.launches),
         "top_launches_ms": [[n, round(t, 5)] for t, n, _ in per[:6]],
         "launches_ms": in_order,
-        "tiles": {n: [hex(code), round(best, 5), round(lib, 5)]
+        "tiles": {n: [hex(code), None if best != best else round(best, 5),
+                      None if lib != lib else round(lib, 5)]
                   for n, (code, best, lib) in tiles.items()},
     }
     if args.copy_probe > 0:
