@@ -223,11 +223,14 @@ def main():
     def work(name):
         """(layer, ops, bytes) of a conv launch ("qconv:": float input)."""
         kind, _, lname = name.partition(":")
-        if kind not in ("conv", "qconv") or lname not in layers:
+        if kind not in ("conv", "qconv", "convpool") or lname not in layers:
             return None
         layer = layers[lname]
-        ops, byts = layer_work(layer, shapes[layer.data_inputs[0]],
-                               4 if kind == "qconv" else 1)
+        xs = shapes[layer.data_inputs[0]]
+        ops, byts = layer_work(layer, xs, 4 if kind == "qconv" else 1)
+        if kind == "convpool":  # the pooled output replaces the conv output
+            cout = layer.w_centered.shape[0]
+            byts -= ops // (2 * layer.w_centered[0].size) - xs[0] * cout
         return layer, ops, byts
 
     in_order = []

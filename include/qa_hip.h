@@ -207,6 +207,24 @@ int qa_plan_epilogue_i8(const qa_epi_params* p, void* plan);
  * on success, -1 on an error (see qa_last_error). */
 int qa_d_conv(const qa_conv_desc* d, void* stream);
 
+/* A convolution whose output only feeds a GlobalAveragePool, fused with
+ * it: runs d as qa_d_conv would (int8 packed weights of layout 0, one
+ * group, an epilogue plan, no residual or second output) but instead of
+ * storing the output it pools it per image and channel,
+ * q = clip(mbqm(sum_p (y_p - in_zp), mult, shift) + zp, qmin, qmax),
+ * stored at out[n * out_sn + c] - out_so (int8); d->y is not written. The
+ * reference runs the two layers separately (quant_layers.py:320-335, then
+ * quant_layers.py:569-583); results are identical. d->tile: 0, or
+ * 0x10000 | wm (64*wm output channels per work-group, wm 1 or 2). */
+typedef struct qa_pool_params {
+    int64_t in_zp;                        /* zero point of the conv output */
+    int64_t mult, shift, zp, qmin, qmax;  /* the pool's requantization */
+    void* out;
+    int64_t out_sn, out_so;
+} qa_pool_params;
+int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
+                   void* stream);
+
 /* Graph-input quantization fused into the first convolution: x is the
  * float32 NCHW input [N, C, H, W]; it is quantized exactly as
  * qa_d_quantize_nhwc would (scale, zp, clip; storage offset

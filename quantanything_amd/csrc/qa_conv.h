@@ -175,4 +175,14 @@ struct QinArgs {
 };
 bool launch_conv_qin(const ConvArgs& a, const QinArgs& q, hipStream_t st);
 
+// A convolution consumed only by a global average pool (qa_conv_pool.hip):
+// pooled int8 output q = clip(mbqm(sum of stored bytes + base, mult, shift)
+// + zp) - out_so per image and channel, base = HW * (so - zp_in).
+struct PoolArgs {
+    int64_t base, mult, shift, zp, qmin, qmax, out_so;
+    int8_t* out;
+    int64_t out_sn;
+};
+bool launch_conv_pool(const ConvArgs& a, const PoolArgs& p, hipStream_t st);
+
 }  // namespace qa

@@ -641,6 +641,31 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
     return launch_conv_valu(a, st) ? 0 : -1;
 }
 
+QA_API int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
+                          void* stream_) {
+    hipStream_t st = (hipStream_t)stream_;
+    ConvArgs a;
+    const int r = desc_args(d, a, "qa_d_conv_pool");
+    if (r < 0) return -1;
+    if (r == 2) return 0;
+    if (r != 1 || !p || !p->out || d->y_code != 1) {
+        set_error("qa_d_conv_pool",
+                  "needs int8 packed weights, int8 storage and a pool");
+        return -1;
+    }
+    PoolArgs pl;
+    pl.base = d->OH * d->OW * (d->y_so - p->in_zp);
+    pl.mult = p->mult;
+    pl.shift = p->shift;
+    pl.zp = p->zp;
+    pl.qmin = p->qmin;
+    pl.qmax = p->qmax;
+    pl.out_so = p->out_so;
+    pl.out = (int8_t*)p->out;
+    pl.out_sn = p->out_sn;
+    return launch_conv_pool(a, pl, st) ? 0 : -1;
+}
+
 QA_API int qa_d_quantize_conv(const qa_conv_desc* d, const float* x,
                               double in_scale, int64_t in_zp, int64_t in_qmin,
                               int64_t in_qmax, void* stream_) {

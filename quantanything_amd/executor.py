@@ -126,6 +126,14 @@ class DeviceTensor:
         return v.to(torch.int32).cpu().numpy() + self.so
 
 
+class PoolParams(ctypes.Structure):
+    """``qa_pool_params`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([(n, _I64) for n in ("in_zp", "mult", "shift", "zp", "qmin",
+                                     "qmax")]
+                + [("out", _P), ("out_sn", _I64), ("out_so", _I64)])
+
+
 class EpiParams(ctypes.Structure):
     """``qa_epi_params`` of ``include/qa_hip.h`` (all fields 8 bytes)."""
 
@@ -208,6 +216,7 @@ class DeviceExecutor:
         self.inputs_f32 = {}
         self.input_q = {}  # graph input -> (float buffer, int8 tensor, qp)
         self.softmax_of = {}  # Softmax output -> (launch name, arguments)
+        self.gap_info = {}  # pool launch -> layer, input, output, parameters
         self.tunables = []  # (launch name, desc, tile codes, fn(stream))
         self.outputs_f32 = {}
         self.cuda_graph = None
@@ -322,6 +331,7 @@ class DeviceExecutor:
                 self.tensors[name] = t
         self._plan_epilogues()
         self._fuse_input_quantization(cons)
+        self._fuse_pools(cons)
         for d, _, _, name in self.mfma_descs:
             if name in dict(self.launches):
                 self.tunables.append(
@@ -540,6 +550,44 @@ class DeviceExecutor:
                           if r <= d.OH]
             self.tunables.append((fused, d, rows, fn))
 
+    def _fuse_pools(self, cons):
+        """An int8 MFMA convolution (one group, table plan, no residual or
+        second output) whose output only feeds a global average pool runs
+        with the pool fused (``qa_d_conv_pool``): its output is never
+        written and the pool has no launch of its own."""
+        for gname, gi in list(self.gap_info.items()):
+            x, layer = gi["x"], gi["layer"]
+            xname = layer.data_inputs[0]
+            if xname in self.graph.outputs or \
+                    [l.name for l in cons.get(xname, [])] != [layer.name]:
+                continue
+            hits = [(d, ln) for d, _, _, ln in self.mfma_descs
+                    if d.y == x.ptr and ln in dict(self.launches)]
+            if len(hits) != 1:
+                continue
+            d, ln = hits[0]
+            if not (d.epi_plan and d.G == 1 and d.w_layout == 0 and
+                    not d.res and not d.y2 and d.y_code == 1 and
+                    self.tensors[xname].buf.data_ptr() == x.buf.data_ptr()):
+                continue
+            o, y = gi["out"], gi["y"]
+            pp = PoolParams()
+            pp.in_zp, pp.mult, pp.shift = layer.in_zp, gi["mult"], gi["shift"]
+            pp.zp, pp.qmin, pp.qmax = o.zp, o.qmin, o.qmax
+            pp.out, pp.out_sn, pp.out_so = y.ptr, y.sn, y.so
+            self.keep.append(pp)
+            fused = f"convpool:{ln[5:]}"
+
+            def fn(s, d=d, pp=pp):
+                _ok(self.lib.qa_d_conv_pool(ctypes.byref(d), ctypes.byref(pp),
+                                            s), "qa_d_conv_pool")
+
+            self.launches = [(fused, fn) if n == ln else (n, f)
+                             for n, f in self.launches if n != gname]
+            codes = [0, 0x10001] + ([0x10002] if d.Cout > 64 else [])
+            self.tunables.append((fused, d, codes, fn))
+            self.tensors.pop(xname, None)  # never materialized
+
     # ------------------------------------------------------- element-wise --
     def _plan_lut(self, layer, ins):
         x = ins[0]
@@ -648,6 +696,9 @@ class DeviceExecutor:
         mult, shift = layer.multiplier(area)
         o = layer.out_qp[0]
         y = self._new((n, ch), o)
+        self.gap_info[f"gap:{layer.name}"] = dict(layer=layer, x=x, y=y,
+                                                  mult=mult, shift=shift,
+                                                  out=o)
         self._add(f"gap:{layer.name}", lambda s: _ok(self.lib.qa_d_gap(
             x.ptr, x.code, x.sn, x.sc, x.sp, n, ch, area, layer.in_zp, x.so,
             mult, shift, o.zp, o.qmin, o.qmax, y.ptr, y.code, y.sn, y.so, s),

@@ -64,6 +64,7 @@ def _declare(lib):
         "qa_pack_weights_i8": (i32, [p] + [i64] * 7 + [p, p, p, p]),
         "qa_d_conv": (i32, [p, p]),
         "qa_d_quantize_conv": (i32, [p, p, f64, i64, i64, i64, p]),
+        "qa_d_conv_pool": (i32, [p, p, p]),
         "qa_epi_plan_bytes": (i64, [i64]),
         "qa_plan_epilogue_i8": (i32, [p, p]),
         "qa_d_requantize": (i32, [p, i32, p, i32] + [i64] * 3 + [p] * 4

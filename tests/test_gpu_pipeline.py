@@ -88,6 +88,9 @@ def test_every_conv_tile_is_bit_exact(hip, tmp_path, model, quant_type):
     ex = c.executor({"images": x.shape})
     assert any(n.startswith("qconv:") for n, _ in ex.launches), \
         "input quantization not fused into the stem"
+    assert any(n.startswith("convpool:") for n, _ in ex.launches) and \
+        not any(n.startswith("gap:") for n, _ in ex.launches), \
+        "pool not fused into the last convolution"
     descs = [t[1] for t in ex.tunables]
     assert len(descs) == len(ex.mfma_descs)
     cands = [t[2] for t in ex.tunables]
