@@ -25,6 +25,8 @@
 //   Q8_GENERAL the 128-bit form for any parameters.
 #pragma once
 
+#include <type_traits>
+
 #include "qa_conv.h"
 
 namespace qa {
@@ -126,6 +128,15 @@ struct KTap {
     int dy, dx;
     int64_t off;
       int nreal;  // real bytes: layout 0 of the 16, layout 1 of each word
+};
+
+// Tap table entry of k-group kg (layout 0), built in LDS by each
+// work-group: the K loop reads one entry a step instead of decoding the
+// tap with divisions.
+struct KTabE {
+    int64_t off;   // byte offset from the receptive-field origin
+    int32_t dydx;  // dy | dx << 16
+    int32_t nreal;
 };
 
 template <int LAYOUT>
@@ -357,11 +368,23 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
     v4i af[AS][WM], bf[D];
     int pd[D];  // pad flags of the slot's activation fragment
     int nr[D];  // real bytes of the slot's activation fragment (row sums)
-    auto fetch = [&](v4i* fa, v4i& fb, int& pds, int& nrs)
+    // layout 0: the work-group's tap table (after its ALDS weights)
+    KTabE* s_kt = (KTabE*)(s_w + (ALDS ? WM * 16 * (a.KGp + 1) : 0));
+    // tab: the table is ready (after the first barrier)
+    auto fetch = [&](auto tab, v4i* fa, v4i& fb, int& pds, int& nrs)
                      __attribute__((always_inline)) {
         const int step = st0 + fi * KSTRIDE;
         if (ftile < ntiles && step < KS) {
-            const KTap t = ktap<LAYOUT>(a, 4 * step + kgl);
+            KTap t;
+            if (decltype(tab)::value && LAYOUT == 0) {
+                const KTabE e = s_kt[4 * step + kgl];
+                t.off = e.off;
+                t.dy = e.dydx & 0xffff;
+                t.dx = e.dydx >> 16;
+                t.nreal = e.nreal;
+            } else {
+                t = ktap<LAYOUT>(a, 4 * step + kgl);
+            }
             if (!ALDS) {
 #pragma unroll
                 for (int i = 0; i < WM; ++i)
@@ -467,7 +490,17 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
     if (has_tile) {
 #pragma unroll
         for (int s = 0; s < D; ++s)
-            fetch(af[ALDS ? 0 : s], bf[s], pd[s], nr[s]);
+            fetch(std::false_type(), af[ALDS ? 0 : s], bf[s], pd[s], nr[s]);
+    }
+    if (LAYOUT == 0) {  // the tap table, read after the barrier
+        for (int kg = threadIdx.x; kg < a.KGp; kg += 256) {
+            const KTap t = ktap<0>(a, kg);
+            KTabE e;
+            e.off = t.off;
+            e.dydx = t.dy | (t.dx << 16);
+            e.nreal = t.nreal;
+            s_kt[kg] = e;
+        }
     }
     if (ALDS) {
 #pragma unroll
@@ -659,7 +692,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
                     psum += LAYOUT == 0 ? bytes_sum(b, nr[s])
                                         : bytes_sum_l1(b, nr[s], a.KW);
             }
-            fetch(af[ALDS ? 0 : s], bf[s], pd[s], nr[s]);
+            fetch(std::true_type(), af[ALDS ? 0 : s], bf[s], pd[s], nr[s]);
             if (++ci == L) {
                 ci = 0;
                 finish_tile();
@@ -722,7 +755,8 @@ bool launch_kernel(const ConvArgs& a0, hipStream_t st) {
             static_lds = (int64_t)fa.sharedSizeBytes;
         resident = nbk;
     }
-    const size_t dyn = ALDS ? (size_t)alds_bytes(WM, a0.KGp) : 0;
+    const size_t dyn = (ALDS ? (size_t)alds_bytes(WM, a0.KGp) : 0) +
+                       (LAYOUT == 0 ? (size_t)a0.KGp * sizeof(KTabE) : 0);
     int res_blocks = resident;
     if (dyn) {  // LDS limit with the staged weights
         const int64_t by_lds = lds_per_cu() / (static_lds + (int64_t)dyn);

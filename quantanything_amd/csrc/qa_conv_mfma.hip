@@ -17,7 +17,9 @@ bool mfma_launch_lds(const ConvArgs& b, int wm, bool split, int epi,
 bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     if (a.M <= 0 || a.Cog <= 0 || a.G <= 0) return true;
     if (a.M >= ((int64_t)1 << 31) || a.KGp < 4 || (a.KGp & 3) ||
-        a.KGp >= (1 << 16) || a.CB < 1 || a.KW < 1) {
+        a.KGp >= (1 << 16) || a.CB < 1 || a.KW < 1 ||
+        (int64_t)(a.KH - 1) * a.DH >= 32768 ||
+        (int64_t)(a.KW - 1) * a.DW >= 32768) {
         set_error("launch_conv_mfma", "unsupported problem size");
         return false;
     }
@@ -70,7 +72,8 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
         return 65536 - 3072 - 64 - (split ? 3 * (w * 4 + 1) * 256 : 0);
     };
     auto fits = [&](int w) {
-        return alds_bytes(w, a.KGp) <= lds_limit(w) &&
+        return alds_bytes(w, a.KGp) + (a.layout == 0 ? a.KGp * 16 : 0) <=
+                   lds_limit(w) &&
                (int64_t)w * 16 * a.KGp <= ALDS_CHUNKS;
     };
     bool alds = fits(wm);
