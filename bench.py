@@ -268,10 +268,22 @@ def main():
 
     kernels = []
     for wl in (GemmWorkload(), ConvWorkload()):
+        code = 0
+        if not args.no_tune:  # the same plan-time tile timing as the pass
+            from quantanything_amd.executor import DeviceExecutor
+
+            wl.launch()
+            times = {}
+            for c_ in DeviceExecutor.tile_candidates(wl.d):
+                wl.d.tile = c_
+                times[c_] = DeviceExecutor._time_launch(wl.launch, 8, 3)
+            code = min(times, key=times.get)
+            wl.d.tile = code
         kms = time_launch(wl.launch, 50, torch)
         r = roofline(wl.ops, wl.bytes, kms)
         tops = wl.ops / (kms * 1e-3) / 1e12
-        kernels.append({"workload": wl.name, "avg_ms": round(kms, 5),
+        kernels.append({"workload": wl.name, "tile": hex(code),
+                        "avg_ms": round(kms, 5),
                         "int8_tops": round(tops, 2),
                         "frac_of_mfma_peak": round(tops / PEAK_I8_TOPS, 4),
                         "roofline": r})

@@ -47,3 +47,19 @@ def test_fused_workloads_repeat_identically(hip):
     for _ in range(3):
         w.launch()
     np.testing.assert_array_equal(a, w.output())
+
+
+@pytest.mark.parametrize("which", ["gemm", "conv"])
+def test_workloads_match_reference_for_every_tile(hip, golden_workloads,
+                                                  which):
+    """Every tile code the executor may pick gives the reference's output."""
+    from quantanything_amd.executor import DeviceExecutor
+    from quantanything_amd.workloads import ConvWorkload, GemmWorkload
+
+    w = GemmWorkload() if which == "gemm" else ConvWorkload()
+    for code in DeviceExecutor.tile_candidates(w.d):
+        w.d.tile = code
+        w.y.fill_(0)
+        w.launch()
+        out = w.output().astype(np.int32)
+        assert sha(out) == golden_workloads[which]["out_sha256"], hex(code)
