@@ -67,6 +67,9 @@ struct ConvArgs {
     const void* w;
     int32_t w_code;                 // 2 int16, 4 int32
     int32_t wide;                   // int64 accumulation
+    // ---- double weights (FP64 MFMA path, qa_pack_weights_f64) ----
+    const double* wf;               // [G][wf_rows][KH*KW][CK]
+    int32_t CK, wf_rows;            // Cg rounded up to 32, Cog to 64
     // ---- per output channel ----
     const int64_t* corr;
     const int32_t* boff;
@@ -165,6 +168,8 @@ bool mfma_launch_lds(const ConvArgs& b, int wm, bool split, int epi,
 bool mfma_launch_l2(const ConvArgs& b, int wm, bool split, int epi,
                     hipStream_t st);
 bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
+// 16-bit operands on the FP64 matrix cores (qa_conv_f64.hip), exact.
+bool launch_conv_f64(const ConvArgs& a, hipStream_t st);
 
 // Input quantization fused into a layout-1 convolution (qa_conv_qin.hip):
 // float32 NCHW graph input, quantized exactly like qa_d_quantize_nhwc.

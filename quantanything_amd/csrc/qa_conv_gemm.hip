@@ -525,10 +525,45 @@ QA_API int qa_pack_weights_i8(const int32_t* w, int64_t Cout, int64_t Cg,
                         boff, needs_rowsum);
 }
 
+QA_API int64_t qa_pack_weights_f64_size(int64_t Cout, int64_t Cg, int64_t KH,
+                                        int64_t KW, int64_t G, int64_t* ck,
+                                        int64_t* rows_per_group) {
+    if (G <= 0 || Cout < 0 || Cout % G || Cg < 0 || KH < 0 || KW < 0)
+        return -1;
+    const int64_t CK = round_up(std::max<int64_t>(Cg, 1), 32);
+    const int64_t rows = round_up(std::max<int64_t>(Cout / G, 1), 64);
+    if (ck) *ck = CK;
+    if (rows_per_group) *rows_per_group = rows;
+    return G * rows * KH * KW * CK;
+}
+
+QA_API int qa_pack_weights_f64(const int32_t* w, int64_t Cout, int64_t Cg,
+                               int64_t KH, int64_t KW, int64_t G, double* wf) {
+    int64_t CK, rows;
+    const int64_t n =
+        qa_pack_weights_f64_size(Cout, Cg, KH, KW, G, &CK, &rows);
+    if (n < 0 || !wf || (!w && Cout * Cg * KH * KW > 0)) return -1;
+    if (KH * KW * CK >= ((int64_t)1 << 19)) return 1;
+    const int64_t Cog = Cout / G, taps = KH * KW;
+    std::fill(wf, wf + n, 0.0);
+    for (int64_t co = 0; co < Cout; ++co) {
+        const int64_t g = co / Cog, r = co % Cog;
+        double* dst = wf + (g * rows + r) * taps * CK;
+        for (int64_t c = 0; c < Cg; ++c)
+            for (int64_t t = 0; t < taps; ++t) {
+                const int32_t v = w[(co * Cg + c) * taps + t];
+                if (v <= -(1 << 17) || v >= (1 << 17)) return 1;
+                dst[t * CK + c] = (double)v;
+            }
+    }
+    return 0;
+}
+
 namespace {
 
 // Kernel arguments of a device descriptor: 1 for the int8 MFMA path, 0 for
-// the VALU path, 2 for an empty problem, -1 on error (recorded for `who`).
+// the VALU path, 3 for the FP64 MFMA path, 2 for an empty problem, -1 on
+// error (recorded for `who`).
 int desc_args(const qa_conv_desc* d, ConvArgs& a, const char* who) {
     if (!d) return -1;
     if (!conv_shape_ok(d->N, d->C, d->H, d->W, d->Cout, d->KH, d->KW, d->SH,
@@ -623,6 +658,23 @@ int desc_args(const qa_conv_desc* d, ConvArgs& a, const char* who) {
         a.tile_hint = (int32_t)d->tile;
         return 1;
     }
+    if (d->w_code == 8) {
+        int64_t CK, rows;
+        qa_pack_weights_f64_size(d->Cout, d->C / d->G, d->KH, d->KW, d->G,
+                                 &CK, &rows);
+        if (d->x_code != 2 || d->x_sc != 1 || d->x_add < -65536 ||
+            d->x_add > 65536 || d->w_kgp != CK || d->w_rows != rows ||
+            d->KH * d->KW * CK >= ((int64_t)1 << 19)) {
+            set_error(who, "FP64 MFMA path: operands do not match");
+            return -1;
+        }
+        a.wf = (const double*)d->w;
+        a.CK = (int32_t)CK;
+        a.wf_rows = (int32_t)rows;
+        a.wide = (int32_t)d->wide;
+        a.tile_hint = (int32_t)d->tile;
+        return 3;
+    }
     a.w = d->w;
     a.w_code = (int32_t)d->w_code;
     a.wide = (int32_t)d->wide;
@@ -638,6 +690,7 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
     if (r < 0) return -1;
     if (r == 2) return 0;
     if (r == 1) return launch_conv_mfma(a, st) ? 0 : -1;
+    if (r == 3) return launch_conv_f64(a, st) ? 0 : -1;
     return launch_conv_valu(a, st) ? 0 : -1;
 }
 

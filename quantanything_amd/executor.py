@@ -371,6 +371,12 @@ class DeviceExecutor:
         return off_bytes % 16 == 0 and x.sn % 16 == 0 and \
             (pix == 1 or x.sp % 16 == 0) and (groups == 1 or cg % 16 == 0)
 
+    @staticmethod
+    def _f64_ok(x, a_off):
+        """16-bit activations the FP64 matrix-core path takes: channels
+        contiguous, centred values within 2^17."""
+        return x.code == 2 and x.sc == 1 and -65536 <= a_off <= 65536
+
     def _weights_dev(self, layer, x, layout, use_mfma):
         p = self._params(layer)
         a_off = x.so - layer.in_zp
@@ -405,6 +411,16 @@ class DeviceExecutor:
                             corr=_dev(corr, np.int64),
                             boff=_dev(boff, np.int32), rowsum=need.value,
                             wide=0)
+        if info is None and self._f64_ok(x, a_off):
+            ck, rows = _I64(0), _I64(0)
+            size = self.lib.qa_pack_weights_f64_size(
+                cout, cg, kh, kw, groups, ctypes.byref(ck), ctypes.byref(rows))
+            wf = np.empty(size, np.float64)
+            if self.lib.qa_pack_weights_f64(w32.ctypes.data, cout, cg, kh,
+                                            kw, groups, wf.ctypes.data) == 0:
+                info = dict(w=_dev(wf, np.float64), w_code=8, layout=0,
+                            kgp=ck.value, rows=rows.value, corr=None,
+                            boff=None, rowsum=0, wide=1)
         if info is None:  # exact VALU path, int64 accumulation
             info = dict(w=_dev(w32, np.int32), w_code=4, layout=0, kgp=0,
                         rows=0, corr=None, boff=None, rowsum=0, wide=1)

@@ -151,6 +151,67 @@ def test_input_quantization_fused_into_stem(hip, tmp_path, quant_type, cin,
                     err_msg=f"{name}, band code {code:#x}")
 
 
+def _conv_graph(cin, cout, k, stride, pad, dil, groups, size):
+    b = G.GraphBuilder(11)
+    y = b.silu(b.conv("images", cin, cout, k, stride, pad=pad, groups=groups,
+                      dilation=dil))
+    y = b.op("Flatten", [b.op("GlobalAveragePool", [y])], axis=1)
+    return b.build("images", [None, cin, size, size], y)
+
+
+@pytest.mark.parametrize("cin,cout,k,stride,pad,dil,groups,size", [
+    (3, 16, 3, 2, 1, 1, 1, 32),    # the stem: 3 of 4 stored channels
+    (16, 24, 3, 1, 1, 1, 1, 17),   # a partial 16-channel block
+    (20, 40, 1, 1, 0, 1, 1, 12),   # 20 channels: one per lane and chunk
+    (48, 32, 3, 2, 2, 2, 1, 19),   # dilation 2, stride 2, 4 per lane
+    (64, 80, 3, 1, 1, 1, 1, 14),   # 8 channels per lane and chunk
+    (32, 64, 3, 1, 1, 1, 2, 10),   # two groups
+    (24, 24, 3, 1, 1, 1, 24, 9),   # depthwise
+])
+def test_int16_conv_on_fp64_matrix_cores(hip, tmp_path, cin, cout, k, stride,
+                                         pad, dil, groups, size):
+    """16-bit convolutions run on the FP64 MFMA path (w_code 8) and every
+    tensor equals the oracle's int64-accumulated one."""
+    from quantanything_amd.executor import ConvDesc
+
+    g = _conv_graph(cin, cout, k, stride, pad, dil, groups, size)
+    calib = [Stream(60 + i).uniform((3, cin, size, size), -1.0, 1.0)
+             .astype(np.float32) for i in range(2)]
+    c = _calibrated(g, "int16", True, calib)
+    x = Stream(70).uniform((3, cin, size, size), -1.3, 1.3).astype(np.float32)
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    oracle.run(x, keep=True)
+    ex = c.executor({"images": x.shape})
+    assert [d.w_code for d in ex.keep if isinstance(d, ConvDesc)] == [8]
+    ex.run({"images": x})
+    checked = 0
+    for name, t in ex.tensors.items():
+        if name in oracle.env:
+            got = t.to_host()
+            np.testing.assert_array_equal(
+                got, oracle.env[name].reshape(got.shape), err_msg=name)
+            checked += 1
+    assert checked >= 2
+
+
+def test_yolov8n_cls_int16_bit_exact(hip, tmp_path):
+    """The 16-bit YOLOv8n-cls pass (every conv and the head GEMM on the FP64
+    matrix cores) equals the oracle's int64 pass."""
+    from quantanything_amd.executor import ConvDesc
+
+    g = G.yolov8n_cls(seed=3, softmax=False)
+    calib = [Stream(40 + i).normal((2, 3, 224, 224)).astype(np.float32)
+             for i in range(2)]
+    c = _calibrated(g, "int16", True, calib)
+    x = Stream(52).normal((2, 3, 224, 224)).astype(np.float32)
+    ex = c.executor({"images": x.shape})
+    codes = [d.w_code for d in ex.keep if isinstance(d, ConvDesc)]
+    assert len(codes) > 20 and set(codes) == {8}
+    got = c.integer_outputs(x)[g.outputs[0]]
+    ints, _ = OraclePipeline(g, _qjson(c, tmp_path)).run(x)
+    np.testing.assert_array_equal(got, ints[g.outputs[0]])
+
+
 def test_tuned_tiles_keep_results(hip):
     g = G.mini_yolo(seed=0)
     calib = [_images(1 + i, 4, 32) for i in range(3)]
