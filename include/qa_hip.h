@@ -128,18 +128,20 @@ int qa_pack_weights_i8(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
                        int8_t* wp, int64_t* corr, int32_t* boff,
                        int32_t* needs_rowsum);
 
-/* Packs centred OIHW weights (w - w_zp, int32) as doubles for the FP64
- * matrix-core path of 16-bit models: wf[g][r][tap][c] with rows r padded to
- * a multiple of 64 per group and input channels c padded to a multiple of
- * 32 (*ck), zero-filled. Returns 0 on success, 1 when some |w| >= 2^17 or
- * KH*KW*ck >= 2^19 (the sums would no longer be exact in double: use the
- * VALU path), -1 on bad arguments. The size function returns the number of
- * doubles of wf. */
+/* Packs centred OIHW weights (w - w_zp, int32) for the FP64 matrix-core
+ * path of 16-bit models: elements of elem_bytes (2: int16, 4: int32) at
+ * wp[g][r][tap][c], rows r padded to a multiple of 64 per group and input
+ * channels c padded to a multiple of 32 (*ck), zero-filled; the kernel
+ * converts them to double. Returns 0 on success, 1 when a value does not fit
+ * the element (int16), |w| >= 2^17 or KH*KW*ck >= 2^19 (the sums would no
+ * longer be exact in double: use the VALU path), -1 on bad arguments. The
+ * size function returns the number of elements of wp. */
 int64_t qa_pack_weights_f64_size(int64_t Cout, int64_t Cg, int64_t KH,
                                  int64_t KW, int64_t G, int64_t* ck,
                                  int64_t* rows_per_group);
 int qa_pack_weights_f64(const int32_t* w, int64_t Cout, int64_t Cg,
-                        int64_t KH, int64_t KW, int64_t G, double* wf);
+                        int64_t KH, int64_t KW, int64_t G, int64_t elem_bytes,
+                        void* wp);
 
 /* Fused integer convolution / GEMM on device tensors:
  *   acc = sum (x_stored + x_add) * w         (exact)
@@ -154,9 +156,10 @@ int qa_pack_weights_f64(const int32_t* w, int64_t Cout, int64_t Cg,
  * w_code 1: weights from qa_pack_weights_i8 (int8 MFMA; needs int8 input
  * with x_sc == 1 and 16-byte aligned channel groups, 4-byte for layout 1);
  * w_code 2/4: OIHW int16/int32 weights (VALU; int64 accumulation when wide);
- * w_code 8: weights from qa_pack_weights_f64 (w_kgp = ck, w_rows = rows per
- * group; FP64 matrix cores, exact; needs int16 input with x_sc == 1 and
- * |x_add| <= 2^16; the sum wraps to int32 unless wide).
+ * w_code 8: weights from qa_pack_weights_f64 (w_layout = their element
+ * bytes, w_kgp = ck, w_rows = rows per group; FP64 matrix cores, exact;
+ * needs int16 input with x_sc == 1 and |x_add| <= 2^16; the sum wraps to
+ * int32 unless wide).
  * A GEMM is the case H = W = KH = KW = 1 with row m as image m. */
 typedef struct qa_conv_desc {
     const void* x;
@@ -188,7 +191,10 @@ typedef struct qa_conv_desc {
                       groups per tile (1, 2, 4, 8), split = the 4 waves of a
                       work-group split K, lds = weights staged in LDS (a
                       caller's measured choice; ignored where it does not
-                      apply). Results do not depend on it. */
+                      apply). FP64 path (w_code 8): 0x10000 | wm | tm << 4
+                      | split << 8 with (wm, tm, split) one of (1,1,0),
+                      (2,1,0), (1,4,0), (1,1,1), (2,1,1), (4,1,1); tm =
+                      16-pixel tiles per wave. Results do not depend on it. */
 } qa_conv_desc;
 
 /* Host-side planner of the int8 table epilogue of qa_d_conv. From the

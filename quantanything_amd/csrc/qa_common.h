@@ -39,15 +39,33 @@ __host__ __device__ __forceinline__ qa_i128 qa_mbqm(int64_t x, int64_t mult,
 // the 128-bit form otherwise. Bit-identical to qa_mbqm for all inputs:
 // floor((p + 2^(t-1)) / 2^t) == (p >> t) + bit (t-1) of p, with no overflow,
 // and for t >= 64 the rounded value of |p| < 2^63 is 0.
-__device__ __forceinline__ qa_i128 qa_mbqm_fast(int64_t x, int64_t mult,
-                                               int64_t shift) {
+//
+// A second path covers |x| < 2^62 with |mult| < 2^31 and 1 <= 31+shift <=
+// 94 (16-bit-model accumulators): the product is formed from two 32x32-bit
+// products, x*m = (x_hi*m) * 2^32 + x_lo*m with x_lo = x mod 2^32 unsigned,
+// each exact in int64, instead of a full 128-bit multiply.
+__host__ __device__ __forceinline__ qa_i128 qa_mbqm_fast(int64_t x,
+                                                        int64_t mult,
+                                                        int64_t shift) {
     const uint64_t ax = x < 0 ? 0ull - (uint64_t)x : (uint64_t)x;
     const uint64_t am = mult < 0 ? 0ull - (uint64_t)mult : (uint64_t)mult;
     const int64_t ts = 31 + shift;
-    if ((ax >> 32) == 0 && (am >> 31) == 0 && ts > 0) {
-        if (ts >= 64) return 0;
-        const int64_t p = x * mult;
-        return (qa_i128)((p >> ts) + ((p >> (ts - 1)) & 1));
+    if ((am >> 31) == 0 && ts > 0) {
+        if ((ax >> 32) == 0) {
+            if (ts >= 64) return 0;
+            const int64_t p = x * mult;
+            return (qa_i128)((p >> ts) + ((p >> (ts - 1)) & 1));
+        }
+        if ((ax >> 62) == 0 && ts <= 94) {
+            const int32_t m = (int32_t)mult;
+            const int64_t p_hi = (x >> 32) * (int64_t)m;  // |.| < 2^61
+            const uint32_t xl = (uint32_t)x;
+            // xl * m as a signed 64-bit value (|.| < 2^63)
+            uint64_t u = (uint64_t)xl * (uint64_t)(uint32_t)m;
+            if (m < 0) u -= (uint64_t)xl << 32;
+            const qa_i128 p = ((qa_i128)p_hi << 32) + (qa_i128)(int64_t)u;
+            return (p + ((qa_i128)1 << (ts - 1))) >> ts;
+        }
     }
     return qa_mbqm(x, mult, shift);
 }

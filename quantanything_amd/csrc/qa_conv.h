@@ -54,8 +54,9 @@ struct ConvArgs {
     int32_t CB, KG, KGp, Kreal;
     uint64_t mg_cb, mg_kw;          // ceil(2^32 / CB), ceil(2^32 / KW)
     int32_t st_dn, st_doy, st_dox;  // a wave's pixel stride as (n, oy, ox)
-    int32_t fastio;                 // y (res, y2): dense channels-last, 4-byte
-                                    // aligned 4-channel words
+    int32_t fastio;                 // y (res, y2): dense channels-last (the
+                                    // int8 path: in 4-byte aligned 4-channel
+                                    // words)
     int64_t y_pst, res_pst, y2_pst; // their pixel strides when fastio
     int32_t tile_hint;              // 0, or TILE_VALID | wm | split << 8 |
                                     // lds << 9 (MFMA tile choice)
@@ -67,9 +68,10 @@ struct ConvArgs {
     const void* w;
     int32_t w_code;                 // 2 int16, 4 int32
     int32_t wide;                   // int64 accumulation
-    // ---- double weights (FP64 MFMA path, qa_pack_weights_f64) ----
-    const double* wf;               // [G][wf_rows][KH*KW][CK]
+    // ---- FP64 MFMA path weights (qa_pack_weights_f64) ----
+    const void* wf;                 // [G][wf_rows][KH*KW][CK] int16 / int32
     int32_t CK, wf_rows;            // Cg rounded up to 32, Cog to 64
+    int32_t wf_bytes;               // element size, 2 or 4
     // ---- per output channel ----
     const int64_t* corr;
     const int32_t* boff;

@@ -9,15 +9,20 @@
 // exact integer sum, converted back to int64 for the 128-bit requantization
 // epilogue. Results are identical to the int64 VALU form.
 //
-// A wave owns 16 output pixels (batch folded in; rows of the MFMA) x WM*16
-// output channels (columns). K runs over the taps and, per tap, over chunks
-// of 4V input channels: lane (pixel col, group q) loads the V consecutive
-// channels 4V*cc + V*q .. + V-1 of its pixel as one vector, and MFMA j
-// (j < V) sums channels {4V*cc + V*q + j : q = 0..3}. Channels past Cg meet
-// zero weights (weights are packed as double rows [group][channel, padded
-// to 64][tap][Cg padded to 32], zero-filled) and are loaded as 0, so every
-// access stays inside the input. The MFMA's result register r of lane l is
-// output row 4r + l/16, column l%16.
+// A wave owns TM tiles of 16 output pixels (batch folded in; rows of the
+// MFMA) x WM*16 output channels (columns), so each weight fragment it loads
+// serves TM tiles and each activation fragment WM channel groups. K runs in
+// steps of one tap x 4V input channels: lane (pixel col, group q) loads the V
+// consecutive channels 4V*cc + V*q .. + V-1 of its pixel as one vector, and
+// MFMA j (j < V) sums channels {4V*cc + V*q + j : q = 0..3}. The fragments
+// of the next D steps are in flight while a step's MFMAs run. Channels past Cg
+// meet zero weights (weights are packed as double rows [group][channel,
+// padded to 64][tap][Cg padded to 32], zero-filled) and are loaded as 0, so
+// every access stays inside the input. With KSPLIT the 4 waves of a
+// work-group share their tiles and take every 4th K-step; the partial sums
+// are added through LDS and each wave finishes a quarter of the outputs.
+// The MFMA's result register r of lane l is output row 4r + l/16, column
+// l%16.
 #include "qa_conv_mfma.h"
 
 namespace qa {
@@ -25,196 +30,375 @@ namespace {
 
 typedef double v4d __attribute__((ext_vector_type(4)));
 
-template <int V>
-struct VecI16;
+// V consecutive int16 or int32 elements loaded as one fragment.
+template <int V, class E>
+struct Frag;
 template <>
-struct VecI16<1> {
+struct Frag<1, int16_t> {
     typedef int16_t T;
-    static __device__ __forceinline__ int get(T v, int) { return v; }
+    static __device__ __forceinline__ int get(const T& v, int) { return v; }
 };
 template <>
-struct VecI16<2> {
-    typedef int T;
-    static __device__ __forceinline__ int get(T v, int j) {
-        return (int)(int16_t)(v >> (16 * j));
-    }
-};
-template <>
-struct VecI16<4> {
+struct Frag<4, int16_t> {
     typedef int2 T;
-    static __device__ __forceinline__ int get(T v, int j) {
+    static __device__ __forceinline__ int get(const T& v, int j) {
         const int w = j < 2 ? v.x : v.y;
         return (int)(int16_t)(w >> (16 * (j & 1)));
     }
 };
 template <>
-struct VecI16<8> {
+struct Frag<8, int16_t> {
     typedef int4 T;
-    static __device__ __forceinline__ int get(T v, int j) {
+    static __device__ __forceinline__ int get(const T& v, int j) {
         const int w = j < 2 ? v.x : (j < 4 ? v.y : (j < 6 ? v.z : v.w));
         return (int)(int16_t)(w >> (16 * (j & 1)));
     }
 };
+template <>
+struct Frag<1, int32_t> {
+    typedef int T;
+    static __device__ __forceinline__ int get(const T& v, int) { return v; }
+};
+template <>
+struct Frag<4, int32_t> {
+    typedef int4 T;
+    static __device__ __forceinline__ int get(const T& v, int j) {
+        return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
+    }
+};
+struct I32x8 {
+    int4 lo, hi;
+};
+template <>
+struct Frag<8, int32_t> {
+    typedef I32x8 T;
+    static __device__ __forceinline__ int get(const T& v, int j) {
+        return Frag<4, int32_t>::get(j < 4 ? v.lo : v.hi, j & 3);
+    }
+};
 
-template <int WM, int V>
+// Position of a K-step: tap (ky, kx) and channel chunk cc.
+struct KPos {
+    int ky, kx, cc;
+};
+
+// Advances by `by` (1 or 4) steps; branch-free, so that the load counters
+// of the ring below stay countable.
+template <int BY>
+__device__ __forceinline__ void kpos_advance(const ConvArgs& a, int nck,
+                                             KPos& k) {
+    k.cc += BY;
+#pragma unroll
+    for (int r = 0; r < BY; ++r) {
+        const bool wrap = k.cc >= nck;
+        k.cc -= wrap ? nck : 0;
+        const bool row = wrap && k.kx + 1 == a.KW;
+        k.kx = row ? 0 : k.kx + (wrap ? 1 : 0);
+        k.ky += row ? 1 : 0;
+    }
+}
+
+// One output element of the exact sum `sum` (mode EPI_QUANT or raw).
+__device__ __forceinline__ void f64_store(const ConvArgs& a, int64_t co,
+                                          int64_t pp, int64_t sum,
+                                          int64_t pre, int64_t m, int64_t s) {
+    const int64_t v = a.wide ? sum : (int64_t)(int32_t)sum;
+    // element indices of y, the residual and the copy: pixel * pixel stride
+    // + channel when all are dense channels-last (fastio), else decoded
+    int64_t yi, ri, y2i;
+    if (a.fastio) {
+        yi = pp * a.y_pst + co;
+        ri = pp * a.res_pst + co;
+        y2i = pp * a.y2_pst + co;
+    } else {
+        const PixPos op = pix_decode(a, pp);
+        const int64_t pix = (int64_t)op.oy * a.OW + op.ox;
+        yi = (int64_t)op.n * a.y_sn + co * a.y_sc + pix * a.y_sp;
+        ri = (int64_t)op.n * a.res_sn + co * a.res_sc + pix * a.res_sp;
+        y2i = (int64_t)op.n * a.y2_sn + co * a.y2_sc + pix * a.y2_sp;
+    }
+    if (a.mode != EPI_QUANT) {
+        store_any(a.y, a.y_code, yi, v);
+        return;
+    }
+    int64_t rq = 0;
+    if (a.res) rq = load_any(a.res, a.y_code, ri) + a.res_so;
+    const int64_t q = quant_one(a, v + pre, m, s, rq);
+    store_any(a.y, a.y_code, yi, q - a.y_so);
+    if (a.y2) store_any(a.y2, a.y_code, y2i, rescale2(a, q) - a.y_so);
+}
+
+template <int WM, int TM, int V, bool KSPLIT, class WE>
 __global__ __launch_bounds__(256) void k_conv_f64(ConvArgs a) {
-    typedef typename VecI16<V>::T VT;
+    typedef Frag<V, int16_t> XF;
+    typedef Frag<V, WE> WF;
+    typedef typename XF::T VT;
+    typedef typename WF::T WT;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kgl = lane >> 4;
     const int g = blockIdx.z;
     const int co0 = blockIdx.y * WM * 16;
-    const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
-    if (tile * 16 >= a.M) return;
-    // this lane's fetch pixel (clamped into the tensor)
-    const int64_t p = min(tile * 16 + col, a.M - 1);
-    const PixPos pos = pix_decode(a, p);
+    const int64_t tile0 =
+        ((int64_t)blockIdx.x * (KSPLIT ? 1 : 4) + (KSPLIT ? 0 : wave)) * TM;
+    if (tile0 * 16 >= a.M) return;  // uniform per work-group with KSPLIT
     const int taps = a.KH * a.KW;
     const int nck = (a.Cg + 4 * V - 1) / (4 * V);
-    const int16_t* xn = (const int16_t*)a.x + (int64_t)pos.n * a.x_sn +
-                        (int64_t)g * a.Cg + V * kgl;
-    const double* wrow =
-        a.wf + ((int64_t)g * a.wf_rows + co0 + col) * taps * a.CK + V * kgl;
+    const int nsteps_all = taps * nck;
+    // this wave's K-steps: all, or every 4th from `wave`
+    const int kfirst = KSPLIT ? wave : 0;
+    const int nsteps =
+        KSPLIT ? (nsteps_all > wave ? (nsteps_all - wave + 3) / 4 : 0)
+               : nsteps_all;
+    // fetch side of the lane's TM pixels (clamped into the tensor)
+    const int16_t* xb[TM];
+    int iy0[TM], ix0[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        const int64_t p = min((tile0 + t) * 16 + col, a.M - 1);
+        const PixPos pos = pix_decode(a, p);
+        xb[t] = (const int16_t*)a.x + (int64_t)pos.n * a.x_sn +
+                (int64_t)g * a.Cg + V * kgl;
+        iy0[t] = pos.oy * a.SH - a.PH;
+        ix0[t] = pos.ox * a.SW - a.PW;
+    }
+    const WE* wrow = (const WE*)a.wf +
+                     ((int64_t)g * a.wf_rows + co0 + col) * taps * a.CK +
+                     V * kgl;
     const int64_t wblk = (int64_t)16 * taps * a.CK;  // the next 16 channels
     const double xadd = (double)a.x_add;
-    v4d acc[WM];
+
+    // a ring of D K-steps in flight: slot d holds the fragments of step
+    // n0 + d. Loads are issued for every lane (padding and channels past Cg
+    // read the image's first element, a valid address, and are masked at
+    // use), so the compiler can count them without branches.
+    constexpr int D = V == 1 ? 4 : 2;
+    VT xr[D][TM];
+    bool lr[D][TM];
+    WT wr[D][WM];
+    KPos kf;  // the next step to fetch
+    kf.ky = 0;
+    kf.kx = 0;
+    kf.cc = 0;
+    for (int r = 0; r < kfirst; ++r) kpos_advance<1>(a, nck, kf);
+    auto fetch = [&](VT (&xo)[TM], bool (&lo)[TM], WT (&bo)[WM]) {
+        const bool chan = 4 * V * kf.cc + V * kgl < a.Cg;
 #pragma unroll
-    for (int i = 0; i < WM; ++i) acc[i] = v4d{0.0, 0.0, 0.0, 0.0};
-    for (int ky = 0; ky < a.KH; ++ky) {
-        const int iy = pos.oy * a.SH - a.PH + ky * a.DH;
-        for (int kx = 0; kx < a.KW; ++kx) {
-            const int ix = pos.ox * a.SW - a.PW + kx * a.DW;
-            const bool in =
-                (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
-            const int16_t* px =
-                xn + (in ? ((int64_t)iy * a.W + ix) * a.x_sp : 0);
-            const double* wt = wrow + (int64_t)(ky * a.KW + kx) * a.CK;
-            for (int cc = 0; cc < nck; ++cc) {
-                // channels 4V*cc + V*kgl + j of the lane's pixel
-                const bool live = in && 4 * V * cc + V * kgl < a.Cg;
-                VT xv;
-                if (live)
-                    xv = *(const VT*)(px + 4 * V * cc);
-                double av[V];
+        for (int t = 0; t < TM; ++t) {
+            const int iy = iy0[t] + kf.ky * a.DH;
+            const int ix = ix0[t] + kf.kx * a.DW;
+            lo[t] = chan && (unsigned)iy < (unsigned)a.H &&
+                    (unsigned)ix < (unsigned)a.W;
+            const int64_t off =
+                lo[t] ? ((int64_t)iy * a.W + ix) * a.x_sp + 4 * V * kf.cc
+                      : -(int64_t)(V * kgl);
+            xo[t] = *(const VT*)(xb[t] + off);
+        }
+        // steps past the end (ky == KH onwards) read tap 0: in bounds
+        const int tap = kf.ky < a.KH ? kf.ky * a.KW + kf.kx : 0;
+        const WE* wt = wrow + (int64_t)tap * a.CK + 4 * V * kf.cc;
 #pragma unroll
-                for (int j = 0; j < V; ++j)
-                    av[j] = live ? (double)VecI16<V>::get(xv, j) + xadd : 0.0;
+        for (int i = 0; i < WM; ++i) bo[i] = *(const WT*)(wt + i * wblk);
+        kpos_advance<KSPLIT ? 4 : 1>(a, nck, kf);
+    };
+    v4d acc[TM][WM];
 #pragma unroll
-                for (int i = 0; i < WM; ++i) {
-                    const double* w = wt + i * wblk + 4 * V * cc;
-                    double bw[V];
-                    if (V == 1) {
-                        bw[0] = w[0];
-                    } else {
+    for (int t = 0; t < TM; ++t)
 #pragma unroll
-                        for (int j = 0; j < V; j += 2) {
-                            const double2 t = *(const double2*)(w + j);
-                            bw[j] = t.x;
-                            bw[j + 1] = t.y;
-                        }
-                    }
+        for (int i = 0; i < WM; ++i) acc[t][i] = v4d{0.0, 0.0, 0.0, 0.0};
+    auto compute = [&](const VT (&xv)[TM], const bool (&lv)[TM],
+                       const WT (&bw)[WM]) {
 #pragma unroll
-                    for (int j = 0; j < V; ++j)
-                        acc[i] = __builtin_amdgcn_mfma_f64_16x16x4f64(
-                            av[j], bw[j], acc[i], 0, 0, 0);
-                }
-            }
+        for (int t = 0; t < TM; ++t) {
+            double av[V];
+#pragma unroll
+            for (int j = 0; j < V; ++j)
+                av[j] = lv[t] ? (double)XF::get(xv[t], j) + xadd : 0.0;
+#pragma unroll
+            for (int j = 0; j < V; ++j)
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+                    acc[t][i] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+                        av[j], (double)WF::get(bw[i], j), acc[t][i], 0, 0,
+                        0);
+        }
+    };
+    // every fetch is issued (steps past the end read in-bounds addresses
+    // and are not used): no load sits behind a branch
+#pragma unroll
+    for (int d = 0; d < D; ++d) fetch(xr[d], lr[d], wr[d]);
+    for (int n0 = 0; n0 < nsteps; n0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (n0 + d < nsteps) compute(xr[d], lr[d], wr[d]);
+            fetch(xr[d], lr[d], wr[d]);
         }
     }
-    // epilogue: the exact sums of the lane's pixels 4r + kgl
+
+    if (KSPLIT) {
+        // partial sums through LDS; wave w finishes row register r = w
+        __shared__ double s_acc[4][WM][4][64];
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s_acc[wave][i][r][lane] = acc[0][i][r];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const double sum = s_acc[0][i][wave][lane] +
+                               s_acc[1][i][wave][lane] +
+                               s_acc[2][i][wave][lane] +
+                               s_acc[3][i][wave][lane];
+            const int c = co0 + i * 16 + col;
+            const int64_t pp = tile0 * 16 + 4 * wave + kgl;
+            if (c >= a.Cog || pp >= a.M) continue;
+            const int64_t co = (int64_t)g * a.Cog + c;
+            const bool q = a.mode == EPI_QUANT;
+            f64_store(a, co, pp, (int64_t)sum, a.pre ? a.pre[co] : 0,
+                      q ? a.mult[co] : 0, q ? a.shift[co] : 0);
+        }
+        return;
+    }
+    // the exact sums of the lane's pixels 4r + kgl of each tile
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
         const int c = co0 + i * 16 + col;
         if (c >= a.Cog) continue;
         const int64_t co = (int64_t)g * a.Cog + c;
+        const bool q = a.mode == EPI_QUANT;
         const int64_t pre = a.pre ? a.pre[co] : 0;
-        const int64_t m = a.mode == EPI_QUANT ? a.mult[co] : 0;
-        const int64_t s = a.mode == EPI_QUANT ? a.shift[co] : 0;
+        const int64_t m = q ? a.mult[co] : 0;
+        const int64_t s = q ? a.shift[co] : 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t pp = tile * 16 + 4 * r + kgl;
-            if (pp >= a.M) continue;
-            const int64_t sum = (int64_t)acc[i][r];
-            const int64_t v = a.wide ? sum : (int64_t)(int32_t)sum;
-            const PixPos op = pix_decode(a, pp);
-            const int64_t pix = (int64_t)op.oy * a.OW + op.ox;
-            const int64_t yi = (int64_t)op.n * a.y_sn + co * a.y_sc +
-                               pix * a.y_sp;
-            if (a.mode != EPI_QUANT) {
-                store_any(a.y, a.y_code, yi, v);
-                continue;
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t pp = (tile0 + t) * 16 + 4 * r + kgl;
+                if (pp < a.M)
+                    f64_store(a, co, pp, (int64_t)acc[t][i][r], pre, m, s);
             }
-            int64_t rq = 0;
-            if (a.res)
-                rq = load_any(a.res, a.y_code,
-                              (int64_t)op.n * a.res_sn + co * a.res_sc +
-                                  pix * a.res_sp) +
-                     a.res_so;
-            const int64_t q = quant_one(a, v + pre, m, s, rq);
-            store_any(a.y, a.y_code, yi, q - a.y_so);
-            if (a.y2)
-                store_any(a.y2, a.y_code,
-                          (int64_t)op.n * a.y2_sn + co * a.y2_sc +
-                              pix * a.y2_sp,
-                          rescale2(a, q) - a.y_so);
-        }
     }
 }
 
-template <int WM>
+template <int WM, int TM, bool KS, class WE>
 void launch_v(const ConvArgs& a, int v, dim3 grid, hipStream_t st) {
     switch (v) {
-        case 8: k_conv_f64<WM, 8><<<grid, 256, 0, st>>>(a); break;
-        case 4: k_conv_f64<WM, 4><<<grid, 256, 0, st>>>(a); break;
-        case 2: k_conv_f64<WM, 2><<<grid, 256, 0, st>>>(a); break;
-        default: k_conv_f64<WM, 1><<<grid, 256, 0, st>>>(a); break;
+        case 8: k_conv_f64<WM, TM, 8, KS, WE><<<grid, 256, 0, st>>>(a); break;
+        case 4: k_conv_f64<WM, TM, 4, KS, WE><<<grid, 256, 0, st>>>(a); break;
+        default:
+            k_conv_f64<WM, TM, 1, KS, WE><<<grid, 256, 0, st>>>(a);
+            break;
     }
 }
+
+template <int WM, int TM, bool KS>
+void launch_w(const ConvArgs& a, int v, dim3 grid, hipStream_t st) {
+    if (a.wf_bytes == 2)
+        launch_v<WM, TM, KS, int16_t>(a, v, grid, st);
+    else
+        launch_v<WM, TM, KS, int32_t>(a, v, grid, st);
+}
+
+struct F64Tile {
+    int wm, tm;
+    bool split;
+};
+
+// Tile code: wm | tm << 4 | split << 8 (also the low bits of a tile hint).
+constexpr int f64_code(const F64Tile& t) {
+    return t.wm | t.tm << 4 | (t.split ? 0x100 : 0);
+}
+
+constexpr F64Tile kF64Tiles[] = {
+    {1, 1, false}, {2, 1, false}, {1, 4, false},
+    {1, 1, true},  {2, 1, true},  {4, 1, true},
+};
 
 }  // namespace
 
 bool launch_conv_f64(const ConvArgs& a, hipStream_t st) {
     if (a.M <= 0 || a.Cog <= 0) return true;
-    if (a.x_code != 2 || a.x_sc != 1 || a.narrow16 || a.M >= ((int64_t)1 << 31) ||
-        a.CK != ((a.Cg + 31) & ~31) || a.wf_rows % 64 ||
-        a.wf_rows < a.Cog || a.x_add < -65536 || a.x_add > 65536 ||
+    if (a.x_code != 2 || a.x_sc != 1 || a.narrow16 || a.Cg < 1 ||
+        a.M >= ((int64_t)1 << 31) || a.CK != ((a.Cg + 31) & ~31) ||
+        a.wf_rows % 64 || a.wf_rows < a.Cog ||
+        (a.wf_bytes != 2 && a.wf_bytes != 4) || a.x_add < -65536 ||
+        a.x_add > 65536 ||
         (int64_t)a.KH * a.KW * a.CK >= ((int64_t)1 << 19) || a.G > 65535) {
         set_error("launch_conv_f64",
                   "needs int16 channels-last activations, weights packed by "
                   "qa_pack_weights_f64 and K below 2^19");
         return false;
     }
-    // channels per lane vector: the widest that divides the channel count,
-    // the strides and the address, without more K-padding than 4 channels
+    // channels per lane vector: 8 or 4 when they divide the channel count,
+    // the strides and the address without more K-padding than 4 channels
     const uintptr_t xa = (uintptr_t)a.x;
     const int64_t cg4 = (a.Cg + 3) & ~3;
     int v = 8;
     while (v > 1 &&
            (a.Cg % v || a.x_sn % v || a.x_sp % v || xa % (2 * v) ||
             ((a.Cg + 4 * v - 1) / (4 * v)) * 4 * v != cg4))
-        v >>= 1;
-    // channel block: as wide as keeps 4 waves per SIMD of every CU busy
-    const int64_t ntiles = ceil_div(a.M, 16);
-    const int64_t want = 16 * (int64_t)cu_count();
-    int wm = a.Cog <= 16 ? 1 : (a.Cog <= 32 ? 2 : 4);
-    if (a.tile_hint & TILE_VALID) {
-        const int h = a.tile_hint & 0xff;
-        if (h == 1 || h == 2 || h == 4) wm = h;
-    } else {
-        while (wm > 1 && ntiles * ceil_div(a.Cog, 16 * wm) * a.G < want)
-            wm >>= 1;
+        v = v == 8 ? 4 : 1;
+    ConvArgs b = a;
+    {
+        // dense channels-last y (residual, copy): element of pixel p and
+        // channel c at p * pixel stride + c (a GEMM row is one pixel)
+        const int64_t ohw = (int64_t)a.OH * a.OW;
+        auto pst = [&](int64_t sn, int64_t sp) { return ohw == 1 ? sn : sp; };
+        auto dense = [&](const void* p, int64_t sn, int64_t sc, int64_t sp) {
+            return p == nullptr || (sc == 1 && (ohw == 1 || sn == ohw * sp));
+        };
+        b.fastio = dense(a.y, a.y_sn, a.y_sc, a.y_sp) &&
+                   dense(a.res, a.res_sn, a.res_sc, a.res_sp) &&
+                   dense(a.y2, a.y2_sn, a.y2_sc, a.y2_sp);
+        b.y_pst = pst(a.y_sn, a.y_sp);
+        b.res_pst = pst(a.res_sn, a.res_sp);
+        b.y2_pst = pst(a.y2_sn, a.y2_sp);
     }
-    const int64_t gx = ceil_div(ntiles, 4);
-    const int64_t gy = ceil_div(a.Cog, 16 * wm);
+    const int64_t ntiles = ceil_div(a.M, 16);
+    auto waves = [&](const F64Tile& t) {
+        return ceil_div(ntiles, t.tm) * ceil_div(a.Cog, 16 * t.wm) * a.G *
+               (t.split ? 4 : 1);
+    };
+    // tile: a caller's choice, else the first of these that gives every CU
+    // 48 waves (a 64-cycle MFMA per wave needs many waves in flight to
+    // cover the fragment loads), else K split over single channel groups
+    F64Tile tile = {1, 1, true};
+    bool chosen = false;
+    if (a.tile_hint & TILE_VALID) {
+        for (const F64Tile& t : kF64Tiles)
+            if (f64_code(t) == (a.tile_hint & 0xffff)) {
+                tile = t;
+                chosen = true;
+            }
+    }
+    if (!chosen) {
+        const F64Tile order[] = {
+            {2, 1, false}, {1, 1, false}, {2, 1, true}, {1, 1, true}};
+        const int64_t want = 48 * (int64_t)cu_count();
+        for (const F64Tile& t : order)
+            if ((t.wm == 1 || a.Cog > 16) && waves(t) >= want) {
+                tile = t;
+                break;
+            }
+    }
+    const int64_t gx = tile.split ? ceil_div(ntiles, tile.tm)
+                                  : ceil_div(ntiles, 4 * tile.tm);
+    const int64_t gy = ceil_div(a.Cog, 16 * tile.wm);
     if (gx >= ((int64_t)1 << 31) || gy > 65535) {
         set_error("launch_conv_f64", "grid too large");
         return false;
     }
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)a.G);
-    switch (wm) {
-        case 1: launch_v<1>(a, v, grid, st); break;
-        case 2: launch_v<2>(a, v, grid, st); break;
-        default: launch_v<4>(a, v, grid, st); break;
+    switch (f64_code(tile)) {
+        case 0x11: launch_w<1, 1, false>(b, v, grid, st); break;
+        case 0x12: launch_w<2, 1, false>(b, v, grid, st); break;
+        case 0x41: launch_w<1, 4, false>(b, v, grid, st); break;
+        case 0x111: launch_w<1, 1, true>(b, v, grid, st); break;
+        case 0x112: launch_w<2, 1, true>(b, v, grid, st); break;
+        case 0x114: launch_w<4, 1, true>(b, v, grid, st); break;
+        default:
+            set_error("launch_conv_f64", "no kernel for this tile");
+            return false;
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

@@ -538,22 +538,31 @@ QA_API int64_t qa_pack_weights_f64_size(int64_t Cout, int64_t Cg, int64_t KH,
 }
 
 QA_API int qa_pack_weights_f64(const int32_t* w, int64_t Cout, int64_t Cg,
-                               int64_t KH, int64_t KW, int64_t G, double* wf) {
+                               int64_t KH, int64_t KW, int64_t G,
+                               int64_t elem_bytes, void* wp) {
     int64_t CK, rows;
     const int64_t n =
         qa_pack_weights_f64_size(Cout, Cg, KH, KW, G, &CK, &rows);
-    if (n < 0 || !wf || (!w && Cout * Cg * KH * KW > 0)) return -1;
+    if (n < 0 || !wp || (elem_bytes != 2 && elem_bytes != 4) ||
+        (!w && Cout * Cg * KH * KW > 0))
+        return -1;
     if (KH * KW * CK >= ((int64_t)1 << 19)) return 1;
+    const int64_t lim = elem_bytes == 2 ? 32768 : (1 << 17);
+    const int64_t K = Cg * KH * KW;
+    for (int64_t i = 0; i < Cout * K; ++i)
+        if (w[i] < -lim || w[i] >= lim) return 1;
     const int64_t Cog = Cout / G, taps = KH * KW;
-    std::fill(wf, wf + n, 0.0);
+    memset(wp, 0, (size_t)(n * elem_bytes));
     for (int64_t co = 0; co < Cout; ++co) {
         const int64_t g = co / Cog, r = co % Cog;
-        double* dst = wf + (g * rows + r) * taps * CK;
+        const int64_t row = (g * rows + r) * taps * CK;
         for (int64_t c = 0; c < Cg; ++c)
             for (int64_t t = 0; t < taps; ++t) {
                 const int32_t v = w[(co * Cg + c) * taps + t];
-                if (v <= -(1 << 17) || v >= (1 << 17)) return 1;
-                dst[t * CK + c] = (double)v;
+                if (elem_bytes == 2)
+                    ((int16_t*)wp)[row + t * CK + c] = (int16_t)v;
+                else
+                    ((int32_t*)wp)[row + t * CK + c] = v;
             }
     }
     return 0;
@@ -664,11 +673,13 @@ int desc_args(const qa_conv_desc* d, ConvArgs& a, const char* who) {
                                  &CK, &rows);
         if (d->x_code != 2 || d->x_sc != 1 || d->x_add < -65536 ||
             d->x_add > 65536 || d->w_kgp != CK || d->w_rows != rows ||
+            (d->w_layout != 2 && d->w_layout != 4) ||
             d->KH * d->KW * CK >= ((int64_t)1 << 19)) {
             set_error(who, "FP64 MFMA path: operands do not match");
             return -1;
         }
-        a.wf = (const double*)d->w;
+        a.wf = d->w;
+        a.wf_bytes = (int32_t)d->w_layout;
         a.CK = (int32_t)CK;
         a.wf_rows = (int32_t)rows;
         a.wide = (int32_t)d->wide;

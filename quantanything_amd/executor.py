@@ -187,6 +187,13 @@ def plan_epilogue(lib, d, mult, shift, pre=None, lut=None):
     return plan if rc == 1 else None
 
 
+# Tiles of the FP64 matrix-core path (qa_conv_f64.hip): 16-channel groups
+# wm | 16-pixel tiles per wave tm << 4 | K split over the work-group << 8.
+F64_TILES = (0x11, 0x12, 0x41, 0x111, 0x112, 0x114)
+# Element types tried, in order, for that path's packed weights.
+F64_WEIGHT_TYPES = (np.int16, np.int32)
+
+
 def _dev(a, dtype):
     return torch.from_numpy(np.array(a, dtype=dtype, copy=True)).cuda()
 
@@ -218,6 +225,7 @@ class DeviceExecutor:
         self.softmax_of = {}  # Softmax output -> (launch name, arguments)
         self.gap_info = {}  # pool launch -> layer, input, output, parameters
         self.tunables = []  # (launch name, desc, tile codes, fn(stream))
+        self.f64_descs = []  # (desc, None, None, launch name), FP64 path
         self.outputs_f32 = {}
         self.cuda_graph = None
         self._plan(input_shapes)
@@ -332,7 +340,7 @@ class DeviceExecutor:
         self._plan_epilogues()
         self._fuse_input_quantization(cons)
         self._fuse_pools(cons)
-        for d, _, _, name in self.mfma_descs:
+        for d, _, _, name in self.mfma_descs + self.f64_descs:
             if name in dict(self.launches):
                 self.tunables.append(
                     (name, d, self.tile_candidates(d),
@@ -415,12 +423,15 @@ class DeviceExecutor:
             ck, rows = _I64(0), _I64(0)
             size = self.lib.qa_pack_weights_f64_size(
                 cout, cg, kh, kw, groups, ctypes.byref(ck), ctypes.byref(rows))
-            wf = np.empty(size, np.float64)
-            if self.lib.qa_pack_weights_f64(w32.ctypes.data, cout, cg, kh,
-                                            kw, groups, wf.ctypes.data) == 0:
-                info = dict(w=_dev(wf, np.float64), w_code=8, layout=0,
-                            kgp=ck.value, rows=rows.value, corr=None,
-                            boff=None, rowsum=0, wide=1)
+            for dt in F64_WEIGHT_TYPES:  # the narrowest element that fits
+                wf = np.empty(size, dt)
+                if self.lib.qa_pack_weights_f64(
+                        w32.ctypes.data, cout, cg, kh, kw, groups,
+                        wf.itemsize, wf.ctypes.data) == 0:
+                    info = dict(w=_dev(wf, dt), w_code=8, layout=wf.itemsize,
+                                kgp=ck.value, rows=rows.value, corr=None,
+                                boff=None, rowsum=0, wide=1)
+                    break
         if info is None:  # exact VALU path, int64 accumulation
             info = dict(w=_dev(w32, np.int32), w_code=4, layout=0, kgp=0,
                         rows=0, corr=None, boff=None, rowsum=0, wide=1)
@@ -517,6 +528,8 @@ class DeviceExecutor:
                 (d, info["host"],
                  None if lut_layer is None else lut_layer.lut,
                  f"conv:{layer.name}"))
+        if d.w_code == 8:
+            self.f64_descs.append((d, None, None, f"conv:{layer.name}"))
         name = add_layer or lut_layer or layer
         self.epi[name.node.outputs[0]] = (d, 0, cout)
         self._add(f"conv:{layer.name}", lambda s, d=d:
@@ -799,13 +812,18 @@ class DeviceExecutor:
     # ------------------------------------------------------------ tiling --
     @staticmethod
     def tile_candidates(d):
-        """``qa_conv_desc.tile`` codes worth timing for one int8 MFMA
-        convolution: 0 (the library's own choice), then every channel-block
+        """``qa_conv_desc.tile`` codes worth timing for one MFMA
+        convolution. FP64 path: 0 (the library's choice), then each of its
+        tiles (16-channel groups, 16-pixel tiles per wave, K split over the
+        work-group). int8: 0, then every channel-block
         width up to the output channels per group, K-split (channel-blocked
         weight layout only) and weights in LDS (where 16 rows per channel
         group of K bytes fit in the 3 KiB-chunk staging budget; the library
         re-checks the LDS size)."""
         cog = d.Cout // d.G
+        if d.w_code == 8:  # FP64 path: wm | tm << 4 | split << 8
+            wm_max = 1 if cog <= 16 else 2 if cog <= 32 else 4
+            return [0] + [0x10000 | c for c in F64_TILES if c & 15 <= wm_max]
         wm_max = 1 if cog <= 16 else 2 if cog <= 32 else 4 if cog <= 64 else 8
         out = [0]
         for wm in (1, 2, 4, 8):

@@ -159,6 +159,7 @@ def _conv_graph(cin, cout, k, stride, pad, dil, groups, size):
     return b.build("images", [None, cin, size, size], y)
 
 
+@pytest.mark.parametrize("wtype", ["int16", "int32"])
 @pytest.mark.parametrize("cin,cout,k,stride,pad,dil,groups,size", [
     (3, 16, 3, 2, 1, 1, 1, 32),    # the stem: 3 of 4 stored channels
     (16, 24, 3, 1, 1, 1, 1, 17),   # a partial 16-channel block
@@ -168,11 +169,16 @@ def _conv_graph(cin, cout, k, stride, pad, dil, groups, size):
     (32, 64, 3, 1, 1, 1, 2, 10),   # two groups
     (24, 24, 3, 1, 1, 1, 24, 9),   # depthwise
 ])
-def test_int16_conv_on_fp64_matrix_cores(hip, tmp_path, cin, cout, k, stride,
-                                         pad, dil, groups, size):
-    """16-bit convolutions run on the FP64 MFMA path (w_code 8) and every
-    tensor equals the oracle's int64-accumulated one."""
+def test_int16_conv_on_fp64_matrix_cores(hip, tmp_path, monkeypatch, wtype,
+                                         cin, cout, k, stride, pad, dil,
+                                         groups, size):
+    """16-bit convolutions run on the FP64 MFMA path (w_code 8, weights
+    packed as int16 or int32) and every tensor equals the oracle's
+    int64-accumulated one."""
+    from quantanything_amd import executor
     from quantanything_amd.executor import ConvDesc
+
+    monkeypatch.setattr(executor, "F64_WEIGHT_TYPES", (np.dtype(wtype).type,))
 
     g = _conv_graph(cin, cout, k, stride, pad, dil, groups, size)
     calib = [Stream(60 + i).uniform((3, cin, size, size), -1.0, 1.0)
@@ -182,16 +188,22 @@ def test_int16_conv_on_fp64_matrix_cores(hip, tmp_path, cin, cout, k, stride,
     oracle = OraclePipeline(g, _qjson(c, tmp_path))
     oracle.run(x, keep=True)
     ex = c.executor({"images": x.shape})
-    assert [d.w_code for d in ex.keep if isinstance(d, ConvDesc)] == [8]
-    ex.run({"images": x})
-    checked = 0
-    for name, t in ex.tensors.items():
-        if name in oracle.env:
-            got = t.to_host()
-            np.testing.assert_array_equal(
-                got, oracle.env[name].reshape(got.shape), err_msg=name)
-            checked += 1
-    assert checked >= 2
+    assert [(d.w_code, d.w_layout) for d in ex.keep
+            if isinstance(d, ConvDesc)] == [(8, np.dtype(wtype).itemsize)]
+    [(_, d, codes, _)] = ex.tunables
+    assert len(codes) >= 4
+    for code in codes:
+        d.tile = code
+        ex.run({"images": x})
+        checked = 0
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, tile {code:#x}")
+                checked += 1
+        assert checked >= 2
 
 
 def test_yolov8n_cls_int16_bit_exact(hip, tmp_path):
@@ -208,8 +220,21 @@ def test_yolov8n_cls_int16_bit_exact(hip, tmp_path):
     codes = [d.w_code for d in ex.keep if isinstance(d, ConvDesc)]
     assert len(codes) > 20 and set(codes) == {8}
     got = c.integer_outputs(x)[g.outputs[0]]
-    ints, _ = OraclePipeline(g, _qjson(c, tmp_path)).run(x)
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    ints, _ = oracle.run(x, keep=True)
     np.testing.assert_array_equal(got, ints[g.outputs[0]])
+    # every layer through each of its tiles
+    assert len(ex.tunables) == len(codes)
+    for r in range(max(len(t[2]) for t in ex.tunables)):
+        for _, d, cc, _ in ex.tunables:
+            d.tile = cc[r % len(cc)]
+        ex.run({"images": x})
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, pass {r}")
 
 
 def test_tuned_tiles_keep_results(hip):
