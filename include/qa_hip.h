@@ -224,6 +224,68 @@ typedef struct qa_epi_params {
 int64_t qa_epi_plan_bytes(int64_t cout);
 int qa_plan_epilogue_i8(const qa_epi_params* p, void* plan);
 
+/* Float fallbacks on device tensors (the reference's dequantize -> float
+ * operator -> quantize, quant_layers.py:195-205), and a strided copy. */
+
+/* Element (i_0, .., i_{ndim-1}) of x at x + sum i_k * xs[k] goes to y +
+ * sum i_k * ys[k] (ndim <= 6, element strides), as q = stored + x_so:
+ * mode 0 unchanged, mode 1 q' = clip(mbqm(q - zp_in, m, s) + zp_out) (the
+ * reference's rescale, qa_kernels.cpp:307-316), mode 2 the float fallback
+ * q' = quantize((float)((q - in_zp) * in_scale), out_scale, zp_out) (e.g.
+ * a Gather, float_ops.py:490-496); stored y = q' - y_so. Layout operators
+ * that are not views (Transpose + Reshape) and Concat along any axis. */
+typedef struct qa_nd_copy {
+    const void* x;
+    int64_t x_code, x_so;
+    void* y;
+    int64_t y_code, y_so;
+    int64_t ndim, shape[6], xs[6], ys[6];
+    int64_t mode, zp_in, m, s, zp_out, qmin, qmax;
+    double in_scale;
+    int64_t in_zp;
+    double out_scale;
+} qa_nd_copy;
+int qa_d_copy_nd(const qa_nd_copy* d, void* stream);
+
+/* LayerNormalization over the last axis of [rows, cols] (row strides in
+ * elements) as float_ops.py:336-347: x = (float)((q - in_zp) * in_scale),
+ * float64 mean and variance, y = (x - mean) / sqrt(var + eps) * gamma
+ * (+ beta), cast to float32, quantized with round-half-even. beta may be
+ * NULL. Results agree with the reference within one quantization step
+ * (float64 summation order). */
+int qa_d_layernorm(const void* x, int x_code, int64_t x_rstride,
+                   int64_t rows, int64_t cols, double in_scale, int64_t in_zp,
+                   int64_t x_so, const float* gamma, const float* beta,
+                   double eps, void* y, int y_code, int64_t y_rstride,
+                   double out_scale, int64_t out_zp, int64_t qmin,
+                   int64_t qmax, int64_t y_so, void* stream);
+
+/* MatMul of two activations, the reference's float fallback
+ * (float_ops.py:181-186): C[b0, b1, m, n] = quantize(sum_k A[b0, b1, m, k] *
+ * B[b0, b1, k, n]) with A, B dequantized. B is passed transposed, as Bt[b0,
+ * b1, n, k] at b + b0*b_s0 + b1*b_s1 + n*b_sn + k; A at a + b0*a_s0 +
+ * b1*a_s1 + m*a_sm + k (unit stride along k for both). The exact integer
+ * sum of (a - a_zp)(b - b_zp) is scaled once by a_scale * b_scale (float32
+ * result), which agrees with the reference's float32 matmul within one
+ * output quantization step. int8 or int16 storage (the same for A and B),
+ * K < 2^17. */
+typedef struct qa_matmul_desc {
+    const void* a;
+    int64_t a_code, a_so, a_zp;
+    double a_scale;
+    int64_t a_s0, a_s1, a_sm;
+    const void* b;
+    int64_t b_code, b_so, b_zp;
+    double b_scale;
+    int64_t b_s0, b_s1, b_sn;
+    int64_t B0, B1, M, N, K;
+    void* y;
+    int64_t y_code, y_so, y_s0, y_s1, y_sm, y_sn;
+    double out_scale;
+    int64_t out_zp, qmin, qmax;
+} qa_matmul_desc;
+int qa_d_matmul_act(const qa_matmul_desc* d, void* stream);
+
 /* `stream` of every qa_d_* entry is the hipStream_t to launch on, used as
  * given (NULL: the null stream). The entries are asynchronous and return 0
  * on success, -1 on an error (see qa_last_error). */

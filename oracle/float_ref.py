@@ -7,7 +7,8 @@ Sigmoid / Exp / Softplus in float64 cast to float32 (``float_ops.py:225-227``
 and neighbours), HardSwish / HardSigmoid / LeakyRelu / Elu / Tanh / Relu,
 Abramowitz-Stegun erf and Gelu (``:289-320``), binary element-wise ops in
 NumPy's promotion, Softmax and LayerNorm in float64 (``:336-347``,
-``:380-385``), and the integer-safe shaping ops.
+``:380-385``), the float32 MatMul of two activations (``:181-186``), Gather
+(``:490-496``) and the integer-safe shaping ops.
 """
 
 import numpy as np
@@ -131,6 +132,29 @@ def eval_node(node, args, opset=13, pad_value=None):
     if op == "Transpose":
         perm = node.attr("perm")
         return [np.transpose(args[0], perm if perm else None)]
+    if op in ("Squeeze", "Unsqueeze"):
+        x = args[0]
+        axes = (np.asarray(args[1]).astype(np.int64).reshape(-1).tolist()
+                if len(args) > 1 and args[1] is not None
+                else node.attr("axes"))
+        if op == "Squeeze":
+            if axes is None:
+                return [np.squeeze(x)]
+            return [np.squeeze(x, axis=tuple(a + x.ndim if a < 0 else a
+                                             for a in axes))]
+        nd = x.ndim + len(axes)
+        for a in sorted(a + nd if a < 0 else a for a in axes):
+            x = np.expand_dims(x, a)
+        return [x]
+    if op == "Gather":
+        return [np.take(args[0], np.asarray(args[1]).astype(np.int64),
+                        axis=node.attr("axis", 0))]
+    if op == "MatMul":
+        # float32 operands, float32 result (float_ops.py:181-186)
+        y = np.matmul(args[0], args[1]).astype(np.float32)
+        if len(args) > 2 and args[2] is not None:
+            y = y + args[2]
+        return [y]
     if op == "Concat":
         return [np.concatenate(args, axis=node.attr("axis"))]
     if op == "GlobalAveragePool":

@@ -320,19 +320,30 @@ class OraclePipeline:
         outs = eval_node(node, full, self.g.opset)
         return [L.quantize_f32(y, *q) for y, q in zip(outs, st["out_qp"])]
 
-    def run(self, x, keep=False):
+    def run(self, x, keep=False, overrides=None):
         """Returns ``{output name: int32 quantized array}`` and the
         dequantized float32 outputs in graph-output order; ``keep`` leaves
-        every tensor of the pass in ``self.env``."""
+        every tensor of the pass in ``self.env``. ``overrides`` maps tensor
+        names to values used in place of the computed ones (the computed
+        values are kept in ``self.computed``), so that layers after a float
+        fallback can be checked on the same inputs as another
+        implementation's."""
         feeds = x if isinstance(x, dict) else {self.g.input_names[0]: x}
         env = {}
         for name, v in feeds.items():
             s, z, lo, hi = self.qp[name]
             env[name] = self.lib.quantize_f32(np.asarray(v, np.float32), s, z,
                                               lo, hi)
+        self.computed = {}
         for st in self.plan:
             args = [env[n] if n in env else self._const(n) for n in st["ins"]]
-            env.update(zip(st["node"].outputs, self._run_step(st, args)))
+            outs = dict(zip(st["node"].outputs, self._run_step(st, args)))
+            for name in list(outs):
+                if overrides and name in overrides:
+                    self.computed[name] = outs[name]
+                    outs[name] = np.asarray(overrides[name]).reshape(
+                        outs[name].shape).astype(np.int32)
+            env.update(outs)
         if keep:
             self.env = env
         ints = {o: env[o] for o in self.g.outputs}

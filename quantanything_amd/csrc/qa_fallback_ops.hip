@@ -1,0 +1,271 @@
+// Float fallbacks of the integer pass on device tensors, and the strided
+// copy behind layout operators that are not views.
+//
+// The reference runs every operator without an integer implementation as
+// dequantize -> float operator -> quantize (quant_layers.py:195-205):
+//   LayerNorm  float_ops.py:336-347 (float64 statistics over the last axis,
+//              then * gamma + beta, cast to float32),
+//   MatMul     float_ops.py:181-186 (float32 matmul of two activations).
+// Here the dequantized input is the reference's float32 value
+// (float)((q - zp) * scale); LayerNorm follows the same float64 steps. The
+// activation x activation MatMul sums the exact integer products
+// sum (a - za)(b - zb) (int8: v_dot4_i32_i8) and scales the sum once,
+// y = (float)(acc * sa * sb): the reference's float32 sums of float32
+// products differ from it by a few float32 roundings, far below one output
+// quantization step, so outputs agree within one step.
+#include <algorithm>
+
+#include "../../include/qa_hip.h"
+#include "qa_conv.h"
+
+namespace qa {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float dequant_f32(int64_t q, int64_t zp,
+                                             double scale) {
+    return (float)((double)(q - zp) * scale);
+}
+
+// ------------------------------------------------------------ N-D copy --
+__global__ __launch_bounds__(kThreads) void k_copy_nd(qa_nd_copy d,
+                                                      int64_t total) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        int64_t rem = i, xo = 0, yo = 0;
+        for (int k = (int)d.ndim - 1; k >= 0; --k) {
+            const int64_t c = rem % d.shape[k];
+            rem /= d.shape[k];
+            xo += c * d.xs[k];
+            yo += c * d.ys[k];
+        }
+        int64_t q = load_any(d.x, (int)d.x_code, xo) + d.x_so;
+        if (d.mode == 1)
+            q = qa_clip128(qa_mbqm_fast(q - d.zp_in, d.m, d.s) + d.zp_out,
+                           d.qmin, d.qmax);
+        else if (d.mode == 2)
+            q = qa_quantize_one(dequant_f32(q, d.in_zp, d.in_scale),
+                                d.out_scale, d.zp_out, d.qmin, d.qmax);
+        store_any(d.y, (int)d.y_code, yo, q - d.y_so);
+    }
+}
+
+// ----------------------------------------------------------- LayerNorm --
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// One wave per row.
+__global__ __launch_bounds__(kThreads) void k_layernorm(
+    const void* __restrict__ x, int x_code, int64_t x_rs, int64_t rows,
+    int64_t cols, double in_scale, int64_t in_zp, int64_t x_so,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    double eps, void* __restrict__ y, int y_code, int64_t y_rs,
+    double out_scale, int64_t out_zp, int64_t qmin, int64_t qmax,
+    int64_t y_so) {
+    const int lane = threadIdx.x & 63;
+    for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows;
+         r += (int64_t)gridDim.x * 4) {
+        auto value = [&](int64_t i) {
+            return (double)dequant_f32(load_any(x, x_code, r * x_rs + i) + x_so,
+                                       in_zp, in_scale);
+        };
+        double s = 0.0;
+        for (int64_t i = lane; i < cols; i += 64) s += value(i);
+        const double mean = wave_sum(s) / (double)cols;
+        double v = 0.0;
+        for (int64_t i = lane; i < cols; i += 64) {
+            const double t = value(i) - mean;
+            v += t * t;
+        }
+        const double sd = sqrt(wave_sum(v) / (double)cols + eps);
+        for (int64_t i = lane; i < cols; i += 64) {
+            double t = (value(i) - mean) / sd * (double)gamma[i];
+            if (beta) t += (double)beta[i];
+            const int64_t q =
+                qa_quantize_one((float)t, out_scale, out_zp, qmin, qmax);
+            store_any(y, y_code, r * y_rs + i, q - y_so);
+        }
+    }
+}
+
+// ---------------------------------------------- activation x activation --
+// C[b0, b1, m, n] = quantize(sa * sb * sum_k (A[.., m, k] - za) *
+// (Bt[.., n, k] - zb)); A and Bt have unit stride along k. A work-group
+// computes a 64 x 64 block of C, 4 x 4 per thread, K staged through LDS in
+// chunks of 64. int8 storage: v_dot4_i32_i8 on the stored bytes, centred by
+// row / column sums; int16: exact int64 products.
+template <class T>
+__global__ __launch_bounds__(kThreads) void k_matmul_act(qa_matmul_desc d) {
+    constexpr int KC = 64;
+    constexpr bool I8 = sizeof(T) == 1;
+    constexpr int PAD = I8 ? 4 : 2;  // keeps 4-byte words aligned
+    __shared__ T sa[64][KC + PAD];
+    __shared__ T sb[64][KC + PAD];
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const int64_t bz = blockIdx.z;
+    const int64_t b0 = bz / d.B1, b1 = bz - b0 * d.B1;
+    const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+    const T* A = (const T*)d.a + b0 * d.a_s0 + b1 * d.a_s1;
+    const T* B = (const T*)d.b + b0 * d.b_s0 + b1 * d.b_s1;
+    // centred = stored + add
+    const int64_t a_add = d.a_so - d.a_zp, b_add = d.b_so - d.b_zp;
+    int64_t acc[4][4] = {};
+    int32_t acc32[4][4] = {};
+    int32_t rs[4] = {0, 0, 0, 0}, cs[4] = {0, 0, 0, 0};  // stored sums
+    for (int64_t k0 = 0; k0 < d.K; k0 += KC) {
+        // stage: 64 rows x KC elements of each operand, zero past the ends
+        for (int e = tid; e < 64 * KC; e += kThreads) {
+            const int r = e / KC, c = e - r * KC;
+            const int64_t k = k0 + c;
+            const int64_t m = m0 + r, n = n0 + r;
+            sa[r][c] = (m < d.M && k < d.K) ? A[m * d.a_sm + k] : (T)0;
+            sb[r][c] = (n < d.N && k < d.K) ? B[n * d.b_sn + k] : (T)0;
+        }
+        __syncthreads();
+        if (I8) {
+#pragma unroll 4
+            for (int kk = 0; kk < KC; kk += 4) {
+                int aw[4], bw[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    aw[i] = *(const int*)&sa[ty * 4 + i][kk];
+                    bw[i] = *(const int*)&sb[tx * 4 + i][kk];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc32[i][j] = __builtin_amdgcn_sdot4(aw[i], bw[j],
+                                                             acc32[i][j], false);
+                if (a_add != 0 || b_add != 0) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        rs[i] = __builtin_amdgcn_sdot4(aw[i], 0x01010101, rs[i],
+                                                       false);
+                        cs[i] = __builtin_amdgcn_sdot4(bw[i], 0x01010101, cs[i],
+                                                       false);
+                    }
+                }
+            }
+        } else {
+            for (int kk = 0; kk < KC && k0 + kk < d.K; ++kk) {
+                int64_t av[4], bv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    av[i] = (int64_t)sa[ty * 4 + i][kk] + a_add;
+                    bv[i] = (int64_t)sb[tx * 4 + i][kk] + b_add;
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+            }
+        }
+        __syncthreads();
+    }
+    const double scale = d.a_scale * d.b_scale;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t m = m0 + ty * 4 + i;
+        if (m >= d.M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t n = n0 + tx * 4 + j;
+            if (n >= d.N) continue;
+            int64_t v = acc[i][j];
+            if (I8)  // (sa + a_add)(sb + b_add) summed over the K real terms
+                v = (int64_t)acc32[i][j] + a_add * cs[j] + b_add * rs[i] +
+                    d.K * a_add * b_add;
+            const float yf = (float)((double)v * scale);
+            const int64_t q =
+                qa_quantize_one(yf, d.out_scale, d.out_zp, d.qmin, d.qmax);
+            store_any(d.y, (int)d.y_code,
+                      b0 * d.y_s0 + b1 * d.y_s1 + m * d.y_sm + n * d.y_sn,
+                      q - d.y_so);
+        }
+    }
+}
+
+bool launched(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_hip_error(what, e);
+        return false;
+    }
+    return true;
+}
+
+bool code_ok(int64_t c) { return c == 1 || c == 2 || c == 4; }
+
+}  // namespace
+}  // namespace qa
+
+using namespace qa;
+
+QA_API int qa_d_copy_nd(const qa_nd_copy* d, void* stream) {
+    if (!d || d->ndim < 1 || d->ndim > 6 || !code_ok(d->x_code) ||
+        !code_ok(d->y_code) || d->mode < 0 || d->mode > 2) {
+        set_error("qa_d_copy_nd", "bad descriptor");
+        return -1;
+    }
+    int64_t total = 1;
+    for (int k = 0; k < d->ndim; ++k) {
+        if (d->shape[k] < 0) {
+            set_error("qa_d_copy_nd", "negative extent");
+            return -1;
+        }
+        total *= d->shape[k];
+    }
+    if (total == 0) return 0;
+    const int64_t blocks = std::min<int64_t>(ceil_div(total, kThreads), 65535);
+    k_copy_nd<<<(unsigned)blocks, kThreads, 0, (hipStream_t)stream>>>(*d,
+                                                                      total);
+    return launched("qa_d_copy_nd") ? 0 : -1;
+}
+
+QA_API int qa_d_layernorm(const void* x, int x_code, int64_t x_rstride,
+                          int64_t rows, int64_t cols, double in_scale,
+                          int64_t in_zp, int64_t x_so, const float* gamma,
+                          const float* beta, double eps, void* y, int y_code,
+                          int64_t y_rstride, double out_scale, int64_t out_zp,
+                          int64_t qmin, int64_t qmax, int64_t y_so,
+                          void* stream) {
+    if (rows <= 0 || cols <= 0) return 0;
+    if (!x || !y || !gamma || !code_ok(x_code) || !code_ok(y_code)) {
+        set_error("qa_d_layernorm", "bad arguments");
+        return -1;
+    }
+    const int64_t blocks = std::min<int64_t>(ceil_div(rows, 4), 65535);
+    k_layernorm<<<(unsigned)blocks, kThreads, 0, (hipStream_t)stream>>>(
+        x, x_code, x_rstride, rows, cols, in_scale, in_zp, x_so, gamma, beta,
+        eps, y, y_code, y_rstride, out_scale, out_zp, qmin, qmax, y_so);
+    return launched("qa_d_layernorm") ? 0 : -1;
+}
+
+QA_API int qa_d_matmul_act(const qa_matmul_desc* d, void* stream) {
+    if (!d || d->a_code != d->b_code || (d->a_code != 1 && d->a_code != 2) ||
+        !code_ok(d->y_code) || d->B0 < 0 || d->B1 <= 0 || d->M < 0 ||
+        d->N < 0 || d->K < 0 || d->K >= (1 << 17)) {
+        set_error("qa_d_matmul_act",
+                  "needs int8 or int16 operands of one storage, K < 2^17");
+        return -1;
+    }
+    if (d->B0 * d->B1 * d->M * d->N == 0) return 0;
+    const int64_t gx = ceil_div(d->N, 64), gy = ceil_div(d->M, 64);
+    const int64_t gz = d->B0 * d->B1;
+    if (gx > 65535 || gy > 65535 || gz > 65535) {
+        set_error("qa_d_matmul_act", "grid too large");
+        return -1;
+    }
+    const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)gz);
+    if (d->a_code == 1)
+        k_matmul_act<int8_t><<<grid, kThreads, 0, (hipStream_t)stream>>>(*d);
+    else
+        k_matmul_act<int16_t><<<grid, kThreads, 0, (hipStream_t)stream>>>(*d);
+    return launched("qa_d_matmul_act") ? 0 : -1;
+}

@@ -79,14 +79,62 @@ def storage_of(bits, signed):
 class DeviceTensor:
     """A quantized tensor (or view) resident in device memory.
 
-    ``shape`` is the logical (NCHW / [N, F]) shape; element (n, c, pix) is at
-    element offset ``offset + n*sn + c*sc + pix*sp``."""
+    ``shape`` is the logical (NCHW / [N, F] / N-D) shape. 4-D and 2-D
+    tensors: element (n, c, pix) is at element offset ``offset + n*sn +
+    c*sc + pix*sp``. Any tensor: element index i at ``offset + sum
+    i_k * nd_strides[k]``; ``strides`` is given for views that are not of
+    the (n, c, pix) form (``nhwc`` is then False)."""
 
-    def __init__(self, buf, offset, shape, sn, sc, sp, code, so, qp):
+    def __init__(self, buf, offset, shape, sn, sc, sp, code, so, qp,
+                 strides=None):
         self.buf, self.offset = buf, int(offset)
         self.shape = tuple(int(s) for s in shape)
         self.sn, self.sc, self.sp = int(sn), int(sc), int(sp)
         self.code, self.so, self.qp = code, int(so), qp
+        self._strides = None if strides is None else \
+            tuple(int(v) for v in strides)
+        self.nhwc = True
+
+    @staticmethod
+    def nd(buf, offset, shape, strides, code, so, qp):
+        """View with explicit N-D element strides."""
+        shape, strides = tuple(shape), tuple(strides)
+        t = DeviceTensor(buf, offset, shape, strides[0] if strides else 0,
+                         strides[1] if len(strides) > 1 else 1, 0, code, so,
+                         qp, strides)
+        if len(shape) == 4 and (shape[3] == 1 or shape[2] == 1 or
+                                strides[2] == shape[3] * strides[3]):
+            t.sp = strides[3] if shape[3] > 1 else strides[2] // max(
+                shape[3], 1)
+        elif len(shape) == 4:
+            t.nhwc = False
+        elif len(shape) != 2:
+            t.nhwc = False
+        return t
+
+    @property
+    def nd_strides(self):
+        if self._strides is not None:
+            return self._strides
+        if len(self.shape) == 4:
+            return (self.sn, self.sc, self.shape[3] * self.sp, self.sp)
+        if len(self.shape) == 2:
+            return (self.sn, self.sc)
+        raise NotImplementedError(f"{len(self.shape)}-D tensor without "
+                                  "strides")
+
+    def meta(self):
+        """A storage-free torch tensor of this view's shape and strides
+        (storage offset 0), for computing the strides of derived views."""
+        return torch.empty_strided(self.shape, self.nd_strides,
+                                   dtype=self.buf.dtype, device="meta")
+
+    def derived(self, m):
+        """The view of this tensor's buffer that the meta tensor ``m``
+        (derived from :meth:`meta`) describes."""
+        return DeviceTensor.nd(self.buf, self.offset + m.storage_offset(),
+                               tuple(m.shape), tuple(m.stride()), self.code,
+                               self.so, self.qp)
 
     @property
     def ptr(self):
@@ -102,20 +150,46 @@ class DeviceTensor:
 
     def rows_view(self):
         """``(rows, cols, row_stride)`` of the tensor as a strided matrix
-        (rows = N*pixels, cols = channels), or None when not expressible."""
+        (4-D: rows = N*pixels, cols = channels; N-D: rows = all but the last
+        axis, cols = the last axis), or None when not expressible."""
+        if self._strides is not None and (len(self.shape) != 2 or
+                                          self._strides[1] != 1):
+            sh, st = self.shape, self._strides
+            if len(sh) < 2 or st[-1] != 1 and sh[-1] > 1:
+                return None
+            dims = [(n, v) for n, v in zip(sh[:-1], st[:-1]) if n > 1]
+            for (n0, s0), (n1, s1) in zip(dims, dims[1:]):
+                if s0 != n1 * s1:
+                    return None
+            rs = dims[-1][1] if dims else sh[-1]
+            return int(np.prod(sh[:-1], dtype=np.int64)), sh[-1], rs
         if len(self.shape) == 2:
             return self.shape[0], self.shape[1], self.sn
-        if self.sc == 1 and self.sn == self.pixels * self.sp:
+        if len(self.shape) == 4 and self.sc == 1 and \
+                self.sn == self.pixels * self.sp:
             return self.shape[0] * self.pixels, self.channels, self.sp
         return None
+
+    def row_major(self):
+        """True when the elements are dense in row-major logical order."""
+        st = self.nd_strides
+        want = 1
+        for n, v in zip(reversed(self.shape), reversed(st)):
+            if n > 1 and v != want:
+                return False
+            want *= n
+        return True
 
     def contiguous_2d(self):
         return len(self.shape) == 2 and self.sn == self.shape[1] and \
             self.sc == 1
 
     def to_host(self):
-        """Quantized values ``q`` as an int32 NumPy array (NCHW / [N, F])."""
-        if len(self.shape) == 4:
+        """Quantized values ``q`` as an int32 NumPy array (logical shape)."""
+        if self._strides is not None:
+            v = torch.as_strided(self.buf, self.shape, self._strides,
+                                 self.offset)
+        elif len(self.shape) == 4:
             n, c, h, w = self.shape
             v = torch.as_strided(self.buf, (n, c, h, w),
                                  (self.sn, self.sc, w * self.sp, self.sp),
@@ -124,6 +198,34 @@ class DeviceTensor:
             v = torch.as_strided(self.buf, self.shape, (self.sn, self.sc),
                                  self.offset)
         return v.to(torch.int32).cpu().numpy() + self.so
+
+
+class NdCopy(ctypes.Structure):
+    """``qa_nd_copy`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("x", _P), ("x_code", _I64), ("x_so", _I64), ("y", _P),
+                 ("y_code", _I64), ("y_so", _I64), ("ndim", _I64),
+                 ("shape", _I64 * 6), ("xs", _I64 * 6), ("ys", _I64 * 6)]
+                + [(n, _I64) for n in ("mode", "zp_in", "m", "s", "zp_out",
+                                       "qmin", "qmax")]
+                + [("in_scale", ctypes.c_double), ("in_zp", _I64),
+                   ("out_scale", ctypes.c_double)])
+
+
+class MatmulDesc(ctypes.Structure):
+    """``qa_matmul_desc`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("a", _P)] + [(n, _I64) for n in ("a_code", "a_so", "a_zp")]
+                + [("a_scale", ctypes.c_double)]
+                + [(n, _I64) for n in ("a_s0", "a_s1", "a_sm")]
+                + [("b", _P)] + [(n, _I64) for n in ("b_code", "b_so", "b_zp")]
+                + [("b_scale", ctypes.c_double)]
+                + [(n, _I64) for n in ("b_s0", "b_s1", "b_sn", "B0", "B1", "M",
+                                       "N", "K")]
+                + [("y", _P)] + [(n, _I64) for n in ("y_code", "y_so", "y_s0",
+                                                     "y_s1", "y_sm", "y_sn")]
+                + [("out_scale", ctypes.c_double)]
+                + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
 
 
 class PoolParams(ctypes.Structure):
@@ -231,10 +333,12 @@ class DeviceExecutor:
         self._plan(input_shapes)
 
     # -------------------------------------------------------------- utils --
-    def _new(self, shape, qp):
-        """Fresh channels-last (4-D) or row-major (2-D) tensor."""
+    def _new(self, shape, qp, dense=False):
+        """Fresh channels-last (4-D, unless ``dense``) or row-major tensor
+        (``dense``: row-major in the logical order, for the N-D operators
+        of transformers)."""
         shape = tuple(int(s) for s in shape)
-        if len(shape) == 4:
+        if len(shape) == 4 and not dense:
             n, c, h, w = shape
             if c <= 4:
                 cs = 4
@@ -246,12 +350,50 @@ class DeviceExecutor:
             buf = torch.empty(numel + TAIL, dtype=self.dtype, device="cuda")
             return DeviceTensor(buf, 0, shape, h * w * cs, 1, cs, self.code,
                                 self.so, qp)
-        if len(shape) == 2:
+        if len(shape) == 2 and not dense:
             numel = shape[0] * shape[1]
             buf = torch.empty(numel + TAIL, dtype=self.dtype, device="cuda")
             return DeviceTensor(buf, 0, shape, shape[1], 1, 0, self.code,
                                 self.so, qp)
-        raise NotImplementedError(f"{len(shape)}-D tensors on the device")
+        if not 1 <= len(shape) <= 6:
+            raise NotImplementedError(f"{len(shape)}-D tensors on the device")
+        numel = int(np.prod(shape, dtype=np.int64))
+        buf = torch.empty(numel + TAIL, dtype=self.dtype, device="cuda")
+        strides = tuple(int(np.prod(shape[k + 1:], dtype=np.int64))
+                        for k in range(len(shape)))
+        return DeviceTensor.nd(buf, 0, shape, strides, self.code, self.so, qp)
+
+    def _copy(self, name, x, y, mode=0, rescale=None, requant=None):
+        """Launch copying x into the view y (same logical shape): mode 0
+        unchanged, 1 integer rescale ``(zp_in, m, s, zp_out, qmin, qmax)``,
+        2 float requantization ``(in_scale, in_zp, out_scale, zp_out, qmin,
+        qmax)``."""
+        d = NdCopy()
+        d.x, d.x_code, d.x_so = x.ptr, x.code, x.so
+        d.y, d.y_code, d.y_so = y.ptr, y.code, y.so
+        shape = x.shape or (1,)
+        d.ndim = len(shape)
+        xs, ys = x.nd_strides or (0,), y.nd_strides or (0,)
+        for k in range(len(shape)):
+            d.shape[k], d.xs[k], d.ys[k] = shape[k], xs[k], ys[k]
+        d.mode = mode
+        d.qmin, d.qmax = -(1 << 62), 1 << 62
+        if mode == 1:
+            d.zp_in, d.m, d.s, d.zp_out, d.qmin, d.qmax = rescale
+        elif mode == 2:
+            (d.in_scale, d.in_zp, d.out_scale, d.zp_out, d.qmin,
+             d.qmax) = requant
+        self.keep.extend([d, x.buf, y.buf])  # the launch's raw pointers
+        self._add(name, lambda s, d=d: _ok(self.lib.qa_d_copy_nd(
+            ctypes.byref(d), s), "qa_d_copy_nd"))
+
+    def _contiguous(self, name, x):
+        """x itself when row-major dense, else a dense copy."""
+        if x.row_major():
+            return x
+        y = self._new(x.shape, x.qp, dense=True)
+        self._copy(name, x, y)
+        return y
 
     def _add(self, name, fn):
         self.launches.append((name, fn))
@@ -281,8 +423,7 @@ class DeviceExecutor:
                                   t.sp, qp.scale, qp.zp, qp.qmin, qp.qmax,
                                   t.so, s), "quantize"))
             else:
-                t = self._new(shape if len(shape) == 2 else
-                              (shape[0], int(np.prod(shape[1:]))), qp)
+                t = self._new(shape, qp)
                 numel = xf.numel()
                 self._add(f"quantize:{name}", lambda s, xf=xf, t=t,
                           numel=numel, qp=qp: _ok(
@@ -292,8 +433,14 @@ class DeviceExecutor:
                               "quantize"))
             self.tensors[name] = t
         for name in c.const_names:
-            raise NotImplementedError(
-                f"constant operand {name} consumed as an activation")
+            # quantized constant operands (e.g. a position embedding),
+            # uploaded once, stored as q - so
+            q = np.asarray(c.const_q[name], dtype=np.int64)
+            t = self._new(q.shape, c.qparams[name], dense=True)
+            host = torch.from_numpy((q - t.so).astype(
+                np.int8 if self.code == 1 else np.int16).reshape(-1))
+            t.buf[:host.numel()].copy_(host)
+            self.tensors[name] = t
 
         layers = c.layers
         producer = g.producer_index()
@@ -348,8 +495,13 @@ class DeviceExecutor:
                                         "qa_d_conv")))
         for name in g.outputs:
             t = self.tensors[name]
-            if not t.contiguous_2d():
-                raise NotImplementedError("graph outputs must be 2-D")
+            if not (t.contiguous_2d() or (t._strides is not None and
+                                          t.row_major())):
+                # a dense copy that the dequantization reads
+                t = self._contiguous(f"copy:{name}", DeviceTensor.nd(
+                    t.buf, t.offset, t.shape, t.nd_strides, t.code, t.so,
+                    t.qp))
+                self.tensors[name] = t
             yf = torch.empty(t.shape, dtype=torch.float32, device="cuda")
             self.outputs_f32[name] = yf
             sm = self.softmax_of.get(name)
@@ -468,14 +620,21 @@ class DeviceExecutor:
                            x.sp == 4) else 0
         else:
             k, ncol = layer.w_centered.shape
-            if x.shape[-1] != k or len(x.shape) != 2:
+            xv = x.rows_view()
+            if x.shape[-1] != k or xv is None or \
+                    (len(x.shape) == 4 and x._strides is None):
                 raise NotImplementedError(
                     f"gemm input {x.shape} x {layer.w_centered.shape}")
-            m = x.shape[0]
+            m = xv[0]
             out_shape = layer.out_shape(x.shape)
             geo = (m, k, 1, 1, ncol, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 1)
             groups, cg, kh, kw, cout = 1, k, 1, 1, ncol
             layout = 0
+            # rows of the input as images of one pixel
+            x = DeviceTensor(x.buf, x.offset, (m, k), xv[2], 1, 0, x.code,
+                             x.so, x.qp)
+        if layer.kind == "conv" and not x.nhwc:
+            raise NotImplementedError("convolution of a strided view")
         use_mfma = self._mfma_ok(layer, x, layout, groups, cg, cg * kh * kw)
         info = self._weights_dev(layer, x, layout, use_mfma)
         (d.N, d.C, d.H, d.W, d.Cout, d.KH, d.KW, d.SH, d.SW, d.PH, d.PW,
@@ -503,7 +662,8 @@ class DeviceExecutor:
             d.lut_offset = lut_layer.lut_offset
             d.lut_len = len(lut_layer.lut)
             final_qp = lut_layer.out_qp[0]
-        y = self._new(out_shape, final_qp)
+        y = self._new(out_shape, final_qp,
+                      dense=layer.kind == "gemm" and len(out_shape) != 2)
         if add_layer is not None:
             rname, first = res
             r = self.tensors[rname]
@@ -514,6 +674,11 @@ class DeviceExecutor:
             o = add_layer.out_qp[0]
             d.res = r.ptr
             d.res_sn, d.res_sc, d.res_sp, d.res_so = r.sn, r.sc, r.sp, r.so
+            if layer.kind == "gemm":
+                rv = r.rows_view()
+                if rv is None:
+                    raise NotImplementedError("residual of a strided view")
+                d.res_sn, d.res_sc, d.res_sp = rv[2], 1, 0
             d.res_first = 1 if first else 0
             d.za, d.ma, d.sa = qa_.zp, ma, sa
             d.zb, d.mb, d.sb = qb_.zp, mb, sb
@@ -522,6 +687,8 @@ class DeviceExecutor:
             y.qp = o
         d.y, d.y_code = y.ptr, y.code
         d.y_sn, d.y_sc, d.y_sp, d.y_so = y.sn, y.sc, y.sp, y.so
+        if layer.kind == "gemm":
+            d.y_sn, d.y_sc, d.y_sp = y.rows_view()[2], 1, 0
         self.keep.append(d)
         if d.w_code == 1 and d.y_code == 1:
             self.mfma_descs.append(
@@ -623,7 +790,7 @@ class DeviceExecutor:
         p = self._params(layer)
         if "lut" not in p:
             p["lut"] = _dev(layer.lut, np.int32)
-        y = self._new(x.shape, layer.out_qp[0])
+        y = self._new(x.shape, layer.out_qp[0], dense=x._strides is not None)
         xv, yv = x.rows_view(), y.rows_view()
         if xv is None or yv is None:
             raise NotImplementedError("table on a non-matrix view")
@@ -636,15 +803,35 @@ class DeviceExecutor:
         return [y]
 
     def _binary_views(self, a, b, y):
+        """Row views ``(rows, cols, row stride)`` of a, b and y; an operand
+        of batch size 1 broadcast over the batch gets row stride 0 (then
+        rows = batch, cols = one item)."""
+        if a.shape != b.shape:
+            big = a if b.shape[0] == 1 else b
+            one = b if big is a else a
+            if len(a.shape) != len(b.shape) or one.shape[0] != 1 or \
+                    one.shape[1:] != big.shape[1:]:
+                raise NotImplementedError("broadcasting element-wise op")
+            item = int(np.prod(big.shape[1:], dtype=np.int64))
+            views = []
+            for t in (a, b, y):
+                if not t.row_major() and t.shape[0] > 1:
+                    raise NotImplementedError("broadcast of a strided view")
+                views.append((big.shape[0], item,
+                              0 if t is one else t.nd_strides[0]))
+            if not one.row_major():
+                raise NotImplementedError("broadcast of a strided view")
+            return tuple(views)
         av, bv, yv = a.rows_view(), b.rows_view(), y.rows_view()
-        if a.shape != b.shape or None in (av, bv, yv):
-            raise NotImplementedError("broadcasting element-wise op")
+        if None in (av, bv, yv):
+            raise NotImplementedError("element-wise op on strided views")
         return av, bv, yv
 
     def _plan_add(self, layer, ins):
         a, b = ins
         o = layer.out_qp[0]
-        y = self._new(a.shape, o)
+        y = self._new(a.shape if a.shape[0] >= b.shape[0] else b.shape, o,
+                      dense=a._strides is not None or b._strides is not None)
         av, bv, yv = self._binary_views(a, b, y)
         (ma, sa), (mb, sb) = layer.mults
         qa_, qb_ = layer.in_qp
@@ -657,7 +844,8 @@ class DeviceExecutor:
     def _plan_mul(self, layer, ins):
         a, b = ins
         o = layer.out_qp[0]
-        y = self._new(a.shape, o)
+        y = self._new(a.shape if a.shape[0] >= b.shape[0] else b.shape, o,
+                      dense=a._strides is not None or b._strides is not None)
         av, bv, yv = self._binary_views(a, b, y)
         qa_, qb_ = layer.in_qp
         self._add(f"mul:{layer.name}", lambda s: _ok(self.lib.qa_d_mul(
@@ -666,12 +854,31 @@ class DeviceExecutor:
             o.qmax, a.so, b.so, y.so, s), "qa_d_mul"))
         return [y]
 
+    def _plan_concat_nd(self, layer, ins, axis):
+        """Concat along any axis: each part copied (rescaled when its
+        parameters differ) into its slice of a dense output."""
+        o = layer.out_qp[0]
+        shape = list(ins[0].shape)
+        shape[axis] = sum(t.shape[axis] for t in ins)
+        y = self._new(tuple(shape), o, dense=True)
+        ym, off = y.meta(), 0
+        for t, qp, (m, s_) in zip(ins, layer.in_qp, layer.mults):
+            part = y.derived(ym.narrow(axis, off, t.shape[axis]))
+            if qp.scale == o.scale and qp.zp == o.zp:
+                self._copy(f"concat:{layer.name}", t, part, mode=1,
+                           rescale=(qp.zp, *IDENTITY, o.zp, o.qmin, o.qmax))
+            else:
+                self._copy(f"concat:{layer.name}", t, part, mode=1,
+                           rescale=(qp.zp, m, s_, o.zp, o.qmin, o.qmax))
+            off += t.shape[axis]
+        return [y]
+
     def _plan_concat(self, layer, ins):
         axis = layer.node.attr("axis")
         nd = len(ins[0].shape)
         axis = axis + nd if axis < 0 else axis
-        if axis != 1:
-            raise NotImplementedError("Concat on the device needs axis 1")
+        if axis != 1 or nd != 4 or any(t._strides is not None for t in ins):
+            return self._plan_concat_nd(layer, ins, axis)
         o = layer.out_qp[0]
         shape = list(ins[0].shape)
         shape[1] = sum(t.shape[1] for t in ins)
@@ -755,14 +962,82 @@ class DeviceExecutor:
             o.qmax, layer.in_zp - x.so, y.so, s), "qa_d_requantize"))
         return [y]
 
+    def _const_list(self, node, index, attr):
+        if len(node.inputs) > index and node.inputs[index]:
+            return [int(v) for v in np.asarray(
+                self.graph.initializers[node.inputs[index]]).reshape(-1)]
+        v = node.attr(attr)
+        return None if v is None else [int(a) for a in np.asarray(v).reshape(
+            -1)]
+
+    def _plan_shape_nd(self, layer, x):
+        """Layout operators on N-D views (no copy unless a Reshape of a
+        non-dense view needs one)."""
+        node, op = layer.node, layer.node.op_type
+        m = x.meta()
+        nd = len(x.shape)
+        if op == "Reshape":
+            shape = self._const_list(node, 1, "shape")
+            if not node.attr("allowzero", 0):
+                shape = [x.shape[i] if v == 0 else v
+                         for i, v in enumerate(shape)]
+            try:
+                return [x.derived(m.view(shape))]
+            except RuntimeError:
+                xc = self._contiguous(f"copy:{layer.name}", x)
+                return [xc.derived(xc.meta().view(shape))]
+        if op == "Flatten":
+            ax = node.attr("axis", 1)
+            ax = ax + nd if ax < 0 else ax
+            shape = [int(np.prod(x.shape[:ax], dtype=np.int64)), -1]
+            try:
+                return [x.derived(m.view(shape))]
+            except RuntimeError:
+                xc = self._contiguous(f"copy:{layer.name}", x)
+                return [xc.derived(xc.meta().view(shape))]
+        if op == "Transpose":
+            perm = node.attr("perm") or list(range(nd))[::-1]
+            return [x.derived(m.permute(*perm))]
+        if op in ("Squeeze", "Unsqueeze"):
+            axes = self._const_list(node, 1, "axes")
+            if op == "Squeeze":
+                if axes is None:
+                    axes = [i for i, n in enumerate(x.shape) if n == 1]
+                axes = sorted(a + nd if a < 0 else a for a in axes)
+                for a in reversed(axes):
+                    m = m.squeeze(a)
+            else:
+                out_nd = nd + len(axes)
+                for a in sorted(a + out_nd if a < 0 else a for a in axes):
+                    m = m.unsqueeze(a)
+            return [x.derived(m)]
+        if op == "Split":
+            ax = node.attr("axis", 0)
+            ax = ax + nd if ax < 0 else ax
+            sizes = self._const_list(node, 1, "split") or \
+                [x.shape[ax] // len(node.outputs)] * len(node.outputs)
+            return [x.derived(v) for v in torch.split(m, sizes, dim=ax)]
+        if op == "Slice":
+            starts = self._const_list(node, 1, "starts")
+            ends = self._const_list(node, 2, "ends")
+            axes = self._const_list(node, 3, "axes") or \
+                list(range(len(starts)))
+            steps = self._const_list(node, 4, "steps") or [1] * len(starts)
+            index = [slice(None)] * nd
+            for st_, en, a, sp in zip(starts, ends, axes, steps):
+                if sp <= 0:
+                    raise NotImplementedError("Slice with a negative step")
+                index[a + nd if a < 0 else a] = slice(
+                    None if st_ >= 2**62 else st_,
+                    None if abs(en) >= 2**62 else en, sp)
+            return [x.derived(m[tuple(index)])]
+        raise NotImplementedError(f"{op} on the device")
+
     def _plan_shape(self, layer, ins):
         x = ins[0]
         op = layer.node.op_type
-        if op == "Split":
-            axis = layer.node.attr("axis", 0)
-            axis = axis + len(x.shape) if axis < 0 else axis
-            if axis != 1:
-                raise NotImplementedError("Split on the device needs axis 1")
+        if op == "Split" and len(x.shape) == 4 and x._strides is None and \
+                (layer.node.attr("axis", 0) in (1, -3)):
             node = layer.node
             if len(node.inputs) > 1 and node.inputs[1]:
                 sizes = self.graph.initializers[node.inputs[1]].astype(
@@ -781,12 +1056,13 @@ class DeviceExecutor:
                     self.epi[name] = (src[0], src[1] + c0, src[2])
                 c0 += sz
             return outs
-        if op == "Flatten":
-            if layer.node.attr("axis", 1) != 1 or x.pixels != 1:
-                raise NotImplementedError("Flatten of a spatial tensor")
+        if op == "Flatten" and len(x.shape) == 4 and x._strides is None \
+                and layer.node.attr("axis", 1) == 1 and x.pixels == 1:
             return [DeviceTensor(x.buf, x.offset, (x.shape[0], x.channels),
                                  x.sn, x.sc, 0, x.code, x.so, x.qp)]
-        raise NotImplementedError(f"{op} on the device")
+        if op in ("Pad", "MaxPool", "GlobalMaxPool"):
+            raise NotImplementedError(f"{op} on the device")
+        return self._plan_shape_nd(layer, x)
 
     def _plan_fallback(self, layer, ins):
         op = layer.node.op_type
@@ -794,11 +1070,13 @@ class DeviceExecutor:
         if op == "Softmax":
             ax = layer.node.attr("axis", -1 if self.graph.opset >= 13 else 1)
             ax = ax + len(x.shape) if ax < 0 else ax
-            if ax != len(x.shape) - 1 or not x.contiguous_2d():
+            if ax != len(x.shape) - 1:
                 raise NotImplementedError("Softmax over a non-last axis")
+            x = self._contiguous(f"copy:{layer.name}", x)
             o = layer.out_qp[0]
-            y = self._new(x.shape, o)
-            rows, cols = x.shape
+            y = self._new(x.shape, o, dense=True)
+            rows, cols, _ = x.rows_view()
+            self.keep.extend([x.buf, y.buf])
             iq = layer.in_qp[0]
             args = (x.ptr, x.code, rows, cols, iq.scale, iq.zp, x.so, y.ptr,
                     y.code, o.scale, o.zp, o.qmin, o.qmax, y.so)
@@ -807,7 +1085,109 @@ class DeviceExecutor:
             self._add(lname, lambda s: _ok(self.lib.qa_d_softmax(*args, s),
                                            "qa_d_softmax"))
             return [y]
+        if op == "LayerNormalization":
+            return self._plan_layernorm(layer, x)
+        if op == "MatMul" and len(ins) == 2:
+            return self._plan_matmul_act(layer, ins[0], ins[1])
+        if op == "Gather":
+            return self._plan_gather(layer, x)
         raise NotImplementedError(f"float fallback of {op} on the device")
+
+    def _plan_layernorm(self, layer, x):
+        """LayerNormalization over the last axis (float fallback)."""
+        node = layer.node
+        ax = node.attr("axis", -1)
+        if ax not in (-1, len(x.shape) - 1):
+            raise NotImplementedError("LayerNorm over more than the last axis")
+        init = self.graph.initializers
+        p = self._params(layer)
+        if "gamma" not in p:
+            p["gamma"] = _dev(init[node.inputs[1]].reshape(-1), np.float32)
+            p["beta"] = (_dev(init[node.inputs[2]].reshape(-1), np.float32)
+                         if len(node.inputs) > 2 and node.inputs[2] else None)
+        xv = x.rows_view()
+        if xv is None:
+            x = self._contiguous(f"copy:{layer.name}", x)
+            xv = x.rows_view()
+        rows, cols, xrs = xv
+        if p["gamma"].numel() != cols:
+            raise NotImplementedError("LayerNorm gain of another length")
+        o, iq = layer.out_qp[0], layer.in_qp[0]
+        y = self._new(x.shape, o, dense=True)
+        yrs = y.rows_view()[2]
+        eps = float(node.attr("epsilon", 1e-5))
+        g, b = p["gamma"], p["beta"]
+        self.keep.extend([x.buf, y.buf])
+        self._add(f"layernorm:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_layernorm(
+                x.ptr, x.code, xrs, rows, cols, iq.scale, iq.zp, x.so,
+                g.data_ptr(), None if b is None else b.data_ptr(), eps,
+                y.ptr, y.code, yrs, o.scale, o.zp, o.qmin, o.qmax, y.so, s),
+            "qa_d_layernorm"))
+        return [y]
+
+    def _plan_matmul_act(self, layer, a, b):
+        """MatMul of two activations (float fallback): [.., M, K] x
+        [.., K, N] with up to two equal batch axes."""
+        if len(a.shape) != len(b.shape) or not 2 <= len(a.shape) <= 4 or \
+                a.shape[:-2] != b.shape[:-2] or a.shape[-1] != b.shape[-2]:
+            raise NotImplementedError(
+                f"MatMul of {a.shape} and {b.shape} on the device")
+        if a.code != b.code:
+            raise NotImplementedError("MatMul of mixed storage")
+        # A with unit stride along K; B passed transposed (unit stride on K)
+        if a.nd_strides[-1] != 1 and a.shape[-1] > 1:
+            a = self._contiguous(f"copy:{layer.name}", a)
+        bt = b.derived(b.meta().transpose(-1, -2))
+        if bt.nd_strides[-1] != 1 and bt.shape[-1] > 1:
+            btc = self._new(bt.shape, b.qp, dense=True)
+            self._copy(f"copy:{layer.name}", bt, btc)
+            bt = btc
+        lead = a.shape[:-2]
+        batch = (1,) * (2 - len(lead)) + tuple(lead)
+        M, K = a.shape[-2:]
+        N = b.shape[-1]
+        o = layer.out_qp[0]
+        y = self._new(tuple(lead) + (M, N), o, dense=True)
+
+        def bstr(t):
+            st = t.nd_strides[:-2]
+            return (0,) * (2 - len(st)) + tuple(st)
+        qa_, qb_ = layer.in_qp
+        d = MatmulDesc()
+        d.a, d.a_code, d.a_so, d.a_zp, d.a_scale = a.ptr, a.code, a.so, \
+            qa_.zp, qa_.scale
+        (d.a_s0, d.a_s1), d.a_sm = bstr(a), a.nd_strides[-2]
+        d.b, d.b_code, d.b_so, d.b_zp, d.b_scale = bt.ptr, bt.code, bt.so, \
+            qb_.zp, qb_.scale
+        (d.b_s0, d.b_s1), d.b_sn = bstr(bt), bt.nd_strides[-2]
+        d.B0, d.B1, d.M, d.N, d.K = batch[0], batch[1], M, N, K
+        d.y, d.y_code, d.y_so = y.ptr, y.code, y.so
+        (d.y_s0, d.y_s1), d.y_sm, d.y_sn = bstr(y), y.nd_strides[-2], \
+            y.nd_strides[-1]
+        d.out_scale, d.out_zp, d.qmin, d.qmax = o.scale, o.zp, o.qmin, o.qmax
+        self.keep.extend([d, a.buf, bt.buf, y.buf])
+        self._add(f"matmul:{layer.name}", lambda s, d=d: _ok(
+            self.lib.qa_d_matmul_act(ctypes.byref(d), s), "qa_d_matmul_act"))
+        return [y]
+
+    def _plan_gather(self, layer, x):
+        """Gather of constant indices (float fallback: the selected values
+        are requantized to the output's parameters)."""
+        node = layer.node
+        idx = np.asarray(self.graph.initializers[node.inputs[1]])
+        ax = node.attr("axis", 0)
+        ax = ax + len(x.shape) if ax < 0 else ax
+        m = x.meta()
+        if idx.ndim == 0:
+            v = x.derived(m.select(ax, int(idx)))
+        else:
+            raise NotImplementedError("Gather of an index array")
+        o, iq = layer.out_qp[0], layer.in_qp[0]
+        y = self._new(v.shape, o, dense=True)
+        self._copy(f"gather:{layer.name}", v, y, mode=2,
+                   requant=(iq.scale, iq.zp, o.scale, o.zp, o.qmin, o.qmax))
+        return [y]
 
     # ------------------------------------------------------------ tiling --
     @staticmethod

@@ -312,6 +312,52 @@ def _transpose(node, ins, opset, **kw):
     return np.transpose(ins[0], perm if perm else None)
 
 
+def _axes(node, ins, index, attr):
+    if len(ins) > index and ins[index] is not None:
+        return [int(a) for a in np.asarray(ins[index]).reshape(-1)]
+    v = node.attr(attr)
+    return None if v is None else [int(a) for a in v]
+
+
+@_reg("Squeeze")
+def _squeeze(node, ins, opset, **kw):
+    axes = _axes(node, ins, 1, "axes")
+    x = ins[0]
+    if axes is None:
+        return np.squeeze(x)
+    return np.squeeze(x, axis=tuple(_axis(a, x.ndim) for a in axes))
+
+
+@_reg("Unsqueeze")
+def _unsqueeze(node, ins, opset, **kw):
+    axes = _axes(node, ins, 1, "axes")
+    x = ins[0]
+    out_nd = x.ndim + len(axes)
+    for a in sorted(_axis(a, out_nd) for a in axes):
+        x = np.expand_dims(x, a)
+    return x
+
+
+@_reg("Gather")
+def _gather(node, ins, opset, **kw):
+    return np.take(ins[0], np.asarray(ins[1]).astype(np.int64),
+                   axis=node.attr("axis", 0))
+
+
+@_reg("Slice")
+def _slice(node, ins, opset, **kw):
+    x = ins[0]
+    starts = _axes(node, ins, 1, "starts")
+    ends = _axes(node, ins, 2, "ends")
+    axes = _axes(node, ins, 3, "axes") or list(range(len(starts)))
+    steps = _axes(node, ins, 4, "steps") or [1] * len(starts)
+    index = [slice(None)] * x.ndim
+    for st, en, a, sp in zip(starts, ends, axes, steps):
+        index[_axis(a, x.ndim)] = slice(None if st >= 2**62 else st,
+                                        None if abs(en) >= 2**62 else en, sp)
+    return x[tuple(index)]
+
+
 @_reg("Concat")
 def _concat(node, ins, opset, **kw):
     return np.concatenate(ins, axis=node.attr("axis"))

@@ -262,6 +262,71 @@ def yolov8n_cls(seed=3, classes=1000, size=224, softmax=True):
     return b.build(x, [None, 3, size, size], y)
 
 
+def vit(seed=5, batch=32, size=224, patch=16, dim=384, depth=12, heads=6,
+        mlp=1536, classes=1000):
+    """ViT-S/16-shaped transformer (random init from the seed) in the form
+    the reference's exporter emits (``vit_from_npz.py:71-190``: patch
+    Conv, Reshape + Transpose to tokens, Concat of the class token, Add of
+    the position embedding, pre-LayerNorm blocks with a fused QKV MatMul,
+    Reshape [B, T, 3, H, hd], Transpose [2, 0, 3, 1, 4], Split + Squeeze,
+    q k^T, Softmax, att v, Transpose + Reshape back, output projection and
+    tanh-Gelu MLP with residual Adds, final LayerNorm on the class token,
+    Gemm head) after its graph passes (``graph_passes.py``): MatMul + bias
+    fused into a three-input MatMul (:66-102), the 1/sqrt(hd) attention
+    scale folded into the query columns (:292-388), the class-token Gather
+    hoisted before the final LayerNorm (:466-504); LayerNorm gains are 1
+    and biases 0, so there is no affine to fold (:391-463). ``batch`` is
+    static, as in the exported graphs."""
+    b = GraphBuilder(seed, opset=17)
+    hd = dim // heads
+    tokens = (size // patch) ** 2 + 1
+    f32 = np.float32
+
+    def ln(x):
+        return b.op("LayerNormalization",
+                    [x, b.const(np.ones(dim, f32), "ln_g"),
+                     b.const(np.zeros(dim, f32), "ln_b")],
+                    axis=-1, epsilon=1e-6)
+
+    def linear(x, k, n, q_cols=0):
+        w = b.rng.normal((k, n), np.sqrt(1.0 / k)).astype(f32)
+        bias = b.rng.normal((n,), 0.02).astype(f32)
+        if q_cols:  # folded attention scale on the query columns
+            w[:, :q_cols] *= f32(hd ** -0.5)
+            bias[:q_cols] *= f32(hd ** -0.5)
+        return b.op("MatMul", [x, b.const(w, "w"), b.const(bias, "b")])
+
+    x = b.conv("images", 3, dim, patch, patch, pad=0,
+               w_scale=np.sqrt(1.0 / (3 * patch * patch)), b_scale=0.02)
+    x = b.op("Reshape", [x, b.const(np.array([batch, dim, -1], np.int64))])
+    x = b.op("Transpose", [x], perm=[0, 2, 1])
+    cls = np.tile(b.rng.normal((1, 1, dim), 0.02).astype(f32), (batch, 1, 1))
+    x = b.op("Concat", [b.const(cls, "cls"), x], axis=1)
+    x = b.op("Add", [x, b.weight(1, tokens, dim, scale=0.02, base="pos")])
+    axis0 = b.const(np.array([0], np.int64))
+    for _ in range(depth):
+        h = ln(x)
+        qkv = linear(h, dim, 3 * dim, q_cols=dim)
+        qkv = b.op("Reshape", [qkv, b.const(
+            np.array([batch, tokens, 3, heads, hd], np.int64))])
+        qkv = b.op("Transpose", [qkv], perm=[2, 0, 3, 1, 4])
+        q, k, v = [b.op("Squeeze", [t, axis0]) for t in
+                   b.op("Split", [qkv], n_out=3, axis=0)]
+        att = b.op("MatMul", [q, b.op("Transpose", [k], perm=[0, 1, 3, 2])])
+        att = b.op("Softmax", [att], axis=-1)
+        o = b.op("Transpose", [b.op("MatMul", [att, v])], perm=[0, 2, 1, 3])
+        o = b.op("Reshape", [o, b.const(np.array([batch, tokens, dim],
+                                                 np.int64))])
+        x = b.op("Add", [x, linear(o, dim, dim)])
+        h = b.op("Gelu", [linear(ln(x), dim, mlp)], approximate="tanh")
+        x = b.op("Add", [x, linear(h, mlp, dim)])
+    x = b.op("Gather", [x, b.const(np.array(0, np.int64))], axis=1)
+    x = ln(x)
+    y = b.op("Gemm", [x, b.weight(classes, dim, scale=np.sqrt(1.0 / dim)),
+                      b.weight(classes, scale=0.01)], transB=1)
+    return b.build("images", [batch, 3, size, size], y)
+
+
 def conv_silu(seed=2, cin=64, cout=64, size=56, k=3, stride=1):
     """One Conv -> SiLU layer (the single-conv workload as a graph)."""
     b = GraphBuilder(seed)

@@ -67,6 +67,11 @@ def _declare(lib):
         "qa_d_conv": (i32, [p, p]),
         "qa_d_quantize_conv": (i32, [p, p, f64, i64, i64, i64, p]),
         "qa_d_conv_pool": (i32, [p, p, p]),
+        "qa_d_copy_nd": (i32, [p, p]),
+        "qa_d_layernorm": (i32, [p, i32, i64, i64, i64, f64, i64, i64, p, p,
+                                 f64, p, i32, i64, f64, i64, i64, i64, i64,
+                                 p]),
+        "qa_d_matmul_act": (i32, [p, p]),
         "qa_epi_plan_bytes": (i64, [i64]),
         "qa_plan_epilogue_i8": (i32, [p, p]),
         "qa_d_requantize": (i32, [p, i32, p, i32] + [i64] * 3 + [p] * 4

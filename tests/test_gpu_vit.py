@@ -1,0 +1,133 @@
+"""Transformer operators on the GPU vs the oracle pipeline: the float
+fallbacks of the integer pass (LayerNorm, activation x activation MatMul,
+Softmax over the last axis of 4-D tensors, Gather; ``quant_layers.py:195-205``)
+agree within one quantization step of the oracle on the same input, and
+every integer layer around them (weight MatMuls with fused bias / Gelu
+table / residual Add, layout views, token Concat, broadcast position Add) is
+bit-exact given the same inputs (the oracle is run with the device's
+fallback outputs substituted for its own)."""
+
+import numpy as np
+import pytest
+
+from oracle.pipeline import OraclePipeline
+from quantanything_amd import graph as G
+from quantanything_amd.container import QuantContainer
+from quantanything_amd.synth import Stream
+
+pytestmark = pytest.mark.gpu
+
+FALLBACK_OPS = ("LayerNormalization", "Softmax", "Gather")
+
+
+def _calibrated(g, quant_type, batches):
+    c = QuantContainer(g, quant_type, True)
+    c.calibrate(batches)
+    return c
+
+
+def _fallback_outputs(g):
+    return [n.outputs[0] for n in g.nodes if n.op_type in FALLBACK_OPS or (
+        n.op_type == "MatMul" and n.inputs[1] not in g.initializers)]
+
+
+def _check_against_oracle(c, g, tmp_path, x, ex, name="images"):
+    """Runs the oracle with the device's fallback outputs; returns the worst
+    fallback difference (steps) and the smallest exact fraction, and asserts
+    every other tensor bit-exact."""
+    path = tmp_path / "q.json"
+    c.save(path)
+    o = OraclePipeline(g, path)
+    fb = _fallback_outputs(g)
+    dev = {n: ex.tensors[n].to_host() for n in fb}
+    o.run(x, keep=True, overrides=dev)
+    worst, exact = 0, 1.0
+    for n in fb:
+        d = np.abs(dev[n].astype(np.int64) -
+                   o.computed[n].reshape(dev[n].shape).astype(np.int64))
+        worst, exact = max(worst, int(d.max())), min(exact,
+                                                     float((d == 0).mean()))
+    checked = 0
+    for n, t in ex.tensors.items():
+        if n in o.env and n not in fb:
+            got = t.to_host()
+            np.testing.assert_array_equal(got, o.env[n].reshape(got.shape),
+                                          err_msg=n)
+            checked += 1
+    return worst, exact, checked
+
+
+def _single_op_graph(kind, shape):
+    b = G.GraphBuilder(21, opset=17)
+    x = "x"
+    if kind == "layernorm":
+        c = shape[-1]
+        y = b.op("LayerNormalization",
+                 [x, b.weight(c, scale=0.5), b.weight(c, scale=0.2)],
+                 axis=-1, epsilon=1e-6)
+    elif kind == "matmul":  # x @ x^T over the last two axes
+        y = b.op("MatMul", [x, b.op("Transpose", [x], perm=[0, 1, 3, 2])])
+    elif kind == "matmul_nt":  # B not contiguous along K: a copy is made
+        t = b.op("Transpose", [x], perm=[0, 1, 3, 2])
+        y = b.op("MatMul", [t, x])
+    elif kind == "softmax":
+        y = b.op("Softmax", [x], axis=-1)
+    else:  # gather of token 0
+        y = b.op("Gather", [x, b.const(np.array(0, np.int64))], axis=1)
+    y = b.op("Relu", [y])  # an integer layer after the fallback
+    return b.build(x, [None] + list(shape[1:]), y)
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8", "int16"])
+@pytest.mark.parametrize("kind,shape", [
+    ("layernorm", (3, 17, 64)),
+    ("layernorm", (2, 5, 384)),
+    ("matmul", (2, 3, 17, 32)),
+    ("matmul", (1, 2, 70, 100)),
+    ("matmul_nt", (2, 2, 33, 20)),
+    ("softmax", (2, 3, 17, 17)),
+    ("gather", (3, 9, 48)),
+])
+def test_fallback_op_within_one_step(hip, tmp_path, quant_type, kind, shape):
+    g = _single_op_graph(kind, shape)
+    calib = [Stream(30 + i).normal(shape).astype(np.float32) for i in range(2)]
+    c = _calibrated(g, quant_type, calib)
+    x = Stream(40).normal(shape).astype(np.float32) * np.float32(1.1)
+    ex = c.executor({"x": x.shape})
+    ex.run({"x": x})
+    worst, exact, checked = _check_against_oracle(c, g, tmp_path, x, ex)
+    assert worst <= 1, f"{kind}: max difference {worst} steps"
+    assert exact >= 0.99, f"{kind}: only {exact:.4f} exact"
+    assert checked >= 2
+
+
+def _tiny_vit():
+    return G.vit(seed=5, batch=3, size=32, patch=8, dim=64, depth=2, heads=2,
+                 mlp=128, classes=10)
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+def test_tiny_vit_matches_oracle(hip, tmp_path, quant_type):
+    g = _tiny_vit()
+    calib = [Stream(50 + i).normal((3, 3, 32, 32)).astype(np.float32)
+             for i in range(2)]
+    c = _calibrated(g, quant_type, calib)
+    x = Stream(60).normal((3, 3, 32, 32)).astype(np.float32)
+    ex = c.executor({"images": x.shape})
+    ex.run({"images": x})
+    worst, exact, checked = _check_against_oracle(c, g, tmp_path, x, ex)
+    assert worst <= 1 and exact >= 0.98, (worst, exact)
+    assert checked >= 20
+
+
+def test_tiny_vit_graph_replay_matches_eager(hip):
+    g = _tiny_vit()
+    calib = [Stream(50).normal((3, 3, 32, 32)).astype(np.float32)]
+    c = _calibrated(g, "int8", calib)
+    ex = c.executor({"images": (3, 3, 32, 32)})
+    x = Stream(62).normal((3, 3, 32, 32)).astype(np.float32)
+    eager = ex.run({"images": x})
+    for _ in range(3):
+        got = ex.run({"images": x}, use_graph=True)
+        for k in eager:
+            np.testing.assert_array_equal(got[k], eager[k])
