@@ -114,8 +114,9 @@ int qa_synchronize(void);
  * Per output channel an offset b_off makes every value int8; K is laid out
  * in 16-byte groups padded to a multiple of 64 bytes, rows padded to a
  * multiple of 128 per group. layout 0: group kg = tap kg/CB, input channels
- * [16*(kg%CB), +16), CB = ceil(Cg/16). layout 1 (Cg <= 4, KW <= 4; inputs
- * stored 4 bytes per pixel): group ky = kernel row, byte 4*kx + c. Writes wp
+ * [16*(kg%CB), +16), CB = ceil(Cg/16). layout 1 (Cg <= 4, KW <= 16;
+ * inputs stored 4 bytes per pixel): CB = ceil(KW/4) groups per kernel row,
+ * group kg = kernel row kg / CB, byte 4*(kx - 4*(kg % CB)) + c. Writes wp
  * (qa_pack_weights_i8_size bytes), corr[c] = a_off*colsum_c +
  * K*a_off*b_off[c] and boff. Returns 0 on success, 1 when a channel spans
  * more than 255 values (use the VALU path), -1 on bad arguments;

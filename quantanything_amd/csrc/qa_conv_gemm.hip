@@ -178,8 +178,10 @@ void set_geometry(ConvArgs& a, int64_t N, int64_t C, int64_t H, int64_t W,
 void pack_geometry(int64_t Cout, int64_t Cg, int64_t KH, int64_t KW,
                    int64_t G, int layout, int64_t* CB, int64_t* KG,
                    int64_t* KGp, int64_t* rows) {
-    *CB = layout == 1 ? 1 : ceil_div(Cg, 16);
-    *KG = layout == 1 ? KH : KH * KW * *CB;
+    // layout 1: CB groups of 4 kernel columns per kernel row
+    *CB = layout == 1 ? ceil_div(std::max<int64_t>(KW, 1), 4)
+                      : ceil_div(Cg, 16);
+    *KG = layout == 1 ? KH * *CB : KH * KW * *CB;
     *KGp = round_up(std::max<int64_t>(*KG, 1), 4);
     *rows = round_up(std::max<int64_t>(Cout / G, 1), kRowPad);
 }
@@ -209,7 +211,7 @@ bool conv_shape_ok(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
 int pack_weights(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
                  int64_t KW, int64_t G, int64_t a_off, int layout, int8_t* wp,
                  int64_t* corr, int32_t* boff, int32_t* needs_rowsum) {
-    if (G <= 0 || Cout % G || Cg < 0 || (layout == 1 && (Cg > 4 || KW > 4)))
+    if (G <= 0 || Cout % G || Cg < 0 || (layout == 1 && (Cg > 4 || KW > 16)))
         return -1;
     const int64_t Cog = Cout / G;
     int64_t CB, KG, KGp, rows;
@@ -237,7 +239,8 @@ int pack_weights(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
                     const int v = row[(c * KH + ky) * KW + kx] - b;
                     colsum += v;
                     const int64_t at =
-                        layout == 1 ? ky * 16 + kx * 4 + c
+                        layout == 1 ? (ky * CB + kx / 4) * 16 +
+                                          kx % 4 * 4 + c
                                     : ((ky * KW + kx) * CB + c / 16) * 16 +
                                           c % 16;
                     dst[at] = (int8_t)v;
@@ -320,7 +323,7 @@ void conv_abi(const int32_t* x, const TW* w, void* y, int64_t N, int64_t C,
 
     int lo, hi, a_off = 0;
     if (!device_range(dx, nx, !WIDE, st, &lo, &hi)) return;
-    const int layout = (G == 1 && Cg <= 4 && KW <= 4) ? 1 : 0;
+    const int layout = (G == 1 && Cg <= 4 && KW <= 16) ? 1 : 0;
     bool mfma = K < 131072 && activation_offset(lo, hi, &a_off) &&
                 (layout == 1 || G == 1 || Cg % 16 == 0);
     if (mfma)

@@ -108,26 +108,29 @@ __device__ __forceinline__ int bytes_sum(v4i v, int nreal) {
     return s;
 }
 
-// sum of the real bytes of a layout-1 fragment: the first nreal bytes of
-// each of the first KW words
-__device__ __forceinline__ int bytes_sum_l1(v4i v, int nreal, int KW) {
-    const int mask = nreal >= 4 ? 0x01010101
-                                : (int)((1u << (8 * nreal)) - 1) & 0x01010101;
+// sum of the real bytes of a layout-1 fragment; nreal = bytes per word
+// (the channels) | real words << 8: the first bytes of the first words
+__device__ __forceinline__ int bytes_sum_l1(v4i v, int nreal) {
+    const int nb = nreal & 0xff, nw = nreal >> 8;
+    const int mask = nb >= 4 ? 0x01010101
+                             : (int)((1u << (8 * nb)) - 1) & 0x01010101;
     int s = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w)
-        if (w < KW) s = __builtin_amdgcn_sdot4(v[w], mask, s, false);
+        if (w < nw) s = __builtin_amdgcn_sdot4(v[w], mask, s, false);
     return s;
 }
 
 
 // Where k-group kg of one lane reads (layout 0: tap kg / CB, channel block
-// kg % CB; layout 1: kernel row kg): input offsets (dy, dx) from the
-// pixel's receptive-field origin and the byte offset of that position.
+// kg % CB; layout 1: kernel row kg / CB, kernel columns 4 (kg % CB) ..
+// + 3): input offsets (dy, dx) from the pixel's receptive-field origin and
+// the byte offset of that position.
 struct KTap {
     int dy, dx;
     int64_t off;
-      int nreal;  // real bytes: layout 0 of the 16, layout 1 of each word
+    int nreal;  // real bytes: layout 0 of the 16; layout 1: of each word,
+                // | real words (kernel columns) << 8
 };
 
 // Tap table entry of k-group kg (layout 0), built in LDS by each
@@ -152,10 +155,15 @@ __device__ __forceinline__ KTap ktap(const ConvArgs& a, int kg) {
         t.off = ((int64_t)t.dy * a.W + t.dx) * a.x_sp + cb * 16;
         t.nreal = kg < a.KG ? min(16, a.Cg - cb * 16) : 0;
     } else {
-        t.dy = kg * a.DH;
-        t.dx = 0;
-        t.off = (int64_t)t.dy * a.W * a.x_sp;
-        t.nreal = kg < a.KG ? a.Cg : 0;
+        int ky = kg, part = 0;
+        if (a.CB > 1) {  // kernels wider than 4 columns
+            ky = kg / a.CB;
+            part = kg - ky * a.CB;
+        }
+        t.dy = ky * a.DH;
+        t.dx = 4 * part * a.DW;
+        t.off = ((int64_t)t.dy * a.W + t.dx) * a.x_sp;
+        t.nreal = kg < a.KG ? (a.Cg | min(4, a.KW - 4 * part) << 8) : 0;
     }
     return t;
 }
@@ -177,10 +185,12 @@ __device__ __forceinline__ v4i load_b(const ConvArgs& a, const FetchPix& P,
     }
     v4i v;
     int m = 0;
+    const int nw = t.nreal >> 8;  // words inside the kernel
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const int ix = P.ix0 + k * a.DW;
-        const bool in = row_ok && (unsigned)ix < (unsigned)a.W;
+        const int ix = P.ix0 + t.dx + k * a.DW;
+        const bool in =
+            row_ok && (unsigned)ix < (unsigned)a.W && k < nw;
         if (!in) m |= 1 << k;
         v[k] = *(const int*)(in ? P.org + t.off + (int64_t)k * a.DW * a.x_sp
                                 : P.base);
@@ -690,7 +700,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
                 }
                 if (a.rowsum)
                     psum += LAYOUT == 0 ? bytes_sum(b, nr[s])
-                                        : bytes_sum_l1(b, nr[s], a.KW);
+                                        : bytes_sum_l1(b, nr[s]);
             }
             fetch(std::true_type(), af[ALDS ? 0 : s], bf[s], pd[s], nr[s]);
             if (++ci == L) {

@@ -162,7 +162,7 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
     // row sums
     const int kbase = min(kgl, a.KH - 1) * a.DH * g.RW + g.c0 - a.PW;
     const int shrw = a.SH * g.RW;
-    const int nreal = kgl < a.KH ? a.Cg : 0;
+    const int nreal = kgl < a.KH ? (a.Cg | a.KW << 8) : 0;
     const int4 hdr = *(const int4*)a.plan;
     for (int cb = 0; cb < g.CBK; ++cb) {
         const int co0 = cb * 16;
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
                 b, wf, v4i{0, 0, 0, 0}, 0, 0, 0);
             int ps[4] = {0, 0, 0, 0};
             if (a.rowsum) {
-                int psum = bytes_sum_l1(b, nreal, a.KW);
+                int psum = bytes_sum_l1(b, nreal);
                 psum += __shfl_xor(psum, 16);
                 psum += __shfl_xor(psum, 32);
 #pragma unroll

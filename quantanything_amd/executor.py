@@ -616,7 +616,7 @@ class DeviceExecutor:
             out_shape = (n, cout, oh, ow)
             geo = (n, cin, h, w, cout, kh, kw, strides[0], strides[1],
                    pads[0], pads[1], dil[0], dil[1], groups, oh, ow)
-            layout = 1 if (groups == 1 and cg <= 4 and kw <= 4 and
+            layout = 1 if (groups == 1 and cg <= 4 and kw <= 16 and
                            x.sp == 4) else 0
         else:
             k, ncol = layer.w_centered.shape

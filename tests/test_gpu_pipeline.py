@@ -237,6 +237,44 @@ def test_yolov8n_cls_int16_bit_exact(hip, tmp_path):
                     err_msg=f"{name}, pass {r}")
 
 
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+@pytest.mark.parametrize("cin,cout,k,stride,pad,size", [
+    (3, 32, 16, 16, 0, 64),   # a ViT patch embedding: 4 groups per row
+    (3, 24, 7, 2, 3, 30),     # 7x7 stem: 2 groups per row, 3 columns real
+    (4, 16, 5, 1, 2, 19),     # 5x5, padding on both sides
+    (1, 16, 8, 4, 0, 36),     # one channel, 8 columns
+])
+def test_wide_kernel_rows_layout(hip, tmp_path, quant_type, cin, cout, k,
+                                 stride, pad, size):
+    """Convolutions of <= 4 channels with kernels wider than 4 columns use
+    the row layout (ceil(KW/4) 16-byte groups per kernel row) and equal the
+    oracle for every tile code."""
+    b = G.GraphBuilder(13)
+    y = b.conv("images", cin, cout, k, stride, pad=pad,
+               w_scale=np.sqrt(1.0 / (cin * k * k)))
+    y = b.op("Relu", [y])
+    g = b.build("images", [None, cin, size, size], y)
+    calib = [Stream(70 + i).normal((2, cin, size, size)).astype(np.float32)
+             for i in range(2)]
+    c = _calibrated(g, quant_type, True, calib)
+    x = Stream(80).normal((2, cin, size, size)).astype(np.float32)
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    oracle.run(x, keep=True)
+    ex = c.executor({"images": x.shape})
+    convs = [t for t in ex.tunables if t[0].startswith("conv:")]
+    assert len(convs) == 1 and convs[0][1].w_layout == 1
+    _, d, codes, _ = convs[0]
+    for code in codes:
+        d.tile = code
+        ex.run({"images": x})
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, tile {code:#x}")
+
+
 def test_tuned_tiles_keep_results(hip):
     g = G.mini_yolo(seed=0)
     calib = [_images(1 + i, 4, 32) for i in range(3)]
