@@ -264,21 +264,22 @@ int qa_d_layernorm(const void* x, int x_code, int64_t x_rstride,
 /* MatMul of two activations, the reference's float fallback
  * (float_ops.py:181-186): C[b0, b1, m, n] = quantize(sum_k A[b0, b1, m, k] *
  * B[b0, b1, k, n]) with A, B dequantized. B is passed transposed, as Bt[b0,
- * b1, n, k] at b + b0*b_s0 + b1*b_s1 + n*b_sn + k; A at a + b0*a_s0 +
- * b1*a_s1 + m*a_sm + k (unit stride along k for both). The exact integer
+ * b1, n, k] at b + b0*b_s0 + b1*b_s1 + n*b_sn + k*b_sk; A at a + b0*a_s0
+ * + b1*a_s1 + m*a_sm + k*a_sk. The exact integer
  * sum of (a - a_zp)(b - b_zp) is scaled once by a_scale * b_scale (float32
  * result), which agrees with the reference's float32 matmul within one
  * output quantization step. int8 or int16 storage (the same for A and B),
- * K < 2^17. */
+ * K < 2^17. a_sk / b_sk: the element strides along k (1 for the layouts
+ * above; any value is accepted). */
 typedef struct qa_matmul_desc {
     const void* a;
     int64_t a_code, a_so, a_zp;
     double a_scale;
-    int64_t a_s0, a_s1, a_sm;
+    int64_t a_s0, a_s1, a_sm, a_sk;
     const void* b;
     int64_t b_code, b_so, b_zp;
     double b_scale;
-    int64_t b_s0, b_s1, b_sn;
+    int64_t b_s0, b_s1, b_sn, b_sk;
     int64_t B0, B1, M, N, K;
     void* y;
     int64_t y_code, y_so, y_s0, y_s1, y_sm, y_sn;

@@ -58,7 +58,12 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// One wave per row.
+// One wave per row; rows of at most 64 * 8 values are read once and held in
+// registers, longer rows are read again for each pass. The statistics are
+// float64 sums in lane order then across lanes (the reference sums in
+// NumPy's order: results agree within one step).
+constexpr int LN_PER = 8;
+
 __global__ __launch_bounds__(kThreads) void k_layernorm(
     const void* __restrict__ x, int x_code, int64_t x_rs, int64_t rows,
     int64_t cols, double in_scale, int64_t in_zp, int64_t x_so,
@@ -67,28 +72,53 @@ __global__ __launch_bounds__(kThreads) void k_layernorm(
     double out_scale, int64_t out_zp, int64_t qmin, int64_t qmax,
     int64_t y_so) {
     const int lane = threadIdx.x & 63;
+    const double inv = 1.0 / out_scale;
+    const bool held = cols <= 64 * LN_PER;
     for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows;
          r += (int64_t)gridDim.x * 4) {
         auto value = [&](int64_t i) {
             return (double)dequant_f32(load_any(x, x_code, r * x_rs + i) + x_so,
                                        in_zp, in_scale);
         };
+        auto emit = [&](int64_t i, double v, double mean, double sd) {
+            double t = (v - mean) / sd * (double)gamma[i];
+            if (beta) t += (double)beta[i];
+            const int64_t q = qa_quantize_one_fast((float)t, out_scale, inv,
+                                                   out_zp, qmin, qmax);
+            store_any(y, y_code, r * y_rs + i, q - y_so);
+        };
+        if (held) {
+            double v[LN_PER];
+            double s = 0.0;
+#pragma unroll
+            for (int k = 0; k < LN_PER; ++k) {
+                const int64_t i = lane + 64 * k;
+                v[k] = i < cols ? value(i) : 0.0;
+                s += v[k];
+            }
+            const double mean = wave_sum(s) / (double)cols;
+            double q2 = 0.0;
+#pragma unroll
+            for (int k = 0; k < LN_PER; ++k) {
+                const double t = v[k] - mean;
+                if (lane + 64 * k < cols) q2 += t * t;
+            }
+            const double sd = sqrt(wave_sum(q2) / (double)cols + eps);
+#pragma unroll
+            for (int k = 0; k < LN_PER; ++k)
+                if (lane + 64 * k < cols) emit(lane + 64 * k, v[k], mean, sd);
+            continue;
+        }
         double s = 0.0;
         for (int64_t i = lane; i < cols; i += 64) s += value(i);
         const double mean = wave_sum(s) / (double)cols;
-        double v = 0.0;
+        double q2 = 0.0;
         for (int64_t i = lane; i < cols; i += 64) {
             const double t = value(i) - mean;
-            v += t * t;
+            q2 += t * t;
         }
-        const double sd = sqrt(wave_sum(v) / (double)cols + eps);
-        for (int64_t i = lane; i < cols; i += 64) {
-            double t = (value(i) - mean) / sd * (double)gamma[i];
-            if (beta) t += (double)beta[i];
-            const int64_t q =
-                qa_quantize_one((float)t, out_scale, out_zp, qmin, qmax);
-            store_any(y, y_code, r * y_rs + i, q - y_so);
-        }
+        const double sd = sqrt(wave_sum(q2) / (double)cols + eps);
+        for (int64_t i = lane; i < cols; i += 64) emit(i, value(i), mean, sd);
     }
 }
 
@@ -118,13 +148,27 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act(qa_matmul_desc d) {
     int32_t acc32[4][4] = {};
     int32_t rs[4] = {0, 0, 0, 0}, cs[4] = {0, 0, 0, 0};  // stored sums
     for (int64_t k0 = 0; k0 < d.K; k0 += KC) {
-        // stage: 64 rows x KC elements of each operand, zero past the ends
+        // stage: 64 rows x KC elements of each operand, zero past the ends;
+        // consecutive threads walk the operand's unit-stride axis
         for (int e = tid; e < 64 * KC; e += kThreads) {
-            const int r = e / KC, c = e - r * KC;
-            const int64_t k = k0 + c;
-            const int64_t m = m0 + r, n = n0 + r;
-            sa[r][c] = (m < d.M && k < d.K) ? A[m * d.a_sm + k] : (T)0;
-            sb[r][c] = (n < d.N && k < d.K) ? B[n * d.b_sn + k] : (T)0;
+            int r = e / KC, c = e - r * KC;
+            if (d.a_sk != 1) {
+                c = e / 64;
+                r = e - c * 64;
+            }
+            const int64_t m = m0 + r, k = k0 + c;
+            sa[r][c] =
+                (m < d.M && k < d.K) ? A[m * d.a_sm + k * d.a_sk] : (T)0;
+        }
+        for (int e = tid; e < 64 * KC; e += kThreads) {
+            int r = e / KC, c = e - r * KC;
+            if (d.b_sk != 1) {
+                c = e / 64;
+                r = e - c * 64;
+            }
+            const int64_t n = n0 + r, k = k0 + c;
+            sb[r][c] =
+                (n < d.N && k < d.K) ? B[n * d.b_sn + k * d.b_sk] : (T)0;
         }
         __syncthreads();
         if (I8) {
@@ -184,6 +228,139 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act(qa_matmul_desc d) {
             const float yf = (float)((double)v * scale);
             const int64_t q =
                 qa_quantize_one(yf, d.out_scale, d.out_zp, d.qmin, d.qmax);
+            store_any(d.y, (int)d.y_code,
+                      b0 * d.y_s0 + b1 * d.y_s1 + m * d.y_sm + n * d.y_sn,
+                      q - d.y_so);
+        }
+    }
+}
+
+// int8 operands on the matrix cores. A work-group owns one (b0, b1) pair
+// and 64 rows of C (16 per wave) and all N columns: it stages its A rows and
+// all of Bt ([N, K]) in LDS, K zero-padded to a multiple of 64, then each
+// wave runs v_mfma_i32_16x16x64_i8 over its 16 rows x every 16-column tile
+// (lane l supplies row / column l % 16, bytes 16 (l / 16) .. + 15 of the
+// 64-byte K-step; result register r of lane l is row 4 (l / 16) + r,
+// column l % 16). Centring by row / column sums as k_matmul_act.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+template <bool SUMS>
+__global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
+    qa_matmul_desc d, int Kp, int Np) {
+    extern __shared__ int4 lds4[];
+    int8_t* lds = (int8_t*)lds4;
+    const int RS = Kp + 16;  // LDS row stride (bytes)
+    int8_t* sa = lds;                    // [64][RS]
+    int8_t* sb = lds + 64 * RS;          // [Np][RS]
+    int* ssum = (int*)(sb + Np * RS);    // [64 + Np] row / column sums
+    const int tid = threadIdx.x;
+    const int64_t bz = blockIdx.y;
+    const int64_t b0 = bz / d.B1, b1 = bz - b0 * d.B1;
+    const int64_t m0 = (int64_t)blockIdx.x * 64;
+    const int8_t* A = (const int8_t*)d.a + b0 * d.a_s0 + b1 * d.a_s1;
+    const int8_t* B = (const int8_t*)d.b + b0 * d.b_s0 + b1 * d.b_s1;
+    // stage rows [r0, r0 + rows) of an operand (element (r, c) at
+    // src[r * rs + c * ks]) as dst[r][c], zero past rlim / K: 16-byte loads
+    // along a unit-stride axis when it is aligned, else byte loads, 8 in
+    // flight per thread
+    auto stage = [&](int8_t* dst, const int8_t* src, int rows, int64_t r0,
+                     int64_t rlim, int64_t rs, int64_t ks) {
+        const bool al = ((uintptr_t)src & 15) == 0;
+        if (ks == 1 && al && rs % 16 == 0 && d.K % 16 == 0) {
+            const int cpr = Kp / 16;  // 16-byte chunks per row
+            for (int e = tid; e < rows * cpr; e += kThreads) {
+                const int r = e / cpr, c = (e - r * cpr) * 16;
+                const int64_t rr = r0 + r;
+                int4 v = {0, 0, 0, 0};
+                if (rr < rlim && c < d.K)
+                    v = *(const int4*)(src + rr * rs + c);
+                *(int4*)(dst + r * RS + c) = v;
+            }
+            return;
+        }
+        if (rs == 1 && al && ks % 16 == 0 && rows % 16 == 0 &&
+            (r0 + rows <= rlim || rlim % 16 == 0)) {
+            // 16 consecutive rows of one column per load, scattered to LDS
+            const int rpc = rows / 16;
+            for (int e = tid; e < rpc * Kp; e += kThreads) {
+                const int c = e / rpc, r = (e - c * rpc) * 16;
+                const int64_t rr = r0 + r;
+                int4 v = {0, 0, 0, 0};
+                if (rr < rlim && c < d.K)
+                    v = *(const int4*)(src + rr + (int64_t)c * ks);
+                const int8_t* b = (const int8_t*)&v;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) dst[(r + j) * RS + c] = b[j];
+            }
+            return;
+        }
+        const int n = rows * Kp;
+        for (int e0 = tid; e0 < n; e0 += 8 * kThreads) {
+            int8_t v[8];
+            int at[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int e = e0 + j * kThreads;
+                int r = e / Kp, c = e - r * Kp;
+                if (ks != 1) {
+                    c = e / rows;
+                    r = e - c * rows;
+                }
+                const int64_t rr = r0 + r;
+                at[j] = e < n ? r * RS + c : -1;
+                v[j] = (e < n && rr < rlim && c < d.K)
+                           ? src[rr * rs + (int64_t)c * ks]
+                           : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (at[j] >= 0) dst[at[j]] = v[j];
+        }
+    };
+    stage(sa, A, 64, m0, d.M, d.a_sm, d.a_sk);
+    stage(sb, B, Np, 0, d.N, d.b_sn, d.b_sk);
+    __syncthreads();
+    if (SUMS) {
+        for (int r = tid; r < 64 + Np; r += kThreads) {
+            const int8_t* row = r < 64 ? sa + r * RS : sb + (r - 64) * RS;
+            int acc = 0;
+            for (int c = 0; c < Kp; c += 4)
+                acc = __builtin_amdgcn_sdot4(*(const int*)(row + c),
+                                             0x01010101, acc, false);
+            ssum[r] = acc;
+        }
+        __syncthreads();
+    }
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, kg = lane >> 4;
+    const int64_t a_add = d.a_so - d.a_zp, b_add = d.b_so - d.b_zp;
+    const double scale = d.a_scale * d.b_scale;
+    const double inv = 1.0 / d.out_scale;
+    const int mr = wave * 16;  // the wave's 16 rows within the block
+    if (m0 + mr >= d.M) return;
+    const int ksteps = Kp / 64;
+    for (int nt = 0; nt < Np; nt += 16) {
+        v4i_t acc = {0, 0, 0, 0};
+        for (int ks = 0; ks < ksteps; ++ks) {
+            const int c = ks * 64 + kg * 16;
+            const v4i_t fa = *(const v4i_t*)(sa + (mr + col) * RS + c);
+            const v4i_t fb = *(const v4i_t*)(sb + (nt + col) * RS + c);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa, fb, acc, 0, 0, 0);
+        }
+        const int64_t n = nt + col;
+        if (n >= d.N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int ml = mr + 4 * kg + r;
+            const int64_t m = m0 + ml;
+            if (m >= d.M) continue;
+            int64_t v = acc[r];
+            if (SUMS)
+                v += a_add * ssum[64 + n] + b_add * ssum[ml] +
+                     d.K * a_add * b_add;
+            const float yf = (float)((double)v * scale);
+            const int64_t q = qa_quantize_one_fast(yf, d.out_scale, inv,
+                                                   d.out_zp, d.qmin, d.qmax);
             store_any(d.y, (int)d.y_code,
                       b0 * d.y_s0 + b1 * d.y_s1 + m * d.y_sm + n * d.y_sn,
                       q - d.y_so);
@@ -263,9 +440,27 @@ QA_API int qa_d_matmul_act(const qa_matmul_desc* d, void* stream) {
         return -1;
     }
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)gz);
-    if (d->a_code == 1)
-        k_matmul_act<int8_t><<<grid, kThreads, 0, (hipStream_t)stream>>>(*d);
-    else
+    if (d->a_code == 1) {
+        // matrix cores when the block's operands fit in LDS
+        const int64_t Kp = round_up(std::max<int64_t>(d->K, 1), 64);
+        const int64_t Np = round_up(d->N, 16);
+        const int64_t bytes = (64 + Np) * (Kp + 16) + (64 + Np) * 4;
+        if (bytes <= 64 * 1024 && ceil_div(d->M, 64) <= 65535) {
+            const dim3 g2((unsigned)ceil_div(d->M, 64), (unsigned)gz);
+            const bool sums = d->a_so != d->a_zp || d->b_so != d->b_zp;
+            if (sums)
+                k_matmul_act_mfma<true><<<g2, kThreads, bytes,
+                                          (hipStream_t)stream>>>(
+                    *d, (int)Kp, (int)Np);
+            else
+                k_matmul_act_mfma<false><<<g2, kThreads, bytes,
+                                           (hipStream_t)stream>>>(
+                    *d, (int)Kp, (int)Np);
+        } else {
+            k_matmul_act<int8_t><<<grid, kThreads, 0, (hipStream_t)stream>>>(
+                *d);
+        }
+    } else
         k_matmul_act<int16_t><<<grid, kThreads, 0, (hipStream_t)stream>>>(*d);
     return launched("qa_d_matmul_act") ? 0 : -1;
 }

@@ -2,6 +2,8 @@
 // GlobalAveragePool (integer sum + requantize, quant_layers.py:563-590) and
 // the float Softmax fallback (dequantize -> float64 softmax -> quantize,
 // quant_layers.py:195-205 with float_ops.py:380-385).
+#include <algorithm>
+
 #include "qa_common.h"
 
 namespace {
@@ -261,6 +263,75 @@ __global__ __launch_bounds__(kThreads) void k_softmax(
     }
 }
 
+// Rows of at most 64 * SOFTMAX_PER values: one wave per row (4 rows per
+// work-group), the row held in registers, reductions by lane shuffles (no
+// LDS, no barrier). Same float32 inputs, float64 exponentials and sums and
+// quantization as k_softmax; only the summation order differs.
+__global__ __launch_bounds__(kThreads) void k_softmax_rows(
+    const void* __restrict__ x, int in_code, int64_t rows, int64_t cols,
+    double in_scale, int64_t in_zp, int64_t in_so, void* out, int out_code,
+    double out_scale, int64_t out_zp, int64_t qmin, int64_t qmax,
+    int64_t out_so, float* __restrict__ outf) {
+    const int lane = threadIdx.x & 63;
+    const double inv = 1.0 / out_scale;
+    for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows;
+         r += (int64_t)gridDim.x * 4) {
+        const int64_t base = r * cols;
+        float xf[SOFTMAX_PER];
+        double mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < SOFTMAX_PER; ++k) {
+            const int64_t i = lane + 64 * k;
+            xf[k] = i < cols
+                        ? (float)((double)(load_s(x, in_code, base + i) +
+                                           in_so - in_zp) *
+                                  in_scale)
+                        : 0.0f;
+            if (i < cols) mx = fmax(mx, (double)xf[k]);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
+        double e[SOFTMAX_PER], sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < SOFTMAX_PER; ++k) {
+            e[k] = lane + 64 * k < cols ? exp((double)xf[k] - mx) : 0.0;
+            sum += e[k];
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+#pragma unroll
+        for (int k = 0; k < SOFTMAX_PER; ++k) {
+            const int64_t i = lane + 64 * k;
+            if (i >= cols) continue;
+            const float y = (float)(e[k] / sum);
+            const int64_t q =
+                qa_quantize_one_fast(y, out_scale, inv, out_zp, qmin, qmax);
+            store_s(out, out_code, base + i, q - out_so);
+            if (outf) outf[base + i] = (float)((double)(q - out_zp) * out_scale);
+        }
+    }
+}
+
+bool softmax_launch(const void* x, int in_code, int64_t rows, int64_t cols,
+                    double in_scale, int64_t in_zp, int64_t in_so, void* out,
+                    int out_code, double out_scale, int64_t out_zp,
+                    int64_t qmin, int64_t qmax, int64_t out_so, float* outf,
+                    hipStream_t st) {
+    if (cols <= 64 * SOFTMAX_PER) {
+        const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
+        k_softmax_rows<<<(unsigned)blocks, kThreads, 0, st>>>(
+            x, in_code, rows, cols, in_scale, in_zp, in_so, out, out_code,
+            out_scale, out_zp, qmin, qmax, out_so, outf);
+    } else {
+        const unsigned blocks = (unsigned)(rows < 65535 ? rows : 65535);
+        k_softmax<<<blocks, kThreads, 0, st>>>(x, in_code, rows, cols,
+                                               in_scale, in_zp, in_so, out,
+                                               out_code, out_scale, out_zp,
+                                               qmin, qmax, out_so, outf);
+    }
+    return true;
+}
+
 bool launched(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -358,12 +429,9 @@ QA_API int qa_d_softmax(const void* x, int in_code, int64_t rows, int64_t cols,
                         int64_t out_zp, int64_t qmin, int64_t qmax,
                         int64_t out_so, void* stream) {
     if (rows <= 0 || cols <= 0) return 0;
-    hipStream_t st = (hipStream_t)stream;
-    const unsigned blocks = (unsigned)(rows < 65535 ? rows : 65535);
-    k_softmax<<<blocks, kThreads, 0, st>>>(x, in_code, rows, cols, in_scale,
-                                           in_zp, in_so, out, out_code,
-                                           out_scale, out_zp, qmin, qmax,
-                                           out_so, nullptr);
+    softmax_launch(x, in_code, rows, cols, in_scale, in_zp, in_so, out,
+                   out_code, out_scale, out_zp, qmin, qmax, out_so, nullptr,
+                   (hipStream_t)stream);
     return launched("qa_d_softmax") ? 0 : -1;
 }
 
@@ -380,11 +448,8 @@ QA_API int qa_d_softmax_f32(const void* x, int in_code, int64_t rows,
         qa::set_error("qa_d_softmax_f32", "no float output");
         return -1;
     }
-    hipStream_t st = (hipStream_t)stream;
-    const unsigned blocks = (unsigned)(rows < 65535 ? rows : 65535);
-    k_softmax<<<blocks, kThreads, 0, st>>>(x, in_code, rows, cols, in_scale,
-                                           in_zp, in_so, out, out_code,
-                                           out_scale, out_zp, qmin, qmax,
-                                           out_so, out_f32);
+    softmax_launch(x, in_code, rows, cols, in_scale, in_zp, in_so, out,
+                   out_code, out_scale, out_zp, qmin, qmax, out_so, out_f32,
+                   (hipStream_t)stream);
     return launched("qa_d_softmax_f32") ? 0 : -1;
 }

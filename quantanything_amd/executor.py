@@ -217,11 +217,11 @@ class MatmulDesc(ctypes.Structure):
 
     _fields_ = ([("a", _P)] + [(n, _I64) for n in ("a_code", "a_so", "a_zp")]
                 + [("a_scale", ctypes.c_double)]
-                + [(n, _I64) for n in ("a_s0", "a_s1", "a_sm")]
+                + [(n, _I64) for n in ("a_s0", "a_s1", "a_sm", "a_sk")]
                 + [("b", _P)] + [(n, _I64) for n in ("b_code", "b_so", "b_zp")]
                 + [("b_scale", ctypes.c_double)]
-                + [(n, _I64) for n in ("b_s0", "b_s1", "b_sn", "B0", "B1", "M",
-                                       "N", "K")]
+                + [(n, _I64) for n in ("b_s0", "b_s1", "b_sn", "b_sk", "B0",
+                                       "B1", "M", "N", "K")]
                 + [("y", _P)] + [(n, _I64) for n in ("y_code", "y_so", "y_s0",
                                                      "y_s1", "y_sm", "y_sn")]
                 + [("out_scale", ctypes.c_double)]
@@ -387,6 +387,20 @@ class DeviceExecutor:
         self._add(name, lambda s, d=d: _ok(self.lib.qa_d_copy_nd(
             ctypes.byref(d), s), "qa_d_copy_nd"))
 
+    def _new_for_users(self, name, shape, qp):
+        """A dense output, laid out in the order its only consumer, a
+        Transpose, reads it (so that the Transpose and a following Reshape
+        are views rather than copies)."""
+        users = self._cons.get(name, [])
+        if name not in self.graph.outputs and len(users) == 1 and \
+                users[0].node.op_type == "Transpose" and \
+                users[0].kind == "shape":
+            perm = users[0].node.attr("perm") or \
+                list(range(len(shape)))[::-1]
+            t = self._new([shape[p] for p in perm], qp, dense=True)
+            return t.derived(t.meta().permute(*np.argsort(perm).tolist()))
+        return self._new(shape, qp, dense=True)
+
     def _contiguous(self, name, x):
         """x itself when row-major dense, else a dense copy."""
         if x.row_major():
@@ -448,6 +462,7 @@ class DeviceExecutor:
         for l in layers:
             for i in l.data_inputs:
                 cons.setdefault(i, []).append(l)
+        self._cons = cons
         absorbed = set()
         for layer in layers:
             if layer.name in absorbed:
@@ -1135,20 +1150,16 @@ class DeviceExecutor:
                 f"MatMul of {a.shape} and {b.shape} on the device")
         if a.code != b.code:
             raise NotImplementedError("MatMul of mixed storage")
-        # A with unit stride along K; B passed transposed (unit stride on K)
-        if a.nd_strides[-1] != 1 and a.shape[-1] > 1:
-            a = self._contiguous(f"copy:{layer.name}", a)
+        # any strides: the kernel stages both operands through LDS; B is
+        # described transposed ([.., N, K])
         bt = b.derived(b.meta().transpose(-1, -2))
-        if bt.nd_strides[-1] != 1 and bt.shape[-1] > 1:
-            btc = self._new(bt.shape, b.qp, dense=True)
-            self._copy(f"copy:{layer.name}", bt, btc)
-            bt = btc
         lead = a.shape[:-2]
         batch = (1,) * (2 - len(lead)) + tuple(lead)
         M, K = a.shape[-2:]
         N = b.shape[-1]
         o = layer.out_qp[0]
-        y = self._new(tuple(lead) + (M, N), o, dense=True)
+        y = self._new_for_users(layer.node.outputs[0],
+                                tuple(lead) + (M, N), o)
 
         def bstr(t):
             st = t.nd_strides[:-2]
@@ -1157,10 +1168,12 @@ class DeviceExecutor:
         d = MatmulDesc()
         d.a, d.a_code, d.a_so, d.a_zp, d.a_scale = a.ptr, a.code, a.so, \
             qa_.zp, qa_.scale
-        (d.a_s0, d.a_s1), d.a_sm = bstr(a), a.nd_strides[-2]
+        (d.a_s0, d.a_s1), d.a_sm, d.a_sk = bstr(a), a.nd_strides[-2], \
+            a.nd_strides[-1]
         d.b, d.b_code, d.b_so, d.b_zp, d.b_scale = bt.ptr, bt.code, bt.so, \
             qb_.zp, qb_.scale
-        (d.b_s0, d.b_s1), d.b_sn = bstr(bt), bt.nd_strides[-2]
+        (d.b_s0, d.b_s1), d.b_sn, d.b_sk = bstr(bt), bt.nd_strides[-2], \
+            bt.nd_strides[-1]
         d.B0, d.B1, d.M, d.N, d.K = batch[0], batch[1], M, N, K
         d.y, d.y_code, d.y_so = y.ptr, y.code, y.so
         (d.y_s0, d.y_s1), d.y_sm, d.y_sn = bstr(y), y.nd_strides[-2], \
