@@ -52,18 +52,19 @@ __global__ __launch_bounds__(kThreads) void k_copy_nd(qa_nd_copy d,
 }
 
 // ----------------------------------------------------------- LayerNorm --
-__device__ __forceinline__ double wave_sum(double v) {
+// GS lanes per row (64 / GS rows per wave): rows of at most GS * PER values
+// are read once and held in registers; longer rows (GS = 64, PER = 0) are
+// read again for each pass. The statistics are float64 sums in lane order
+// then across the lane group (the reference sums in NumPy's order: results
+// agree within one step).
+template <int GS>
+__device__ __forceinline__ double group_sum(double v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    for (int o = GS / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
 }
 
-// One wave per row; rows of at most 64 * 8 values are read once and held in
-// registers, longer rows are read again for each pass. The statistics are
-// float64 sums in lane order then across lanes (the reference sums in
-// NumPy's order: results agree within one step).
-constexpr int LN_PER = 8;
-
+template <int GS, int PER>
 __global__ __launch_bounds__(kThreads) void k_layernorm(
     const void* __restrict__ x, int x_code, int64_t x_rs, int64_t rows,
     int64_t cols, double in_scale, int64_t in_zp, int64_t x_so,
@@ -71,54 +72,61 @@ __global__ __launch_bounds__(kThreads) void k_layernorm(
     double eps, void* __restrict__ y, int y_code, int64_t y_rs,
     double out_scale, int64_t out_zp, int64_t qmin, int64_t qmax,
     int64_t y_so) {
+    constexpr int RPW = 64 / GS;
     const int lane = threadIdx.x & 63;
+    const int gl = lane % GS;
     const double inv = 1.0 / out_scale;
-    const bool held = cols <= 64 * LN_PER;
-    for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows;
-         r += (int64_t)gridDim.x * 4) {
+    const int64_t first =
+        ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / GS;
+    for (int64_t r = first; r - lane / GS < rows;
+         r += (int64_t)gridDim.x * 4 * RPW) {
+        const bool live = r < rows;
+        const int64_t rr = live ? r : 0;
         auto value = [&](int64_t i) {
-            return (double)dequant_f32(load_any(x, x_code, r * x_rs + i) + x_so,
-                                       in_zp, in_scale);
+            return (double)dequant_f32(
+                load_any(x, x_code, rr * x_rs + i) + x_so, in_zp, in_scale);
         };
         auto emit = [&](int64_t i, double v, double mean, double sd) {
             double t = (v - mean) / sd * (double)gamma[i];
             if (beta) t += (double)beta[i];
             const int64_t q = qa_quantize_one_fast((float)t, out_scale, inv,
                                                    out_zp, qmin, qmax);
-            store_any(y, y_code, r * y_rs + i, q - y_so);
+            store_any(y, y_code, rr * y_rs + i, q - y_so);
         };
-        if (held) {
-            double v[LN_PER];
+        if (PER > 0) {
+            double v[PER > 0 ? PER : 1];
             double s = 0.0;
 #pragma unroll
-            for (int k = 0; k < LN_PER; ++k) {
-                const int64_t i = lane + 64 * k;
+            for (int k = 0; k < PER; ++k) {
+                const int64_t i = gl + GS * k;
                 v[k] = i < cols ? value(i) : 0.0;
                 s += v[k];
             }
-            const double mean = wave_sum(s) / (double)cols;
+            const double mean = group_sum<GS>(s) / (double)cols;
             double q2 = 0.0;
 #pragma unroll
-            for (int k = 0; k < LN_PER; ++k) {
+            for (int k = 0; k < PER; ++k) {
                 const double t = v[k] - mean;
-                if (lane + 64 * k < cols) q2 += t * t;
+                if (gl + GS * k < cols) q2 += t * t;
             }
-            const double sd = sqrt(wave_sum(q2) / (double)cols + eps);
+            const double sd = sqrt(group_sum<GS>(q2) / (double)cols + eps);
+            if (!live) continue;
 #pragma unroll
-            for (int k = 0; k < LN_PER; ++k)
-                if (lane + 64 * k < cols) emit(lane + 64 * k, v[k], mean, sd);
+            for (int k = 0; k < PER; ++k)
+                if (gl + GS * k < cols) emit(gl + GS * k, v[k], mean, sd);
             continue;
         }
         double s = 0.0;
-        for (int64_t i = lane; i < cols; i += 64) s += value(i);
-        const double mean = wave_sum(s) / (double)cols;
+        for (int64_t i = gl; i < cols; i += GS) s += value(i);
+        const double mean = group_sum<GS>(s) / (double)cols;
         double q2 = 0.0;
-        for (int64_t i = lane; i < cols; i += 64) {
+        for (int64_t i = gl; i < cols; i += GS) {
             const double t = value(i) - mean;
             q2 += t * t;
         }
-        const double sd = sqrt(wave_sum(q2) / (double)cols + eps);
-        for (int64_t i = lane; i < cols; i += 64) emit(i, value(i), mean, sd);
+        const double sd = sqrt(group_sum<GS>(q2) / (double)cols + eps);
+        if (!live) continue;
+        for (int64_t i = gl; i < cols; i += GS) emit(i, value(i), mean, sd);
     }
 }
 
@@ -417,10 +425,20 @@ QA_API int qa_d_layernorm(const void* x, int x_code, int64_t x_rstride,
         set_error("qa_d_layernorm", "bad arguments");
         return -1;
     }
-    const int64_t blocks = std::min<int64_t>(ceil_div(rows, 4), 65535);
-    k_layernorm<<<(unsigned)blocks, kThreads, 0, (hipStream_t)stream>>>(
-        x, x_code, x_rstride, rows, cols, in_scale, in_zp, x_so, gamma, beta,
-        eps, y, y_code, y_rstride, out_scale, out_zp, qmin, qmax, y_so);
+    hipStream_t st = (hipStream_t)stream;
+    if (cols <= 32 * 16) {  // 32 lanes a row, 2 rows a wave
+        const int64_t blocks = std::min<int64_t>(ceil_div(rows, 8), 65535);
+        k_layernorm<32, 16><<<(unsigned)blocks, kThreads, 0, st>>>(
+            x, x_code, x_rstride, rows, cols, in_scale, in_zp, x_so, gamma,
+            beta, eps, y, y_code, y_rstride, out_scale, out_zp, qmin, qmax,
+            y_so);
+    } else {
+        const int64_t blocks = std::min<int64_t>(ceil_div(rows, 4), 65535);
+        k_layernorm<64, 0><<<(unsigned)blocks, kThreads, 0, st>>>(
+            x, x_code, x_rstride, rows, cols, in_scale, in_zp, x_so, gamma,
+            beta, eps, y, y_code, y_rstride, out_scale, out_zp, qmin, qmax,
+            y_so);
+    }
     return launched("qa_d_layernorm") ? 0 : -1;
 }
 

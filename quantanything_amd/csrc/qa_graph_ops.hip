@@ -263,45 +263,54 @@ __global__ __launch_bounds__(kThreads) void k_softmax(
     }
 }
 
-// Rows of at most 64 * SOFTMAX_PER values: one wave per row (4 rows per
-// work-group), the row held in registers, reductions by lane shuffles (no
-// LDS, no barrier). Same float32 inputs, float64 exponentials and sums and
-// quantization as k_softmax; only the summation order differs.
+// Rows of at most GS * PER values: GS lanes per row (64 / GS rows per
+// wave, 4 waves per work-group), the row held in registers, reductions by
+// lane shuffles within the lane group (no LDS, no barrier). Same float32
+// inputs, float64 exponentials and sums and quantization as k_softmax; the
+// maximum is taken over the float32 values (exact), and only the summation
+// order differs.
+template <int GS, int PER>
 __global__ __launch_bounds__(kThreads) void k_softmax_rows(
     const void* __restrict__ x, int in_code, int64_t rows, int64_t cols,
     double in_scale, int64_t in_zp, int64_t in_so, void* out, int out_code,
     double out_scale, int64_t out_zp, int64_t qmin, int64_t qmax,
     int64_t out_so, float* __restrict__ outf) {
+    constexpr int RPW = 64 / GS;  // rows per wave
     const int lane = threadIdx.x & 63;
+    const int gl = lane % GS;
     const double inv = 1.0 / out_scale;
-    for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows;
-         r += (int64_t)gridDim.x * 4) {
-        const int64_t base = r * cols;
-        float xf[SOFTMAX_PER];
-        double mx = -INFINITY;
+    const int64_t first = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW +
+                          lane / GS;
+    for (int64_t r = first; r - lane / GS < rows;
+         r += (int64_t)gridDim.x * 4 * RPW) {
+        const bool live = r < rows;
+        const int64_t base = (live ? r : 0) * cols;
+        float xf[PER];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < SOFTMAX_PER; ++k) {
-            const int64_t i = lane + 64 * k;
-            xf[k] = i < cols
+        for (int k = 0; k < PER; ++k) {
+            const int64_t i = gl + GS * k;
+            xf[k] = live && i < cols
                         ? (float)((double)(load_s(x, in_code, base + i) +
                                            in_so - in_zp) *
                                   in_scale)
-                        : 0.0f;
-            if (i < cols) mx = fmax(mx, (double)xf[k]);
+                        : -INFINITY;
+            mx = fmaxf(mx, xf[k]);
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
-        double e[SOFTMAX_PER], sum = 0.0;
+        for (int o = GS / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        double e[PER], sum = 0.0;
 #pragma unroll
-        for (int k = 0; k < SOFTMAX_PER; ++k) {
-            e[k] = lane + 64 * k < cols ? exp((double)xf[k] - mx) : 0.0;
+        for (int k = 0; k < PER; ++k) {
+            e[k] = gl + GS * k < cols ? exp((double)xf[k] - (double)mx) : 0.0;
             sum += e[k];
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        for (int o = GS / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (!live) continue;
 #pragma unroll
-        for (int k = 0; k < SOFTMAX_PER; ++k) {
-            const int64_t i = lane + 64 * k;
+        for (int k = 0; k < PER; ++k) {
+            const int64_t i = gl + GS * k;
             if (i >= cols) continue;
             const float y = (float)(e[k] / sum);
             const int64_t q =
@@ -317,9 +326,14 @@ bool softmax_launch(const void* x, int in_code, int64_t rows, int64_t cols,
                     int out_code, double out_scale, int64_t out_zp,
                     int64_t qmin, int64_t qmax, int64_t out_so, float* outf,
                     hipStream_t st) {
-    if (cols <= 64 * SOFTMAX_PER) {
+    if (cols <= 16 * 16) {  // 16 lanes a row, 4 rows a wave
+        const int64_t blocks = std::min<int64_t>((rows + 15) / 16, 65535);
+        k_softmax_rows<16, 16><<<(unsigned)blocks, kThreads, 0, st>>>(
+            x, in_code, rows, cols, in_scale, in_zp, in_so, out, out_code,
+            out_scale, out_zp, qmin, qmax, out_so, outf);
+    } else if (cols <= 64 * SOFTMAX_PER) {
         const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
-        k_softmax_rows<<<(unsigned)blocks, kThreads, 0, st>>>(
+        k_softmax_rows<64, SOFTMAX_PER><<<(unsigned)blocks, kThreads, 0, st>>>(
             x, in_code, rows, cols, in_scale, in_zp, in_so, out, out_code,
             out_scale, out_zp, qmin, qmax, out_so, outf);
     } else {
