@@ -54,6 +54,8 @@ def parse():
     p.add_argument("--tiles", metavar="JSON",
                    help="fixed tile codes instead of timing them: a bench "
                         "line's \"tiles\" object, or that object alone")
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the ViT-S and int16 YOLOv8n-cls passes")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="finish with one device copy of MIB MiB (a plain "
                         "copy kernel that calibrates byte counters)")
@@ -106,6 +108,38 @@ def roofline(ops, byts, ms):
     return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
             "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4),
             "traffic": None}
+
+
+def measure_pass(name, g, quant_type, batch, steps, tune, torch):
+    """Images/s of one captured integer pass of graph ``g`` (calibrated on
+    32 seeded N(0, 1) images, tiles tuned as for the headline pass)."""
+    from quantanything_amd.container import QuantContainer
+    from quantanything_amd.synth import Stream
+
+    c = QuantContainer(g, quant_type, per_channel=True)
+    calib = Stream(4).normal((32, 3, 224, 224)).astype(np.float32)
+    c.calibrate([calib[:batch] if batch < 32 else calib])
+    x = Stream(5).normal((batch, 3, 224, 224)).astype(np.float32)
+    ex = c.executor({"images": x.shape})
+    ex.inputs_f32["images"].copy_(torch.from_numpy(x))
+    ex.launch()
+    torch.cuda.synchronize()
+    if tune:
+        ex.tune()
+    ex.capture()
+    for _ in range(3):
+        ex.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ex.replay()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"workload": name, "quant_type": quant_type, "global_batch": batch,
+            "images_per_s": round(batch / dt, 1),
+            "ms_per_step": round(dt * 1e3, 4), "steps": steps,
+            "launches_per_step": len(ex.launches),
+            "params": g.num_params()}
 
 
 def main():
@@ -288,6 +322,17 @@ def main():
                         "frac_of_mfma_peak": round(tops / PEAK_I8_TOPS, 4),
                         "roofline": r})
 
+    # ---- the other end-to-end configurations (parity: tests/) ------------
+    extra = []
+    if not args.no_extra and not args.profile_only:
+        steps = max(5, min(args.steps, 50))
+        extra.append(measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",
+                                  G.vit(seed=5, batch=32), "int8", 32, steps,
+                                  not args.no_tune, torch))
+        extra.append(measure_pass("YOLOv8n-cls int16 (wide accumulation)",
+                                  G.yolov8n_cls(seed=3), "int16", B, steps,
+                                  not args.no_tune, torch))
+
     line = {
         "metric": "int8 YOLOv8n-cls images/s (b=64) + qGEMM TOPS as % of "
                   "i8 MFMA peak",
@@ -309,6 +354,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "other_configs": extra,
         "gate": gate,
         "launches_per_step": len(ex.launches),
         "top_launches_ms": [[n, round(t, 5)] for t, n, _ in per[:6]],

@@ -170,6 +170,11 @@ bool mfma_launch_lds(const ConvArgs& b, int wm, bool split, int epi,
 bool mfma_launch_l2(const ConvArgs& b, int wm, bool split, int epi,
                     hipStream_t st);
 bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
+// Large GEMM descriptors (H = W = 1, K a multiple of 64) with the int8 table
+// epilogue on 128 x 128 blocks (qa_gemm_big.hip); `epi` as chosen by
+// launch_conv_mfma.
+bool gemm_big_applies(const ConvArgs& b, int epi);
+bool launch_gemm_big(const ConvArgs& b, hipStream_t st);
 // 16-bit operands on the FP64 matrix cores (qa_conv_f64.hip), exact.
 bool launch_conv_f64(const ConvArgs& a, hipStream_t st);
 

@@ -54,6 +54,12 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     if (a.mode == EPI_QUANT && a.plan && b.fastio) epi = Q8_TABLE;
     b.mg_cb = (((uint64_t)1 << 32) + a.CB - 1) / (uint64_t)a.CB;
     b.mg_kw = (((uint64_t)1 << 32) + a.KW - 1) / (uint64_t)a.KW;
+    // large GEMMs: 128 x 128 blocks (tile hint bit 10 chooses)
+    if (gemm_big_applies(b, epi)) {
+        bool big = a.M >= 1024 && a.Cout >= 128;
+        if (a.tile_hint & TILE_VALID) big = (a.tile_hint >> 10) & 1;
+        if (big) return launch_gemm_big(b, st);
+    }
     const int64_t ntiles = ceil_div(a.M, 16);
     const int64_t simds = 4 * (int64_t)cu_count();
     auto waves = [&](int wm, bool split) {

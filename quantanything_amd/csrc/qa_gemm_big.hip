@@ -1,0 +1,244 @@
+// Large int8 GEMMs with the table epilogue (the weight MatMuls of
+// transformers: M = batch x tokens rows, K and N in the hundreds or more).
+//
+// The convolution kernel computes 16-row tiles and reuses each weight
+// fragment once per tile; for GEMMs of thousands of rows that leaves the
+// matrix cores waiting on the memory pipe. Here a work-group computes a
+// 128 x 128 block of C: its 4 waves (2 x 2) own 64 x 64 each, i.e. 4 x 4
+// MFMA tiles of v_mfma_i32_16x16x64_i8, so every A fragment feeds 4 MFMAs
+// and every B fragment 4. K runs in 64-byte steps through two LDS buffers
+// (global -> registers for step k+1 while step k's MFMAs run, one barrier a
+// step). The epilogue is the int8 table plan of qa_conv.h (per-channel
+// multiply-add and shift, 256-entry clip / activation / residual / copy
+// tables), identical to the convolution kernel's.
+//
+// Operands: A row p (one pixel of a GEMM descriptor, H = W = 1) at
+// x + p * x_sn, K = Cg bytes; B = the packed weight rows (layout 0, one
+// group), K bytes each, rows padded to 128.
+#include "qa_conv_mfma.h"
+
+namespace qa {
+namespace {
+
+constexpr int GB_M = 128, GB_N = 128;
+
+// BK: K bytes a step (64 or 128: one or two MFMA K-depths per barrier)
+template <int P, int BK>
+__global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
+    constexpr int GB_K = BK;
+    constexpr int GB_RS = BK + 16;  // LDS row stride (bytes)
+    constexpr int CPR = BK / 16;    // 16-byte chunks per row
+    constexpr int CH = GB_M * CPR / 256;  // chunks per thread and operand
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][GB_M * GB_RS];
+    __shared__ __attribute__((aligned(16))) int8_t sB[2][GB_N * GB_RS];
+    __shared__ int s_tab[768];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int col = lane & 15, kg = lane >> 4;
+    // tile of this work-group: consecutive work-groups go to different
+    // XCDs (round robin), so the linear index is remapped to make the
+    // tiles of each XCD consecutive; consecutive tiles share their A rows
+    // (column blocks fastest), which then stay in that XCD's L2
+    const int nb = (a.Cout + GB_N - 1) / GB_N;
+    const int ntile = gridDim.x;
+    const int per = (ntile + 7) / 8;
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7, idx = bid >> 3;
+    // XCDs 0..rem-1 hold per tiles, the others per - 1 (when ntile % 8)
+    const int rem = ntile - 8 * (per - 1);
+    const int t = xcd < rem ? xcd * per + idx
+                            : rem * per + (xcd - rem) * (per - 1) + idx;
+    const int64_t m0 = (int64_t)(t / nb) * GB_M;
+    const int n0 = (t % nb) * GB_N;
+    const int K = a.KGp * 16;
+    const int nk = K / GB_K;  // a multiple of P
+    const int8_t* xa = (const int8_t*)a.x;
+
+    // tables of the plan and the lane's 4 channels' constants
+    for (int i = tid; i < 768; i += 256)
+        s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
+    const int4 hdr = *(const int4*)a.plan;
+    int cm[4], ct[4];
+    int64_t cc[4];
+    uint32_t ccorr[4], cbo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = min(n0 + 64 * wn + 16 * j + col, a.Cout - 1);
+        const int4 pc = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
+        cm[j] = pc.x;
+        ct[j] = pc.y;
+        cc[j] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
+        ccorr[j] = a.corr ? (uint32_t)a.corr[c] : 0u;
+        cbo[j] = a.rowsum ? (uint32_t)a.boff[c] : 0u;
+    }
+
+    // global -> registers, P steps ahead: per operand and step, CH chunks
+    // of 16 bytes per thread (chunk tid + 256 j: row (tid / CPR) + j * 256
+    // / CPR, bytes 16 (tid % CPR)); loads past the last step re-read it (in
+    // bounds, unused)
+    constexpr int RSTEP = 256 / CPR;  // rows between a thread's chunks
+    const int lr = tid / CPR, lk = (tid % CPR) * 16;
+    // the ring slots (P of them used): SSA vectors of CH 16-byte chunks
+    // per operand, so that they stay in VGPRs
+    typedef int vch __attribute__((ext_vector_type(4 * CH)));
+    vch s0a, s0b, s1a, s1b;
+    auto gload = [&](vch& va, vch& vb, int ks) __attribute__((always_inline)) {
+        const int o = min(ks, nk - 1) * GB_K + lk;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int r = lr + j * RSTEP;
+            const int4 x = *(const int4*)(xa + min(m0 + r, a.M - 1) * a.x_sn +
+                                          o);
+            const int4 w =
+                *(const int4*)(a.wp + (int64_t)(n0 + r) * a.wp_rstride + o);
+            va[4 * j] = x.x;
+            va[4 * j + 1] = x.y;
+            va[4 * j + 2] = x.z;
+            va[4 * j + 3] = x.w;
+            vb[4 * j] = w.x;
+            vb[4 * j + 1] = w.y;
+            vb[4 * j + 2] = w.z;
+            vb[4 * j + 3] = w.w;
+        }
+    };
+    auto sstore = [&](const vch& va, const vch& vb, int buf)
+                      __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int r = lr + j * RSTEP;
+            *(int4*)&sA[buf][r * GB_RS + lk] =
+                int4{va[4 * j], va[4 * j + 1], va[4 * j + 2], va[4 * j + 3]};
+            *(int4*)&sB[buf][r * GB_RS + lk] =
+                int4{vb[4 * j], vb[4 * j + 1], vb[4 * j + 2], vb[4 * j + 3]};
+        }
+    };
+#define GB_LOAD(S, ks) gload(S##a, S##b, (ks))
+#define GB_STORE(S, buf) sstore(S##a, S##b, (buf))
+    v4i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    int psum[4] = {0, 0, 0, 0};  // stored-byte sums of the lane's A rows
+    // one K-step (BK / 64 MFMA depths) from LDS buffer buf
+    auto mfma_step = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < BK / 64; ++h) {
+            v4i fa[4], fb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[i] = *(const v4i*)&sA[buf][(64 * wm + 16 * i + col) *
+                                                  GB_RS + 64 * h + 16 * kg];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                fb[j] = *(const v4i*)&sB[buf][(64 * wn + 16 * j + col) *
+                                                  GB_RS + 64 * h + 16 * kg];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        fa[i], fb[j], acc[i][j], 0, 0, 0);
+            if (a.rowsum) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) psum[i] += bytes_sum(fa[i], 16);
+            }
+        }
+    };
+    // step ks from slot S: to LDS (that buffer was last read two steps
+    // ago, before the previous step's barrier), refill S with step ks + P,
+    // barrier, MFMAs
+#define GB_STEP(S, ks)                      \
+    do {                                    \
+        const int b_ = (ks) & 1;            \
+        GB_STORE(S, b_);                    \
+        GB_LOAD(S, (ks) + P);               \
+        __syncthreads();                    \
+        mfma_step(b_);                      \
+    } while (0)
+    GB_LOAD(s0, 0);
+    if (P > 1) GB_LOAD(s1, 1);
+    for (int k0 = 0; k0 < nk; k0 += P) {
+        GB_STEP(s0, k0);
+        if (P > 1) GB_STEP(s1, k0 + 1);
+    }
+#undef GB_STEP
+#undef GB_STORE
+#undef GB_LOAD
+
+    // epilogue: lane holds rows 16 i + 4 kg + r, columns 16 j + col
+    const int pA = hdr.x, pB = hdr.y, pSH = hdr.z;
+    const bool res = a.res != nullptr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int ps[4] = {0, 0, 0, 0};
+        if (a.rowsum) {
+            int s = psum[i];
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ps[r] = __shfl(s, 4 * kg + r);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t p = m0 + 64 * wm + 16 * i + 4 * kg + r;
+            if (p >= a.M) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = n0 + 64 * wn + 16 * j + col;
+                if (c >= a.Cout) continue;
+                uint32_t wu = (uint32_t)acc[i][j][r] + ccorr[j];
+                if (a.rowsum) wu += cbo[j] * (uint32_t)ps[r];
+                const int q0 =
+                    (int)(((int64_t)(int)wu * cm[j] + cc[j]) >> ct[j]);
+                int e = min(max(q0, pA), pB) - pA;
+                if (res) {
+                    const int u =
+                        (uint8_t)((const int8_t*)a.res)[p * a.res_pst + c];
+                    e = min(max(s_tab[256 + e] + s_tab[512 + u], 0), pSH);
+                }
+                const int ev = s_tab[e];
+                ((int8_t*)a.y)[p * a.y_pst + c] = (int8_t)(ev & 255);
+                if (a.y2)
+                    ((int8_t*)a.y2)[p * a.y2_pst + c] =
+                        (int8_t)((ev >> 8) & 255);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool gemm_big_applies(const ConvArgs& b, int epi) {
+    const uintptr_t xa = (uintptr_t)b.x;
+    return epi == Q8_TABLE && b.mode == EPI_QUANT && b.fastio && b.plan &&
+           b.G == 1 && b.layout == 0 && b.KH == 1 && b.KW == 1 &&
+           b.H == 1 && b.W == 1 && b.OH == 1 && b.OW == 1 && b.x_code == 1 &&
+           b.x_sc == 1 && b.Cg % 64 == 0 && b.KGp * 16 == b.Cg &&
+           b.wp_rstride == (int64_t)b.KGp * 16 && b.x_sn % 16 == 0 &&
+           xa % 16 == 0 && b.y_code == 1 && b.M < ((int64_t)1 << 31);
+}
+
+bool launch_gemm_big(const ConvArgs& b, hipStream_t st) {
+    const int64_t tiles = ceil_div(b.M, GB_M) * ceil_div(b.Cout, GB_N);
+    if (tiles >= ((int64_t)1 << 31)) {
+        set_error("launch_gemm_big", "grid too large");
+        return false;
+    }
+    // 128-byte steps when K allows, else 64-byte steps; the next step's
+    // loads in flight (deeper rings cost the second wave per SIMD)
+    const int K = b.KGp * 16;
+    const dim3 grid((unsigned)tiles);
+    if (K % 128 == 0)
+        k_gemm_big<1, 128><<<grid, 256, 0, st>>>(b);
+    else
+        k_gemm_big<1, 64><<<grid, 256, 0, st>>>(b);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_hip_error("launch_gemm_big", e);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace qa

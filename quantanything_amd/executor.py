@@ -1219,6 +1219,9 @@ class DeviceExecutor:
             return [0] + [0x10000 | c for c in F64_TILES if c & 15 <= wm_max]
         wm_max = 1 if cog <= 16 else 2 if cog <= 32 else 4 if cog <= 64 else 8
         out = [0]
+        if d.H == d.W == d.KH == d.KW == 1 and d.G == 1 and \
+                d.w_layout == 0 and d.C % 64 == 0:
+            out.append(0x10400)  # the large-GEMM kernel (128 x 128 blocks)
         for wm in (1, 2, 4, 8):
             if wm > wm_max:
                 break

@@ -131,3 +131,53 @@ def test_tiny_vit_graph_replay_matches_eager(hip):
         got = ex.run({"images": x}, use_graph=True)
         for k in eager:
             np.testing.assert_array_equal(got[k], eager[k])
+
+
+def _gemm_block_graph(k, n, act, residual):
+    """x [M, k] -> MatMul(+bias) [-> Gelu] [-> + residual (a second
+    MatMul of x)]: the weight GEMM forms of a transformer block."""
+    b = G.GraphBuilder(31, opset=17)
+    w = b.weight(k, n, scale=float(np.sqrt(1.0 / k)))
+    y = b.op("MatMul", ["x", w, b.weight(n, scale=0.05)])
+    if act:
+        y = b.op("Gelu", [y], approximate="tanh")
+    if residual:
+        r = b.op("MatMul", ["x", b.weight(k, n, scale=float(np.sqrt(1.0 / k))),
+                            b.weight(n, scale=0.05)])
+        y = b.op("Add", [r, y])
+    return b.build("x", [None, k], y)
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+@pytest.mark.parametrize("m,k,n,act,residual", [
+    (1500, 384, 1152, False, False),   # QKV-like, partial row block
+    (1100, 256, 384, True, False),     # fc1-like with the Gelu table
+    (1030, 1536, 200, False, True),    # fc2-like, residual, partial column block
+    (2048, 320, 256, True, True),      # 64-byte K steps (K / 64 odd)
+])
+def test_large_gemm_kernel_bit_exact(hip, tmp_path, quant_type, m, k, n, act,
+                                     residual):
+    """Weight GEMMs of >= 1024 rows (the 128 x 128 block kernel, tile code
+    0x10400, and every other tile code) equal the oracle bit for bit."""
+    g = _gemm_block_graph(k, n, act, residual)
+    calib = [Stream(90 + i).normal((256, k)).astype(np.float32)
+             for i in range(2)]
+    c = _calibrated(g, quant_type, calib)
+    x = Stream(95).normal((m, k)).astype(np.float32)
+    path = tmp_path / "q.json"
+    c.save(path)
+    o = OraclePipeline(g, path)
+    o.run(x, keep=True)
+    ex = c.executor({"x": x.shape})
+    descs = [t for t in ex.tunables]
+    assert descs and all(0x10400 in t[2] for t in descs)
+    for r in range(max(len(t[2]) for t in descs)):
+        for _, d, codes, _ in descs:
+            d.tile = codes[r % len(codes)]
+        ex.run({"x": x})
+        for name, t in ex.tensors.items():
+            if name in o.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, o.env[name].reshape(got.shape),
+                    err_msg=f"{name}, tiles {[hex(t[1].tile) for t in descs]}")
