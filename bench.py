@@ -56,6 +56,10 @@ def parse():
                         "line's \"tiles\" object, or that object alone")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the ViT-S and int16 YOLOv8n-cls passes")
+    p.add_argument("--only", choices=("vit", "int16"),
+                   help="time only that pass (ViT-S/16 int8 b32 or "
+                        "YOLOv8n-cls int16) and print its record, e.g. "
+                        "under a profiler")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="finish with one device copy of MIB MiB (a plain "
                         "copy kernel that calibrates byte counters)")
@@ -159,6 +163,17 @@ def main():
 
     native.require()
     B = args.batch
+    if args.only:
+        if args.only == "vit":
+            rec = measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",
+                               G.vit(seed=5, batch=32), "int8", 32,
+                               args.steps, not args.no_tune, torch)
+        else:
+            rec = measure_pass("YOLOv8n-cls int16 (wide accumulation)",
+                               G.yolov8n_cls(seed=3), "int16", B, args.steps,
+                               not args.no_tune, torch)
+        print(json.dumps(rec))
+        return 0
     g = G.yolov8n_cls(seed=3)
     c = QuantContainer(g, "int8", per_channel=True)
     c.calibrate([Stream(4).normal((32, 3, 224, 224)).astype(np.float32)])

@@ -254,8 +254,9 @@ int qa_d_copy_nd(const qa_nd_copy* d, void* stream);
  * elements) as float_ops.py:336-347: x = (float)((q - in_zp) * in_scale),
  * float64 mean and variance, y = (x - mean) / sqrt(var + eps) * gamma
  * (+ beta), cast to float32, quantized with round-half-even. beta may be
- * NULL. Results agree with the reference within one quantization step
- * (float64 summation order). */
+ * NULL. x and y of one storage, int8 or int16 (codes 1 / 2). Results agree
+ * with the reference within one quantization step (float64 summation
+ * order). */
 int qa_d_layernorm(const void* x, int x_code, int64_t x_rstride,
                    int64_t rows, int64_t cols, double in_scale, int64_t in_zp,
                    int64_t x_so, const float* gamma, const float* beta,

@@ -64,14 +64,13 @@ __device__ __forceinline__ double group_sum(double v) {
     return v;
 }
 
-template <int GS, int PER>
+template <int GS, int PER, class TI, class TO>
 __global__ __launch_bounds__(kThreads) void k_layernorm(
-    const void* __restrict__ x, int x_code, int64_t x_rs, int64_t rows,
+    const TI* __restrict__ x, int64_t x_rs, int64_t rows,
     int64_t cols, double in_scale, int64_t in_zp, int64_t x_so,
     const float* __restrict__ gamma, const float* __restrict__ beta,
-    double eps, void* __restrict__ y, int y_code, int64_t y_rs,
-    double out_scale, int64_t out_zp, int64_t qmin, int64_t qmax,
-    int64_t y_so) {
+    double eps, TO* __restrict__ y, int64_t y_rs, double out_scale,
+    int64_t out_zp, int64_t qmin, int64_t qmax, int64_t y_so) {
     constexpr int RPW = 64 / GS;
     const int lane = threadIdx.x & 63;
     const int gl = lane % GS;
@@ -83,15 +82,15 @@ __global__ __launch_bounds__(kThreads) void k_layernorm(
         const bool live = r < rows;
         const int64_t rr = live ? r : 0;
         auto value = [&](int64_t i) {
-            return (double)dequant_f32(
-                load_any(x, x_code, rr * x_rs + i) + x_so, in_zp, in_scale);
+            return (double)dequant_f32((int64_t)x[rr * x_rs + i] + x_so,
+                                       in_zp, in_scale);
         };
         auto emit = [&](int64_t i, double v, double mean, double sd) {
             double t = (v - mean) / sd * (double)gamma[i];
             if (beta) t += (double)beta[i];
             const int64_t q = qa_quantize_one_fast((float)t, out_scale, inv,
                                                    out_zp, qmin, qmax);
-            store_any(y, y_code, rr * y_rs + i, q - y_so);
+            y[rr * y_rs + i] = (TO)(q - y_so);
         };
         if (PER > 0) {
             double v[PER > 0 ? PER : 1];
@@ -252,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act(qa_matmul_desc d) {
 // column l % 16). Centring by row / column sums as k_matmul_act.
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
-template <bool SUMS>
+template <bool SUMS, class TO>
 __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
     qa_matmul_desc d, int Kp, int Np) {
     extern __shared__ int4 lds4[];
@@ -369,9 +368,8 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
             const float yf = (float)((double)v * scale);
             const int64_t q = qa_quantize_one_fast(yf, d.out_scale, inv,
                                                    d.out_zp, d.qmin, d.qmax);
-            store_any(d.y, (int)d.y_code,
-                      b0 * d.y_s0 + b1 * d.y_s1 + m * d.y_sm + n * d.y_sn,
-                      q - d.y_so);
+            ((TO*)d.y)[b0 * d.y_s0 + b1 * d.y_s1 + m * d.y_sm + n * d.y_sn] =
+                (TO)(q - d.y_so);
         }
     }
 }
@@ -426,18 +424,31 @@ QA_API int qa_d_layernorm(const void* x, int x_code, int64_t x_rstride,
         return -1;
     }
     hipStream_t st = (hipStream_t)stream;
-    if (cols <= 32 * 16) {  // 32 lanes a row, 2 rows a wave
-        const int64_t blocks = std::min<int64_t>(ceil_div(rows, 8), 65535);
-        k_layernorm<32, 16><<<(unsigned)blocks, kThreads, 0, st>>>(
-            x, x_code, x_rstride, rows, cols, in_scale, in_zp, x_so, gamma,
-            beta, eps, y, y_code, y_rstride, out_scale, out_zp, qmin, qmax,
-            y_so);
-    } else {
-        const int64_t blocks = std::min<int64_t>(ceil_div(rows, 4), 65535);
-        k_layernorm<64, 0><<<(unsigned)blocks, kThreads, 0, st>>>(
-            x, x_code, x_rstride, rows, cols, in_scale, in_zp, x_so, gamma,
-            beta, eps, y, y_code, y_rstride, out_scale, out_zp, qmin, qmax,
-            y_so);
+    auto go = [&](auto ti, auto to) {
+        typedef decltype(ti) TI;
+        typedef decltype(to) TO;
+        if (cols <= 32 * 16) {  // 32 lanes a row, 2 rows a wave
+            const int64_t blocks = std::min<int64_t>(ceil_div(rows, 8), 65535);
+            k_layernorm<32, 16, TI, TO><<<(unsigned)blocks, kThreads, 0, st>>>(
+                (const TI*)x, x_rstride, rows, cols, in_scale, in_zp, x_so,
+                gamma, beta, eps, (TO*)y, y_rstride, out_scale, out_zp, qmin,
+                qmax, y_so);
+        } else {
+            const int64_t blocks = std::min<int64_t>(ceil_div(rows, 4), 65535);
+            k_layernorm<64, 0, TI, TO><<<(unsigned)blocks, kThreads, 0, st>>>(
+                (const TI*)x, x_rstride, rows, cols, in_scale, in_zp, x_so,
+                gamma, beta, eps, (TO*)y, y_rstride, out_scale, out_zp, qmin,
+                qmax, y_so);
+        }
+    };
+    if (x_code == 1 && y_code == 1)
+        go(int8_t{}, int8_t{});
+    else if (x_code == 2 && y_code == 2)
+        go(int16_t{}, int16_t{});
+    else {
+        set_error("qa_d_layernorm", "input and output of one int8 / int16 "
+                                    "storage");
+        return -1;
     }
     return launched("qa_d_layernorm") ? 0 : -1;
 }
@@ -463,16 +474,17 @@ QA_API int qa_d_matmul_act(const qa_matmul_desc* d, void* stream) {
         const int64_t Kp = round_up(std::max<int64_t>(d->K, 1), 64);
         const int64_t Np = round_up(d->N, 16);
         const int64_t bytes = (64 + Np) * (Kp + 16) + (64 + Np) * 4;
-        if (bytes <= 64 * 1024 && ceil_div(d->M, 64) <= 65535) {
+        if (bytes <= 64 * 1024 && ceil_div(d->M, 64) <= 65535 &&
+            d->y_code == 1) {
             const dim3 g2((unsigned)ceil_div(d->M, 64), (unsigned)gz);
             const bool sums = d->a_so != d->a_zp || d->b_so != d->b_zp;
             if (sums)
-                k_matmul_act_mfma<true><<<g2, kThreads, bytes,
-                                          (hipStream_t)stream>>>(
+                k_matmul_act_mfma<true, int8_t><<<g2, kThreads, bytes,
+                                                  (hipStream_t)stream>>>(
                     *d, (int)Kp, (int)Np);
             else
-                k_matmul_act_mfma<false><<<g2, kThreads, bytes,
-                                           (hipStream_t)stream>>>(
+                k_matmul_act_mfma<false, int8_t><<<g2, kThreads, bytes,
+                                                   (hipStream_t)stream>>>(
                     *d, (int)Kp, (int)Np);
         } else {
             k_matmul_act<int8_t><<<grid, kThreads, 0, (hipStream_t)stream>>>(

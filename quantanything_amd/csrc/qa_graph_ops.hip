@@ -269,12 +269,12 @@ __global__ __launch_bounds__(kThreads) void k_softmax(
 // inputs, float64 exponentials and sums and quantization as k_softmax; the
 // maximum is taken over the float32 values (exact), and only the summation
 // order differs.
-template <int GS, int PER>
+template <int GS, int PER, class TI, class TO>
 __global__ __launch_bounds__(kThreads) void k_softmax_rows(
-    const void* __restrict__ x, int in_code, int64_t rows, int64_t cols,
-    double in_scale, int64_t in_zp, int64_t in_so, void* out, int out_code,
-    double out_scale, int64_t out_zp, int64_t qmin, int64_t qmax,
-    int64_t out_so, float* __restrict__ outf) {
+    const TI* __restrict__ x, int64_t rows, int64_t cols, double in_scale,
+    int64_t in_zp, int64_t in_so, TO* __restrict__ out, double out_scale,
+    int64_t out_zp, int64_t qmin, int64_t qmax, int64_t out_so,
+    float* __restrict__ outf) {
     constexpr int RPW = 64 / GS;  // rows per wave
     const int lane = threadIdx.x & 63;
     const int gl = lane % GS;
@@ -291,8 +291,8 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(
         for (int k = 0; k < PER; ++k) {
             const int64_t i = gl + GS * k;
             xf[k] = live && i < cols
-                        ? (float)((double)(load_s(x, in_code, base + i) +
-                                           in_so - in_zp) *
+                        ? (float)((double)((int64_t)x[base + i] + in_so -
+                                           in_zp) *
                                   in_scale)
                         : -INFINITY;
             mx = fmaxf(mx, xf[k]);
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(
             const float y = (float)(e[k] / sum);
             const int64_t q =
                 qa_quantize_one_fast(y, out_scale, inv, out_zp, qmin, qmax);
-            store_s(out, out_code, base + i, q - out_so);
+            out[base + i] = (TO)(q - out_so);
             if (outf) outf[base + i] = (float)((double)(q - out_zp) * out_scale);
         }
     }
@@ -326,16 +326,29 @@ bool softmax_launch(const void* x, int in_code, int64_t rows, int64_t cols,
                     int out_code, double out_scale, int64_t out_zp,
                     int64_t qmin, int64_t qmax, int64_t out_so, float* outf,
                     hipStream_t st) {
-    if (cols <= 16 * 16) {  // 16 lanes a row, 4 rows a wave
-        const int64_t blocks = std::min<int64_t>((rows + 15) / 16, 65535);
-        k_softmax_rows<16, 16><<<(unsigned)blocks, kThreads, 0, st>>>(
-            x, in_code, rows, cols, in_scale, in_zp, in_so, out, out_code,
-            out_scale, out_zp, qmin, qmax, out_so, outf);
-    } else if (cols <= 64 * SOFTMAX_PER) {
-        const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
-        k_softmax_rows<64, SOFTMAX_PER><<<(unsigned)blocks, kThreads, 0, st>>>(
-            x, in_code, rows, cols, in_scale, in_zp, in_so, out, out_code,
-            out_scale, out_zp, qmin, qmax, out_so, outf);
+    auto rows_kernel = [&](auto ti, auto to) {
+        typedef decltype(ti) TI;
+        typedef decltype(to) TO;
+        if (cols <= 16 * 16) {  // 16 lanes a row, 4 rows a wave
+            const int64_t blocks = std::min<int64_t>((rows + 15) / 16, 65535);
+            k_softmax_rows<16, 16, TI, TO><<<(unsigned)blocks, kThreads, 0,
+                                             st>>>(
+                (const TI*)x, rows, cols, in_scale, in_zp, in_so, (TO*)out,
+                out_scale, out_zp, qmin, qmax, out_so, outf);
+        } else {
+            const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
+            k_softmax_rows<64, SOFTMAX_PER, TI, TO><<<(unsigned)blocks,
+                                                      kThreads, 0, st>>>(
+                (const TI*)x, rows, cols, in_scale, in_zp, in_so, (TO*)out,
+                out_scale, out_zp, qmin, qmax, out_so, outf);
+        }
+    };
+    const bool same = in_code == out_code && (in_code == 1 || in_code == 2);
+    if (same && cols <= 64 * SOFTMAX_PER) {
+        if (in_code == 1)
+            rows_kernel(int8_t{}, int8_t{});
+        else
+            rows_kernel(int16_t{}, int16_t{});
     } else {
         const unsigned blocks = (unsigned)(rows < 65535 ? rows : 65535);
         k_softmax<<<blocks, kThreads, 0, st>>>(x, in_code, rows, cols,
