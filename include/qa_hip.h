@@ -193,7 +193,10 @@ typedef struct qa_conv_desc {
                       work-group split K, lds = weights staged in LDS (a
                       caller's measured choice; ignored where it does not
                       apply); 0x10400: GEMM descriptors (H = W = 1, C a
-                      multiple of 64) on 128 x 128 blocks. FP64 path (w_code
+                      multiple of 64) on 128 x 128 blocks; 0x10800 | wm
+                      (wm 1, 2, 4): bands of output rows with the input band
+                      and the weights in LDS (layout 0, one group, a table
+                      plan). FP64 path (w_code
                       8): 0x10000 | wm | tm << 4
                       | split << 8 with (wm, tm, split) one of (1,1,0),
                       (2,1,0), (1,4,0), (1,1,1), (2,1,1), (4,1,1); tm =

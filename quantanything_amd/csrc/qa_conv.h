@@ -175,6 +175,10 @@ bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
 // launch_conv_mfma.
 bool gemm_big_applies(const ConvArgs& b, int epi);
 bool launch_gemm_big(const ConvArgs& b, hipStream_t st);
+// int8 convolutions over bands of output rows with the input band and the
+// weights in LDS (qa_conv_band.hip); wm = 16-channel groups per work-group.
+bool conv_band_applies(const ConvArgs& b, int epi, int wm);
+bool launch_conv_band(const ConvArgs& b, int wm, hipStream_t st);
 // 16-bit operands on the FP64 matrix cores (qa_conv_f64.hip), exact.
 bool launch_conv_f64(const ConvArgs& a, hipStream_t st);
 

@@ -54,6 +54,14 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     if (a.mode == EPI_QUANT && a.plan && b.fastio) epi = Q8_TABLE;
     b.mg_cb = (((uint64_t)1 << 32) + a.CB - 1) / (uint64_t)a.CB;
     b.mg_kw = (((uint64_t)1 << 32) + a.KW - 1) / (uint64_t)a.KW;
+    // bands of output rows with operands in LDS (tile hint bit 11, with
+    // wm in the low bits)
+    // (ignored, like every hint, where it does not apply)
+    if ((a.tile_hint & TILE_VALID) && ((a.tile_hint >> 11) & 1)) {
+        const int bw = a.tile_hint & 0xff;
+        if ((bw == 1 || bw == 2 || bw == 4) && conv_band_applies(b, epi, bw))
+            return launch_conv_band(b, bw, st);
+    }
     // large GEMMs: 128 x 128 blocks (tile hint bit 10 chooses)
     if (gemm_big_applies(b, epi)) {
         bool big = a.M >= 1024 && a.Cout >= 128;

@@ -273,15 +273,26 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
     auto stage = [&](int8_t* dst, const int8_t* src, int rows, int64_t r0,
                      int64_t rlim, int64_t rs, int64_t ks) {
         const bool al = ((uintptr_t)src & 15) == 0;
+        constexpr int U = 4;  // loads in flight per thread
         if (ks == 1 && al && rs % 16 == 0 && d.K % 16 == 0) {
             const int cpr = Kp / 16;  // 16-byte chunks per row
-            for (int e = tid; e < rows * cpr; e += kThreads) {
-                const int r = e / cpr, c = (e - r * cpr) * 16;
-                const int64_t rr = r0 + r;
-                int4 v = {0, 0, 0, 0};
-                if (rr < rlim && c < d.K)
-                    v = *(const int4*)(src + rr * rs + c);
-                *(int4*)(dst + r * RS + c) = v;
+            const int n16 = rows * cpr;
+            for (int e0 = tid; e0 < n16; e0 += U * kThreads) {
+                int4 v[U];
+                int at[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int e = e0 + u * kThreads;
+                    const int r = e / cpr, c = (e - r * cpr) * 16;
+                    const int64_t rr = r0 + r;
+                    v[u] = int4{0, 0, 0, 0};
+                    at[u] = e < n16 ? r * RS + c : -1;
+                    if (e < n16 && rr < rlim && c < d.K)
+                        v[u] = *(const int4*)(src + rr * rs + c);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (at[u] >= 0) *(int4*)(dst + at[u]) = v[u];
             }
             return;
         }
@@ -289,15 +300,27 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
             (r0 + rows <= rlim || rlim % 16 == 0)) {
             // 16 consecutive rows of one column per load, scattered to LDS
             const int rpc = rows / 16;
-            for (int e = tid; e < rpc * Kp; e += kThreads) {
-                const int c = e / rpc, r = (e - c * rpc) * 16;
-                const int64_t rr = r0 + r;
-                int4 v = {0, 0, 0, 0};
-                if (rr < rlim && c < d.K)
-                    v = *(const int4*)(src + rr + (int64_t)c * ks);
-                const int8_t* b = (const int8_t*)&v;
+            const int n16 = rpc * Kp;
+            for (int e0 = tid; e0 < n16; e0 += U * kThreads) {
+                int4 v[U];
 #pragma unroll
-                for (int j = 0; j < 16; ++j) dst[(r + j) * RS + c] = b[j];
+                for (int u = 0; u < U; ++u) {
+                    const int e = e0 + u * kThreads;
+                    const int c = e / rpc, r = (e - c * rpc) * 16;
+                    const int64_t rr = r0 + r;
+                    v[u] = int4{0, 0, 0, 0};
+                    if (e < n16 && rr < rlim && c < d.K)
+                        v[u] = *(const int4*)(src + rr + (int64_t)c * ks);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int e = e0 + u * kThreads;
+                    if (e >= n16) continue;
+                    const int c = e / rpc, r = (e - c * rpc) * 16;
+                    const int8_t* b = (const int8_t*)&v[u];
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) dst[(r + j) * RS + c] = b[j];
+                }
             }
             return;
         }

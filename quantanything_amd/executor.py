@@ -1222,6 +1222,11 @@ class DeviceExecutor:
         if d.H == d.W == d.KH == d.KW == 1 and d.G == 1 and \
                 d.w_layout == 0 and d.C % 64 == 0:
             out.append(0x10400)  # the large-GEMM kernel (128 x 128 blocks)
+        if d.w_layout == 0 and d.G == 1 and d.C % 16 == 0 and \
+                d.OW <= 256 and d.epi_plan and (d.H > 1 or d.W > 1):
+            # bands of output rows, operands in LDS (the library checks the
+            # LDS size and falls back when the band does not fit)
+            out += [0x10800 | wm for wm in (1, 2, 4) if wm <= wm_max]
         for wm in (1, 2, 4, 8):
             if wm > wm_max:
                 break
