@@ -196,7 +196,11 @@ typedef struct qa_conv_desc {
                       multiple of 64) on 128 x 128 blocks; 0x10800 | wm
                       (wm 1, 2, 4): bands of output rows with the input band
                       and the weights in LDS (layout 0, one group, a table
-                      plan). FP64 path (w_code
+                      plan); 0x11000 | wm (wm 1, 2, 4): the weights held in
+                      registers (at most 36 / wm K-steps of 64 bytes), input
+                      bands double-buffered in LDS, persistent work-groups
+                      (layout 0, one group, a table plan, int8 weights
+                      without a zero point). FP64 path (w_code
                       8): 0x10000 | wm | tm << 4
                       | split << 8 with (wm, tm, split) one of (1,1,0),
                       (2,1,0), (1,4,0), (1,1,1), (2,1,1), (4,1,1); tm =

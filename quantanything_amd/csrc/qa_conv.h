@@ -179,6 +179,11 @@ bool launch_gemm_big(const ConvArgs& b, hipStream_t st);
 // weights in LDS (qa_conv_band.hip); wm = 16-channel groups per work-group.
 bool conv_band_applies(const ConvArgs& b, int epi, int wm);
 bool launch_conv_band(const ConvArgs& b, int wm, hipStream_t st);
+// Convolution with the work-group's weights held in VGPRs and the input
+// bands in double-buffered LDS (qa_conv_wr.hip); wm = 16-channel groups per
+// work-group (K <= 36 / wm K-steps of 64 bytes).
+bool conv_wr_applies(const ConvArgs& b, int epi, int wm);
+bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st);
 // 16-bit operands on the FP64 matrix cores (qa_conv_f64.hip), exact.
 bool launch_conv_f64(const ConvArgs& a, hipStream_t st);
 

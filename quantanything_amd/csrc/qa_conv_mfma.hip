@@ -62,6 +62,12 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
         if ((bw == 1 || bw == 2 || bw == 4) && conv_band_applies(b, epi, bw))
             return launch_conv_band(b, bw, st);
     }
+    // weights in registers, bands in LDS (tile hint bit 12, with wm in the
+    // low bits)
+    if ((a.tile_hint & TILE_VALID) && ((a.tile_hint >> 12) & 1)) {
+        const int ww = a.tile_hint & 0xff;
+        if (conv_wr_applies(b, epi, ww)) return launch_conv_wr(b, ww, st);
+    }
     // large GEMMs: 128 x 128 blocks (tile hint bit 10 chooses)
     if (gemm_big_applies(b, epi)) {
         bool big = a.M >= 1024 && a.Cout >= 128;

@@ -1,0 +1,444 @@
+// int8 convolution with the weights held in registers, one band of output
+// rows per work-group, operands staged in LDS with every load in flight.
+//
+// For convolutions with few output channels per work-group (Cout <= 64 for
+// 3x3 taps of 64 channels: K <= 576 bytes with 4 channel tiles), a wave
+// can hold every weight fragment it needs in VGPRs: WM channel tiles x KS
+// K-steps x 4 registers (144 VGPRs at the largest). The K loop then reads
+// only the activation fragment from LDS (one 16-byte read a lane per
+// K-step, feeding WM MFMAs), which keeps the LDS traffic at 16 bytes per
+// lane and MFMA group instead of 16 (WM + 1).
+//
+// A work-group owns R output rows of one image (the band) and WM*16 output
+// channels; R is chosen so that the grid is about one work-group per CU.
+// Staging is latency-bound on this memory system unless many loads are in
+// flight, so each thread issues all of its chunks of the band's input rows
+// and of the weight rows (up to WR_SB + WR_SW 16-byte chunks) before it
+// stores any to LDS (image padding: the pad value, stored separately);
+// one barrier, then the weights go from LDS to registers and the
+// waves split the band's 16-pixel tiles (tile t goes to wave t % WR_NW). MFMA:
+// v_mfma_i32_16x16x64_i8 with the 16 pixels as rows and 16 output channels
+// as columns; a K-step is four 16-byte k-groups of the packed layout-0
+// weights (tap kg / CB, channels 16 (kg % CB) ..), whose band offsets come
+// from a k-group table in LDS (k-groups past the real K point at offset 0:
+// their weights are zero).
+//
+// Epilogue: the int8 table plan of qa_conv.h (per-channel multiply-add and
+// shift, 256-entry clip / activation / residual / copy tables), 4 channels
+// of a pixel stored as one word after a 4x4 byte transpose within each
+// lane quad, residual words fetched before the tile's MFMAs.
+#include "qa_conv_mfma.h"
+
+namespace qa {
+namespace {
+
+constexpr int WR_NW = 8;          // waves per work-group
+constexpr int WR_NT = 64 * WR_NW;  // threads per work-group
+constexpr int WR_SB = 8;          // band chunks (16 bytes) a thread stages
+constexpr int WR_SW = 8;          // weight chunks a thread stages
+
+// K-step counts the kernel is instantiated for (a layer runs the smallest
+// one >= its K-steps); WM channel tiles hold at most 36 / WM steps (144
+// weight VGPRs)
+constexpr int WR_STEPS[] = {1, 2, 3, 5, 9, 18, 36};
+
+int wr_steps(int wm, int ks) {
+    for (int v : WR_STEPS)
+        if (v >= ks && v <= 36 / wm) return v;
+    return 0;
+}
+
+struct WrGeom {
+    int R, BR, BW, PS;    // rows per band, band rows / columns, pixel bytes
+    int nbands, bpi;      // bands in all, bands per image
+    int band_bytes;       // the LDS band
+    int RSW;              // LDS row stride of the staged weights
+    int lds;              // dynamic LDS bytes (0: does not fit)
+    int KSR;              // K-steps the kernel runs (>= KGp / 4, zero-padded)
+    // ceil(2^32 / d) for d = band columns, KGp, OW, W (all >= 2):
+    // floor(n / d) = (n * m) >> 32 for the n < 2^16 used here
+    uint32_t m_bw, m_kgp, m_ow, m_w;
+};
+
+__device__ __forceinline__ int wr_div(int n, uint32_t m) {
+    return (int)__umulhi((uint32_t)n, m);
+}
+
+// KS: K-steps of 64 bytes, a compile-time count (the packed K rounded up
+// to one of the instantiated counts; the extra steps have zero weights).
+template <int WM, int KS>
+__global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
+    extern __shared__ int4 lds4[];
+    int8_t* s_band = (int8_t*)lds4;                          // band
+    int8_t* s_w = s_band + bg.band_bytes;                    // weights
+    int* s_kt = (int*)(s_w + WM * 16 * bg.RSW);              // k-groups
+    __shared__ int s_tab[768];
+    __shared__ int4 s_pc[WM * 16];
+    __shared__ uint32_t s_corr[WM * 16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, kgl = lane >> 4;
+    const int co0 = blockIdx.y * WM * 16;
+    const int KGp = a.KGp;
+    const int cpp = a.Cg >> 4;  // 16-byte chunks per input pixel
+    const int nch = bg.BR * bg.BW * cpp;
+    const int pv = splat4(a.pad_value);
+    const v4i pad4 = {pv, pv, pv, pv};
+
+    const int band = blockIdx.x;
+    const int n = band / bg.bpi;
+    const int oy0 = (band - n * bg.bpi) * bg.R;
+    const int iy0 = oy0 * a.SH - a.PH;
+    const int8_t* xn = (const int8_t*)a.x + (int64_t)n * a.x_sn;
+    const int wch = WM * 16 * KGp;
+
+    // ---- staging. The band's rows inside the image are one run of
+    // pixels p = 0 .. (r_hi - r_lo) W - 1 from image row iy0 + r_lo; chunk
+    // e < nreal is pixel e / cpp, 16-byte part e % cpp, at band row
+    // r_lo + p / W, column PW + p % W (columns past the band's width are
+    // loaded and dropped); weight chunk e is row e / KGp, part e % KGp.
+    // Every load of the thread (WR_SB band and WR_SW weight chunks) is
+    // issued before its stores, from straight-line code with few
+    // instructions a chunk (it runs once, from a cold instruction cache);
+    // the pad value fills the band's other positions in a separate loop.
+    const int r_lo = max(0, -iy0), r_hi = min(bg.BR, a.H - iy0);
+    const int nreal = max(r_hi - r_lo, 0) * a.W * cpp;
+    {
+        const int lcpp = __builtin_ctz(cpp);  // cpp is a power of two
+        v4i vx[WR_SB], vw[WR_SW];
+        int ax[WR_SB], aw[WR_SW];
+        {
+            const int xsp = (int)a.x_sp;
+            const int8_t* xrow = xn + (int64_t)(iy0 + r_lo) * a.W * a.x_sp;
+            const int colmax = bg.BW - a.PW;  // real columns kept
+            const int ch = tid & (cpp - 1);   // the same part for every u
+#pragma unroll
+            for (int u = 0; u < WR_SB; ++u) {
+                const int e = tid + u * WR_NT;
+                const int p = e >> lcpp;
+                const int row = wr_div(p, bg.m_w), ix = p - row * a.W;
+                const bool ok = e < nreal && ix < colmax;
+                ax[u] = ok ? ((r_lo + row) * bg.BW + ix + a.PW) * bg.PS +
+                                 ch * 16
+                           : -1;
+                vx[u] = *(const v4i*)(xrow + (e < nreal ? p * xsp + ch * 16
+                                                        : 0));
+            }
+        }
+        {
+            const int wrs = (int)a.wp_rstride;
+            const int8_t* wrow = a.wp + (int64_t)co0 * a.wp_rstride;
+#pragma unroll
+            for (int u = 0; u < WR_SW; ++u) {
+                const int e = tid + u * WR_NT;
+                const int r = wr_div(e, bg.m_kgp), k = e - r * KGp;
+                const bool ok = e < wch;
+                aw[u] = ok ? r * bg.RSW + k * 16 : -1;
+                vw[u] = *(const v4i*)(wrow + (ok ? r * wrs + k * 16 : 0));
+            }
+        }
+        // pad value: band rows outside the image, columns left of the
+        // image and right of it
+        for (int e = tid; e < nch; e += WR_NT) {
+            const int p = e >> lcpp, ch = e & (cpp - 1);
+            const int row = wr_div(p, bg.m_bw), col = p - row * bg.BW;
+            if (row < r_lo || row >= r_hi || col < a.PW || col >= a.PW + a.W)
+                *(v4i*)(s_band + p * bg.PS + ch * 16) = pad4;
+        }
+        for (int kg = tid; kg < 4 * KS; kg += WR_NT) {
+            int off = 0;  // padding k-groups: any in-band address
+            if (kg < a.KG) {
+                const int tap = kg / a.CB, cb = kg - tap * a.CB;
+                const int ky = tap / a.KW, kx = tap - ky * a.KW;
+                off = (ky * a.DH * bg.BW + kx * a.DW) * bg.PS + cb * 16;
+            }
+            s_kt[kg] = off;
+        }
+        for (int i = tid; i < 768; i += WR_NT)
+            s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
+        if (tid < WM * 16) {
+            const int c = min(co0 + tid, a.Cout - 1);
+            s_pc[tid] = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
+            s_corr[tid] = a.corr ? (uint32_t)a.corr[c] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < WR_SB; ++u)
+            if (ax[u] >= 0) *(v4i*)(s_band + ax[u]) = vx[u];
+#pragma unroll
+        for (int u = 0; u < WR_SW; ++u)
+            if (aw[u] >= 0) *(v4i*)(s_w + aw[u]) = vw[u];
+    }
+    __syncthreads();
+
+    // weights of the lane: channel tile i, K-step s: row co0 + 16 i + col,
+    // bytes 64 s + 16 kgl
+    // (steps past KGp / 4 hold zeros); band offsets of its k-groups
+    v4i wb[KS][WM];
+    int kt[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        kt[s] = s_kt[4 * s + kgl];
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+            wb[s][i] = 4 * s < KGp ? *(const v4i*)(s_w + (16 * i + col) * bg.RSW +
+                                                   64 * s + 16 * kgl)
+                                   : v4i{0, 0, 0, 0};
+    }
+    int cm[WM], ct[WM];
+    int64_t cc[WM];
+    uint32_t ccorr[WM];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+        const int4 pc = s_pc[16 * i + col];
+        cm[i] = pc.x;
+        ct[i] = pc.y;
+        cc[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
+        ccorr[i] = s_corr[16 * i + col];
+    }
+    const int4 hdr = *(const int4*)a.plan;
+    const int pA = hdr.x, pB = hdr.y, pSH = hdr.z;
+    const bool res = a.res != nullptr;
+    const int q = lane & 3;
+    const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
+    const uint32_t sel2 = (q & 1) ? 0x03070105u : 0x06020400u;
+    const int cq = col & ~3;
+
+    {
+        const int npix = min(bg.R, a.OH - oy0) * a.OW;
+        const int ntile = (npix + 15) >> 4;
+        const int64_t pimg = (int64_t)n * a.OH * a.OW + (int64_t)oy0 * a.OW;
+        const int8_t* sb = s_band;
+        for (int t = wave; t < ntile; t += WR_NW) {
+            // residual words of the pixel this lane stores (4 channels)
+            const int pq = 16 * t + 4 * kgl + q;  // pixel within the band
+            const bool pok = pq < npix;
+            const int64_t p = pimg + pq;
+            uint32_t rw[WM];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                rw[i] = 0;
+                const int c0 = co0 + 16 * i + cq;
+                if (res && pok) {
+                    const int8_t* pr = (const int8_t*)a.res + p * a.res_pst + c0;
+                    if (c0 + 3 < a.Cout) {
+                        rw[i] = *(const uint32_t*)pr;
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (c0 + r < a.Cout)
+                                rw[i] |= (uint32_t)(uint8_t)pr[r] << (8 * r);
+                    }
+                }
+            }
+            // the lane's pixel (rows of the MFMA) in the band buffer
+            const int qp = min(16 * t + col, npix - 1);
+            const int r = wr_div(qp, bg.m_ow), ox = qp - r * a.OW;
+            const int8_t* xb = sb + (r * a.SH * bg.BW + ox * a.SW) * bg.PS;
+            v4i acc[WM];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) acc[i] = v4i{0, 0, 0, 0};
+            v4i fa[KS];
+#pragma unroll
+            for (int s = 0; s < KS; ++s) fa[s] = *(const v4i*)(xb + kt[s]);
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        fa[s], wb[s][i], acc[i], 0, 0, 0);
+            // epilogue: lane holds pixels 4 kgl + r, channel co0 + 16 i + col
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                int e[4];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const uint32_t wu = (uint32_t)acc[i][rr] + ccorr[i];
+                    const int q0 =
+                        (int)(((int64_t)(int)wu * cm[i] + cc[i]) >> ct[i]);
+                    e[rr] = min(max(q0, pA), pB) - pA;
+                }
+                if (res) {
+                    const uint32_t rv = quad_transpose(rw[i], sel1, sel2);
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const int v = s_tab[256 + e[rr]] +
+                                      s_tab[512 + ((rv >> (8 * rr)) & 255)];
+                        e[rr] = min(max(v, 0), pSH);
+                    }
+                }
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) e[rr] = s_tab[e[rr]];
+                const int c0 = co0 + 16 * i + cq;
+                const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
+                if (pok) {
+                    int8_t* py = (int8_t*)a.y + p * a.y_pst + c0;
+                    if (c0 + 3 < a.Cout) {
+                        *(uint32_t*)py = wy;
+                    } else {
+#pragma unroll
+                        for (int rr = 0; rr < 4; ++rr)
+                            if (c0 + rr < a.Cout) py[rr] = (int8_t)(wy >> (8 * rr));
+                    }
+                }
+                if (a.y2) {
+                    const uint32_t w2 =
+                        quad_transpose(pack_entries(e, 1), sel1, sel2);
+                    if (pok) {
+                        int8_t* p2 = (int8_t*)a.y2 + p * a.y2_pst + c0;
+                        if (c0 + 3 < a.Cout) {
+                            *(uint32_t*)p2 = w2;
+                        } else {
+#pragma unroll
+                            for (int rr = 0; rr < 4; ++rr)
+                                if (c0 + rr < a.Cout)
+                                    p2[rr] = (int8_t)(w2 >> (8 * rr));
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Geometry for bands of R output rows; lds = 0 when it does not fit in LDS
+// or the band and weight chunks exceed what the threads stage.
+WrGeom wr_geom(const ConvArgs& b, int wm, int R) {
+    WrGeom g;
+    g.R = R;
+    g.BR = (R - 1) * b.SH + (b.KH - 1) * b.DH + 1;
+    g.BW = (b.OW - 1) * b.SW + (b.KW - 1) * b.DW + 1;
+    g.PS = b.Cg + (((b.Cg >> 4) & 1) ? 0 : 16);
+    g.bpi = (b.OH + R - 1) / R;
+    g.nbands = b.N * g.bpi;
+    g.RSW = b.KGp * 16 + 16;
+    const int64_t band = (int64_t)g.BR * g.BW * g.PS;
+    const int64_t bchunks = (int64_t)g.BR * b.W * (b.Cg >> 4);
+    const int64_t wchunks = (int64_t)wm * 16 * b.KGp;
+    g.band_bytes = (int)std::min<int64_t>(band, 1 << 30);
+    auto magic = [](int64_t d) {
+        return (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) /
+                          (uint64_t)std::max<int64_t>(d, 2));
+    };
+    g.m_bw = magic(g.BW);
+    g.m_kgp = magic(b.KGp);
+    g.m_ow = magic(b.OW);
+    g.m_w = magic(b.W);
+    g.KSR = wr_steps(wm, b.KGp / 4);
+    const int64_t bytes =
+        band + (int64_t)wm * 16 * g.RSW + (int64_t)g.KSR * 16;
+    // gfx950 gives a work-group up to 160 KB of LDS
+    g.lds = bytes <= 150 * 1024 && bchunks <= (int64_t)WR_SB * WR_NT &&
+                    wchunks <= (int64_t)WR_SW * WR_NT &&
+                    (int64_t)g.BR * g.BW * (b.Cg >> 4) < (1 << 16)
+                ? (int)bytes
+                : 0;
+    return g;
+}
+
+using WrKern = void (*)(ConvArgs, WrGeom);
+
+template <int WM>
+WrKern wr_kernel(int ks) {
+    switch (ks) {
+        case 1: return &k_conv_wr<WM, 1>;
+        case 2: return &k_conv_wr<WM, 2>;
+        case 3: return &k_conv_wr<WM, 3>;
+        case 5: return &k_conv_wr<WM, 5>;
+        case 9: return &k_conv_wr<WM, 9>;
+        case 18:
+            if constexpr (WM <= 2) return &k_conv_wr<WM, 18>;
+            break;
+        case 36:
+            if constexpr (WM == 1) return &k_conv_wr<WM, 36>;
+            break;
+        default: break;
+    }
+    return nullptr;
+}
+
+WrKern wr_kernel_rt(int wm, int ks) {
+    return wm == 1 ? wr_kernel<1>(ks)
+           : wm == 2 ? wr_kernel<2>(ks)
+           : wm == 4 ? wr_kernel<4>(ks)
+                     : nullptr;
+}
+
+// Work-groups of a kernel resident per CU with `lds` dynamic bytes.
+int wr_resident(WrKern k, int lds) {
+    int nbk = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &nbk, (const void*)k, WR_NT, (size_t)lds) != hipSuccess ||
+        nbk <= 0)
+        nbk = 1;
+    return nbk;
+}
+
+}  // namespace
+
+bool conv_wr_applies(const ConvArgs& b, int epi, int wm) {
+    const uintptr_t xa = (uintptr_t)b.x, ya = (uintptr_t)b.y;
+    if (wm != 1 && wm != 2 && wm != 4) return false;
+    if (!(epi == Q8_TABLE && b.mode == EPI_QUANT && b.fastio && b.plan &&
+          b.G == 1 && b.layout == 0 && b.x_code == 1 && b.x_sc == 1 &&
+          b.rowsum == 0 && b.Cg % 16 == 0 && b.Cg > 0 &&
+          ((b.Cg >> 4) & ((b.Cg >> 4) - 1)) == 0 && b.W >= 2 &&
+          b.OW >= 2 &&
+          b.KGp % 4 == 0 && wr_steps(wm, b.KGp / 4) > 0 && xa % 16 == 0 &&
+          b.x_sp % 16 == 0 && b.x_sn % 16 == 0 && b.y_code == 1 &&
+          ya % 4 == 0 && b.y_pst % 4 == 0 &&
+          (b.res == nullptr ||
+           ((uintptr_t)b.res % 4 == 0 && b.res_pst % 4 == 0)) &&
+          (b.y2 == nullptr ||
+           ((uintptr_t)b.y2 % 4 == 0 && b.y2_pst % 4 == 0)) &&
+          b.M < ((int64_t)1 << 31) && b.N * (int64_t)b.OH < (1 << 30) &&
+          (int64_t)b.H * b.W * b.x_sp < ((int64_t)1 << 31) &&
+          (int64_t)(b.Cout + 128) * b.wp_rstride < ((int64_t)1 << 31)))
+        return false;
+    return wr_geom(b, wm, 1).lds > 0;
+}
+
+bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st) {
+    if (!conv_wr_applies(b, Q8_TABLE, wm)) {
+        set_error("launch_conv_wr", "convolution outside the kernel's scope");
+        return false;
+    }
+    // R: the least (rounds of resident work-groups) x (staging, counted as
+    // 4 tiles, + tiles per wave)
+    const int cus = cu_count();
+    const int64_t cblocks = ceil_div(b.Cout, 16 * wm);
+    int bestR = 1;
+    int64_t best = -1;
+    for (int R = 1; R <= b.OH; ++R) {
+        const WrGeom g = wr_geom(b, wm, R);
+        if (g.lds == 0) break;
+        const int res = wr_resident(wr_kernel_rt(wm, g.KSR), g.lds);
+        const int64_t rounds = ceil_div(g.nbands * cblocks, (int64_t)res * cus);
+        const int64_t cost =
+            rounds * (4 + ceil_div(ceil_div((int64_t)R * b.OW, 16), WR_NW));
+        if (best < 0 || cost < best) {
+            best = cost;
+            bestR = R;
+        }
+    }
+    const WrGeom g = wr_geom(b, wm, bestR);
+    const int64_t gx = g.nbands;
+    if (cblocks > 65535 || gx >= ((int64_t)1 << 31)) {
+        set_error("launch_conv_wr", "grid too large");
+        return false;
+    }
+    const dim3 grid((unsigned)gx, (unsigned)cblocks);
+    const WrKern kern = wr_kernel_rt(wm, g.KSR);
+    if (!kern) {
+        set_error("launch_conv_wr", "no kernel for the K-steps");
+        return false;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(WR_NT), (size_t)g.lds, st, b, g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_hip_error("launch_conv_wr", e);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace qa

@@ -1227,6 +1227,10 @@ class DeviceExecutor:
             # bands of output rows, operands in LDS (the library checks the
             # LDS size and falls back when the band does not fit)
             out += [0x10800 | wm for wm in (1, 2, 4) if wm <= wm_max]
+            # weights held in registers (K up to 36 / wm steps of 64 bytes;
+            # the library checks the rest and falls back)
+            out += [0x11000 | wm for wm in (1, 2, 4)
+                    if wm <= wm_max and d.w_kgp // 4 <= 36 // wm]
         for wm in (1, 2, 4, 8):
             if wm > wm_max:
                 break

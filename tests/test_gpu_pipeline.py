@@ -335,3 +335,50 @@ def test_graph_replay_matches_eager(hip):
 def test_uncalibrated_container_refuses(hip):
     with pytest.raises(ValueError, match="not calibrated"):
         QuantContainer(G.mini_yolo()).run_graph(_images(0, 1, 32), "integer")
+
+
+@pytest.mark.parametrize("cin,cout,k,stride,pad,dil,size,residual", [
+    (64, 64, 3, 1, 1, 1, 23, False),   # 4 channel tiles, ragged rows
+    (32, 40, 3, 2, 1, 1, 31, True),    # partial channel quad, stride 2
+    (48, 16, 3, 1, 2, 2, 17, False),   # 3 channel blocks a tap, dilation 2
+    (16, 96, 1, 1, 0, 1, 9, True),     # 1x1, two channel blocks of 64
+    (128, 24, 3, 1, 0, 1, 12, False),  # no padding, 18 K-steps
+])
+def test_weights_in_registers_kernel(hip, tmp_path, cin, cout, k, stride, pad,
+                                     dil, size, residual):
+    """The convolution kernel that holds its weights in VGPRs (tile codes
+    0x11000 | wm) equals the oracle on ragged bands, partial channel
+    blocks, strides, dilation and a fused residual Add, for every tile code
+    of the layer."""
+    b = G.GraphBuilder(17)
+    r = None
+    if residual:  # built first, so that the Add fuses into the k x k conv
+        r = b.conv("images", cin, cout, 1, stride, pad=0,
+                   w_scale=np.sqrt(1.0 / cin))
+    y = b.silu(b.conv("images", cin, cout, k, stride, pad=pad, dilation=dil,
+                      w_scale=np.sqrt(1.0 / (cin * k * k))))
+    if residual:
+        y = b.op("Add", [r, y])
+    g = b.build("images", [None, cin, size, size], y)
+    calib = [Stream(110 + i).normal((3, cin, size, size)).astype(np.float32)
+             for i in range(2)]
+    c = _calibrated(g, "int8", True, calib)
+    x = Stream(120).normal((3, cin, size, size)).astype(np.float32)
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    oracle.run(x, keep=True)
+    ex = c.executor({"images": x.shape})
+    main = [t for t in ex.tunables
+            if (t[1].res is not None) == residual and t[1].KH == k]
+    assert len(main) == 1
+    assert any(code & 0x11000 == 0x11000 for code in main[0][2])
+    codes = main[0][2]
+    for code in codes:
+        for _, d, _, _ in ex.tunables:
+            d.tile = code if d is main[0][1] else 0
+        ex.run({"images": x})
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, tile {code:#x}")
