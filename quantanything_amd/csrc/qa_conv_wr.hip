@@ -66,7 +66,10 @@ __device__ __forceinline__ int wr_div(int n, uint32_t m) {
 
 // KS: K-steps of 64 bytes, a compile-time count (the packed K rounded up
 // to one of the instantiated counts; the extra steps have zero weights).
-template <int WM, int KS>
+// RES: a residual Add is fused (its words are fetched one tile ahead; the
+// variant without it has no loads in the tile loop, so no wait there on
+// the counter that the output stores share).
+template <int WM, int KS, bool RES>
 __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
     extern __shared__ int4 lds4[];
     int8_t* s_band = (int8_t*)lds4;                          // band
@@ -197,7 +200,6 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
     }
     const int4 hdr = *(const int4*)a.plan;
     const int pA = hdr.x, pB = hdr.y, pSH = hdr.z;
-    const bool res = a.res != nullptr;
     const int q = lane & 3;
     const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
     const uint32_t sel2 = (q & 1) ? 0x03070105u : 0x06020400u;
@@ -208,27 +210,29 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
         const int ntile = (npix + 15) >> 4;
         const int64_t pimg = (int64_t)n * a.OH * a.OW + (int64_t)oy0 * a.OW;
         const int8_t* sb = s_band;
+        // residual words (4 channels of the pixel this lane stores) of
+        // tile t: 0 past the band or the channels
+        auto load_res = [&](int t, uint32_t (&rw)[WM]) {
+            const int pq = 16 * t + 4 * kgl + q;
+            const bool ok = pq < npix;
+            const int8_t* pr = (const int8_t*)a.res + (pimg + pq) * a.res_pst;
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const int c0 = co0 + 16 * i + cq;
+                rw[i] = ok && c0 < a.Cout ? *(const uint32_t*)(pr + c0) : 0u;
+            }
+        };
+        uint32_t rwn[WM];
+        if (RES) load_res(wave, rwn);
         for (int t = wave; t < ntile; t += WR_NW) {
-            // residual words of the pixel this lane stores (4 channels)
             const int pq = 16 * t + 4 * kgl + q;  // pixel within the band
             const bool pok = pq < npix;
             const int64_t p = pimg + pq;
             uint32_t rw[WM];
+            if (RES) {
 #pragma unroll
-            for (int i = 0; i < WM; ++i) {
-                rw[i] = 0;
-                const int c0 = co0 + 16 * i + cq;
-                if (res && pok) {
-                    const int8_t* pr = (const int8_t*)a.res + p * a.res_pst + c0;
-                    if (c0 + 3 < a.Cout) {
-                        rw[i] = *(const uint32_t*)pr;
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            if (c0 + r < a.Cout)
-                                rw[i] |= (uint32_t)(uint8_t)pr[r] << (8 * r);
-                    }
-                }
+                for (int i = 0; i < WM; ++i) rw[i] = rwn[i];
+                if (t + WR_NW < ntile) load_res(t + WR_NW, rwn);
             }
             // the lane's pixel (rows of the MFMA) in the band buffer
             const int qp = min(16 * t + col, npix - 1);
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
                         (int)(((int64_t)(int)wu * cm[i] + cc[i]) >> ct[i]);
                     e[rr] = min(max(q0, pA), pB) - pA;
                 }
-                if (res) {
+                if (RES) {
                     const uint32_t rv = quad_transpose(rw[i], sel1, sel2);
 #pragma unroll
                     for (int rr = 0; rr < 4; ++rr) {
@@ -268,32 +272,15 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
                 }
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) e[rr] = s_tab[e[rr]];
-                const int c0 = co0 + 16 * i + cq;
+                const int c0 = co0 + 16 * i + cq;  // Cout % 4 == 0
+                const bool sok = pok && c0 < a.Cout;
                 const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
-                if (pok) {
-                    int8_t* py = (int8_t*)a.y + p * a.y_pst + c0;
-                    if (c0 + 3 < a.Cout) {
-                        *(uint32_t*)py = wy;
-                    } else {
-#pragma unroll
-                        for (int rr = 0; rr < 4; ++rr)
-                            if (c0 + rr < a.Cout) py[rr] = (int8_t)(wy >> (8 * rr));
-                    }
-                }
+                if (sok) *(uint32_t*)((int8_t*)a.y + p * a.y_pst + c0) = wy;
                 if (a.y2) {
                     const uint32_t w2 =
                         quad_transpose(pack_entries(e, 1), sel1, sel2);
-                    if (pok) {
-                        int8_t* p2 = (int8_t*)a.y2 + p * a.y2_pst + c0;
-                        if (c0 + 3 < a.Cout) {
-                            *(uint32_t*)p2 = w2;
-                        } else {
-#pragma unroll
-                            for (int rr = 0; rr < 4; ++rr)
-                                if (c0 + rr < a.Cout)
-                                    p2[rr] = (int8_t)(w2 >> (8 * rr));
-                        }
-                    }
+                    if (sok)
+                        *(uint32_t*)((int8_t*)a.y2 + p * a.y2_pst + c0) = w2;
                 }
             }
         }
@@ -337,29 +324,34 @@ WrGeom wr_geom(const ConvArgs& b, int wm, int R) {
 
 using WrKern = void (*)(ConvArgs, WrGeom);
 
-template <int WM>
+template <int WM, bool RES>
 WrKern wr_kernel(int ks) {
     switch (ks) {
-        case 1: return &k_conv_wr<WM, 1>;
-        case 2: return &k_conv_wr<WM, 2>;
-        case 3: return &k_conv_wr<WM, 3>;
-        case 5: return &k_conv_wr<WM, 5>;
-        case 9: return &k_conv_wr<WM, 9>;
+        case 1: return &k_conv_wr<WM, 1, RES>;
+        case 2: return &k_conv_wr<WM, 2, RES>;
+        case 3: return &k_conv_wr<WM, 3, RES>;
+        case 5: return &k_conv_wr<WM, 5, RES>;
+        case 9: return &k_conv_wr<WM, 9, RES>;
         case 18:
-            if constexpr (WM <= 2) return &k_conv_wr<WM, 18>;
+            if constexpr (WM <= 2) return &k_conv_wr<WM, 18, RES>;
             break;
         case 36:
-            if constexpr (WM == 1) return &k_conv_wr<WM, 36>;
+            if constexpr (WM == 1) return &k_conv_wr<WM, 36, RES>;
             break;
         default: break;
     }
     return nullptr;
 }
 
-WrKern wr_kernel_rt(int wm, int ks) {
-    return wm == 1 ? wr_kernel<1>(ks)
-           : wm == 2 ? wr_kernel<2>(ks)
-           : wm == 4 ? wr_kernel<4>(ks)
+WrKern wr_kernel_rt(int wm, int ks, bool res) {
+    if (res)
+        return wm == 1 ? wr_kernel<1, true>(ks)
+               : wm == 2 ? wr_kernel<2, true>(ks)
+               : wm == 4 ? wr_kernel<4, true>(ks)
+                         : nullptr;
+    return wm == 1 ? wr_kernel<1, false>(ks)
+           : wm == 2 ? wr_kernel<2, false>(ks)
+           : wm == 4 ? wr_kernel<4, false>(ks)
                      : nullptr;
 }
 
@@ -382,6 +374,7 @@ bool conv_wr_applies(const ConvArgs& b, int epi, int wm) {
           b.G == 1 && b.layout == 0 && b.x_code == 1 && b.x_sc == 1 &&
           b.rowsum == 0 && b.Cg % 16 == 0 && b.Cg > 0 &&
           ((b.Cg >> 4) & ((b.Cg >> 4) - 1)) == 0 && b.W >= 2 &&
+          b.Cout % 4 == 0 &&
           b.OW >= 2 &&
           b.KGp % 4 == 0 && wr_steps(wm, b.KGp / 4) > 0 && xa % 16 == 0 &&
           b.x_sp % 16 == 0 && b.x_sn % 16 == 0 && b.y_code == 1 &&
@@ -411,7 +404,7 @@ bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st) {
     for (int R = 1; R <= b.OH; ++R) {
         const WrGeom g = wr_geom(b, wm, R);
         if (g.lds == 0) break;
-        const int res = wr_resident(wr_kernel_rt(wm, g.KSR), g.lds);
+        const int res = wr_resident(wr_kernel_rt(wm, g.KSR, b.res != nullptr), g.lds);
         const int64_t rounds = ceil_div(g.nbands * cblocks, (int64_t)res * cus);
         const int64_t cost =
             rounds * (4 + ceil_div(ceil_div((int64_t)R * b.OW, 16), WR_NW));
@@ -427,7 +420,7 @@ bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st) {
         return false;
     }
     const dim3 grid((unsigned)gx, (unsigned)cblocks);
-    const WrKern kern = wr_kernel_rt(wm, g.KSR);
+    const WrKern kern = wr_kernel_rt(wm, g.KSR, b.res != nullptr);
     if (!kern) {
         set_error("launch_conv_wr", "no kernel for the K-steps");
         return false;
