@@ -63,10 +63,15 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
             return launch_conv_band(b, bw, st);
     }
     // weights in registers, bands in LDS (tile hint bit 12, with wm in the
-    // low bits)
+    // low bits); without a hint, the default for convolutions of more than
+    // one 64-byte K-step (measured the fastest choice for most 3x3 layers)
     if ((a.tile_hint & TILE_VALID) && ((a.tile_hint >> 12) & 1)) {
         const int ww = a.tile_hint & 0xff;
         if (conv_wr_applies(b, epi, ww)) return launch_conv_wr(b, ww, st);
+    }
+    if (!(a.tile_hint & TILE_VALID) && a.KGp > 4 && (a.KH > 1 || a.KW > 1)) {
+        for (int ww = a.Cog >= 64 ? 4 : a.Cog >= 32 ? 2 : 1; ww >= 1; ww >>= 1)
+            if (conv_wr_applies(b, epi, ww)) return launch_conv_wr(b, ww, st);
     }
     // large GEMMs: 128 x 128 blocks (tile hint bit 10 chooses)
     if (gemm_big_applies(b, epi)) {
