@@ -20,6 +20,7 @@ namespace qa {
 namespace {
 
 constexpr int QIN_THREADS = 256;
+constexpr int QIN_U = 2;  // input items a thread loads per round
 
 struct QinGeom {
     int R;           // output rows per band
@@ -30,6 +31,7 @@ struct QinGeom {
     int f32;         // the float32 quantization form applies
     uint64_t mg_ow;  // ceil(2^32 / OW)
     uint64_t mg_pw;  // ceil(2^32 / pad columns per row)
+    uint64_t mg_gw;  // ceil(2^32 / items per input row)
 };
 
 // Quantized word of one pixel: channel c in byte c (storage offset so
@@ -91,51 +93,57 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
     const bool f32 = g.f32;
     constexpr int PX = VEC ? 4 : 1;  // pixels per item
     const int GW = a.W / PX;          // items per input row
-    // wave w fills rows w, w + 4, ..., two rows at a time (loads of both
-    // in flight); lane = item of the row
-    for (int r0 = wave; r0 < g.IR; r0 += 8) {
-        for (int u = lane; u < GW; u += 64) {
-            float v[2][CIN][PX];
-            bool in[2];
+    // items (PX pixels of one input row, all CIN planes) i = tid + 256 k:
+    // row i / GW, item i % GW; QIN_U items a thread, all their loads in
+    // flight before the first quantization (one memory round trip a
+    // round)
+    const int items = g.IR * GW;
+    for (int i0 = tid; i0 < items; i0 += QIN_THREADS * QIN_U) {
+        float v[QIN_U][CIN][PX];
+        int dsto[QIN_U];
+        bool in[QIN_U];
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int iy = iy_base + min(r0 + 4 * k, g.IR - 1);
-                in[k] = (unsigned)iy < (unsigned)a.H;
-                const float* src = xn + (in[k] ? iy : 0) * a.W + PX * u;
+        for (int k = 0; k < QIN_U; ++k) {
+            const int i = i0 + k * QIN_THREADS;
+            const bool ok = i < items;
+            const int r = ok ? div_magic(i, g.mg_gw) : 0;
+            const int u = ok ? i - r * GW : 0;
+            const int iy = iy_base + r;
+            in[k] = ok && (unsigned)iy < (unsigned)a.H;
+            dsto[k] = ok ? r * g.RW + g.c0 + PX * u : -1;
+            const float* src = xn + (in[k] ? iy : 0) * a.W + PX * u;
 #pragma unroll
-                for (int c = 0; c < CIN; ++c) {
-                    if (VEC) {
-                        const float4 t = *(const float4*)(src + c * HW);
-                        v[k][c][0] = t.x;
-                        v[k][c][PX > 1 ? 1 : 0] = t.y;
-                        v[k][c][PX > 2 ? 2 : 0] = t.z;
-                        v[k][c][PX > 3 ? 3 : 0] = t.w;
-                    } else {
-                        v[k][c][0] = src[c * HW];
-                    }
+            for (int c = 0; c < CIN; ++c) {
+                if (VEC) {
+                    const float4 t = *(const float4*)(src + c * HW);
+                    v[k][c][0] = t.x;
+                    v[k][c][PX > 1 ? 1 : 0] = t.y;
+                    v[k][c][PX > 2 ? 2 : 0] = t.z;
+                    v[k][c][PX > 3 ? 3 : 0] = t.w;
+                } else {
+                    v[k][c][0] = src[c * HW];
                 }
             }
+        }
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int r = r0 + 4 * k;
-                if (r >= g.IR) break;
-                uint32_t w[PX];
+        for (int k = 0; k < QIN_U; ++k) {
+            if (dsto[k] < 0) continue;
+            uint32_t w[PX];
 #pragma unroll
-                for (int p = 0; p < PX; ++p) {
-                    float f[CIN];
+            for (int p = 0; p < PX; ++p) {
+                float f[CIN];
 #pragma unroll
-                    for (int c = 0; c < CIN; ++c) f[c] = v[k][c][p];
-                    w[p] = pixel_word<CIN>(f, q, invf, f32);
-                    if (!in[k]) w[p] = (uint32_t)pv;
-                }
-                int* dst = s_raw + r * g.RW + g.c0 + PX * u;
-                if (VEC)
-                    *(uint4*)dst = make_uint4(w[0], w[PX > 1 ? 1 : 0],
-                                              w[PX > 2 ? 2 : 0],
-                                              w[PX > 3 ? 3 : 0]);
-                else
-                    *dst = (int)w[0];
+                for (int c = 0; c < CIN; ++c) f[c] = v[k][c][p];
+                w[p] = pixel_word<CIN>(f, q, invf, f32);
+                if (!in[k]) w[p] = (uint32_t)pv;
             }
+            int* dst = s_raw + dsto[k];
+            if (VEC)
+                *(uint4*)dst = make_uint4(w[0], w[PX > 1 ? 1 : 0],
+                                          w[PX > 2 ? 2 : 0],
+                                          w[PX > 3 ? 3 : 0]);
+            else
+                *dst = (int)w[0];
         }
     }
     {  // pad columns: c0 - PW .. c0 - 1 and c0 + W .. RW - 1
@@ -291,6 +299,7 @@ bool launch_conv_qin(const ConvArgs& a0, const QinArgs& q, hipStream_t st) {
     }
     g.mg_ow = magic(a.OW);
     g.mg_pw = magic(std::max(g.RW - (g.c0 - a.PW) - a.W, 1));
+    g.mg_gw = magic(std::max(vec ? a.W / 4 : a.W, 1));
     auto go = [&](auto kern) {
         kern<<<(unsigned)blocks, QIN_THREADS, shm, st>>>(a, q, g);
     };
