@@ -321,6 +321,20 @@ typedef struct qa_pool_params {
 int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
                    void* stream);
 
+/* Two chained convolutions in one launch (the bottleneck of a C2f block):
+ * d1 and d2 are int8 3x3 stride-1 pad-1 convolutions C -> C (C = 16, 32
+ * or 64; packed layout 0, one group, epilogue plans, dense channels-last
+ * tensors), d1 without residual or rescaled copy, and d2 reads d1's output
+ * (d2->x == d1->y). The result is what qa_d_conv(d1) then qa_d_conv(d2)
+ * would store at d2->y (and d2->y2), with d2's residual Add; d1->y is not
+ * written (the intermediate stays in LDS). Returns -1, launching nothing,
+ * for any other pair. The reference runs the two convolutions and the Add
+ * one after another (quant_layers.py:320-335 twice, quant_layers.py:493-
+ * 513). qa_conv_pair_supported checks a pair without launching (1 or 0). */
+int qa_conv_pair_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
+int qa_d_conv_pair(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                   void* stream);
+
 /* Graph-input quantization fused into the first convolution: x is the
  * float32 NCHW input [N, C, H, W]; it is quantized exactly as
  * qa_d_quantize_nhwc would (scale, zp, clip; storage offset

@@ -184,6 +184,15 @@ bool launch_conv_band(const ConvArgs& b, int wm, hipStream_t st);
 // work-group (K <= 36 / wm K-steps of 64 bytes).
 bool conv_wr_applies(const ConvArgs& b, int epi, int wm);
 bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st);
+// Launch form of a descriptor's arguments (fastio, pixel strides, magic
+// divisors); returns the epilogue variant (qa_conv_mfma.hip).
+int fast_io_args(const ConvArgs& a, ConvArgs& b, int epi);
+// Two chained 3x3 stride-1 convolutions (C -> C, C in {16, 32, 64}) in one
+// launch, the intermediate kept in LDS (qa_conv_pair.hip); arguments in
+// launch form.
+bool conv_pair_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
+                       int epi2);
+bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2, hipStream_t st);
 // 16-bit operands on the FP64 matrix cores (qa_conv_f64.hip), exact.
 bool launch_conv_f64(const ConvArgs& a, hipStream_t st);
 

@@ -708,6 +708,37 @@ QA_API int qa_d_conv(const qa_conv_desc* d, void* stream_) {
     return launch_conv_valu(a, st) ? 0 : -1;
 }
 
+// Launch forms of two chained convolution descriptors that the fused
+// kernel takes, or false.
+static bool pair_args(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                      ConvArgs& b1, ConvArgs& b2, const char* who) {
+    ConvArgs a1, a2;
+    if (desc_args(d1, a1, who) != 1 || desc_args(d2, a2, who) != 1)
+        return false;
+    const int e1 = fast_io_args(a1, b1, -1);  // Q8_TABLE or -1
+    const int e2 = fast_io_args(a2, b2, -1);
+    return conv_pair_applies(b1, e1, b2, e2);
+}
+
+QA_API int qa_conv_pair_supported(const qa_conv_desc* d1,
+                                  const qa_conv_desc* d2) {
+    ConvArgs b1, b2;
+    return pair_args(d1, d2, b1, b2, "qa_conv_pair_supported") ? 1 : 0;
+}
+
+QA_API int qa_d_conv_pair(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                          void* stream_) {
+    ConvArgs b1, b2;
+    if (!pair_args(d1, d2, b1, b2, "qa_d_conv_pair")) {
+        set_error("qa_d_conv_pair",
+                  "needs two int8 3x3 stride-1 C -> C convolutions (C 16, "
+                  "32 or 64) with table plans, the second reading the "
+                  "first's output");
+        return -1;
+    }
+    return launch_conv_pair(b1, b2, (hipStream_t)stream_) ? 0 : -1;
+}
+
 QA_API int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
                           void* stream_) {
     hipStream_t st = (hipStream_t)stream_;

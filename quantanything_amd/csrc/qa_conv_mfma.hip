@@ -9,29 +9,12 @@ bool mfma_launch_lds(const ConvArgs& b, int wm, bool split, int epi,
     return launch_variant<true>(b, wm, split, epi, st);
 }
 
-// Tile choice (from measured sweeps over the channel-block width WM and
-// K-splitting on MI355X): the widest channel block that still gives about
-// 1.5 waves per SIMD (0.75 when K is long, >= 9 steps: those waves are long
-// enough on their own), and the 4 waves of a work-group split K only when
-// even 16-channel blocks leave most SIMDs idle.
-bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
-    if (a.M <= 0 || a.Cog <= 0 || a.G <= 0) return true;
-    if (a.M >= ((int64_t)1 << 31) || a.KGp < 4 || (a.KGp & 3) ||
-        a.KGp >= (1 << 16) || a.CB < 1 || a.KW < 1 ||
-        (int64_t)(a.KH - 1) * a.DH >= 32768 ||
-        (int64_t)(a.KW - 1) * a.DW >= 32768) {
-        set_error("launch_conv_mfma", "unsupported problem size");
-        return false;
-    }
-    int epi = a.mode;
-    if (a.mode == EPI_QUANT) {
-        if (a.y_code != 1) {
-            set_error("launch_conv_mfma", "int8 output expected");
-            return false;
-        }
-        epi = Q8_GENERAL;  // chosen below, once the layout is known
-    }
-    ConvArgs b = a;
+// The launch form of a descriptor's arguments: whether the output (and
+// residual / copy) is dense channels-last (fastio, pixel strides *_pst),
+// the table epilogue when a plan applies, and the magic divisors of the
+// tap decode. Returns the epilogue variant (epi when no plan applies).
+int fast_io_args(const ConvArgs& a, ConvArgs& b, int epi) {
+    b = a;
     // dense channels-last int8 output (and residual / copy): 4-channel
     // words of a pixel at pixel * sp + channel, 4-byte aligned
     {
@@ -54,6 +37,33 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     if (a.mode == EPI_QUANT && a.plan && b.fastio) epi = Q8_TABLE;
     b.mg_cb = (((uint64_t)1 << 32) + a.CB - 1) / (uint64_t)a.CB;
     b.mg_kw = (((uint64_t)1 << 32) + a.KW - 1) / (uint64_t)a.KW;
+    return epi;
+}
+
+// Tile choice (from measured sweeps over the channel-block width WM and
+// K-splitting on MI355X): the widest channel block that still gives about
+// 1.5 waves per SIMD (0.75 when K is long, >= 9 steps: those waves are long
+// enough on their own), and the 4 waves of a work-group split K only when
+// even 16-channel blocks leave most SIMDs idle.
+bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
+    if (a.M <= 0 || a.Cog <= 0 || a.G <= 0) return true;
+    if (a.M >= ((int64_t)1 << 31) || a.KGp < 4 || (a.KGp & 3) ||
+        a.KGp >= (1 << 16) || a.CB < 1 || a.KW < 1 ||
+        (int64_t)(a.KH - 1) * a.DH >= 32768 ||
+        (int64_t)(a.KW - 1) * a.DW >= 32768) {
+        set_error("launch_conv_mfma", "unsupported problem size");
+        return false;
+    }
+    int epi = a.mode;
+    if (a.mode == EPI_QUANT) {
+        if (a.y_code != 1) {
+            set_error("launch_conv_mfma", "int8 output expected");
+            return false;
+        }
+        epi = Q8_GENERAL;  // chosen below, once the layout is known
+    }
+    ConvArgs b;
+    epi = fast_io_args(a, b, epi);
     // bands of output rows with operands in LDS (tile hint bit 11, with
     // wm in the low bits)
     // (ignored, like every hint, where it does not apply)

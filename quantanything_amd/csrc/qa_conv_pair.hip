@@ -1,0 +1,427 @@
+// Two chained 3x3 convolutions in one launch: y = f2(f1(x)) (+ residual),
+// the bottleneck of a C2f block (3x3 stride-1 conv, SiLU, 3x3 conv, SiLU,
+// Add of the block input), each conv C -> C channels with C in {16, 32, 64}.
+//
+// A work-group owns R output rows of one image and all C channels. It
+// stages in LDS, with every load of a thread in flight before its stores:
+// the input rows oy0 - 2 .. oy0 + R + 1 (the image padding holds conv 1's
+// pad value), and both convs' packed weight rows. Phase 1 computes conv 1
+// over the intermediate rows oy0 - 1 .. oy0 + R that lie inside the image
+// (halo rows are recomputed by the neighbouring bands) and writes its
+// stored bytes (table epilogue) into a second LDS band whose image padding
+// holds conv 2's pad value; the intermediate tensor never goes to HBM.
+// Phase 2 computes conv 2 from that band with the full table epilogue
+// (residual Add from HBM, rescaled copy) and stores the output words.
+// Each phase holds its conv's weight fragments in VGPRs (C/16 channel tiles
+// x KS K-steps) and reads only the activation fragment from LDS per K-step;
+// v_mfma_i32_16x16x64_i8 with 16 pixels as rows and 16 channels as
+// columns, the k-group layout of the packed layout-0 weights (tap kg / CB,
+// channels 16 (kg % CB) ..), one k-group offset table for both bands (same
+// width and pixel stride).
+#include "qa_conv_mfma.h"
+
+namespace qa {
+namespace {
+
+constexpr int CP_NW = 8;           // waves per work-group
+constexpr int CP_NT = 64 * CP_NW;  // threads per work-group
+constexpr int CP_SB = 8;           // band chunks (16 bytes) a thread stages
+constexpr int CP_SW = 5;           // weight chunks a thread stages per conv
+
+struct PairGeom {
+    int R;                 // output rows per band
+    int BW, PS;            // band width (pixels) and pixel bytes in LDS
+    int bpi, nbands;       // bands per image, in all
+    int xb_bytes;          // input band (R + 4 rows)
+    int mb_bytes;          // intermediate band (R + 2 rows)
+    int RSW;               // LDS row stride of the staged weights
+    int lds;               // dynamic LDS bytes (0: does not fit)
+    uint32_t m_w, m_bw, m_kgp;  // ceil(2^32 / d), d >= 2
+};
+
+__device__ __forceinline__ int cp_div(int n, uint32_t m) {
+    return (int)__umulhi((uint32_t)n, m);
+}
+
+template <int WM, bool RES>
+__global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
+                                                     PairGeom g) {
+    constexpr int C = 16 * WM;          // channels of every tensor
+    constexpr int KS = (9 * WM + 3) / 4;  // K-steps: KGp = round_up(9 WM, 4)
+    constexpr int LCPP = WM == 1 ? 0 : WM == 2 ? 1 : 2;  // log2 chunks/pixel
+    extern __shared__ int4 lds4[];
+    int8_t* s_x = (int8_t*)lds4;         // input band
+    int8_t* s_m = s_x + g.xb_bytes;      // intermediate band
+    int8_t* s_w1 = s_m + g.mb_bytes;     // conv 1 weights: C rows x RSW
+    int8_t* s_w2 = s_w1 + C * g.RSW;     // conv 2 weights
+    int* s_kt = (int*)(s_w2 + C * g.RSW);  // 4 KS k-group offsets
+    __shared__ int s_tab1[256];
+    __shared__ int s_tab2[768];
+    __shared__ int4 s_pc[2][C];
+    __shared__ uint32_t s_corr[2][C];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, kgl = lane >> 4;
+    const int KGp = 4 * KS;
+    const int W = a1.W, OW = a2.OW, OH = a2.OH;
+    const int band = blockIdx.x;
+    const int n = band / g.bpi;
+    const int oy0 = (band - n * g.bpi) * g.R;
+    const int R = min(g.R, OH - oy0);   // output rows of this band
+    const int iy0 = oy0 - 2;            // image row of input band row 0
+    const int BR = R + 4;               // input band rows
+    const int MR = R + 2;               // intermediate band rows
+    const int pv1 = splat4(a1.pad_value), pv2 = splat4(a2.pad_value);
+    const v4i pad1 = {pv1, pv1, pv1, pv1}, pad2 = {pv2, pv2, pv2, pv2};
+
+    // ---- staging: input rows inside the image as one run of pixels from
+    // row iy0 + r_lo (chunk e: pixel e / C16, part e % C16, at band row
+    // r_lo + p / W, column 1 + p % W), then the weight rows of both convs
+    // (chunk e: row e / KGp, part e % KGp); all loads before the stores
+    const int r_lo = max(0, -iy0), r_hi = min(BR, a1.H - iy0);
+    const int nreal = max(r_hi - r_lo, 0) * W * WM;
+    const int wch = C * KGp;
+    {
+        v4i vx[CP_SB], w1[CP_SW], w2[CP_SW];
+        int ax[CP_SB], aw[CP_SW];
+        {
+            const int xsp = (int)a1.x_sp;
+            const int8_t* xrow = (const int8_t*)a1.x + (int64_t)n * a1.x_sn +
+                                 (int64_t)(iy0 + r_lo) * W * a1.x_sp;
+            const int ch = tid & (WM - 1);  // the same part for every u
+#pragma unroll
+            for (int u = 0; u < CP_SB; ++u) {
+                const int e = tid + u * CP_NT;
+                const int p = e >> LCPP;
+                const int row = cp_div(p, g.m_w), ix = p - row * W;
+                const bool ok = e < nreal;
+                ax[u] = ok ? ((r_lo + row) * g.BW + ix + 1) * g.PS + ch * 16
+                           : -1;
+                vx[u] = *(const v4i*)(xrow + (ok ? p * xsp + ch * 16 : 0));
+            }
+        }
+        {
+            const int rs1 = (int)a1.wp_rstride, rs2 = (int)a2.wp_rstride;
+#pragma unroll
+            for (int u = 0; u < CP_SW; ++u) {
+                const int e = tid + u * CP_NT;
+                const int r = cp_div(e, g.m_kgp), k = e - r * KGp;
+                const bool ok = e < wch;
+                aw[u] = ok ? r * g.RSW + k * 16 : -1;
+                w1[u] = *(const v4i*)(a1.wp + (ok ? r * rs1 + k * 16 : 0));
+                w2[u] = *(const v4i*)(a2.wp + (ok ? r * rs2 + k * 16 : 0));
+            }
+        }
+        // pad values: input band rows outside the image and its two pad
+        // columns; intermediate rows outside the image and its pad columns
+        for (int e = tid; e < BR * g.BW * WM; e += CP_NT) {
+            const int p = e >> LCPP, ch = e & (WM - 1);
+            const int row = cp_div(p, g.m_bw), c = p - row * g.BW;
+            if (row < r_lo || row >= r_hi || c == 0 || c == g.BW - 1)
+                *(v4i*)(s_x + p * g.PS + ch * 16) = pad1;
+        }
+        for (int e = tid; e < MR * g.BW * WM; e += CP_NT) {
+            const int p = e >> LCPP, ch = e & (WM - 1);
+            const int row = cp_div(p, g.m_bw), c = p - row * g.BW;
+            const int my = oy0 - 1 + row;
+            if ((unsigned)my >= (unsigned)OH || c == 0 || c == g.BW - 1)
+                *(v4i*)(s_m + p * g.PS + ch * 16) = pad2;
+        }
+        for (int kg = tid; kg < KGp; kg += CP_NT) {
+            int off = 0;  // padding k-groups: any in-band address
+            if (kg < 9 * WM) {
+                const int tap = kg / WM, cb = kg - tap * WM;
+                const int ky = tap / 3, kx = tap - ky * 3;
+                off = (ky * g.BW + kx) * g.PS + cb * 16;
+            }
+            s_kt[kg] = off;
+        }
+        for (int i = tid; i < 256; i += CP_NT)
+            s_tab1[i] = ((const int*)((const char*)a1.plan + PLAN_E))[i];
+        for (int i = tid; i < 768; i += CP_NT)
+            s_tab2[i] = ((const int*)((const char*)a2.plan + PLAN_E))[i];
+        if (tid < C) {
+            s_pc[0][tid] = ((const int4*)((const char*)a1.plan + PLAN_CH))[tid];
+            s_corr[0][tid] = a1.corr ? (uint32_t)a1.corr[tid] : 0u;
+        } else if (tid < 2 * C) {
+            const int c = tid - C;
+            s_pc[1][c] = ((const int4*)((const char*)a2.plan + PLAN_CH))[c];
+            s_corr[1][c] = a2.corr ? (uint32_t)a2.corr[c] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < CP_SB; ++u)
+            if (ax[u] >= 0) *(v4i*)(s_x + ax[u]) = vx[u];
+#pragma unroll
+        for (int u = 0; u < CP_SW; ++u)
+            if (aw[u] >= 0) {
+                *(v4i*)(s_w1 + aw[u]) = w1[u];
+                *(v4i*)(s_w2 + aw[u]) = w2[u];
+            }
+    }
+    __syncthreads();
+
+    const int q = lane & 3;
+    const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
+    const uint32_t sel2 = (q & 1) ? 0x03070105u : 0x06020400u;
+    const int cq = col & ~3;
+    int kt[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kt[s] = s_kt[4 * s + kgl];
+    v4i wb[KS][WM];
+    int cm[WM], ct[WM];
+    int64_t cc[WM];
+    uint32_t ccorr[WM];
+    auto load_conv = [&](const int8_t* s_w, int which) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+                wb[s][i] = *(const v4i*)(s_w + (16 * i + col) * g.RSW +
+                                         64 * s + 16 * kgl);
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int4 pc = s_pc[which][16 * i + col];
+            cm[i] = pc.x;
+            ct[i] = pc.y;
+            cc[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                              (uint32_t)pc.z);
+            ccorr[i] = s_corr[which][16 * i + col];
+        }
+    };
+    // accumulators of the 16 pixels whose band base offsets are xb
+    auto tile_mfma = [&](const int8_t* xb, v4i (&acc)[WM]) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i) acc[i] = v4i{0, 0, 0, 0};
+        v4i fa[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) fa[s] = *(const v4i*)(xb + kt[s]);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+                acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    fa[s], wb[s][i], acc[i], 0, 0, 0);
+    };
+
+    // ---- phase 1: conv 1 over the intermediate rows inside the image ----
+    load_conv(s_w1, 0);
+    {
+        const int4 h1 = *(const int4*)a1.plan;
+        const int mr_lo = max(0, 1 - oy0), mr_hi = min(MR, OH + 1 - oy0);
+        const int npix = (mr_hi - mr_lo) * OW;
+        const int ntile = (npix + 15) >> 4;
+        for (int t = wave; t < ntile; t += CP_NW) {
+            const int qp = mr_lo * OW + min(16 * t + col, npix - 1);
+            const int mr = cp_div(qp, g.m_w), mc = qp - mr * OW;
+            v4i acc[WM];
+            tile_mfma(s_x + (mr * g.BW + mc) * g.PS, acc);
+            // lane q stores pixel 16 t + 4 kgl + q, channels 16 i + cq ..
+            const int pq = 16 * t + 4 * kgl + q;
+            const bool pok = pq < npix;
+            const int sq = mr_lo * OW + min(pq, npix - 1);
+            const int sr = cp_div(sq, g.m_w), sc = sq - sr * OW;
+            int8_t* dst = s_m + (sr * g.BW + sc + 1) * g.PS + cq;
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                int e[4];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const uint32_t wu = (uint32_t)acc[i][rr] + ccorr[i];
+                    const int q0 =
+                        (int)(((int64_t)(int)wu * cm[i] + cc[i]) >> ct[i]);
+                    e[rr] = s_tab1[min(max(q0, h1.x), h1.y) - h1.x];
+                }
+                const uint32_t wy =
+                    quad_transpose(pack_entries(e, 0), sel1, sel2);
+                if (pok) *(uint32_t*)(dst + 16 * i) = wy;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 2: conv 2 over the band's output rows ----
+    load_conv(s_w2, 1);
+    {
+        const int4 h2 = *(const int4*)a2.plan;
+        const int pA = h2.x, pB = h2.y, pSH = h2.z;
+        const int npix = R * OW;
+        const int ntile = (npix + 15) >> 4;
+        const int64_t pimg = ((int64_t)n * OH + oy0) * OW;
+        for (int t = wave; t < ntile; t += CP_NW) {
+            const int pq = 16 * t + 4 * kgl + q;  // pixel this lane stores
+            const bool pok = pq < npix;
+            const int64_t p = pimg + min(pq, npix - 1);
+            uint32_t rw[WM];
+            if (RES) {
+                const int8_t* pr = (const int8_t*)a2.res + p * a2.res_pst;
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+                    rw[i] = *(const uint32_t*)(pr + 16 * i + cq);
+            }
+            const int qp = min(16 * t + col, npix - 1);
+            const int r = cp_div(qp, g.m_w), ox = qp - r * OW;
+            v4i acc[WM];
+            tile_mfma(s_m + (r * g.BW + ox) * g.PS, acc);
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                int e[4];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const uint32_t wu = (uint32_t)acc[i][rr] + ccorr[i];
+                    const int q0 =
+                        (int)(((int64_t)(int)wu * cm[i] + cc[i]) >> ct[i]);
+                    e[rr] = min(max(q0, pA), pB) - pA;
+                }
+                if (RES) {
+                    const uint32_t rv = quad_transpose(rw[i], sel1, sel2);
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const int v = s_tab2[256 + e[rr]] +
+                                      s_tab2[512 + ((rv >> (8 * rr)) & 255)];
+                        e[rr] = min(max(v, 0), pSH);
+                    }
+                }
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) e[rr] = s_tab2[e[rr]];
+                const int c0 = 16 * i + cq;
+                const uint32_t wy =
+                    quad_transpose(pack_entries(e, 0), sel1, sel2);
+                if (pok) *(uint32_t*)((int8_t*)a2.y + p * a2.y_pst + c0) = wy;
+                if (a2.y2) {
+                    const uint32_t w2 =
+                        quad_transpose(pack_entries(e, 1), sel1, sel2);
+                    if (pok)
+                        *(uint32_t*)((int8_t*)a2.y2 + p * a2.y2_pst + c0) = w2;
+                }
+            }
+        }
+    }
+}
+
+uint32_t cp_magic(int64_t d) {
+    return (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) /
+                      (uint64_t)std::max<int64_t>(d, 2));
+}
+
+// Geometry for bands of R output rows; lds = 0 when it does not fit or the
+// staging exceeds what the threads hold.
+PairGeom pair_geom(const ConvArgs& b, int R) {
+    const int C = b.Cg, wm = C / 16;
+    PairGeom g;
+    g.R = R;
+    g.BW = b.W + 2;
+    g.PS = C + ((wm & 1) ? 0 : 16);
+    g.bpi = (b.OH + R - 1) / R;
+    g.nbands = b.N * g.bpi;
+    g.RSW = b.KGp * 16 + 16;
+    const int64_t xb = (int64_t)(R + 4) * g.BW * g.PS;
+    const int64_t mb = (int64_t)(R + 2) * g.BW * g.PS;
+    g.xb_bytes = (int)std::min<int64_t>(xb, 1 << 30);
+    g.mb_bytes = (int)std::min<int64_t>(mb, 1 << 30);
+    const int64_t bytes = xb + mb + 2 * (int64_t)C * g.RSW + b.KGp * 4;
+    const int64_t bchunks = (int64_t)(R + 4) * b.W * wm;
+    const int64_t wchunks = (int64_t)C * b.KGp;
+    g.lds = bytes <= 140 * 1024 && bchunks <= (int64_t)CP_SB * CP_NT &&
+                    wchunks <= (int64_t)CP_SW * CP_NT &&
+                    (int64_t)(R + 4) * g.BW * wm < (1 << 16)
+                ? (int)bytes
+                : 0;
+    g.m_w = cp_magic(b.W);
+    g.m_bw = cp_magic(g.BW);
+    g.m_kgp = cp_magic(b.KGp);
+    return g;
+}
+
+using PairKern = void (*)(ConvArgs, ConvArgs, PairGeom);
+
+PairKern pair_kernel(int wm, bool res) {
+    switch (wm * 2 + (res ? 1 : 0)) {
+        case 2: return &k_conv_pair<1, false>;
+        case 3: return &k_conv_pair<1, true>;
+        case 4: return &k_conv_pair<2, false>;
+        case 5: return &k_conv_pair<2, true>;
+        case 8: return &k_conv_pair<4, false>;
+        case 9: return &k_conv_pair<4, true>;
+        default: return nullptr;
+    }
+}
+
+bool conv_3x3_same(const ConvArgs& b) {
+    return b.G == 1 && b.layout == 0 && b.KH == 3 && b.KW == 3 &&
+           b.SH == 1 && b.SW == 1 && b.PH == 1 && b.PW == 1 && b.DH == 1 &&
+           b.DW == 1 && b.OH == b.H && b.OW == b.W && b.Cg == b.Cout;
+}
+
+}  // namespace
+
+bool conv_pair_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
+                       int epi2) {
+    const int C = b1.Cout;
+    if (!(C == 16 || C == 32 || C == 64)) return false;
+    if (!(epi1 == Q8_TABLE && epi2 == Q8_TABLE && b1.mode == EPI_QUANT &&
+          b2.mode == EPI_QUANT && b1.fastio && b2.fastio && b1.plan &&
+          b2.plan && conv_3x3_same(b1) && conv_3x3_same(b2) &&
+          b2.Cout == C && b1.N == b2.N && b2.H == b1.OH && b2.W == b1.OW &&
+          b1.KGp == 4 * ((9 * C / 16 + 3) / 4) && b2.KGp == b1.KGp &&
+          b1.x_code == 1 && b1.x_sc == 1 && b2.x_code == 1 &&
+          b2.x_sc == 1 && b1.rowsum == 0 && b2.rowsum == 0 &&
+          b1.res == nullptr && b1.y2 == nullptr && b2.x == b1.y &&
+          b2.y_code == 1 && b1.W >= 2 &&
+          (uintptr_t)b1.x % 16 == 0 && b1.x_sp % 16 == 0 &&
+          b1.x_sn % 16 == 0 &&
+          (int64_t)b1.H * b1.W * b1.x_sp < ((int64_t)1 << 31) &&
+          (int64_t)(C + 128) * b1.wp_rstride < ((int64_t)1 << 31) &&
+          (int64_t)(C + 128) * b2.wp_rstride < ((int64_t)1 << 31) &&
+          b2.M < ((int64_t)1 << 31) && b1.N * (int64_t)b1.OH < (1 << 30)))
+        return false;
+    return pair_geom(b1, 1).lds > 0;
+}
+
+bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2,
+                      hipStream_t st) {
+    const int wm = b1.Cout / 16;
+    const PairKern kern = pair_kernel(wm, b2.res != nullptr);
+    if (!kern) {
+        set_error("launch_conv_pair", "unsupported channel count");
+        return false;
+    }
+    // R: the least (rounds of resident work-groups) x (staging, counted as
+    // 4 tile rounds, + tile rounds of both phases)
+    const int cus = cu_count();
+    int bestR = 1;
+    int64_t best = -1;
+    for (int R = 1; R <= b1.OH; ++R) {
+        const PairGeom g = pair_geom(b1, R);
+        if (g.lds == 0) break;
+        int res = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &res, (const void*)kern, CP_NT, (size_t)g.lds) !=
+                hipSuccess ||
+            res <= 0)
+            res = 1;
+        const int64_t rounds = ceil_div(g.nbands, (int64_t)res * cus);
+        const int64_t t1 = ceil_div(ceil_div((int64_t)(R + 2) * b1.OW, 16),
+                                    CP_NW);
+        const int64_t t2 = ceil_div(ceil_div((int64_t)R * b1.OW, 16), CP_NW);
+        const int64_t cost = rounds * (4 + t1 + t2);
+        if (best < 0 || cost < best) {
+            best = cost;
+            bestR = R;
+        }
+    }
+    const PairGeom g = pair_geom(b1, bestR);
+    if (g.lds == 0 || g.nbands >= ((int64_t)1 << 31)) {
+        set_error("launch_conv_pair", "band does not fit");
+        return false;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)g.nbands), dim3(CP_NT),
+                       (size_t)g.lds, st, b1, b2, g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_hip_error("launch_conv_pair", e);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace qa
