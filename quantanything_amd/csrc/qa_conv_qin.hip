@@ -35,32 +35,37 @@ struct QinGeom {
 };
 
 // Quantized word of one pixel: channel c in byte c (storage offset so
-// subtracted), bytes above CIN zero, exactly qa_quantize_one per value.
+// subtracted), bytes above CIN zero. The float32 form; *slow is set when a
+// value is near a rounding tie, NaN, or the scales are outside that form
+// (f32 false), and then the word must be recomputed by pixel_word_exact.
 template <int CIN>
-__device__ __forceinline__ uint32_t pixel_word(const float (&f)[CIN],
-                                               const QinArgs& q, float invf,
-                                               bool f32) {
+__device__ __forceinline__ uint32_t pixel_word_f32(const float (&f)[CIN],
+                                                   const QinArgs& q,
+                                                   float invf, bool f32,
+                                                   bool* slow) {
     uint32_t w = 0;
-    bool slow = !f32;
-    if (f32) {  // clip(r + zp) - so == clip(r + zp - so) with shifted bounds
-        const int so = (int)q.so;
+    *slow |= !f32;
+    const int so = (int)q.so;
 #pragma unroll
-        for (int c = 0; c < CIN; ++c)
-            w |= (uint32_t)(uint8_t)qa_quantize_f32(
-                     f[c], invf, (int)q.zp - so, (int)q.qmin - so,
-                     (int)q.qmax - so, &slow)
-                 << (8 * c);
-    }
-    if (slow) {  // near a rounding tie, NaN, or scales outside the f32 form
-        w = 0;
-#pragma unroll
-        for (int c = 0; c < CIN; ++c)
-            w |= (uint32_t)(uint8_t)(qa_quantize_one_fast(f[c], q.scale, q.inv,
-                                                          q.zp, q.qmin,
-                                                          q.qmax) -
-                                     q.so)
-                 << (8 * c);
-    }
+    for (int c = 0; c < CIN; ++c)
+        w |= (uint32_t)(uint8_t)qa_quantize_f32(f[c], invf, (int)q.zp - so,
+                                                (int)q.qmin - so,
+                                                (int)q.qmax - so, slow)
+             << (8 * c);
+    return w;
+}
+
+// The same word exactly as qa_quantize_one per value (double division).
+template <int CIN>
+__device__ __forceinline__ uint32_t pixel_word_exact(const float* src, int HW,
+                                                  const QinArgs& q) {
+    uint32_t w = 0;
+    for (int c = 0; c < CIN; ++c)
+        w |= (uint32_t)(uint8_t)(qa_quantize_one_fast(src[(int64_t)c * HW],
+                                                      q.scale, q.inv, q.zp,
+                                                      q.qmin, q.qmax) -
+                                 q.so)
+             << (8 * c);
     return w;
 }
 
@@ -125,6 +130,7 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
                 }
             }
         }
+        uint32_t slowbits = 0;  // bit k * PX + p: recompute exactly
 #pragma unroll
         for (int k = 0; k < QIN_U; ++k) {
             if (dsto[k] < 0) continue;
@@ -134,8 +140,10 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
                 float f[CIN];
 #pragma unroll
                 for (int c = 0; c < CIN; ++c) f[c] = v[k][c][p];
-                w[p] = pixel_word<CIN>(f, q, invf, f32);
+                bool slow = false;
+                w[p] = pixel_word_f32<CIN>(f, q, invf, f32, &slow);
                 if (!in[k]) w[p] = (uint32_t)pv;
+                if (slow && in[k]) slowbits |= 1u << (k * PX + p);
             }
             int* dst = s_raw + dsto[k];
             if (VEC)
@@ -144,6 +152,18 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
                                           w[PX > 3 ? 3 : 0]);
             else
                 *dst = (int)w[0];
+        }
+        // rare: values near a rounding tie (or scales outside the float32
+        // form) take the exact double-division path, one pixel at a time
+        while (slowbits) {
+            const int b = __builtin_ctz(slowbits);
+            slowbits &= slowbits - 1;
+            const int k = b / PX, p = b - k * PX;
+            const int i = i0 + k * QIN_THREADS;
+            const int r = div_magic(i, g.mg_gw), u = i - r * GW;
+            const float* src = xn + (iy_base + r) * a.W + PX * u + p;
+            s_raw[r * g.RW + g.c0 + PX * u + p] =
+                (int)pixel_word_exact<CIN>(src, HW, q);
         }
     }
     {  // pad columns: c0 - PW .. c0 - 1 and c0 + W .. RW - 1
