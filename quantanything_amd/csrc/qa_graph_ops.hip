@@ -321,6 +321,73 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(
     }
 }
 
+// int8 Softmax rows through a table of exponentials: t[256 m + s] =
+// exp(F(s) - F(m)) in float64 for stored bytes s <= m (index byte + 128),
+// F(b) = float32((b + in_so - in_zp) * in_scale), the values k_softmax_rows
+// exponentiates (F is non-decreasing, so a row's maximum is F of its
+// largest byte). Built once per layer.
+__global__ __launch_bounds__(kThreads) void k_softmax_table(
+    double in_scale, int64_t in_zp, int64_t in_so, double* __restrict__ t) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= 65536) return;
+    const int m = i >> 8, s = i & 255;
+    const float fs = (float)((double)((int64_t)(s - 128) + in_so - in_zp) *
+                             in_scale);
+    const float fm = (float)((double)((int64_t)(m - 128) + in_so - in_zp) *
+                             in_scale);
+    t[i] = s <= m ? exp((double)fs - (double)fm) : 0.0;
+}
+
+// k_softmax_rows for int8 input and output with the exponentials read from
+// k_softmax_table: the same float64 values, summed in the same order, so
+// the results are those of k_softmax_rows.
+template <int GS, int PER>
+__global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
+    const int8_t* __restrict__ x, int64_t rows, int64_t cols,
+    const double* __restrict__ t, int8_t* __restrict__ out, double out_scale,
+    int64_t out_zp, int64_t qmin, int64_t qmax, int64_t out_so) {
+    constexpr int RPW = 64 / GS;  // rows per wave
+    const int lane = threadIdx.x & 63;
+    const int gl = lane % GS;
+    const double inv = 1.0 / out_scale;
+    const int64_t first = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW +
+                          lane / GS;
+    for (int64_t r = first; r - lane / GS < rows;
+         r += (int64_t)gridDim.x * 4 * RPW) {
+        const bool live = r < rows;
+        const int64_t base = (live ? r : 0) * cols;
+        int sv[PER];
+        int mx = 0;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int64_t i = gl + GS * k;
+            sv[k] = live && i < cols ? (int)x[base + i] + 128 : -1;
+            mx = max(mx, sv[k]);
+        }
+#pragma unroll
+        for (int o = GS / 2; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
+        const double* tr = t + 256 * mx;
+        double e[PER], sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            e[k] = sv[k] >= 0 ? tr[sv[k]] : 0.0;
+            sum += e[k];
+        }
+#pragma unroll
+        for (int o = GS / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (!live) continue;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int64_t i = gl + GS * k;
+            if (i >= cols) continue;
+            const float y = (float)(e[k] / sum);
+            const int64_t q =
+                qa_quantize_one_fast(y, out_scale, inv, out_zp, qmin, qmax);
+            out[base + i] = (int8_t)(q - out_so);
+        }
+    }
+}
+
 bool softmax_launch(const void* x, int in_code, int64_t rows, int64_t cols,
                     double in_scale, int64_t in_zp, int64_t in_so, void* out,
                     int out_code, double out_scale, int64_t out_zp,
@@ -460,6 +527,46 @@ QA_API int qa_d_softmax(const void* x, int in_code, int64_t rows, int64_t cols,
                    out_code, out_scale, out_zp, qmin, qmax, out_so, nullptr,
                    (hipStream_t)stream);
     return launched("qa_d_softmax") ? 0 : -1;
+}
+
+// Table of exponentials for qa_d_softmax_lut (65536 doubles).
+QA_API int qa_d_softmax_table(double in_scale, int64_t in_zp, int64_t in_so,
+                              double* table, void* stream) {
+    if (!table || !(in_scale > 0.0)) {
+        qa::set_error("qa_d_softmax_table", "needs a table and a positive scale");
+        return -1;
+    }
+    k_softmax_table<<<65536 / kThreads, kThreads, 0, (hipStream_t)stream>>>(
+        in_scale, in_zp, in_so, table);
+    return launched("qa_d_softmax_table") ? 0 : -1;
+}
+
+// qa_d_softmax for int8 input and output reading the exponentials from a
+// qa_d_softmax_table table of the same input quantization.
+QA_API int qa_d_softmax_lut(const void* x, int64_t rows, int64_t cols,
+                            const double* table, void* out, double out_scale,
+                            int64_t out_zp, int64_t qmin, int64_t qmax,
+                            int64_t out_so, void* stream) {
+    if (rows <= 0 || cols <= 0) return 0;
+    if (!table || cols > 64 * SOFTMAX_PER) {
+        qa::set_error("qa_d_softmax_lut", "needs a table and at most 512 "
+                                          "columns");
+        return -1;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    if (cols <= 16 * 16) {
+        const int64_t blocks = std::min<int64_t>((rows + 15) / 16, 65535);
+        k_softmax_rows_lut<16, 16><<<(unsigned)blocks, kThreads, 0, st>>>(
+            (const int8_t*)x, rows, cols, table, (int8_t*)out, out_scale,
+            out_zp, qmin, qmax, out_so);
+    } else {
+        const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
+        k_softmax_rows_lut<64, SOFTMAX_PER><<<(unsigned)blocks, kThreads, 0,
+                                              st>>>(
+            (const int8_t*)x, rows, cols, table, (int8_t*)out, out_scale,
+            out_zp, qmin, qmax, out_so);
+    }
+    return launched("qa_d_softmax_lut") ? 0 : -1;
 }
 
 // qa_d_softmax that also writes the dequantized output (float32, same

@@ -1131,8 +1131,22 @@ class DeviceExecutor:
                     y.code, o.scale, o.zp, o.qmin, o.qmax, y.so)
             lname = f"softmax:{layer.name}"
             self.softmax_of[layer.node.outputs[0]] = (lname, args)
-            self._add(lname, lambda s: _ok(self.lib.qa_d_softmax(*args, s),
-                                           "qa_d_softmax"))
+            if x.code == 1 and y.code == 1 and cols <= 512:
+                # int8: exponentials from a table built once per layer
+                tab = torch.empty(65536, dtype=torch.float64, device="cuda")
+                _ok(self.lib.qa_d_softmax_table(
+                    iq.scale, iq.zp, x.so, tab.data_ptr(),
+                    torch.cuda.current_stream().cuda_stream),
+                    "qa_d_softmax_table")
+                torch.cuda.synchronize()
+                self.keep.append(tab)
+                largs = (x.ptr, rows, cols, tab.data_ptr(), y.ptr, o.scale,
+                         o.zp, o.qmin, o.qmax, y.so)
+                self._add(lname, lambda s: _ok(
+                    self.lib.qa_d_softmax_lut(*largs, s), "qa_d_softmax_lut"))
+            else:
+                self._add(lname, lambda s: _ok(
+                    self.lib.qa_d_softmax(*args, s), "qa_d_softmax"))
             return [y]
         if op == "LayerNormalization":
             return self._plan_layernorm(layer, x)

@@ -181,3 +181,34 @@ def test_large_gemm_kernel_bit_exact(hip, tmp_path, quant_type, m, k, n, act,
                 np.testing.assert_array_equal(
                     got, o.env[name].reshape(got.shape),
                     err_msg=f"{name}, tiles {[hex(t[1].tile) for t in descs]}")
+
+
+@pytest.mark.parametrize("rows,cols", [(37, 17), (64, 197), (9, 256),
+                                       (12, 300), (5, 512)])
+def test_softmax_table_equals_direct(hip, rows, cols):
+    """The int8 Softmax through the table of exponentials stores exactly
+    what the per-element float64 form stores (same exponentials, same
+    summation order), rows of mixed byte ranges included."""
+    import torch
+    lib = hip.require()
+    rng = np.random.default_rng(rows * 1000 + cols)
+    x = rng.integers(-128, 128, size=(rows, cols), dtype=np.int64)
+    x[0, :] = 17                      # a constant row
+    x[1 % rows, :] = rng.integers(-128, -120, size=cols)  # low bytes only
+    xd = torch.from_numpy(x.astype(np.int8)).cuda()
+    in_scale, in_zp, in_so = 0.0713, 3, 0
+    o_scale, o_zp, o_so = 1.0 / 255, -128, 0
+    ya = torch.empty_like(xd)
+    yb = torch.empty_like(xd)
+    tab = torch.empty(65536, dtype=torch.float64, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.qa_d_softmax_table(in_scale, in_zp, in_so, tab.data_ptr(),
+                                  s) == 0
+    assert lib.qa_d_softmax(xd.data_ptr(), 1, rows, cols, in_scale, in_zp,
+                            in_so, ya.data_ptr(), 1, o_scale, o_zp, -128, 127,
+                            o_so, s) == 0
+    assert lib.qa_d_softmax_lut(xd.data_ptr(), rows, cols, tab.data_ptr(),
+                                yb.data_ptr(), o_scale, o_zp, -128, 127,
+                                o_so, s) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(yb.cpu().numpy(), ya.cpu().numpy())
