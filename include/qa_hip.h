@@ -335,6 +335,22 @@ int qa_conv_pair_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
 int qa_d_conv_pair(const qa_conv_desc* d1, const qa_conv_desc* d2,
                    void* stream);
 
+/* A convolution followed by a 1x1 convolution in one launch (the stride-2
+ * conv feeding a C2f block's first 1x1 conv): d1 an int8 convolution of
+ * C = 16, 32 or 64 output channels (packed layout 0, one group, a table
+ * plan, no residual or rescaled copy, up to 9 K-steps of 64 bytes), d2 an
+ * int8 1x1 stride-1 convolution C -> C with a table plan and no residual
+ * (a rescaled copy d2->y2 is allowed), reading d1's output (d2->x ==
+ * d1->y). The result is what qa_d_conv(d1) then qa_d_conv(d2) store at
+ * d2->y (and d2->y2); d1->y is not
+ * written. Returns -1, launching nothing, for any other pair; the
+ * reference runs the two convolutions one after the other
+ * (quant_layers.py:320-335 twice). qa_conv_chain_supported checks a pair
+ * without launching (1 or 0). */
+int qa_conv_chain_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
+int qa_d_conv_chain(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                    void* stream);
+
 /* Graph-input quantization fused into the first convolution: x is the
  * float32 NCHW input [N, C, H, W]; it is quantized exactly as
  * qa_d_quantize_nhwc would (scale, zp, clip; storage offset

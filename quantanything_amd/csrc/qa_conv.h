@@ -193,6 +193,12 @@ int fast_io_args(const ConvArgs& a, ConvArgs& b, int epi);
 bool conv_pair_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
                        int epi2);
 bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2, hipStream_t st);
+// A convolution (weights-in-registers kernel, Cout 16, 32 or 64) whose
+// output feeds only a 1x1 convolution of the same width: both in one
+// launch, the intermediate kept per wave in LDS (qa_conv_wr.hip).
+bool conv_chain_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
+                        int epi2);
+bool launch_conv_chain(const ConvArgs& b1, const ConvArgs& b2, hipStream_t st);
 // 16-bit operands on the FP64 matrix cores (qa_conv_f64.hip), exact.
 bool launch_conv_f64(const ConvArgs& a, hipStream_t st);
 

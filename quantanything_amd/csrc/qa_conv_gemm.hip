@@ -739,6 +739,36 @@ QA_API int qa_d_conv_pair(const qa_conv_desc* d1, const qa_conv_desc* d2,
     return launch_conv_pair(b1, b2, (hipStream_t)stream_) ? 0 : -1;
 }
 
+static bool chain_args(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                       ConvArgs& b1, ConvArgs& b2, const char* who) {
+    ConvArgs a1, a2;
+    if (desc_args(d1, a1, who) != 1 || desc_args(d2, a2, who) != 1)
+        return false;
+    const int e1 = fast_io_args(a1, b1, -1);  // Q8_TABLE or -1
+    const int e2 = fast_io_args(a2, b2, -1);
+    return conv_chain_applies(b1, e1, b2, e2);
+}
+
+QA_API int qa_conv_chain_supported(const qa_conv_desc* d1,
+                                   const qa_conv_desc* d2) {
+    ConvArgs b1, b2;
+    return chain_args(d1, d2, b1, b2, "qa_conv_chain_supported") ? 1 : 0;
+}
+
+QA_API int qa_d_conv_chain(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                           void* stream_) {
+    ConvArgs b1, b2;
+    if (!chain_args(d1, d2, b1, b2, "qa_d_conv_chain")) {
+        set_error("qa_d_conv_chain",
+                  "needs an int8 convolution of 16, 32 or 64 output channels "
+                  "(weights-in-registers form, no residual) and a 1x1 "
+                  "convolution of the same width reading its output, both "
+                  "with table plans");
+        return -1;
+    }
+    return launch_conv_chain(b1, b2, (hipStream_t)stream_) ? 0 : -1;
+}
+
 QA_API int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
                           void* stream_) {
     hipStream_t st = (hipStream_t)stream_;

@@ -69,15 +69,29 @@ __device__ __forceinline__ int wr_div(int n, uint32_t m) {
 // RES: a residual Add is fused (its words are fetched one tile ahead; the
 // variant without it has no loads in the tile loop, so no wait there on
 // the counter that the output stores share).
-template <int WM, int KS, bool RES>
-__global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
+// CH: a 1x1 convolution a2 (WM*16 -> WM*16 channels, stride 1, no
+// residual; its rescaled copy y2 allowed) consumes the output, which then
+// never leaves the work-group:
+// each tile's stored bytes go to a per-wave LDS tile (16 pixels x 80
+// bytes), are read back as the 1x1 conv's activation fragment (one K-step)
+// and a2's table epilogue stores a2's output (a covers every channel:
+// blockIdx.y == 0).
+template <int WM, int KS, bool RES, bool CH>
+__global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
+                                                   ConvArgs a2) {
     extern __shared__ int4 lds4[];
     int8_t* s_band = (int8_t*)lds4;                          // band
     int8_t* s_w = s_band + bg.band_bytes;                    // weights
     int* s_kt = (int*)(s_w + WM * 16 * bg.RSW);              // k-groups
+    // CH: a2's weights (WM*16 rows of 64 + 16 bytes), the wave tiles
+    int8_t* s_w2 = (int8_t*)(s_kt + 4 * KS);
+    int8_t* s_t = s_w2 + (CH ? WM * 16 * 80 : 0);
     __shared__ int s_tab[768];
     __shared__ int4 s_pc[WM * 16];
     __shared__ uint32_t s_corr[WM * 16];
+    __shared__ int s_tab2[CH ? 256 : 1];
+    __shared__ int4 s_pc2[CH ? WM * 16 : 1];
+    __shared__ uint32_t s_corr2[CH ? WM * 16 : 1];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kgl = lane >> 4;
@@ -164,6 +178,20 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
             s_pc[tid] = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
             s_corr[tid] = a.corr ? (uint32_t)a.corr[c] : 0u;
         }
+        if (CH) {
+            // a2's weight rows: 4 chunks each (K = one 64-byte step)
+            for (int e = tid; e < WM * 16 * 4; e += WR_NT) {
+                const int r = e >> 2, k = e & 3;
+                *(v4i*)(s_w2 + r * 80 + k * 16) =
+                    *(const v4i*)(a2.wp + (int64_t)r * a2.wp_rstride + k * 16);
+            }
+            for (int i = tid; i < 256; i += WR_NT)
+                s_tab2[i] = ((const int*)((const char*)a2.plan + PLAN_E))[i];
+            if (tid < WM * 16) {
+                s_pc2[tid] = ((const int4*)((const char*)a2.plan + PLAN_CH))[tid];
+                s_corr2[tid] = a2.corr ? (uint32_t)a2.corr[tid] : 0u;
+            }
+        }
 #pragma unroll
         for (int u = 0; u < WR_SB; ++u)
             if (ax[u] >= 0) *(v4i*)(s_band + ax[u]) = vx[u];
@@ -200,6 +228,26 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
     }
     const int4 hdr = *(const int4*)a.plan;
     const int pA = hdr.x, pB = hdr.y, pSH = hdr.z;
+    // CH: a2's weight fragments (one K-step) and per-channel constants
+    v4i wb2[CH ? WM : 1];
+    int cm2[CH ? WM : 1], ct2[CH ? WM : 1];
+    int64_t cc2[CH ? WM : 1];
+    uint32_t ccorr2[CH ? WM : 1];
+    int4 hdr2 = int4{0, 0, 0, 0};
+    if (CH) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            wb2[i] = *(const v4i*)(s_w2 + (16 * i + col) * 80 + 16 * kgl);
+            const int4 pc = s_pc2[16 * i + col];
+            cm2[i] = pc.x;
+            ct2[i] = pc.y;
+            cc2[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                               (uint32_t)pc.z);
+            ccorr2[i] = s_corr2[16 * i + col];
+        }
+        hdr2 = *(const int4*)a2.plan;
+    }
+    int8_t* s_tw = s_t + wave * (16 * 80);  // this wave's tile (CH)
     const int q = lane & 3;
     const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
     const uint32_t sel2 = (q & 1) ? 0x03070105u : 0x06020400u;
@@ -275,6 +323,10 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
                 const int c0 = co0 + 16 * i + cq;  // Cout % 4 == 0
                 const bool sok = pok && c0 < a.Cout;
                 const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
+                if (CH) {  // pixel 4 kgl + q of the tile, channels c0 ..
+                    *(uint32_t*)(s_tw + (4 * kgl + q) * 80 + c0) = wy;
+                    continue;
+                }
                 if (sok) *(uint32_t*)((int8_t*)a.y + p * a.y_pst + c0) = wy;
                 if (a.y2) {
                     const uint32_t w2 =
@@ -283,13 +335,52 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg) {
                         *(uint32_t*)((int8_t*)a.y2 + p * a.y2_pst + c0) = w2;
                 }
             }
+            if (CH) {
+                // the wave's own LDS writes above, read back by other lanes
+                // of the same wave (LDS instructions of a wave complete in
+                // order; the wait also keeps the compiler from moving them)
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                __builtin_amdgcn_wave_barrier();
+                // 1x1 conv: pixel col of the tile, channels 16 kgl .. (the
+                // k-groups past WM*16 channels have zero weights)
+                const v4i fa2 = *(const v4i*)(s_tw + col * 80 + 16 * kgl);
+                v4i acc2[WM];
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+                    acc2[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        fa2, wb2[i], v4i{0, 0, 0, 0}, 0, 0, 0);
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int i = 0; i < WM; ++i) {
+                    int e[4];
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const uint32_t wu = (uint32_t)acc2[i][rr] + ccorr2[i];
+                        const int q0 = (int)(((int64_t)(int)wu * cm2[i] +
+                                              cc2[i]) >> ct2[i]);
+                        e[rr] = s_tab2[min(max(q0, hdr2.x), hdr2.y) - hdr2.x];
+                    }
+                    const int c0 = 16 * i + cq;
+                    const uint32_t wy =
+                        quad_transpose(pack_entries(e, 0), sel1, sel2);
+                    if (pok)
+                        *(uint32_t*)((int8_t*)a2.y + p * a2.y_pst + c0) = wy;
+                    if (a2.y2) {  // a2's rescaled copy (a Concat input)
+                        const uint32_t w2 =
+                            quad_transpose(pack_entries(e, 1), sel1, sel2);
+                        if (pok)
+                            *(uint32_t*)((int8_t*)a2.y2 + p * a2.y2_pst +
+                                         c0) = w2;
+                    }
+                }
+            }
         }
     }
 }
 
 // Geometry for bands of R output rows; lds = 0 when it does not fit in LDS
 // or the band and weight chunks exceed what the threads stage.
-WrGeom wr_geom(const ConvArgs& b, int wm, int R) {
+WrGeom wr_geom(const ConvArgs& b, int wm, int R, bool ch = false) {
     WrGeom g;
     g.R = R;
     g.BR = (R - 1) * b.SH + (b.KH - 1) * b.DH + 1;
@@ -312,7 +403,8 @@ WrGeom wr_geom(const ConvArgs& b, int wm, int R) {
     g.m_w = magic(b.W);
     g.KSR = wr_steps(wm, b.KGp / 4);
     const int64_t bytes =
-        band + (int64_t)wm * 16 * g.RSW + (int64_t)g.KSR * 16;
+        band + (int64_t)wm * 16 * g.RSW + (int64_t)g.KSR * 16 +
+        (ch ? (int64_t)wm * 16 * 80 + WR_NW * 16 * 80 : 0);
     // gfx950 gives a work-group up to 160 KB of LDS
     g.lds = bytes <= 150 * 1024 && bchunks <= (int64_t)WR_SB * WR_NT &&
                     wchunks <= (int64_t)WR_SW * WR_NT &&
@@ -322,36 +414,43 @@ WrGeom wr_geom(const ConvArgs& b, int wm, int R) {
     return g;
 }
 
-using WrKern = void (*)(ConvArgs, WrGeom);
+using WrKern = void (*)(ConvArgs, WrGeom, ConvArgs);
 
-template <int WM, bool RES>
+template <int WM, bool RES, bool CH>
 WrKern wr_kernel(int ks) {
     switch (ks) {
-        case 1: return &k_conv_wr<WM, 1, RES>;
-        case 2: return &k_conv_wr<WM, 2, RES>;
-        case 3: return &k_conv_wr<WM, 3, RES>;
-        case 5: return &k_conv_wr<WM, 5, RES>;
-        case 9: return &k_conv_wr<WM, 9, RES>;
+        case 1: return &k_conv_wr<WM, 1, RES, CH>;
+        case 2: return &k_conv_wr<WM, 2, RES, CH>;
+        case 3: return &k_conv_wr<WM, 3, RES, CH>;
+        case 5: return &k_conv_wr<WM, 5, RES, CH>;
+        case 9: return &k_conv_wr<WM, 9, RES, CH>;
         case 18:
-            if constexpr (WM <= 2) return &k_conv_wr<WM, 18, RES>;
+            if constexpr (WM <= 2 && !CH) return &k_conv_wr<WM, 18, RES, CH>;
             break;
         case 36:
-            if constexpr (WM == 1) return &k_conv_wr<WM, 36, RES>;
+            if constexpr (WM == 1 && !CH) return &k_conv_wr<WM, 36, RES, CH>;
             break;
         default: break;
     }
     return nullptr;
 }
 
-WrKern wr_kernel_rt(int wm, int ks, bool res) {
-    if (res)
-        return wm == 1 ? wr_kernel<1, true>(ks)
-               : wm == 2 ? wr_kernel<2, true>(ks)
-               : wm == 4 ? wr_kernel<4, true>(ks)
+// ch: with a chained 1x1 convolution (no residual variant)
+WrKern wr_kernel_rt(int wm, int ks, bool res, bool ch = false) {
+    if (ch)
+        return res ? nullptr
+               : wm == 1 ? wr_kernel<1, false, true>(ks)
+               : wm == 2 ? wr_kernel<2, false, true>(ks)
+               : wm == 4 ? wr_kernel<4, false, true>(ks)
                          : nullptr;
-    return wm == 1 ? wr_kernel<1, false>(ks)
-           : wm == 2 ? wr_kernel<2, false>(ks)
-           : wm == 4 ? wr_kernel<4, false>(ks)
+    if (res)
+        return wm == 1 ? wr_kernel<1, true, false>(ks)
+               : wm == 2 ? wr_kernel<2, true, false>(ks)
+               : wm == 4 ? wr_kernel<4, true, false>(ks)
+                         : nullptr;
+    return wm == 1 ? wr_kernel<1, false, false>(ks)
+           : wm == 2 ? wr_kernel<2, false, false>(ks)
+           : wm == 4 ? wr_kernel<4, false, false>(ks)
                      : nullptr;
 }
 
@@ -390,22 +489,25 @@ bool conv_wr_applies(const ConvArgs& b, int epi, int wm) {
     return wr_geom(b, wm, 1).lds > 0;
 }
 
-bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st) {
-    if (!conv_wr_applies(b, Q8_TABLE, wm)) {
-        set_error("launch_conv_wr", "convolution outside the kernel's scope");
-        return false;
-    }
+namespace {
+
+// Shared launcher: b alone (ch false, b2 unused) or b with the chained 1x1
+// convolution b2.
+bool wr_launch(const ConvArgs& b, int wm, bool ch, const ConvArgs& b2,
+               hipStream_t st) {
     // R: the least (rounds of resident work-groups) x (staging, counted as
     // 4 tiles, + tiles per wave)
     const int cus = cu_count();
     const int64_t cblocks = ceil_div(b.Cout, 16 * wm);
+    const bool res = b.res != nullptr;
     int bestR = 1;
     int64_t best = -1;
     for (int R = 1; R <= b.OH; ++R) {
-        const WrGeom g = wr_geom(b, wm, R);
+        const WrGeom g = wr_geom(b, wm, R, ch);
         if (g.lds == 0) break;
-        const int res = wr_resident(wr_kernel_rt(wm, g.KSR, b.res != nullptr), g.lds);
-        const int64_t rounds = ceil_div(g.nbands * cblocks, (int64_t)res * cus);
+        const int nres = wr_resident(wr_kernel_rt(wm, g.KSR, res, ch), g.lds);
+        const int64_t rounds =
+            ceil_div(g.nbands * cblocks, (int64_t)nres * cus);
         const int64_t cost =
             rounds * (4 + ceil_div(ceil_div((int64_t)R * b.OW, 16), WR_NW));
         if (best < 0 || cost < best) {
@@ -413,25 +515,60 @@ bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st) {
             bestR = R;
         }
     }
-    const WrGeom g = wr_geom(b, wm, bestR);
+    const WrGeom g = wr_geom(b, wm, bestR, ch);
     const int64_t gx = g.nbands;
-    if (cblocks > 65535 || gx >= ((int64_t)1 << 31)) {
-        set_error("launch_conv_wr", "grid too large");
+    if (g.lds == 0 || cblocks > 65535 || gx >= ((int64_t)1 << 31)) {
+        set_error("launch_conv_wr", "band or grid does not fit");
         return false;
     }
     const dim3 grid((unsigned)gx, (unsigned)cblocks);
-    const WrKern kern = wr_kernel_rt(wm, g.KSR, b.res != nullptr);
+    const WrKern kern = wr_kernel_rt(wm, g.KSR, res, ch);
     if (!kern) {
         set_error("launch_conv_wr", "no kernel for the K-steps");
         return false;
     }
-    hipLaunchKernelGGL(kern, grid, dim3(WR_NT), (size_t)g.lds, st, b, g);
+    hipLaunchKernelGGL(kern, grid, dim3(WR_NT), (size_t)g.lds, st, b, g, b2);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("launch_conv_wr", e);
         return false;
     }
     return true;
+}
+
+}  // namespace
+
+bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st) {
+    if (!conv_wr_applies(b, Q8_TABLE, wm)) {
+        set_error("launch_conv_wr", "convolution outside the kernel's scope");
+        return false;
+    }
+    return wr_launch(b, wm, false, b, st);
+}
+
+bool conv_chain_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
+                        int epi2) {
+    const int wm = b1.Cout / 16;
+    if (!((wm == 1 || wm == 2 || wm == 4) && b1.Cout == 16 * wm &&
+          conv_wr_applies(b1, epi1, wm) && b1.res == nullptr &&
+          b1.y2 == nullptr && wr_steps(wm, b1.KGp / 4) <= 9))
+        return false;
+    return epi2 == Q8_TABLE && b2.mode == EPI_QUANT && b2.fastio && b2.plan &&
+           b2.G == 1 && b2.layout == 0 && b2.KH == 1 && b2.KW == 1 &&
+           b2.SH == 1 && b2.SW == 1 && b2.PH == 0 && b2.PW == 0 &&
+           b2.Cg == b1.Cout && b2.Cout == b1.Cout && b2.KGp == 4 &&
+           b2.x == b1.y && b2.N == b1.N && b2.H == b1.OH && b2.W == b1.OW &&
+           b2.OH == b2.H && b2.OW == b2.W && b2.res == nullptr &&
+           (b2.y2 == nullptr ||
+            ((uintptr_t)b2.y2 % 4 == 0 && b2.y2_pst % 4 == 0)) &&
+           b2.rowsum == 0 && b2.y_code == 1 &&
+           (uintptr_t)b2.y % 4 == 0 && b2.y_pst % 4 == 0 &&
+           wr_geom(b1, wm, 1, true).lds > 0;
+}
+
+bool launch_conv_chain(const ConvArgs& b1, const ConvArgs& b2,
+                       hipStream_t st) {
+    return wr_launch(b1, b1.Cout / 16, true, b2, st);
 }
 
 }  // namespace qa

@@ -503,6 +503,7 @@ class DeviceExecutor:
         self._fuse_input_quantization(cons)
         self._fuse_pools(cons)
         self._fuse_pairs(cons)
+        self._fuse_chains(cons)
         for d, _, _, name in self.mfma_descs + self.f64_descs:
             if name in dict(self.launches):
                 self.tunables.append(
@@ -827,6 +828,39 @@ class DeviceExecutor:
                 _ok(self.lib.qa_d_conv_pair(ctypes.byref(d1),
                                             ctypes.byref(d2), s),
                     "qa_d_conv_pair")
+
+            self.launches = [(fused, fn) if n == ln2 else (n, f)
+                             for n, f in self.launches if n != ln1]
+            self.tunables.append((fused, d2, [0], fn))
+            self.tensors.pop(mids[0], None)  # never materialized
+
+    def _fuse_chains(self, cons):
+        """An int8 convolution of 16, 32 or 64 output channels whose output
+        only feeds a 1x1 convolution of the same width runs with it as one
+        launch (``qa_d_conv_chain``): the intermediate never leaves the
+        work-group."""
+        for d2, _, _, ln2 in self.mfma_descs:
+            live = dict(self.launches)
+            if ln2 not in live or d2.KH != 1 or d2.KW != 1:
+                continue
+            firsts = [(d, ln) for d, _, _, ln in self.mfma_descs
+                      if d.y == d2.x and ln in live and ln != ln2]
+            if len(firsts) != 1:
+                continue
+            d1, ln1 = firsts[0]
+            mids = [n for n, t in self.tensors.items() if t.ptr == d1.y]
+            if len(mids) != 1 or mids[0] in self.graph.outputs or \
+                    [l.name for l in cons.get(mids[0], [])] != [ln2[5:]]:
+                continue
+            if not self.lib.qa_conv_chain_supported(ctypes.byref(d1),
+                                                    ctypes.byref(d2)):
+                continue
+            fused = f"chain:{ln1[5:]}+{ln2[5:]}"
+
+            def fn(s, d1=d1, d2=d2):
+                _ok(self.lib.qa_d_conv_chain(ctypes.byref(d1),
+                                             ctypes.byref(d2), s),
+                    "qa_d_conv_chain")
 
             self.launches = [(fused, fn) if n == ln2 else (n, f)
                              for n, f in self.launches if n != ln1]

@@ -69,6 +69,8 @@ def _declare(lib):
         "qa_d_conv_pool": (i32, [p, p, p]),
         "qa_conv_pair_supported": (i32, [p, p]),
         "qa_d_conv_pair": (i32, [p, p, p]),
+        "qa_conv_chain_supported": (i32, [p, p]),
+        "qa_d_conv_chain": (i32, [p, p, p]),
         "qa_d_copy_nd": (i32, [p, p]),
         "qa_d_layernorm": (i32, [p, i32, i64, i64, i64, f64, i64, i64, p, p,
                                  f64, p, i32, i64, f64, i64, i64, i64, i64,

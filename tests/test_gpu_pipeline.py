@@ -93,7 +93,7 @@ def test_every_conv_tile_is_bit_exact(hip, tmp_path, model, quant_type):
         "pool not fused into the last convolution"
     descs = [t[1] for t in ex.tunables]
     # a fused pair of convolutions is one tunable launch
-    pairs = sum(n.startswith("pair:") for n, _ in ex.launches)
+    pairs = sum(n.startswith(("pair:", "chain:")) for n, _ in ex.launches)
     assert len(descs) == len(ex.mfma_descs) - pairs
     cands = [t[2] for t in ex.tunables]
     for r in range(max(len(cc) for cc in cands)):
@@ -412,6 +412,49 @@ def test_fused_conv_pair(hip, tmp_path, c, size, batch, residual):
     oracle.run(x, keep=True)
     ex = cq.executor({"images": x.shape})
     assert [n for n, _ in ex.launches if n.startswith("pair:")], \
+        [n for n, _ in ex.launches]
+    ex.run({"images": x})
+    checked = 0
+    for name, tt in ex.tensors.items():
+        if name in oracle.env:
+            got = tt.to_host()
+            np.testing.assert_array_equal(
+                got, oracle.env[name].reshape(got.shape), err_msg=name)
+            checked += 1
+    assert checked >= 2
+
+
+@pytest.mark.parametrize("cin,c,k,stride,size,batch", [
+    (16, 32, 3, 2, 29, 2),   # a stride-2 conv feeding a C2f's 1x1
+    (32, 64, 3, 2, 15, 3),
+    (16, 16, 3, 1, 20, 2),
+    (64, 64, 1, 1, 9, 3),    # 1x1 then 1x1
+])
+def test_fused_conv_chain(hip, tmp_path, cin, c, k, stride, size, batch):
+    """A convolution whose output only feeds a 1x1 convolution of the same
+    width runs with it as one launch (the intermediate kept in LDS) and the
+    result equals the oracle bit for bit; the intermediate tensor is never
+    materialized."""
+    b = G.GraphBuilder(29)
+    t = b.silu(b.conv("images", cin, c, k, stride,
+                      w_scale=np.sqrt(1.0 / (k * k * cin)), b_scale=0.05))
+    y = b.silu(b.conv(t, c, c, 1, 1, pad=0, w_scale=np.sqrt(1.0 / c),
+                      b_scale=0.05))
+    if c >= 32:  # a C2f-style Split / Concat: the 1x1 output gets a copy
+        h1, h2 = b.op("Split", [y, b.const(np.array([c // 2, c // 2],
+                                                     np.int64))],
+                      n_out=2, axis=1)
+        y = b.op("Concat", [h1, b.silu(b.conv(h2, c // 2, c // 2, 3, 1,
+                                               w_scale=0.1)), h2], axis=1)
+    g = b.build("images", [None, cin, size, size], y)
+    calib = [Stream(150 + i).normal((2, cin, size, size)).astype(np.float32)
+             for i in range(2)]
+    cq = _calibrated(g, "int8", True, calib)
+    x = Stream(160).normal((batch, cin, size, size)).astype(np.float32)
+    oracle = OraclePipeline(g, _qjson(cq, tmp_path))
+    oracle.run(x, keep=True)
+    ex = cq.executor({"images": x.shape})
+    assert [n for n, _ in ex.launches if n.startswith("chain:")], \
         [n for n, _ in ex.launches]
     ex.run({"images": x})
     checked = 0
