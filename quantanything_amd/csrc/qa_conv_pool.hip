@@ -37,10 +37,24 @@ __global__ __launch_bounds__(256) void k_conv_pool(ConvArgs a, PoolArgs pl) {
     {
         const int8_t* src = a.wp + (int64_t)cb0 * a.wp_rstride;
         const int units = 4 * WM * 16 * a.KGp;
-        for (int u = threadIdx.x; u < units; u += 256) {
-            const int row = u / a.KGp, kc = u - row * a.KGp;
-            s_w[row * RS + kc] =
-                *(const v4i*)(src + (int64_t)row * a.wp_rstride + kc * 16);
+        // eight loads in flight per thread before their stores (a loop of
+        // load-then-store would wait one memory round trip per unit)
+        for (int u0 = threadIdx.x; u0 < units; u0 += 8 * 256) {
+            v4i w[8];
+            int at[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int u = u0 + j * 256;
+                const bool ok = u < units;
+                const int row = ok ? u / a.KGp : 0;
+                const int kc = ok ? u - row * a.KGp : 0;
+                at[j] = ok ? row * RS + kc : -1;
+                w[j] = *(const v4i*)(src + (int64_t)row * a.wp_rstride +
+                                     kc * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (at[j] >= 0) s_w[at[j]] = w[j];
         }
         s_tab[threadIdx.x] = ((const int*)((const char*)a.plan + PLAN_E))[threadIdx.x];
     }
