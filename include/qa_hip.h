@@ -322,8 +322,8 @@ int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
                    void* stream);
 
 /* Two chained convolutions in one launch (the bottleneck of a C2f block):
- * d1 and d2 are int8 3x3 stride-1 pad-1 convolutions C -> C (C = 16, 32
- * or 64; packed layout 0, one group, epilogue plans, dense channels-last
+ * d1 and d2 are int8 3x3 stride-1 pad-1 convolutions C -> C (C = 16, 32,
+ * 64 or 128; packed layout 0, one group, epilogue plans, dense channels-last
  * tensors), d1 without residual or rescaled copy, and d2 reads d1's output
  * (d2->x == d1->y). The result is what qa_d_conv(d1) then qa_d_conv(d2)
  * would store at d2->y (and d2->y2), with d2's residual Add; d1->y is not

@@ -187,7 +187,7 @@ bool launch_conv_wr(const ConvArgs& b, int wm, hipStream_t st);
 // Launch form of a descriptor's arguments (fastio, pixel strides, magic
 // divisors); returns the epilogue variant (qa_conv_mfma.hip).
 int fast_io_args(const ConvArgs& a, ConvArgs& b, int epi);
-// Two chained 3x3 stride-1 convolutions (C -> C, C in {16, 32, 64}) in one
+// Two chained 3x3 stride-1 convolutions (C -> C, C in {16, 32, 64, 128}) in one
 // launch, the intermediate kept in LDS (qa_conv_pair.hip); arguments in
 // launch form.
 bool conv_pair_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,

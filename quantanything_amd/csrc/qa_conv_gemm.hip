@@ -732,7 +732,7 @@ QA_API int qa_d_conv_pair(const qa_conv_desc* d1, const qa_conv_desc* d2,
     if (!pair_args(d1, d2, b1, b2, "qa_d_conv_pair")) {
         set_error("qa_d_conv_pair",
                   "needs two int8 3x3 stride-1 C -> C convolutions (C 16, "
-                  "32 or 64) with table plans, the second reading the "
+                  "32, 64 or 128) with table plans, the second reading the "
                   "first's output");
         return -1;
     }

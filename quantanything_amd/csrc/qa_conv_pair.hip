@@ -1,6 +1,7 @@
 // Two chained 3x3 convolutions in one launch: y = f2(f1(x)) (+ residual),
 // the bottleneck of a C2f block (3x3 stride-1 conv, SiLU, 3x3 conv, SiLU,
-// Add of the block input), each conv C -> C channels with C in {16, 32, 64}.
+// Add of the block input), each conv C -> C channels with C in {16, 32, 64}
+// (and 128: k_conv_pair_cs below).
 //
 // A work-group owns R output rows of one image and all C channels. It
 // stages in LDS, with every load of a thread in flight before its stores:
@@ -298,6 +299,216 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
     }
 }
 
+// The 128-channel form (8 channel tiles): both weight sets (2 x 150 KB)
+// exceed LDS, so the 8 waves split the channels instead of the tiles: wave
+// w owns channels 16 w .. 16 w + 15 of both convs, loads its weight
+// fragments of conv 1 (18 K-steps) straight from L2 into VGPRs while the
+// band is staged and those of conv 2 during phase 1, and walks every tile
+// of the band in both phases (all waves read the same activation
+// fragments from LDS). Staging, bands, tables and epilogues as above.
+template <bool RES>
+__global__ __launch_bounds__(CP_NT) void k_conv_pair_cs(ConvArgs a1,
+                                                        ConvArgs a2,
+                                                        PairGeom g) {
+    constexpr int WM = 8, C = 128, KS = 18, LCPP = 3;
+    extern __shared__ int4 lds4[];
+    int8_t* s_x = (int8_t*)lds4;         // input band
+    int8_t* s_m = s_x + g.xb_bytes;      // intermediate band
+    int* s_kt = (int*)(s_m + g.mb_bytes);  // 4 KS k-group offsets
+    __shared__ int s_tab1[256];
+    __shared__ int s_tab2[768];
+    __shared__ int4 s_pc[2][C];
+    __shared__ uint32_t s_corr[2][C];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, kgl = lane >> 4;
+    const int KGp = 4 * KS;
+    const int W = a1.W, OW = a2.OW, OH = a2.OH;
+    const int band = blockIdx.x;
+    const int n = band / g.bpi;
+    const int oy0 = (band - n * g.bpi) * g.R;
+    const int R = min(g.R, OH - oy0);
+    const int iy0 = oy0 - 2;
+    const int BR = R + 4, MR = R + 2;
+    const int pv1 = splat4(a1.pad_value), pv2 = splat4(a2.pad_value);
+    const v4i pad1 = {pv1, pv1, pv1, pv1}, pad2 = {pv2, pv2, pv2, pv2};
+    const int co = 16 * wave + col;  // this lane's weight row (both convs)
+    // conv 1's weight fragments, in flight with the band's loads
+    v4i wb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+        wb[s] = *(const v4i*)(a1.wp + (int64_t)co * a1.wp_rstride + 64 * s +
+                              16 * kgl);
+    const int r_lo = max(0, -iy0), r_hi = min(BR, a1.H - iy0);
+    const int nreal = max(r_hi - r_lo, 0) * W * WM;
+    {
+        v4i vx[CP_SB];
+        int ax[CP_SB];
+        const int xsp = (int)a1.x_sp;
+        const int8_t* xrow = (const int8_t*)a1.x + (int64_t)n * a1.x_sn +
+                             (int64_t)(iy0 + r_lo) * W * a1.x_sp;
+        const int ch = tid & (WM - 1);
+#pragma unroll
+        for (int u = 0; u < CP_SB; ++u) {
+            const int e = tid + u * CP_NT;
+            const int p = e >> LCPP;
+            const int row = cp_div(p, g.m_w), ix = p - row * W;
+            const bool ok = e < nreal;
+            ax[u] = ok ? ((r_lo + row) * g.BW + ix + 1) * g.PS + ch * 16 : -1;
+            vx[u] = *(const v4i*)(xrow + (ok ? p * xsp + ch * 16 : 0));
+        }
+        for (int e = tid; e < BR * g.BW * WM; e += CP_NT) {
+            const int p = e >> LCPP, c = e & (WM - 1);
+            const int row = cp_div(p, g.m_bw), cc = p - row * g.BW;
+            if (row < r_lo || row >= r_hi || cc == 0 || cc == g.BW - 1)
+                *(v4i*)(s_x + p * g.PS + c * 16) = pad1;
+        }
+        for (int e = tid; e < MR * g.BW * WM; e += CP_NT) {
+            const int p = e >> LCPP, c = e & (WM - 1);
+            const int row = cp_div(p, g.m_bw), cc = p - row * g.BW;
+            const int my = oy0 - 1 + row;
+            if ((unsigned)my >= (unsigned)OH || cc == 0 || cc == g.BW - 1)
+                *(v4i*)(s_m + p * g.PS + c * 16) = pad2;
+        }
+        for (int kg = tid; kg < KGp; kg += CP_NT) {
+            const int tap = kg / WM, cb = kg - tap * WM;  // 72 = 9 x 8 real
+            const int ky = tap / 3, kx = tap - ky * 3;
+            s_kt[kg] = (ky * g.BW + kx) * g.PS + cb * 16;
+        }
+        for (int i = tid; i < 256; i += CP_NT)
+            s_tab1[i] = ((const int*)((const char*)a1.plan + PLAN_E))[i];
+        for (int i = tid; i < 768; i += CP_NT)
+            s_tab2[i] = ((const int*)((const char*)a2.plan + PLAN_E))[i];
+        if (tid < C) {
+            s_pc[0][tid] = ((const int4*)((const char*)a1.plan + PLAN_CH))[tid];
+            s_corr[0][tid] = a1.corr ? (uint32_t)a1.corr[tid] : 0u;
+        } else if (tid < 2 * C) {
+            const int c = tid - C;
+            s_pc[1][c] = ((const int4*)((const char*)a2.plan + PLAN_CH))[c];
+            s_corr[1][c] = a2.corr ? (uint32_t)a2.corr[c] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < CP_SB; ++u)
+            if (ax[u] >= 0) *(v4i*)(s_x + ax[u]) = vx[u];
+    }
+    __syncthreads();
+
+    const int q = lane & 3;
+    const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
+    const uint32_t sel2 = (q & 1) ? 0x03070105u : 0x06020400u;
+    const int cq = col & ~3;
+    int kt[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kt[s] = s_kt[4 * s + kgl];
+    auto consts = [&](int which, int& cm, int& ct, int64_t& cc,
+                      uint32_t& cr) {
+        const int4 pc = s_pc[which][co];
+        cm = pc.x;
+        ct = pc.y;
+        cc = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
+        cr = s_corr[which][co];
+    };
+    auto tile_acc = [&](const int8_t* xb, const v4i (&w)[KS]) {
+        v4i fa[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) fa[s] = *(const v4i*)(xb + kt[s]);
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[s], w[s], acc, 0,
+                                                        0, 0);
+        return acc;
+    };
+
+    // ---- phase 1 (conv 2's weights in flight) ----
+    v4i wb2[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+        wb2[s] = *(const v4i*)(a2.wp + (int64_t)co * a2.wp_rstride + 64 * s +
+                               16 * kgl);
+    {
+        int cm, ct;
+        int64_t cc;
+        uint32_t cr;
+        consts(0, cm, ct, cc, cr);
+        const int4 h1 = *(const int4*)a1.plan;
+        const int mr_lo = max(0, 1 - oy0), mr_hi = min(MR, OH + 1 - oy0);
+        const int npix = (mr_hi - mr_lo) * OW;
+        const int ntile = (npix + 15) >> 4;
+        for (int t = 0; t < ntile; ++t) {
+            const int qp = mr_lo * OW + min(16 * t + col, npix - 1);
+            const int mr = cp_div(qp, g.m_w), mc = qp - mr * OW;
+            const v4i acc = tile_acc(s_x + (mr * g.BW + mc) * g.PS, wb);
+            const int pq = 16 * t + 4 * kgl + q;
+            const int sq = mr_lo * OW + min(pq, npix - 1);
+            const int sr = cp_div(sq, g.m_w), sc = sq - sr * OW;
+            int e[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const uint32_t wu = (uint32_t)acc[rr] + cr;
+                const int q0 = (int)(((int64_t)(int)wu * cm + cc) >> ct);
+                e[rr] = s_tab1[min(max(q0, h1.x), h1.y) - h1.x];
+            }
+            const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
+            if (pq < npix)
+                *(uint32_t*)(s_m + (sr * g.BW + sc + 1) * g.PS + 16 * wave +
+                             cq) = wy;
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 2 ----
+    {
+        int cm, ct;
+        int64_t cc;
+        uint32_t cr;
+        consts(1, cm, ct, cc, cr);
+        const int4 h2 = *(const int4*)a2.plan;
+        const int pA = h2.x, pB = h2.y, pSH = h2.z;
+        const int npix = R * OW;
+        const int ntile = (npix + 15) >> 4;
+        const int64_t pimg = ((int64_t)n * OH + oy0) * OW;
+        const int c0 = 16 * wave + cq;
+        for (int t = 0; t < ntile; ++t) {
+            const int pq = 16 * t + 4 * kgl + q;
+            const bool pok = pq < npix;
+            const int64_t p = pimg + min(pq, npix - 1);
+            uint32_t rw = 0;
+            if (RES)
+                rw = *(const uint32_t*)((const int8_t*)a2.res +
+                                        p * a2.res_pst + c0);
+            const int qp = min(16 * t + col, npix - 1);
+            const int r = cp_div(qp, g.m_w), ox = qp - r * OW;
+            const v4i acc = tile_acc(s_m + (r * g.BW + ox) * g.PS, wb2);
+            int e[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const uint32_t wu = (uint32_t)acc[rr] + cr;
+                const int q0 = (int)(((int64_t)(int)wu * cm + cc) >> ct);
+                e[rr] = min(max(q0, pA), pB) - pA;
+            }
+            if (RES) {
+                const uint32_t rv = quad_transpose(rw, sel1, sel2);
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int v = s_tab2[256 + e[rr]] +
+                                  s_tab2[512 + ((rv >> (8 * rr)) & 255)];
+                    e[rr] = min(max(v, 0), pSH);
+                }
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) e[rr] = s_tab2[e[rr]];
+            const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
+            if (pok) *(uint32_t*)((int8_t*)a2.y + p * a2.y_pst + c0) = wy;
+            if (a2.y2) {
+                const uint32_t w2 =
+                    quad_transpose(pack_entries(e, 1), sel1, sel2);
+                if (pok) *(uint32_t*)((int8_t*)a2.y2 + p * a2.y2_pst + c0) = w2;
+            }
+        }
+    }
+}
+
 uint32_t cp_magic(int64_t d) {
     return (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) /
                       (uint64_t)std::max<int64_t>(d, 2));
@@ -318,9 +529,11 @@ PairGeom pair_geom(const ConvArgs& b, int R) {
     const int64_t mb = (int64_t)(R + 2) * g.BW * g.PS;
     g.xb_bytes = (int)std::min<int64_t>(xb, 1 << 30);
     g.mb_bytes = (int)std::min<int64_t>(mb, 1 << 30);
-    const int64_t bytes = xb + mb + 2 * (int64_t)C * g.RSW + b.KGp * 4;
+    // 128 channels: the weights go straight to VGPRs, not through LDS
+    const int64_t wbytes = C == 128 ? 0 : 2 * (int64_t)C * g.RSW;
+    const int64_t bytes = xb + mb + wbytes + b.KGp * 4;
     const int64_t bchunks = (int64_t)(R + 4) * b.W * wm;
-    const int64_t wchunks = (int64_t)C * b.KGp;
+    const int64_t wchunks = C == 128 ? 0 : (int64_t)C * b.KGp;
     g.lds = bytes <= 140 * 1024 && bchunks <= (int64_t)CP_SB * CP_NT &&
                     wchunks <= (int64_t)CP_SW * CP_NT &&
                     (int64_t)(R + 4) * g.BW * wm < (1 << 16)
@@ -336,6 +549,8 @@ using PairKern = void (*)(ConvArgs, ConvArgs, PairGeom);
 
 PairKern pair_kernel(int wm, bool res) {
     switch (wm * 2 + (res ? 1 : 0)) {
+        case 16: return &k_conv_pair_cs<false>;
+        case 17: return &k_conv_pair_cs<true>;
         case 2: return &k_conv_pair<1, false>;
         case 3: return &k_conv_pair<1, true>;
         case 4: return &k_conv_pair<2, false>;
@@ -357,7 +572,7 @@ bool conv_3x3_same(const ConvArgs& b) {
 bool conv_pair_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
                        int epi2) {
     const int C = b1.Cout;
-    if (!(C == 16 || C == 32 || C == 64)) return false;
+    if (!(C == 16 || C == 32 || C == 64 || C == 128)) return false;
     if (!(epi1 == Q8_TABLE && epi2 == Q8_TABLE && b1.mode == EPI_QUANT &&
           b2.mode == EPI_QUANT && b1.fastio && b2.fastio && b1.plan &&
           b2.plan && conv_3x3_same(b1) && conv_3x3_same(b2) &&
@@ -400,9 +615,10 @@ bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2,
             res <= 0)
             res = 1;
         const int64_t rounds = ceil_div(g.nbands, (int64_t)res * cus);
+        const int64_t split = wm == 8 ? 1 : CP_NW;  // waves sharing tiles
         const int64_t t1 = ceil_div(ceil_div((int64_t)(R + 2) * b1.OW, 16),
-                                    CP_NW);
-        const int64_t t2 = ceil_div(ceil_div((int64_t)R * b1.OW, 16), CP_NW);
+                                    split);
+        const int64_t t2 = ceil_div(ceil_div((int64_t)R * b1.OW, 16), split);
         const int64_t cost = rounds * (4 + t1 + t2);
         if (best < 0 || cost < best) {
             best = cost;

@@ -802,7 +802,7 @@ class DeviceExecutor:
             self.tensors.pop(xname, None)  # never materialized
 
     def _fuse_pairs(self, cons):
-        """Two int8 3x3 stride-1 convolutions C -> C (C 16, 32 or 64), the
+        """Two int8 3x3 stride-1 convolutions C -> C (C 16 to 128), the
         second the only reader of the first's output (a C2f bottleneck), run
         as one launch (``qa_d_conv_pair``): the intermediate tensor stays in
         LDS and is never written."""

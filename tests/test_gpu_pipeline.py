@@ -392,10 +392,13 @@ def test_weights_in_registers_kernel(hip, tmp_path, cin, cout, k, stride, pad,
     (64, 9, 3, True),
     (32, 11, 2, False),
     (64, 7, 1, False),
+    (128, 7, 2, True),    # channel-split form (weights from L2)
+    (128, 10, 1, False),
 ])
 def test_fused_conv_pair(hip, tmp_path, c, size, batch, residual):
     """Two chained 3x3 convolutions (a C2f bottleneck: conv, SiLU, conv,
-    SiLU, Add of the input) run as one launch with the intermediate in LDS
+    SiLU, Add of the input; 16 to 128 channels) run as one launch with the
+    intermediate in LDS
     and equal the oracle bit for bit; the intermediate tensor is never
     materialized."""
     b = G.GraphBuilder(23)
