@@ -134,6 +134,34 @@ __device__ __forceinline__ int qa_quantize_f32(float x, float invf, int zp,
     return min(max(q, qmin), qmax);
 }
 
+// Whether qa_quantize_f32 applies to a quantization (scale in [2^-60,
+// 2^60], clip range narrower than 2^20, zero point inside it).
+__host__ __device__ __forceinline__ bool qa_f32_form_ok(double scale,
+                                                       int64_t zp,
+                                                       int64_t qmin,
+                                                       int64_t qmax) {
+    return scale >= 0x1p-60 && scale <= 0x1p60 && qmax - qmin < (1 << 20) &&
+           qmin >= INT32_MIN && qmax <= INT32_MAX && zp >= qmin && zp <= qmax;
+}
+
+// qa_quantize_one_fast's result through the float32 form where that form
+// decides (f32ok from qa_f32_form_ok, invf = float(1 / scale)), the double
+// form otherwise (near-ties, NaN): a few float instructions per value
+// instead of the double ones.
+__device__ __forceinline__ int64_t qa_quantize_mixed(float x, bool f32ok,
+                                                     float invf, double scale,
+                                                     double inv, int64_t zp,
+                                                     int64_t qmin,
+                                                     int64_t qmax) {
+    if (f32ok) {
+        bool slow = false;
+        const int q = qa_quantize_f32(x, invf, (int)zp, (int)qmin, (int)qmax,
+                                      &slow);
+        if (!slow) return q;
+    }
+    return qa_quantize_one_fast(x, scale, inv, zp, qmin, qmax);
+}
+
 // --------------------------------------------------------------- errors ---
 namespace qa {
 

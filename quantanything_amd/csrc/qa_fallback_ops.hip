@@ -75,6 +75,8 @@ __global__ __launch_bounds__(kThreads) void k_layernorm(
     const int lane = threadIdx.x & 63;
     const int gl = lane % GS;
     const double inv = 1.0 / out_scale;
+    const bool f32ok = qa_f32_form_ok(out_scale, out_zp, qmin, qmax);
+    const float invf = (float)inv;
     const int64_t first =
         ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / GS;
     for (int64_t r = first; r - lane / GS < rows;
@@ -88,8 +90,9 @@ __global__ __launch_bounds__(kThreads) void k_layernorm(
         auto emit = [&](int64_t i, double v, double mean, double sd) {
             double t = (v - mean) / sd * (double)gamma[i];
             if (beta) t += (double)beta[i];
-            const int64_t q = qa_quantize_one_fast((float)t, out_scale, inv,
-                                                   out_zp, qmin, qmax);
+            const int64_t q = qa_quantize_mixed((float)t, f32ok, invf,
+                                                out_scale, inv, out_zp, qmin,
+                                                qmax);
             y[rr * y_rs + i] = (TO)(q - y_so);
         };
         if (PER > 0) {
@@ -366,6 +369,8 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
     const int64_t a_add = d.a_so - d.a_zp, b_add = d.b_so - d.b_zp;
     const double scale = d.a_scale * d.b_scale;
     const double inv = 1.0 / d.out_scale;
+    const bool f32ok = qa_f32_form_ok(d.out_scale, d.out_zp, d.qmin, d.qmax);
+    const float invf = (float)inv;
     const int mr = wave * 16;  // the wave's 16 rows within the block
     if (m0 + mr >= d.M) return;
     const int ksteps = Kp / 64;
@@ -389,8 +394,8 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
                 v += a_add * ssum[64 + n] + b_add * ssum[ml] +
                      d.K * a_add * b_add;
             const float yf = (float)((double)v * scale);
-            const int64_t q = qa_quantize_one_fast(yf, d.out_scale, inv,
-                                                   d.out_zp, d.qmin, d.qmax);
+            const int64_t q = qa_quantize_mixed(yf, f32ok, invf, d.out_scale,
+                                                inv, d.out_zp, d.qmin, d.qmax);
             ((TO*)d.y)[b0 * d.y_s0 + b1 * d.y_s1 + m * d.y_sm + n * d.y_sn] =
                 (TO)(q - d.y_so);
         }

@@ -279,6 +279,8 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(
     const int lane = threadIdx.x & 63;
     const int gl = lane % GS;
     const double inv = 1.0 / out_scale;
+    const bool f32ok = qa_f32_form_ok(out_scale, out_zp, qmin, qmax);
+    const float invf = (float)inv;
     const int64_t first = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW +
                           lane / GS;
     for (int64_t r = first; r - lane / GS < rows;
@@ -313,8 +315,8 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(
             const int64_t i = gl + GS * k;
             if (i >= cols) continue;
             const float y = (float)(e[k] / sum);
-            const int64_t q =
-                qa_quantize_one_fast(y, out_scale, inv, out_zp, qmin, qmax);
+            const int64_t q = qa_quantize_mixed(y, f32ok, invf, out_scale, inv,
+                                                out_zp, qmin, qmax);
             out[base + i] = (TO)(q - out_so);
             if (outf) outf[base + i] = (float)((double)(q - out_zp) * out_scale);
         }
@@ -350,6 +352,8 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
     const int lane = threadIdx.x & 63;
     const int gl = lane % GS;
     const double inv = 1.0 / out_scale;
+    const bool f32ok = qa_f32_form_ok(out_scale, out_zp, qmin, qmax);
+    const float invf = (float)inv;
     const int64_t first = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW +
                           lane / GS;
     for (int64_t r = first; r - lane / GS < rows;
@@ -381,8 +385,8 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
             const int64_t i = gl + GS * k;
             if (i >= cols) continue;
             const float y = (float)(e[k] / sum);
-            const int64_t q =
-                qa_quantize_one_fast(y, out_scale, inv, out_zp, qmin, qmax);
+            const int64_t q = qa_quantize_mixed(y, f32ok, invf, out_scale, inv,
+                                                out_zp, qmin, qmax);
             out[base + i] = (int8_t)(q - out_so);
         }
     }
