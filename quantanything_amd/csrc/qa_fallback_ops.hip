@@ -374,6 +374,13 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
     const int mr = wave * 16;  // the wave's 16 rows within the block
     if (m0 + mr >= d.M) return;
     const int ksteps = Kp / 64;
+    // output row bases of the lane's 4 rows (hoisted out of the column
+    // loop: four 64-bit products per element otherwise)
+    TO* yrow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        yrow[r] = (TO*)d.y + b0 * d.y_s0 + b1 * d.y_s1 +
+                  (m0 + mr + 4 * kg + r) * d.y_sm;
     for (int nt = 0; nt < Np; nt += 16) {
         v4i_t acc = {0, 0, 0, 0};
         for (int ks = 0; ks < ksteps; ++ks) {
@@ -396,8 +403,7 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
             const float yf = (float)((double)v * scale);
             const int64_t q = qa_quantize_mixed(yf, f32ok, invf, d.out_scale,
                                                 inv, d.out_zp, d.qmin, d.qmax);
-            ((TO*)d.y)[b0 * d.y_s0 + b1 * d.y_s1 + m * d.y_sm + n * d.y_sn] =
-                (TO)(q - d.y_so);
+            yrow[r][n * d.y_sn] = (TO)(q - d.y_so);
         }
     }
 }
