@@ -269,9 +269,30 @@ def main():
         per.append((time_launch(fn, 20, torch), name, fn))
     layers = {l.name: l for l in c.layers}
 
+    def conv_out_shape(layer, xs):
+        n, _, h, w = xs
+        cout, _, kh, kw = layer.w_centered.shape
+        strides, pads, dil, _ = layer.geometry(xs)
+        return (n, cout,
+                (h + pads[0] + pads[2] - dil[0] * (kh - 1) - 1) // strides[0]
+                + 1,
+                (w + pads[1] + pads[3] - dil[1] * (kw - 1) - 1) // strides[1]
+                + 1)
+
     def work(name):
-        """(layer, ops, bytes) of a conv launch ("qconv:": float input)."""
+        """(layer, ops, bytes) of a conv launch ("qconv:": float input;
+        "pair:" / "chain:": two convs, the intermediate not in HBM)."""
         kind, _, lname = name.partition(":")
+        if kind in ("pair", "chain"):
+            a, _, b = lname.partition("+")
+            if a not in layers or b not in layers:
+                return None
+            la, lb = layers[a], layers[b]
+            xs = shapes[la.data_inputs[0]]
+            mid = conv_out_shape(la, xs)
+            oa, ba = layer_work(la, xs)
+            ob, bb = layer_work(lb, mid)
+            return lb, oa + ob, ba + bb - 2 * int(np.prod(mid))
         if kind not in ("conv", "qconv", "convpool") or lname not in layers:
             return None
         layer = layers[lname]
@@ -295,9 +316,10 @@ def main():
     if w is not None:
         top, ops, byts = w
         roof = roofline(ops, byts, top_ms)
-        roof["kernel"] = (f"fused conv {top.name} (int8 MFMA"
-                          + (", float input quantized in" if
-                             top_name.startswith("qconv:") else "") + ")")
+        roof["kernel"] = (f"fused conv {top_name.partition(':')[2]} (int8 "
+                          "MFMA" + (", float input quantized in" if
+                                    top_name.startswith("qconv:") else "")
+                          + ")")
         roof["ops_per_launch"] = ops
         roof["bytes_per_launch"] = byts
     else:
