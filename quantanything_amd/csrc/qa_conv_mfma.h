@@ -25,6 +25,9 @@
 //   Q8_GENERAL the 128-bit form for any parameters.
 #pragma once
 
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <type_traits>
 
 #include "qa_conv.h"
@@ -710,6 +713,32 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
             }
         }
     }
+}
+
+// Work-groups of `block` threads of kernel k resident per CU with `lds`
+// dynamic LDS bytes on the current device, cached per (kernel, block, lds,
+// device): the band launchers ask for every candidate band height at every
+// launch.
+inline int resident_blocks(const void* k, int block, int lds) {
+    static std::mutex mu;
+    static std::map<std::tuple<const void*, int, int, int>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    const auto key = std::make_tuple(k, block, lds, dev);
+    {
+        std::lock_guard<std::mutex> g(mu);
+        const auto it = cache.find(key);
+        if (it != cache.end()) return it->second;
+    }
+    int nbk = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nbk, k, block,
+                                                     (size_t)lds) !=
+            hipSuccess ||
+        nbk <= 0)
+        nbk = 1;
+    std::lock_guard<std::mutex> g(mu);
+    cache[key] = nbk;
+    return nbk;
 }
 
 // Compute units of the current device (cached per device).

@@ -608,12 +608,7 @@ bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2,
     for (int R = 1; R <= b1.OH; ++R) {
         const PairGeom g = pair_geom(b1, R);
         if (g.lds == 0) break;
-        int res = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &res, (const void*)kern, CP_NT, (size_t)g.lds) !=
-                hipSuccess ||
-            res <= 0)
-            res = 1;
+        const int res = resident_blocks((const void*)kern, CP_NT, g.lds);
         const int64_t rounds = ceil_div(g.nbands, (int64_t)res * cus);
         const int64_t split = wm == 8 ? 1 : CP_NW;  // waves sharing tiles
         const int64_t t1 = ceil_div(ceil_div((int64_t)(R + 2) * b1.OW, 16),

@@ -456,12 +456,7 @@ WrKern wr_kernel_rt(int wm, int ks, bool res, bool ch = false) {
 
 // Work-groups of a kernel resident per CU with `lds` dynamic bytes.
 int wr_resident(WrKern k, int lds) {
-    int nbk = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &nbk, (const void*)k, WR_NT, (size_t)lds) != hipSuccess ||
-        nbk <= 0)
-        nbk = 1;
-    return nbk;
+    return resident_blocks((const void*)k, WR_NT, lds);
 }
 
 }  // namespace
