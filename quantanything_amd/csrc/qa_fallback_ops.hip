@@ -381,6 +381,15 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
     for (int r = 0; r < 4; ++r)
         yrow[r] = (TO*)d.y + b0 * d.y_s0 + b1 * d.y_s1 +
                   (m0 + mr + 4 * kg + r) * d.y_sm;
+    // zero-point corrections: the row terms of the lane's 4 rows once per
+    // wave, the column term once per column tile
+    int64_t rterm[4] = {0, 0, 0, 0};
+    if (SUMS) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            rterm[r] = b_add * ssum[min(mr + 4 * kg + r, 63)] +
+                       d.K * a_add * b_add;
+    }
     for (int nt = 0; nt < Np; nt += 16) {
         v4i_t acc = {0, 0, 0, 0};
         for (int ks = 0; ks < ksteps; ++ks) {
@@ -391,15 +400,14 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
         }
         const int64_t n = nt + col;
         if (n >= d.N) continue;
+        const int64_t cterm = SUMS ? a_add * ssum[64 + n] : 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int ml = mr + 4 * kg + r;
             const int64_t m = m0 + ml;
             if (m >= d.M) continue;
             int64_t v = acc[r];
-            if (SUMS)
-                v += a_add * ssum[64 + n] + b_add * ssum[ml] +
-                     d.K * a_add * b_add;
+            if (SUMS) v += cterm + rterm[r];
             const float yf = (float)((double)v * scale);
             const int64_t q = qa_quantize_mixed(yf, f32ok, invf, d.out_scale,
                                                 inv, d.out_zp, d.qmin, d.qmax);
