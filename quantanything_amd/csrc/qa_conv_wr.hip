@@ -55,9 +55,10 @@ struct WrGeom {
     int RSW;              // LDS row stride of the staged weights
     int lds;              // dynamic LDS bytes (0: does not fit)
     int KSR;              // K-steps the kernel runs (>= KGp / 4, zero-padded)
-    // ceil(2^32 / d) for d = band columns, KGp, OW, W (all >= 2):
+    // ceil(2^32 / d) for d = band columns, KGp, OW, W (all >= 2) and the
+    // 16-byte chunks of a pixel (used when >= 2):
     // floor(n / d) = (n * m) >> 32 for the n < 2^16 used here
-    uint32_t m_bw, m_kgp, m_ow, m_w;
+    uint32_t m_bw, m_kgp, m_ow, m_w, m_cpp;
 };
 
 __device__ __forceinline__ int wr_div(int n, uint32_t m) {
@@ -121,18 +122,17 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
     const int r_lo = max(0, -iy0), r_hi = min(bg.BR, a.H - iy0);
     const int nreal = max(r_hi - r_lo, 0) * a.W * cpp;
     {
-        const int lcpp = __builtin_ctz(cpp);  // cpp is a power of two
         v4i vx[WR_SB], vw[WR_SW];
         int ax[WR_SB], aw[WR_SW];
         {
             const int xsp = (int)a.x_sp;
             const int8_t* xrow = xn + (int64_t)(iy0 + r_lo) * a.W * a.x_sp;
             const int colmax = bg.BW - a.PW;  // real columns kept
-            const int ch = tid & (cpp - 1);   // the same part for every u
 #pragma unroll
             for (int u = 0; u < WR_SB; ++u) {
                 const int e = tid + u * WR_NT;
-                const int p = e >> lcpp;
+                const int p = cpp == 1 ? e : wr_div(e, bg.m_cpp);
+                const int ch = e - p * cpp;
                 const int row = wr_div(p, bg.m_w), ix = p - row * a.W;
                 const bool ok = e < nreal && ix < colmax;
                 ax[u] = ok ? ((r_lo + row) * bg.BW + ix + a.PW) * bg.PS +
@@ -157,7 +157,8 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
         // pad value: band rows outside the image, columns left of the
         // image and right of it
         for (int e = tid; e < nch; e += WR_NT) {
-            const int p = e >> lcpp, ch = e & (cpp - 1);
+            const int p = cpp == 1 ? e : wr_div(e, bg.m_cpp);
+            const int ch = e - p * cpp;
             const int row = wr_div(p, bg.m_bw), col = p - row * bg.BW;
             if (row < r_lo || row >= r_hi || col < a.PW || col >= a.PW + a.W)
                 *(v4i*)(s_band + p * bg.PS + ch * 16) = pad4;
@@ -401,6 +402,7 @@ WrGeom wr_geom(const ConvArgs& b, int wm, int R, bool ch = false) {
     g.m_kgp = magic(b.KGp);
     g.m_ow = magic(b.OW);
     g.m_w = magic(b.W);
+    g.m_cpp = magic(b.Cg >> 4);
     g.KSR = wr_steps(wm, b.KGp / 4);
     const int64_t bytes =
         band + (int64_t)wm * 16 * g.RSW + (int64_t)g.KSR * 16 +
@@ -467,7 +469,7 @@ bool conv_wr_applies(const ConvArgs& b, int epi, int wm) {
     if (!(epi == Q8_TABLE && b.mode == EPI_QUANT && b.fastio && b.plan &&
           b.G == 1 && b.layout == 0 && b.x_code == 1 && b.x_sc == 1 &&
           b.rowsum == 0 && b.Cg % 16 == 0 && b.Cg > 0 &&
-          ((b.Cg >> 4) & ((b.Cg >> 4) - 1)) == 0 && b.W >= 2 &&
+          b.W >= 2 &&
           b.Cout % 4 == 0 &&
           b.OW >= 2 &&
           b.KGp % 4 == 0 && wr_steps(wm, b.KGp / 4) > 0 && xa % 16 == 0 &&
