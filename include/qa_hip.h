@@ -7,8 +7,15 @@
  * with QA_LIB at native.py:137). Signatures, argument meaning and results are
  * those of quantization/kernels/qa_kernels.cpp; results are bit-identical.
  * These entries take host (or device) pointers, run on the GPU and return
- * when the output is written. Like the reference they return void; a failure
- * is reported through qa_last_error() and printed to stderr once.
+ * when the output is written. Like the reference they return void and are
+ * re-entrant: each calling thread has its own stream and scratch buffers.
+ * A failure (a geometry the reference would divide by zero on, a HIP error)
+ * never aborts the process: the call fills its output with zeros, records
+ * the message for qa_last_error() and prints it to stderr. Every call starts
+ * afresh, so a later call computes its full result whether or not the caller
+ * ever reads or clears the error (the reference's loader never does). Shapes
+ * the reference accepts are all computed (no limit on N, Cout or M beyond
+ * the 2^31 element bound of a dimension).
  *
  * Part 2 is additional surface the reference's loader ignores: backend
  * identification and errors, weight packing, and device-pointer entries used
@@ -100,11 +107,13 @@ void qa_dequantize_f32(const int32_t* q, float* x, int64_t n, double scale,
 /* No counterpart in the reference: its loader ignores these symbols. */
 
 const char* qa_backend(void);       /* "hip-gfx950" */
-const char* qa_last_error(void);    /* NULL when no error on this thread */
+const char* qa_last_error(void);    /* most recent failure of this thread
+                                       since qa_clear_error, or NULL */
 void qa_clear_error(void);
 int qa_device_count(void);
 int qa_device_arch(char* buf, int64_t len);
-void* qa_stream(void);              /* library stream (hipStream_t) */
+void* qa_stream(void);              /* the calling thread's library stream
+                                       (hipStream_t) on the current device */
 int qa_synchronize(void);
 
 /* Storage codes of device tensors: 1 int8, 2 int16, 4 int32, 8 int64.

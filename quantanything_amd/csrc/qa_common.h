@@ -165,10 +165,13 @@ __device__ __forceinline__ int64_t qa_quantize_mixed(float x, bool f32ok,
 // --------------------------------------------------------------- errors ---
 namespace qa {
 
-// Records the first failure of the calling thread (see qa_last_error) and
-// prints it to stderr once, so that a caller that never checks still sees it.
+// Records a failure of the calling thread: it marks the current host-pointer
+// ABI call as failed (see AbiCall), makes the message the one qa_last_error
+// returns, and prints it to stderr (the first 16 failures of a thread), so a
+// caller that never checks still sees it.
 void set_error(const char* where, const char* what);
 void set_hip_error(const char* where, hipError_t e);
+// False once the current ABI call (since its AbiCall was constructed) failed.
 bool ok();
 
 #define QA_HIP(call)                                        \
@@ -189,17 +192,30 @@ bool ok();
         }                                                   \
     } while (0)
 
-// Library stream of the current device (default priority, non-blocking).
+// Stream of the calling thread on the current device (default priority,
+// non-blocking). Each thread has its own, so host-pointer ABI calls from
+// several threads run concurrently, like the reference's re-entrant kernels.
 hipStream_t stream();
 
-// A device scratch buffer of at least `bytes`, owned by the library and
-// reused across host-pointer ABI calls (which serialise on a mutex).
+// A device scratch buffer of at least `bytes`, owned by the calling thread
+// (one set of slots per thread and device), reused across its ABI calls.
 void* scratch(int slot, size_t bytes);
 
-// Serialises host-pointer ABI calls (they share the scratch buffers).
-struct AbiLock {
-    AbiLock();
-    ~AbiLock();
+// Scope of one host-pointer ABI call. Construction starts a new call: the
+// per-call failure flag is cleared (an earlier failure on this thread never
+// makes a later call skip its work) and so is HIP's last-error state.
+// Destruction, when the call failed, fills the caller's output with zeros
+// (out may be a host or a device pointer), so no call returns with its
+// output unwritten.
+struct AbiCall {
+    AbiCall(void* out, size_t out_bytes);
+    ~AbiCall();
+    AbiCall(const AbiCall&) = delete;
+    AbiCall& operator=(const AbiCall&) = delete;
+
+  private:
+    void* out_;
+    size_t bytes_;
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

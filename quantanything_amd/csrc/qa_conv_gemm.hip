@@ -201,11 +201,13 @@ bool conv_shape_ok(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
             set_error("conv", "dimension outside [0, 2^31)");
             return false;
         }
-    if (Cout > 65535 || N > 65535) {
-        set_error("conv", "Cout and N must be at most 65535");
-        return false;
-    }
     return true;
+}
+
+// Whether the int8 MFMA kernels' grids can hold the problem: work-group
+// channel blocks of at least 16 channels on grid axis y, groups on axis z.
+bool mfma_grid_ok(int64_t Cog, int64_t G) {
+    return ceil_div(Cog, 16) <= 65535 && G <= 65535;
 }
 
 int pack_weights(const int32_t* w, int64_t Cout, int64_t Cg, int64_t KH,
@@ -288,12 +290,12 @@ void conv_abi(const int32_t* x, const TW* w, void* y, int64_t N, int64_t C,
               int64_t DW, int64_t G, int64_t OH, int64_t OW) {
     const int64_t nout = N * Cout * OH * OW;
     if (nout <= 0) return;
+    const size_t ybytes = (size_t)nout * (WIDE ? 8 : 4);
+    AbiCall call(y, ybytes);
     if (!conv_shape_ok(N, C, H, W, Cout, KH, KW, SH, SW, DH, DW, G, OH, OW))
         return;
-    AbiLock lk;
     hipStream_t st = stream();
     if (!st) return;
-    const size_t ybytes = (size_t)nout * (WIDE ? 8 : 4);
     void* dy = scratch(1, ybytes);
     if (!dy) return;
     const int64_t Cg = C / G;
@@ -325,7 +327,8 @@ void conv_abi(const int32_t* x, const TW* w, void* y, int64_t N, int64_t C,
     if (!device_range(dx, nx, !WIDE, st, &lo, &hi)) return;
     const int layout = (G == 1 && Cg <= 4 && KW <= 16) ? 1 : 0;
     bool mfma = K < 131072 && activation_offset(lo, hi, &a_off) &&
-                (layout == 1 || G == 1 || Cg % 16 == 0);
+                (layout == 1 || G == 1 || Cg % 16 == 0) &&
+                mfma_grid_ok(Cout / G, G);
     if (mfma)
         mfma = upload_weights(w32, Cout, Cg, KH, KW, G, a_off, layout, a, st);
     if (!ok()) return;
@@ -366,14 +369,14 @@ template <bool WIDE, class T>
 void gemm_abi(int64_t M, int64_t N, int64_t K, const T* A, const T* B,
               void* Cm) {
     if (M <= 0 || N <= 0) return;
-    if (!fits_i32(M) || !fits_i32(N) || !fits_i32(K) || N > 65535) {
-        set_error("gemm", "dimension outside the supported range");
+    const size_t cbytes = (size_t)(M * N) * (WIDE ? 8 : 4);
+    AbiCall call(Cm, cbytes);
+    if (!fits_i32(M) || !fits_i32(N) || !fits_i32(K)) {
+        set_error("gemm", "dimension outside [0, 2^31)");
         return;
     }
-    AbiLock lk;
     hipStream_t st = stream();
     if (!st) return;
-    const size_t cbytes = (size_t)(M * N) * (WIDE ? 8 : 4);
     void* dc = scratch(1, cbytes);
     if (!dc) return;
     if (K == 0) {
@@ -387,7 +390,8 @@ void gemm_abi(int64_t M, int64_t N, int64_t K, const T* A, const T* B,
     if (!host_copy(B, K * N, hb)) return;
     int lo, hi, a_off = 0;
     if (!device_range(da, M * K, false, st, &lo, &hi)) return;
-    bool mfma = K < 131072 && activation_offset(lo, hi, &a_off);
+    bool mfma = K < 131072 && activation_offset(lo, hi, &a_off) &&
+                mfma_grid_ok(N, 1);
     ConvArgs a;
     memset(&a, 0, sizeof(a));
     // A GEMM is a 1x1 convolution of M one-pixel "images" with K channels.
@@ -451,7 +455,7 @@ QA_API int qa_has_openmp(void) { return 0; }
 QA_API void qa_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A,
                         const float* B, float* C) {
     if (M <= 0 || N <= 0) return;
-    AbiLock lk;
+    AbiCall call(C, (size_t)(M * N) * 4);
     hipStream_t st = stream();
     if (!st) return;
     const float* da = upload(0, A, M * K, st);
@@ -482,9 +486,9 @@ QA_API void qa_conv_f32(const float* x, const float* w, float* y,
                         QA_CONV_PARAMS) {
     const int64_t nout = N * Cout * OH * OW;
     if (nout <= 0) return;
+    AbiCall call(y, (size_t)nout * 4);
     if (!conv_shape_ok(N, C, H, W, Cout, KH, KW, SH, SW, DH, DW, G, OH, OW))
         return;
-    AbiLock lk;
     hipStream_t st = stream();
     if (!st) return;
     const float* dx = upload(0, x, N * C * H * W, st);

@@ -207,7 +207,7 @@ void requantize_abi(const TAcc* acc, int32_t* out, int64_t outer, int64_t C,
                     int64_t qmin, int64_t qmax) {
     const int64_t n = outer * C * inner;
     if (n <= 0) return;
-    qa::AbiLock lk;
+    qa::AbiCall call(out, (size_t)n * 4);
     hipStream_t st = qa::stream();
     if (!st) return;
     const TAcc* da = upload(0, acc, n, st);
@@ -252,7 +252,7 @@ QA_API void qa_rescale(const int32_t* x, int32_t* out, int64_t n,
                        int64_t zp_in, int64_t m, int64_t s, int64_t zp_out,
                        int64_t qmin, int64_t qmax) {
     if (n <= 0) return;
-    qa::AbiLock lk;
+    qa::AbiCall call(out, (size_t)n * 4);
     hipStream_t st = qa::stream();
     if (!st) return;
     const int32_t* dx = upload(0, x, n, st);
@@ -269,7 +269,7 @@ QA_API void qa_add(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
                    int64_t sb, int64_t sign, int64_t zp_out, int64_t qmin,
                    int64_t qmax) {
     if (n <= 0) return;
-    qa::AbiLock lk;
+    qa::AbiCall call(out, (size_t)n * 4);
     hipStream_t st = qa::stream();
     if (!st) return;
     const int32_t* da = upload(0, a, n, st);
@@ -287,7 +287,7 @@ QA_API void qa_mul(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
                    int64_t za, int64_t zb, int64_t m, int64_t s, int64_t zp_out,
                    int64_t qmin, int64_t qmax) {
     if (n <= 0) return;
-    qa::AbiLock lk;
+    qa::AbiCall call(out, (size_t)n * 4);
     hipStream_t st = qa::stream();
     if (!st) return;
     const int32_t* da = upload(0, a, n, st);
@@ -302,8 +302,12 @@ QA_API void qa_mul(const int32_t* a, const int32_t* b, int32_t* out, int64_t n,
 
 QA_API void qa_lut(const int32_t* x, int32_t* out, int64_t n, int64_t offset,
                    const int32_t* lut, int64_t lut_len) {
-    if (n <= 0 || lut_len <= 0) return;
-    qa::AbiLock lk;
+    if (n <= 0) return;
+    qa::AbiCall call(out, (size_t)n * 4);
+    if (lut_len <= 0) {
+        qa::set_error("qa_lut", "empty table");
+        return;
+    }
     hipStream_t st = qa::stream();
     if (!st) return;
     const int32_t* dx = upload(0, x, n, st);
@@ -320,7 +324,7 @@ QA_API void qa_quantize_f32(const float* x, int32_t* q, int64_t n,
                             double scale, int64_t zp, int64_t qmin,
                             int64_t qmax) {
     if (n <= 0) return;
-    qa::AbiLock lk;
+    qa::AbiCall call(q, (size_t)n * 4);
     hipStream_t st = qa::stream();
     if (!st) return;
     const float* dx = upload(0, x, n, st);
@@ -335,7 +339,7 @@ QA_API void qa_quantize_f32(const float* x, int32_t* q, int64_t n,
 QA_API void qa_dequantize_f32(const int32_t* q, float* x, int64_t n,
                               double scale, int64_t zp) {
     if (n <= 0) return;
-    qa::AbiLock lk;
+    qa::AbiCall call(x, (size_t)n * 4);
     hipStream_t st = qa::stream();
     if (!st) return;
     const int32_t* dq = upload(0, q, n, st);

@@ -3,8 +3,6 @@
 #include <stdio.h>
 #include <string.h>
 
-#include <mutex>
-
 #include "qa_common.h"
 
 namespace qa {
@@ -13,19 +11,39 @@ namespace {
 
 constexpr int kMaxDevices = 16;
 constexpr int kSlots = 8;
+constexpr int kMaxPrinted = 16;
 
+// One thread's stream and scratch buffers on one device.
 struct DeviceState {
     hipStream_t stream = nullptr;
     void* buf[kSlots] = {};
     size_t cap[kSlots] = {};
 };
 
-DeviceState g_dev[kMaxDevices];
-std::mutex g_init_mutex;
-std::recursive_mutex g_abi_mutex;
+// A thread's state on every device. The destructor runs at thread exit
+// (for the main thread: at exit(), before static destructors and so while
+// the HIP runtime is still up); it drains the thread's streams and releases
+// its buffers.
+struct ThreadState {
+    DeviceState dev[kMaxDevices];
+    ~ThreadState() {
+        for (int d = 0; d < kMaxDevices; ++d) {
+            DeviceState& s = dev[d];
+            if (!s.stream) continue;
+            if (hipSetDevice(d) != hipSuccess) continue;
+            hipStreamSynchronize(s.stream);
+            for (int k = 0; k < kSlots; ++k)
+                if (s.buf[k]) hipFree(s.buf[k]);
+            hipStreamDestroy(s.stream);
+        }
+    }
+};
 
+thread_local ThreadState t_state;
 thread_local char t_error[512] = {0};
-thread_local bool t_failed = false;
+thread_local bool t_failed = false;       // since the last qa_clear_error
+thread_local bool t_call_failed = false;  // in the current ABI call
+thread_local int t_printed = 0;
 
 int current_device() {
     int d = 0;
@@ -36,47 +54,48 @@ int current_device() {
 }  // namespace
 
 void set_error(const char* where, const char* what) {
-    if (!t_failed) {
-        snprintf(t_error, sizeof(t_error), "%s: %s", where, what);
-        fprintf(stderr, "[qa_hip] error: %s\n", t_error);
+    snprintf(t_error, sizeof(t_error), "%s: %s", where, what);
+    if (t_printed < kMaxPrinted) {
+        fprintf(stderr, "[qa_hip] error: %s%s\n", t_error,
+                t_printed + 1 == kMaxPrinted
+                    ? " (further errors of this thread are not printed)"
+                    : "");
+        ++t_printed;
     }
     t_failed = true;
+    t_call_failed = true;
 }
 
 void set_hip_error(const char* where, hipError_t e) {
     set_error(where, hipGetErrorString(e));
 }
 
-bool ok() { return !t_failed; }
+bool ok() { return !t_call_failed; }
 
 hipStream_t stream() {
-    const int d = current_device();
-    DeviceState& s = g_dev[d];
+    DeviceState& s = t_state.dev[current_device()];
     if (!s.stream) {
-        std::lock_guard<std::mutex> lk(g_init_mutex);
-        if (!s.stream) {
-            hipStream_t st = nullptr;
-            // Default priority on purpose: streams of different priorities
-            // are not used anywhere in this library.
-            hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
-            if (e != hipSuccess) {
-                set_hip_error("hipStreamCreateWithFlags", e);
-                return nullptr;
-            }
-            s.stream = st;
+        hipStream_t st = nullptr;
+        // Default priority on purpose: streams of different priorities
+        // are not used anywhere in this library.
+        hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            set_hip_error("hipStreamCreateWithFlags", e);
+            return nullptr;
         }
+        s.stream = st;
     }
     return s.stream;
 }
 
 void* scratch(int slot, size_t bytes) {
-    DeviceState& s = g_dev[current_device()];
+    DeviceState& s = t_state.dev[current_device()];
     if (bytes == 0) bytes = 256;
     if (s.cap[slot] < bytes) {
         if (s.buf[slot]) {
             // Freed only once the stream has drained (the buffer may still be
             // read by the previous call's kernels).
-            hipStreamSynchronize(stream());
+            if (s.stream) hipStreamSynchronize(s.stream);
             hipFree(s.buf[slot]);
             s.buf[slot] = nullptr;
             s.cap[slot] = 0;
@@ -95,8 +114,27 @@ void* scratch(int slot, size_t bytes) {
     return s.buf[slot];
 }
 
-AbiLock::AbiLock() { g_abi_mutex.lock(); }
-AbiLock::~AbiLock() { g_abi_mutex.unlock(); }
+AbiCall::AbiCall(void* out, size_t out_bytes) : out_(out), bytes_(out_bytes) {
+    t_call_failed = false;
+    (void)hipGetLastError();
+}
+
+AbiCall::~AbiCall() {
+    if (!t_call_failed || !out_ || bytes_ == 0) return;
+    // Device (or managed) memory is cleared through HIP; anything else is
+    // host memory the caller allocated.
+    hipPointerAttribute_t at;
+    bool device = false;
+    if (hipPointerGetAttributes(&at, out_) == hipSuccess)
+        device = at.type == hipMemoryTypeDevice ||
+                 at.type == hipMemoryTypeManaged;
+    (void)hipGetLastError();  // an unknown host pointer reports an error
+    if (device) {
+        if (hipMemset(out_, 0, bytes_) != hipSuccess) (void)hipGetLastError();
+    } else {
+        memset(out_, 0, bytes_);
+    }
+}
 
 }  // namespace qa
 
@@ -106,9 +144,11 @@ AbiLock::~AbiLock() { g_abi_mutex.unlock(); }
 // not a CPU build) is the one loaded.
 QA_API const char* qa_backend(void) { return "hip-gfx950"; }
 
-// First error recorded on the calling thread since the last qa_clear_error,
-// or NULL. Host-pointer ABI entries return void like the reference's, so
-// this is how a caller learns that a call failed.
+// Message of the most recent failure on the calling thread, or NULL when no
+// call of this thread failed since the last qa_clear_error. Host-pointer ABI
+// entries return void like the reference's, so this is how a caller learns
+// that a call failed; a failed call leaves zeros in its output, and the next
+// call runs normally whether or not the error was cleared.
 QA_API const char* qa_last_error(void) {
     return qa::t_failed ? qa::t_error : nullptr;
 }
@@ -139,10 +179,12 @@ QA_API int qa_device_arch(char* buf, int64_t len) {
     return 0;
 }
 
-// The library's stream on the current device (hipStream_t as a pointer).
+// The calling thread's library stream on the current device (hipStream_t as
+// a pointer).
 QA_API void* qa_stream(void) { return (void*)qa::stream(); }
 
-// Waits for all work the library queued on the current device.
+// Waits for all work the calling thread queued through the library on the
+// current device.
 QA_API int qa_synchronize(void) {
     hipError_t e = hipStreamSynchronize(qa::stream());
     if (e != hipSuccess) {

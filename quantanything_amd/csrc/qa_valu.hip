@@ -11,15 +11,12 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// grid: x = pixel blocks of one image, y = output channel, z = image.
+// grid: x = pixel blocks of one image, y = output channels, z = images
+// (y and z loop when Cout or N exceed the grid).
 // Element (n, c, iy, ix) of x at x + n*x_sn + c*x_sc + (iy*W + ix)*x_sp.
 template <bool WIDE>
-__global__ __launch_bounds__(kThreads) void k_conv_valu(ConvArgs a) {
-    const int co = blockIdx.y;
-    const int n = blockIdx.z;
-    const int OHW = a.OH * a.OW;
-    const int pix = blockIdx.x * kThreads + threadIdx.x;
-    if (pix >= OHW) return;
+__device__ __forceinline__ void conv_valu_one(const ConvArgs& a, int n, int co,
+                                              int pix) {
     const int oy = pix / a.OW;
     const int ox = pix - oy * a.OW;
     const int g = co / a.Cog;
@@ -71,6 +68,15 @@ __global__ __launch_bounds__(kThreads) void k_conv_valu(ConvArgs a) {
 }
 
 template <bool WIDE>
+__global__ __launch_bounds__(kThreads) void k_conv_valu(ConvArgs a) {
+    const int pix = blockIdx.x * kThreads + threadIdx.x;
+    if (pix >= a.OH * a.OW) return;
+    for (int n = blockIdx.z; n < a.N; n += gridDim.z)
+        for (int co = blockIdx.y; co < a.Cout; co += gridDim.y)
+            conv_valu_one<WIDE>(a, n, co, pix);
+}
+
+template <bool WIDE>
 __global__ __launch_bounds__(kThreads) void k_gemm_valu(
     const void* A, int a_code, const void* B, int b_code, void* C, int64_t M,
     int64_t N, int64_t K) {
@@ -97,31 +103,32 @@ __global__ __launch_bounds__(kThreads) void k_gemm_valu(
 __global__ __launch_bounds__(kThreads) void k_conv_f32(const float* x,
                                                        const float* w,
                                                        float* y, ConvArgs a) {
-    const int co = blockIdx.y;
-    const int n = blockIdx.z;
     const int OHW = a.OH * a.OW;
     const int pix = blockIdx.x * kThreads + threadIdx.x;
     if (pix >= OHW) return;
     const int oy = pix / a.OW;
     const int ox = pix - oy * a.OW;
-    const int g = co / a.Cog;
     const int64_t HW = (int64_t)a.H * a.W;
-    const float* xb = x + (int64_t)n * a.Cg * a.G * HW +
-                      (int64_t)g * a.Cg * HW;
-    const float* wb = w + (int64_t)co * a.Cg * a.KH * a.KW;
-    float acc = 0.f;
-    for (int ci = 0; ci < a.Cg; ++ci)
-        for (int ky = 0; ky < a.KH; ++ky) {
-            const int iy = oy * a.SH - a.PH + ky * a.DH;
-            if (iy < 0 || iy >= a.H) continue;
-            for (int kx = 0; kx < a.KW; ++kx) {
-                const int ix = ox * a.SW - a.PW + kx * a.DW;
-                if (ix < 0 || ix >= a.W) continue;
-                acc = fmaf(wb[(ci * a.KH + ky) * a.KW + kx],
-                           xb[ci * HW + (int64_t)iy * a.W + ix], acc);
-            }
+    for (int n = blockIdx.z; n < a.N; n += gridDim.z)
+        for (int co = blockIdx.y; co < a.Cout; co += gridDim.y) {
+            const int g = co / a.Cog;
+            const float* xb = x + (int64_t)n * a.Cg * a.G * HW +
+                              (int64_t)g * a.Cg * HW;
+            const float* wb = w + (int64_t)co * a.Cg * a.KH * a.KW;
+            float acc = 0.f;
+            for (int ci = 0; ci < a.Cg; ++ci)
+                for (int ky = 0; ky < a.KH; ++ky) {
+                    const int iy = oy * a.SH - a.PH + ky * a.DH;
+                    if (iy < 0 || iy >= a.H) continue;
+                    for (int kx = 0; kx < a.KW; ++kx) {
+                        const int ix = ox * a.SW - a.PW + kx * a.DW;
+                        if (ix < 0 || ix >= a.W) continue;
+                        acc = fmaf(wb[(ci * a.KH + ky) * a.KW + kx],
+                                   xb[ci * HW + (int64_t)iy * a.W + ix], acc);
+                    }
+                }
+            y[((int64_t)n * a.Cout + co) * OHW + pix] = acc;
         }
-    y[((int64_t)n * a.Cout + co) * OHW + pix] = acc;
 }
 
 // 16x16 output tile per 256 threads, K staged through LDS in slices of 16.
@@ -164,12 +171,9 @@ bool check(const char* what) {
 bool launch_conv_valu(const ConvArgs& a, hipStream_t st) {
     const int OHW = a.OH * a.OW;
     if (OHW <= 0 || a.N <= 0 || a.Cout <= 0) return true;
-    if (a.N > 65535 || a.Cout > 65535) {
-        set_error("launch_conv_valu", "N and Cout must be at most 65535");
-        return false;
-    }
-    dim3 grid((unsigned)ceil_div(OHW, kThreads), (unsigned)a.Cout,
-              (unsigned)a.N);
+    dim3 grid((unsigned)ceil_div(OHW, kThreads),
+              (unsigned)std::min<int64_t>(a.Cout, 65535),
+              (unsigned)std::min<int64_t>(a.N, 65535));
     if (a.wide)
         k_conv_valu<true><<<grid, kThreads, 0, st>>>(a);
     else
@@ -196,8 +200,9 @@ bool launch_conv_f32(const float* x, const float* w, float* y,
                      const ConvArgs& a, hipStream_t st) {
     const int OHW = a.OH * a.OW;
     if (OHW <= 0 || a.N <= 0 || a.Cout <= 0) return true;
-    dim3 grid((unsigned)ceil_div(OHW, kThreads), (unsigned)a.Cout,
-              (unsigned)a.N);
+    dim3 grid((unsigned)ceil_div(OHW, kThreads),
+              (unsigned)std::min<int64_t>(a.Cout, 65535),
+              (unsigned)std::min<int64_t>(a.N, 65535));
     k_conv_f32<<<grid, kThreads, 0, st>>>(x, w, y, a);
     return check("k_conv_f32");
 }

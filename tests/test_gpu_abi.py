@@ -204,3 +204,94 @@ def test_conv_workload_abi(hip, golden_workloads):
                         c["zp_out"], c["qmin"], c["qmax"], c["bias"])
     assert sha(rq) == exp["rq_sha256"]
     assert sha(hip.lut(rq, c["lut"], 0)) == exp["out_sha256"]
+
+
+# ------------------------------------------ error path under a raw loader --
+def _raw_conv(lib, x, w, y, n, c, h, w_, co, k, s, p, d, g):
+    """A conv call made exactly as the reference's loader makes it: ctypes,
+    no error check, no qa_clear_error."""
+    import ctypes
+
+    oh = (h + 2 * p - d * (k - 1) - 1) // s + 1
+    ow = (w_ + 2 * p - d * (k - 1) - 1) // s + 1
+    ptr = lambda a: ctypes.c_void_p(a.ctypes.data)  # noqa: E731
+    lib.qa_conv_i32_i16_i32(ptr(x), ptr(w), ptr(y), n, c, h, w_, co, k, k, s,
+                            s, p, p, d, d, g, oh, ow)
+    return oh, ow
+
+
+def test_failed_call_does_not_poison_later_calls(hip, golden):
+    """A host-side validation failure (groups = 0) zero-fills its output and
+    records an error; later calls on the same thread, with the error never
+    cleared, compute their full outputs (native.py:104-145 never reads the
+    error state)."""
+    import ctypes
+
+    lib = hip.library()
+    lib.qa_clear_error()
+    x = np.ones((1, 4, 5, 5), np.int32)
+    w = np.ones((3, 4, 3, 3), np.int16)
+    y = np.full((1, 3, 5, 5), 7, np.int32)
+    _raw_conv(lib, x, w, y, 1, 4, 5, 5, 3, 3, 1, 1, 1, 0)
+    first = lib.qa_last_error()
+    assert first is not None and b"geometry" in first
+    assert not y.any(), "a failed call must not leave its output unwritten"
+
+    for i in (0, 5):  # a small case and a 64-channel case
+        xi, wi, _ = conv_case_inputs(i)
+        n, c, h, w_, co, k, s, p, d, g = CONV_CASES[i]
+        oh = (h + 2 * p - d * (k - 1) - 1) // s + 1
+        ow = (w_ + 2 * p - d * (k - 1) - 1) // s + 1
+        yi = np.full((n, co, oh, ow), -1, np.int32)
+        _raw_conv(lib, np.ascontiguousarray(xi),
+                  np.ascontiguousarray(wi.astype(np.int16)), yi, *CONV_CASES[i])
+        np.testing.assert_array_equal(yi, golden[f"conv{i}_y0"])
+
+    a, b = gemm_case_inputs(0)
+    m, k = a.shape
+    n = b.shape[1]
+    a16, b16 = a.astype(np.int16), b.astype(np.int16)
+    cm = np.full((m, n), -1, np.int32)
+    lib.qa_gemm_i16_i32(m, n, k, ctypes.c_void_p(a16.ctypes.data),
+                        ctypes.c_void_p(b16.ctypes.data),
+                        ctypes.c_void_p(cm.ctypes.data))
+    np.testing.assert_array_equal(cm, golden["gemm0_c0"])
+    # the error stays readable until the caller clears it
+    assert lib.qa_last_error() is not None
+    lib.qa_clear_error()
+    assert lib.qa_last_error() is None
+
+
+@pytest.mark.parametrize("spread", [200, 600])  # MFMA path / VALU path
+def test_more_than_65535_output_channels(hip, oracle_lib, spread):
+    st = synth.Stream(7300 + spread)
+    x = st.integers(-spread // 2, spread // 2, (1, 2, 3, 3)).astype(np.int32)
+    w = st.integers(-100, 100, (70001, 2, 1, 1)).astype(np.int32)
+    args = ((1, 1), (0, 0, 0, 0), (1, 1), 1)
+    for wide in (False, True):
+        np.testing.assert_array_equal(
+            hip.conv2d_int(x, w, *args, wide=wide),
+            oracle_lib.conv2d_int(x, w, *args, wide=wide))
+
+
+@pytest.mark.parametrize("spread", [200, 600])
+def test_more_than_65535_images(hip, oracle_lib, spread):
+    st = synth.Stream(7400 + spread)
+    x = st.integers(-spread // 2, spread // 2, (70003, 1, 2, 2)).astype(
+        np.int32)
+    w = st.integers(-100, 100, (3, 1, 2, 2)).astype(np.int32)
+    args = ((1, 1), (1, 1, 1, 1), (1, 1), 1)
+    for wide in (False, True):
+        np.testing.assert_array_equal(
+            hip.conv2d_int(x, w, *args, wide=wide),
+            oracle_lib.conv2d_int(x, w, *args, wide=wide))
+
+
+@pytest.mark.parametrize("spread", [200, 600])
+def test_gemm_more_than_65535_columns(hip, spread):
+    st = synth.Stream(7500 + spread)
+    a = st.integers(-spread // 2, spread // 2, (3, 5)).astype(np.int32)
+    b = st.integers(-100, 100, (5, 70001)).astype(np.int32)
+    exact = a.astype(np.int64) @ b.astype(np.int64)
+    for wide in (False, True):
+        np.testing.assert_array_equal(hip.gemm_int(a, b, wide), exact)
