@@ -464,6 +464,25 @@ int qa_d_softmax_f32(const void* x, int in_code, int64_t rows, int64_t cols,
                      int64_t qmin, int64_t qmax, int64_t out_so,
                      float* out_f32, void* stream);
 
+/* ---------------------------------------------- allocation-free GEMM --- */
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): C[M,N] = A[M,K] B[K,N] with qa_gemm_i16_i32's semantics
+ * (int16 operands, int32 sums modulo 2^32; results bit-identical to it), on
+ * device-resident A, B, C, queued on `stream` (NULL: the null stream) with
+ * no allocation and no host synchronisation. Its working memory (activation
+ * range, int8-packed operands, correction terms, path flag) is one static
+ * device array of qa_noalloc_scratch_bytes() bytes (32 MiB) per GPU, held
+ * until the process ends; a problem needing more
+ * (qa_gemm_i16_i32_noalloc_need) is rejected with -1 and an error message
+ * before anything is queued. Every call on a GPU shares that array: calls
+ * that overlap on one GPU (other streams, other threads) race. Returns 0
+ * when queued, -1 on an error (see qa_last_error). */
+int64_t qa_noalloc_scratch_bytes(void);
+int64_t qa_gemm_i16_i32_noalloc_need(int64_t M, int64_t N, int64_t K);
+int qa_gemm_i16_i32_noalloc(int64_t M, int64_t N, int64_t K, const int16_t* A,
+                            const int16_t* B, int32_t* C, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

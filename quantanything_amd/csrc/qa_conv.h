@@ -93,6 +93,9 @@ struct ConvArgs {
     void* y2;                       // optional rescaled copy (same code)
     int64_t y2_sn, y2_sc, y2_sp;
     int64_t r2_zp_in, r2_m, r2_s, r2_zp_out, r2_qmin, r2_qmax;
+    // ---- device-side path choice (NULL: always run) ----
+    const int32_t* gate;            // the kernel runs only if *gate == gate_on
+    int32_t gate_on;
 };
 
 // Table epilogue plan for int8 outputs (device buffer written by

@@ -322,6 +322,8 @@ template <int WM, int LAYOUT, int EPI, bool KSPLIT, bool ALDS>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
     ConvArgs a) {
+    // a path chosen on the device (work-group-uniform, before any barrier)
+    if (a.gate != nullptr && *a.gate != a.gate_on) return;
     constexpr bool QUANT = EPI == Q8_TABLE || EPI == Q8_GENERAL;
     constexpr bool TABLE = EPI == Q8_TABLE;
     constexpr int KSTRIDE = KSPLIT ? 4 : 1;

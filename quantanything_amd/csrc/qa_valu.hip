@@ -79,7 +79,8 @@ __global__ __launch_bounds__(kThreads) void k_conv_valu(ConvArgs a) {
 template <bool WIDE>
 __global__ __launch_bounds__(kThreads) void k_gemm_valu(
     const void* A, int a_code, const void* B, int b_code, void* C, int64_t M,
-    int64_t N, int64_t K) {
+    int64_t N, int64_t K, const int32_t* gate, int32_t gate_on) {
+    if (gate != nullptr && *gate != gate_on) return;
     const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (j >= N) return;
     for (int64_t i = blockIdx.y; i < M; i += gridDim.y) {
@@ -183,16 +184,17 @@ bool launch_conv_valu(const ConvArgs& a, hipStream_t st) {
 
 bool launch_gemm_valu(const void* A, int a_code, const void* B, int b_code,
                       void* C, int64_t M, int64_t N, int64_t K, bool wide,
-                      hipStream_t st) {
+                      hipStream_t st, const int32_t* gate, int32_t gate_on) {
     if (M <= 0 || N <= 0) return true;
     dim3 grid((unsigned)ceil_div(N, kThreads),
               (unsigned)std::min<int64_t>(M, 65535));
     if (wide)
         k_gemm_valu<true><<<grid, kThreads, 0, st>>>(A, a_code, B, b_code, C,
-                                                     M, N, K);
+                                                     M, N, K, gate, gate_on);
     else
         k_gemm_valu<false><<<grid, kThreads, 0, st>>>(A, a_code, B, b_code,
-                                                      C, M, N, K);
+                                                      C, M, N, K, gate,
+                                                      gate_on);
     return check("k_gemm_valu");
 }
 

@@ -98,6 +98,9 @@ def _declare(lib):
         "qa_d_quantize_f32": (i32, [p, p, i32, i64, f64, i64, i64, i64, i64,
                                     p]),
         "qa_d_dequantize_f32": (i32, [p, i32, p, i64, f64, i64, i64, p]),
+        "qa_noalloc_scratch_bytes": (i64, []),
+        "qa_gemm_i16_i32_noalloc_need": (i64, [i64] * 3),
+        "qa_gemm_i16_i32_noalloc": (i32, [i64] * 3 + [p] * 4),
     }
     for name in ("qa_conv_f32", "qa_conv_i32_i16_i32", "qa_conv_i32_i32_i64"):
         sigs[name] = (None, [p, p, p] + [i64] * 16)
