@@ -266,6 +266,39 @@ typedef struct qa_nd_copy {
 } qa_nd_copy;
 int qa_d_copy_nd(const qa_nd_copy* d, void* stream);
 
+/* Integer Pad with the zero point (the reference's ShapingQuantize on a
+ * Pad node: float_ops.py:499-513 called with pad_value = input zero point,
+ * quant_layers.py:642-650). Output element (i_0, .., i_{ndim-1}) of shape
+ * `shape` (ndim <= 6) is x[i_k - lo_k] when every i_k - lo_k lies in
+ * [0, xshape_k), else `fill` (the zero point as a stored value, zp - so);
+ * element strides xs / ys; storage code 1, 2 or 4 for both. */
+typedef struct qa_nd_pad {
+    const void* x;
+    int64_t code;
+    void* y;
+    int64_t ndim, shape[6], lo[6], xshape[6], xs[6], ys[6];
+    int64_t fill;
+} qa_nd_pad;
+int qa_d_pad_nd(const qa_nd_pad* d, void* stream);
+
+/* Integer MaxPool / GlobalMaxPool over stored values (float_ops.py:518-560
+ * with pad_value = input qmin, quant_layers.py:642-650; GlobalMaxPool,
+ * float_ops.py:586-589, is the window of the whole image). y[n, c, oy, ox]
+ * = max over ky < KH, kx < KW of x[n, c, oy*SH - PT + ky*DH, ox*SW - PL +
+ * kx*DW], a tap outside the image counting as `pad` (qmin - so). The caller
+ * resolves auto_pad and ceil_mode into PT / PL and OH / OW. Element strides
+ * of x and y per axis (n, c, h, w); storage code 1, 2 or 4 for both. */
+typedef struct qa_maxpool_desc {
+    const void* x;
+    int64_t code;
+    int64_t x_sn, x_sc, x_sh, x_sw;
+    int64_t N, C, H, W, KH, KW, SH, SW, DH, DW, PT, PL, OH, OW;
+    int64_t pad;
+    void* y;
+    int64_t y_sn, y_sc, y_sh, y_sw;
+} qa_maxpool_desc;
+int qa_d_maxpool(const qa_maxpool_desc* d, void* stream);
+
 /* LayerNormalization over the last axis of [rows, cols] (row strides in
  * elements) as float_ops.py:336-347: x = (float)((q - in_zp) * in_scale),
  * float64 mean and variance, y = (x - mean) / sqrt(var + eps) * gamma

@@ -77,6 +77,34 @@ def layer_norm(x, gamma, beta, axis, eps):
     return _f32(y + beta if beta is not None else y)
 
 
+def pool_pads(node, in_hw, kernel, strides, dilations):
+    """``(top, left, bottom, right)`` of a pooling window: ``auto_pad``
+    (SAME_UPPER / SAME_LOWER / VALID) or ``pads`` as the reference resolves
+    them (``float_ops.py:132-146``), then, under ``ceil_mode``, the end pads
+    grown so that the last partial window is included (``:518-531``)."""
+    auto = node.attr("auto_pad", "NOTSET")
+    if auto in ("SAME_UPPER", "SAME_LOWER"):
+        lo, hi = [], []
+        for size, k, s, d in zip(in_hw, kernel, strides, dilations):
+            out = -(-size // s)
+            total = max((out - 1) * s + d * (k - 1) + 1 - size, 0)
+            small, big = total // 2, total - total // 2
+            lo.append(small if auto == "SAME_UPPER" else big)
+            hi.append(big if auto == "SAME_UPPER" else small)
+        pads = [lo[0], lo[1], hi[0], hi[1]]
+    elif auto == "VALID":
+        pads = [0, 0, 0, 0]
+    else:
+        pads = list(node.attr("pads", [0, 0, 0, 0]))
+    if node.attr("ceil_mode", 0):
+        for ax in range(2):
+            size = in_hw[ax] + pads[ax] + pads[ax + 2]
+            ek = dilations[ax] * (kernel[ax] - 1) + 1
+            out = -(-(size - ek) // strides[ax]) + 1
+            pads[ax + 2] += max((out - 1) * strides[ax] + ek - size, 0)
+    return tuple(pads)
+
+
 def eval_node(node, args, opset=13, pad_value=None):
     """Evaluates one node on NumPy arrays; returns the list of outputs."""
     op = node.op_type
@@ -170,14 +198,22 @@ def eval_node(node, args, opset=13, pad_value=None):
         return [np.pad(x, [(pads[i], pads[i + n]) for i in range(n)],
                        constant_values=value)]
     if op == "MaxPool":
+        # float_ops.py:518-560: pads from auto_pad / pads, the end pads
+        # grown under ceil_mode, then the max over dilated windows
         x = args[0]
         k = tuple(node.attr("kernel_shape"))
-        s = tuple(node.attr("strides", [1, 1]))
-        p = node.attr("pads", [0, 0, 0, 0])
+        s = tuple(node.attr("strides", [1] * len(k)))
+        d = tuple(node.attr("dilations", [1] * len(k)))
+        p = list(pool_pads(node, x.shape[2:], k, s, d))
         value = pad_value if pad_value is not None else (
             -np.inf if x.dtype.kind == "f" else np.iinfo(x.dtype).min)
         xp = np.pad(x, ((0, 0), (0, 0), (p[0], p[2]), (p[1], p[3])),
                     constant_values=value)
-        win = sliding_window_view(xp, k, axis=(2, 3))[:, :, ::s[0], ::s[1]]
+        ek = tuple(dd * (kk - 1) + 1 for kk, dd in zip(k, d))
+        win = sliding_window_view(xp, ek, axis=(2, 3))
+        win = win[:, :, ::s[0], ::s[1], ::d[0], ::d[1]]
         return [win.max(axis=(4, 5))]
+    if op == "GlobalMaxPool":  # float_ops.py:586-589
+        x = args[0]
+        return [x.max(axis=tuple(range(2, x.ndim)), keepdims=True)]
     raise NotImplementedError(f"oracle has no float semantics for {op}")

@@ -31,7 +31,7 @@ import ctypes
 import numpy as np
 import torch
 
-from quantanything_amd import native
+from quantanything_amd import float_ops, native
 
 _I64 = ctypes.c_int64
 _P = ctypes.c_void_p
@@ -212,6 +212,27 @@ class NdCopy(ctypes.Structure):
                    ("out_scale", ctypes.c_double)])
 
 
+class PadDesc(ctypes.Structure):
+    """``qa_nd_pad`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("x", _P), ("code", _I64), ("y", _P), ("ndim", _I64)]
+                + [(n, _I64 * 6) for n in ("shape", "lo", "xshape", "xs",
+                                           "ys")]
+                + [("fill", _I64)])
+
+
+class MaxPoolDesc(ctypes.Structure):
+    """``qa_maxpool_desc`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("x", _P)]
+                + [(n, _I64) for n in ("code", "x_sn", "x_sc", "x_sh", "x_sw",
+                                       "N", "C", "H", "W", "KH", "KW", "SH",
+                                       "SW", "DH", "DW", "PT", "PL", "OH",
+                                       "OW", "pad")]
+                + [("y", _P)]
+                + [(n, _I64) for n in ("y_sn", "y_sc", "y_sh", "y_sw")])
+
+
 class MatmulDesc(ctypes.Structure):
     """``qa_matmul_desc`` of ``include/qa_hip.h``."""
 
@@ -336,7 +357,9 @@ class DeviceExecutor:
     def _new(self, shape, qp, dense=False):
         """Fresh channels-last (4-D, unless ``dense``) or row-major tensor
         (``dense``: row-major in the logical order, for the N-D operators
-        of transformers)."""
+        of transformers). Buffers start zeroed once, at planning: no kernel
+        writes the padding channels of a channels-last pixel, and the int8
+        MFMA path's pixel sums (weight rows with an offset) read them."""
         shape = tuple(int(s) for s in shape)
         if len(shape) == 4 and not dense:
             n, c, h, w = shape
@@ -347,18 +370,18 @@ class DeviceExecutor:
             else:
                 cs = c
             numel = n * h * w * cs
-            buf = torch.empty(numel + TAIL, dtype=self.dtype, device="cuda")
+            buf = torch.zeros(numel + TAIL, dtype=self.dtype, device="cuda")
             return DeviceTensor(buf, 0, shape, h * w * cs, 1, cs, self.code,
                                 self.so, qp)
         if len(shape) == 2 and not dense:
             numel = shape[0] * shape[1]
-            buf = torch.empty(numel + TAIL, dtype=self.dtype, device="cuda")
+            buf = torch.zeros(numel + TAIL, dtype=self.dtype, device="cuda")
             return DeviceTensor(buf, 0, shape, shape[1], 1, 0, self.code,
                                 self.so, qp)
         if not 1 <= len(shape) <= 6:
             raise NotImplementedError(f"{len(shape)}-D tensors on the device")
         numel = int(np.prod(shape, dtype=np.int64))
-        buf = torch.empty(numel + TAIL, dtype=self.dtype, device="cuda")
+        buf = torch.zeros(numel + TAIL, dtype=self.dtype, device="cuda")
         strides = tuple(int(np.prod(shape[k + 1:], dtype=np.int64))
                         for k in range(len(shape)))
         return DeviceTensor.nd(buf, 0, shape, strides, self.code, self.so, qp)
@@ -1143,9 +1166,69 @@ class DeviceExecutor:
                 and layer.node.attr("axis", 1) == 1 and x.pixels == 1:
             return [DeviceTensor(x.buf, x.offset, (x.shape[0], x.channels),
                                  x.sn, x.sc, 0, x.code, x.so, x.qp)]
-        if op in ("Pad", "MaxPool", "GlobalMaxPool"):
-            raise NotImplementedError(f"{op} on the device")
+        if op == "Pad":
+            return self._plan_pad(layer, x)
+        if op in ("MaxPool", "GlobalMaxPool"):
+            return self._plan_maxpool(layer, x)
         return self._plan_shape_nd(layer, x)
+
+    def _plan_pad(self, layer, x):
+        """Pad with the input zero point (constant mode; any rank <= 6)."""
+        node = layer.node
+        nd = len(x.shape)
+        pads = self._const_list(node, 1, "pads")
+        if pads is None or len(pads) != 2 * nd:
+            raise NotImplementedError("Pad without 2 * rank constant pads")
+        if min(pads) < 0:
+            raise NotImplementedError("Pad with negative pads (cropping)")
+        shape = tuple(x.shape[k] + pads[k] + pads[k + nd] for k in range(nd))
+        iq = layer.in_qp[0]
+        y = self._new(shape, layer.out_qp[0])
+        d = PadDesc()
+        d.x, d.code, d.y, d.ndim = x.ptr, x.code, y.ptr, nd
+        for k in range(nd):
+            d.shape[k], d.lo[k], d.xshape[k] = shape[k], pads[k], x.shape[k]
+            d.xs[k], d.ys[k] = x.nd_strides[k], y.nd_strides[k]
+        d.fill = int(iq.zp) - x.so
+        self.keep.extend([x.buf, y.buf, d])
+        self._add(f"pad:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_pad_nd(ctypes.byref(d), s), "qa_d_pad_nd"))
+        return [y]
+
+    def _plan_maxpool(self, layer, x):
+        """MaxPool with the input qmin as padding value (auto_pad, ceil_mode
+        and dilations resolved on the host); GlobalMaxPool as the window of
+        the whole image."""
+        node = layer.node
+        if len(x.shape) != 4:
+            raise NotImplementedError(f"{node.op_type} of a "
+                                      f"{len(x.shape)}-D tensor")
+        n, c, h, w = x.shape
+        if node.op_type == "GlobalMaxPool":
+            k, s, dl, p = (h, w), (1, 1), (1, 1), (0, 0, 0, 0)
+        else:
+            k, s, dl, p = float_ops.pool_geometry(node, (h, w))
+            if len(k) != 2:
+                raise NotImplementedError("MaxPool that is not 2-D")
+        oh = (h + p[0] + p[2] - (dl[0] * (k[0] - 1) + 1)) // s[0] + 1
+        ow = (w + p[1] + p[3] - (dl[1] * (k[1] - 1) + 1)) // s[1] + 1
+        if oh < 1 or ow < 1:
+            raise NotImplementedError("MaxPool window larger than the input")
+        iq = layer.in_qp[0]
+        y = self._new((n, c, oh, ow), layer.out_qp[0])
+        d = MaxPoolDesc()
+        d.x, d.code, d.y = x.ptr, x.code, y.ptr
+        d.x_sn, d.x_sc, d.x_sh, d.x_sw = x.nd_strides
+        d.y_sn, d.y_sc, d.y_sh, d.y_sw = y.nd_strides
+        d.N, d.C, d.H, d.W, d.OH, d.OW = n, c, h, w, oh, ow
+        d.KH, d.KW, d.SH, d.SW, d.DH, d.DW = k[0], k[1], s[0], s[1], dl[0], \
+            dl[1]
+        d.PT, d.PL = p[0], p[1]
+        d.pad = int(iq.qmin) - x.so
+        self.keep.extend([x.buf, y.buf, d])
+        self._add(f"maxpool:{layer.name}", lambda s_: _ok(
+            self.lib.qa_d_maxpool(ctypes.byref(d), s_), "qa_d_maxpool"))
+        return [y]
 
     def _plan_fallback(self, layer, ins):
         op = layer.node.op_type

@@ -404,19 +404,28 @@ def _pad(node, ins, opset, pad_value=None, **kw):
     return np.pad(x, width, mode="constant", constant_values=pad_value)
 
 
-@_reg("MaxPool")
-def _maxpool(node, ins, opset, pad_value=None, **kw):
-    x = ins[0]
+def pool_geometry(node, in_hw):
+    """``(kernel, strides, dilations, (top, left, bottom, right))`` of a 2-D
+    pooling node: pads from ``auto_pad`` / ``pads``, then the end pads grown
+    under ``ceil_mode`` so the last partial window is included
+    (``float_ops.py:518-531``)."""
     kernel = tuple(node.attr("kernel_shape"))
     strides = tuple(node.attr("strides", [1] * len(kernel)))
     dil = tuple(node.attr("dilations", [1] * len(kernel)))
-    pads = list(conv_pads(node, x.shape[2:], kernel, strides, dil))
+    pads = list(conv_pads(node, in_hw, kernel, strides, dil))
     if node.attr("ceil_mode", 0):
         for ax in range(2):
-            size = x.shape[2 + ax] + pads[ax] + pads[ax + 2]
+            size = in_hw[ax] + pads[ax] + pads[ax + 2]
             ek = dil[ax] * (kernel[ax] - 1) + 1
             out = -(-(size - ek) // strides[ax]) + 1
             pads[ax + 2] += max((out - 1) * strides[ax] + ek - size, 0)
+    return kernel, strides, dil, tuple(pads)
+
+
+@_reg("MaxPool")
+def _maxpool(node, ins, opset, pad_value=None, **kw):
+    x = ins[0]
+    kernel, strides, dil, pads = pool_geometry(node, x.shape[2:])
     if pad_value is None:
         pad_value = (-np.inf if np.issubdtype(x.dtype, np.floating)
                      else np.iinfo(x.dtype).min)

@@ -217,6 +217,41 @@ def mini_yolo(seed=0, size=32, classes=10, width=8, softmax=True):
     return b.build(x, [None, 3, size, size], y)
 
 
+def mini_sppf(seed=0, size=32, width=16, classes=10):
+    """Pooling and padding operators in a small conv net: a YOLOv8 SPPF
+    block (1x1 conv, three chained 5x5 stride-1 MaxPools, Concat of the
+    four, 1x1 conv), an explicit zero Pad of H / W and channels before an
+    unpadded conv, a dilated ceil-mode MaxPool, a SAME_LOWER MaxPool,
+    GlobalMaxPool, Flatten, a Pad of the [N, F] features and a Gemm.
+    Outputs: the logits and the SPPF result (a 4-D tensor)."""
+    b = GraphBuilder(seed)
+    x = "images"
+    y = b.silu(b.conv(x, 3, width, 3, stride=2))
+    c = width // 2
+    t = b.silu(b.conv(y, width, c, 1))
+    p1 = b.op("MaxPool", [t], kernel_shape=[5, 5], strides=[1, 1],
+              pads=[2, 2, 2, 2])
+    p2 = b.op("MaxPool", [p1], kernel_shape=[5, 5], strides=[1, 1],
+              pads=[2, 2, 2, 2])
+    p3 = b.op("MaxPool", [p2], kernel_shape=[5, 5], strides=[1, 1],
+              pads=[2, 2, 2, 2])
+    sppf = b.silu(b.conv(b.op("Concat", [t, p1, p2, p3], axis=1), 4 * c,
+                         width, 1))
+    y = b.op("Pad", [sppf, b.const(np.array([0, 2, 1, 2, 0, 1, 2, 1],
+                                            np.int64))], mode="constant")
+    y = b.silu(b.conv(y, width + 3, width, 3, pad=0))
+    y = b.op("MaxPool", [y], kernel_shape=[3, 3], strides=[2, 2],
+             pads=[1, 0, 1, 1], dilations=[2, 1], ceil_mode=1)
+    y = b.op("MaxPool", [y], kernel_shape=[2, 3], strides=[2, 2],
+             auto_pad="SAME_LOWER")
+    y = b.op("GlobalMaxPool", [y])
+    y = b.op("Flatten", [y], axis=1)
+    y = b.op("Pad", [y, b.const(np.array([0, 3, 0, 2], np.int64))])
+    y = b.op("Gemm", [y, b.weight(classes, width + 5),
+                      b.weight(classes, scale=0.1)], transB=1)
+    return b.build(x, [None, 3, size, size], [y, sppf])
+
+
 def yolov8n_cls(seed=3, classes=1000, size=224, softmax=True):
     """YOLOv8n-cls-shaped network with BatchNorm folded into the convs:
     Conv-SiLU stem (3->16, s2), 3x3 stride-2 downsamples to 32/64/128/256
