@@ -334,6 +334,12 @@ class OraclePipeline:
             s, z, lo, hi = self.qp[name]
             env[name] = self.lib.quantize_f32(np.asarray(v, np.float32), s, z,
                                               lo, hi)
+        return self.run_integers(env, keep, overrides)
+
+    def run_integers(self, env, keep=False, overrides=None):
+        """:meth:`run` from already quantized graph inputs ``{name: int32
+        array}``."""
+        env = {k: np.asarray(v, np.int32) for k, v in env.items()}
         self.computed = {}
         for st in self.plan:
             args = [env[n] if n in env else self._const(n) for n in st["ins"]]
