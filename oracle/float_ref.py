@@ -213,6 +213,12 @@ def eval_node(node, args, opset=13, pad_value=None):
         win = sliding_window_view(xp, ek, axis=(2, 3))
         win = win[:, :, ::s[0], ::s[1], ::d[0], ::d[1]]
         return [win.max(axis=(4, 5))]
+    if op == "BatchNormalization":  # float_ops.py:200-206, float32
+        x, gamma, beta, mean, var = args[:5]
+        shape = [1, -1] + [1] * (x.ndim - 2)
+        a = gamma / np.sqrt(var + node.attr("epsilon", 1e-5))
+        b = beta - a * mean
+        return [_f32(x * a.reshape(shape) + b.reshape(shape))]
     if op == "GlobalMaxPool":  # float_ops.py:586-589
         x = args[0]
         return [x.max(axis=tuple(range(2, x.ndim)), keepdims=True)]

@@ -183,12 +183,19 @@ class OraclePipeline:
             lo, hi = ((-(1 << 63), (1 << 63) - 1) if bits > 8 else INT32)
             bias_int = np.clip(np.round(bias / (in_scale * sc)), lo, hi
                                ).astype(np.int64)
+        # fake quantization (quant_layers.py:264-279): dequantized weights,
+        # the integer bias back on the float grid
+        fake_w = ((wq.astype(np.int64) - zp.reshape(shape)) *
+                  sc.reshape(shape)).astype(np.float32)
+        fake_b = (None if bias_int is None else
+                  (bias_int * (in_scale * sc)).astype(np.float32))
         pairs = [multiplier(v) for v in in_scale * sc / out_scale]
         mult = np.array([p[0] for p in pairs], dtype=np.int64)
         shift = np.array([p[1] for p in pairs], dtype=np.int64)
         if not self.per_channel:
             mult, shift = mult[:1], shift[:1]
-        return dict(wc=wc, wide=wide, bias=bias_int, mult=mult, shift=shift)
+        return dict(wc=wc, wide=wide, bias=bias_int, mult=mult, shift=shift,
+                    fake_w=fake_w, fake_b=fake_b)
 
     def _prepare(self, node):
         kind = self._kind(node)
@@ -356,6 +363,60 @@ class OraclePipeline:
         floats = [self.lib.dequantize_f32(env[o], *self.qp[o][:2])
                   for o in self.g.outputs]
         return ints, floats
+
+    # ------------------------------------------------ fake quantization --
+    def _fq(self, x, qp):
+        s, z, lo, hi = qp
+        return self.lib.dequantize_f32(
+            self.lib.quantize_f32(np.asarray(x, np.float32), s, z, lo, hi),
+            s, z)
+
+    def fake_step(self, st, args):
+        """One layer of the fake-quantized pass (``quant_layers.py:178-193``;
+        Conv :311-318 and Gemm :376-382 with dequantized weights and the
+        bias on the float grid; shaping ops :638-640 without output
+        quantization) on float inputs ``args`` (constants given as
+        floats)."""
+        node, kind = st["node"], st["kind"]
+        xs = [self._fq(a, q) for a, q in zip(args, st["in_qp"])]
+        if kind == "conv":
+            x = xs[0]
+            strides = tuple(node.attr("strides", [1, 1]))
+            dil = tuple(node.attr("dilations", [1, 1]))
+            p = node.attr("pads", [0, 0, 0, 0])
+            y = self.lib.conv2d_f32(x, st["fake_w"], strides, tuple(p), dil,
+                                    node.attr("group", 1))
+            if st["fake_b"] is not None:
+                y = y + st["fake_b"].reshape(1, -1, 1, 1)
+            outs = [y]
+        elif kind == "gemm":
+            x = xs[0]
+            y = self.lib.gemm_f32(x.reshape(-1, x.shape[-1]), st["fake_w"])
+            if st["fake_b"] is not None:
+                y = y + st["fake_b"]
+            n = st["fake_w"].shape[1]
+            outs = [y.reshape((x.shape[0], n) if node.op_type == "Gemm"
+                              else x.shape[:-1] + (n,))]
+        else:
+            data = dict(zip(st["ins"], xs))
+            full = [None if not n else data[n] if n in data
+                    else self.g.initializers[n] for n in node.inputs]
+            outs = eval_node(node, full, self.g.opset)
+            if kind == "shape":
+                return outs
+        return [self._fq(o, q) for o, q in zip(outs, st["out_qp"])]
+
+    def run_fake(self, x):
+        """The fake-quantized pass (``quant_container.py:150-160``):
+        ``{tensor: float32}`` for every tensor of the pass."""
+        feeds = x if isinstance(x, dict) else {self.g.input_names[0]: x}
+        env = {k: self._fq(v, self.qp[k]) for k, v in feeds.items()}
+        for st in self.plan:
+            args = [env[n] if n in env else
+                    self.g.initializers[n].astype(np.float32)
+                    for n in st["ins"]]
+            env.update(zip(st["node"].outputs, self.fake_step(st, args)))
+        return env
 
     def _const(self, name):
         v = self.g.initializers[name].astype(np.float32)

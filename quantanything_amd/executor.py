@@ -335,7 +335,7 @@ class DeviceExecutor:
         self.lib = native.require()
         self.c = container
         self.graph = container.graph
-        bits, signed = container.layers[0].num_bits, \
+        bits, signed = container.layers[0].bits, \
             container.layers[0].signed
         self.code, self.dtype, self.so = storage_of(bits, signed)
         self.launches = []  # (name, fn(stream))
@@ -497,7 +497,7 @@ class DeviceExecutor:
                 out_name = layer.node.outputs[0]
                 users = cons.get(out_name, [])
                 if out_name not in g.outputs and len(users) == 1 and \
-                        users[0].kind == "lut":
+                        users[0].kind == "table":
                     lut_layer = users[0]
                     out_name = lut_layer.node.outputs[0]
                     users = cons.get(out_name, [])
@@ -891,7 +891,7 @@ class DeviceExecutor:
             self.tensors.pop(mids[0], None)  # never materialized
 
     # ------------------------------------------------------- element-wise --
-    def _plan_lut(self, layer, ins):
+    def _plan_table(self, layer, ins):
         x = ins[0]
         p = self._params(layer)
         if "lut" not in p:
@@ -1230,7 +1230,7 @@ class DeviceExecutor:
             self.lib.qa_d_maxpool(ctypes.byref(d), s_), "qa_d_maxpool"))
         return [y]
 
-    def _plan_fallback(self, layer, ins):
+    def _plan_float(self, layer, ins):
         op = layer.node.op_type
         x = ins[0]
         if op == "Softmax":
