@@ -18,8 +18,17 @@ The JSON line also carries
   HIP events on the launch stream;
 * ``kernels``: the standalone fused qGEMM (M=4096 K=576 N=64) and qconv
   (b32 64->64 3x3 56x56) launches with their int8 TOPS vs MFMA peak;
-* ``cpu_baseline``: the same pipeline on the host cores with the reference's
-  own compiled kernels (OpenMP), on a bounded sample.
+* ``cpu_baseline``: the same pass on the host's physical cores with the
+  reference's own compiled kernels (OpenMP, threads bound to cores), the
+  median of ten timed passes after three untimed ones; ``cpu_baselines``
+  adds the standalone GEMM and conv at the ABI level, the int16 and ViT-S
+  passes on samples, and single-thread rows;
+* the standalone requantize and SiLU-table kernels over the conv's 6.42 M
+  outputs, in HBM GB/s.
+
+Tile codes of the convolutions come from the committed
+``profiles/yolov8n_cls_b64_int8_tiles.json`` (the set the committed counter
+profile measured) unless ``--retune`` times them again.
 """
 
 import argparse
@@ -28,10 +37,17 @@ import os
 import sys
 import time
 
-import numpy as np
+# CPU baseline threads: bound to the physical cores (read by the OpenMP
+# runtime when it starts, so set before anything loads it)
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+
+import numpy as np  # noqa: E402
 
 PEAK_I8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, GB/s
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TILES = os.path.join(ROOT, "profiles", "yolov8n_cls_b64_int8_tiles.json")
 
 
 def parse():
@@ -40,8 +56,6 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--batch", type=int, default=64)
-    p.add_argument("--cpu-seconds", type=float, default=12.0,
-                   help="lower bound of the CPU-baseline sample duration")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--profile-only", action="store_true",
                    help="skip the CPU baseline and the correctness gate")
@@ -51,9 +65,13 @@ def parse():
     p.add_argument("--no-tune", action="store_true",
                    help="keep the library's own conv tiling (no plan-time "
                         "timing of the tile variants)")
-    p.add_argument("--tiles", metavar="JSON",
+    p.add_argument("--tiles", metavar="JSON", default=TILES,
                    help="fixed tile codes instead of timing them: a bench "
-                        "line's \"tiles\" object, or that object alone")
+                        "line's \"tiles\" object, or that object alone "
+                        "(default: the committed set, when present)")
+    p.add_argument("--retune", action="store_true",
+                   help="time the tile variants of every convolution "
+                        "instead of using the committed set")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the ViT-S and int16 YOLOv8n-cls passes")
     p.add_argument("--only", choices=("vit", "int16"),
@@ -143,7 +161,7 @@ def measure_pass(name, g, quant_type, batch, steps, tune, torch):
             "images_per_s": round(batch / dt, 1),
             "ms_per_step": round(dt * 1e3, 4), "steps": steps,
             "launches_per_step": len(ex.launches),
-            "params": g.num_params()}
+            "params": g.num_params()}, c
 
 
 def main():
@@ -153,25 +171,36 @@ def main():
               "build measures the single-GPU path; the multi-GPU sharding is "
               "a design note.", file=sys.stderr)
         return 2
+    if not (args.no_cpu or args.profile_only):
+        from oracle import cpu_baseline
+
+        # counted before an OpenMP runtime pins this thread to one core
+        cpu_baseline.physical_cores()
     import torch
 
     from quantanything_amd import graph as G
     from quantanything_amd import native
     from quantanything_amd.container import QuantContainer
     from quantanything_amd.synth import Stream
-    from quantanything_amd.workloads import ConvWorkload, GemmWorkload
+    from quantanything_amd import synth
+    from quantanything_amd.workloads import (
+        ConvWorkload,
+        GemmWorkload,
+        LutWorkload,
+        RequantizeWorkload,
+    )
 
     native.require()
     B = args.batch
     if args.only:
         if args.only == "vit":
-            rec = measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",
-                               G.vit(seed=5, batch=32), "int8", 32,
-                               args.steps, not args.no_tune, torch)
+            rec, _ = measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",
+                                  G.vit(seed=5, batch=32), "int8", 32,
+                                  args.steps, not args.no_tune, torch)
         else:
-            rec = measure_pass("YOLOv8n-cls int16 (wide accumulation)",
-                               G.yolov8n_cls(seed=3), "int16", B, args.steps,
-                               not args.no_tune, torch)
+            rec, _ = measure_pass("YOLOv8n-cls int16 (wide accumulation)",
+                                  G.yolov8n_cls(seed=3), "int16", B,
+                                  args.steps, not args.no_tune, torch)
         print(json.dumps(rec))
         return 0
     g = G.yolov8n_cls(seed=3)
@@ -183,7 +212,9 @@ def main():
     ex.launch()
     torch.cuda.synchronize()
     tiles = {}
-    if args.tiles:  # a recorded choice (reproducible profiles)
+    if args.retune:
+        args.tiles = None
+    if args.tiles and os.path.exists(args.tiles):  # a recorded choice
         with open(args.tiles) as f:
             fixed = json.load(f)
         fixed = fixed.get("tiles", fixed)
@@ -200,50 +231,53 @@ def main():
 
     # ---- correctness gate + CPU baseline (reference kernels on the host) --
     cpu = None
+    cpu_rows = []
     gate = None
+    qdir = None
     if not args.profile_only:
         import tempfile
 
-        from oracle import abi
+        from oracle import cpu_baseline
         from oracle.pipeline import OraclePipeline
 
+        cores = cpu_baseline.physical_cores()
         soft = g.nodes[-1]
         logits_name = soft.inputs[0]
-        with tempfile.TemporaryDirectory() as td:
-            qpath = os.path.join(td, "q.json")
-            c.save(qpath)
-            kind = "reference" if abi.ref_available() else "port"
-            lib = "ref" if kind == "reference" else "oracle"
-            cores = len(os.sched_getaffinity(0))
-            abi.load(lib).set_num_threads(cores)
-            gl = G.yolov8n_cls(seed=3, softmax=False)
-            n_gate = min(4, B)
-            ints, _ = OraclePipeline(gl, qpath, lib=lib).run(x[:n_gate])
-            dev_logits = ex.tensors[logits_name].to_host()[:n_gate]
-            exact = bool(np.array_equal(dev_logits, ints[gl.outputs[0]]))
-            full = OraclePipeline(g, qpath, lib=lib)
-            t0 = time.perf_counter()
-            ref_out, _ = full.run(x)
-            passes = 1
-            while time.perf_counter() - t0 < args.cpu_seconds and \
-                    not args.no_cpu:
-                full.run(x)
-                passes += 1
-            cpu_s = time.perf_counter() - t0
-            dev_out = ex.tensors[g.outputs[0]].to_host()
-            soft_diff = int(np.abs(dev_out.astype(np.int64)
-                                   - ref_out[g.outputs[0]]).max())
-            gate = {"logits_bit_exact": exact, "images_checked": n_gate,
-                    "softmax_max_step_diff": soft_diff}
-            if not exact or soft_diff > 1:
-                print(json.dumps({"error": "correctness gate failed",
-                                  "gate": gate}))
-                return 1
-            cpu = {"value": round(passes * B / cpu_s, 2), "unit": "images/s",
-                   "cores": cores, "kind": kind,
-                   "sample": f"{passes} pass(es) over the batch-{B} input "
-                             f"({passes * B} images) with the reference's "
-                             "compiled kernels, OpenMP"}
+        qdir = tempfile.TemporaryDirectory()
+        qpath = os.path.join(qdir.name, "q.json")
+        c.save(qpath)
+        lib_kind = "ref" if cpu_baseline.abi.ref_available() else "oracle"
+        cpu_baseline.abi.load(lib_kind).set_num_threads(cores)
+        gl = G.yolov8n_cls(seed=3, softmax=False)
+        n_gate = min(4, B)
+        ints, _ = OraclePipeline(gl, qpath, lib=lib_kind).run(x[:n_gate])
+        dev_logits = ex.tensors[logits_name].to_host()[:n_gate]
+        exact = bool(np.array_equal(dev_logits, ints[gl.outputs[0]]))
+        ref_out, _ = OraclePipeline(g, qpath, lib=lib_kind).run(x)
+        dev_out = ex.tensors[g.outputs[0]].to_host()
+        soft_diff = int(np.abs(dev_out.astype(np.int64)
+                               - ref_out[g.outputs[0]]).max())
+        gate = {"logits_bit_exact": exact, "images_checked": n_gate,
+                "softmax_max_step_diff": soft_diff}
+        if not exact or soft_diff > 1:
+            print(json.dumps({"error": "correctness gate failed",
+                              "gate": gate}))
+            return 1
+        if not args.no_cpu:
+            name = f"YOLOv8n-cls int8 b{B} (integer pass)"
+            head = cpu_baseline.pipeline_rows(name, g, qpath, x, [cores])[0]
+            cpu = {k: head[k] for k in ("value", "unit", "cores", "kind")}
+            cpu["sample"] = (f"{head['runs']} timed passes over the batch-{B} "
+                             "input after 3 untimed, median; the reference's "
+                             "compiled kernels, OpenMP threads bound to the "
+                             "physical cores")
+            cpu_rows.append(head)
+            cpu_rows += cpu_baseline.pipeline_rows(
+                "YOLOv8n-cls int8 (integer pass)", g, qpath, x[:4], [1])
+            cpu_rows += cpu_baseline.gemm_rows(synth.gemm_workload(),
+                                               [cores, 1])
+            cpu_rows += cpu_baseline.conv_rows(synth.conv_workload(),
+                                               [cores, 1])
 
     # ---- timed region: captured graph replays ----------------------------
     step = ex.launch if args.eager else ex.replay
@@ -359,16 +393,43 @@ def main():
                         "frac_of_mfma_peak": round(tops / PEAK_I8_TOPS, 4),
                         "roofline": r})
 
+    for wl in (RequantizeWorkload(), LutWorkload()):
+        kms = time_launch(wl.launch, 50, torch)
+        gbs = wl.bytes / (kms * 1e-3) / 1e9
+        kernels.append({"workload": wl.name, "avg_ms": round(kms, 5),
+                        "bytes_per_launch": wl.bytes,
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                     "traffic": None}})
+
     # ---- the other end-to-end configurations (parity: tests/) ------------
     extra = []
     if not args.no_extra and not args.profile_only:
         steps = max(5, min(args.steps, 50))
-        extra.append(measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",
-                                  G.vit(seed=5, batch=32), "int8", 32, steps,
-                                  not args.no_tune, torch))
-        extra.append(measure_pass("YOLOv8n-cls int16 (wide accumulation)",
-                                  G.yolov8n_cls(seed=3), "int16", B, steps,
-                                  not args.no_tune, torch))
+        rec, cv = measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",
+                               G.vit(seed=5, batch=32), "int8", 32, steps,
+                               not args.no_tune, torch)
+        extra.append(rec)
+        rec, c16 = measure_pass("YOLOv8n-cls int16 (wide accumulation)",
+                                G.yolov8n_cls(seed=3), "int16", B, steps,
+                                not args.no_tune, torch)
+        extra.append(rec)
+        if qdir is not None and not args.no_cpu:
+            from oracle import cpu_baseline
+
+            cores = cpu_baseline.physical_cores()
+            p16 = os.path.join(qdir.name, "q16.json")
+            c16.save(p16)
+            cpu_rows += cpu_baseline.pipeline_rows(
+                "YOLOv8n-cls int16 (integer pass, int64 accumulation)", g,
+                p16, x[:8], [cores])
+            pv = os.path.join(qdir.name, "qvit.json")
+            cv.save(pv)
+            xv = Stream(5).normal((2, 3, 224, 224)).astype(np.float32)
+            cpu_rows += cpu_baseline.pipeline_rows(
+                "ViT-S/16 int8 (integer pass, float fallbacks)",
+                G.vit(seed=5, batch=2), pv, xv, [cores])
 
     line = {
         "metric": "int8 YOLOv8n-cls images/s (b=64) + qGEMM TOPS as % of "
@@ -390,6 +451,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "cpu_baselines": cpu_rows,
         "kernels": kernels,
         "other_configs": extra,
         "gate": gate,

@@ -41,6 +41,134 @@ __global__ __launch_bounds__(kThreads) void k_requant(
     }
 }
 
+// Requantize of int32 accumulators to int8 storage, [outer, C, inner]
+// view with inner % 16 == 0: 16 consecutive accumulators (one row, so one
+// channel) per thread, all four 16-byte loads issued before any arithmetic.
+// With x = acc - sub + pre[c] in int32 and |m| < 2^31, 1 <= 31 + s <= 62,
+// mbqm is one 64-bit multiply-add and an arithmetic shift:
+// (x*m + 2^(t-1)) >> t, t = 31 + s (|x*m| < 2^62, no overflow); any other
+// element takes the 128-bit form. Both clip in 64 bits.
+__device__ __forceinline__ int64_t requant_elem(int64_t x, int64_t m,
+                                                int64_t s, bool fast32,
+                                                int64_t rnd, int64_t qb,
+                                                int64_t lo, int64_t hi) {
+    int64_t q;
+    if (fast32 && x == (int64_t)(int32_t)x)
+        q = ((int64_t)(int32_t)x * (int32_t)m + rnd) >> (31 + s);
+    else
+        q = qa_clip128(qa_mbqm_fast(x, m, s), -((int64_t)1 << 62),
+                       (int64_t)1 << 62);
+    q += qb;
+    return q < lo ? lo : (q > hi ? hi : q);
+}
+
+__global__ __launch_bounds__(kThreads) void k_requant_v16_i32_i8(
+    const int4* __restrict__ acc, int4* __restrict__ out, int64_t n16,
+    uint32_t C, uint32_t inner16, const int64_t* __restrict__ mult,
+    const int64_t* __restrict__ shift, const int64_t* __restrict__ pre,
+    const int64_t* __restrict__ post, int64_t zp, int64_t qmin, int64_t qmax,
+    int64_t sub, int64_t out_so) {
+    const int64_t lo = qmin - out_so, hi = qmax - out_so;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n16;
+         i += (int64_t)gridDim.x * kThreads) {
+        int4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = acc[i * 4 + k];
+        const uint32_t c = (uint32_t)((uint64_t)i / inner16) % C;
+        const int64_t m = mult[c], s = shift[c];
+        const int64_t pb = (pre ? pre[c] : 0) - sub;
+        const int64_t qb = (post ? post[c] : 0) + zp - out_so;
+        const int64_t am = m < 0 ? -m : m;
+        const bool fast32 = am < ((int64_t)1 << 31) && s >= -30 && s <= 31;
+        const int64_t rnd = fast32 ? (int64_t)1 << (30 + s) : 0;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int a[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                word |= (uint32_t)(uint8_t)requant_elem(
+                            (int64_t)a[j] + pb, m, s, fast32, rnd, qb, lo,
+                            hi)
+                        << (8 * j);
+            w[k] = word;
+        }
+        out[i] = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+    }
+}
+
+// int8 storage in and out, contiguous: the table as 256 stored bytes in
+// LDS (entry u = the output for stored input byte u), 64 bytes a thread
+// whose loads are issued before the table is built.
+__global__ __launch_bounds__(kThreads) void k_lut_i8_v64(
+    const int4* __restrict__ x, int4* __restrict__ out, int64_t n16,
+    int64_t offset, const int32_t* __restrict__ lut, int64_t len,
+    int64_t in_so, int64_t out_so) {
+    __shared__ uint8_t tab[256];
+    const int64_t base = ((int64_t)blockIdx.x * kThreads) * 4;
+    const int64_t stride = (int64_t)gridDim.x * kThreads * 4;
+    int4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t e = base + k * kThreads + threadIdx.x;
+        if (e < n16) v[k] = x[e];
+    }
+    {
+        const int u = threadIdx.x;  // stored byte, as int8
+        int64_t idx = (int64_t)(int8_t)u + in_so - offset;
+        idx = idx < 0 ? 0 : (idx >= len ? len - 1 : idx);
+        tab[u] = (uint8_t)(int8_t)((int64_t)lut[idx] - out_so);
+    }
+    __syncthreads();
+    for (int64_t b = base; b < n16; b += stride) {
+        if (b != base) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int64_t e = b + k * kThreads + threadIdx.x;
+                if (e < n16) v[k] = x[e];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t e = b + k * kThreads + threadIdx.x;
+            if (e >= n16) continue;
+            uint32_t w[4] = {(uint32_t)v[k].x, (uint32_t)v[k].y,
+                             (uint32_t)v[k].z, (uint32_t)v[k].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                w[q] = (uint32_t)tab[w[q] & 255] |
+                       ((uint32_t)tab[(w[q] >> 8) & 255] << 8) |
+                       ((uint32_t)tab[(w[q] >> 16) & 255] << 16) |
+                       ((uint32_t)tab[w[q] >> 24] << 24);
+            out[e] = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+        }
+    }
+}
+
+// Whether the vector kernel takes a requantize: int32 accumulators to int8,
+// rows of whole 16-value groups, 16-byte aligned operands.
+bool requant_v16_ok(const void* acc, const void* out, int64_t n, int64_t C,
+                    int64_t inner) {
+    return inner % 16 == 0 && ((uintptr_t)acc & 15) == 0 &&
+           ((uintptr_t)out & 15) == 0 && n / 16 < ((int64_t)1 << 32) &&
+           C < ((int64_t)1 << 32);
+}
+
+void launch_requant_v16(const int32_t* acc, int8_t* out, int64_t n,
+                        int64_t C, int64_t inner, const int64_t* mult,
+                        const int64_t* shift, const int64_t* pre,
+                        const int64_t* post, int64_t zp, int64_t qmin,
+                        int64_t qmax, int64_t sub, int64_t out_so,
+                        hipStream_t st) {
+    const int64_t n16 = n / 16;
+    k_requant_v16_i32_i8<<<qa::grid_1d(n16, kThreads, 1 << 16), kThreads, 0,
+                           st>>>((const int4*)acc, (int4*)out, n16,
+                                 (uint32_t)C, (uint32_t)(inner / 16), mult,
+                                 shift, pre, post, zp, qmin, qmax, sub,
+                                 out_so);
+}
+
 // Row-strided element-wise kernels: `rows` rows of `cols` elements, each
 // operand with its own row stride (a channel slice of a channels-last tensor
 // is rows = N*H*W pixels, cols = C_slice, stride = the buffer's channel
@@ -375,6 +503,13 @@ QA_API int qa_d_requantize(const void* acc, int acc_code, void* out,
     const int64_t n = outer * C * inner;
     if (n <= 0) return 0;
     hipStream_t st = pick(stream);
+    if (acc_code == 4 && out_code == 1 &&
+        requant_v16_ok(acc, out, n, C, inner)) {
+        launch_requant_v16((const int32_t*)acc, (int8_t*)out, n, C, inner,
+                           mult, shift, pre_bias, post_bias, zp, qmin, qmax,
+                           sub, out_so, st);
+        return launched("qa_d_requantize") ? 0 : -1;
+    }
     const unsigned g = qa::grid_1d(n, kThreads, 1 << 20);
     if (acc_code == 8) {
         QA_DISPATCH_STORAGE(out_code, TO,
@@ -455,6 +590,17 @@ QA_API int qa_d_lut(const void* x, int in_code, int64_t x_rstride, void* out,
                     void* stream) {
     if (rows <= 0 || cols <= 0) return 0;
     hipStream_t st = pick(stream);
+    const int64_t n = rows * cols;
+    if (in_code == 1 && out_code == 1 && lut_len > 0 && n % 16 == 0 &&
+        (rows == 1 || (x_rstride == cols && out_rstride == cols)) &&
+        ((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0) {
+        k_lut_i8_v64<<<qa::grid_1d(qa::ceil_div(n / 16, 4), kThreads,
+                                   1 << 16),
+                       kThreads, 0, st>>>((const int4*)x, (int4*)out, n / 16,
+                                          offset, lut, lut_len, in_so,
+                                          out_so);
+        return launched("qa_d_lut") ? 0 : -1;
+    }
     const dim3 g = grid_rows(rows, cols);
     QA_DISPATCH_STORAGE(in_code, TI,
         QA_DISPATCH_STORAGE(out_code, TO,

@@ -158,3 +158,66 @@ class ConvWorkload(_Workload):
         self.bytes = x.size + w.size + n * cout * oh * ow + cout * 24 + 1024
         self.name = (f"qconv b{n} {cin}->{cout} {kh}x{kw} s{s} p{p} {h}x{wd} "
                      "u8 (+bias, requantize, SiLU table)")
+
+
+class RequantizeWorkload(_Workload):
+    """The standalone requantize of the conv workload's accumulators: int32
+    NCHW [32, 64, 56, 56] (6.42 M values) + per-channel bias -> mbqm ->
+    uint8 (int8 storage), one ``qa_d_requantize`` launch (the reference's
+    separate ``qa_requantize_i32`` step, qa_kernels.cpp:207-228)."""
+
+    def __init__(self, seed=2, batch=32):
+        super().__init__()
+        c = synth.conv_workload(seed, batch=batch)
+        n, cout, hw = batch, c["w"].shape[0], c["x"].shape[2]
+        st = synth.Stream(seed + 100)
+        acc = st.integers(-(2**20), 2**20, (n, cout, hw * hw)).astype(
+            np.int32)
+        self.acc = _dev(acc, np.int32)
+        self.numel = acc.size
+        self.y = torch.empty(self.numel, dtype=torch.int8, device="cuda")
+        self.params = [_dev(c[k], np.int64) for k in ("mult", "shift",
+                                                      "bias")]
+        self.args = (n, cout, hw * hw, c["zp_out"], c["qmin"], c["qmax"])
+        self.ops = self.numel
+        self.bytes = self.numel * (4 + 1) + cout * 24
+        self.name = (f"requantize int32 [{n},{cout},{hw},{hw}] -> u8 "
+                     "(per-channel bias, mbqm)")
+
+    def launch(self, stream=None):
+        s = stream if stream is not None else \
+            torch.cuda.current_stream().cuda_stream
+        outer, cc, inner, zp, qmin, qmax = self.args
+        m, sh, b = (p.data_ptr() for p in self.params)
+        _ok(self.lib.qa_d_requantize(self.acc.data_ptr(), 4,
+                                     self.y.data_ptr(), 1, outer, cc, inner,
+                                     m, sh, b, None, zp, qmin, qmax, 0, 128,
+                                     s), "qa_d_requantize")
+
+
+class LutWorkload(_Workload):
+    """The standalone 256-entry SiLU table over the conv workload's uint8
+    output (6.42 M values, int8 storage in and out), one ``qa_d_lut``
+    launch (the reference's separate ``qa_lut`` step,
+    qa_kernels.cpp:348-358)."""
+
+    def __init__(self, seed=2, batch=32):
+        super().__init__()
+        c = synth.conv_workload(seed, batch=batch)
+        n = batch * c["w"].shape[0] * c["x"].shape[2] * c["x"].shape[3]
+        st = synth.Stream(seed + 200)
+        self.x = _dev(st.integers(-128, 127, (n,)), np.int8)
+        self.y = torch.empty(n, dtype=torch.int8, device="cuda")
+        self.lut = _dev(c["lut"], np.int32)
+        self.numel = n
+        self.ops = n
+        self.bytes = 2 * n + 4 * len(c["lut"])
+        self.name = f"SiLU table u8 -> u8, {n} values"
+
+    def launch(self, stream=None):
+        s = stream if stream is not None else \
+            torch.cuda.current_stream().cuda_stream
+        n = self.numel
+        _ok(self.lib.qa_d_lut(self.x.data_ptr(), 1, n, self.y.data_ptr(), 1,
+                              n, 1, n, 0, self.lut.data_ptr(),
+                              self.lut.numel(), 128, 128, s), "qa_d_lut")
