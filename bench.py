@@ -74,7 +74,7 @@ def parse():
                         "instead of using the committed set")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the ViT-S and int16 YOLOv8n-cls passes")
-    p.add_argument("--only", choices=("vit", "int16"),
+    p.add_argument("--only", choices=("vit", "int16", "gemm"),
                    help="time only that pass (ViT-S/16 int8 b32 or "
                         "YOLOv8n-cls int16) and print its record, e.g. "
                         "under a profiler")
@@ -192,6 +192,19 @@ def main():
 
     native.require()
     B = args.batch
+    if args.only == "gemm":  # the weight GEMM shapes of a ViT-S block
+        from quantanything_amd.workloads import vit_gemm_shapes
+
+        for name, m, k, n in vit_gemm_shapes():
+            wl = GemmWorkload(seed=7, M=m, K=k, N=n)
+            kms = time_launch(wl.launch, args.steps, torch)
+            tops = wl.ops / (kms * 1e-3) / 1e12
+            print(json.dumps({"workload": f"vit {name} {m}x{k}x{n}",
+                              "tile": hex(wl.d.tile), "avg_ms": round(kms, 5),
+                              "int8_tops": round(tops, 1),
+                              "frac_of_mfma_peak": round(tops / PEAK_I8_TOPS,
+                                                         4)}), flush=True)
+        return 0
     if args.only:
         if args.only == "vit":
             rec, _ = measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",

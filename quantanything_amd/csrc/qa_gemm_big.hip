@@ -6,15 +6,20 @@
 // matrix cores waiting on the memory pipe. Here a work-group computes a
 // 128 x 128 block of C: its 4 waves (2 x 2) own 64 x 64 each, i.e. 4 x 4
 // MFMA tiles of v_mfma_i32_16x16x64_i8, so every A fragment feeds 4 MFMAs
-// and every B fragment 4. K runs in 64-byte steps through two LDS buffers
-// (global -> registers for step k+1 while step k's MFMAs run, one barrier a
-// step). The epilogue is the int8 table plan of qa_conv.h (per-channel
-// multiply-add and shift, 256-entry clip / activation / residual / copy
-// tables), identical to the convolution kernel's.
+// and every B fragment 4. K runs in 64- or 128-byte steps through two LDS
+// buffers (global -> registers for the next step while a step's MFMAs run,
+// one barrier a step). The epilogue is the int8 table plan of qa_conv.h
+// (per-channel multiply-add and shift, 256-entry clip / activation /
+// residual / copy tables), identical in results to the convolution
+// kernel's; residual, copy and pixel sums are template flags, full tiles
+// skip the bounds tests, and each lane stores 4 channels of a row as one
+// word (4x4 byte transpose across a lane quad).
 //
 // Operands: A row p (one pixel of a GEMM descriptor, H = W = 1) at
 // x + p * x_sn, K = Cg bytes; B = the packed weight rows (layout 0, one
 // group), K bytes each, rows padded to 128.
+#include <type_traits>
+
 #include "qa_conv_mfma.h"
 
 namespace qa {
@@ -22,8 +27,14 @@ namespace {
 
 constexpr int GB_M = 128, GB_N = 128;
 
-// BK: K bytes a step (64 or 128: one or two MFMA K-depths per barrier)
-template <int P, int BK>
+// BK: K bytes a step (64 or 128: one or two MFMA K-depths per barrier);
+// P: steps whose global loads are in flight (a ring of P register slots:
+// step k's operands are requested when step k - P is stored to LDS, so the
+// memory latency is covered by P steps of MFMAs; with K <= P * BK every
+// load is issued before the first MFMA).
+// RES / Y2 / RS: residual Add, rescaled second output, pixel sums of the
+// activations (weights with an offset) in the epilogue.
+template <int P, int BK, bool RES, bool Y2, bool RS>
 __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
     constexpr int GB_K = BK;
     constexpr int GB_RS = BK + 16;  // LDS row stride (bytes)
@@ -51,37 +62,17 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
     const int64_t m0 = (int64_t)(t / nb) * GB_M;
     const int n0 = (t % nb) * GB_N;
     const int K = a.KGp * 16;
-    const int nk = K / GB_K;  // a multiple of P
+    const int nk = K / GB_K;
     const int8_t* xa = (const int8_t*)a.x;
 
-    // tables of the plan and the lane's 4 channels' constants
-    for (int i = tid; i < 768; i += 256)
-        s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
-    const int4 hdr = *(const int4*)a.plan;
-    int cm[4], ct[4];
-    int64_t cc[4];
-    uint32_t ccorr[4], cbo[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int c = min(n0 + 64 * wn + 16 * j + col, a.Cout - 1);
-        const int4 pc = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
-        cm[j] = pc.x;
-        ct[j] = pc.y;
-        cc[j] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
-        ccorr[j] = a.corr ? (uint32_t)a.corr[c] : 0u;
-        cbo[j] = a.rowsum ? (uint32_t)a.boff[c] : 0u;
-    }
-
-    // global -> registers, P steps ahead: per operand and step, CH chunks
-    // of 16 bytes per thread (chunk tid + 256 j: row (tid / CPR) + j * 256
-    // / CPR, bytes 16 (tid % CPR)); loads past the last step re-read it (in
-    // bounds, unused)
+    // global -> registers: per operand and step, CH chunks of 16 bytes per
+    // thread (chunk tid + 256 j: row (tid / CPR) + j * 256 / CPR, bytes
+    // 16 (tid % CPR)); loads past the last step re-read it (in bounds,
+    // unused)
     constexpr int RSTEP = 256 / CPR;  // rows between a thread's chunks
     const int lr = tid / CPR, lk = (tid % CPR) * 16;
-    // the ring slots (P of them used): SSA vectors of CH 16-byte chunks
-    // per operand, so that they stay in VGPRs
     typedef int vch __attribute__((ext_vector_type(4 * CH)));
-    vch s0a, s0b, s1a, s1b;
+    vch ra[P], rb[P];
     auto gload = [&](vch& va, vch& vb, int ks) __attribute__((always_inline)) {
         const int o = min(ks, nk - 1) * GB_K + lk;
 #pragma unroll
@@ -112,8 +103,28 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
                 int4{vb[4 * j], vb[4 * j + 1], vb[4 * j + 2], vb[4 * j + 3]};
         }
     };
-#define GB_LOAD(S, ks) gload(S##a, S##b, (ks))
-#define GB_STORE(S, buf) sstore(S##a, S##b, (buf))
+    // every slot's loads first: they overlap the table set-up below
+#pragma unroll
+    for (int sl = 0; sl < P; ++sl) gload(ra[sl], rb[sl], sl);
+
+    // tables of the plan and the lane's 4 channels' constants
+    for (int i = tid; i < 768; i += 256)
+        s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
+    const int4 hdr = *(const int4*)a.plan;
+    int cm[4], ct[4];
+    int64_t cc[4];
+    uint32_t ccorr[4], cbo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = min(n0 + 64 * wn + 16 * j + col, a.Cout - 1);
+        const int4 pc = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
+        cm[j] = pc.x;
+        ct[j] = pc.y;
+        cc[j] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
+        ccorr[j] = a.corr ? (uint32_t)a.corr[c] : 0u;
+        cbo[j] = RS ? (uint32_t)a.boff[c] : 0u;
+    }
+
     v4i acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -139,72 +150,119 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                         fa[i], fb[j], acc[i][j], 0, 0, 0);
-            if (a.rowsum) {
+            if (RS) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) psum[i] += bytes_sum(fa[i], 16);
             }
         }
     };
-    // step ks from slot S: to LDS (that buffer was last read two steps
-    // ago, before the previous step's barrier), refill S with step ks + P,
-    // barrier, MFMAs
-#define GB_STEP(S, ks)                      \
-    do {                                    \
-        const int b_ = (ks) & 1;            \
-        GB_STORE(S, b_);                    \
-        GB_LOAD(S, (ks) + P);               \
-        __syncthreads();                    \
-        mfma_step(b_);                      \
-    } while (0)
-    GB_LOAD(s0, 0);
-    if (P > 1) GB_LOAD(s1, 1);
+    // step ks from slot sl: to LDS buffer ks & 1 (last read two steps ago,
+    // before the previous step's barrier), refill the slot with step
+    // ks + P, barrier, MFMAs
     for (int k0 = 0; k0 < nk; k0 += P) {
-        GB_STEP(s0, k0);
-        if (P > 1) GB_STEP(s1, k0 + 1);
-    }
-#undef GB_STEP
-#undef GB_STORE
-#undef GB_LOAD
-
-    // epilogue: lane holds rows 16 i + 4 kg + r, columns 16 j + col
-    const int pA = hdr.x, pB = hdr.y, pSH = hdr.z;
-    const bool res = a.res != nullptr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int ps[4] = {0, 0, 0, 0};
-        if (a.rowsum) {
-            int s = psum[i];
-            s += __shfl_xor(s, 16);
-            s += __shfl_xor(s, 32);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ps[r] = __shfl(s, 4 * kg + r);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t p = m0 + 64 * wm + 16 * i + 4 * kg + r;
-            if (p >= a.M) continue;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = n0 + 64 * wn + 16 * j + col;
-                if (c >= a.Cout) continue;
-                uint32_t wu = (uint32_t)acc[i][j][r] + ccorr[j];
-                if (a.rowsum) wu += cbo[j] * (uint32_t)ps[r];
-                const int q0 =
-                    (int)(((int64_t)(int)wu * cm[j] + cc[j]) >> ct[j]);
-                int e = min(max(q0, pA), pB) - pA;
-                if (res) {
-                    const int u =
-                        (uint8_t)((const int8_t*)a.res)[p * a.res_pst + c];
-                    e = min(max(s_tab[256 + e] + s_tab[512 + u], 0), pSH);
-                }
-                const int ev = s_tab[e];
-                ((int8_t*)a.y)[p * a.y_pst + c] = (int8_t)(ev & 255);
-                if (a.y2)
-                    ((int8_t*)a.y2)[p * a.y2_pst + c] =
-                        (int8_t)((ev >> 8) & 255);
+        for (int sl = 0; sl < P; ++sl) {
+            const int ks = k0 + sl;
+            if (ks < nk) {
+                sstore(ra[sl], rb[sl], ks & 1);
+                if (ks + P < nk) gload(ra[sl], rb[sl], ks + P);
+                __syncthreads();
+                mfma_step(ks & 1);
             }
         }
     }
+
+    // epilogue: lane holds rows 16 i + 4 kg + r, column 16 j + col; the
+    // quad's 4 channels of one row go out as one word (lane q of a quad
+    // stores row 16 i + 4 kg + q, channels cq .. cq + 3). Per value: the
+    // plan's multiply-add and shift, one med3 clip and one table read whose
+    // LDS address folds in the clip's lower bound.
+    const int pA = hdr.x, pB = hdr.y, pSH = hdr.z;
+    const int* tabE = s_tab - pA;  // tabE[v] = E[v - pA] for v in [pA, pB]
+    const int q = lane & 3;
+    const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
+    const uint32_t sel2 = (q & 1) ? 0x03070105u : 0x06020400u;
+    const int cq = col & ~3;
+    // the tile's rows and columns all inside the output: no bounds tests
+    const bool full = m0 + GB_M <= a.M && n0 + GB_N <= a.Cout;
+    auto epilogue = [&](auto checked) __attribute__((always_inline)) {
+        constexpr bool CHK = decltype(checked)::value;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int ps[4] = {0, 0, 0, 0};
+            if (RS) {
+                int sm = psum[i];
+                sm += __shfl_xor(sm, 16);
+                sm += __shfl_xor(sm, 32);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ps[r] = __shfl(sm, 4 * kg + r);
+            }
+            const int64_t pq = m0 + 64 * wm + 16 * i + 4 * kg + q;
+            const bool pok = !CHK || pq < a.M;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c0 = n0 + 64 * wn + 16 * j + cq;
+                const bool cfull = !CHK || c0 + 3 < a.Cout;
+                uint32_t rv = 0;
+                if (RES) {
+                    uint32_t w = 0;
+                    const int8_t* pr =
+                        (const int8_t*)a.res + pq * a.res_pst + c0;
+                    if (!CHK) {
+                        w = *(const uint32_t*)pr;
+                    } else if (pok) {
+                        if (cfull) {
+                            w = *(const uint32_t*)pr;
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (c0 + r < a.Cout)
+                                    w |= (uint32_t)(uint8_t)pr[r] << (8 * r);
+                        }
+                    }
+                    rv = quad_transpose(w, sel1, sel2);
+                }
+                int e[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    uint32_t wu = (uint32_t)acc[i][j][r] + ccorr[j];
+                    if (RS) wu += cbo[j] * (uint32_t)ps[r];
+                    const int q0 =
+                        (int)(((int64_t)(int)wu * cm[j] + cc[j]) >> ct[j]);
+                    const int v = min(max(q0, pA), pB);
+                    if (RES) {
+                        const int tsum = s_tab[256 - pA + v] +
+                                         s_tab[512 + ((rv >> (8 * r)) & 255)];
+                        e[r] = s_tab[min(max(tsum, 0), pSH)];
+                    } else {
+                        e[r] = tabE[v];
+                    }
+                }
+                const uint32_t wy =
+                    quad_transpose(pack_entries(e, 0), sel1, sel2);
+                const uint32_t w2 =
+                    Y2 ? quad_transpose(pack_entries(e, 1), sel1, sel2) : 0u;
+                int8_t* py = (int8_t*)a.y + pq * a.y_pst + c0;
+                int8_t* p2 = Y2 ? (int8_t*)a.y2 + pq * a.y2_pst + c0
+                                : nullptr;
+                if (!CHK || (pok && cfull)) {
+                    *(uint32_t*)py = wy;
+                    if (Y2) *(uint32_t*)p2 = w2;
+                } else if (pok) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (c0 + r < a.Cout) {
+                            py[r] = (int8_t)(wy >> (8 * r));
+                            if (Y2) p2[r] = (int8_t)(w2 >> (8 * r));
+                        }
+                }
+            }
+        }
+    };
+    if (full)
+        epilogue(std::false_type{});
+    else
+        epilogue(std::true_type{});
 }
 
 }  // namespace
@@ -229,10 +287,28 @@ bool launch_gemm_big(const ConvArgs& b, hipStream_t st) {
     // loads in flight (deeper rings cost the second wave per SIMD)
     const int K = b.KGp * 16;
     const dim3 grid((unsigned)tiles);
+    const int flags = (b.res ? 1 : 0) | (b.y2 ? 2 : 0) | (b.rowsum ? 4 : 0);
+    auto go = [&](auto kp, auto kbk) {
+        constexpr int KP = decltype(kp)::value, KBK = decltype(kbk)::value;
+        switch (flags) {
+#define QA_GB_CASE(F)                                                    \
+    case F:                                                              \
+        k_gemm_big<KP, KBK, (F & 1) != 0, (F & 2) != 0, (F & 4) != 0>     \
+            <<<grid, 256, 0, st>>>(b);                                   \
+        break;
+            QA_GB_CASE(0) QA_GB_CASE(1) QA_GB_CASE(2) QA_GB_CASE(3)
+            QA_GB_CASE(4) QA_GB_CASE(5) QA_GB_CASE(6) QA_GB_CASE(7)
+#undef QA_GB_CASE
+        }
+    };
+    // 128-byte steps when K allows, else 64-byte steps, the next step's
+    // loads in flight (measured on the ViT-S GEMMs: deeper rings, which
+    // cost VGPRs and so occupancy, were not faster)
+    using I1 = std::integral_constant<int, 1>;
     if (K % 128 == 0)
-        k_gemm_big<1, 128><<<grid, 256, 0, st>>>(b);
+        go(I1{}, std::integral_constant<int, 128>{});
     else
-        k_gemm_big<1, 64><<<grid, 256, 0, st>>>(b);
+        go(I1{}, std::integral_constant<int, 64>{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("launch_gemm_big", e);

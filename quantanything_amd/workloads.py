@@ -77,11 +77,13 @@ class _Workload:
 
 
 class GemmWorkload(_Workload):
-    """uint8 [M,K] x int8 [K,N] + bias -> requantize -> uint8 [M,N]."""
+    """uint8 [M,K] x int8 [K,N] + bias -> requantize -> uint8 [M,N]
+    (default: M=4096 K=576 N=64; ``vit_gemm_shapes`` lists the weight GEMMs
+    of one ViT-S/16 block at batch 32)."""
 
-    def __init__(self, seed=1):
+    def __init__(self, seed=1, M=4096, K=576, N=64):
         super().__init__()
-        g = synth.gemm_workload(seed)
+        g = synth.gemm_workload(seed, M=M, K=K, N=N)
         self.spec = g
         m, k, n = g["M"], g["K"], g["N"]
         self.x = _dev(g["a"].astype(np.int16) - 128, np.int8)
@@ -221,3 +223,10 @@ class LutWorkload(_Workload):
         _ok(self.lib.qa_d_lut(self.x.data_ptr(), 1, n, self.y.data_ptr(), 1,
                               n, 1, n, 0, self.lut.data_ptr(),
                               self.lut.numel(), 128, 128, s), "qa_d_lut")
+
+
+def vit_gemm_shapes(batch=32, tokens=197, dim=384, mlp=1536):
+    """``(name, M, K, N)`` of the weight GEMMs of one ViT block."""
+    m = batch * tokens
+    return [("qkv", m, dim, 3 * dim), ("proj", m, dim, dim),
+            ("fc1", m, dim, mlp), ("fc2", m, mlp, dim)]
