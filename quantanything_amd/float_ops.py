@@ -435,3 +435,67 @@ def _maxpool(node, ins, opset, pad_value=None, **kw):
     win = sliding_window_view(xp, tuple(ek), axis=(2, 3))
     win = win[:, :, ::strides[0], ::strides[1], ::dil[0], ::dil[1]]
     return win.max(axis=(4, 5))
+
+
+# ------------------------------------------------- model-file operators ----
+def constant_value(node):
+    """The value of an ONNX ``Constant`` node (``float_ops.py:101-118``)."""
+    a = node.attrs
+    for key in ("value", "value_float", "value_int", "value_floats",
+                "value_ints"):
+        if key in a:
+            v = np.asarray(a[key])
+            if key == "value_float":
+                v = v.astype(np.float32)
+            elif key in ("value_int", "value_ints"):
+                v = v.astype(np.int64)
+            return v
+    raise UnsupportedOp(f"Constant node '{node.name}' has no supported "
+                        "value")
+
+
+@_reg("Constant")
+def _constant(node, ins, opset, **kw):
+    return constant_value(node)
+
+
+@_reg("Shape")
+def _shape(node, ins, opset, **kw):
+    shape = np.array(np.shape(ins[0]), np.int64)
+    return shape[node.attr("start", 0):node.attr("end", None)]
+
+
+def _per_axis(v, x, axis):
+    """A per-axis parameter shaped to broadcast along ``axis`` of x."""
+    v = np.asarray(v)
+    if v.ndim == 0 or x.ndim == 0:
+        return v
+    shape = [1] * x.ndim
+    shape[axis % x.ndim] = -1
+    return v.reshape(shape)
+
+
+@_reg("QuantizeLinear")
+def _quantize_linear(node, ins, opset, **kw):
+    """y = saturate(round_half_even(x / scale) + zero_point) in the zero
+    point's type (uint8 without one), float32 arithmetic."""
+    x = np.asarray(ins[0], np.float32)
+    axis = node.attr("axis", 1)
+    scale = _per_axis(np.asarray(ins[1], np.float32), x, axis)
+    zp = ins[2] if len(ins) > 2 and ins[2] is not None else \
+        np.zeros((), np.uint8)
+    info = np.iinfo(np.asarray(zp).dtype)
+    y = np.rint(x / scale) + _per_axis(np.asarray(zp), x, axis).astype(
+        np.float32)
+    return np.clip(y, info.min, info.max).astype(np.asarray(zp).dtype)
+
+
+@_reg("DequantizeLinear")
+def _dequantize_linear(node, ins, opset, **kw):
+    """x = (q - zero_point) * scale in float32."""
+    q = np.asarray(ins[0])
+    axis = node.attr("axis", 1)
+    zp = ins[2] if len(ins) > 2 and ins[2] is not None else 0
+    zpf = _per_axis(np.asarray(zp), q, axis).astype(np.float32)
+    scale = _per_axis(np.asarray(ins[1], np.float32), q, axis)
+    return ((q.astype(np.float32) - zpf) * scale).astype(np.float32)

@@ -1,0 +1,308 @@
+"""The ONNX codec and loader (quantanything_amd.onnx_io) against an
+independent implementation of the same wire format: the protobuf runtime,
+given a descriptor of the ONNX schema subset written here from onnx.proto's
+field numbers. Models encoded by the runtime must decode to the same
+values, models this package writes must parse in the runtime to the same
+values, and the loader must apply the reference's constant folding,
+Identity removal, Conv + BatchNorm folding and MatMul + bias fusion
+(onnx_graph.py:177-235, graph_passes.py:66-101, :507-556)."""
+
+import numpy as np
+import pytest
+from google.protobuf import descriptor_pb2, descriptor_pool, message_factory
+
+from quantanything_amd import graph as G
+from quantanything_amd import onnx_io
+
+F = descriptor_pb2.FieldDescriptorProto
+
+
+def _schema():
+    """Message classes of the ONNX subset (proto2, as onnx.proto)."""
+    fp = descriptor_pb2.FileDescriptorProto(name="onnx_subset.proto",
+                                            package="t", syntax="proto2")
+
+    def msg(name, fields):
+        m = fp.message_type.add(name=name)
+        for fname, no, ftype, label, tname, packed in fields:
+            f = m.field.add(name=fname, number=no, type=ftype, label=label)
+            if tname:
+                f.type_name = ".t." + tname
+            if packed:
+                f.options.packed = True
+        return m
+
+    O, R = F.LABEL_OPTIONAL, F.LABEL_REPEATED
+    msg("TensorProto", [
+        ("dims", 1, F.TYPE_INT64, R, None, False),
+        ("data_type", 2, F.TYPE_INT32, O, None, False),
+        ("float_data", 4, F.TYPE_FLOAT, R, None, True),
+        ("int32_data", 5, F.TYPE_INT32, R, None, True),
+        ("string_data", 6, F.TYPE_BYTES, R, None, False),
+        ("int64_data", 7, F.TYPE_INT64, R, None, True),
+        ("name", 8, F.TYPE_STRING, O, None, False),
+        ("raw_data", 9, F.TYPE_BYTES, O, None, False),
+        ("double_data", 10, F.TYPE_DOUBLE, R, None, True),
+        ("uint64_data", 11, F.TYPE_UINT64, R, None, True)])
+    msg("AttributeProto", [
+        ("name", 1, F.TYPE_STRING, O, None, False),
+        ("f", 2, F.TYPE_FLOAT, O, None, False),
+        ("i", 3, F.TYPE_INT64, O, None, False),
+        ("s", 4, F.TYPE_BYTES, O, None, False),
+        ("t", 5, F.TYPE_MESSAGE, O, "TensorProto", False),
+        ("floats", 7, F.TYPE_FLOAT, R, None, False),
+        ("ints", 8, F.TYPE_INT64, R, None, False),
+        ("strings", 9, F.TYPE_BYTES, R, None, False),
+        ("type", 20, F.TYPE_INT32, O, None, False)])
+    msg("NodeProto", [
+        ("input", 1, F.TYPE_STRING, R, None, False),
+        ("output", 2, F.TYPE_STRING, R, None, False),
+        ("name", 3, F.TYPE_STRING, O, None, False),
+        ("op_type", 4, F.TYPE_STRING, O, None, False),
+        ("attribute", 5, F.TYPE_MESSAGE, R, "AttributeProto", False),
+        ("domain", 7, F.TYPE_STRING, O, None, False)])
+    msg("Dimension", [("dim_value", 1, F.TYPE_INT64, O, None, False),
+                      ("dim_param", 2, F.TYPE_STRING, O, None, False)])
+    msg("TensorShapeProto", [("dim", 1, F.TYPE_MESSAGE, R, "Dimension",
+                              False)])
+    msg("TensorType", [("elem_type", 1, F.TYPE_INT32, O, None, False),
+                       ("shape", 2, F.TYPE_MESSAGE, O, "TensorShapeProto",
+                        False)])
+    msg("TypeProto", [("tensor_type", 1, F.TYPE_MESSAGE, O, "TensorType",
+                       False)])
+    msg("ValueInfoProto", [("name", 1, F.TYPE_STRING, O, None, False),
+                           ("type", 2, F.TYPE_MESSAGE, O, "TypeProto",
+                            False)])
+    msg("GraphProto", [
+        ("node", 1, F.TYPE_MESSAGE, R, "NodeProto", False),
+        ("name", 2, F.TYPE_STRING, O, None, False),
+        ("initializer", 5, F.TYPE_MESSAGE, R, "TensorProto", False),
+        ("input", 11, F.TYPE_MESSAGE, R, "ValueInfoProto", False),
+        ("output", 12, F.TYPE_MESSAGE, R, "ValueInfoProto", False)])
+    msg("OperatorSetIdProto", [("domain", 1, F.TYPE_STRING, O, None, False),
+                               ("version", 2, F.TYPE_INT64, O, None,
+                                False)])
+    msg("ModelProto", [
+        ("ir_version", 1, F.TYPE_INT64, O, None, False),
+        ("producer_name", 2, F.TYPE_STRING, O, None, False),
+        ("graph", 7, F.TYPE_MESSAGE, O, "GraphProto", False),
+        ("opset_import", 8, F.TYPE_MESSAGE, R, "OperatorSetIdProto",
+         False)])
+    pool = descriptor_pool.DescriptorPool()
+    pool.Add(fp)
+    return {m.name: message_factory.GetMessageClass(
+        pool.FindMessageTypeByName("t." + m.name)) for m in fp.message_type}
+
+
+PB = _schema()
+
+
+def _pb_tensor(t, name, arr, form):
+    arr = np.asarray(arr)
+    t.name = name
+    t.dims.extend(arr.shape)
+    t.data_type = onnx_io.CODES[arr.dtype]
+    if form == "raw":
+        t.raw_data = arr.astype(arr.dtype.newbyteorder("<")).tobytes()
+    elif arr.dtype == np.float32:
+        t.float_data.extend(arr.reshape(-1).tolist())
+    elif arr.dtype == np.float64:
+        t.double_data.extend(arr.reshape(-1).tolist())
+    elif arr.dtype == np.int64:
+        t.int64_data.extend(arr.reshape(-1).tolist())
+    else:
+        t.int32_data.extend(arr.reshape(-1).astype(np.int64).tolist())
+
+
+def _pb_model():
+    """A model written by the protobuf runtime: every attribute kind,
+    tensors in every storage field, symbolic and fixed dimensions, two
+    opset imports."""
+    m = PB["ModelProto"](ir_version=8, producer_name="t")
+    m.opset_import.add(domain="com.other", version=1)
+    m.opset_import.add(domain="", version=17)
+    g = m.graph
+    g.name = "g"
+    rng = np.random.default_rng(0)
+    tensors = {
+        "w_f32_list": (rng.normal(size=(3, 2)).astype(np.float32), "list"),
+        "w_f32_raw": (rng.normal(size=(2, 2, 3)).astype(np.float32), "raw"),
+        "i64": (np.array([-5, 7, 2**40, -(2**62)], np.int64), "list"),
+        "i8": (np.array([[-128, 127], [0, -1]], np.int8), "list"),
+        "u8raw": (np.array([0, 255, 17], np.uint8), "raw"),
+        "i16": (np.array([-32768, 32767, 3], np.int16), "list"),
+        "f64": (np.array([1.5, -2.25], np.float64), "list"),
+        "scalar": (np.array(3.0, np.float32), "list"),
+    }
+    for name, (arr, form) in tensors.items():
+        _pb_tensor(g.initializer.add(), name, arr, form)
+    n = g.node.add(name="n0", op_type="Conv")
+    n.input.extend(["x", "w_f32_list", ""])
+    n.output.append("y")
+    a = n.attribute.add(name="kernel_shape", type=onnx_io.A_INTS)
+    a.ints.extend([3, 3])
+    n.attribute.add(name="alpha", type=onnx_io.A_FLOAT, f=0.25)
+    n.attribute.add(name="group", type=onnx_io.A_INT, i=-2)
+    n.attribute.add(name="auto_pad", type=onnx_io.A_STRING, s=b"SAME_UPPER")
+    a = n.attribute.add(name="scales", type=onnx_io.A_FLOATS)
+    a.floats.extend([0.5, 2.0])
+    a = n.attribute.add(name="modes", type=onnx_io.A_STRINGS)
+    a.strings.extend([b"a", b"bc"])
+    a = n.attribute.add(name="value", type=onnx_io.A_TENSOR)
+    _pb_tensor(a.t, "v", np.array([1, 2], np.int64), "list")
+    vi = g.input.add(name="x")
+    sh = vi.type.tensor_type
+    sh.elem_type = 1
+    sh.shape.dim.add(dim_param="batch")
+    sh.shape.dim.add(dim_value=3)
+    sh.shape.dim.add(dim_value=8)
+    g.output.add(name="y")
+    return m, tensors
+
+
+def test_decoder_reads_what_the_protobuf_runtime_writes():
+    m, tensors = _pb_model()
+    graph, opset = onnx_io.decode_model(m.SerializeToString())
+    assert opset == 17 and graph["name"] == "g"
+    for name, (arr, _) in tensors.items():
+        got = graph["initializers"][name]
+        assert got.dtype == arr.dtype and got.shape == arr.shape, name
+        np.testing.assert_array_equal(got, arr)
+    (node,) = graph["nodes"]
+    assert (node.name, node.op_type, node.inputs, node.outputs) == \
+        ("n0", "Conv", ["x", "w_f32_list", ""], ["y"])
+    at = node.attrs
+    assert at["kernel_shape"] == [3, 3] and at["group"] == -2
+    assert at["alpha"] == 0.25 and at["auto_pad"] == "SAME_UPPER"
+    assert at["scales"] == [0.5, 2.0] and at["modes"] == ["a", "bc"]
+    np.testing.assert_array_equal(at["value"], [1, 2])
+    assert graph["inputs"] == [("x", ["batch", 3, 8], 1)]
+    assert [o[0] for o in graph["outputs"]] == ["y"]
+
+
+def test_writer_output_parses_in_the_protobuf_runtime():
+    g = G.mini_sppf(seed=1)
+    data = onnx_io.save_onnx(g)
+    m = PB["ModelProto"]()
+    m.ParseFromString(data)
+    assert [o.version for o in m.opset_import if o.domain == ""] == [13]
+    names = {t.name: t for t in m.graph.initializer}
+    for k, v in g.initializers.items():
+        t = names[k]
+        assert list(t.dims) == list(v.shape) and \
+            t.data_type == onnx_io.CODES[v.dtype]
+        np.testing.assert_array_equal(
+            np.frombuffer(t.raw_data, v.dtype).reshape(v.shape), v)
+    ops = [n.op_type for n in m.graph.node]
+    # the fused SiLU regions are written back as Sigmoid + Mul
+    assert "FusedElementwise" not in ops and ops.count("Sigmoid") == \
+        ops.count("Mul") >= 4
+    mp = [n for n in m.graph.node if n.op_type == "MaxPool"
+          and any(a.name == "ceil_mode" for a in n.attribute)]
+    assert len(mp) == 1
+    attrs = {a.name: a for a in mp[0].attribute}
+    assert list(attrs["dilations"].ints) == [2, 1]
+    assert attrs["ceil_mode"].i == 1
+    assert attrs["ceil_mode"].type == onnx_io.A_INT
+    sh = m.graph.input[0].type.tensor_type.shape
+    assert sh.dim[0].dim_param and [d.dim_value for d in sh.dim[1:]] == \
+        [3, 32, 32]
+
+
+@pytest.mark.parametrize("build", [
+    lambda: G.mini_yolo(seed=0), lambda: G.mini_sppf(seed=2),
+    lambda: G.vit(seed=5, batch=2, size=32, patch=8, dim=64, depth=2,
+                  heads=2, mlp=128, classes=10)])
+def test_round_trip_preserves_the_graph(build):
+    g = build()
+    h = onnx_io.load_onnx(onnx_io.save_onnx(g))
+    assert [(n.name, n.op_type, n.inputs, n.outputs) for n in g.nodes] == \
+        [(n.name, n.op_type, n.inputs, n.outputs) for n in h.nodes]
+    for a, b in zip(g.nodes, h.nodes):
+        assert a.attrs.keys() == b.attrs.keys()
+        if a.op_type == "FusedElementwise":
+            assert [n.op_type for n in a.attrs["nodes"]] == \
+                [n.op_type for n in b.attrs["nodes"]]
+        else:
+            for k in a.attrs:
+                va, vb = np.asarray(a.attrs[k]), np.asarray(b.attrs[k])
+                if va.dtype.kind == "f":  # ONNX float attributes are float32
+                    va = va.astype(np.float32)
+                np.testing.assert_array_equal(va, vb)
+    assert sorted(g.initializers) == sorted(h.initializers)
+    for k, v in g.initializers.items():
+        assert h.initializers[k].dtype == v.dtype
+        np.testing.assert_array_equal(h.initializers[k], v)
+    assert g.outputs == h.outputs and list(g.inputs) == list(h.inputs)
+
+
+def _raw_graph():
+    """Conv -> BatchNormalization, MatMul + Add(bias), an Identity, a Shape
+    of a static input feeding a constant Reshape target, a Constant node."""
+    rng = np.random.default_rng(3)
+    f32 = np.float32
+    inits = {
+        "w": rng.normal(size=(4, 3, 3, 3)).astype(f32),
+        "cb": rng.normal(size=4).astype(f32),
+        "g": rng.uniform(0.5, 2, 4).astype(f32),
+        "be": rng.normal(size=4).astype(f32),
+        "mu": rng.normal(size=4).astype(f32),
+        "var": rng.uniform(0.1, 3, 4).astype(f32),
+        "wm": rng.normal(size=(4 * 6 * 6, 5)).astype(f32),
+        "bm": rng.normal(size=5).astype(f32),
+        "idx": np.array([0], np.int64),
+    }
+    N = G.Node
+    nodes = [
+        N("conv", "Conv", ["x", "w", "cb"], ["c"],
+          {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}),
+        N("bn", "BatchNormalization", ["c", "g", "be", "mu", "var"], ["b"],
+          {"epsilon": 1e-3}),
+        N("id", "Identity", ["b"], ["b2"], {}),
+        N("shape", "Shape", ["x"], ["s"], {}),
+        N("gat", "Gather", ["s", "idx"], ["n"], {"axis": 0}),
+        N("k", "Constant", [], ["minus1"],
+          {"value": np.array([-1], np.int64)}),
+        N("cat", "Concat", ["n", "minus1"], ["tgt"], {"axis": 0}),
+        N("resh", "Reshape", ["b2", "tgt"], ["flat"], {}),
+        N("mm", "MatMul", ["flat", "wm"], ["m"], {}),
+        N("add", "Add", ["m", "bm"], ["y"], {}),
+    ]
+    return G.Graph(nodes, inits, {"x": [2, 3, 6, 6]}, ["y"])
+
+
+def test_loader_folds_constants_and_applies_the_rewrites():
+    g = _raw_graph()
+    h = onnx_io.load_onnx(onnx_io.save_onnx(g))
+    assert [n.op_type for n in h.nodes] == ["Conv", "Reshape", "MatMul"]
+    conv, resh, mm = h.nodes
+    # Shape of the static input -> Gather -> Concat folded to [2, -1]
+    np.testing.assert_array_equal(h.initializers[resh.inputs[1]], [2, -1])
+    # Conv + BatchNorm: float64 arithmetic, float32 results
+    i = g.initializers
+    a = i["g"].astype(np.float64) / np.sqrt(i["var"].astype(np.float64) +
+                                            1e-3)
+    want_w = (i["w"].astype(np.float64) * a[:, None, None, None]).astype(
+        np.float32)
+    want_b = (a * (i["cb"].astype(np.float64) - i["mu"]) + i["be"]).astype(
+        np.float32)
+    np.testing.assert_array_equal(h.initializers[conv.inputs[1]], want_w)
+    np.testing.assert_array_equal(h.initializers[conv.inputs[2]], want_b)
+    assert conv.outputs == ["b"] and resh.inputs[0] == "b"
+    # MatMul + bias: three-input MatMul writing the Add's output
+    assert mm.inputs == ["flat", "wm", "bm"] and mm.outputs == ["y"]
+    # without the rewrites only folding and Identity removal happen
+    raw = onnx_io.load_onnx(onnx_io.save_onnx(g), optimize=False)
+    assert [n.op_type for n in raw.nodes] == ["Conv", "BatchNormalization",
+                                             "Reshape", "MatMul", "Add"]
+
+
+def test_rejects_truncated_and_external_data():
+    data = onnx_io.save_onnx(G.mini_yolo(seed=0))
+    with pytest.raises(ValueError):
+        onnx_io.load_onnx(data[:-7])
+    t = PB["TensorProto"](name="e", data_type=1)
+    t.dims.append(2)
+    ext = t.SerializeToString() + bytes([14 << 3, 1])  # data_location = 1
+    with pytest.raises(ValueError, match="external data"):
+        onnx_io.decode_tensor(ext)
