@@ -218,7 +218,11 @@ def main():
         return 0
     g = G.yolov8n_cls(seed=3)
     c = QuantContainer(g, "int8", per_channel=True)
-    c.calibrate([Stream(4).normal((32, 3, 224, 224)).astype(np.float32)])
+    calib = Stream(4).normal((32, 3, 224, 224)).astype(np.float32)
+    QuantContainer(g, "int8", per_channel=True).calibrate([calib[:2]])
+    t0 = time.perf_counter()
+    c.calibrate([calib])  # float pass (GPU conv / GEMM), ranges, parameters
+    calib_s = time.perf_counter() - t0
     x = Stream(5).normal((B, 3, 224, 224)).astype(np.float32)
     ex = c.executor({"images": x.shape})
     ex.inputs_f32["images"].copy_(torch.from_numpy(x))
@@ -468,6 +472,7 @@ def main():
         "kernels": kernels,
         "other_configs": extra,
         "gate": gate,
+        "calibration_s": round(calib_s, 3),
         "launches_per_step": len(ex.launches),
         "top_launches_ms": [[n, round(t, 5)] for t, n, _ in per[:6]],
         "launches_ms": in_order,

@@ -497,6 +497,102 @@ int qa_d_softmax_f32(const void* x, int in_code, int64_t rows, int64_t cols,
                      int64_t qmin, int64_t qmax, int64_t out_so,
                      float* out_f32, void* stream);
 
+/* More float fallbacks (dequantize -> float op -> quantize, the reference's
+ * quant_layers.py:195-205) for operators with no integer form. Operands
+ * dequantize to (float)((q + so - zp) * scale); results quantize as
+ * qa_quantize_f32 (double division, half to even) and are stored as q - so.
+ * Element strides everywhere (a stride 0 broadcasts). */
+
+/* Div (op 0), Max (1), Min (2) in float32 and Pow (3) in float64, of two
+ * activations (float_ops.py:217-222, :321-325); output element
+ * (i_0, .., i_{ndim-1}) of `shape` reads a at sum i_k as[k], b at
+ * sum i_k bs[k], writes y at sum i_k ys[k]. An operand of code 0 is a
+ * float32 constant, read as is. */
+typedef struct qa_fb_binary {
+    const void* a;
+    int64_t a_code, a_so, a_zp;
+    double a_scale;
+    int64_t as[6];
+    const void* b;
+    int64_t b_code, b_so, b_zp;
+    double b_scale;
+    int64_t bs[6];
+    void* y;
+    int64_t y_code, y_so;
+    int64_t ys[6];
+    int64_t ndim, shape[6], op;
+    double out_scale;
+    int64_t out_zp, qmin, qmax;
+} qa_fb_binary;
+int qa_d_fb_binary(const qa_fb_binary* d, void* stream);
+
+/* Integer Add / Sub (op 0) or Mul (op 1) with NumPy broadcasting
+ * (quantization/native.py:465-500 broadcasts both operands, then calls
+ * qa_add / qa_mul, qa_kernels.cpp:346-386). Element (i_0, .., i_{ndim-1})
+ * of `shape` reads a at sum i_k as[k] and b at sum i_k bs[k] (stride 0 on a
+ * broadcast axis) and writes y at sum i_k ys[k]:
+ *   op 0: clip(mbqm(a - za, ma, sa) + sign * mbqm(b - zb, mb, sb) + zp_out)
+ *   op 1: clip(mbqm((a - za) * (b - zb), ma, sa) + zp_out)
+ * Values are stored as q - so (a_so, b_so, y_so) in storage codes 1, 2, 4. */
+typedef struct qa_binary_nd {
+    const void* a;
+    const void* b;
+    void* y;
+    int64_t a_code, b_code, y_code, a_so, b_so, y_so;
+    int64_t ndim, shape[6], as[6], bs[6], ys[6];
+    int64_t op, za, ma, sa, zb, mb, sb, sign, zp_out, qmin, qmax;
+} qa_binary_nd;
+int qa_d_binary_nd(const qa_binary_nd* d, void* stream);
+
+/* ReduceMean (float_ops.py:594-601): output element o (the kept dims,
+ * written densely at y + o) = the mean over the reduced dims, summed in
+ * float64. */
+typedef struct qa_fb_reduce {
+    const void* x;
+    int64_t x_code, x_so, x_zp;
+    double x_scale;
+    int64_t nkeep, keep[6], xks[6];
+    int64_t nred, red[6], xrs[6];
+    void* y;
+    int64_t y_code, y_so;
+    double out_scale;
+    int64_t out_zp, qmin, qmax;
+} qa_fb_reduce;
+int qa_d_fb_reduce_mean(const qa_fb_reduce* d, void* stream);
+
+/* Softmax (log = 0) or LogSoftmax (log = 1) over one axis of length `len`
+ * (float_ops.py:380-395, float64): row (o, i) of outer x inner rows, its
+ * element k at o xs_o + k xs_k + i xs_i (likewise for y). */
+typedef struct qa_fb_softmax {
+    const void* x;
+    int64_t x_code, x_so, x_zp;
+    double x_scale;
+    int64_t outer, len, inner, xs_o, xs_k, xs_i;
+    void* y;
+    int64_t y_code, y_so, ys_o, ys_k, ys_i;
+    int64_t log;
+    double out_scale;
+    int64_t out_zp, qmin, qmax;
+} qa_fb_softmax;
+int qa_d_fb_softmax(const qa_fb_softmax* d, void* stream);
+
+/* AveragePool (float_ops.py:563-577): the mean of the window's taps inside
+ * the image (count_pad = 0) or their sum over KH*KW (count_pad = 1, the
+ * zero padding counted); the caller resolves pads / auto_pad / ceil_mode
+ * into PT, PL, OH, OW. Strides per axis (n, c, h, w). */
+typedef struct qa_fb_avgpool {
+    const void* x;
+    int64_t x_code, x_so, x_zp;
+    double x_scale;
+    int64_t x_sn, x_sc, x_sh, x_sw;
+    int64_t N, C, H, W, KH, KW, SH, SW, PT, PL, OH, OW, count_pad;
+    void* y;
+    int64_t y_code, y_so, y_sn, y_sc, y_sh, y_sw;
+    double out_scale;
+    int64_t out_zp, qmin, qmax;
+} qa_fb_avgpool;
+int qa_d_fb_avgpool(const qa_fb_avgpool* d, void* stream);
+
 /* ---------------------------------------------- allocation-free GEMM --- */
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid

@@ -131,6 +131,41 @@ def eval_node(node, args, opset=13, pad_value=None):
     if op == "Softmax":
         ax = node.attr("axis", -1 if opset >= 13 else 1)
         return [softmax(args[0], ax + args[0].ndim if ax < 0 else ax)]
+    if op == "LogSoftmax":  # float_ops.py:388-395
+        ax = node.attr("axis", -1 if opset >= 13 else 1)
+        x = args[0].astype(np.float64)
+        ax = ax + x.ndim if ax < 0 else ax
+        z = x - x.max(axis=ax, keepdims=True)
+        return [_f32(z - np.log(np.exp(z).sum(axis=ax, keepdims=True)))]
+    if op == "ReduceMean":  # float_ops.py:594-601
+        x = args[0]
+        axes = (np.asarray(args[1]).astype(np.int64).tolist()
+                if len(args) > 1 and args[1] is not None
+                else node.attr("axes"))
+        axes = tuple(a + x.ndim if a < 0 else a for a in axes) if axes \
+            else None
+        return [_f32(x.mean(axis=axes,
+                            keepdims=bool(node.attr("keepdims", 1))))]
+    if op == "Expand":  # float_ops.py:328-333
+        shape = tuple(int(v) for v in np.asarray(args[1]).reshape(-1))
+        return [np.broadcast_to(args[0], np.broadcast_shapes(
+            args[0].shape, shape)).copy()]
+    if op == "Cast" and node.attr("to") == 1:  # float_ops.py:398-403
+        return [args[0].astype(np.float32)]
+    if op == "AveragePool":  # float_ops.py:563-577
+        x = args[0].astype(np.float32)
+        k = tuple(node.attr("kernel_shape"))
+        s = tuple(node.attr("strides", [1] * len(k)))
+        p = pool_pads(node, x.shape[2:], k, s, (1, 1))
+        pad = ((0, 0), (0, 0), (p[0], p[2]), (p[1], p[3]))
+        win = sliding_window_view(np.pad(x, pad), k, axis=(2, 3))
+        total = win[:, :, ::s[0], ::s[1]].sum(axis=(4, 5))
+        if node.attr("count_include_pad", 0):
+            return [_f32(total / (k[0] * k[1]))]
+        ones = np.pad(np.ones_like(x[:1, :1]), pad)
+        cnt = sliding_window_view(ones, k, axis=(2, 3))[
+            :, :, ::s[0], ::s[1]].sum(axis=(4, 5))
+        return [_f32(total / cnt)]
     if op == "LayerNormalization":
         ax = node.attr("axis", -1)
         return [layer_norm(args[0], args[1], args[2] if len(args) > 2

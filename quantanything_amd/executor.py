@@ -155,7 +155,9 @@ class DeviceTensor:
         if self._strides is not None and (len(self.shape) != 2 or
                                           self._strides[1] != 1):
             sh, st = self.shape, self._strides
-            if len(sh) < 2 or st[-1] != 1 and sh[-1] > 1:
+            if not sh:
+                return 1, 1, 1  # a scalar
+            if st[-1] != 1 and sh[-1] > 1:
                 return None
             dims = [(n, v) for n, v in zip(sh[:-1], st[:-1]) if n > 1]
             for (n0, s0), (n1, s1) in zip(dims, dims[1:]):
@@ -165,6 +167,8 @@ class DeviceTensor:
             return int(np.prod(sh[:-1], dtype=np.int64)), sh[-1], rs
         if len(self.shape) == 2:
             return self.shape[0], self.shape[1], self.sn
+        if len(self.shape) == 4 and self.sc == 1 and self.pixels == 1:
+            return self.shape[0], self.channels, self.sn  # e.g. [N, C, 1, 1]
         if len(self.shape) == 4 and self.sc == 1 and \
                 self.sn == self.pixels * self.sp:
             return self.shape[0] * self.pixels, self.channels, self.sp
@@ -231,6 +235,86 @@ class MaxPoolDesc(ctypes.Structure):
                                        "OW", "pad")]
                 + [("y", _P)]
                 + [(n, _I64) for n in ("y_sn", "y_sc", "y_sh", "y_sw")])
+
+
+_D = ctypes.c_double
+
+
+class FbBinary(ctypes.Structure):
+    """``qa_fb_binary`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("a", _P)] + [(n, _I64) for n in ("a_code", "a_so", "a_zp")]
+                + [("a_scale", _D), ("as_", _I64 * 6), ("b", _P)]
+                + [(n, _I64) for n in ("b_code", "b_so", "b_zp")]
+                + [("b_scale", _D), ("bs", _I64 * 6), ("y", _P)]
+                + [(n, _I64) for n in ("y_code", "y_so")]
+                + [("ys", _I64 * 6), ("ndim", _I64), ("shape", _I64 * 6),
+                   ("op", _I64), ("out_scale", _D)]
+                + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
+
+
+class BinaryNd(ctypes.Structure):
+    """``qa_binary_nd`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("a", _P), ("b", _P), ("y", _P)]
+                + [(n, _I64) for n in ("a_code", "b_code", "y_code", "a_so",
+                                       "b_so", "y_so", "ndim")]
+                + [("shape", _I64 * 6), ("as_", _I64 * 6), ("bs", _I64 * 6),
+                   ("ys", _I64 * 6)]
+                + [(n, _I64) for n in ("op", "za", "ma", "sa", "zb", "mb",
+                                       "sb", "sign", "zp_out", "qmin",
+                                       "qmax")])
+
+
+class FbReduce(ctypes.Structure):
+    """``qa_fb_reduce`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("x", _P)] + [(n, _I64) for n in ("x_code", "x_so", "x_zp")]
+                + [("x_scale", _D), ("nkeep", _I64), ("keep", _I64 * 6),
+                   ("xks", _I64 * 6), ("nred", _I64), ("red", _I64 * 6),
+                   ("xrs", _I64 * 6), ("y", _P)]
+                + [(n, _I64) for n in ("y_code", "y_so")]
+                + [("out_scale", _D)]
+                + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
+
+
+class FbSoftmax(ctypes.Structure):
+    """``qa_fb_softmax`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("x", _P)] + [(n, _I64) for n in ("x_code", "x_so", "x_zp")]
+                + [("x_scale", _D)]
+                + [(n, _I64) for n in ("outer", "len", "inner", "xs_o",
+                                       "xs_k", "xs_i")]
+                + [("y", _P)]
+                + [(n, _I64) for n in ("y_code", "y_so", "ys_o", "ys_k",
+                                       "ys_i", "log")]
+                + [("out_scale", _D)]
+                + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
+
+
+class FbAvgPool(ctypes.Structure):
+    """``qa_fb_avgpool`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("x", _P)] + [(n, _I64) for n in ("x_code", "x_so", "x_zp")]
+                + [("x_scale", _D)]
+                + [(n, _I64) for n in ("x_sn", "x_sc", "x_sh", "x_sw", "N",
+                                       "C", "H", "W", "KH", "KW", "SH", "SW",
+                                       "PT", "PL", "OH", "OW", "count_pad")]
+                + [("y", _P)]
+                + [(n, _I64) for n in ("y_code", "y_so", "y_sn", "y_sc",
+                                       "y_sh", "y_sw")]
+                + [("out_scale", _D)]
+                + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
+
+
+def _collapse(shape, strides, lo, hi):
+    """The element stride of axes lo..hi-1 taken as one index (row-major
+    order), or None when their strides do not allow it; 0 for no axes."""
+    dims = [(n, s) for n, s in zip(shape[lo:hi], strides[lo:hi]) if n > 1]
+    for (n0, s0), (n1, s1) in zip(dims, dims[1:]):
+        if s0 != n1 * s1:
+            return None
+    return dims[-1][1] if dims else 0
 
 
 class MatmulDesc(ctypes.Structure):
@@ -378,9 +462,9 @@ class DeviceExecutor:
             buf = torch.zeros(numel + TAIL, dtype=self.dtype, device="cuda")
             return DeviceTensor(buf, 0, shape, shape[1], 1, 0, self.code,
                                 self.so, qp)
-        if not 1 <= len(shape) <= 6:
+        if len(shape) > 6:
             raise NotImplementedError(f"{len(shape)}-D tensors on the device")
-        numel = int(np.prod(shape, dtype=np.int64))
+        numel = int(np.prod(shape, dtype=np.int64))  # 1 for a scalar
         buf = torch.zeros(numel + TAIL, dtype=self.dtype, device="cuda")
         strides = tuple(int(np.prod(shape[k + 1:], dtype=np.int64))
                         for k in range(len(shape)))
@@ -933,8 +1017,66 @@ class DeviceExecutor:
             raise NotImplementedError("element-wise op on strided views")
         return av, bv, yv
 
+    @staticmethod
+    def _rows_pair(a, b):
+        """Whether the row kernels cover a (op) b: one storage code and equal
+        shapes as row views, or one operand of batch 1 repeated over the
+        other's batch (both row-major)."""
+        if a.code != b.code:
+            return False
+        if a.shape == b.shape:
+            av, bv = a.rows_view(), b.rows_view()
+            if av is None or bv is None:
+                return False
+            if a._strides is None and b._strides is None:
+                return True  # one default layout (and so the output's)
+            # the output is dense row-major: rows must be the leading axes
+            want = (int(np.prod(a.shape[:-1], dtype=np.int64)), a.shape[-1])
+            return tuple(av[:2]) == want and tuple(bv[:2]) == want
+        one, big = (b, a) if b.shape[0] == 1 else (a, b)
+        return len(a.shape) == len(b.shape) and one.shape[0] == 1 and \
+            one.shape[1:] == big.shape[1:] and one.row_major() and \
+            (big.row_major() or big.shape[0] == 1)
+
+    def _plan_binary_nd(self, layer, ins, op):
+        """Add / Sub (op 0) or Mul (op 1) with NumPy broadcasting of any two
+        operand shapes and strides (``qa_d_binary_nd``)."""
+        a, b = ins
+        out = tuple(np.broadcast_shapes(a.shape, b.shape))
+        nd = len(out)
+        if not 1 <= nd <= 6:
+            raise NotImplementedError(f"{layer.node.op_type} of rank {nd}")
+        o = layer.out_qp[0]
+        y = self._new(out, o, dense=nd not in (2, 4))
+        d = BinaryNd()
+        for side, t in (("a", a), ("b", b)):
+            st = t.nd_strides
+            arr = d.as_ if side == "a" else d.bs
+            for j in range(1, len(t.shape) + 1):  # right-aligned
+                arr[nd - j] = 0 if t.shape[-j] == 1 else st[-j]
+            setattr(d, side, t.ptr)
+            setattr(d, side + "_code", t.code)
+            setattr(d, side + "_so", t.so)
+        d.y, d.y_code, d.y_so, d.ndim, d.op = y.ptr, y.code, y.so, nd, op
+        for j, (n_, s_) in enumerate(zip(out, y.nd_strides)):
+            d.shape[j], d.ys[j] = n_, s_
+        qa_, qb_ = layer.in_qp
+        d.za, d.zb = int(qa_.zp), int(qb_.zp)
+        if op == 0:
+            (d.ma, d.sa), (d.mb, d.sb) = layer.mults
+            d.sign = layer.sign
+        else:
+            d.ma, d.sa = layer.mult, layer.shift
+        d.zp_out, d.qmin, d.qmax = int(o.zp), int(o.qmin), int(o.qmax)
+        self.keep.extend([a.buf, b.buf, y.buf, d])
+        self._add(f"{('add', 'mul')[op]}:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_binary_nd(ctypes.byref(d), s), "qa_d_binary_nd"))
+        return [y]
+
     def _plan_add(self, layer, ins):
         a, b = ins
+        if not self._rows_pair(a, b):
+            return self._plan_binary_nd(layer, ins, 0)
         o = layer.out_qp[0]
         y = self._new(a.shape if a.shape[0] >= b.shape[0] else b.shape, o,
                       dense=a._strides is not None or b._strides is not None)
@@ -949,6 +1091,8 @@ class DeviceExecutor:
 
     def _plan_mul(self, layer, ins):
         a, b = ins
+        if not self._rows_pair(a, b):
+            return self._plan_binary_nd(layer, ins, 1)
         o = layer.out_qp[0]
         y = self._new(a.shape if a.shape[0] >= b.shape[0] else b.shape, o,
                       dense=a._strides is not None or b._strides is not None)
@@ -1237,7 +1381,7 @@ class DeviceExecutor:
             ax = layer.node.attr("axis", -1 if self.graph.opset >= 13 else 1)
             ax = ax + len(x.shape) if ax < 0 else ax
             if ax != len(x.shape) - 1:
-                raise NotImplementedError("Softmax over a non-last axis")
+                return self._plan_fb_softmax(layer, x, log=False)
             x = self._contiguous(f"copy:{layer.name}", x)
             o = layer.out_qp[0]
             y = self._new(x.shape, o, dense=True)
@@ -1271,14 +1415,208 @@ class DeviceExecutor:
             return self._plan_matmul_act(layer, ins[0], ins[1])
         if op == "Gather":
             return self._plan_gather(layer, x)
+        if op in ("Div", "Max", "Min", "Pow"):
+            return self._plan_fb_binary(layer, ins)
+        if op == "ReduceMean":
+            return self._plan_fb_reduce(layer, x)
+        if op == "LogSoftmax":
+            return self._plan_fb_softmax(layer, x, log=True)
+        if op == "AveragePool":
+            return self._plan_fb_avgpool(layer, x)
+        if op == "Expand" or (op == "Cast" and layer.node.attr("to") == 1):
+            return self._plan_fb_copy(layer, x)
         raise NotImplementedError(f"float fallback of {op} on the device")
+
+    @staticmethod
+    def _qargs(qp):
+        return float(qp.scale), int(qp.zp), int(qp.qmin), int(qp.qmax)
+
+    def _plan_fb_binary(self, layer, ins):
+        """Div / Max / Min / Pow of two operands, either quantized
+        activations or float constants, with NumPy broadcasting."""
+        node = layer.node
+        init = self.graph.initializers
+        data = dict(zip(layer.inputs, ins))
+        qps = dict(zip(layer.inputs, layer.in_qp))
+        ops = []
+        for name in node.inputs[:2]:
+            if name in data:
+                ops.append((data[name], qps[name]))
+            else:  # a float constant, read as float32 (code 0)
+                v = np.ascontiguousarray(init[name], np.float32)
+                t = _dev(v, np.float32)
+                st = tuple(int(np.prod(v.shape[k + 1:], dtype=np.int64))
+                           for k in range(v.ndim))
+                ops.append((t, v.shape, st))
+        shapes = [o[0].shape if len(o) == 2 else o[1] for o in ops]
+        out = tuple(np.broadcast_shapes(*shapes))
+        nd = len(out)
+        if not 1 <= nd <= 6:
+            raise NotImplementedError(f"{node.op_type} of rank {nd}")
+        o = layer.out_qp[0]
+        y = self._new(out, o, dense=len(out) not in (2, 4))
+        d = FbBinary()
+        for k, (side, src) in enumerate(zip(("a", "b"), ops)):
+            if len(src) == 2:
+                t, qp = src
+                shp, st = t.shape, t.nd_strides
+                ptr, code, so, zp, sc = t.ptr, t.code, t.so, qp.zp, qp.scale
+                self.keep.append(t.buf)
+            else:
+                t, shp, st = src
+                ptr, code, so, zp, sc = t.data_ptr(), 0, 0, 0, 1.0
+                self.keep.append(t)
+            strides = [0] * nd
+            for j in range(1, len(shp) + 1):  # right-aligned broadcasting
+                if shp[-j] != 1:
+                    strides[-j] = st[-j]
+            setattr(d, side, ptr)
+            setattr(d, side + "_code", code)
+            setattr(d, side + "_so", so)
+            setattr(d, side + "_zp", int(zp))
+            setattr(d, side + "_scale", float(sc))
+            arr = d.as_ if side == "a" else d.bs
+            for j in range(nd):
+                arr[j] = strides[j]
+        d.y, d.y_code, d.y_so = y.ptr, y.code, y.so
+        for j, (n_, s_) in enumerate(zip(out, y.nd_strides)):
+            d.shape[j], d.ys[j] = n_, s_
+        d.ndim = nd
+        d.op = ("Div", "Max", "Min", "Pow").index(node.op_type)
+        d.out_scale, d.out_zp, d.qmin, d.qmax = self._qargs(o)
+        self.keep.extend([y.buf, d])
+        self._add(f"fallback:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_fb_binary(ctypes.byref(d), s), "qa_d_fb_binary"))
+        return [y]
+
+    def _plan_fb_reduce(self, layer, x):
+        node = layer.node
+        nd = len(x.shape)
+        axes = self._const_list(node, 1, "axes")
+        axes = sorted({a + nd if a < 0 else a for a in axes}) if axes \
+            else list(range(nd))
+        keep = [k for k in range(nd) if k not in axes]
+        keepdims = bool(node.attr("keepdims", 1))
+        shape = tuple(1 if k in axes else x.shape[k] for k in range(nd)) \
+            if keepdims else tuple(x.shape[k] for k in keep)
+        o = layer.out_qp[0]
+        y = self._new(shape or (1,), o, dense=True)
+        st = x.nd_strides
+        d = FbReduce()
+        d.x, d.x_code, d.x_so = x.ptr, x.code, x.so
+        d.x_zp, d.x_scale = int(layer.in_qp[0].zp), float(layer.in_qp[0].scale)
+        d.nkeep, d.nred = len(keep), len(axes)
+        for j, k in enumerate(keep):
+            d.keep[j], d.xks[j] = x.shape[k], st[k]
+        for j, k in enumerate(axes):
+            d.red[j], d.xrs[j] = x.shape[k], st[k]
+        d.y, d.y_code, d.y_so = y.ptr, y.code, y.so
+        d.out_scale, d.out_zp, d.qmin, d.qmax = self._qargs(o)
+        self.keep.extend([x.buf, y.buf, d])
+        self._add(f"fallback:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_fb_reduce_mean(ctypes.byref(d), s),
+            "qa_d_fb_reduce_mean"))
+        if not shape:
+            y = DeviceTensor.nd(y.buf, y.offset, (), (), y.code, y.so, y.qp)
+        return [y]
+
+    def _plan_fb_softmax(self, layer, x, log):
+        """Softmax / LogSoftmax over any axis, float64 rows."""
+        node = layer.node
+        nd = len(x.shape)
+        ax = node.attr("axis", -1 if self.graph.opset >= 13 else 1)
+        ax = ax + nd if ax < 0 else ax
+
+        def form(t):
+            st = t.nd_strides
+            so_, si = _collapse(t.shape, st, 0, ax), \
+                _collapse(t.shape, st, ax + 1, nd)
+            return None if so_ is None or si is None else (so_, st[ax], si)
+
+        if form(x) is None:
+            x = self._contiguous(f"copy:{layer.name}", x)
+        o = layer.out_qp[0]
+        y = self._new(x.shape, o, dense=nd not in (2, 4))
+        if form(y) is None:
+            y = self._new(x.shape, o, dense=True)
+        (xo, xk, xi), (yo, yk, yi) = form(x), form(y)
+        d = FbSoftmax()
+        d.x, d.x_code, d.x_so = x.ptr, x.code, x.so
+        d.x_zp, d.x_scale = int(layer.in_qp[0].zp), float(layer.in_qp[0].scale)
+        d.outer = int(np.prod(x.shape[:ax], dtype=np.int64))
+        d.len = x.shape[ax]
+        d.inner = int(np.prod(x.shape[ax + 1:], dtype=np.int64))
+        d.xs_o, d.xs_k, d.xs_i = xo, xk, xi
+        d.y, d.y_code, d.y_so = y.ptr, y.code, y.so
+        d.ys_o, d.ys_k, d.ys_i = yo, yk, yi
+        d.log = int(log)
+        d.out_scale, d.out_zp, d.qmin, d.qmax = self._qargs(o)
+        self.keep.extend([x.buf, y.buf, d])
+        self._add(f"fallback:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_fb_softmax(ctypes.byref(d), s), "qa_d_fb_softmax"))
+        return [y]
+
+    def _plan_fb_avgpool(self, layer, x):
+        node = layer.node
+        if len(x.shape) != 4:
+            raise NotImplementedError("AveragePool that is not 2-D")
+        n, c, h, w = x.shape
+        k, s_, _, p = float_ops.pool_geometry(node, (h, w))
+        oh = (h + p[0] + p[2] - k[0]) // s_[0] + 1
+        ow = (w + p[1] + p[3] - k[1]) // s_[1] + 1
+        o = layer.out_qp[0]
+        y = self._new((n, c, oh, ow), o)
+        d = FbAvgPool()
+        d.x, d.x_code, d.x_so = x.ptr, x.code, x.so
+        d.x_zp, d.x_scale = int(layer.in_qp[0].zp), float(layer.in_qp[0].scale)
+        d.x_sn, d.x_sc, d.x_sh, d.x_sw = x.nd_strides
+        d.N, d.C, d.H, d.W, d.OH, d.OW = n, c, h, w, oh, ow
+        d.KH, d.KW, d.SH, d.SW, d.PT, d.PL = k[0], k[1], s_[0], s_[1], p[0], \
+            p[1]
+        d.count_pad = int(node.attr("count_include_pad", 0))
+        d.y, d.y_code, d.y_so = y.ptr, y.code, y.so
+        d.y_sn, d.y_sc, d.y_sh, d.y_sw = y.nd_strides
+        d.out_scale, d.out_zp, d.qmin, d.qmax = self._qargs(o)
+        self.keep.extend([x.buf, y.buf, d])
+        self._add(f"fallback:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_fb_avgpool(ctypes.byref(d), s), "qa_d_fb_avgpool"))
+        return [y]
+
+    def _plan_fb_copy(self, layer, x):
+        """Expand (a broadcast copy) and Cast to float: the values move, and
+        are requantized with the output parameters."""
+        node = layer.node
+        shape = x.shape
+        if node.op_type == "Expand":
+            tgt = tuple(self._const_list(node, 1, "shape"))
+            shape = tuple(np.broadcast_shapes(x.shape, tgt))
+        o, iq = layer.out_qp[0], layer.in_qp[0]
+        y = self._new(shape, o, dense=len(shape) not in (2, 4))
+        nd = len(shape)
+        st = x.nd_strides
+        xs = [0] * nd
+        for j in range(1, len(x.shape) + 1):
+            if x.shape[-j] != 1:
+                xs[-j] = st[-j]
+        xv = DeviceTensor.nd(x.buf, x.offset, shape, xs, x.code, x.so, x.qp)
+        self._copy(f"fallback:{layer.name}", xv, y, mode=2,
+                   requant=(float(iq.scale), int(iq.zp), float(o.scale),
+                            int(o.zp), int(o.qmin), int(o.qmax)))
+        return [y]
 
     def _plan_layernorm(self, layer, x):
         """LayerNormalization over the last axis (float fallback)."""
         node = layer.node
         ax = node.attr("axis", -1)
-        if ax not in (-1, len(x.shape) - 1):
-            raise NotImplementedError("LayerNorm over more than the last axis")
+        ax = ax + len(x.shape) if ax < 0 else ax
+        out_shape = x.shape
+        if ax != len(x.shape) - 1:
+            # the trailing axes as one row of a dense row-major view
+            x = self._contiguous(f"copy:{layer.name}", x)
+            cols = int(np.prod(x.shape[ax:], dtype=np.int64))
+            rows = int(np.prod(x.shape[:ax], dtype=np.int64))
+            x = DeviceTensor.nd(x.buf, x.offset, (rows, cols), (cols, 1),
+                                x.code, x.so, x.qp)
         init = self.graph.initializers
         p = self._params(layer)
         if "gamma" not in p:
@@ -1304,6 +1642,11 @@ class DeviceExecutor:
                 g.data_ptr(), None if b is None else b.data_ptr(), eps,
                 y.ptr, y.code, yrs, o.scale, o.zp, o.qmin, o.qmax, y.so, s),
             "qa_d_layernorm"))
+        if y.shape != out_shape:  # back to the operator's shape (dense)
+            st = tuple(int(np.prod(out_shape[k + 1:], dtype=np.int64))
+                       for k in range(len(out_shape)))
+            y = DeviceTensor.nd(y.buf, y.offset, out_shape, st, y.code, y.so,
+                                y.qp)
         return [y]
 
     def _plan_matmul_act(self, layer, a, b):

@@ -272,6 +272,15 @@ def _softmax(node, ins, opset, **kw):
     return (e / e.sum(axis=ax, keepdims=True)).astype(np.float32)
 
 
+@_reg("LogSoftmax")
+def _log_softmax(node, ins, opset, **kw):
+    x = ins[0].astype(np.float64)
+    ax = _axis(node.attr("axis", -1 if opset >= 13 else 1), x.ndim)
+    z = x - x.max(axis=ax, keepdims=True)
+    return (z - np.log(np.exp(z).sum(axis=ax, keepdims=True))).astype(
+        np.float32)
+
+
 @_reg("LayerNormalization")
 def _layer_norm(node, ins, opset, **kw):
     x = ins[0].astype(np.float64)
@@ -499,3 +508,51 @@ def _dequantize_linear(node, ins, opset, **kw):
     zpf = _per_axis(np.asarray(zp), q, axis).astype(np.float32)
     scale = _per_axis(np.asarray(ins[1], np.float32), q, axis)
     return ((q.astype(np.float32) - zpf) * scale).astype(np.float32)
+
+
+@_reg("Expand")
+def _expand(node, ins, opset, **kw):
+    shape = tuple(int(v) for v in np.asarray(ins[1]).reshape(-1))
+    return np.broadcast_to(ins[0], np.broadcast_shapes(ins[0].shape,
+                                                       shape)).copy()
+
+
+# ONNX TensorProto data types of Cast's "to"
+CAST_TYPES = {1: np.float32, 2: np.uint8, 3: np.int8, 4: np.uint16,
+              5: np.int16, 6: np.int32, 7: np.int64, 9: np.bool_,
+              10: np.float16, 11: np.float64}
+
+
+@_reg("Cast")
+def _cast(node, ins, opset, **kw):
+    to = node.attr("to")
+    if to not in CAST_TYPES:
+        raise UnsupportedOp(f"Cast to data type {to}")
+    return ins[0].astype(CAST_TYPES[to])
+
+
+@_reg("AveragePool")
+def _avgpool(node, ins, opset, **kw):
+    """Window sums of the zero-padded input over the window's element count
+    (or the whole window with count_include_pad), float32."""
+    x = ins[0].astype(np.float32)
+    kernel, strides, _, pads = pool_geometry(node, x.shape[2:])
+    pad = ((0, 0), (0, 0), (pads[0], pads[2]), (pads[1], pads[3]))
+    win = sliding_window_view(np.pad(x, pad), tuple(kernel), axis=(2, 3))
+    total = win[:, :, ::strides[0], ::strides[1]].sum(axis=(4, 5))
+    if node.attr("count_include_pad", 0):
+        return (total / (kernel[0] * kernel[1])).astype(np.float32)
+    ones = np.pad(np.ones_like(x[:1, :1]), pad)
+    cnt = sliding_window_view(ones, tuple(kernel), axis=(2, 3))[
+        :, :, ::strides[0], ::strides[1]].sum(axis=(4, 5))
+    return (total / cnt).astype(np.float32)
+
+
+@_reg("ReduceMean")
+def _reduce_mean(node, ins, opset, **kw):
+    x = ins[0]
+    axes = (np.asarray(ins[1]).astype(np.int64).tolist()
+            if len(ins) > 1 and ins[1] is not None else node.attr("axes"))
+    axes = tuple(_axis(a, x.ndim) for a in axes) if axes else None
+    return x.mean(axis=axes, keepdims=bool(node.attr("keepdims", 1))).astype(
+        np.float32)

@@ -100,6 +100,11 @@ def _declare(lib):
         "qa_d_dequantize_f32": (i32, [p, i32, p, i64, f64, i64, i64, p]),
         "qa_d_pad_nd": (i32, [p, p]),
         "qa_d_maxpool": (i32, [p, p]),
+        "qa_d_fb_binary": (i32, [p, p]),
+        "qa_d_binary_nd": (i32, [p, p]),
+        "qa_d_fb_reduce_mean": (i32, [p, p]),
+        "qa_d_fb_softmax": (i32, [p, p]),
+        "qa_d_fb_avgpool": (i32, [p, p]),
         "qa_noalloc_scratch_bytes": (i64, []),
         "qa_gemm_i16_i32_noalloc_need": (i64, [i64] * 3),
         "qa_gemm_i16_i32_noalloc": (i32, [i64] * 3 + [p] * 4),
