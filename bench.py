@@ -74,10 +74,12 @@ def parse():
                         "instead of using the committed set")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the ViT-S and int16 YOLOv8n-cls passes")
-    p.add_argument("--only", choices=("vit", "int16", "gemm"),
-                   help="time only that pass (ViT-S/16 int8 b32 or "
-                        "YOLOv8n-cls int16) and print its record, e.g. "
-                        "under a profiler")
+    p.add_argument("--only", choices=("vit", "int16", "gemm", "kernels"),
+                   help="time only that pass (ViT-S/16 int8 b32, "
+                        "YOLOv8n-cls int16, the ViT-S weight GEMMs, or the "
+                        "standalone GEMM / conv / requantize / table "
+                        "kernels) and print its records, e.g. under a "
+                        "profiler")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="finish with one device copy of MIB MiB (a plain "
                         "copy kernel that calibrates byte counters)")
@@ -164,6 +166,51 @@ def measure_pass(name, g, quant_type, batch, steps, tune, torch):
             "params": g.num_params()}, c
 
 
+def kernel_rows(tune, torch, steps=50):
+    """The standalone GEMM + requantize and conv + requantize + SiLU table
+    workloads (int8 TOPS) and the element-wise requantize / table kernels
+    (HBM GB/s), each timed over ``steps`` launches."""
+    from quantanything_amd.workloads import (
+        ConvWorkload,
+        GemmWorkload,
+        LutWorkload,
+        RequantizeWorkload,
+    )
+
+    kernels = []
+    for wl in (GemmWorkload(), ConvWorkload()):
+        code = 0
+        if tune:  # the same plan-time tile timing as the pass
+            from quantanything_amd.executor import DeviceExecutor
+
+            wl.launch()
+            times = {}
+            for c_ in DeviceExecutor.tile_candidates(wl.d):
+                wl.d.tile = c_
+                times[c_] = DeviceExecutor._time_launch(wl.launch, 8, 3)
+            code = min(times, key=times.get)
+            wl.d.tile = code
+        kms = time_launch(wl.launch, steps, torch)
+        r = roofline(wl.ops, wl.bytes, kms)
+        tops = wl.ops / (kms * 1e-3) / 1e12
+        kernels.append({"workload": wl.name, "tile": hex(code),
+                        "avg_ms": round(kms, 5),
+                        "int8_tops": round(tops, 2),
+                        "frac_of_mfma_peak": round(tops / PEAK_I8_TOPS, 4),
+                        "roofline": r})
+
+    for wl in (RequantizeWorkload(), LutWorkload()):
+        kms = time_launch(wl.launch, steps, torch)
+        gbs = wl.bytes / (kms * 1e-3) / 1e9
+        kernels.append({"workload": wl.name, "avg_ms": round(kms, 5),
+                        "bytes_per_launch": wl.bytes,
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                     "traffic": None}})
+    return kernels
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -183,15 +230,14 @@ def main():
     from quantanything_amd.container import QuantContainer
     from quantanything_amd.synth import Stream
     from quantanything_amd import synth
-    from quantanything_amd.workloads import (
-        ConvWorkload,
-        GemmWorkload,
-        LutWorkload,
-        RequantizeWorkload,
-    )
+    from quantanything_amd.workloads import GemmWorkload
 
     native.require()
     B = args.batch
+    if args.only == "kernels":  # the standalone kernel workloads alone
+        for row in kernel_rows(not args.no_tune, torch, args.steps):
+            print(json.dumps(row), flush=True)
+        return 0
     if args.only == "gemm":  # the weight GEMM shapes of a ViT-S block
         from quantanything_amd.workloads import vit_gemm_shapes
 
@@ -388,37 +434,7 @@ def main():
         if top_name in measured:
             roof["traffic"] = measured[top_name]
 
-    kernels = []
-    for wl in (GemmWorkload(), ConvWorkload()):
-        code = 0
-        if not args.no_tune:  # the same plan-time tile timing as the pass
-            from quantanything_amd.executor import DeviceExecutor
-
-            wl.launch()
-            times = {}
-            for c_ in DeviceExecutor.tile_candidates(wl.d):
-                wl.d.tile = c_
-                times[c_] = DeviceExecutor._time_launch(wl.launch, 8, 3)
-            code = min(times, key=times.get)
-            wl.d.tile = code
-        kms = time_launch(wl.launch, 50, torch)
-        r = roofline(wl.ops, wl.bytes, kms)
-        tops = wl.ops / (kms * 1e-3) / 1e12
-        kernels.append({"workload": wl.name, "tile": hex(code),
-                        "avg_ms": round(kms, 5),
-                        "int8_tops": round(tops, 2),
-                        "frac_of_mfma_peak": round(tops / PEAK_I8_TOPS, 4),
-                        "roofline": r})
-
-    for wl in (RequantizeWorkload(), LutWorkload()):
-        kms = time_launch(wl.launch, 50, torch)
-        gbs = wl.bytes / (kms * 1e-3) / 1e9
-        kernels.append({"workload": wl.name, "avg_ms": round(kms, 5),
-                        "bytes_per_launch": wl.bytes,
-                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
-                                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                     "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                     "traffic": None}})
+    kernels = kernel_rows(not args.no_tune, torch)
 
     # ---- the other end-to-end configurations (parity: tests/) ------------
     extra = []

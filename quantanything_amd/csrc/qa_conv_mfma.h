@@ -236,6 +236,29 @@ __device__ __forceinline__ int64_t quant_general(const ConvArgs& a,
     return q;
 }
 
+// med3(x, lo, hi) = clip(x, lo, hi) for lo <= hi, as one VALU instruction
+// (the compiler otherwise emits a max and a min).
+__device__ __forceinline__ int med3_i32(int x, int lo, int hi) {
+    int r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(lo), "v"(hi));
+    return r;
+}
+
+// q0 = (w*m + c) >> t for a table-plan constant c that has the channel's
+// correction term folded in: c = c_plan + corr*m (mod 2^64). w is the raw
+// MFMA sum and w + corr the corrected int32 accumulator, exact when
+// |w| + |corr| < 2^31 (8-bit operands, K < 2^16); the sum w*m + c equals
+// (w + corr)*m + c_plan, which the planner keeps within int64, so the
+// modular arithmetic gives it exactly.
+__device__ __forceinline__ int plan_q0(int w, int m, int64_t c, int t) {
+    return (int)((int64_t)((uint64_t)((int64_t)w * m) + (uint64_t)c) >> t);
+}
+
+// The table-plan constant with the correction term folded in (see plan_q0).
+__device__ __forceinline__ int64_t plan_fold(int64_t c, uint32_t corr, int m) {
+    return (int64_t)((uint64_t)c + (uint64_t)((int64_t)(int)corr * m));
+}
+
 // Low bytes of four table entries packed into one word (byte = 0), or their
 // second bytes (byte = 1).
 __device__ __forceinline__ uint32_t pack_entries(const int e[4], int byte) {

@@ -24,7 +24,8 @@
 // their weights are zero).
 //
 // Epilogue: the int8 table plan of qa_conv.h (per-channel multiply-add and
-// shift, 256-entry clip / activation / residual / copy tables), 4 channels
+// shift with the zero-point correction folded into the constant, one med3
+// clip, 256-entry clip / activation / residual / copy tables), 4 channels
 // of a pixel stored as one word after a 4x4 byte transpose within each
 // lane quad, residual words fetched before the tile's MFMAs.
 #include "qa_conv_mfma.h"
@@ -36,6 +37,7 @@ constexpr int WR_NW = 8;          // waves per work-group
 constexpr int WR_NT = 64 * WR_NW;  // threads per work-group
 constexpr int WR_SB = 8;          // band chunks (16 bytes) a thread stages
 constexpr int WR_SW = 8;          // weight chunks a thread stages
+constexpr int WR_HB = 2;          // band rounds held through phase 0
 
 // K-step counts the kernel is instantiated for (a layer runs the smallest
 // one >= its K-steps); WM channel tiles hold at most 36 / WM steps (144
@@ -80,6 +82,8 @@ __device__ __forceinline__ int wr_div(int n, uint32_t m) {
 template <int WM, int KS, bool RES, bool CH>
 __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
                                                    ConvArgs a2) {
+    constexpr int NW = WR_NW, NT = WR_NT;
+    constexpr int SB = WR_SB, SW = WR_SW, HB = WR_HB;
     extern __shared__ int4 lds4[];
     int8_t* s_band = (int8_t*)lds4;                          // band
     int8_t* s_w = s_band + bg.band_bytes;                    // weights
@@ -115,55 +119,122 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
     // e < nreal is pixel e / cpp, 16-byte part e % cpp, at band row
     // r_lo + p / W, column PW + p % W (columns past the band's width are
     // loaded and dropped); weight chunk e is row e / KGp, part e % KGp.
-    // Every load of the thread (WR_SB band and WR_SW weight chunks) is
-    // issued before its stores, from straight-line code with few
-    // instructions a chunk (it runs once, from a cold instruction cache);
-    // the pad value fills the band's other positions in a separate loop.
-    const int r_lo = max(0, -iy0), r_hi = min(bg.BR, a.H - iy0);
-    const int nreal = max(r_hi - r_lo, 0) * a.W * cpp;
+    // Every load of the thread (band and weight chunks, in rounds of NT
+    // chunks; rounds past the data are skipped) is issued before its
+    // stores, from straight-line code with few instructions a chunk (it
+    // runs once, from a cold instruction cache); the pad value fills the
+    // band's other positions. The band's rounds are stored in two phases:
+    // all but the last nh <= HB rounds before the first barrier, the
+    // held ones after the tiles that need only the earlier rows (phase 0)
+    // have been computed, so that the later loads' latency overlaps phase
+    // 0's MFMAs.
+    const int r_lo = max(0, -iy0);
+    const int r_hi = max(min(bg.BR, a.H - iy0), r_lo);
+    const int nreal = (r_hi - r_lo) * a.W * cpp;
+    const int nr = (nreal + NT - 1) / NT;  // rounds of band chunks
+    const int nh = min(HB, max(nr - 1, 0));  // the last rounds, held
+    const int h = nr - nh;                       // rounds stored first
+    v4i vx[SB], vh[HB];
+    int ax[SB], axh[HB];
+    const int xsp = (int)a.x_sp;
+    const int8_t* xrow = xn + (int64_t)(iy0 + r_lo) * a.W * a.x_sp;
+    const int colmax = bg.BW - a.PW;  // real columns kept
+    auto load_round = [&](int u, v4i& v, int& at) {
+        const int e = tid + u * NT;
+        const int p = cpp == 1 ? e : wr_div(e, bg.m_cpp);
+        const int ch = e - p * cpp;
+        const int row = wr_div(p, bg.m_w), ix = p - row * a.W;
+        const bool ok = e < nreal && ix < colmax;
+        at = ok ? ((r_lo + row) * bg.BW + ix + a.PW) * bg.PS + ch * 16 : -1;
+        v = *(const v4i*)(xrow + (e < nreal ? p * xsp + ch * 16 : 0));
+    };
+    // weights, tables and per-channel constants: loaded first and stored
+    // behind their own barrier, so that the weights' copy into registers
+    // overlaps the band's loads (the loads complete in issue order)
     {
-        v4i vx[WR_SB], vw[WR_SW];
-        int ax[WR_SB], aw[WR_SW];
-        {
-            const int xsp = (int)a.x_sp;
-            const int8_t* xrow = xn + (int64_t)(iy0 + r_lo) * a.W * a.x_sp;
-            const int colmax = bg.BW - a.PW;  // real columns kept
-#pragma unroll
-            for (int u = 0; u < WR_SB; ++u) {
-                const int e = tid + u * WR_NT;
-                const int p = cpp == 1 ? e : wr_div(e, bg.m_cpp);
-                const int ch = e - p * cpp;
-                const int row = wr_div(p, bg.m_w), ix = p - row * a.W;
-                const bool ok = e < nreal && ix < colmax;
-                ax[u] = ok ? ((r_lo + row) * bg.BW + ix + a.PW) * bg.PS +
-                                 ch * 16
-                           : -1;
-                vx[u] = *(const v4i*)(xrow + (e < nreal ? p * xsp + ch * 16
-                                                        : 0));
-            }
-        }
+        v4i vw[SW];
+        int aw[SW];
         {
             const int wrs = (int)a.wp_rstride;
             const int8_t* wrow = a.wp + (int64_t)co0 * a.wp_rstride;
 #pragma unroll
-            for (int u = 0; u < WR_SW; ++u) {
-                const int e = tid + u * WR_NT;
-                const int r = wr_div(e, bg.m_kgp), k = e - r * KGp;
-                const bool ok = e < wch;
-                aw[u] = ok ? r * bg.RSW + k * 16 : -1;
-                vw[u] = *(const v4i*)(wrow + (ok ? r * wrs + k * 16 : 0));
+            for (int u = 0; u < SW; ++u) {
+                aw[u] = -1;
+                if (u * NT < wch) {
+                    const int e = tid + u * NT;
+                    const int r = wr_div(e, bg.m_kgp), k = e - r * KGp;
+                    const bool ok = e < wch;
+                    aw[u] = ok ? r * bg.RSW + k * 16 : -1;
+                    vw[u] = *(const v4i*)(wrow + (ok ? r * wrs + k * 16 : 0));
+                }
             }
         }
-        // pad value: band rows outside the image, columns left of the
-        // image and right of it
-        for (int e = tid; e < nch; e += WR_NT) {
-            const int p = cpp == 1 ? e : wr_div(e, bg.m_cpp);
-            const int ch = e - p * cpp;
-            const int row = wr_div(p, bg.m_bw), col = p - row * bg.BW;
-            if (row < r_lo || row >= r_hi || col < a.PW || col >= a.PW + a.W)
-                *(v4i*)(s_band + p * bg.PS + ch * 16) = pad4;
+        constexpr int NTV = (768 + NT - 1) / NT;
+        int tv[NTV];
+#pragma unroll
+        for (int j = 0; j < NTV; ++j)
+            tv[j] = tid + j * NT < 768
+                        ? ((const int*)((const char*)a.plan +
+                                        PLAN_E))[tid + j * NT]
+                        : 0;
+        int4 pcv = int4{0, 0, 0, 0};
+        uint32_t corrv = 0;
+        if (tid < WM * 16) {
+            const int c = min(co0 + tid, a.Cout - 1);
+            pcv = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
+            corrv = a.corr ? (uint32_t)a.corr[c] : 0u;
         }
-        for (int kg = tid; kg < 4 * KS; kg += WR_NT) {
+        // a2's weight rows (4 chunks each, K = one 64-byte step), table
+        // and constants
+        v4i w2v = v4i{0, 0, 0, 0};
+        int t2v = 0;
+        int4 pc2v = int4{0, 0, 0, 0};
+        uint32_t corr2v = 0;
+        if (CH) {
+            if (tid < WM * 16 * 4)
+                w2v = *(const v4i*)(a2.wp + (int64_t)(tid >> 2) * a2.wp_rstride +
+                                    (tid & 3) * 16);
+            if (tid < 256)
+                t2v = ((const int*)((const char*)a2.plan + PLAN_E))[tid];
+            if (tid < WM * 16) {
+                pc2v = ((const int4*)((const char*)a2.plan + PLAN_CH))[tid];
+                corr2v = a2.corr ? (uint32_t)a2.corr[tid] : 0u;
+            }
+        }
+        // the band: rounds stored after the first barrier, then the held
+        // ones (issued last)
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+            ax[u] = -1;
+            if (u < h) load_round(u, vx[u], ax[u]);
+        }
+#pragma unroll
+        for (int j = 0; j < HB; ++j) {
+            axh[j] = -1;
+            if (j < nh) load_round(h + j, vh[j], axh[j]);
+        }
+        // pad value: band rows outside the image (all columns), then the
+        // columns left and right of the image on the other rows
+        {
+            const int rowc = bg.BW * cpp;  // chunks of a band row
+            const int nprow = r_lo + (bg.BR - r_hi);
+            for (int e = tid; e < nprow * rowc; e += NT) {
+                const int rr = e / rowc, c = e - rr * rowc;
+                const int row = rr < r_lo ? rr : r_hi + (rr - r_lo);
+                *(v4i*)(s_band + row * bg.BW * bg.PS + (c / cpp) * bg.PS +
+                        (c % cpp) * 16) = pad4;
+            }
+            const int rpad = max(bg.BW - a.PW - a.W, 0);  // right columns
+            const int pc = (a.PW + rpad) * cpp;           // chunks a row
+            for (int e = tid; e < (r_hi - r_lo) * pc; e += NT) {
+                const int rr = e / pc, c = e - rr * pc;
+                const int j = c / cpp, ch = c - j * cpp;
+                const int col = j < a.PW ? j : a.W + j;
+                *(v4i*)(s_band + ((r_lo + rr) * bg.BW + col) * bg.PS +
+                        ch * 16) = pad4;
+            }
+        }
+        for (int kg = tid; kg < 4 * KS; kg += NT) {
             int off = 0;  // padding k-groups: any in-band address
             if (kg < a.KG) {
                 const int tap = kg / a.CB, cb = kg - tap * a.CB;
@@ -172,39 +243,40 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
             }
             s_kt[kg] = off;
         }
-        for (int i = tid; i < 768; i += WR_NT)
-            s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
+        // weight rows past KGp chunks up to the instantiated K-steps: zero
+        if (4 * KS > KGp) {
+            const int tail = 4 * KS - KGp;
+            for (int e = tid; e < WM * 16 * tail; e += NT) {
+                const int r = e / tail;
+                *(v4i*)(s_w + r * bg.RSW + (KGp + e - r * tail) * 16) =
+                    v4i{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SW; ++u)
+            if (aw[u] >= 0) *(v4i*)(s_w + aw[u]) = vw[u];
+#pragma unroll
+        for (int j = 0; j < NTV; ++j)
+            if (tid + j * NT < 768) s_tab[tid + j * NT] = tv[j];
         if (tid < WM * 16) {
-            const int c = min(co0 + tid, a.Cout - 1);
-            s_pc[tid] = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
-            s_corr[tid] = a.corr ? (uint32_t)a.corr[c] : 0u;
+            s_pc[tid] = pcv;
+            s_corr[tid] = corrv;
         }
         if (CH) {
-            // a2's weight rows: 4 chunks each (K = one 64-byte step)
-            for (int e = tid; e < WM * 16 * 4; e += WR_NT) {
-                const int r = e >> 2, k = e & 3;
-                *(v4i*)(s_w2 + r * 80 + k * 16) =
-                    *(const v4i*)(a2.wp + (int64_t)r * a2.wp_rstride + k * 16);
-            }
-            for (int i = tid; i < 256; i += WR_NT)
-                s_tab2[i] = ((const int*)((const char*)a2.plan + PLAN_E))[i];
+            if (tid < WM * 16 * 4)
+                *(v4i*)(s_w2 + (tid >> 2) * 80 + (tid & 3) * 16) = w2v;
+            if (tid < 256) s_tab2[tid] = t2v;
             if (tid < WM * 16) {
-                s_pc2[tid] = ((const int4*)((const char*)a2.plan + PLAN_CH))[tid];
-                s_corr2[tid] = a2.corr ? (uint32_t)a2.corr[tid] : 0u;
+                s_pc2[tid] = pc2v;
+                s_corr2[tid] = corr2v;
             }
         }
-#pragma unroll
-        for (int u = 0; u < WR_SB; ++u)
-            if (ax[u] >= 0) *(v4i*)(s_band + ax[u]) = vx[u];
-#pragma unroll
-        for (int u = 0; u < WR_SW; ++u)
-            if (aw[u] >= 0) *(v4i*)(s_w + aw[u]) = vw[u];
     }
     __syncthreads();
 
     // weights of the lane: channel tile i, K-step s: row co0 + 16 i + col,
-    // bytes 64 s + 16 kgl
-    // (steps past KGp / 4 hold zeros); band offsets of its k-groups
+    // bytes 64 s + 16 kgl (steps past KGp / 4 hold zeros); band offsets of
+    // its k-groups
     v4i wb[KS][WM];
     int kt[KS];
 #pragma unroll
@@ -212,28 +284,30 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
         kt[s] = s_kt[4 * s + kgl];
 #pragma unroll
         for (int i = 0; i < WM; ++i)
-            wb[s][i] = 4 * s < KGp ? *(const v4i*)(s_w + (16 * i + col) * bg.RSW +
-                                                   64 * s + 16 * kgl)
-                                   : v4i{0, 0, 0, 0};
+            wb[s][i] = *(const v4i*)(s_w + (16 * i + col) * bg.RSW + 64 * s +
+                                     16 * kgl);
     }
+    // per-channel plan constants, the correction term folded in (plan_q0;
+    // K <= 36 K-steps: |w| + |corr| < 2^27)
     int cm[WM], ct[WM];
     int64_t cc[WM];
-    uint32_t ccorr[WM];
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
         const int4 pc = s_pc[16 * i + col];
         cm[i] = pc.x;
         ct[i] = pc.y;
-        cc[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
-        ccorr[i] = s_corr[16 * i + col];
+        cc[i] = plan_fold(
+            (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z),
+            s_corr[16 * i + col], pc.x);
     }
     const int4 hdr = *(const int4*)a.plan;
     const int pA = hdr.x, pB = hdr.y, pSH = hdr.z;
+    const int* tabE = s_tab - pA;  // tabE[v] = E[v - pA] for v in [pA, pB]
+    const int* tabC = s_tab + 256 - pA;
     // CH: a2's weight fragments (one K-step) and per-channel constants
     v4i wb2[CH ? WM : 1];
     int cm2[CH ? WM : 1], ct2[CH ? WM : 1];
     int64_t cc2[CH ? WM : 1];
-    uint32_t ccorr2[CH ? WM : 1];
     int4 hdr2 = int4{0, 0, 0, 0};
     if (CH) {
 #pragma unroll
@@ -242,12 +316,19 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
             const int4 pc = s_pc2[16 * i + col];
             cm2[i] = pc.x;
             ct2[i] = pc.y;
-            cc2[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
-                               (uint32_t)pc.z);
-            ccorr2[i] = s_corr2[16 * i + col];
+            cc2[i] = plan_fold((int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                                         (uint32_t)pc.z),
+                               s_corr2[16 * i + col], pc.x);
         }
         hdr2 = *(const int4*)a2.plan;
     }
+    const int* tabE2 = s_tab2 - hdr2.x;
+    // the band's first rounds (the loads have had the weights' copy to
+    // arrive)
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+        if (ax[u] >= 0) *(v4i*)(s_band + ax[u]) = vx[u];
+    __syncthreads();
     int8_t* s_tw = s_t + wave * (16 * 80);  // this wave's tile (CH)
     const int q = lane & 3;
     const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
@@ -271,59 +352,69 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
                 rw[i] = ok && c0 < a.Cout ? *(const uint32_t*)(pr + c0) : 0u;
             }
         };
-        uint32_t rwn[WM];
-        if (RES) load_res(wave, rwn);
-        for (int t = wave; t < ntile; t += WR_NW) {
-            const int pq = 16 * t + 4 * kgl + q;  // pixel within the band
-            const bool pok = pq < npix;
-            const int64_t p = pimg + pq;
-            uint32_t rw[WM];
-            if (RES) {
-#pragma unroll
-                for (int i = 0; i < WM; ++i) rw[i] = rwn[i];
-                if (t + WR_NW < ntile) load_res(t + WR_NW, rwn);
-            }
-            // the lane's pixel (rows of the MFMA) in the band buffer
+        // activation fragments of tile t: the lane's pixel (rows of the
+        // MFMA) in the band buffer, one 16-byte read per K-step (tiles past
+        // the band read its last pixel)
+        auto frags = [&](v4i (&f)[KS], int t) {
             const int qp = min(16 * t + col, npix - 1);
             const int r = wr_div(qp, bg.m_ow), ox = qp - r * a.OW;
             const int8_t* xb = sb + (r * a.SH * bg.BW + ox * a.SW) * bg.PS;
-            v4i acc[WM];
 #pragma unroll
-            for (int i = 0; i < WM; ++i) acc[i] = v4i{0, 0, 0, 0};
-            v4i fa[KS];
+            for (int s = 0; s < KS; ++s) f[s] = *(const v4i*)(xb + kt[s]);
+        };
+        auto mfmas = [&](const v4i (&f)[KS], v4i (&c)[WM]) {
 #pragma unroll
-            for (int s = 0; s < KS; ++s) fa[s] = *(const v4i*)(xb + kt[s]);
+            for (int i = 0; i < WM; ++i) c[i] = v4i{0, 0, 0, 0};
 #pragma unroll
             for (int s = 0; s < KS; ++s)
 #pragma unroll
                 for (int i = 0; i < WM; ++i)
-                    acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        fa[s], wb[s][i], acc[i], 0, 0, 0);
-            // epilogue: lane holds pixels 4 kgl + r, channel co0 + 16 i + col
+                    c[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        f[s], wb[s][i], c[i], 0, 0, 0);
+        };
+        // epilogue, branch-free part: lane holds pixels 4 kgl + r, channel
+        // co0 + 16 i + col. Per value: multiply-add, shift, one med3 clip
+        // and one table read whose address folds in the clip's lower
+        // bound; every table read of the tile is issued before the first
+        // use. e4 gets the entries (bits 0..7 the stored byte of y, 8..15
+        // that of y2).
+        auto epi_math = [&](const v4i (&c)[WM], const uint32_t (&rw)[WM],
+                            int (&e4)[WM][4]) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    e4[i][rr] = med3_i32(
+                        plan_q0(c[i][rr], cm[i], cc[i], ct[i]), pA, pB);
 #pragma unroll
             for (int i = 0; i < WM; ++i) {
-                int e[4];
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const uint32_t wu = (uint32_t)acc[i][rr] + ccorr[i];
-                    const int q0 =
-                        (int)(((int64_t)(int)wu * cm[i] + cc[i]) >> ct[i]);
-                    e[rr] = min(max(q0, pA), pB) - pA;
-                }
                 if (RES) {
                     const uint32_t rv = quad_transpose(rw[i], sel1, sel2);
 #pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) {
-                        const int v = s_tab[256 + e[rr]] +
-                                      s_tab[512 + ((rv >> (8 * rr)) & 255)];
-                        e[rr] = min(max(v, 0), pSH);
-                    }
-                }
+                    for (int rr = 0; rr < 4; ++rr)
+                        e4[i][rr] = tabC[e4[i][rr]] +
+                                    s_tab[512 + ((rv >> (8 * rr)) & 255)];
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) e[rr] = s_tab[e[rr]];
+                    for (int rr = 0; rr < 4; ++rr)
+                        e4[i][rr] = s_tab[med3_i32(e4[i][rr], 0, pSH)];
+                } else {
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) e4[i][rr] = tabE[e4[i][rr]];
+                }
+            }
+        };
+        // the stores of tile t: 4 channels of a pixel as one word (CH: the
+        // wave's LDS tile)
+        auto epi_store = [&](int t, const int (&e4)[WM][4], bool tok) {
+            const int pq = 16 * t + 4 * kgl + q;  // pixel within the band
+            const bool pok = tok && pq < npix;
+            const int64_t p = pimg + pq;
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
                 const int c0 = co0 + 16 * i + cq;  // Cout % 4 == 0
                 const bool sok = pok && c0 < a.Cout;
-                const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
+                const uint32_t wy =
+                    quad_transpose(pack_entries(e4[i], 0), sel1, sel2);
                 if (CH) {  // pixel 4 kgl + q of the tile, channels c0 ..
                     *(uint32_t*)(s_tw + (4 * kgl + q) * 80 + c0) = wy;
                     continue;
@@ -331,10 +422,49 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
                 if (sok) *(uint32_t*)((int8_t*)a.y + p * a.y_pst + c0) = wy;
                 if (a.y2) {
                     const uint32_t w2 =
-                        quad_transpose(pack_entries(e, 1), sel1, sel2);
+                        quad_transpose(pack_entries(e4[i], 1), sel1, sel2);
                     if (sok)
                         *(uint32_t*)((int8_t*)a.y2 + p * a.y2_pst + c0) = w2;
                 }
+            }
+        };
+        // phase 0: the tiles whose input rows are all among the band rows
+        // of the first h rounds (the rows above the image count as staged)
+        int T0 = ntile;
+        if (h < nr) {
+            const int rows = r_lo + (h * NT) / (a.W * cpp);
+            const int need = (a.KH - 1) * a.DH + 1;  // band rows a row uses
+            const int orows = rows >= need ? (rows - need) / a.SH + 1 : 0;
+            T0 = min(orows * a.OW, npix) >> 4;
+        }
+#pragma unroll 1
+        for (int ph = 0; ph < 2; ++ph) {
+          if (ph == 1) {
+#pragma unroll
+              for (int j = 0; j < HB; ++j)
+                  if (axh[j] >= 0) *(v4i*)(s_band + axh[j]) = vh[j];
+              __syncthreads();
+          }
+          const int tb = ph == 0 ? 0 : T0, te = ph == 0 ? T0 : ntile;
+          uint32_t rwn[WM];
+          if (RES && tb + wave < te) load_res(tb + wave, rwn);
+          for (int t = tb + wave; t < te; t += NW) {
+            const int pq = 16 * t + 4 * kgl + q;  // pixel within the band
+            const bool pok = pq < npix;
+            const int64_t p = pimg + pq;
+            uint32_t rw[WM];
+            if (RES) {
+#pragma unroll
+                for (int i = 0; i < WM; ++i) rw[i] = rwn[i];
+                if (t + NW < te) load_res(t + NW, rwn);
+            }
+            v4i fa[KS], acc[WM];
+            frags(fa, t);
+            mfmas(fa, acc);
+            {
+                int e4[WM][4];
+                epi_math(acc, rw, e4);
+                epi_store(t, e4, true);
             }
             if (CH) {
                 // the wave's own LDS writes above, read back by other lanes
@@ -355,12 +485,10 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
                 for (int i = 0; i < WM; ++i) {
                     int e[4];
 #pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) {
-                        const uint32_t wu = (uint32_t)acc2[i][rr] + ccorr2[i];
-                        const int q0 = (int)(((int64_t)(int)wu * cm2[i] +
-                                              cc2[i]) >> ct2[i]);
-                        e[rr] = s_tab2[min(max(q0, hdr2.x), hdr2.y) - hdr2.x];
-                    }
+                    for (int rr = 0; rr < 4; ++rr)
+                        e[rr] = tabE2[med3_i32(
+                            plan_q0(acc2[i][rr], cm2[i], cc2[i], ct2[i]),
+                            hdr2.x, hdr2.y)];
                     const int c0 = 16 * i + cq;
                     const uint32_t wy =
                         quad_transpose(pack_entries(e, 0), sel1, sel2);
@@ -375,6 +503,7 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
                     }
                 }
             }
+          }
         }
     }
 }
@@ -389,7 +518,9 @@ WrGeom wr_geom(const ConvArgs& b, int wm, int R, bool ch = false) {
     g.PS = b.Cg + (((b.Cg >> 4) & 1) ? 0 : 16);
     g.bpi = (b.OH + R - 1) / R;
     g.nbands = b.N * g.bpi;
-    g.RSW = b.KGp * 16 + 16;
+    g.KSR = wr_steps(wm, b.KGp / 4);
+    // weight rows hold the instantiated K-steps (the tail chunks zeroed)
+    g.RSW = std::max<int>(4 * g.KSR, b.KGp) * 16 + 16;
     const int64_t band = (int64_t)g.BR * g.BW * g.PS;
     const int64_t bchunks = (int64_t)g.BR * b.W * (b.Cg >> 4);
     const int64_t wchunks = (int64_t)wm * 16 * b.KGp;
@@ -403,7 +534,6 @@ WrGeom wr_geom(const ConvArgs& b, int wm, int R, bool ch = false) {
     g.m_ow = magic(b.OW);
     g.m_w = magic(b.W);
     g.m_cpp = magic(b.Cg >> 4);
-    g.KSR = wr_steps(wm, b.KGp / 4);
     const int64_t bytes =
         band + (int64_t)wm * 16 * g.RSW + (int64_t)g.KSR * 16 +
         (ch ? (int64_t)wm * 16 * 80 + WR_NW * 16 * 80 : 0);
@@ -425,7 +555,9 @@ WrKern wr_kernel(int ks) {
         case 2: return &k_conv_wr<WM, 2, RES, CH>;
         case 3: return &k_conv_wr<WM, 3, RES, CH>;
         case 5: return &k_conv_wr<WM, 5, RES, CH>;
-        case 9: return &k_conv_wr<WM, 9, RES, CH>;
+        case 9:  // with the chained conv, 4 channel tiles would spill
+            if constexpr (!(CH && WM == 4)) return &k_conv_wr<WM, 9, RES, CH>;
+            break;
         case 18:
             if constexpr (WM <= 2 && !CH) return &k_conv_wr<WM, 18, RES, CH>;
             break;
@@ -437,23 +569,19 @@ WrKern wr_kernel(int ks) {
     return nullptr;
 }
 
+template <bool RES, bool CH>
+WrKern wr_kernel_wm(int wm, int ks) {
+    return wm == 1   ? wr_kernel<1, RES, CH>(ks)
+           : wm == 2 ? wr_kernel<2, RES, CH>(ks)
+           : wm == 4 ? wr_kernel<4, RES, CH>(ks)
+                     : nullptr;
+}
+
 // ch: with a chained 1x1 convolution (no residual variant)
 WrKern wr_kernel_rt(int wm, int ks, bool res, bool ch = false) {
-    if (ch)
-        return res ? nullptr
-               : wm == 1 ? wr_kernel<1, false, true>(ks)
-               : wm == 2 ? wr_kernel<2, false, true>(ks)
-               : wm == 4 ? wr_kernel<4, false, true>(ks)
-                         : nullptr;
-    if (res)
-        return wm == 1 ? wr_kernel<1, true, false>(ks)
-               : wm == 2 ? wr_kernel<2, true, false>(ks)
-               : wm == 4 ? wr_kernel<4, true, false>(ks)
-                         : nullptr;
-    return wm == 1 ? wr_kernel<1, false, false>(ks)
-           : wm == 2 ? wr_kernel<2, false, false>(ks)
-           : wm == 4 ? wr_kernel<4, false, false>(ks)
-                     : nullptr;
+    if (ch) return res ? nullptr : wr_kernel_wm<false, true>(wm, ks);
+    return res ? wr_kernel_wm<true, false>(wm, ks)
+               : wr_kernel_wm<false, false>(wm, ks);
 }
 
 // Work-groups of a kernel resident per CU with `lds` dynamic bytes.
@@ -548,7 +676,7 @@ bool conv_chain_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
     const int wm = b1.Cout / 16;
     if (!((wm == 1 || wm == 2 || wm == 4) && b1.Cout == 16 * wm &&
           conv_wr_applies(b1, epi1, wm) && b1.res == nullptr &&
-          b1.y2 == nullptr && wr_steps(wm, b1.KGp / 4) <= 9))
+          b1.y2 == nullptr && wr_steps(wm, b1.KGp / 4) <= (wm == 4 ? 5 : 9)))
         return false;
     return epi2 == Q8_TABLE && b2.mode == EPI_QUANT && b2.fastio && b2.plan &&
            b2.G == 1 && b2.layout == 0 && b2.KH == 1 && b2.KW == 1 &&
