@@ -2,6 +2,9 @@
 // and the diagnostic exports (qa_backend, qa_last_error, ...).
 #include <stdio.h>
 #include <string.h>
+#include <sys/syscall.h>
+#include <sys/types.h>
+#include <unistd.h>
 
 #include "qa_common.h"
 
@@ -26,7 +29,13 @@ struct DeviceState {
 // its buffers.
 struct ThreadState {
     DeviceState dev[kMaxDevices];
+    // A thread that ends while the process runs returns its stream and
+    // buffers. The main thread's state is destroyed only inside exit(),
+    // after which the HIP runtime (and a profiler attached to it) may
+    // already be torn down: there nothing is released, the driver reclaims
+    // the process's streams and memory.
     ~ThreadState() {
+        if ((pid_t)syscall(SYS_gettid) == getpid()) return;
         for (int d = 0; d < kMaxDevices; ++d) {
             DeviceState& s = dev[d];
             if (!s.stream) continue;
