@@ -112,36 +112,45 @@ __device__ __forceinline__ int64_t qa_quantize_one_fast(float x, double scale,
 }
 
 // float32 form of qa_quantize_one for scales in [2^-60, 2^60] and clip
-// ranges narrower than 2^20, with invf = float(1 / scale). y = x * invf is
-// within 2^-22.8 * |y| of x / scale (two float roundings), and the
-// reference's double quotient within 2^-53 of it, so when y is farther than
-// 2^-20 * |y| from every half-integer all three round to the same integer
-// (|y| < 2^21, where rintf and the int conversion are exact); when
-// |y| >= 2^21 the clip decides by the sign alone (+-2^21 + zp lies outside
-// the clip range). Otherwise (a near-tie, NaN) *slow is set and the caller
-// must use qa_quantize_one_fast.
-__device__ __forceinline__ int qa_quantize_f32(float x, float invf, int zp,
-                                               int qmin, int qmax,
+// bounds within [-2^22, 2^22] whose width B = 2 max(qmax - zp, zp - qmin) + 2
+// is at most 2^20, with invf = float(1 / scale) and tie = 0.5 - B 2^-22
+// (qa_f32_tie). r = rint(x * invf) in float32 and d = x * invf - r by one
+// fused multiply-add. invf is within 2^-24 of 1 / scale relatively and the
+// reference's double quotient y* within 2^-53 of x / scale, so for |y*| <= B
+// the distance of y* from r is below |d| + 2^-25 + (B + 1) 2^-24, under 1/2
+// when |d| < tie: y* rounds to r. Beyond B, r + zp lies past qmin or qmax
+// whichever way r rounds, and the clip decides. r + zp is exact while
+// |r| < 2^23, and past the clip bounds beyond. A near-tie (|d| >= tie),
+// NaN or an infinity sets *slow, and the caller must use
+// qa_quantize_one_fast.
+__device__ __forceinline__ int qa_quantize_f32(float x, float invf, float tie,
+                                               int zp, int qmin, int qmax,
                                                bool* slow) {
-    const float y = x * invf;
-    const float ay = fabsf(y);
-    const float r = rintf(y);
-    // no short-circuit: one select-free test (false for NaN)
-    const bool ok = (ay >= 0x1p21f) | (0.5f - fabsf(y - r) > ay * 0x1p-20f);
-    *slow |= !ok;
-    // |r| >= 2^21 saturates to +-2^21, which the clip takes to qmin / qmax
-    const int q = (int)fminf(fmaxf(r, -0x1p21f), 0x1p21f) + zp;
-    return min(max(q, qmin), qmax);
+    const float r = rintf(x * invf);
+    const float d = fmaf(x, invf, -r);
+    *slow |= !(fabsf(d) < tie);  // also for NaN (inf - inf included)
+    // one med3 clip; for a NaN x the result is not used (*slow is set)
+    return (int)__builtin_amdgcn_fmed3f(r + (float)zp, (float)qmin,
+                                        (float)qmax);
+}
+
+// qa_quantize_f32's threshold for a clip range (exact in float32).
+__host__ __device__ __forceinline__ float qa_f32_tie(int64_t zp, int64_t qmin,
+                                                    int64_t qmax) {
+    const int64_t w = qmax - zp > zp - qmin ? qmax - zp : zp - qmin;
+    return (float)(0.5 - (double)(2 * w + 2) * 0x1p-22);
 }
 
 // Whether qa_quantize_f32 applies to a quantization (scale in [2^-60,
-// 2^60], clip range narrower than 2^20, zero point inside it).
+// 2^60], clip bounds within +-2^22 and less than 2^19 from the zero point,
+// which lies inside them).
 __host__ __device__ __forceinline__ bool qa_f32_form_ok(double scale,
                                                        int64_t zp,
                                                        int64_t qmin,
                                                        int64_t qmax) {
-    return scale >= 0x1p-60 && scale <= 0x1p60 && qmax - qmin < (1 << 20) &&
-           qmin >= INT32_MIN && qmax <= INT32_MAX && zp >= qmin && zp <= qmax;
+    return scale >= 0x1p-60 && scale <= 0x1p60 && qmin >= -(1 << 22) &&
+           qmax <= (1 << 22) && zp >= qmin && zp <= qmax &&
+           qmax - zp < (1 << 19) && zp - qmin < (1 << 19);
 }
 
 // qa_quantize_one_fast's result through the float32 form where that form
@@ -155,8 +164,8 @@ __device__ __forceinline__ int64_t qa_quantize_mixed(float x, bool f32ok,
                                                      int64_t qmax) {
     if (f32ok) {
         bool slow = false;
-        const int q = qa_quantize_f32(x, invf, (int)zp, (int)qmin, (int)qmax,
-                                      &slow);
+        const int q = qa_quantize_f32(x, invf, qa_f32_tie(zp, qmin, qmax),
+                                      (int)zp, (int)qmin, (int)qmax, &slow);
         if (!slow) return q;
     }
     return qa_quantize_one_fast(x, scale, inv, zp, qmin, qmax);

@@ -46,9 +46,11 @@ __device__ __forceinline__ uint32_t pixel_word_f32(const float (&f)[CIN],
     uint32_t w = 0;
     *slow |= !f32;
     const int so = (int)q.so;
+    const float tie = qa_f32_tie(q.zp - so, q.qmin - so, q.qmax - so);
 #pragma unroll
     for (int c = 0; c < CIN; ++c)
-        w |= (uint32_t)(uint8_t)qa_quantize_f32(f[c], invf, (int)q.zp - so,
+        w |= (uint32_t)(uint8_t)qa_quantize_f32(f[c], invf, tie,
+                                                (int)q.zp - so,
                                                 (int)q.qmin - so,
                                                 (int)q.qmax - so, slow)
              << (8 * c);
@@ -192,15 +194,18 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
     const int shrw = a.SH * g.RW;
     const int nreal = kgl < a.KH ? (a.Cg | a.KW << 8) : 0;
     const int4 hdr = *(const int4*)a.plan;
+    const int* tabE = s_tab - hdr.x;  // tabE[v] = E[v - A] for v in [A, B]
     for (int cb = 0; cb < g.CBK; ++cb) {
         const int co0 = cb * 16;
         const v4i wf =
             *(const v4i*)(a.wp + (int64_t)(co0 + col) * a.wp_rstride + kgl * 16);
         const int c = min(co0 + col, a.Cout - 1);
         const int4 pc = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
-        const int64_t cc = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
-                                     (uint32_t)pc.z);
-        const uint32_t ccorr = a.corr ? (uint32_t)a.corr[c] : 0u;
+        // the correction folded into the plan constant (plan_q0; K is one
+        // 64-byte step: |w| + |corr| + |boff * rowsum| < 2^26)
+        const int64_t cc = plan_fold(
+            (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z),
+            a.corr ? (uint32_t)a.corr[c] : 0u, pc.x);
         const uint32_t cbo = a.rowsum ? (uint32_t)a.boff[c] : 0u;
         // this lane's fetch pixel walks the band 64 pixels a step
         int fp = min(wave * 16 + col, bpix - 1);
@@ -237,10 +242,10 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
             int e[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                uint32_t wu = (uint32_t)acc[r] + ccorr;
-                if (a.rowsum) wu += cbo * (uint32_t)ps[r];
-                const int q0 = (int)(((int64_t)(int)wu * pc.x + cc) >> pc.y);
-                e[r] = s_tab[min(max(q0, hdr.x), hdr.y) - hdr.x];
+                int w = acc[r];
+                if (a.rowsum) w += (int)(cbo * (uint32_t)ps[r]);
+                e[r] = tabE[med3_i32(plan_q0(w, pc.x, cc, pc.y), hdr.x,
+                                     hdr.y)];
             }
             const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
             const int pq = t * 16 + 4 * kgl + qd;  // pixel this lane stores
@@ -290,9 +295,8 @@ bool launch_conv_qin(const ConvArgs& a0, const QinArgs& q, hipStream_t st) {
         g.RW = (last + 1 + 3) / 4 * 4;
     }
     g.CBK = (a.Cout + 15) / 16;
-    g.f32 = q.scale >= 0x1p-60 && q.scale <= 0x1p60 &&
-            q.qmax - q.qmin < (1 << 20) && q.qmin >= INT32_MIN &&
-            q.qmax <= INT32_MAX && q.zp >= q.qmin && q.zp <= q.qmax;
+    // the float32 form on stored values (q - so)
+    g.f32 = qa_f32_form_ok(q.scale, q.zp - q.so, q.qmin - q.so, q.qmax - q.so);
     auto in_rows = [&](int R) { return (R - 1) * a.SH + (a.KH - 1) * a.DH + 1; };
     auto lds = [&](int R) { return (int64_t)in_rows(R) * g.RW * 4; };
     int R = 0;

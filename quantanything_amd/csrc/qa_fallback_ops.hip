@@ -132,6 +132,83 @@ __global__ __launch_bounds__(kThreads) void k_layernorm(
     }
 }
 
+// int8 rows of at most 512 values, a multiple of 4 (transformer widths):
+// 32 lanes a row (2 rows a wave), lane l holding the WPL 4-byte words
+// l, l + 32, ... of its row (coalesced word loads and stores). The same
+// float64 statistics as k_layernorm; each value is then scaled by the
+// row's reciprocal deviation (one division a row instead of one a value).
+template <int WPL>
+__global__ __launch_bounds__(kThreads) void k_layernorm_w(
+    const int8_t* __restrict__ x, int64_t x_rs, int64_t rows, int64_t cols,
+    double in_scale, int64_t in_zp, int64_t x_so,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    double eps, int8_t* __restrict__ y, int64_t y_rs, double out_scale,
+    int64_t out_zp, int64_t qmin, int64_t qmax, int64_t y_so) {
+    const int lane = threadIdx.x & 63;
+    const int gl = lane & 31;
+    const double inv = 1.0 / out_scale;
+    const bool f32ok = qa_f32_form_ok(out_scale, out_zp, qmin, qmax);
+    const float invf = (float)inv;
+    const int words = (int)(cols >> 2);
+    const int64_t first =
+        ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
+    for (int64_t r = first; r - (lane >> 5) < rows;
+         r += (int64_t)gridDim.x * 8) {
+        const bool live = r < rows;
+        const int64_t rr = live ? r : 0;
+        const uint32_t* xr = (const uint32_t*)(x + rr * x_rs);
+        double v[WPL][4];
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < WPL; ++k) {
+            const int w = gl + 32 * k;
+            const uint32_t u = w < words ? xr[w] : 0u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                v[k][b] = w < words
+                              ? (double)dequant_f32(
+                                    (int64_t)(int8_t)(u >> (8 * b)) + x_so,
+                                    in_zp, in_scale)
+                              : 0.0;
+                s += v[k][b];
+            }
+        }
+        const double mean = group_sum<32>(s) / (double)cols;
+        double q2 = 0.0;
+#pragma unroll
+        for (int k = 0; k < WPL; ++k)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const double t = v[k][b] - mean;
+                if (gl + 32 * k < words) q2 += t * t;
+            }
+        const double rsd = 1.0 / sqrt(group_sum<32>(q2) / (double)cols + eps);
+        if (!live) continue;
+        uint32_t* yr = (uint32_t*)(y + rr * y_rs);
+#pragma unroll
+        for (int k = 0; k < WPL; ++k) {
+            const int w = gl + 32 * k;
+            if (w >= words) continue;
+            const float4 g4 = ((const float4*)gamma)[w];
+            const float4 b4 = beta ? ((const float4*)beta)[w]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float gg[4] = {g4.x, g4.y, g4.z, g4.w};
+            const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+            uint32_t out = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const double t =
+                    (v[k][b] - mean) * rsd * (double)gg[b] + (double)bb[b];
+                const int64_t q = qa_quantize_mixed((float)t, f32ok, invf,
+                                                    out_scale, inv, out_zp,
+                                                    qmin, qmax);
+                out |= (uint32_t)(uint8_t)(int8_t)(q - y_so) << (8 * b);
+            }
+            yr[w] = out;
+        }
+    }
+}
+
 // ---------------------------------------------- activation x activation --
 // C[b0, b1, m, n] = quantize(sa * sb * sum_k (A[.., m, k] - za) *
 // (Bt[.., n, k] - zb)); A and Bt have unit stride along k. A work-group
@@ -466,6 +543,29 @@ QA_API int qa_d_layernorm(const void* x, int x_code, int64_t x_rstride,
         return -1;
     }
     hipStream_t st = (hipStream_t)stream;
+    // int8 rows of 4-byte words, at most 512 values: the word kernel
+    if (x_code == 1 && y_code == 1 && cols % 4 == 0 && cols <= 512 &&
+        x_rstride % 4 == 0 && y_rstride % 4 == 0 &&
+        ((uintptr_t)x | (uintptr_t)y | (uintptr_t)gamma |
+         (uintptr_t)(beta ? beta : gamma)) % 16 == 0) {
+        const int64_t blocks = std::min<int64_t>(ceil_div(rows, 8), 65535);
+        auto run = [&](auto kern) {
+            kern<<<(unsigned)blocks, kThreads, 0, st>>>(
+                (const int8_t*)x, x_rstride, rows, cols, in_scale, in_zp, x_so,
+                gamma, beta, eps, (int8_t*)y, y_rstride, out_scale, out_zp,
+                qmin, qmax, y_so);
+        };
+        const int wpl = (int)ceil_div(cols / 4, 32);
+        if (wpl <= 1)
+            run(k_layernorm_w<1>);
+        else if (wpl <= 2)
+            run(k_layernorm_w<2>);
+        else if (wpl == 3)
+            run(k_layernorm_w<3>);
+        else
+            run(k_layernorm_w<4>);
+        return launched("qa_d_layernorm") ? 0 : -1;
+    }
     auto go = [&](auto ti, auto to) {
         typedef decltype(ti) TI;
         typedef decltype(to) TO;

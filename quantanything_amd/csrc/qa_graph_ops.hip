@@ -1,7 +1,11 @@
 // Whole-tensor operators of the quantized graph that are not element-wise:
 // GlobalAveragePool (integer sum + requantize, quant_layers.py:563-590) and
 // the float Softmax fallback (dequantize -> float64 softmax -> quantize,
-// quant_layers.py:195-205 with float_ops.py:380-385).
+// quant_layers.py:195-205 with float_ops.py:380-385). The exponentials are
+// normalized by one reciprocal of their sum a row (the reference divides
+// each: the float64 results differ by at most one unit in the last place,
+// far below the float32 rounding that follows, and the outputs agree
+// within one quantization step).
 #include <algorithm>
 
 #include "qa_common.h"
@@ -216,8 +220,8 @@ __global__ __launch_bounds__(kThreads) void k_softmax(
                                     in_zp) *
                            in_scale);
         };
-        auto emit = [&](int64_t i, double e, double sum) {
-            const float y = (float)(e / sum);
+        auto emit = [&](int64_t i, double e, double rsum) {
+            const float y = (float)(e * rsum);
             const int64_t q = qa_quantize_one(y, out_scale, out_zp, qmin, qmax);
             store_s(out, out_code, base + i, q - out_so);
             if (outf)
@@ -242,10 +246,11 @@ __global__ __launch_bounds__(kThreads) void k_softmax(
                 sum += e[k];
             }
             sum = block_reduce(sum, false, sh);
+            const double rsum = 1.0 / sum;
 #pragma unroll
             for (int k = 0; k < SOFTMAX_PER; ++k) {
                 const int64_t i = threadIdx.x + (int64_t)k * kThreads;
-                if (i < cols) emit(i, e[k], sum);
+                if (i < cols) emit(i, e[k], rsum);
             }
         } else {
             double mx = -INFINITY;
@@ -256,8 +261,9 @@ __global__ __launch_bounds__(kThreads) void k_softmax(
             for (int64_t i = threadIdx.x; i < cols; i += kThreads)
                 sum += exp((double)value(i) - mx);
             sum = block_reduce(sum, false, sh);
+            const double rsum = 1.0 / sum;
             for (int64_t i = threadIdx.x; i < cols; i += kThreads)
-                emit(i, exp((double)value(i) - mx), sum);
+                emit(i, exp((double)value(i) - mx), rsum);
         }
         __syncthreads();
     }
@@ -309,12 +315,13 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows(
         }
 #pragma unroll
         for (int o = GS / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        const double rsum = 1.0 / sum;  // one division a row
         if (!live) continue;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int64_t i = gl + GS * k;
             if (i >= cols) continue;
-            const float y = (float)(e[k] / sum);
+            const float y = (float)(e[k] * rsum);
             const int64_t q = qa_quantize_mixed(y, f32ok, invf, out_scale, inv,
                                                 out_zp, qmin, qmax);
             out[base + i] = (TO)(q - out_so);
@@ -379,12 +386,13 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
         }
 #pragma unroll
         for (int o = GS / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        const double rsum = 1.0 / sum;  // one division a row
         if (!live) continue;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int64_t i = gl + GS * k;
             if (i >= cols) continue;
-            const float y = (float)(e[k] / sum);
+            const float y = (float)(e[k] * rsum);
             const int64_t q = qa_quantize_mixed(y, f32ok, invf, out_scale, inv,
                                                 out_zp, qmin, qmax);
             out[base + i] = (int8_t)(q - out_so);

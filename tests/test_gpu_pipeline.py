@@ -153,6 +153,49 @@ def test_input_quantization_fused_into_stem(hip, tmp_path, quant_type, cin,
                     err_msg=f"{name}, band code {code:#x}")
 
 
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+def test_stem_quantization_edge_values(hip, tmp_path, quant_type):
+    """The fused stem's float32 quantization (exact unless a value is near a
+    rounding tie, where the double form decides) on the values that test
+    it: exact ties (k + 1/2) * scale, one float step either side of them,
+    the clip bounds and one step past them, magnitudes beyond 2^23 steps,
+    +-1e30, +-inf and -0.0; every integer tensor equals the oracle's."""
+    g = _stem_graph(3, 16, 3, 2, 1, 1, 32)
+    calib = [Stream(20).uniform((3, 3, 32, 32), -1.0, 1.0).astype(np.float32)]
+    c = _calibrated(g, quant_type, True, calib)
+    qp = c.qparams["images"]
+    scale, zp = float(qp.scale), int(qp.zp)
+    x = Stream(31).uniform((3, 3, 32, 32), -1.2, 1.2).astype(np.float32)
+    flat = x.reshape(-1)
+    ks = np.arange(-140, 140)
+    ties = ((ks + 0.5) * scale).astype(np.float32)
+    special = np.concatenate([
+        ties,
+        np.nextafter(ties, np.float32(np.inf)),
+        np.nextafter(ties, np.float32(-np.inf)),
+        np.float32([(qp.qmin - zp) * scale, (qp.qmax - zp) * scale,
+                    (qp.qmin - zp - 1) * scale, (qp.qmax - zp + 1) * scale,
+                    2.0 ** 23 * scale, -(2.0 ** 23) * scale,
+                    2.0 ** 24 * scale, -(2.0 ** 24) * scale,
+                    1e30, -1e30, np.inf, -np.inf, -0.0, 0.0,
+                    1e-40, -1e-40])])
+    idx = Stream(32).integers(0, flat.size - 1, (special.size,))
+    flat[idx] = special
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    oracle.run(x, keep=True)
+    ex = c.executor({"images": x.shape})
+    assert any(t[0].startswith("qconv:") for t in ex.tunables)
+    ex.run({"images": x})
+    checked = 0
+    for name, t in ex.tensors.items():
+        if name in oracle.env:
+            got = t.to_host()
+            np.testing.assert_array_equal(
+                got, oracle.env[name].reshape(got.shape), err_msg=name)
+            checked += 1
+    assert checked >= 2
+
+
 def _conv_graph(cin, cout, k, stride, pad, dil, groups, size):
     b = G.GraphBuilder(11)
     y = b.silu(b.conv("images", cin, cout, k, stride, pad=pad, groups=groups,
