@@ -61,6 +61,7 @@ struct ConvArgs {
     int32_t tile_hint;              // 0, or TILE_VALID | wm | split << 8 |
                                     // lds << 9 (MFMA tile choice)
     int64_t wp_gstride, wp_rstride; // bytes
+    int32_t xcd_yfast;              // XCD order: channel blocks fastest
     int32_t pad_value;
     int32_t rowsum;                 // some b_off != 0
     const void* plan;               // table epilogue plan (int8 output)

@@ -35,9 +35,11 @@ __global__ __launch_bounds__(256) void k_conv_band(ConvArgs a, BandGeom bg) {
     __shared__ int s_tab[768];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, kgl = lane >> 4;
-    const int n = blockIdx.x / bg.nbands;
-    const int oy0 = (blockIdx.x - n * bg.nbands) * bg.R;
-    const int co0 = blockIdx.y * WM * 16;
+    // the channel blocks of a band read the same band: one XCD runs them
+    const XcdBlock blk = xcd_block(true);
+    const int n = (int)blk.x / bg.nbands;
+    const int oy0 = ((int)blk.x - n * bg.nbands) * bg.R;
+    const int co0 = (int)blk.y * WM * 16;
     const int rows = min(bg.R, a.OH - oy0);     // output rows of the band
     const int npix = rows * a.OW;
     const int KGp = a.KGp;

@@ -4,7 +4,7 @@
 //
 // Persistent tiles. A tile is 16 consecutive output pixels (batch folded
 // in) times the WM*16 output channels of the work-group's channel block
-// (blockIdx.y). Each wave64 walks its own sequence of tiles (tile, tile +
+// (the grid's y after xcd_block). Each wave64 walks its own sequence of tiles (tile, tile +
 // stride, ...); with KSPLIT the 4 waves of a work-group share each tile and
 // split its K-steps. Fragments come straight from global memory into
 // registers (16 contiguous bytes per lane) through a ring of D K-steps that
@@ -95,6 +95,37 @@ __device__ __forceinline__ int div_magic(int n, uint64_t m) {
 
 __device__ __forceinline__ int splat4(int b) {
     return (int)((uint32_t)(uint8_t)b * 0x01010101u);
+}
+
+// The work-group's (x, y, z) block after an XCD-aware reordering of the
+// grid. Work-groups are dealt to the 8 XCDs (each with its own L2)
+// round-robin in flattened-id order, x fastest: work-group f runs on XCD
+// f % 8 as that XCD's (f / 8)-th. XCD i takes the i-th contiguous range of
+// a linear order of the grid (XCD i holds q + (i < r) work-groups for
+// q = total / 8, r = total % 8) in which y varies fastest (yfast: the
+// channel blocks of one pixel block, which read the same activations, run
+// on one XCD) or x does (the pixel blocks of one channel block, which read
+// the same weights). Wave-uniform scalar arithmetic, once per work-group.
+struct XcdBlock {
+    uint32_t x, y, z;
+};
+__device__ __forceinline__ XcdBlock xcd_block(bool yfast) {
+    const uint32_t gx = gridDim.x, gy = gridDim.y;
+    const uint32_t gxy = gx * gy, total = gxy * gridDim.z;
+    const uint32_t f = (blockIdx.z * gy + blockIdx.y) * gx + blockIdx.x;
+    const uint32_t xcd = f & 7, q = total >> 3, r = total & 7;
+    const uint32_t lid = xcd * q + min(xcd, r) + (f >> 3);
+    const uint32_t z = lid / gxy, rem = lid - z * gxy;
+    XcdBlock b;
+    b.z = z;
+    if (yfast) {
+        b.x = rem / gy;
+        b.y = rem - b.x * gy;
+    } else {
+        b.y = rem / gx;
+        b.x = rem - b.y * gx;
+    }
+    return b;
 }
 
 // sum of the first nreal signed bytes of v (nreal in 0..16)
@@ -358,10 +389,12 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
     const int lane = threadIdx.x & 63;
     // wave index in a scalar register: the tile walk below is wave-uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int g = blockIdx.z;
+    // (pixel block, channel block, group) of the work-group
+    const XcdBlock blk = xcd_block(a.xcd_yfast != 0);
+    const int g = (int)blk.z;
     const int kgl = lane >> 4;
     const int col = lane & 15;
-    const int co0 = blockIdx.y * (WM * 16);
+    const int co0 = (int)blk.y * (WM * 16);
     const bool res = TABLE && a.res != nullptr;
     // the epilogue tables first: their loads overlap everything below
     const int ntab = res ? 768 : 256;
@@ -375,14 +408,11 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<WM>(), 8))) void k_conv_mfma(
         }
     }
 
-    // Tiles of 16 consecutive output pixels; the work-groups that run on
-    // one XCD (consecutive block ids go round-robin over the 8 XCDs) take a
-    // contiguous range. A wave's tiles are tile, tile + tstride, ...
+    // Tiles of 16 consecutive output pixels; the pixel blocks that run on
+    // one XCD form contiguous ranges (xcd_block). A wave's tiles are tile,
+    // tile + tstride, ...
     const uint32_t nb = gridDim.x;
-    // block b runs on XCD b % 8 as that XCD's (b / 8)-th block; XCD x holds
-    // q + (x < r) blocks (nb = 8q + r) and takes the x-th contiguous range
-    const uint32_t xcd = blockIdx.x & 7, q8 = nb >> 3, r8 = nb & 7;
-    const uint32_t bx = xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3);
+    const uint32_t bx = blk.x;
     const int64_t ntiles = (a.M + 15) >> 4;
     const int64_t tstride = KSPLIT ? (int64_t)nb : (int64_t)nb * 4;
     int64_t tile = KSPLIT ? (int64_t)bx : (int64_t)bx * 4 + wave;
@@ -839,6 +869,12 @@ bool launch_kernel(const ConvArgs& a0, hipStream_t st) {
     a.st_dn = (int32_t)(stride / ohw);
     a.st_doy = (int32_t)((stride % ohw) / a.OW);
     a.st_dox = (int32_t)((stride % ohw) % a.OW);
+    // the channel blocks of a pixel block on one XCD when the activations
+    // outweigh the weights (each XCD then reads all weights once), else
+    // the pixel blocks of a channel block (each XCD reads all activations)
+    const int64_t in_bytes = (int64_t)a.N * a.H * a.W * a.Cg * a.G;
+    const int64_t w_bytes = (int64_t)a.Cout * a.KGp * 16;
+    a.xcd_yfast = in_bytes >= w_bytes ? 1 : 0;
     dim3 grid((unsigned)gx, (unsigned)cblocks, (unsigned)a.G);
     kern<<<grid, 256, dyn, st>>>(a);
     hipError_t e = hipGetLastError();

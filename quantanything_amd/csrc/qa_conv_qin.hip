@@ -32,6 +32,7 @@ struct QinGeom {
     uint64_t mg_ow;  // ceil(2^32 / OW)
     uint64_t mg_pw;  // ceil(2^32 / pad columns per row)
     uint64_t mg_gw;  // ceil(2^32 / items per input row)
+    int s64y, s64x;  // 64 output pixels as rows and columns (s64x < OW)
 };
 
 // Quantized word of one pixel: channel c in byte c (storage offset so
@@ -195,73 +196,93 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
     const int nreal = kgl < a.KH ? (a.Cg | a.KW << 8) : 0;
     const int4 hdr = *(const int4*)a.plan;
     const int* tabE = s_tab - hdr.x;  // tabE[v] = E[v - A] for v in [A, B]
-    for (int cb = 0; cb < g.CBK; ++cb) {
-        const int co0 = cb * 16;
-        const v4i wf =
-            *(const v4i*)(a.wp + (int64_t)(co0 + col) * a.wp_rstride + kgl * 16);
-        const int c = min(co0 + col, a.Cout - 1);
-        const int4 pc = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
-        // the correction folded into the plan constant (plan_q0; K is one
-        // 64-byte step: |w| + |corr| + |boff * rowsum| < 2^26)
-        const int64_t cc = plan_fold(
-            (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z),
-            a.corr ? (uint32_t)a.corr[c] : 0u, pc.x);
-        const uint32_t cbo = a.rowsum ? (uint32_t)a.boff[c] : 0u;
-        // this lane's fetch pixel walks the band 64 pixels a step
-        int fp = min(wave * 16 + col, bpix - 1);
-        int oyl = div_magic(fp, g.mg_ow);
-        int ox = fp - oyl * a.OW;
-        for (int t = wave; t < ntile; t += 4) {
-            const int base = __mul24(oyl, shrw) + kbase + __mul24(ox, a.SW);
-            v4i b;
+    // LDS word of band pixel p's receptive field (this lane's kernel row);
+    // increasing in p, so pixels past the band clamp to the last one's
+    auto fbase = [&](int p) {
+        const int oyl = div_magic(p, g.mg_ow);
+        return __mul24(oyl, shrw) + kbase + __mul24(p - oyl * a.OW, a.SW);
+    };
+    const int bmax = fbase(bpix - 1);
+    // a wave's next tile is 64 pixels on: s64y rows and s64x < OW columns,
+    // plus one carry into the next row
+    const int dstep = __mul24(g.s64y, shrw) + __mul24(g.s64x, a.SW);
+    const int dcarry = shrw - __mul24(a.OW, a.SW);
+    int8_t* const yb = (int8_t*)a.y + pix0 * a.y_pst;  // the band's output
+    const int ypst = (int)a.y_pst;  // bpix * y_pst < 2^31 (host)
+    const bool whole = (a.Cout & 3) == 0;  // every 4-channel word stored
+    auto tiles = [&](auto RS) {
+        constexpr bool ROWSUM = decltype(RS)::value;
+        for (int cb = 0; cb < g.CBK; ++cb) {
+            const int co0 = cb * 16;
+            const v4i wf = *(const v4i*)(a.wp +
+                                         (int64_t)(co0 + col) * a.wp_rstride +
+                                         kgl * 16);
+            const int c = min(co0 + col, a.Cout - 1);
+            const int4 pc = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
+            // the correction folded into the plan constant (plan_q0; K is
+            // one 64-byte step: |w| + |corr| + |boff * rowsum| < 2^26); kept
+            // opaque so that the tile loop is one 32x32->64 multiply-add a
+            // value rather than a re-associated 64x64 product
+            int64_t cc = plan_fold(
+                (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z),
+                a.corr ? (uint32_t)a.corr[c] : 0u, pc.x);
+            asm volatile("" : "+v"(cc));
+            const uint32_t cbo = ROWSUM ? (uint32_t)a.boff[c] : 0u;
+            // this lane's fetch pixel walks the band 64 pixels a step
+            const int fp0 = wave * 16 + col;
+            int ox = fp0 - div_magic(fp0, g.mg_ow) * a.OW;
+            int base = fbase(fp0);
+            for (int t = wave; t < ntile; t += 4) {
+                const int bs = min(base, bmax);
+                v4i b;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) b[k] = s_raw[base + k * a.DW];
-            // next tile of this wave (pixels past the band stay clamped)
-            if (fp + 64 < bpix) {
-                fp += 64;
-                ox += 64;
-                while (ox >= a.OW) {
-                    ox -= a.OW;
-                    ++oyl;
-                }
-            } else {
-                fp = bpix - 1;
-                oyl = div_magic(fp, g.mg_ow);
-                ox = fp - oyl * a.OW;
-            }
-            const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                b, wf, v4i{0, 0, 0, 0}, 0, 0, 0);
-            int ps[4] = {0, 0, 0, 0};
-            if (a.rowsum) {
-                int psum = bytes_sum_l1(b, nreal);
-                psum += __shfl_xor(psum, 16);
-                psum += __shfl_xor(psum, 32);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) ps[r] = __shfl(psum, 4 * kgl + r);
-            }
-            int e[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                int w = acc[r];
-                if (a.rowsum) w += (int)(cbo * (uint32_t)ps[r]);
-                e[r] = tabE[med3_i32(plan_q0(w, pc.x, cc, pc.y), hdr.x,
-                                     hdr.y)];
-            }
-            const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
-            const int pq = t * 16 + 4 * kgl + qd;  // pixel this lane stores
-            const int c0 = co0 + cq;
-            if (pq < bpix && c0 < a.Cout) {
-                int8_t* py = (int8_t*)a.y + (pix0 + pq) * a.y_pst + c0;
-                if (c0 + 3 < a.Cout) {
-                    *(uint32_t*)py = wy;
-                } else {
+                for (int k = 0; k < 4; ++k) b[k] = s_raw[bs + k * a.DW];
+                ox += g.s64x;
+                base += dstep;
+                const bool carry = ox >= a.OW;
+                ox -= carry ? a.OW : 0;
+                base += carry ? dcarry : 0;
+                const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    b, wf, v4i{0, 0, 0, 0}, 0, 0, 0);
+                int ps[4] = {0, 0, 0, 0};
+                if (ROWSUM) {
+                    int psum = bytes_sum_l1(b, nreal);
+                    psum += __shfl_xor(psum, 16);
+                    psum += __shfl_xor(psum, 32);
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (c0 + r < a.Cout) py[r] = (int8_t)(wy >> (8 * r));
+                        ps[r] = __shfl(psum, 4 * kgl + r);
+                }
+                int e[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    int w = acc[r];
+                    if (ROWSUM) w += (int)(cbo * (uint32_t)ps[r]);
+                    e[r] = tabE[med3_i32(plan_q0(w, pc.x, cc, pc.y), hdr.x,
+                                         hdr.y)];
+                }
+                const uint32_t wy =
+                    quad_transpose(pack_entries(e, 0), sel1, sel2);
+                const int pq = t * 16 + 4 * kgl + qd;  // pixel this lane stores
+                const int c0 = co0 + cq;
+                if (pq < bpix && c0 < a.Cout) {
+                    int8_t* py = yb + (pq * ypst + c0);
+                    if (whole || c0 + 3 < a.Cout) {
+                        *(uint32_t*)py = wy;
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (c0 + r < a.Cout)
+                                py[r] = (int8_t)(wy >> (8 * r));
+                    }
                 }
             }
         }
-    }
+    };
+    if (a.rowsum)
+        tiles(std::true_type());
+    else
+        tiles(std::false_type());
 }
 
 uint64_t magic(int d) { return (((uint64_t)1 << 32) + d - 1) / (uint64_t)d; }
@@ -317,11 +338,14 @@ bool launch_conv_qin(const ConvArgs& a0, const QinArgs& q, hipStream_t st) {
     const int64_t shm = lds(R);
     const int64_t blocks = (int64_t)a.N * g.bands;
     if (shm > 60 * 1024 || (int64_t)R * a.OW >= (1 << 16) ||
+        (int64_t)R * a.OW * a.y_pst + a.Cout >= ((int64_t)1 << 31) ||
         (int64_t)g.IR * g.RW >= (1 << 16) || blocks >= ((int64_t)1 << 31)) {
         set_error("qa_d_quantize_conv", "image rows too wide for one band");
         return false;
     }
     g.mg_ow = magic(a.OW);
+    g.s64y = 64 / a.OW;
+    g.s64x = 64 % a.OW;
     g.mg_pw = magic(std::max(g.RW - (g.c0 - a.PW) - a.W, 1));
     g.mg_gw = magic(std::max(vec ? a.W / 4 : a.W, 1));
     auto go = [&](auto kern) {

@@ -78,7 +78,7 @@ __device__ __forceinline__ int wr_div(int n, uint32_t m) {
 // each tile's stored bytes go to a per-wave LDS tile (16 pixels x 80
 // bytes), are read back as the 1x1 conv's activation fragment (one K-step)
 // and a2's table epilogue stores a2's output (a covers every channel:
-// blockIdx.y == 0).
+// one channel block).
 template <int WM, int KS, bool RES, bool CH>
 __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
                                                    ConvArgs a2) {
@@ -100,14 +100,16 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kgl = lane >> 4;
-    const int co0 = blockIdx.y * WM * 16;
+    // the channel blocks of a band read the same band: one XCD runs them
+    const XcdBlock blk = xcd_block(true);
+    const int co0 = (int)blk.y * WM * 16;
     const int KGp = a.KGp;
     const int cpp = a.Cg >> 4;  // 16-byte chunks per input pixel
     const int nch = bg.BR * bg.BW * cpp;
     const int pv = splat4(a.pad_value);
     const v4i pad4 = {pv, pv, pv, pv};
 
-    const int band = blockIdx.x;
+    const int band = (int)blk.x;
     const int n = band / bg.bpi;
     const int oy0 = (band - n * bg.bpi) * bg.R;
     const int iy0 = oy0 * a.SH - a.PH;
