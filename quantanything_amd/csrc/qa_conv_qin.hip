@@ -35,27 +35,54 @@ struct QinGeom {
     int s64y, s64x;  // 64 output pixels as rows and columns (s64x < OW)
 };
 
+// The float32 quantization form (qa_quantize_f32) with the rounding and
+// the conversion to an integer done by additions of M = 1.5 * 2^23:
+// t = fma(x, invf, M) is M plus the integer nearest to x * invf when
+// |x * invf| < 2^22 (the floats in [2^23, 2^24) are the integers there),
+// r = t - M is that integer exactly and d = fma(x, invf, -r) the residual
+// that qa_quantize_f32 tests (*slow unless |d| < tie; NaN fails the test).
+// t + zp clipped to [M + qmin, M + qmax] is the quantized value plus M, an
+// integer float in [2^23, 2^24], so its low mantissa byte is the value's
+// low two's-complement byte (2^22 is a multiple of 256); the result is
+// those float bits. For |x * invf| >= 2^22 the clip gives qmax or qmin
+// (qmax - zp and zp - qmin < 2^19, and the additions round monotonically),
+// as the exact form does. qa_f32_form_ok bounds qmin, qmax and zp.
+struct QinF32 {
+    float invf, tie, zpf, lo, hi;
+};
+constexpr float QIN_M = 12582912.0f;  // 1.5 * 2^23
+
+__device__ __forceinline__ uint32_t quant_bits(float x, const QinF32& k,
+                                               bool* slow) {
+    const float t = fmaf(x, k.invf, QIN_M);
+    const float r = t - QIN_M;
+    const float d = fmaf(x, k.invf, -r);
+    *slow |= !(fabsf(d) < k.tie);
+    return __float_as_uint(__builtin_amdgcn_fmed3f(t + k.zpf, k.lo, k.hi));
+}
+
 // Quantized word of one pixel: channel c in byte c (storage offset so
 // subtracted), bytes above CIN zero. The float32 form; *slow is set when a
 // value is near a rounding tie, NaN, or the scales are outside that form
 // (f32 false), and then the word must be recomputed by pixel_word_exact.
 template <int CIN>
 __device__ __forceinline__ uint32_t pixel_word_f32(const float (&f)[CIN],
-                                                   const QinArgs& q,
-                                                   float invf, bool f32,
+                                                   const QinF32& k, bool f32,
                                                    bool* slow) {
-    uint32_t w = 0;
     *slow |= !f32;
-    const int so = (int)q.so;
-    const float tie = qa_f32_tie(q.zp - so, q.qmin - so, q.qmax - so);
+    uint32_t b[CIN];
 #pragma unroll
-    for (int c = 0; c < CIN; ++c)
-        w |= (uint32_t)(uint8_t)qa_quantize_f32(f[c], invf, tie,
-                                                (int)q.zp - so,
-                                                (int)q.qmin - so,
-                                                (int)q.qmax - so, slow)
-             << (8 * c);
-    return w;
+    for (int c = 0; c < CIN; ++c) b[c] = quant_bits(f[c], k, slow);
+    // low bytes gathered (v_perm: selector bytes 0-3 pick the second
+    // operand's bytes, 4-7 the first's, 0x0c a zero)
+    if (CIN == 1) return b[0] & 0xffu;
+    const uint32_t lo2 =
+        __builtin_amdgcn_perm(b[CIN > 1 ? 1 : 0], b[0], 0x0c0c0400u);
+    if (CIN == 2) return lo2;
+    if (CIN == 3) return __builtin_amdgcn_perm(b[2], lo2, 0x0c040100u);
+    const uint32_t hi2 = __builtin_amdgcn_perm(b[CIN > 3 ? 3 : 0],
+                                               b[CIN > 2 ? 2 : 0], 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi2, lo2, 0x05040100u);
 }
 
 // The same word exactly as qa_quantize_one per value (double division).
@@ -97,7 +124,16 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
         s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
     const int HW = a.H * a.W;
     const float* xn = q.xf + (int64_t)n * CIN * HW;
-    const float invf = (float)q.inv;
+    QinF32 qk;
+    {
+        const int so = (int)q.so;
+        const int zp = (int)q.zp - so;
+        qk.invf = (float)q.inv;
+        qk.tie = qa_f32_tie(zp, q.qmin - so, q.qmax - so);
+        qk.zpf = (float)zp;
+        qk.lo = QIN_M + (float)((int)q.qmin - so);
+        qk.hi = QIN_M + (float)((int)q.qmax - so);
+    }
     const bool f32 = g.f32;
     constexpr int PX = VEC ? 4 : 1;  // pixels per item
     const int GW = a.W / PX;          // items per input row
@@ -144,7 +180,7 @@ __global__ __launch_bounds__(QIN_THREADS) void k_conv_qin(ConvArgs a,
 #pragma unroll
                 for (int c = 0; c < CIN; ++c) f[c] = v[k][c][p];
                 bool slow = false;
-                w[p] = pixel_word_f32<CIN>(f, q, invf, f32, &slow);
+                w[p] = pixel_word_f32<CIN>(f, qk, f32, &slow);
                 if (!in[k]) w[p] = (uint32_t)pv;
                 if (slow && in[k]) slowbits |= 1u << (k * PX + p);
             }
