@@ -340,6 +340,29 @@ typedef struct qa_matmul_desc {
 } qa_matmul_desc;
 int qa_d_matmul_act(const qa_matmul_desc* d, void* stream);
 
+/* Attention of one layer in one launch: S = MatMul(q, k^T) as
+ * qa_d_matmul_act of `qk`, P = Softmax over S's rows as qa_d_softmax_lut
+ * with `table` (qa_d_softmax_table of S's quantization and storage
+ * offset), O = MatMul(P, v) as qa_d_matmul_act of `av`; S and P stay on
+ * chip and are never written (qk.y and av.a are unused; qk.y_so / out_*
+ * give S's storage offset and quantization, p_* and av.a_scale / a_zp /
+ * a_so P's). The results equal those three launches bit for bit. No
+ * counterpart in the reference, which runs the three operators one by one
+ * (quant_layers.py:195-205, float_ops.py:181-186, :270-282). Conditions
+ * (qa_attention_supported returns 1 when they hold): int8 operands and
+ * output, operands stored at their zero points, S and O rows of at most
+ * 256 columns, av.K == qk.N, av.M == qk.M, equal batch axes, the staged
+ * operands within the LDS budget. */
+typedef struct qa_attention_desc {
+    qa_matmul_desc qk;
+    const double* table;
+    double p_scale;
+    int64_t p_zp, p_qmin, p_qmax, p_so;
+    qa_matmul_desc av;
+} qa_attention_desc;
+int qa_attention_supported(const qa_attention_desc* d);
+int qa_d_attention(const qa_attention_desc* d, void* stream);
+
 /* `stream` of every qa_d_* entry is the hipStream_t to launch on, used as
  * given (NULL: the null stream). The entries are asynchronous and return 0
  * on success, -1 on an error (see qa_last_error). */

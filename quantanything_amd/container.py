@@ -121,14 +121,17 @@ class QuantContainer:
         if not self.calibrated:
             raise ValueError("Container is not calibrated; call calibrate().")
 
-    def executor(self, input_shapes):
-        """The (cached) device executor for these input shapes."""
+    def executor(self, input_shapes, fuse_attention=True):
+        """The (cached) device executor for these input shapes
+        (``fuse_attention``: see ``DeviceExecutor``)."""
         self._require_calibration()
         from quantanything_amd.executor import DeviceExecutor
 
-        key = tuple(sorted((k, tuple(v)) for k, v in input_shapes.items()))
+        key = tuple(sorted((k, tuple(v)) for k, v in input_shapes.items())) \
+            + (bool(fuse_attention),)
         if key not in self._executors:
-            self._executors[key] = DeviceExecutor(self, dict(input_shapes))
+            self._executors[key] = DeviceExecutor(
+                self, dict(input_shapes), fuse_attention=fuse_attention)
         return self._executors[key]
 
     def run_graph(self, x, mode="quantize", use_graph=False):

@@ -17,6 +17,7 @@
 
 #include "../../include/qa_hip.h"
 #include "qa_conv.h"
+#include "qa_stage.h"
 
 namespace qa {
 namespace {
@@ -346,86 +347,9 @@ __global__ __launch_bounds__(kThreads) void k_matmul_act_mfma(
     const int64_t m0 = (int64_t)blockIdx.x * 64;
     const int8_t* A = (const int8_t*)d.a + b0 * d.a_s0 + b1 * d.a_s1;
     const int8_t* B = (const int8_t*)d.b + b0 * d.b_s0 + b1 * d.b_s1;
-    // stage rows [r0, r0 + rows) of an operand (element (r, c) at
-    // src[r * rs + c * ks]) as dst[r][c], zero past rlim / K: 16-byte loads
-    // along a unit-stride axis when it is aligned, else byte loads, 8 in
-    // flight per thread
     auto stage = [&](int8_t* dst, const int8_t* src, int rows, int64_t r0,
                      int64_t rlim, int64_t rs, int64_t ks) {
-        const bool al = ((uintptr_t)src & 15) == 0;
-        constexpr int U = 4;  // loads in flight per thread
-        if (ks == 1 && al && rs % 16 == 0 && d.K % 16 == 0) {
-            const int cpr = Kp / 16;  // 16-byte chunks per row
-            const int n16 = rows * cpr;
-            for (int e0 = tid; e0 < n16; e0 += U * kThreads) {
-                int4 v[U];
-                int at[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int e = e0 + u * kThreads;
-                    const int r = e / cpr, c = (e - r * cpr) * 16;
-                    const int64_t rr = r0 + r;
-                    v[u] = int4{0, 0, 0, 0};
-                    at[u] = e < n16 ? r * RS + c : -1;
-                    if (e < n16 && rr < rlim && c < d.K)
-                        v[u] = *(const int4*)(src + rr * rs + c);
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u)
-                    if (at[u] >= 0) *(int4*)(dst + at[u]) = v[u];
-            }
-            return;
-        }
-        if (rs == 1 && al && ks % 16 == 0 && rows % 16 == 0 &&
-            (r0 + rows <= rlim || rlim % 16 == 0)) {
-            // 16 consecutive rows of one column per load, scattered to LDS
-            const int rpc = rows / 16;
-            const int n16 = rpc * Kp;
-            for (int e0 = tid; e0 < n16; e0 += U * kThreads) {
-                int4 v[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int e = e0 + u * kThreads;
-                    const int c = e / rpc, r = (e - c * rpc) * 16;
-                    const int64_t rr = r0 + r;
-                    v[u] = int4{0, 0, 0, 0};
-                    if (e < n16 && rr < rlim && c < d.K)
-                        v[u] = *(const int4*)(src + rr + (int64_t)c * ks);
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int e = e0 + u * kThreads;
-                    if (e >= n16) continue;
-                    const int c = e / rpc, r = (e - c * rpc) * 16;
-                    const int8_t* b = (const int8_t*)&v[u];
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) dst[(r + j) * RS + c] = b[j];
-                }
-            }
-            return;
-        }
-        const int n = rows * Kp;
-        for (int e0 = tid; e0 < n; e0 += 8 * kThreads) {
-            int8_t v[8];
-            int at[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int e = e0 + j * kThreads;
-                int r = e / Kp, c = e - r * Kp;
-                if (ks != 1) {
-                    c = e / rows;
-                    r = e - c * rows;
-                }
-                const int64_t rr = r0 + r;
-                at[j] = e < n ? r * RS + c : -1;
-                v[j] = (e < n && rr < rlim && c < d.K)
-                           ? src[rr * rs + (int64_t)c * ks]
-                           : 0;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (at[j] >= 0) dst[at[j]] = v[j];
-        }
+        stage_i8_rows(dst, RS, src, rows, r0, rlim, rs, ks, d.K, Kp, tid);
     };
     stage(sa, A, 64, m0, d.M, d.a_sm, d.a_sk);
     stage(sb, B, Np, 0, d.N, d.b_sn, d.b_sk);

@@ -333,6 +333,15 @@ class MatmulDesc(ctypes.Structure):
                 + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
 
 
+class AttentionDesc(ctypes.Structure):
+    """``qa_attention_desc`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("qk", MatmulDesc), ("table", _P),
+                 ("p_scale", ctypes.c_double)]
+                + [(n, _I64) for n in ("p_zp", "p_qmin", "p_qmax", "p_so")]
+                + [("av", MatmulDesc)])
+
+
 class PoolParams(ctypes.Structure):
     """``qa_pool_params`` of ``include/qa_hip.h``."""
 
@@ -413,10 +422,14 @@ def _ok(rc, what):
 
 
 class DeviceExecutor:
-    """Plans and runs one integer inference pass for fixed input shapes."""
+    """Plans and runs one integer inference pass for fixed input shapes.
+    ``fuse_attention``: q k^T -> Softmax -> . v as one launch where it
+    applies (identical results; the scores and probabilities are then not
+    kept as tensors)."""
 
-    def __init__(self, container, input_shapes):
+    def __init__(self, container, input_shapes, fuse_attention=True):
         self.lib = native.require()
+        self.fuse_attention = fuse_attention
         self.c = container
         self.graph = container.graph
         bits, signed = container.layers[0].bits, \
@@ -430,6 +443,10 @@ class DeviceExecutor:
         self.inputs_f32 = {}
         self.input_q = {}  # graph input -> (float buffer, int8 tensor, qp)
         self.softmax_of = {}  # Softmax output -> (launch name, arguments)
+        # activation MatMul output -> (launch name, desc, first operand)
+        self.matmul_act = {}
+        # table Softmax output -> (launch name, input, table, out qp, so)
+        self.softmax_lut = {}
         self.gap_info = {}  # pool launch -> layer, input, output, parameters
         self.tunables = []  # (launch name, desc, tile codes, fn(stream))
         self.f64_descs = []  # (desc, None, None, launch name), FP64 path
@@ -611,6 +628,8 @@ class DeviceExecutor:
         self._fuse_pools(cons)
         self._fuse_pairs(cons)
         self._fuse_chains(cons)
+        if self.fuse_attention:
+            self._fuse_attention(cons)
         for d, _, _, name in self.mfma_descs + self.f64_descs:
             if name in dict(self.launches):
                 self.tunables.append(
@@ -907,6 +926,47 @@ class DeviceExecutor:
             codes = [0, 0x10001] + ([0x10002] if d.Cout > 64 else [])
             self.tunables.append((fused, d, codes, fn))
             self.tensors.pop(xname, None)  # never materialized
+
+    def _fuse_attention(self, cons):
+        """MatMul(q, k^T) -> Softmax over its rows -> MatMul(., v), int8,
+        the scores and the probabilities read by nothing else, run as one
+        launch (``qa_d_attention``): both stay on chip and are never
+        written; the results are those of the three launches."""
+        g = self.graph
+        for pname, (sm_ln, sname, x_ptr, tab, o, p_so) in \
+                self.softmax_lut.items():
+            qk = self.matmul_act.get(sname)
+            avs = [(ln, d) for ln, d, a_name in self.matmul_act.values()
+                   if a_name == pname]
+            if qk is None or len(avs) != 1 or qk[1].y != x_ptr or \
+                    sname in g.outputs or pname in g.outputs or \
+                    len(cons.get(sname, [])) != 1 or \
+                    len(cons.get(pname, [])) != 1:
+                continue
+            qk_ln, qkd, _ = qk
+            av_ln, avd = avs[0]
+            live = dict(self.launches)
+            if not all(n in live for n in (qk_ln, sm_ln, av_ln)):
+                continue
+            ad = AttentionDesc()
+            ad.qk, ad.av = qkd, avd
+            ad.table = tab.data_ptr()
+            ad.p_scale, ad.p_zp, ad.p_qmin, ad.p_qmax, ad.p_so = \
+                o.scale, o.zp, o.qmin, o.qmax, p_so
+            if not self.lib.qa_attention_supported(ctypes.byref(ad)):
+                continue
+            self.keep.append(ad)
+            fused = f"attention:{qk_ln[7:]}+{av_ln[7:]}"
+
+            def fn(s, ad=ad):
+                _ok(self.lib.qa_d_attention(ctypes.byref(ad), s),
+                    "qa_d_attention")
+
+            self.launches = [(fused, fn) if n == av_ln else (n, f)
+                             for n, f in self.launches
+                             if n not in (qk_ln, sm_ln)]
+            self.tensors.pop(sname, None)  # never materialized
+            self.tensors.pop(pname, None)
 
     def _fuse_pairs(self, cons):
         """Two int8 3x3 stride-1 convolutions C -> C (C 16 to 128), the
@@ -1403,6 +1463,8 @@ class DeviceExecutor:
                 self.keep.append(tab)
                 largs = (x.ptr, rows, cols, tab.data_ptr(), y.ptr, o.scale,
                          o.zp, o.qmin, o.qmax, y.so)
+                self.softmax_lut[layer.node.outputs[0]] = (
+                    lname, layer.data_inputs[0], x.ptr, tab, o, y.so)
                 self._add(lname, lambda s: _ok(
                     self.lib.qa_d_softmax_lut(*largs, s), "qa_d_softmax_lut"))
             else:
@@ -1688,6 +1750,8 @@ class DeviceExecutor:
             y.nd_strides[-1]
         d.out_scale, d.out_zp, d.qmin, d.qmax = o.scale, o.zp, o.qmin, o.qmax
         self.keep.extend([d, a.buf, bt.buf, y.buf])
+        self.matmul_act[layer.node.outputs[0]] = (
+            f"matmul:{layer.name}", d, layer.data_inputs[0])
         self._add(f"matmul:{layer.name}", lambda s, d=d: _ok(
             self.lib.qa_d_matmul_act(ctypes.byref(d), s), "qa_d_matmul_act"))
         return [y]

@@ -76,6 +76,8 @@ def _declare(lib):
                                  f64, p, i32, i64, f64, i64, i64, i64, i64,
                                  p]),
         "qa_d_matmul_act": (i32, [p, p]),
+        "qa_attention_supported": (i32, [p]),
+        "qa_d_attention": (i32, [p, p]),
         "qa_epi_plan_bytes": (i64, [i64]),
         "qa_plan_epilogue_i8": (i32, [p, p]),
         "qa_d_requantize": (i32, [p, i32, p, i32] + [i64] * 3 + [p] * 4

@@ -113,11 +113,42 @@ def test_tiny_vit_matches_oracle(hip, tmp_path, quant_type):
              for i in range(2)]
     c = _calibrated(g, quant_type, calib)
     x = Stream(60).normal((3, 3, 32, 32)).astype(np.float32)
-    ex = c.executor({"images": x.shape})
+    # each operator on its own (the scores and probabilities kept)
+    ex = c.executor({"images": x.shape}, fuse_attention=False)
     ex.run({"images": x})
     worst, exact, checked = _check_against_oracle(c, g, tmp_path, x, ex)
     assert worst <= 1 and exact >= 0.98, (worst, exact)
     assert checked >= 20
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+def test_tiny_vit_fused_attention_equals_unfused(hip, quant_type):
+    """q k^T -> Softmax -> . v as one launch (int8) gives the three
+    launches' results bit for bit: every tensor both passes keep, and the
+    logits."""
+    g = _tiny_vit()
+    calib = [Stream(50 + i).normal((3, 3, 32, 32)).astype(np.float32)
+             for i in range(2)]
+    c = _calibrated(g, quant_type, calib)
+    x = Stream(61).normal((3, 3, 32, 32)).astype(np.float32)
+    fused = c.executor({"images": x.shape})
+    plain = c.executor({"images": x.shape}, fuse_attention=False)
+    n_att = sum(n.startswith("attention:") for n, _ in fused.launches)
+    # uint8 activations are stored shifted from their zero points, which
+    # the fused kernel does not take: those passes stay unfused
+    assert n_att == (2 if quant_type == "int8" else 0), \
+        [n for n, _ in fused.launches]
+    assert not any(n.startswith("attention:") for n, _ in plain.launches)
+    out_f = fused.run({"images": x})
+    out_p = plain.run({"images": x})
+    common = [n for n in fused.tensors if n in plain.tensors]
+    assert len(common) >= 20
+    for n in common:
+        np.testing.assert_array_equal(fused.tensors[n].to_host(),
+                                      plain.tensors[n].to_host(), err_msg=n)
+    assert out_f.keys() == out_p.keys()
+    for n in out_f:
+        np.testing.assert_array_equal(out_f[n], out_p[n], err_msg=n)
 
 
 def test_tiny_vit_graph_replay_matches_eager(hip):

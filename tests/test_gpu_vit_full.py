@@ -3,8 +3,10 @@ class token = 197 tokens, dim 384, 6 heads, MLP 1536, 12 layers) through the
 device executor against the oracle: every integer tensor bit-exact given
 the same inputs, the float fallbacks (LayerNorm, Softmax, activation x
 activation MatMul, Gather) within one step and exact on >= 98% of elements
-(the scheme of test_gpu_vit.py), at batch 2; then the batch-32 pass of the
-same model and q.json reproduces the batch-2 logits in its first two rows."""
+(the scheme of test_gpu_vit.py), at batch 2, each operator on its own; the
+fused attention launches give that pass bit for bit; then the batch-32
+pass of the same model and q.json reproduces the batch-2 logits in its
+first two rows."""
 
 import time
 
@@ -29,7 +31,8 @@ def test_vit_s16_full_size(hip, tmp_path, monkeypatch):
     c = QuantContainer(g2, "int8", True)
     c.calibrate(calib)
     x2 = Stream(85).normal((2, 3, 224, 224)).astype(np.float32)
-    ex = c.executor({"images": x2.shape})
+    # each operator on its own for the oracle comparison
+    ex = c.executor({"images": x2.shape}, fuse_attention=False)
     out2 = ex.run({"images": x2})
     print(f"calibrated and ran b2 in {time.time() - t0:.1f}s", flush=True)
     # the compiled reference kernels are the faster CPU checker here
@@ -46,7 +49,16 @@ def test_vit_s16_full_size(hip, tmp_path, monkeypatch):
     assert worst <= 1 and exact >= 0.98, (worst, exact)
     assert checked >= 12 * 8
 
-    # batch 32 with the same weights and q.json
+    # the fused attention launches give the same integer pass
+    exf = c.executor({"images": x2.shape})
+    assert sum(n.startswith("attention:") for n, _ in exf.launches) == 12
+    exf.run({"images": x2})
+    for n, t in exf.tensors.items():
+        if n in ex.tensors:
+            np.testing.assert_array_equal(t.to_host(), ex.tensors[n].to_host(),
+                                          err_msg=n)
+
+    # batch 32 (fused attention) with the same weights and q.json
     path = tmp_path / "q.json"
     c.save(path)
     g32 = G.vit(seed=5, batch=32)
