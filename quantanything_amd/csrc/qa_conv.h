@@ -113,8 +113,10 @@ constexpr int PLAN_E = 64;             // int32 E[256]
 constexpr int PLAN_TC = PLAN_E + 1024;  // int32 TC[256]
 constexpr int PLAN_TR = PLAN_TC + 1024; // int32 TR[256]
 constexpr int PLAN_CH = PLAN_TR + 1024; // int32x4 {m, t, c_lo, c_hi} per channel
-// header (int32): [0] A, [1] B, [2] SH, [3] flags
-constexpr int PLAN_RES = 1, PLAN_Y2 = 2;
+// header (int32): [0] A, [1] B, [2] SH, [3] flags, [4] with PLAN_IDENT
+// (no activation table, residual or second output: E[i] is the byte of
+// A + i + D) the offset D = zp - y_so
+constexpr int PLAN_RES = 1, PLAN_Y2 = 2, PLAN_IDENT = 4;
 
 // Requantize, table and residual Add of one accumulator (mode EPI_QUANT):
 // returns the quantized value q (before the storage offset).
@@ -178,7 +180,8 @@ bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
 // epilogue on 128 x 128 blocks (qa_gemm_big.hip); `epi` as chosen by
 // launch_conv_mfma.
 bool gemm_big_applies(const ConvArgs& b, int epi);
-bool launch_gemm_big(const ConvArgs& b, hipStream_t st);
+// variant: the ring of K-steps in flight (0: the default; see the kernel)
+bool launch_gemm_big(const ConvArgs& b, hipStream_t st, int variant = 0);
 // int8 convolutions over bands of output rows with the input band and the
 // weights in LDS (qa_conv_band.hip); wm = 16-channel groups per work-group.
 bool conv_band_applies(const ConvArgs& b, int epi, int wm);

@@ -128,5 +128,9 @@ QA_API int qa_plan_epilogue_i8(const qa_epi_params* p, void* plan_) {
     hd[1] = (int32_t)B;
     hd[2] = (int32_t)sh;
     hd[3] = (p->has_res ? qa::PLAN_RES : 0) | (p->has_y2 ? qa::PLAN_Y2 : 0);
+    if (!p->has_res && !p->has_y2 && !p->lut) {
+        hd[3] |= qa::PLAN_IDENT;
+        hd[4] = (int32_t)(p->zp - p->y_so);
+    }
     return 1;
 }

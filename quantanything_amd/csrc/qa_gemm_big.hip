@@ -111,17 +111,21 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
     for (int i = tid; i < 768; i += 256)
         s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
     const int4 hdr = *(const int4*)a.plan;
+    // the lane's 4 channels' constants, the zero-point correction folded
+    // into the plan constant (plan_q0; K <= 16384 keeps |w| + |corr| +
+    // |boff * rowsum| below 2^31, so the int32 sum never wraps)
     int cm[4], ct[4];
     int64_t cc[4];
-    uint32_t ccorr[4], cbo[4];
+    uint32_t cbo[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int c = min(n0 + 64 * wn + 16 * j + col, a.Cout - 1);
         const int4 pc = ((const int4*)((const char*)a.plan + PLAN_CH))[c];
         cm[j] = pc.x;
         ct[j] = pc.y;
-        cc[j] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
-        ccorr[j] = a.corr ? (uint32_t)a.corr[c] : 0u;
+        cc[j] = plan_fold(
+            (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z),
+            a.corr ? (uint32_t)a.corr[c] : 0u, pc.x);
         cbo[j] = RS ? (uint32_t)a.boff[c] : 0u;
     }
 
@@ -178,6 +182,9 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
     // plan's multiply-add and shift, one med3 clip and one table read whose
     // LDS address folds in the clip's lower bound.
     const int pA = hdr.x, pB = hdr.y, pSH = hdr.z;
+    // identity table (a plain requantize): the byte of clip(q0) + D
+    const bool ident = !RES && !Y2 && (hdr.w & PLAN_IDENT);
+    const int pD = ((const int*)a.plan)[4];
     const int* tabE = s_tab - pA;  // tabE[v] = E[v - pA] for v in [pA, pB]
     const int q = lane & 3;
     const uint32_t sel1 = q < 2 ? 0x05040100u : 0x03020706u;
@@ -185,8 +192,10 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
     const int cq = col & ~3;
     // the tile's rows and columns all inside the output: no bounds tests
     const bool full = m0 + GB_M <= a.M && n0 + GB_N <= a.Cout;
-    auto epilogue = [&](auto checked) __attribute__((always_inline)) {
+    auto epilogue = [&](auto checked, auto identity)
+                        __attribute__((always_inline)) {
         constexpr bool CHK = decltype(checked)::value;
+        constexpr bool IDT = decltype(identity)::value;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             int ps[4] = {0, 0, 0, 0};
@@ -225,15 +234,16 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
                 int e[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    uint32_t wu = (uint32_t)acc[i][j][r] + ccorr[j];
-                    if (RS) wu += cbo[j] * (uint32_t)ps[r];
-                    const int q0 =
-                        (int)(((int64_t)(int)wu * cm[j] + cc[j]) >> ct[j]);
-                    const int v = min(max(q0, pA), pB);
+                    int w = acc[i][j][r];
+                    if (RS) w += (int)(cbo[j] * (uint32_t)ps[r]);
+                    const int v =
+                        med3_i32(plan_q0(w, cm[j], cc[j], ct[j]), pA, pB);
                     if (RES) {
                         const int tsum = s_tab[256 - pA + v] +
                                          s_tab[512 + ((rv >> (8 * r)) & 255)];
-                        e[r] = s_tab[min(max(tsum, 0), pSH)];
+                        e[r] = s_tab[med3_i32(tsum, 0, pSH)];
+                    } else if (IDT) {
+                        e[r] = v + pD;
                     } else {
                         e[r] = tabE[v];
                     }
@@ -259,10 +269,16 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
             }
         }
     };
-    if (full)
-        epilogue(std::false_type{});
-    else
-        epilogue(std::true_type{});
+    if (ident) {
+        if (full)
+            epilogue(std::false_type{}, std::true_type{});
+        else
+            epilogue(std::true_type{}, std::true_type{});
+    } else if (full) {
+        epilogue(std::false_type{}, std::false_type{});
+    } else {
+        epilogue(std::true_type{}, std::false_type{});
+    }
 }
 
 }  // namespace
@@ -272,19 +288,18 @@ bool gemm_big_applies(const ConvArgs& b, int epi) {
     return epi == Q8_TABLE && b.mode == EPI_QUANT && b.fastio && b.plan &&
            b.G == 1 && b.layout == 0 && b.KH == 1 && b.KW == 1 &&
            b.H == 1 && b.W == 1 && b.OH == 1 && b.OW == 1 && b.x_code == 1 &&
-           b.x_sc == 1 && b.Cg % 64 == 0 && b.KGp * 16 == b.Cg &&
+           b.x_sc == 1 && b.Cg % 64 == 0 && b.Cg <= 16384 &&
+           b.KGp * 16 == b.Cg &&
            b.wp_rstride == (int64_t)b.KGp * 16 && b.x_sn % 16 == 0 &&
            xa % 16 == 0 && b.y_code == 1 && b.M < ((int64_t)1 << 31);
 }
 
-bool launch_gemm_big(const ConvArgs& b, hipStream_t st) {
+bool launch_gemm_big(const ConvArgs& b, hipStream_t st, int variant) {
     const int64_t tiles = ceil_div(b.M, GB_M) * ceil_div(b.Cout, GB_N);
     if (tiles >= ((int64_t)1 << 31)) {
         set_error("launch_gemm_big", "grid too large");
         return false;
     }
-    // 128-byte steps when K allows, else 64-byte steps; the next step's
-    // loads in flight (deeper rings cost the second wave per SIMD)
     const int K = b.KGp * 16;
     const dim3 grid((unsigned)tiles);
     const int flags = (b.res ? 1 : 0) | (b.y2 ? 2 : 0) | (b.rowsum ? 4 : 0);
@@ -301,14 +316,37 @@ bool launch_gemm_big(const ConvArgs& b, hipStream_t st) {
 #undef QA_GB_CASE
         }
     };
-    // 128-byte steps when K allows, else 64-byte steps, the next step's
-    // loads in flight (measured on the ViT-S GEMMs: deeper rings, which
-    // cost VGPRs and so occupancy, were not faster)
+    // deeper rings (more K-steps' loads in flight, more registers): for
+    // no flags or a residual Add only
+    auto go_deep = [&](auto kp, auto kbk) {
+        constexpr int KP = decltype(kp)::value, KBK = decltype(kbk)::value;
+        if (flags == 1)
+            k_gemm_big<KP, KBK, true, false, false><<<grid, 256, 0, st>>>(b);
+        else
+            k_gemm_big<KP, KBK, false, false, false><<<grid, 256, 0, st>>>(b);
+    };
     using I1 = std::integral_constant<int, 1>;
-    if (K % 128 == 0)
-        go(I1{}, std::integral_constant<int, 128>{});
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using B64 = std::integral_constant<int, 64>;
+    using B128 = std::integral_constant<int, 128>;
+    // variant: 0 the default (128-byte steps when K allows, else 64, the
+    // next step's loads in flight), 1 / 2: two / three 128-byte steps in
+    // flight, 3 / 4: two / four 64-byte steps in flight
+    const bool deep_ok = flags == 0 || flags == 1;
+    if (deep_ok && variant == 1 && K % 128 == 0)
+        go_deep(I2{}, B128{});
+    else if (deep_ok && variant == 2 && K % 128 == 0)
+        go_deep(I3{}, B128{});
+    else if (deep_ok && variant == 3)
+        go_deep(I2{}, B64{});
+    else if (deep_ok && variant == 4)
+        go_deep(I4{}, B64{});
+    else if (K % 128 == 0)
+        go(I1{}, B128{});
     else
-        go(I1{}, std::integral_constant<int, 64>{});
+        go(I1{}, B64{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("launch_gemm_big", e);
