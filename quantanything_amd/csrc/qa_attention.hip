@@ -22,7 +22,6 @@
 // N_S), read back as the A operand of O = P v.
 #include "../../include/qa_hip.h"
 #include "qa_conv_mfma.h"
-#include "qa_stage.h"
 
 namespace qa {
 namespace {
@@ -30,6 +29,7 @@ namespace {
 typedef int v4a __attribute__((ext_vector_type(4)));
 
 constexpr int QA_ATT_KSQ = 2;  // q / k depth up to 128 bytes
+constexpr int QA_ATT_U = 8;    // staging chunks a thread has in flight
 
 struct AttnGeom {
     int NpS;       // S columns rounded up to 16 (at most 256)
@@ -63,22 +63,26 @@ struct AttnArgs {
     AttnQ S, P, O;
 };
 
-// qa_quantize_mixed with the constants precomputed (the same operations):
-// the float32 form where it decides, else the double form, called out of
-// line (near-ties and NaN only), which keeps its registers out of the
-// callers' unrolled loops.
+// qa_quantize_mixed with the constants precomputed, split: quant_fast is
+// the float32 form (qa_quantize_f32) and sets *slow where that form does not
+// decide (near-ties, NaN, or the scales outside the form); those values are
+// recomputed by quant_exact, the double form, called out of line so that
+// its registers stay out of the callers' loops. Together they return
+// qa_quantize_mixed's value.
 __device__ __noinline__ int quant_exact(float y, double scale, double inv,
                                         int zp, int qmin, int qmax) {
     return (int)qa_quantize_one_fast(y, scale, inv, zp, qmin, qmax);
 }
 
-__device__ __forceinline__ int quant(float y, const AttnQ& c) {
-    if (c.f32) {
-        const float r = rintf(y * c.invf);
-        const float dd = fmaf(y, c.invf, -r);
-        if (fabsf(dd) < c.tie)
-            return (int)__builtin_amdgcn_fmed3f(r + c.zpf, c.qminf, c.qmaxf);
-    }
+__device__ __forceinline__ int quant_fast(float y, const AttnQ& c,
+                                          bool* slow) {
+    const float r = rintf(y * c.invf);
+    const float dd = fmaf(y, c.invf, -r);
+    *slow = !(c.f32 && fabsf(dd) < c.tie);
+    return (int)__builtin_amdgcn_fmed3f(r + c.zpf, c.qminf, c.qmaxf);
+}
+
+__device__ __forceinline__ int quant_slow(float y, const AttnQ& c) {
     return quant_exact(y, c.scale, c.inv, c.zp, c.qmin, c.qmax);
 }
 
@@ -90,63 +94,138 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs d, AttnGeom g) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kg = lane >> 4;
-    const int64_t bz = blockIdx.y;
+    // the work-groups of one (b0, b1) pair read the same k and v: one XCD
+    // runs them (xcd_block, x fastest)
+    const XcdBlock blk = xcd_block(false);
+    const int64_t bz = blk.y;
     const int64_t b0 = bz / d.B1, b1 = bz - b0 * d.B1;
-    const int rt0 = blockIdx.x * g.tpw;
+    const int rt0 = (int)blk.x * g.tpw;
     const int rt1 = min(rt0 + g.tpw, g.tiles);
 
-    stage_i8_rows(sk, g.RSK, d.k + b0 * d.k_s0 + b1 * d.k_s1, g.NpS, 0, d.Ns,
-                  d.k_sn, d.k_sk, d.Kq, g.KpQ, tid);
-    stage_i8_rows(sv, g.RSV, d.v + b0 * d.v_s0 + b1 * d.v_s1, g.NV, 0, d.No,
-                  d.v_sn, d.v_sk, d.Ns, g.KpV, tid);
+    // the wave's q fragments of tile rt (rows past M read row M - 1,
+    // bytes past K are zero); the first tile's are requested before the
+    // staging below
+    const int8_t* qb = d.q + b0 * d.q_s0 + b1 * d.q_s1;
+    const int ksq = g.KpQ >> 6;
+    v4a fa[QA_ATT_KSQ];
+    auto load_q = [&](int rt) {
+        const int8_t* qr =
+            qb + min((int64_t)rt * 16 + col, (int64_t)d.M - 1) * d.q_sm;
+#pragma unroll
+        for (int ks = 0; ks < QA_ATT_KSQ; ++ks) {
+            const int c = ks * 64 + kg * 16;
+            fa[ks] = v4a{0, 0, 0, 0};
+            if (ks < ksq && c < d.Kq) fa[ks] = *(const v4a*)(qr + c);
+        }
+    };
+    load_q(rt0 + wave);
+
+    // ---- staging: k rows (16-byte chunks along the depth) and v^T rows
+    // (16 consecutive v columns of one row per chunk, scattered to 16 LDS
+    // rows), zero past N_S and the depth; every load of the thread in
+    // flight before the first store ----
+    {
+        const int8_t* kb = d.k + b0 * d.k_s0 + b1 * d.k_s1;
+        const int8_t* vb = d.v + b0 * d.v_s0 + b1 * d.v_s1;
+        const int cpr = g.KpQ >> 4;        // k chunks per row
+        const int nk = g.NpS * cpr;        // k chunks
+        const int nvr = g.NV >> 4;         // v^T row groups
+        const int nch = nk + nvr * g.KpV;  // all chunks
+        for (int e0 = tid; e0 < nch; e0 += QA_ATT_U * 256) {
+            v4a ch[QA_ATT_U];
+#pragma unroll
+            for (int u = 0; u < QA_ATT_U; ++u) {
+                const int e = e0 + u * 256;
+                ch[u] = v4a{0, 0, 0, 0};
+                if (e < nk) {
+                    const int r = e / cpr, c = (e - r * cpr) * 16;
+                    if (r < d.Ns && c < d.Kq)
+                        ch[u] = *(const v4a*)(kb + (int64_t)r * d.k_sn + c);
+                } else if (e < nch) {
+                    const int f = e - nk;
+                    const int c = f / nvr, n = (f - c * nvr) * 16;
+                    if (c < d.Ns)
+                        ch[u] = *(const v4a*)(vb + (int64_t)c * d.v_sk + n);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < QA_ATT_U; ++u) {
+                const int e = e0 + u * 256;
+                if (e < nk) {
+                    const int r = e / cpr, c = (e - r * cpr) * 16;
+                    *(v4a*)(sk + r * g.RSK + c) = ch[u];
+                } else if (e < nch) {
+                    const int f = e - nk;
+                    const int c = f / nvr, n = (f - c * nvr) * 16;
+                    const int8_t* bt = (const int8_t*)&ch[u];
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        sv[(n + j) * g.RSV + c] = bt[j];
+                }
+            }
+        }
+    }
     __syncthreads();
 
     // the wave's tile: S as columns of 16 row bytes (column n at 16 n, so a
     // lane's 4 rows 4 kg + r of a column are one word), then P over it as
     // rows of RSV bytes (P's columns past N_S meet v^T's zero rows)
     int8_t* pw = sp + wave * 16 * g.RSV;
-    const int nts = g.NpS >> 4, ksq = g.KpQ >> 6;
+    const int nts = g.NpS >> 4;
     const int ksv = g.KpV >> 6, dts = g.NV >> 4;
-    const int8_t* qb = d.q + b0 * d.q_s0 + b1 * d.q_s1;
     int8_t* const yb = d.y + b0 * d.y_s0 + b1 * d.y_s1;
 
     for (int rt = rt0 + wave; rt < rt1; rt += 4) {
         const int64_t m0 = (int64_t)rt * 16;  // the tile's first row
-        // ---- S = q k^T: the q fragments from global memory (rows past M
-        // read row M - 1, bytes past K are zero) ----
-        v4a fa[QA_ATT_KSQ];
-        {
-            const int8_t* qr = qb + min(m0 + col, (int64_t)d.M - 1) * d.q_sm;
-#pragma unroll
-            for (int ks = 0; ks < QA_ATT_KSQ; ++ks) {
-                const int c = ks * 64 + kg * 16;
-                fa[ks] = v4a{0, 0, 0, 0};
-                if (ks < ksq && c < d.Kq) fa[ks] = *(const v4a*)(qr + c);
-            }
-        }
+        if (rt != rt0 + wave) load_q(rt);  // a later tile of the wave
         // ---- S quantized a 16 x 16 block at a time: the stored bytes +
         // 128 of the lane's 4 rows, one word a column ----
-        for (int nt = 0; nt < nts; ++nt) {
-            v4a acc = v4a{0, 0, 0, 0};
+        for (int nt0 = 0; nt0 < nts; nt0 += 4) {  // 4 blocks at a time
+            v4a acc[4];
 #pragma unroll
-            for (int ks = 0; ks < QA_ATT_KSQ; ++ks)
-                if (ks < ksq)
-                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        fa[ks],
-                        *(const v4a*)(sk + (nt * 16 + col) * g.RSK + ks * 64 +
-                                      kg * 16),
-                        acc, 0, 0, 0);
-            if (nt * 16 + col < d.Ns) {
-                uint32_t w = 0;
+            for (int u = 0; u < 4; ++u) {
+                acc[u] = v4a{0, 0, 0, 0};
+                const int nt = min(nt0 + u, nts - 1);
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    w |= (uint32_t)((quant((float)((double)(int64_t)acc[r] *
-                                                   d.sS),
-                                           d.S) -
-                                     d.S.so + 128) &
-                                    255)
-                         << (8 * r);
-                *(uint32_t*)(pw + (nt * 16 + col) * 16 + 4 * kg) = w;
+                for (int ks = 0; ks < QA_ATT_KSQ; ++ks)
+                    if (ks < ksq)
+                        acc[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            fa[ks],
+                            *(const v4a*)(sk + (nt * 16 + col) * g.RSK +
+                                          ks * 64 + kg * 16),
+                            acc[u], 0, 0, 0);
+            }
+            float yf[4][4];
+            int qv[4][4];
+            uint32_t slow = 0;  // bit 4 u + r: the double form
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    bool sl;
+                    yf[u][r] = (float)((double)acc[u][r] * d.sS);
+                    qv[u][r] = quant_fast(yf[u][r], d.S, &sl);
+                    slow |= (uint32_t)sl << (4 * u + r);
+                }
+            if (slow) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if ((slow >> (4 * u + r)) & 1)
+                            qv[u][r] = quant_slow(yf[u][r], d.S);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int n = (nt0 + u) * 16 + col;
+                if (nt0 + u < nts && n < d.Ns) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        w |= (uint32_t)((qv[u][r] - d.S.so + 128) & 255)
+                             << (8 * r);
+                    *(uint32_t*)(pw + n * 16 + 4 * kg) = w;
+                }
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -194,34 +273,75 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs d, AttnGeom g) {
                     sum[h] += __shfl_xor(sum[h], o);
                 const double rsum = 1.0 / sum[h];  // one division a row
                 int8_t* prow = pw + (4 * kg + r0 + h) * g.RSV;
+                float yp[16];
+                int qp[16];
+                uint32_t slow = 0;
+#pragma unroll
+                for (int nt = 0; nt < 16; ++nt) {
+                    bool sl;
+                    yp[nt] = (float)(e[h][nt] * rsum);
+                    qp[nt] = quant_fast(yp[nt], d.P, &sl);
+                    slow |= (uint32_t)sl << nt;
+                }
+                if (slow) {
+#pragma unroll
+                    for (int nt = 0; nt < 16; ++nt)
+                        if ((slow >> nt) & 1) qp[nt] = quant_slow(yp[nt], d.P);
+                }
 #pragma unroll
                 for (int nt = 0; nt < 16; ++nt)
                     if (nt < nts && nt * 16 + col < d.Ns)
-                        prow[nt * 16 + col] = (int8_t)(
-                            quant((float)(e[h][nt] * rsum), d.P) - d.P.so);
+                        prow[nt * 16 + col] = (int8_t)(qp[nt] - d.P.so);
             }
         }
         // the wave's P bytes before its reads of them
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        // ---- O = P v: 16 rows x NV columns ----
-        for (int dt = 0; dt < dts; ++dt) {
-            v4a acc2 = v4a{0, 0, 0, 0};
-            for (int ks = 0; ks < ksv; ++ks) {
-                const int c = ks * 64 + kg * 16;
-                acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                    *(const v4a*)(pw + col * g.RSV + c),
-                    *(const v4a*)(sv + (dt * 16 + col) * g.RSV + c), acc2, 0,
-                    0, 0);
-            }
-            const int n = dt * 16 + col;
-            if (n >= d.No) continue;
+        // ---- O = P v: 16 rows x NV columns, 4 blocks at a time ----
+        for (int dt0 = 0; dt0 < dts; dt0 += 4) {
+            v4a acc2[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t m = m0 + 4 * kg + r;
-                if (m >= d.M) continue;
-                yb[m * d.y_sm + n * d.y_sn] = (int8_t)(
-                    quant((float)((double)(int64_t)acc2[r] * d.sO), d.O) -
-                    d.O.so);
+            for (int u = 0; u < 4; ++u) {
+                acc2[u] = v4a{0, 0, 0, 0};
+                const int dt = min(dt0 + u, dts - 1);
+                for (int ks = 0; ks < ksv; ++ks) {
+                    const int c = ks * 64 + kg * 16;
+                    acc2[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        *(const v4a*)(pw + col * g.RSV + c),
+                        *(const v4a*)(sv + (dt * 16 + col) * g.RSV + c),
+                        acc2[u], 0, 0, 0);
+                }
+            }
+            float yo[4][4];
+            int qo[4][4];
+            uint32_t slow = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    bool sl;
+                    yo[u][r] = (float)((double)acc2[u][r] * d.sO);
+                    qo[u][r] = quant_fast(yo[u][r], d.O, &sl);
+                    slow |= (uint32_t)sl << (4 * u + r);
+                }
+            if (slow) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if ((slow >> (4 * u + r)) & 1)
+                            qo[u][r] = quant_slow(yo[u][r], d.O);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int n = (dt0 + u) * 16 + col;
+                if (dt0 + u >= dts || n >= d.No) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t m = m0 + 4 * kg + r;
+                    if (m < d.M)
+                        yb[m * d.y_sm + n * d.y_sn] =
+                            (int8_t)(qo[u][r] - d.O.so);
+                }
             }
         }
         // this tile's reads of P before the next tile's S words
@@ -247,8 +367,14 @@ bool attn_geom(const qa_attention_desc* d, AttnGeom* g, int64_t* lds,
         *why = "needs the exponential table and positive scales";
     } else if (qk.a_sk != 1 || qk.K % 16 != 0 || qk.a_sm % 16 != 0 ||
                qk.a_s0 % 16 != 0 || qk.a_s1 % 16 != 0 ||
-               (uintptr_t)qk.a % 16 != 0) {
-        *why = "needs q rows of 16-byte aligned, contiguous depth";
+               (uintptr_t)qk.a % 16 != 0 || qk.b_sk != 1 ||
+               qk.b_sn % 16 != 0 || qk.b_s0 % 16 != 0 ||
+               qk.b_s1 % 16 != 0 || (uintptr_t)qk.b % 16 != 0 ||
+               av.b_sn != 1 || av.b_sk % 16 != 0 || av.b_s0 % 16 != 0 ||
+               av.b_s1 % 16 != 0 || (uintptr_t)av.b % 16 != 0 ||
+               av.N % 16 != 0) {
+        *why = "needs q and k rows and v columns of 16-byte aligned, "
+               "contiguous bytes";
     } else if (qk.B0 < 1 || qk.B1 < 1 || qk.M < 1 || qk.N < 1 ||
                qk.N > 256 || qk.K < 1 || qk.K > 64 * QA_ATT_KSQ || av.N < 1 ||
                av.N > 256 || av.K != qk.N || av.M != qk.M ||
