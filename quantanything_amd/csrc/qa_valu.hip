@@ -198,10 +198,122 @@ bool launch_gemm_valu(const void* A, int a_code, const void* B, int b_code,
     return check("k_gemm_valu");
 }
 
+// float32 convolution of one group as an implicit GEMM on the matrix cores
+// (v_mfma_f32_16x16x4f32: lane i + 16 k holds A[i][k] and B[k][i], result
+// register r of lane j + 16 g is C[4 g + r][j]). A work-group computes 64
+// output pixels x 64 output channels of one image; each wave 16 pixels x
+// the 64 channels (4 MFMA tiles). K = Cg KH KW runs in slices of 32: the
+// im2col slice of the input (zero at the padding) and the weight slice go
+// to LDS (rows of 80 floats, so that the 4 lane groups of a fragment read
+// disjoint banks), double-buffered: slice s + 1's loads are in flight
+// while slice s's MFMAs run. Products are float32, summed in float32 in
+// another order than k_conv_f32 (agreement within float32 rounding).
+constexpr int CF_K = 32, CF_RS = 80;
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kThreads) void k_conv_f32_mfma(
+    const float* __restrict__ x, const float* __restrict__ w,
+    float* __restrict__ y, ConvArgs a, uint64_t mg_khw, uint64_t mg_kw) {
+    __shared__ float sa[2][CF_K * CF_RS];  // [k][pixel]
+    __shared__ float sb[2][CF_K * CF_RS];  // [k][channel]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int OHW = a.OH * a.OW;
+    const int m0 = blockIdx.x * 64, co0 = blockIdx.y * 64;
+    const int n = blockIdx.z;
+    const int KHW = a.KH * a.KW;
+    const int K = a.Cg * KHW;
+    const int64_t HW = (int64_t)a.H * a.W;
+    const float* xn = x + (int64_t)n * a.Cg * HW;
+    // this thread's staging: pixel tid % 64 of the A slice (k rows tid / 64
+    // + 4 u), channel tid / 32 + 8 u of the B slice (k column tid % 32)
+    const int ap = tid & 63, ak = tid >> 6;
+    const int pix = m0 + ap;
+    const bool pin = pix < OHW;
+    const int oy = pin ? pix / a.OW : 0;
+    const int ox = pin ? pix - oy * a.OW : 0;
+    const int iy0 = oy * a.SH - a.PH, ix0 = ox * a.SW - a.PW;
+    const int bk = tid & 31, bc = tid >> 5;
+    float ra[8], rb[8];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int k = k0 + ak + 4 * u;
+            float v = 0.f;
+            if (pin && k < K) {
+                const int ci = (int)(((uint64_t)(uint32_t)k * mg_khw) >> 32);
+                const int t = k - ci * KHW;
+                const int ky = (int)(((uint64_t)(uint32_t)t * mg_kw) >> 32);
+                const int kx = t - ky * a.KW;
+                const int iy = iy0 + ky * a.DH, ix = ix0 + kx * a.DW;
+                if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+                    v = xn[ci * HW + (int64_t)iy * a.W + ix];
+            }
+            ra[u] = v;
+            const int co = co0 + bc + 8 * u, kb = k0 + bk;
+            rb[u] = (co < a.Cout && kb < K) ? w[(int64_t)co * K + kb] : 0.f;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            sa[buf][(ak + 4 * u) * CF_RS + ap] = ra[u];
+            sb[buf][bk * CF_RS + bc + 8 * u] = rb[u];
+        }
+    };
+    v4f acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int col = lane & 15, kg = lane >> 4;
+    const int nsl = (K + CF_K - 1) / CF_K;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int s = 0; s < nsl; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < nsl) load((s + 1) * CF_K);  // in flight during the MFMAs
+#pragma unroll
+        for (int kk = 0; kk < CF_K; kk += 4) {
+            const float fa = sa[buf][(kk + kg) * CF_RS + wave * 16 + col];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                    fa, sb[buf][(kk + kg) * CF_RS + j * 16 + col], acc[j], 0,
+                    0, 0);
+        }
+        if (s + 1 < nsl) store(buf ^ 1);  // the buffer last read at s - 1
+        __syncthreads();
+    }
+    // lane j + 16 g holds pixels m0 + 16 wave + 4 g + r of channel 16 jt + j
+    float* yn = y + (int64_t)n * a.Cout * OHW;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int co = co0 + j * 16 + col;
+        if (co >= a.Cout) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int p = m0 + wave * 16 + 4 * kg + r;
+            if (p < OHW) yn[(int64_t)co * OHW + p] = acc[j][r];
+        }
+    }
+}
+
 bool launch_conv_f32(const float* x, const float* w, float* y,
                      const ConvArgs& a, hipStream_t st) {
     const int OHW = a.OH * a.OW;
     if (OHW <= 0 || a.N <= 0 || a.Cout <= 0) return true;
+    const int64_t K = (int64_t)a.Cg * a.KH * a.KW;
+    // (the multiply-shift divisions of k are exact for k < 2^16)
+    if (a.G == 1 && K < 65536 && a.N <= 65535 &&
+        ceil_div(a.Cout, 64) <= 65535) {
+        const int khw = a.KH * a.KW;
+        const uint64_t mg_khw = (((uint64_t)1 << 32) + khw - 1) / khw;
+        const uint64_t mg_kw = (((uint64_t)1 << 32) + a.KW - 1) / a.KW;
+        const dim3 grid((unsigned)ceil_div(OHW, 64),
+                        (unsigned)ceil_div(a.Cout, 64), (unsigned)a.N);
+        k_conv_f32_mfma<<<grid, kThreads, 0, st>>>(x, w, y, a, mg_khw, mg_kw);
+        return check("k_conv_f32_mfma");
+    }
     dim3 grid((unsigned)ceil_div(OHW, kThreads),
               (unsigned)std::min<int64_t>(a.Cout, 65535),
               (unsigned)std::min<int64_t>(a.N, 65535));
