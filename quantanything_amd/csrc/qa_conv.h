@@ -180,8 +180,7 @@ bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
 // epilogue on 128 x 128 blocks (qa_gemm_big.hip); `epi` as chosen by
 // launch_conv_mfma.
 bool gemm_big_applies(const ConvArgs& b, int epi);
-// variant: the ring of K-steps in flight (0: the default; see the kernel)
-bool launch_gemm_big(const ConvArgs& b, hipStream_t st, int variant = 0);
+bool launch_gemm_big(const ConvArgs& b, hipStream_t st);
 // int8 convolutions over bands of output rows with the input band and the
 // weights in LDS (qa_conv_band.hip); wm = 16-channel groups per work-group.
 bool conv_band_applies(const ConvArgs& b, int epi, int wm);

@@ -294,7 +294,7 @@ bool gemm_big_applies(const ConvArgs& b, int epi) {
            xa % 16 == 0 && b.y_code == 1 && b.M < ((int64_t)1 << 31);
 }
 
-bool launch_gemm_big(const ConvArgs& b, hipStream_t st, int variant) {
+bool launch_gemm_big(const ConvArgs& b, hipStream_t st) {
     const int64_t tiles = ceil_div(b.M, GB_M) * ceil_div(b.Cout, GB_N);
     if (tiles >= ((int64_t)1 << 31)) {
         set_error("launch_gemm_big", "grid too large");
@@ -316,37 +316,14 @@ bool launch_gemm_big(const ConvArgs& b, hipStream_t st, int variant) {
 #undef QA_GB_CASE
         }
     };
-    // deeper rings (more K-steps' loads in flight, more registers): for
-    // no flags or a residual Add only
-    auto go_deep = [&](auto kp, auto kbk) {
-        constexpr int KP = decltype(kp)::value, KBK = decltype(kbk)::value;
-        if (flags == 1)
-            k_gemm_big<KP, KBK, true, false, false><<<grid, 256, 0, st>>>(b);
-        else
-            k_gemm_big<KP, KBK, false, false, false><<<grid, 256, 0, st>>>(b);
-    };
+    // 128-byte steps when K allows, else 64-byte steps, the next step's
+    // loads in flight (measured on the ViT-S GEMMs: deeper rings, which
+    // cost VGPRs and so occupancy, were not faster in the pass)
     using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
-    using I4 = std::integral_constant<int, 4>;
-    using B64 = std::integral_constant<int, 64>;
-    using B128 = std::integral_constant<int, 128>;
-    // variant: 0 the default (128-byte steps when K allows, else 64, the
-    // next step's loads in flight), 1 / 2: two / three 128-byte steps in
-    // flight, 3 / 4: two / four 64-byte steps in flight
-    const bool deep_ok = flags == 0 || flags == 1;
-    if (deep_ok && variant == 1 && K % 128 == 0)
-        go_deep(I2{}, B128{});
-    else if (deep_ok && variant == 2 && K % 128 == 0)
-        go_deep(I3{}, B128{});
-    else if (deep_ok && variant == 3)
-        go_deep(I2{}, B64{});
-    else if (deep_ok && variant == 4)
-        go_deep(I4{}, B64{});
-    else if (K % 128 == 0)
-        go(I1{}, B128{});
+    if (K % 128 == 0)
+        go(I1{}, std::integral_constant<int, 128>{});
     else
-        go(I1{}, B64{});
+        go(I1{}, std::integral_constant<int, 64>{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("launch_gemm_big", e);

@@ -1793,8 +1793,7 @@ class DeviceExecutor:
         out = [0]
         if d.H == d.W == d.KH == d.KW == 1 and d.G == 1 and \
                 d.w_layout == 0 and d.C % 64 == 0:
-            # the large-GEMM kernel (128 x 128 blocks), its ring variants
-            out += [0x10400 | v for v in range(5)]
+            out.append(0x10400)  # the large-GEMM kernel (128 x 128 blocks)
         if d.w_layout == 0 and d.G == 1 and d.C % 16 == 0 and \
                 d.OW <= 256 and d.epi_plan and (d.H > 1 or d.W > 1):
             # bands of output rows, operands in LDS (the library checks the
