@@ -378,8 +378,22 @@ def main():
 
     def work(name):
         """(layer, ops, bytes) of a conv launch ("qconv:": float input;
-        "pair:" / "chain:": two convs, the intermediate not in HBM)."""
+        "pair:" / "chain:": two convs, the intermediate not in HBM;
+        "pairtail:": a pair and the 1x1 conv reading the Concat it ends,
+        whose last channels come from LDS)."""
         kind, _, lname = name.partition(":")
+        if kind == "pairtail":
+            a, b, t = lname.split("+")
+            if a not in layers or b not in layers or t not in layers:
+                return None
+            la, lb, lt = layers[a], layers[b], layers[t]
+            xs = shapes[la.data_inputs[0]]
+            mid = conv_out_shape(la, xs)
+            oa, ba = layer_work(la, xs)
+            ob, bb = layer_work(lb, mid)
+            ot, bt = layer_work(lt, shapes[lt.data_inputs[0]])
+            return (lt, oa + ob + ot,
+                    ba + bb + bt - 3 * int(np.prod(mid)))
         if kind in ("pair", "chain"):
             a, _, b = lname.partition("+")
             if a not in layers or b not in layers:

@@ -400,6 +400,24 @@ int qa_conv_pair_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
 int qa_d_conv_pair(const qa_conv_desc* d1, const qa_conv_desc* d2,
                    void* stream);
 
+/* qa_d_conv_pair (C = 16 or 32) with the C2f block's last 1x1
+ * convolution d3 in the same launch: d3 reads the block's Concat, a dense
+ * channels-last int8 tensor of at most 256 channels whose last C channels
+ * are the pair's output or its rescaled copy (d2->y or d2->y2 == d3->x +
+ * d3->C - C, the same pixel stride) and whose other channels earlier
+ * launches have written; d3 has a table plan, no residual or rescaled copy
+ * and at most 128 output channels (a multiple of 16). The results are what
+ * qa_d_conv_pair then qa_d_conv(d3) store (d2->y and d2->y2 are still
+ * written). Returns -1, launching nothing, for any
+ * other triple; the reference runs the three convolutions one after another
+ * (quant_layers.py:320-335 three times). qa_conv_pair_tail_supported
+ * checks a triple without launching (1 or 0). */
+int qa_conv_pair_tail_supported(const qa_conv_desc* d1,
+                                const qa_conv_desc* d2,
+                                const qa_conv_desc* d3);
+int qa_d_conv_pair_tail(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                        const qa_conv_desc* d3, void* stream);
+
 /* A convolution followed by a 1x1 convolution in one launch (the stride-2
  * conv feeding a C2f block's first 1x1 conv): d1 an int8 convolution of
  * C = 16, 32 or 64 output channels (packed layout 0, one group, a table

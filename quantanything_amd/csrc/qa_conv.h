@@ -198,7 +198,11 @@ int fast_io_args(const ConvArgs& a, ConvArgs& b, int epi);
 // launch form.
 bool conv_pair_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
                        int epi2);
-bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2, hipStream_t st);
+bool conv_pair_tail_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
+                            int epi2, const ConvArgs& b3, int epi3);
+// b3: the C2f block's cv2 run in the same launch (conv_pair_tail_applies)
+bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2, hipStream_t st,
+                      const ConvArgs* b3 = nullptr);
 // A convolution (weights-in-registers kernel, Cout 16, 32 or 64) whose
 // output feeds only a 1x1 convolution of the same width: both in one
 // launch, the intermediate kept per wave in LDS (qa_conv_wr.hip).

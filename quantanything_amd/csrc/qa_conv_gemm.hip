@@ -743,6 +743,44 @@ QA_API int qa_d_conv_pair(const qa_conv_desc* d1, const qa_conv_desc* d2,
     return launch_conv_pair(b1, b2, (hipStream_t)stream_) ? 0 : -1;
 }
 
+static bool pair_tail_args(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                           const qa_conv_desc* d3, ConvArgs& b1, ConvArgs& b2,
+                           ConvArgs& b3, const char* who) {
+    ConvArgs a1, a2, a3;
+    if (desc_args(d1, a1, who) != 1 || desc_args(d2, a2, who) != 1 ||
+        desc_args(d3, a3, who) != 1)
+        return false;
+    const int e1 = fast_io_args(a1, b1, -1);  // Q8_TABLE or -1
+    const int e2 = fast_io_args(a2, b2, -1);
+    const int e3 = fast_io_args(a3, b3, -1);
+    return conv_pair_tail_applies(b1, e1, b2, e2, b3, e3);
+}
+
+QA_API int qa_conv_pair_tail_supported(const qa_conv_desc* d1,
+                                       const qa_conv_desc* d2,
+                                       const qa_conv_desc* d3) {
+    ConvArgs b1, b2, b3;
+    return pair_tail_args(d1, d2, d3, b1, b2, b3,
+                          "qa_conv_pair_tail_supported")
+               ? 1
+               : 0;
+}
+
+QA_API int qa_d_conv_pair_tail(const qa_conv_desc* d1,
+                               const qa_conv_desc* d2,
+                               const qa_conv_desc* d3, void* stream_) {
+    ConvArgs b1, b2, b3;
+    if (!pair_tail_args(d1, d2, d3, b1, b2, b3, "qa_d_conv_pair_tail")) {
+        set_error("qa_d_conv_pair_tail",
+                  "needs a fused pair (C 16 or 32) whose output is the "
+                  "last channels of a 1x1 convolution's dense input (at most "
+                  "256 input and 128 output channels, table plan, no "
+                  "residual or second output)");
+        return -1;
+    }
+    return launch_conv_pair(b1, b2, (hipStream_t)stream_, &b3) ? 0 : -1;
+}
+
 static bool chain_args(const qa_conv_desc* d1, const qa_conv_desc* d2,
                        ConvArgs& b1, ConvArgs& b2, const char* who) {
     ConvArgs a1, a2;

@@ -19,6 +19,18 @@
 // columns, the k-group layout of the packed layout-0 weights (tap kg / CB,
 // channels 16 (kg % CB) ..), one k-group offset table for both bands (same
 // width and pixel stride).
+//
+// TAIL (C 16/32): the C2f block's last 1x1 convolution (cv2) runs in the
+// same launch. Its input is the block's Concat, whose last C channels are
+// this pair's output or its rescaled second output, and whose other
+// channels (the prefix) earlier launches wrote. The band's output pixels' prefix channels are staged in LDS with
+// everything else; per phase-2 tile conv 2's output words also go to a
+// per-wave LDS tile (16 pixels x C bytes), and cv2's MFMAs read their
+// fragments from those two, with cv2's weights staged in LDS; cv2's table
+// epilogue stores its output. cv2 is a separate launch otherwise, and for
+// C = 64, where the pair's weights leave too little LDS for cv2's weights
+// and bands of more than two rows (every extra band stages all weights
+// again: slower than the two launches).
 #include "qa_conv_mfma.h"
 
 namespace qa {
@@ -38,15 +50,21 @@ struct PairGeom {
     int RSW;               // LDS row stride of the staged weights
     int lds;               // dynamic LDS bytes (0: does not fit)
     uint32_t m_w, m_bw, m_kgp;  // ceil(2^32 / d), d >= 2
+    // TAIL: cv2's weights (T3 16-channel blocks, rows of RSW3 bytes, KS3
+    // K-steps), the per-wave tiles (16 rows of RT bytes) and the band's
+    // prefix channels (rows of RP bytes a pixel) in LDS, at these offsets;
+    // the pair's output (t_y2: its second output) is Concat channels off_d ..
+    int t_w3, t_tile, t_pre, RSW3, KS3, T3, RT, RP, off_d, Ctot, t_y2;
+    uint32_t m_kgp3;
 };
 
 __device__ __forceinline__ int cp_div(int n, uint32_t m) {
     return (int)__umulhi((uint32_t)n, m);
 }
 
-template <int WM, bool RES>
+template <int WM, bool RES, bool TAIL>
 __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
-                                                     PairGeom g) {
+                                                     PairGeom g, ConvArgs a3) {
     constexpr int C = 16 * WM;          // channels of every tensor
     constexpr int KS = (9 * WM + 3) / 4;  // K-steps: KGp = round_up(9 WM, 4)
     constexpr int LCPP = WM == 1 ? 0 : WM == 2 ? 1 : 2;  // log2 chunks/pixel
@@ -60,6 +78,12 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
     __shared__ int s_tab2[768];
     __shared__ int4 s_pc[2][C];
     __shared__ uint32_t s_corr[2][C];
+    __shared__ int s_tab3[TAIL ? 256 : 1];
+    __shared__ int4 s_pc3[TAIL ? 128 : 1];
+    __shared__ uint32_t s_corr3[TAIL ? 128 : 1];
+    int8_t* s_w3 = (int8_t*)lds4 + g.t_w3;    // TAIL: cv2's weights
+    int8_t* s_t = (int8_t*)lds4 + g.t_tile;   // TAIL: per-wave tiles
+    int8_t* s_pre = (int8_t*)lds4 + g.t_pre;  // TAIL: the band's prefix
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kgl = lane >> 4;
@@ -158,6 +182,53 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
                 *(v4i*)(s_w1 + aw[u]) = w1[u];
                 *(v4i*)(s_w2 + aw[u]) = w2[u];
             }
+        if (TAIL) {  // cv2's weight rows, table and per-channel constants
+            const int kgp3 = 4 * g.KS3;
+            const int n3 = 16 * g.T3 * kgp3;
+            const int rs3 = (int)a3.wp_rstride;
+            for (int e0 = tid; e0 < n3; e0 += 4 * CP_NT) {
+                v4i w3[4];
+                int a3w[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int e = e0 + u * CP_NT;
+                    const int r = cp_div(e, g.m_kgp3), k = e - r * kgp3;
+                    const bool ok = e < n3;
+                    a3w[u] = ok ? r * g.RSW3 + k * 16 : -1;
+                    w3[u] = *(const v4i*)(a3.wp + (ok ? r * rs3 + k * 16 : 0));
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (a3w[u] >= 0) *(v4i*)(s_w3 + a3w[u]) = w3[u];
+            }
+            // the prefix channels of the band's output pixels
+            const int cpp = g.off_d >> 4;
+            const int np = R * OW * cpp;
+            const int8_t* xp = (const int8_t*)a3.x +
+                               ((int64_t)n * OH + oy0) * OW * a3.x_sp;
+            for (int e0 = tid; e0 < np; e0 += 4 * CP_NT) {
+                v4i pv[4];
+                int ap[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int e = e0 + u * CP_NT;
+                    const bool ok = e < np;
+                    const int px = ok ? e / cpp : 0, c = ok ? e - px * cpp : 0;
+                    ap[u] = ok ? px * g.RP + c * 16 : -1;
+                    pv[u] = *(const v4i*)(xp + (int64_t)px * a3.x_sp + c * 16);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (ap[u] >= 0) *(v4i*)(s_pre + ap[u]) = pv[u];
+            }
+            for (int i = tid; i < 256; i += CP_NT)
+                s_tab3[i] = ((const int*)((const char*)a3.plan + PLAN_E))[i];
+            for (int c = tid; c < 16 * g.T3; c += CP_NT) {
+                const int cl = min(c, a3.Cout - 1);
+                s_pc3[c] = ((const int4*)((const char*)a3.plan + PLAN_CH))[cl];
+                s_corr3[c] = a3.corr ? (uint32_t)a3.corr[cl] : 0u;
+            }
+        }
     }
     __syncthreads();
 
@@ -263,6 +334,7 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
             const int r = cp_div(qp, g.m_w), ox = qp - r * OW;
             v4i acc[WM];
             tile_mfma(s_m + (r * g.BW + ox) * g.PS, acc);
+            int8_t* tw = s_t + wave * 16 * g.RT;  // TAIL: the wave's tile
 #pragma unroll
             for (int i = 0; i < WM; ++i) {
                 int e[4];
@@ -288,12 +360,74 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
                 const uint32_t wy =
                     quad_transpose(pack_entries(e, 0), sel1, sel2);
                 if (pok) *(uint32_t*)((int8_t*)a2.y + p * a2.y_pst + c0) = wy;
+                uint32_t w2 = 0;
                 if (a2.y2) {
-                    const uint32_t w2 =
-                        quad_transpose(pack_entries(e, 1), sel1, sel2);
+                    w2 = quad_transpose(pack_entries(e, 1), sel1, sel2);
                     if (pok)
                         *(uint32_t*)((int8_t*)a2.y2 + p * a2.y2_pst + c0) = w2;
                 }
+                if (TAIL)
+                    *(uint32_t*)(tw + (4 * kgl + q) * g.RT + c0) =
+                        g.t_y2 ? w2 : wy;
+            }
+            if (TAIL) {
+                // the wave's tile words before its reads of them
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                const int4 h3 = *(const int4*)a3.plan;
+                constexpr int TJ = 4;  // cv2's channel blocks at a time
+                for (int j0 = 0; j0 < g.T3; j0 += TJ) {
+                    v4i acc3[TJ];
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j) acc3[j] = v4i{0, 0, 0, 0};
+#pragma unroll
+                    for (int s3 = 0; s3 < 4; ++s3) {
+                        if (s3 >= g.KS3) continue;
+                        // row col of the tile: pixel qp of the band
+                        const int c16 = (4 * s3 + kgl) * 16;
+                        const v4i fa3 =
+                            c16 < g.off_d
+                                ? *(const v4i*)(s_pre + qp * g.RP + c16)
+                                : c16 < g.Ctot
+                                      ? *(const v4i*)(tw + col * g.RT + c16 -
+                                                      g.off_d)
+                                      : v4i{0, 0, 0, 0};
+#pragma unroll
+                        for (int j = 0; j < TJ; ++j)
+                            if (j0 + j < g.T3)
+                                acc3[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                    fa3,
+                                    *(const v4i*)(s_w3 +
+                                                  (16 * (j0 + j) + col) *
+                                                      g.RSW3 +
+                                                  64 * s3 + 16 * kgl),
+                                    acc3[j], 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j) {
+                        const int c3 = 16 * (j0 + j) + cq;
+                        if (j0 + j >= g.T3) continue;
+                        const int4 pc3 = s_pc3[16 * (j0 + j) + col];
+                        const int64_t cc3 = plan_fold(
+                            (int64_t)(((uint64_t)(uint32_t)pc3.w << 32) |
+                                      (uint32_t)pc3.z),
+                            s_corr3[16 * (j0 + j) + col], pc3.x);
+                        int e3[4];
+#pragma unroll
+                        for (int rr = 0; rr < 4; ++rr)
+                            e3[rr] = s_tab3[med3_i32(
+                                             plan_q0(acc3[j][rr], pc3.x, cc3,
+                                                     pc3.y),
+                                             h3.x, h3.y) -
+                                             h3.x];
+                        const uint32_t wy3 =
+                            quad_transpose(pack_entries(e3, 0), sel1, sel2);
+                        if (pok && c3 < a3.Cout)
+                            *(uint32_t*)((int8_t*)a3.y + p * a3.y_pst + c3) =
+                                wy3;
+                    }
+                }
+                // this tile's reads before the next tile's words
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
             }
         }
     }
@@ -309,7 +443,8 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
 template <bool RES>
 __global__ __launch_bounds__(CP_NT) void k_conv_pair_cs(ConvArgs a1,
                                                         ConvArgs a2,
-                                                        PairGeom g) {
+                                                        PairGeom g,
+                                                        ConvArgs) {
     constexpr int WM = 8, C = 128, KS = 18, LCPP = 3;
     extern __shared__ int4 lds4[];
     int8_t* s_x = (int8_t*)lds4;         // input band
@@ -514,9 +649,9 @@ uint32_t cp_magic(int64_t d) {
                       (uint64_t)std::max<int64_t>(d, 2));
 }
 
-// Geometry for bands of R output rows; lds = 0 when it does not fit or the
-// staging exceeds what the threads hold.
-PairGeom pair_geom(const ConvArgs& b, int R) {
+// Geometry for bands of R output rows (with b3: and cv2's tail); lds = 0
+// when it does not fit or the staging exceeds what the threads hold.
+PairGeom pair_geom(const ConvArgs& b, int R, const ConvArgs* b3 = nullptr) {
     const int C = b.Cg, wm = C / 16;
     PairGeom g;
     g.R = R;
@@ -531,7 +666,27 @@ PairGeom pair_geom(const ConvArgs& b, int R) {
     g.mb_bytes = (int)std::min<int64_t>(mb, 1 << 30);
     // 128 channels: the weights go straight to VGPRs, not through LDS
     const int64_t wbytes = C == 128 ? 0 : 2 * (int64_t)C * g.RSW;
-    const int64_t bytes = xb + mb + wbytes + b.KGp * 4;
+    int64_t bytes = xb + mb + wbytes + b.KGp * 4;
+    g.t_w3 = g.t_tile = g.t_pre = g.RSW3 = g.KS3 = g.T3 = g.RT = g.RP = 0;
+    g.off_d = g.Ctot = g.t_y2 = 0;
+    g.m_kgp3 = 2;
+    if (b3) {
+        bytes = (bytes + 15) / 16 * 16;
+        g.Ctot = b3->Cg;
+        g.off_d = b3->Cg - C;
+        g.KS3 = b3->KGp / 4;
+        g.T3 = (b3->Cout + 15) / 16;
+        g.RSW3 = b3->KGp * 16 + 16;
+        g.RT = C + 16;
+        g.t_w3 = (int)bytes;
+        bytes += (int64_t)16 * g.T3 * g.RSW3;
+        g.t_tile = (int)bytes;
+        bytes += (int64_t)CP_NW * 16 * g.RT;
+        g.RP = g.off_d + 16;
+        g.t_pre = (int)bytes;
+        bytes += (int64_t)R * b.OW * g.RP;
+        g.m_kgp3 = cp_magic(b3->KGp);
+    }
     const int64_t bchunks = (int64_t)(R + 4) * b.W * wm;
     const int64_t wchunks = C == 128 ? 0 : (int64_t)C * b.KGp;
     g.lds = bytes <= 140 * 1024 && bchunks <= (int64_t)CP_SB * CP_NT &&
@@ -545,18 +700,27 @@ PairGeom pair_geom(const ConvArgs& b, int R) {
     return g;
 }
 
-using PairKern = void (*)(ConvArgs, ConvArgs, PairGeom);
+using PairKern = void (*)(ConvArgs, ConvArgs, PairGeom, ConvArgs);
 
-PairKern pair_kernel(int wm, bool res) {
+PairKern pair_kernel(int wm, bool res, bool tail) {
+    if (tail) {
+        switch (wm * 2 + (res ? 1 : 0)) {
+            case 2: return &k_conv_pair<1, false, true>;
+            case 3: return &k_conv_pair<1, true, true>;
+            case 4: return &k_conv_pair<2, false, true>;
+            case 5: return &k_conv_pair<2, true, true>;
+            default: return nullptr;
+        }
+    }
     switch (wm * 2 + (res ? 1 : 0)) {
         case 16: return &k_conv_pair_cs<false>;
         case 17: return &k_conv_pair_cs<true>;
-        case 2: return &k_conv_pair<1, false>;
-        case 3: return &k_conv_pair<1, true>;
-        case 4: return &k_conv_pair<2, false>;
-        case 5: return &k_conv_pair<2, true>;
-        case 8: return &k_conv_pair<4, false>;
-        case 9: return &k_conv_pair<4, true>;
+        case 2: return &k_conv_pair<1, false, false>;
+        case 3: return &k_conv_pair<1, true, false>;
+        case 4: return &k_conv_pair<2, false, false>;
+        case 5: return &k_conv_pair<2, true, false>;
+        case 8: return &k_conv_pair<4, false, false>;
+        case 9: return &k_conv_pair<4, true, false>;
         default: return nullptr;
     }
 }
@@ -592,10 +756,40 @@ bool conv_pair_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
     return pair_geom(b1, 1).lds > 0;
 }
 
+// cv2 of a C2f block after the pair whose output is the last C channels
+// of its input (the block's Concat): a 1x1 stride-1 int8 conv with a table
+// plan, no residual, second output or row sums, dense channels-last input
+// and output, at most 256 input and 128 output channels.
+bool conv_pair_tail_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
+                            int epi2, const ConvArgs& b3, int epi3) {
+    const int C = b1.Cout;
+    if (C > 32 || !conv_pair_applies(b1, epi1, b2, epi2)) return false;
+    if (!(epi3 == Q8_TABLE && b3.mode == EPI_QUANT && b3.fastio && b3.plan &&
+          b3.G == 1 && b3.layout == 0 && b3.KH == 1 && b3.KW == 1 &&
+          b3.SH == 1 && b3.SW == 1 && b3.PH == 0 && b3.PW == 0 &&
+          b3.H == b2.OH && b3.W == b2.OW && b3.OH == b3.H && b3.OW == b3.W &&
+          b3.N == b2.N && b3.x_code == 1 && b3.x_sc == 1 && b3.rowsum == 0 &&
+          b3.res == nullptr && b3.y2 == nullptr && b3.y_code == 1 &&
+          b3.Cg % 16 == 0 && b3.Cg <= 256 && b3.Cg >= C &&
+          b3.KGp == 4 * ((b3.Cg / 16 + 3) / 4) && b3.Cout % 16 == 0 &&
+          b3.Cout <= 128 && (uintptr_t)b3.x % 16 == 0 &&
+          b3.x_sp % 16 == 0 &&
+          b3.x_sn == (int64_t)b3.H * b3.W * b3.x_sp &&
+          (((const int8_t*)b2.y == (const int8_t*)b3.x + (b3.Cg - C) &&
+            b2.y_pst == b3.x_sp) ||
+           (b2.y2 != nullptr &&
+            (const int8_t*)b2.y2 == (const int8_t*)b3.x + (b3.Cg - C) &&
+            b2.y2_pst == b3.x_sp)) &&
+          (int64_t)b3.Cout * b3.wp_rstride < ((int64_t)1 << 31) &&
+          b3.M < ((int64_t)1 << 31)))
+        return false;
+    return pair_geom(b1, 1, &b3).lds > 0;
+}
+
 bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2,
-                      hipStream_t st) {
+                      hipStream_t st, const ConvArgs* b3) {
     const int wm = b1.Cout / 16;
-    const PairKern kern = pair_kernel(wm, b2.res != nullptr);
+    const PairKern kern = pair_kernel(wm, b2.res != nullptr, b3 != nullptr);
     if (!kern) {
         set_error("launch_conv_pair", "unsupported channel count");
         return false;
@@ -606,7 +800,7 @@ bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2,
     int bestR = 1;
     int64_t best = -1;
     for (int R = 1; R <= b1.OH; ++R) {
-        const PairGeom g = pair_geom(b1, R);
+        const PairGeom g = pair_geom(b1, R, b3);
         if (g.lds == 0) break;
         const int res = resident_blocks((const void*)kern, CP_NT, g.lds);
         const int64_t rounds = ceil_div(g.nbands, (int64_t)res * cus);
@@ -620,13 +814,16 @@ bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2,
             bestR = R;
         }
     }
-    const PairGeom g = pair_geom(b1, bestR);
+    PairGeom g = pair_geom(b1, bestR, b3);
+    // which of the pair's outputs is the Concat's slice
+    if (b3)
+        g.t_y2 = (const int8_t*)b2.y == (const int8_t*)b3->x + g.off_d ? 0 : 1;
     if (g.lds == 0 || g.nbands >= ((int64_t)1 << 31)) {
         set_error("launch_conv_pair", "band does not fit");
         return false;
     }
     hipLaunchKernelGGL(kern, dim3((unsigned)g.nbands), dim3(CP_NT),
-                       (size_t)g.lds, st, b1, b2, g);
+                       (size_t)g.lds, st, b1, b2, g, b3 ? *b3 : b2);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("launch_conv_pair", e);

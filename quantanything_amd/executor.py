@@ -448,6 +448,7 @@ class DeviceExecutor:
         # table Softmax output -> (launch name, input, table, out qp, so)
         self.softmax_lut = {}
         self.gap_info = {}  # pool launch -> layer, input, output, parameters
+        self.pair_descs = {}  # fused pair launch -> (first, second desc)
         self.tunables = []  # (launch name, desc, tile codes, fn(stream))
         self.f64_descs = []  # (desc, None, None, launch name), FP64 path
         self.outputs_f32 = {}
@@ -627,6 +628,7 @@ class DeviceExecutor:
         self._fuse_input_quantization(cons)
         self._fuse_pools(cons)
         self._fuse_pairs(cons)
+        self._fuse_pair_tails(cons)
         self._fuse_chains(cons)
         if self.fuse_attention:
             self._fuse_attention(cons)
@@ -999,7 +1001,56 @@ class DeviceExecutor:
             self.launches = [(fused, fn) if n == ln2 else (n, f)
                              for n, f in self.launches if n != ln1]
             self.tunables.append((fused, d2, [0], fn))
+            self.pair_descs[fused] = (d1, d2)
             self.tensors.pop(mids[0], None)  # never materialized
+
+    def _fuse_pair_tails(self, cons):
+        """A C2f block's last 1x1 convolution (cv2) whose input, the block's
+        Concat, ends with the last bottleneck pair's output runs inside that
+        pair's launch (``qa_d_conv_pair_tail``). The fused launch takes
+        cv2's place, after every launch that writes the Concat's other
+        channels, so the pair's outputs and the Concat may have no reader
+        but the Concat and cv2 respectively."""
+        g = self.graph
+        layer_of = {l.name: l for l in self.c.layers}
+        made_by = {o: l for l in self.c.layers for o in l.node.outputs}
+        for fused, (d1, d2) in list(self.pair_descs.items()):
+            live = dict(self.launches)
+            if fused not in live:
+                continue
+            for d3, _, _, ln3 in self.mfma_descs:
+                if ln3 not in live or d3.KH != 1 or d3.KW != 1 or \
+                        not self.lib.qa_conv_pair_tail_supported(
+                            ctypes.byref(d1), ctypes.byref(d2),
+                            ctypes.byref(d3)):
+                    continue
+                cv2 = layer_of.get(ln3[5:])
+                if cv2 is None:
+                    continue
+                cname = cv2.data_inputs[0]
+                cat = made_by.get(cname)
+                if cat is None or cname in g.outputs or \
+                        [l.name for l in cons.get(cname, [])] != [cv2.name]:
+                    continue
+                outs = [n for n, t in self.tensors.items()
+                        if t.ptr in (d2.y, d2.y2) and n != cname]
+                if not outs or any(
+                        n in g.outputs or
+                        {l.name for l in cons.get(n, [])} != {cat.name}
+                        for n in outs):
+                    continue
+                tname = f"pairtail:{fused[5:]}+{cv2.name}"
+
+                def fn(s, d1=d1, d2=d2, d3=d3):
+                    _ok(self.lib.qa_d_conv_pair_tail(
+                        ctypes.byref(d1), ctypes.byref(d2), ctypes.byref(d3),
+                        s), "qa_d_conv_pair_tail")
+
+                self.launches = [(tname, fn) if n == ln3 else (n, f)
+                                 for n, f in self.launches if n != fused]
+                self.tunables = [t for t in self.tunables if t[0] != fused]
+                self.tunables.append((tname, d2, [0], fn))
+                break
 
     def _fuse_chains(self, cons):
         """An int8 convolution of 16, 32 or 64 output channels whose output

@@ -68,6 +68,8 @@ def _declare(lib):
         "qa_d_quantize_conv": (i32, [p, p, f64, i64, i64, i64, p]),
         "qa_d_conv_pool": (i32, [p, p, p]),
         "qa_conv_pair_supported": (i32, [p, p]),
+        "qa_conv_pair_tail_supported": (i32, [p, p, p]),
+        "qa_d_conv_pair_tail": (i32, [p, p, p, p]),
         "qa_d_conv_pair": (i32, [p, p, p]),
         "qa_conv_chain_supported": (i32, [p, p]),
         "qa_d_conv_chain": (i32, [p, p, p]),

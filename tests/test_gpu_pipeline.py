@@ -92,9 +92,11 @@ def test_every_conv_tile_is_bit_exact(hip, tmp_path, model, quant_type):
         not any(n.startswith("gap:") for n, _ in ex.launches), \
         "pool not fused into the last convolution"
     descs = [t[1] for t in ex.tunables]
-    # a fused pair of convolutions is one tunable launch
-    pairs = sum(n.startswith(("pair:", "chain:")) for n, _ in ex.launches)
-    assert len(descs) == len(ex.mfma_descs) - pairs
+    # fused convolutions (a pair, a chain, a pair with its block's 1x1
+    # tail: names joined by "+") are one tunable launch
+    fused = sum(n.count("+") for n, _ in ex.launches
+                if n.startswith(("pair:", "chain:", "pairtail:")))
+    assert len(descs) == len(ex.mfma_descs) - fused
     cands = [t[2] for t in ex.tunables]
     for r in range(max(len(cc) for cc in cands)):
         for d, cc in zip(descs, cands):
