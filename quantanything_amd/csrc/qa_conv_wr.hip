@@ -57,6 +57,7 @@ struct WrGeom {
     int RSW;              // LDS row stride of the staged weights
     int lds;              // dynamic LDS bytes (0: does not fit)
     int KSR;              // K-steps the kernel runs (>= KGp / 4, zero-padded)
+    int ost;              // output staged through a per-wave LDS tile
     // ceil(2^32 / d) for d = band columns, KGp, OW, W (all >= 2) and the
     // 16-byte chunks of a pixel (used when >= 2):
     // floor(n / d) = (n * m) >> 32 for the n < 2^16 used here
@@ -430,6 +431,49 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
                 }
             }
         };
+        // ost (no residual or chained conv; 16-byte aligned outputs, Cout
+        // a multiple of 16): the tile's stored bytes go to the wave's LDS
+        // tile (16 pixels x OS bytes; byte writes at immediate offsets,
+        // no packing or lane exchange), then each lane stores 16 channels
+        // of one pixel: pixel lp of the tile, channels co0 + 16 lc ..
+        constexpr int OS = 16 * WM + 16;
+        int8_t* const s_ow = s_t + wave * (16 * OS);
+        const int lp = lane / WM, lc = lane % WM;
+        const bool lact = lane < 16 * WM && co0 + 16 * lc < a.Cout;
+        const int ypst = (int)a.y_pst, y2pst = (int)a.y2_pst;
+        int8_t* const yb = (int8_t*)a.y + pimg * a.y_pst + co0 + 16 * lc;
+        int8_t* const y2b =
+            a.y2 ? (int8_t*)a.y2 + pimg * a.y2_pst + co0 + 16 * lc : nullptr;
+        auto epi_store_staged = [&](int t, const int (&e4)[WM][4]) {
+            const int pq = 16 * t + lp;
+            const bool sok = lact && pq < npix;
+            int8_t* const wbyte = s_ow + 4 * kgl * OS + col;
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    wbyte[rr * OS + 16 * i] = (int8_t)e4[i][rr];
+            // the wave's byte writes before its reads of them by other
+            // lanes (LDS instructions of a wave complete in order; the
+            // wait also keeps the compiler from moving them)
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            const v4i v = *(const v4i*)(s_ow + lp * OS + 16 * lc);
+            __builtin_amdgcn_wave_barrier();
+            if (sok) *(v4i*)(yb + pq * ypst) = v;
+            if (a.y2) {  // the rescaled copy: the entries' second bytes
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                        wbyte[rr * OS + 16 * i] = (int8_t)(e4[i][rr] >> 8);
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                __builtin_amdgcn_wave_barrier();
+                const v4i v2 = *(const v4i*)(s_ow + lp * OS + 16 * lc);
+                __builtin_amdgcn_wave_barrier();
+                if (sok) *(v4i*)(y2b + pq * y2pst) = v2;
+            }
+        };
         // phase 0: the tiles whose input rows are all among the band rows
         // of the first h rounds (the rows above the image count as staged)
         int T0 = ntile;
@@ -466,7 +510,10 @@ __global__ __launch_bounds__(WR_NT) void k_conv_wr(ConvArgs a, WrGeom bg,
             {
                 int e4[WM][4];
                 epi_math(acc, rw, e4);
-                epi_store(t, e4, true);
+                if (!CH && !RES && bg.ost)
+                    epi_store_staged(t, e4);
+                else
+                    epi_store(t, e4, true);
             }
             if (CH) {
                 // the wave's own LDS writes above, read back by other lanes
@@ -536,9 +583,20 @@ WrGeom wr_geom(const ConvArgs& b, int wm, int R, bool ch = false) {
     g.m_ow = magic(b.OW);
     g.m_w = magic(b.W);
     g.m_cpp = magic(b.Cg >> 4);
-    const int64_t bytes =
+    int64_t bytes =
         band + (int64_t)wm * 16 * g.RSW + (int64_t)g.KSR * 16 +
         (ch ? (int64_t)wm * 16 * 80 + WR_NW * 16 * 80 : 0);
+    // the output staged through LDS (16-byte stores of whole 16-channel
+    // blocks, never the pixel's padding channels) when it fits
+    const int64_t otile = (int64_t)WR_NW * 16 * (16 * wm + 16);
+    g.ost = !ch && b.res == nullptr && b.Cout % 16 == 0 &&
+            (uintptr_t)b.y % 16 == 0 && b.y_pst % 16 == 0 &&
+            (b.y2 == nullptr ||
+             ((uintptr_t)b.y2 % 16 == 0 && b.y2_pst % 16 == 0)) &&
+            (int64_t)R * b.OW * std::max(b.y_pst, b.y2_pst) <
+                ((int64_t)1 << 31) &&
+            bytes + otile <= 150 * 1024;
+    if (g.ost) bytes += otile;
     // gfx950 gives a work-group up to 160 KB of LDS
     g.lds = bytes <= 150 * 1024 && bchunks <= (int64_t)WR_SB * WR_NT &&
                     wchunks <= (int64_t)WR_SW * WR_NT &&
