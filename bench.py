@@ -365,6 +365,16 @@ def main():
     for name, fn in ex.launches:
         per.append((time_launch(fn, 20, torch), name, fn))
     layers = {l.name: l for l in c.layers}
+    # a conv's fused residual Add reads, and its Concat copy writes, one
+    # more output-sized tensor
+    descs = {ln[5:]: d for d, _, _, ln in ex.mfma_descs}
+
+    def fused_io(lname, out_shape):
+        d = descs.get(lname)
+        if d is None:
+            return 0
+        return int(np.prod(out_shape)) * ((1 if d.res else 0) +
+                                          (1 if d.y2 else 0))
 
     def conv_out_shape(layer, xs):
         n, _, h, w = xs
@@ -393,7 +403,7 @@ def main():
             ob, bb = layer_work(lb, mid)
             ot, bt = layer_work(lt, shapes[lt.data_inputs[0]])
             return (lt, oa + ob + ot,
-                    ba + bb + bt - 3 * int(np.prod(mid)))
+                    ba + bb + bt - 3 * int(np.prod(mid)) + fused_io(b, mid))
         if kind in ("pair", "chain"):
             a, _, b = lname.partition("+")
             if a not in layers or b not in layers:
@@ -403,7 +413,8 @@ def main():
             mid = conv_out_shape(la, xs)
             oa, ba = layer_work(la, xs)
             ob, bb = layer_work(lb, mid)
-            return lb, oa + ob, ba + bb - 2 * int(np.prod(mid))
+            return lb, oa + ob, (ba + bb - 2 * int(np.prod(mid)) +
+                                 fused_io(b, conv_out_shape(lb, mid)))
         if kind not in ("conv", "qconv", "convpool") or lname not in layers:
             return None
         layer = layers[lname]
@@ -412,6 +423,8 @@ def main():
         if kind == "convpool":  # the pooled output replaces the conv output
             cout = layer.w_centered.shape[0]
             byts -= ops // (2 * layer.w_centered[0].size) - xs[0] * cout
+        elif layer.kind == "conv":
+            byts += fused_io(lname, conv_out_shape(layer, xs))
         return layer, ops, byts
 
     in_order = []

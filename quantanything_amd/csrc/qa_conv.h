@@ -180,7 +180,9 @@ bool launch_conv_valu(const ConvArgs& a, hipStream_t st);
 // epilogue on 128 x 128 blocks (qa_gemm_big.hip); `epi` as chosen by
 // launch_conv_mfma.
 bool gemm_big_applies(const ConvArgs& b, int epi);
-bool launch_gemm_big(const ConvArgs& b, hipStream_t st);
+// stages 3 or 4: the K loop through that many LDS stages filled by direct
+// loads; otherwise the register-staged two-buffer loop
+bool launch_gemm_big(const ConvArgs& b, hipStream_t st, int stages = 0);
 // int8 convolutions over bands of output rows with the input band and the
 // weights in LDS (qa_conv_band.hip); wm = 16-channel groups per work-group.
 bool conv_band_applies(const ConvArgs& b, int epi, int wm);

@@ -83,11 +83,16 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
         for (int ww = a.Cog >= 64 ? 4 : a.Cog >= 32 ? 2 : 1; ww >= 1; ww >>= 1)
             if (conv_wr_applies(b, epi, ww)) return launch_conv_wr(b, ww, st);
     }
-    // large GEMMs: 128 x 128 blocks (tile hint bit 10 chooses)
+    // large GEMMs: 128 x 128 blocks (tile hint bit 10 chooses; its low
+    // bits 3 or 4 the direct-to-LDS pipeline with that many stages)
     if (gemm_big_applies(b, epi)) {
         bool big = a.M >= 1024 && a.Cout >= 128;
-        if (a.tile_hint & TILE_VALID) big = (a.tile_hint >> 10) & 1;
-        if (big) return launch_gemm_big(b, st);
+        int stages = 0;
+        if (a.tile_hint & TILE_VALID) {
+            big = (a.tile_hint >> 10) & 1;
+            stages = a.tile_hint & 0xff;
+        }
+        if (big) return launch_gemm_big(b, st, stages);
     }
     const int64_t ntiles = ceil_div(a.M, 16);
     const int64_t simds = 4 * (int64_t)cu_count();

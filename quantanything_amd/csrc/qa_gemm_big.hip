@@ -8,7 +8,9 @@
 // MFMA tiles of v_mfma_i32_16x16x64_i8, so every A fragment feeds 4 MFMAs
 // and every B fragment 4. K runs in 64- or 128-byte steps through two LDS
 // buffers (global -> registers for the next step while a step's MFMAs run,
-// one barrier a step). The epilogue is the int8 table plan of qa_conv.h
+// one barrier a step), or (S > 0) in 64-byte steps through S LDS stages
+// filled straight from global memory (global_load_lds_dwordx4: no
+// registers hold loads in flight, so S - 1 steps are requested ahead). The epilogue is the int8 table plan of qa_conv.h
 // (per-channel multiply-add and shift, 256-entry clip / activation /
 // residual / copy tables), identical in results to the convolution
 // kernel's; residual, copy and pixel sums are template flags, full tiles
@@ -34,16 +36,38 @@ constexpr int GB_M = 128, GB_N = 128;
 // load is issued before the first MFMA).
 // RES / Y2 / RS: residual Add, rescaled second output, pixel sums of the
 // activations (weights with an offset) in the epilogue.
-template <int P, int BK, bool RES, bool Y2, bool RS>
+// S > 0 (BK 64, P unused): stage s holds A (128 rows x 64 bytes) and B
+// (128 x 64) at dynamic LDS bytes 16384 s and 16384 s + 8192; row r's
+// 16-byte chunk c sits at position c ^ ((r >> 1) & 3) of the row, so that
+// the 8 rows one fragment read serves at a time fall in distinct banks
+// without padding (a 64-lane direct load fills 1 KB contiguously: 16 rows
+// of 4 positions, lane l at row l / 4, position l % 4).
+constexpr int GB_STAGE = 16384;
+
+// vmcnt(n) for n a multiple of 4 up to 12 (expcnt and lgkmcnt not waited)
+__device__ __forceinline__ void wait_vm(int n) {
+    switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+        case 4: __builtin_amdgcn_s_waitcnt(0x0f74); break;
+        case 8: __builtin_amdgcn_s_waitcnt(0x0f78); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0f7c); break;
+    }
+}
+template <int P, int BK, bool RES, bool Y2, bool RS, int S>
 __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
+    static_assert(S == 0 || (BK == 64 && S >= 2 && S <= 5), "stages");
     constexpr int GB_K = BK;
     constexpr int GB_RS = BK + 16;  // LDS row stride (bytes)
     constexpr int CPR = BK / 16;    // 16-byte chunks per row
     constexpr int CH = GB_M * CPR / 256;  // chunks per thread and operand
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][GB_M * GB_RS];
-    __shared__ __attribute__((aligned(16))) int8_t sB[2][GB_N * GB_RS];
+    // the two register-path buffers (S > 0: the dynamic stages instead)
+    constexpr int SAB = S > 0 ? 16 : GB_M * GB_RS;
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][SAB];
+    __shared__ __attribute__((aligned(16))) int8_t sB[2][SAB];
+    extern __shared__ int4 gb_dyn[];
     __shared__ int s_tab[768];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int col = lane & 15, kg = lane >> 4;
     // tile of this work-group: consecutive work-groups go to different
@@ -72,7 +96,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
     constexpr int RSTEP = 256 / CPR;  // rows between a thread's chunks
     const int lr = tid / CPR, lk = (tid % CPR) * 16;
     typedef int vch __attribute__((ext_vector_type(4 * CH)));
-    vch ra[P], rb[P];
+    vch ra[S > 0 ? 1 : P], rb[S > 0 ? 1 : P];
     auto gload = [&](vch& va, vch& vb, int ks) __attribute__((always_inline)) {
         const int o = min(ks, nk - 1) * GB_K + lk;
 #pragma unroll
@@ -103,13 +127,52 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
                 int4{vb[4 * j], vb[4 * j + 1], vb[4 * j + 2], vb[4 * j + 3]};
         }
     };
-    // every slot's loads first: they overlap the table set-up below
+    // S > 0: this lane's direct loads: rows 32 wave + lane / 4 (+ 16) of
+    // A and B, the global chunk stored at position lane % 4 of its row
+    int8_t* const stg = (int8_t*)gb_dyn;
+    const int lrow = 32 * wave + (lane >> 2);
+    const int gch = 16 * ((lane & 3) ^ ((lrow >> 1) & 3));
+    const int8_t* const ga0 =
+        xa + min(m0 + lrow, a.M - 1) * a.x_sn + gch;
+    const int8_t* const ga1 =
+        xa + min(m0 + lrow + 16, a.M - 1) * a.x_sn + gch;
+    const int8_t* const gb0 = a.wp + (int64_t)(n0 + lrow) * a.wp_rstride + gch;
+    const int8_t* const gb1 = gb0 + 16 * a.wp_rstride;
+    // step ks of 64 bytes into stage ks % S (4 direct loads a lane)
+    auto dload = [&](int ks) __attribute__((always_inline)) {
+        int8_t* const sb = stg + (ks % S) * GB_STAGE + 32 * 64 * wave;
+        const int ko = ks * 64;
+        __builtin_amdgcn_global_load_lds(ga0 + ko, sb, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(ga1 + ko, sb + 16 * 64, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(gb0 + ko, sb + 8192, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(gb1 + ko, sb + 8192 + 16 * 64, 16,
+                                         0, 0);
+    };
+    // the plan's tables (768 entries, 3 a thread) requested before the
+    // operands, so that storing them waits for them alone (loads complete
+    // in issue order)
+    int tv[3];
 #pragma unroll
-    for (int sl = 0; sl < P; ++sl) gload(ra[sl], rb[sl], sl);
+    for (int j = 0; j < 3; ++j)
+        tv[j] = ((const int*)((const char*)a.plan + PLAN_E))[tid + 256 * j];
+    if constexpr (S > 0) {
+        // the first S - 1 steps in flight: they overlap the set-up below
+#pragma unroll
+        for (int sl = 0; sl < S - 1; ++sl)
+            if (sl < nk) dload(sl);
+    } else {
+        // every slot's loads first: they overlap the table set-up below
+#pragma unroll
+        for (int sl = 0; sl < P; ++sl) gload(ra[sl], rb[sl], sl);
+    }
 
-    // tables of the plan and the lane's 4 channels' constants
-    for (int i = tid; i < 768; i += 256)
-        s_tab[i] = ((const int*)((const char*)a.plan + PLAN_E))[i];
+    // tables of the plan (S > 0: stored after the K loop, since an LDS
+    // store here would wait for the direct loads in flight) and the lane's
+    // 4 channels' constants
+    if constexpr (S == 0) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) s_tab[tid + 256 * j] = tv[j];
+    }
     const int4 hdr = *(const int4*)a.plan;
     // the lane's 4 channels' constants, the zero-point correction folded
     // into the plan constant (plan_q0; K <= 16384 keeps |w| + |corr| +
@@ -160,6 +223,50 @@ __global__ __launch_bounds__(256) void k_gemm_big(ConvArgs a) {
             }
         }
     };
+    // S > 0: a lane's fragment of rows 16 i + col, chunk kg, at position
+    // kg ^ ((col >> 1) & 3) of the row (the tile's row bases are multiples
+    // of 16)
+    const int foff = col * 64 + 16 * (kg ^ ((col >> 1) & 3));
+    auto mfma_stage = [&](const int8_t* sb) __attribute__((always_inline)) {
+        v4i fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            fa[i] = *(const v4i*)(sb + (64 * wm + 16 * i) * 64 + foff);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            fb[j] = *(const v4i*)(sb + 8192 + (64 * wn + 16 * j) * 64 + foff);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    fa[i], fb[j], acc[i][j], 0, 0, 0);
+        if (RS) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) psum[i] += bytes_sum(fa[i], 16);
+        }
+    };
+    if constexpr (S > 0) {
+        // step ks: this wave's loads of it done (those of the next
+        // min(S - 2, nk - 1 - ks) steps may still be in flight), barrier
+        // (every wave's part landed, and every wave is past step ks - 1,
+        // whose stage the refill below overwrites), request step
+        // ks + S - 1, MFMAs
+        for (int ks = 0; ks < nk; ++ks) {
+            wait_vm(4 * min(S - 2, nk - 1 - ks));
+            // a bare barrier: the explicit wait above is the only one the
+            // direct loads need (a fenced barrier would wait for all of
+            // them); the empty asm keeps LDS accesses on their side of it
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (ks + S - 1 < nk) dload(ks + S - 1);
+            mfma_stage(stg + (ks % S) * GB_STAGE);
+        }
+#pragma unroll
+        for (int j = 0; j < 3; ++j) s_tab[tid + 256 * j] = tv[j];
+        __syncthreads();
+    } else
     // step ks from slot sl: to LDS buffer ks & 1 (last read two steps ago,
     // before the previous step's barrier), refill the slot with step
     // ks + P, barrier, MFMAs
@@ -294,7 +401,7 @@ bool gemm_big_applies(const ConvArgs& b, int epi) {
            xa % 16 == 0 && b.y_code == 1 && b.M < ((int64_t)1 << 31);
 }
 
-bool launch_gemm_big(const ConvArgs& b, hipStream_t st) {
+bool launch_gemm_big(const ConvArgs& b, hipStream_t st, int stages) {
     const int64_t tiles = ceil_div(b.M, GB_M) * ceil_div(b.Cout, GB_N);
     if (tiles >= ((int64_t)1 << 31)) {
         set_error("launch_gemm_big", "grid too large");
@@ -303,13 +410,15 @@ bool launch_gemm_big(const ConvArgs& b, hipStream_t st) {
     const int K = b.KGp * 16;
     const dim3 grid((unsigned)tiles);
     const int flags = (b.res ? 1 : 0) | (b.y2 ? 2 : 0) | (b.rowsum ? 4 : 0);
-    auto go = [&](auto kp, auto kbk) {
+    auto go = [&](auto kp, auto kbk, auto ks) {
         constexpr int KP = decltype(kp)::value, KBK = decltype(kbk)::value;
+        constexpr int KS = decltype(ks)::value;
+        const size_t lds = (size_t)KS * GB_STAGE;
         switch (flags) {
 #define QA_GB_CASE(F)                                                    \
     case F:                                                              \
-        k_gemm_big<KP, KBK, (F & 1) != 0, (F & 2) != 0, (F & 4) != 0>     \
-            <<<grid, 256, 0, st>>>(b);                                   \
+        k_gemm_big<KP, KBK, (F & 1) != 0, (F & 2) != 0, (F & 4) != 0, KS> \
+            <<<grid, 256, lds, st>>>(b);                                 \
         break;
             QA_GB_CASE(0) QA_GB_CASE(1) QA_GB_CASE(2) QA_GB_CASE(3)
             QA_GB_CASE(4) QA_GB_CASE(5) QA_GB_CASE(6) QA_GB_CASE(7)
@@ -319,11 +428,18 @@ bool launch_gemm_big(const ConvArgs& b, hipStream_t st) {
     // 128-byte steps when K allows, else 64-byte steps, the next step's
     // loads in flight (measured on the ViT-S GEMMs: deeper rings, which
     // cost VGPRs and so occupancy, were not faster in the pass)
+    // or (stages 3 / 4) the direct-to-LDS pipeline of 64-byte steps
     using I1 = std::integral_constant<int, 1>;
-    if (K % 128 == 0)
-        go(I1{}, std::integral_constant<int, 128>{});
+    using I0 = std::integral_constant<int, 0>;
+    using B64 = std::integral_constant<int, 64>;
+    if (stages == 3)
+        go(I1{}, B64{}, std::integral_constant<int, 3>{});
+    else if (stages == 4)
+        go(I1{}, B64{}, std::integral_constant<int, 4>{});
+    else if (K % 128 == 0)
+        go(I1{}, std::integral_constant<int, 128>{}, I0{});
     else
-        go(I1{}, std::integral_constant<int, 64>{});
+        go(I1{}, B64{}, I0{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("launch_gemm_big", e);

@@ -1844,7 +1844,9 @@ class DeviceExecutor:
         out = [0]
         if d.H == d.W == d.KH == d.KW == 1 and d.G == 1 and \
                 d.w_layout == 0 and d.C % 64 == 0:
-            out.append(0x10400)  # the large-GEMM kernel (128 x 128 blocks)
+            # the large-GEMM kernel (128 x 128 blocks): K steps staged
+            # through registers, or through 3 / 4 LDS stages of direct loads
+            out += [0x10400, 0x10403, 0x10404]
         if d.w_layout == 0 and d.G == 1 and d.C % 16 == 0 and \
                 d.OW <= 256 and d.epi_plan and (d.H > 1 or d.W > 1):
             # bands of output rows, operands in LDS (the library checks the
