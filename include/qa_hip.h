@@ -153,6 +153,19 @@ int qa_pack_weights_f64(const int32_t* w, int64_t Cout, int64_t Cg,
                         int64_t KH, int64_t KW, int64_t G, int64_t elem_bytes,
                         void* wp);
 
+/* Splits centred OIHW weights (w - w_zp, each in int16) for the byte-split
+ * path of 16-bit models (int8 matrix cores): plane 0 the high bytes w >> 8,
+ * plane 1 the low bytes (w & 255) - 128, each in the layout-0 form of
+ * qa_pack_weights_i8 (qa_pack_weights_i8_size with layout 0 gives one
+ * plane's bytes, kgp and rows; wp holds both planes, plane 1 right after
+ * plane 0; positions without a weight hold w = 0), and wsum[co] the sum of
+ * output channel co's weights. No counterpart in the reference: its 16-bit
+ * convolution is qa_conv_i32_i32_i64 (qa_kernels.cpp:281-284). Returns 0,
+ * 1 when a weight is outside int16, -1 on bad arguments. */
+int qa_pack_weights_i16s(const int32_t* w, int64_t Cout, int64_t Cg,
+                         int64_t KH, int64_t KW, int64_t G, int8_t* wp,
+                         int64_t* wsum);
+
 /* Fused integer convolution / GEMM on device tensors:
  *   acc = sum (x_stored + x_add) * w         (exact)
  *   q   = clip(mbqm(acc + pre_bias[c], mult[c], shift[c]) + zp)
@@ -202,7 +215,9 @@ typedef struct qa_conv_desc {
                       work-group split K, lds = weights staged in LDS (a
                       caller's measured choice; ignored where it does not
                       apply); 0x10400: GEMM descriptors (H = W = 1, C a
-                      multiple of 64) on 128 x 128 blocks; 0x10800 | wm
+                      multiple of 64) on 128 x 128 blocks (0x10403 /
+                      0x10404: K through 3 / 4 LDS stages filled by direct
+                      loads); 0x10800 | wm
                       (wm 1, 2, 4): bands of output rows with the input band
                       and the weights in LDS (layout 0, one group, a table
                       plan); 0x11000 | wm (wm 1, 2, 4): the weights held in
@@ -213,7 +228,19 @@ typedef struct qa_conv_desc {
                       8): 0x10000 | wm | tm << 4
                       | split << 8 with (wm, tm, split) one of (1,1,0),
                       (2,1,0), (1,4,0), (1,1,1), (2,1,1), (4,1,1); tm =
-                      16-pixel tiles per wave. Results do not depend on it. */
+                      16-pixel tiles per wave; with wsplit, 0x11000 | wm |
+                      tm << 4 ((wm, tm) in {1, 2, 4} x {1, 2}) runs the
+                      byte-split form. Results do not depend on it. */
+    const void* wsplit;        /* w_code 8 only, optional: the same weights
+                                  from qa_pack_weights_i16s (both planes);
+                                  the int16 input then runs on the int8
+                                  matrix cores when it fits (C / G a
+                                  multiple of 16, 16-byte aligned pixels,
+                                  |x_add| <= 32767): x = 256 xh + xl + 128
+                                  and w split alike, four int8 products and
+                                  the pixel sums, exact in int64 */
+    const int64_t* wsplit_k;   /* with wsplit: per output channel
+                                  (128 + x_add) * wsum[co] */
 } qa_conv_desc;
 
 /* Host-side planner of the int8 table epilogue of qa_d_conv. From the

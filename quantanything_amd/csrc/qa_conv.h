@@ -73,6 +73,11 @@ struct ConvArgs {
     const void* wf;                 // [G][wf_rows][KH*KW][CK] int16 / int32
     int32_t CK, wf_rows;            // Cg rounded up to 32, Cog to 64
     int32_t wf_bytes;               // element size, 2 or 4
+    // ---- the same weights split into two int8 planes (byte-split path,
+    // qa_pack_weights_i16s): high bytes, then low bytes - 128, each in the
+    // layout-0 form (CB, KG, KGp, wp_rstride, wp_gstride, mg_cb, mg_kw)
+    const int8_t* ws;               // NULL: FP64 path only
+    const int64_t* ws_k;            // per channel: (128 + x_add) * sum w
     // ---- per output channel ----
     const int64_t* corr;
     const int32_t* boff;

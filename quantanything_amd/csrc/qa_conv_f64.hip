@@ -280,6 +280,170 @@ __global__ __launch_bounds__(256) void k_conv_f64(ConvArgs a) {
     }
 }
 
+// ---- the byte-split form: 16-bit convolution on the int8 matrix cores --
+//
+// A stored activation x (int16) is 256 xh + xl + 128 with xh = x >> 8 and
+// xl = (x & 255) - 128, both int8, and a centred weight w = 256 wh + wl +
+// 128 likewise (qa_pack_weights_i16s: planes of wh and wl, w = 0 where no
+// weight sits). Over the K' positions one output sums (the 16 KGp bytes of
+// a packed row; positions without a weight have w = 0, so whatever x they
+// hold cancels):
+//   sum (x + x_add) w = 65536 Hh + 256 (Hl + Lh) + Ll + 128 U
+//                       + (128 + x_add) W
+// with Hh = sum xh wh, Hl = sum xh wl, Lh = sum xl wh, Ll = sum xl wl (int8
+// MFMA sums: |Hh| <= 2^14 K', |Hl + Lh| <= 2^15 K', exact in int32 for K' <
+// 2^16), U = sum (256 xh + xl) (two MFMAs against all-ones columns, which
+// leave each pixel's sum in the accumulator layout) and W = sum w (ws_k
+// holds (128 + x_add) W). Image padding positions hold the stored zero
+// point -x_add (x + x_add = 0). The exact int64 sum then takes the FP64
+// path's epilogue. A wave owns TM tiles of 16 pixels (rows) x WM 16-channel
+// blocks (columns); a lane's K-values of a step are the 16 channels of
+// k-group 4 s + lane / 16 (32 bytes of int16, split with v_perm), loaded
+// straight from memory with the next step's loads in flight.
+template <int WM, int TM>
+__global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kgl = lane >> 4;
+    const int g = blockIdx.z;
+    const int co0 = blockIdx.y * WM * 16;
+    const int64_t tile0 = ((int64_t)blockIdx.x * 4 + wave) * TM;
+    if (tile0 * 16 >= a.M) return;
+    const int nsteps = a.KGp >> 2;
+    const int16_t* xb[TM];
+    int iy0[TM], ix0[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        const int64_t p = min((tile0 + t) * 16 + col, a.M - 1);
+        const PixPos pos = pix_decode(a, p);
+        xb[t] = (const int16_t*)a.x + (int64_t)pos.n * a.x_sn +
+                (int64_t)g * a.Cg;
+        iy0[t] = pos.oy * a.SH - a.PH;
+        ix0[t] = pos.ox * a.SW - a.PW;
+    }
+    // the lane's weight row (channel co0 + 16 i + col) in the high plane;
+    // the low plane G groups further
+    const int8_t* wrow = a.ws + (int64_t)g * a.wp_gstride +
+                         (int64_t)(co0 + col) * a.wp_rstride + 16 * kgl;
+    const int64_t lo_off = (int64_t)a.G * a.wp_gstride;
+    const int64_t wblk = 16 * a.wp_rstride;
+    // the stored zero point's bytes, as four copies
+    const int pz = (int)(-a.x_add);
+    const int ph = (int)(((uint32_t)(pz >> 8) & 255u) * 0x01010101u);
+    const int pl = (int)((((uint32_t)pz & 255u) ^ 0x80u) * 0x01010101u);
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+
+    constexpr int D = 2;  // steps in flight
+    int4 xr[D][TM][2];
+    bool xin[D][TM];
+    v4i whr[D][WM], wlr[D][WM];
+    auto fetch = [&](int d, int s) {
+        s = min(s, nsteps - 1);  // steps past the end: in bounds, unused
+        const int kg = 4 * s + kgl;
+        const int tap = (int)(((uint64_t)kg * a.mg_cb) >> 32);
+        const int cb = kg - tap * a.CB;
+        const int ky = (int)(((uint64_t)tap * a.mg_kw) >> 32);
+        const int kx = tap - ky * a.KW;
+        const bool kok = kg < a.KG;
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            const int iy = iy0[t] + ky * a.DH, ix = ix0[t] + kx * a.DW;
+            const bool in = kok && (unsigned)iy < (unsigned)a.H &&
+                            (unsigned)ix < (unsigned)a.W;
+            // outside: the image's first pixel (in bounds, not used)
+            const int64_t off =
+                in ? ((int64_t)iy * a.W + ix) * a.x_sp + 16 * cb : 0;
+            xr[d][t][0] = *(const int4*)(xb[t] + off);
+            xr[d][t][1] = *(const int4*)(xb[t] + off + 8);
+            xin[d][t] = in;
+        }
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int8_t* wp = wrow + i * wblk + 64 * s;
+            whr[d][i] = *(const v4i*)wp;
+            wlr[d][i] = *(const v4i*)(wp + lo_off);
+        }
+    };
+    v4i hh[TM][WM], md[TM][WM], ll[TM][WM], sh[TM], sl[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        sh[t] = sl[t] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+            hh[t][i] = md[t][i] = ll[t][i] = v4i{0, 0, 0, 0};
+    }
+    auto compute = [&](int d) {
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            // int16 channels 2j (low half) and 2j + 1 of dword j: the high
+            // bytes are bytes 1 and 3 of each dword, the low bytes 0 and 2
+            const int4 u = xr[d][t][0], w = xr[d][t][1];
+            v4i xh = {(int)__builtin_amdgcn_perm(u.y, u.x, 0x07050301u),
+                      (int)__builtin_amdgcn_perm(u.w, u.z, 0x07050301u),
+                      (int)__builtin_amdgcn_perm(w.y, w.x, 0x07050301u),
+                      (int)__builtin_amdgcn_perm(w.w, w.z, 0x07050301u)};
+            v4i xl = {(int)__builtin_amdgcn_perm(u.y, u.x, 0x06040200u),
+                      (int)__builtin_amdgcn_perm(u.w, u.z, 0x06040200u),
+                      (int)__builtin_amdgcn_perm(w.y, w.x, 0x06040200u),
+                      (int)__builtin_amdgcn_perm(w.w, w.z, 0x06040200u)};
+            xl ^= (int)0x80808080u;
+            if (!xin[d][t]) {
+                xh = v4i{ph, ph, ph, ph};
+                xl = v4i{pl, pl, pl, pl};
+            }
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                hh[t][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    xh, whr[d][i], hh[t][i], 0, 0, 0);
+                md[t][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    xh, wlr[d][i], md[t][i], 0, 0, 0);
+                md[t][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    xl, whr[d][i], md[t][i], 0, 0, 0);
+                ll[t][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    xl, wlr[d][i], ll[t][i], 0, 0, 0);
+            }
+            sh[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xh, ones, sh[t], 0,
+                                                          0, 0);
+            sl[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xl, ones, sl[t], 0,
+                                                          0, 0);
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) fetch(d, d);
+    for (int n0 = 0; n0 < nsteps; n0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (n0 + d < nsteps) compute(d);
+            fetch(d, n0 + d + D);
+        }
+    }
+    // result register r of lane (col, kgl): pixel 4 kgl + r of the tile,
+    // channel col of the block
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+        const int c = co0 + i * 16 + col;
+        if (c >= a.Cog) continue;
+        const int64_t co = (int64_t)g * a.Cog + c;
+        const bool q = a.mode == EPI_QUANT;
+        const int64_t pre = a.pre ? a.pre[co] : 0;
+        const int64_t m = q ? a.mult[co] : 0;
+        const int64_t sft = q ? a.shift[co] : 0;
+        const int64_t kc = a.ws_k[co];
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t pp = (tile0 + t) * 16 + 4 * kgl + r;
+                if (pp >= a.M) continue;
+                const int64_t u = (int64_t)sh[t][r] * 256 + sl[t][r];
+                const int64_t v = (int64_t)hh[t][i][r] * 65536 +
+                                  (int64_t)md[t][i][r] * 256 + ll[t][i][r] +
+                                  u * 128 + kc;
+                f64_store(a, co, pp, v, pre, m, sft);
+            }
+    }
+}
+
 template <int WM, int TM, bool KS, class WE>
 void launch_v(const ConvArgs& a, int v, dim3 grid, hipStream_t st) {
     switch (v) {
@@ -355,6 +519,41 @@ bool launch_conv_f64(const ConvArgs& a, hipStream_t st) {
         b.y2_pst = pst(a.y2_sn, a.y2_sp);
     }
     const int64_t ntiles = ceil_div(a.M, 16);
+    // the byte-split form on the int8 matrix cores: when the split planes
+    // are given and the input fits it (16-byte aligned 16-channel groups,
+    // K' = 16 KGp < 2^16, the stored zero point an int16); tile code 0x1000
+    // | wm | tm << 4, by default the widest channel block, one tile a wave
+    if (a.ws && a.ws_k && a.Cg % 16 == 0 && a.x_sp % 8 == 0 &&
+        a.x_sn % 8 == 0 && xa % 16 == 0 && a.KGp > 0 && a.KGp < 4096 &&
+        a.x_add >= -32767 && a.x_add <= 32768) {
+        int code = 0x1010 | (a.Cog >= 64 ? 4 : a.Cog >= 32 ? 2 : 1);
+        if (a.tile_hint & TILE_VALID) code = a.tile_hint & 0xffff;
+        const int wm = code & 15, tm = (code >> 4) & 15;
+        if ((code & 0xff00) == 0x1000 && (wm == 1 || wm == 2 || wm == 4) &&
+            (tm == 1 || tm == 2)) {
+            const int64_t gx = ceil_div(ntiles, 4 * tm);
+            const int64_t gy = ceil_div(a.Cog, 16 * wm);
+            if (gx >= ((int64_t)1 << 31) || gy > 65535) {
+                set_error("launch_conv_f64", "grid too large");
+                return false;
+            }
+            const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)a.G);
+            switch (code) {
+                case 0x1011: k_conv_bs<1, 1><<<grid, 256, 0, st>>>(b); break;
+                case 0x1012: k_conv_bs<2, 1><<<grid, 256, 0, st>>>(b); break;
+                case 0x1014: k_conv_bs<4, 1><<<grid, 256, 0, st>>>(b); break;
+                case 0x1021: k_conv_bs<1, 2><<<grid, 256, 0, st>>>(b); break;
+                case 0x1022: k_conv_bs<2, 2><<<grid, 256, 0, st>>>(b); break;
+                default: k_conv_bs<4, 2><<<grid, 256, 0, st>>>(b); break;
+            }
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) {
+                set_hip_error("launch_conv_f64", e);
+                return false;
+            }
+            return true;
+        }
+    }
     auto waves = [&](const F64Tile& t) {
         return ceil_div(ntiles, t.tm) * ceil_div(a.Cog, 16 * t.wm) * a.G *
                (t.split ? 4 : 1);

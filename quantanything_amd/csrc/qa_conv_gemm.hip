@@ -575,6 +575,42 @@ QA_API int qa_pack_weights_f64(const int32_t* w, int64_t Cout, int64_t Cg,
     return 0;
 }
 
+QA_API int qa_pack_weights_i16s(const int32_t* w, int64_t Cout, int64_t Cg,
+                                int64_t KH, int64_t KW, int64_t G, int8_t* wp,
+                                int64_t* wsum) {
+    if (G <= 0 || Cout < 0 || Cout % G || Cg < 0 || KH < 0 || KW < 0 ||
+        !wp || !wsum || (!w && Cout * Cg * KH * KW > 0))
+        return -1;
+    int64_t CB, KG, KGp, rows;
+    pack_geometry(Cout, Cg, KH, KW, G, 0, &CB, &KG, &KGp, &rows);
+    const int64_t plane = G * rows * KGp * 16, K = Cg * KH * KW;
+    for (int64_t i = 0; i < Cout * K; ++i)
+        if (w[i] < -32768 || w[i] > 32767) return 1;
+    // w = 0 where no weight sits: high byte 0, low byte 0 - 128
+    memset(wp, 0, (size_t)plane);
+    memset(wp + plane, 0x80, (size_t)plane);
+    const int64_t Cog = Cout / G;
+    for (int64_t co = 0; co < Cout; ++co) {
+        const int32_t* row = w + co * K;
+        const int64_t g = co / Cog, r = co % Cog;
+        int8_t* hi = wp + (g * rows + r) * KGp * 16;
+        int8_t* lo = hi + plane;
+        int64_t sum = 0;
+        for (int64_t c = 0; c < Cg; ++c)
+            for (int64_t ky = 0; ky < KH; ++ky)
+                for (int64_t kx = 0; kx < KW; ++kx) {
+                    const int v = row[(c * KH + ky) * KW + kx];
+                    const int64_t at =
+                        ((ky * KW + kx) * CB + c / 16) * 16 + c % 16;
+                    hi[at] = (int8_t)(v >> 8);
+                    lo[at] = (int8_t)((v & 255) - 128);
+                    sum += v;
+                }
+        wsum[co] = sum;
+    }
+    return 0;
+}
+
 namespace {
 
 // Kernel arguments of a device descriptor: 1 for the int8 MFMA path, 0 for
@@ -691,6 +727,21 @@ int desc_args(const qa_conv_desc* d, ConvArgs& a, const char* who) {
         a.wf_rows = (int32_t)rows;
         a.wide = (int32_t)d->wide;
         a.tile_hint = (int32_t)d->tile;
+        if (d->wsplit && d->wsplit_k) {  // the byte-split planes
+            int64_t CB, KG, KGp, prow;
+            pack_geometry(d->Cout, d->C / d->G, d->KH, d->KW, d->G, 0, &CB,
+                          &KG, &KGp, &prow);
+            a.ws = (const int8_t*)d->wsplit;
+            a.ws_k = d->wsplit_k;
+            a.CB = (int32_t)CB;
+            a.KG = (int32_t)KG;
+            a.KGp = (int32_t)KGp;
+            a.wp_rstride = KGp * 16;
+            a.wp_gstride = prow * KGp * 16;
+            a.mg_cb = (((uint64_t)1 << 32) + CB - 1) / (uint64_t)CB;
+            a.mg_kw = (((uint64_t)1 << 32) + std::max<int64_t>(d->KW, 1) -
+                       1) / (uint64_t)std::max<int64_t>(d->KW, 1);
+        }
         return 3;
     }
     a.w = d->w;

@@ -63,7 +63,7 @@ class ConvDesc(ctypes.Structure):
                                              "r2_zp_in", "r2_m", "r2_s",
                                              "r2_zp_out", "r2_qmin",
                                              "r2_qmax")]
-        + [("tile", _I64)])
+        + [("tile", _I64), ("wsplit", _P), ("wsplit_k", _P)])
 
 
 def storage_of(bits, signed):
@@ -728,6 +728,20 @@ class DeviceExecutor:
                     info = dict(w=_dev(wf, dt), w_code=8, layout=wf.itemsize,
                                 kgp=ck.value, rows=rows.value, corr=None,
                                 boff=None, rowsum=0, wide=1)
+                    if dt == np.int16 and cg % 16 == 0:
+                        # the same weights as two int8 planes: the library
+                        # may run the byte-split form on the int8 cores
+                        kgp8, rows8 = _I64(0), _I64(0)
+                        n8 = self.lib.qa_pack_weights_i8_size(
+                            cout, cg, kh, kw, groups, 0, ctypes.byref(kgp8),
+                            ctypes.byref(rows8))
+                        ws = np.empty(2 * n8, np.int8)
+                        wsum = np.empty(cout, np.int64)
+                        if self.lib.qa_pack_weights_i16s(
+                                w32.ctypes.data, cout, cg, kh, kw, groups,
+                                ws.ctypes.data, wsum.ctypes.data) == 0:
+                            info["wsplit"] = _dev(ws, np.int8)
+                            info["wsum"] = wsum
                     break
         if info is None:  # exact VALU path, int64 accumulation
             info = dict(w=_dev(w32, np.int32), w_code=4, layout=0, kgp=0,
@@ -791,6 +805,11 @@ class DeviceExecutor:
         d.w_code, d.w_layout = info["w_code"], info["layout"]
         d.w_kgp, d.w_rows = info["kgp"], info["rows"]
         d.wide, d.needs_rowsum = info["wide"], info["rowsum"]
+        if info.get("wsplit") is not None:
+            kc = _dev((128 + int(d.x_add)) * info["wsum"], np.int64)
+            self.keep.append(kc)
+            d.wsplit = info["wsplit"].data_ptr()
+            d.wsplit_k = kc.data_ptr()
         d.corr = info["corr"].data_ptr() if info["corr"] is not None else None
         d.boff = info["boff"].data_ptr() if info["boff"] is not None else None
         d.pre_bias = info["pre"].data_ptr() if info["pre"] is not None \
@@ -1839,7 +1858,11 @@ class DeviceExecutor:
         cog = d.Cout // d.G
         if d.w_code == 8:  # FP64 path: wm | tm << 4 | split << 8
             wm_max = 1 if cog <= 16 else 2 if cog <= 32 else 4
-            return [0] + [0x10000 | c for c in F64_TILES if c & 15 <= wm_max]
+            out = [0] + [0x10000 | c for c in F64_TILES if c & 15 <= wm_max]
+            if d.wsplit:  # byte split: 0x1000 | wm | tm << 4
+                out += [0x11000 | wm | tm << 4 for tm in (1, 2)
+                        for wm in (1, 2, 4) if wm <= wm_max]
+            return out
         wm_max = 1 if cog <= 16 else 2 if cog <= 32 else 4 if cog <= 64 else 8
         out = [0]
         if d.H == d.W == d.KH == d.KW == 1 and d.G == 1 and \

@@ -64,6 +64,7 @@ def _declare(lib):
         "qa_pack_weights_i8": (i32, [p] + [i64] * 7 + [p, p, p, p]),
         "qa_pack_weights_f64_size": (i64, [i64] * 5 + [p, p]),
         "qa_pack_weights_f64": (i32, [p] + [i64] * 6 + [p]),
+        "qa_pack_weights_i16s": (i32, [p] + [i64] * 5 + [p, p]),
         "qa_d_conv": (i32, [p, p]),
         "qa_d_quantize_conv": (i32, [p, p, f64, i64, i64, i64, p]),
         "qa_d_conv_pool": (i32, [p, p, p]),
