@@ -123,26 +123,32 @@ constexpr int PLAN_CH = PLAN_TR + 1024; // int32x4 {m, t, c_lo, c_hi} per channe
 // A + i + D) the offset D = zp - y_so
 constexpr int PLAN_RES = 1, PLAN_Y2 = 2, PLAN_IDENT = 4;
 
+// The residual Add of a quantized value q and the residual's value res_q.
+__device__ __forceinline__ int64_t quant_add(const ConvArgs& a, int64_t q,
+                                             int64_t res_q) {
+    const int64_t first = a.res_first ? res_q : q;
+    const int64_t second = a.res_first ? q : res_q;
+    const qa_i128 t = qa_mbqm_fast(first - a.za, a.ma, a.sa) +
+                      (qa_i128)a.add_sign *
+                          qa_mbqm_fast(second - a.zb, a.mb, a.sb) +
+                      a.add_zp;
+    return qa_clip128(t, a.add_qmin, a.add_qmax);
+}
+
+// The table index of a requantized value.
+__device__ __forceinline__ int64_t lut_index(const ConvArgs& a, int64_t q) {
+    const int64_t idx = q - a.lut_off;
+    return idx < 0 ? 0 : (idx >= a.lut_len ? a.lut_len - 1 : idx);
+}
+
 // Requantize, table and residual Add of one accumulator (mode EPI_QUANT):
 // returns the quantized value q (before the storage offset).
 __device__ __forceinline__ int64_t quant_one(const ConvArgs& a, int64_t v,
                                              int64_t m, int64_t s,
                                              int64_t res_q) {
     int64_t q = qa_clip128(qa_mbqm_fast(v, m, s) + a.zp, a.qmin, a.qmax);
-    if (a.lut) {
-        int64_t idx = q - a.lut_off;
-        idx = idx < 0 ? 0 : (idx >= a.lut_len ? a.lut_len - 1 : idx);
-        q = a.lut[idx];
-    }
-    if (a.res) {
-        const int64_t first = a.res_first ? res_q : q;
-        const int64_t second = a.res_first ? q : res_q;
-        const qa_i128 t = qa_mbqm_fast(first - a.za, a.ma, a.sa) +
-                          (qa_i128)a.add_sign *
-                              qa_mbqm_fast(second - a.zb, a.mb, a.sb) +
-                          a.add_zp;
-        q = qa_clip128(t, a.add_qmin, a.add_qmax);
-    }
+    if (a.lut) q = a.lut[lut_index(a, q)];
+    if (a.res) q = quant_add(a, q, res_q);
     return q;
 }
 

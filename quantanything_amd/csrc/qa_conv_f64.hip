@@ -128,6 +128,43 @@ __device__ __forceinline__ void f64_store(const ConvArgs& a, int64_t co,
     if (a.y2) store_any(a.y2, a.y_code, y2i, rescale2(a, q) - a.y_so);
 }
 
+// The epilogue of NV exact sums v[j] of one output channel co at pixels
+// pp[j] (skipped at or past M) for int16 outputs (mode EPI_QUANT, dense
+// channels-last y / residual / copy): every value's table read and
+// residual read is issued before the first of them is used and before the
+// first store (one at a time they would each wait a memory round trip).
+template <int NV>
+__device__ __forceinline__ void epi16_batch(const ConvArgs& a, int64_t co,
+                                            const int64_t (&pp)[NV],
+                                            const int64_t (&v)[NV],
+                                            int64_t pre, int64_t m,
+                                            int64_t s) {
+    int64_t q[NV];
+    int32_t lv[NV];
+    int32_t rv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t p = min(pp[j], a.M - 1);  // in bounds, unused past M
+        const int64_t x = a.wide ? v[j] : (int64_t)(int32_t)v[j];
+        q[j] = qa_clip128(qa_mbqm_fast(x + pre, m, s) + a.zp, a.qmin,
+                          a.qmax);
+        lv[j] = 0;
+        rv[j] = 0;
+        if (a.lut) lv[j] = a.lut[lut_index(a, q[j])];
+        if (a.res) rv[j] = ((const int16_t*)a.res)[p * a.res_pst + co];
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (pp[j] >= a.M) continue;
+        int64_t qq = a.lut ? (int64_t)lv[j] : q[j];
+        if (a.res) qq = quant_add(a, qq, (int64_t)rv[j] + a.res_so);
+        ((int16_t*)a.y)[pp[j] * a.y_pst + co] = (int16_t)(qq - a.y_so);
+        if (a.y2)
+            ((int16_t*)a.y2)[pp[j] * a.y2_pst + co] =
+                (int16_t)(rescale2(a, qq) - a.y_so);
+    }
+}
+
 template <int WM, int TM, int V, bool KSPLIT, class WE>
 __global__ __launch_bounds__(256) void k_conv_f64(ConvArgs a) {
     typedef Frag<V, int16_t> XF;
@@ -269,6 +306,18 @@ __global__ __launch_bounds__(256) void k_conv_f64(ConvArgs a) {
         const int64_t pre = a.pre ? a.pre[co] : 0;
         const int64_t m = q ? a.mult[co] : 0;
         const int64_t s = q ? a.shift[co] : 0;
+        if (q && a.fastio && a.y_code == 2) {
+            int64_t pp[TM * 4], v[TM * 4];
+#pragma unroll
+            for (int t = 0; t < TM; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    pp[4 * t + r] = (tile0 + t) * 16 + 4 * r + kgl;
+                    v[4 * t + r] = (int64_t)acc[t][i][r];
+                }
+            epi16_batch(a, co, pp, v, pre, m, s);
+            continue;
+        }
 #pragma unroll
         for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -429,18 +478,24 @@ __global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
         const int64_t m = q ? a.mult[co] : 0;
         const int64_t sft = q ? a.shift[co] : 0;
         const int64_t kc = a.ws_k[co];
+        int64_t pp[TM * 4], v[TM * 4];
 #pragma unroll
         for (int t = 0; t < TM; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t pp = (tile0 + t) * 16 + 4 * kgl + r;
-                if (pp >= a.M) continue;
                 const int64_t u = (int64_t)sh[t][r] * 256 + sl[t][r];
-                const int64_t v = (int64_t)hh[t][i][r] * 65536 +
-                                  (int64_t)md[t][i][r] * 256 + ll[t][i][r] +
-                                  u * 128 + kc;
-                f64_store(a, co, pp, v, pre, m, sft);
+                pp[4 * t + r] = (tile0 + t) * 16 + 4 * kgl + r;
+                v[4 * t + r] = (int64_t)hh[t][i][r] * 65536 +
+                               (int64_t)md[t][i][r] * 256 + ll[t][i][r] +
+                               u * 128 + kc;
             }
+        if (q && a.fastio && a.y_code == 2) {
+            epi16_batch(a, co, pp, v, pre, m, sft);
+            continue;
+        }
+#pragma unroll
+        for (int j = 0; j < TM * 4; ++j)
+            if (pp[j] < a.M) f64_store(a, co, pp[j], v[j], pre, m, sft);
     }
 }
 
