@@ -128,26 +128,83 @@ __device__ __forceinline__ void f64_store(const ConvArgs& a, int64_t co,
     if (a.y2) store_any(a.y2, a.y_code, y2i, rescale2(a, q) - a.y_so);
 }
 
+// The 128-bit requantization of one value (out of line: the float64 form
+// below hands it the rare values it cannot decide).
+__device__ __noinline__ int64_t requant_exact(int64_t x, int64_t m, int64_t s,
+                                              int64_t zp, int64_t lo,
+                                              int64_t hi) {
+    return qa_clip128(qa_mbqm_fast(x, m, s) + zp, lo, hi);
+}
+
+// Exact float64 forms of the fixed-point multiplies of the 16-bit epilogue
+// (qa_mbqm: floor(x m 2^-ts + 1/2), ts = 31 + shift):
+//  * requantize, |x| < 2^53, |m| < 2^31, 1 <= ts <= 120, clip bounds within
+//    2^19: y = fma(x, m 2^-ts, 1/2 + zp) is one rounding of the exact value
+//    (x and m 2^-ts are exact doubles), |error| <= 2^-52 |y|; below |y| =
+//    2^20, floor(y) is the exact result unless frac(y) lies within 2^-30 of
+//    0 or 1 (those values take requant_exact); above, the clip gives the
+//    same bound either way.
+//  * multiplies of a clipped value (|d| < 2^20) by |m| < 2^31 with 1 <= ts
+//    <= 53 (the residual Add, the rescaled copy): d m is an exact double
+//    below 2^51, and so is d m 2^-ts + 1/2, so floor gives the exact result.
+struct MulD {
+    double md;
+    bool ok;
+};
+__device__ __forceinline__ MulD mul_d(int64_t m, int64_t shift, int64_t tmax) {
+    const int64_t ts = 31 + shift;
+    MulD r;
+    r.ok = ts >= 1 && ts <= tmax && m > -((int64_t)1 << 31) &&
+           m < ((int64_t)1 << 31);
+    r.md = r.ok ? ldexp((double)m, -(int)ts) : 0.0;
+    return r;
+}
+__device__ __forceinline__ double round_d(double d, double md) {
+    return floor(fma(d, md, 0.5));
+}
+__device__ __forceinline__ double clamp_d(double v, int64_t lo, int64_t hi) {
+    return fmin(fmax(v, (double)lo), (double)hi);
+}
+
 // The epilogue of NV exact sums v[j] of one output channel co at pixels
 // pp[j] (skipped at or past M) for int16 outputs (mode EPI_QUANT, dense
 // channels-last y / residual / copy): every value's table read and
 // residual read is issued before the first of them is used and before the
-// first store (one at a time they would each wait a memory round trip).
+// first store (one at a time they would each wait a memory round trip);
+// the multiplies in their float64 forms where those apply.
 template <int NV>
 __device__ __forceinline__ void epi16_batch(const ConvArgs& a, int64_t co,
                                             const int64_t (&pp)[NV],
                                             const int64_t (&v)[NV],
                                             int64_t pre, int64_t m,
                                             int64_t s) {
+    constexpr int64_t B19 = (int64_t)1 << 19, B20 = (int64_t)1 << 20;
+    const MulD rq = mul_d(m, s, 120);
+    const bool fast = rq.ok && a.qmin > -B19 && a.qmax < B19;
+    const double c0 = 0.5 + (double)a.zp;
+    const MulD ra = mul_d(a.ma, a.sa, 53), rb = mul_d(a.mb, a.sb, 53);
+    const bool rfast = ra.ok && rb.ok && (a.add_sign == 1 || a.add_sign == -1) &&
+                       a.za > -B20 && a.za < B20 && a.zb > -B20 &&
+                       a.zb < B20 && a.res_so > -B20 && a.res_so < B20 &&
+                       a.qmin > -B19 && a.qmax < B19;
+    const MulD r2 = mul_d(a.r2_m, a.r2_s, 53);
+    const bool r2fast = r2.ok && a.r2_zp_in > -B20 && a.r2_zp_in < B20;
     int64_t q[NV];
     int32_t lv[NV];
     int32_t rv[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int64_t p = min(pp[j], a.M - 1);  // in bounds, unused past M
-        const int64_t x = a.wide ? v[j] : (int64_t)(int32_t)v[j];
-        q[j] = qa_clip128(qa_mbqm_fast(x + pre, m, s) + a.zp, a.qmin,
-                          a.qmax);
+        const int64_t x = (a.wide ? v[j] : (int64_t)(int32_t)v[j]) + pre;
+        bool slow = !fast || x >= ((int64_t)1 << 53) ||
+                    x <= -((int64_t)1 << 53);
+        const double y = fma((double)x, rq.md, c0);
+        const double f = floor(y);
+        const double fr = y - f;
+        slow = slow || ((fr < 0x1p-30 || fr > 1.0 - 0x1p-30) &&
+                        fabs(y) < 0x1p20);
+        q[j] = slow ? requant_exact(x, m, s, a.zp, a.qmin, a.qmax)
+                    : (int64_t)clamp_d(f, a.qmin, a.qmax);
         lv[j] = 0;
         rv[j] = 0;
         if (a.lut) lv[j] = a.lut[lut_index(a, q[j])];
@@ -157,11 +214,32 @@ __device__ __forceinline__ void epi16_batch(const ConvArgs& a, int64_t co,
     for (int j = 0; j < NV; ++j) {
         if (pp[j] >= a.M) continue;
         int64_t qq = a.lut ? (int64_t)lv[j] : q[j];
-        if (a.res) qq = quant_add(a, qq, (int64_t)rv[j] + a.res_so);
+        if (a.res) {
+            const int64_t r = (int64_t)rv[j] + a.res_so;
+            if (rfast && qq > -B19 && qq < B19) {
+                const int64_t first = a.res_first ? r : qq;
+                const int64_t second = a.res_first ? qq : r;
+                const double t =
+                    round_d((double)(first - a.za), ra.md) +
+                    (double)a.add_sign *
+                        round_d((double)(second - a.zb), rb.md) +
+                    (double)a.add_zp;
+                qq = (int64_t)clamp_d(t, a.add_qmin, a.add_qmax);
+            } else {
+                qq = quant_add(a, qq, r);
+            }
+        }
         ((int16_t*)a.y)[pp[j] * a.y_pst + co] = (int16_t)(qq - a.y_so);
-        if (a.y2)
-            ((int16_t*)a.y2)[pp[j] * a.y2_pst + co] =
-                (int16_t)(rescale2(a, qq) - a.y_so);
+        if (a.y2) {
+            const int64_t c =
+                r2fast && qq > -B19 && qq < B19
+                    ? (int64_t)clamp_d(round_d((double)(qq - a.r2_zp_in),
+                                               r2.md) +
+                                           (double)a.r2_zp_out,
+                                       a.r2_qmin, a.r2_qmax)
+                    : rescale2(a, qq);
+            ((int16_t*)a.y2)[pp[j] * a.y2_pst + co] = (int16_t)(c - a.y_so);
+        }
     }
 }
 
