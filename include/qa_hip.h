@@ -422,7 +422,10 @@ int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
  * written (the intermediate stays in LDS). Returns -1, launching nothing,
  * for any other pair. The reference runs the two convolutions and the Add
  * one after another (quant_layers.py:320-335 twice, quant_layers.py:493-
- * 513). qa_conv_pair_supported checks a pair without launching (1 or 0). */
+ * 513). qa_conv_pair_supported checks a pair without launching (1 or 0).
+ * d2->tile: 0 (the library picks the band height), or 0x10000 | R for
+ * bands of R output rows a work-group (ignored where they do not fit);
+ * results do not depend on it. */
 int qa_conv_pair_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
 int qa_d_conv_pair(const qa_conv_desc* d1, const qa_conv_desc* d2,
                    void* stream);

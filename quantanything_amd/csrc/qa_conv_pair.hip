@@ -814,6 +814,13 @@ bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2,
             bestR = R;
         }
     }
+    // a caller's measured band height (tile code 0x10000 | R on the second
+    // descriptor), where the band fits
+    if (b2.tile_hint & TILE_VALID) {
+        const int rh = b2.tile_hint & 0xffff;
+        if (rh >= 1 && rh <= b1.OH && pair_geom(b1, rh, b3).lds > 0)
+            bestR = rh;
+    }
     PairGeom g = pair_geom(b1, bestR, b3);
     // which of the pair's outputs is the Concat's slice
     if (b3)

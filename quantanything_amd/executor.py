@@ -1019,7 +1019,9 @@ class DeviceExecutor:
 
             self.launches = [(fused, fn) if n == ln2 else (n, f)
                              for n, f in self.launches if n != ln1]
-            self.tunables.append((fused, d2, [0], fn))
+            # band heights to time (0: the library's cost model)
+            rows = [0] + [0x10000 | r for r in range(1, min(d2.OH, 16) + 1)]
+            self.tunables.append((fused, d2, rows, fn))
             self.pair_descs[fused] = (d1, d2)
             self.tensors.pop(mids[0], None)  # never materialized
 
@@ -1067,8 +1069,9 @@ class DeviceExecutor:
 
                 self.launches = [(tname, fn) if n == ln3 else (n, f)
                                  for n, f in self.launches if n != fused]
+                rows = next(t[2] for t in self.tunables if t[0] == fused)
                 self.tunables = [t for t in self.tunables if t[0] != fused]
-                self.tunables.append((tname, d2, [0], fn))
+                self.tunables.append((tname, d2, rows, fn))
                 break
 
     def _fuse_chains(self, cons):
