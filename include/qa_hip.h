@@ -220,11 +220,11 @@ typedef struct qa_conv_desc {
                       loads); 0x10800 | wm
                       (wm 1, 2, 4): bands of output rows with the input band
                       and the weights in LDS (layout 0, one group, a table
-                      plan); 0x11000 | wm (wm 1, 2, 4): the weights held in
-                      registers (at most 36 / wm K-steps of 64 bytes), input
-                      bands double-buffered in LDS, persistent work-groups
-                      (layout 0, one group, a table plan, int8 weights
-                      without a zero point). FP64 path (w_code
+                      plan); 0x11000 | wm | R << 4 (wm 1, 2, 4): the weights
+                      held in registers (at most 36 / wm K-steps of 64
+                      bytes), bands of R output rows (R 0: the library's
+                      choice) in LDS (layout 0, one group, a table plan,
+                      int8 weights without a zero point). FP64 path (w_code
                       8): 0x10000 | wm | tm << 4
                       | split << 8 with (wm, tm, split) one of (1,1,0),
                       (2,1,0), (1,4,0), (1,1,1), (2,1,1), (4,1,1); tm =
@@ -459,7 +459,8 @@ int qa_d_conv_pair_tail(const qa_conv_desc* d1, const qa_conv_desc* d2,
  * written. Returns -1, launching nothing, for any other pair; the
  * reference runs the two convolutions one after the other
  * (quant_layers.py:320-335 twice). qa_conv_chain_supported checks a pair
- * without launching (1 or 0). */
+ * without launching (1 or 0). d2->tile: 0, or 0x10000 | R for bands of R
+ * output rows a work-group (ignored where they do not fit). */
 int qa_conv_chain_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
 int qa_d_conv_chain(const qa_conv_desc* d1, const qa_conv_desc* d2,
                     void* stream);

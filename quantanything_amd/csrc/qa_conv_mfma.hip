@@ -76,7 +76,7 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     // low bits); without a hint, the default for convolutions of more than
     // one 64-byte K-step (measured the fastest choice for most 3x3 layers)
     if ((a.tile_hint & TILE_VALID) && ((a.tile_hint >> 12) & 1)) {
-        const int ww = a.tile_hint & 0xff;
+        const int ww = a.tile_hint & 0xf;  // bits 4..7: the band height
         if (conv_wr_applies(b, epi, ww)) return launch_conv_wr(b, ww, st);
     }
     if (!(a.tile_hint & TILE_VALID) && a.KGp > 4 && (a.KH > 1 || a.KW > 1)) {

@@ -700,6 +700,15 @@ bool wr_launch(const ConvArgs& b, int wm, bool ch, const ConvArgs& b2,
             bestR = R;
         }
     }
+    // a caller's measured band height: tile code 0x11000 | wm | R << 4 of
+    // the convolution, or 0x10000 | R of the chained 1x1 convolution
+    int rh = 0;
+    if (ch) {
+        if (b2.tile_hint & TILE_VALID) rh = b2.tile_hint & 0xffff;
+    } else if ((b.tile_hint & TILE_VALID) && ((b.tile_hint >> 12) & 1)) {
+        rh = (b.tile_hint >> 4) & 15;
+    }
+    if (rh >= 1 && rh <= b.OH && wr_geom(b, wm, rh, ch).lds > 0) bestR = rh;
     const WrGeom g = wr_geom(b, wm, bestR, ch);
     const int64_t gx = g.nbands;
     if (g.lds == 0 || cblocks > 65535 || gx >= ((int64_t)1 << 31)) {

@@ -406,6 +406,9 @@ def plan_epilogue(lib, d, mult, shift, pre=None, lut=None):
 # Tiles of the FP64 matrix-core path (qa_conv_f64.hip): 16-channel groups
 # wm | 16-pixel tiles per wave tm << 4 | K split over the work-group << 8.
 F64_TILES = (0x11, 0x12, 0x41, 0x111, 0x112, 0x114)
+# Band heights (output rows a work-group) timed for the band kernels, beside
+# the library's own choice.
+BAND_ROWS = (1, 2, 3, 4, 6, 8, 12)
 # Element types tried, in order, for that path's packed weights.
 F64_WEIGHT_TYPES = (np.int16, np.int32)
 
@@ -1096,6 +1099,7 @@ class DeviceExecutor:
                                                     ctypes.byref(d2)):
                 continue
             fused = f"chain:{ln1[5:]}+{ln2[5:]}"
+            rows = [0] + [0x10000 | r for r in BAND_ROWS if r <= d1.OH]
 
             def fn(s, d1=d1, d2=d2):
                 _ok(self.lib.qa_d_conv_chain(ctypes.byref(d1),
@@ -1104,7 +1108,7 @@ class DeviceExecutor:
 
             self.launches = [(fused, fn) if n == ln2 else (n, f)
                              for n, f in self.launches if n != ln1]
-            self.tunables.append((fused, d2, [0], fn))
+            self.tunables.append((fused, d2, rows, fn))
             self.tensors.pop(mids[0], None)  # never materialized
 
     # ------------------------------------------------------- element-wise --
@@ -1880,8 +1884,9 @@ class DeviceExecutor:
             out += [0x10800 | wm for wm in (1, 2, 4) if wm <= wm_max]
             # weights held in registers (K up to 36 / wm steps of 64 bytes;
             # the library checks the rest and falls back)
-            out += [0x11000 | wm for wm in (1, 2, 4)
-                    if wm <= wm_max and d.w_kgp // 4 <= 36 // wm]
+            out += [0x11000 | wm | r << 4 for wm in (1, 2, 4)
+                    if wm <= wm_max and d.w_kgp // 4 <= 36 // wm
+                    for r in (0,) + BAND_ROWS if r <= d.OH]
         for wm in (1, 2, 4, 8):
             if wm > wm_max:
                 break
