@@ -23,6 +23,8 @@
 // are added through LDS and each wave finishes a quarter of the outputs.
 // The MFMA's result register r of lane l is output row 4r + l/16, column
 // l%16.
+#include <type_traits>
+
 #include "qa_conv_mfma.h"
 
 namespace qa {
@@ -426,8 +428,11 @@ __global__ __launch_bounds__(256) void k_conv_f64(ConvArgs a) {
 // path's epilogue. A wave owns TM tiles of 16 pixels (rows) x WM 16-channel
 // blocks (columns); a lane's K-values of a step are the 16 channels of
 // k-group 4 s + lane / 16 (32 bytes of int16, split with v_perm), loaded
-// straight from memory with the next step's loads in flight.
-template <int WM, int TM>
+// straight from memory with the next step's loads in flight. NARROW (at
+// most 4 channels, stored 4 a pixel: the image stem): a lane loads its
+// pixel's 8 bytes and the group's other 12 positions hold 0 (their weights
+// are 0).
+template <int WM, int TM, bool NARROW>
 __global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -480,8 +485,14 @@ __global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
             // outside: the image's first pixel (in bounds, not used)
             const int64_t off =
                 in ? ((int64_t)iy * a.W + ix) * a.x_sp + 16 * cb : 0;
-            xr[d][t][0] = *(const int4*)(xb[t] + off);
-            xr[d][t][1] = *(const int4*)(xb[t] + off + 8);
+            if (NARROW) {
+                const int2 u = *(const int2*)(xb[t] + off);
+                xr[d][t][0] = int4{u.x, u.y, 0, 0};
+                xr[d][t][1] = int4{0, 0, 0, 0};
+            } else {
+                xr[d][t][0] = *(const int4*)(xb[t] + off);
+                xr[d][t][1] = *(const int4*)(xb[t] + off + 8);
+            }
             xin[d][t] = in;
         }
 #pragma unroll
@@ -656,9 +667,15 @@ bool launch_conv_f64(const ConvArgs& a, hipStream_t st) {
     // are given and the input fits it (16-byte aligned 16-channel groups,
     // K' = 16 KGp < 2^16, the stored zero point an int16); tile code 0x1000
     // | wm | tm << 4, by default the widest channel block, one tile a wave
-    if (a.ws && a.ws_k && a.Cg % 16 == 0 && a.x_sp % 8 == 0 &&
-        a.x_sn % 8 == 0 && xa % 16 == 0 && a.KGp > 0 && a.KGp < 4096 &&
-        a.x_add >= -32767 && a.x_add <= 32768) {
+    // narrow: at most 4 channels in 8-byte aligned 4-channel pixels
+    const bool narrow = a.Cg <= 4 && a.G == 1 && a.x_sp % 4 == 0 &&
+                        a.x_sn % 4 == 0 && xa % 8 == 0;
+    if (a.ws && a.ws_k &&
+        ((a.Cg % 16 == 0 && a.x_sp % 8 == 0 && a.x_sn % 8 == 0 &&
+          xa % 16 == 0) ||
+         narrow) &&
+        a.KGp > 0 && a.KGp < 4096 && a.x_add >= -32767 &&
+        a.x_add <= 32768) {
         int code = 0x1010 | (a.Cog >= 64 ? 4 : a.Cog >= 32 ? 2 : 1);
         if (a.tile_hint & TILE_VALID) code = a.tile_hint & 0xffff;
         const int wm = code & 15, tm = (code >> 4) & 15;
@@ -671,14 +688,21 @@ bool launch_conv_f64(const ConvArgs& a, hipStream_t st) {
                 return false;
             }
             const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)a.G);
-            switch (code) {
-                case 0x1011: k_conv_bs<1, 1><<<grid, 256, 0, st>>>(b); break;
-                case 0x1012: k_conv_bs<2, 1><<<grid, 256, 0, st>>>(b); break;
-                case 0x1014: k_conv_bs<4, 1><<<grid, 256, 0, st>>>(b); break;
-                case 0x1021: k_conv_bs<1, 2><<<grid, 256, 0, st>>>(b); break;
-                case 0x1022: k_conv_bs<2, 2><<<grid, 256, 0, st>>>(b); break;
-                default: k_conv_bs<4, 2><<<grid, 256, 0, st>>>(b); break;
-            }
+            auto go = [&](auto nr) {
+                constexpr bool NR = decltype(nr)::value;
+                switch (code) {
+                    case 0x1011: k_conv_bs<1, 1, NR><<<grid, 256, 0, st>>>(b); break;
+                    case 0x1012: k_conv_bs<2, 1, NR><<<grid, 256, 0, st>>>(b); break;
+                    case 0x1014: k_conv_bs<4, 1, NR><<<grid, 256, 0, st>>>(b); break;
+                    case 0x1021: k_conv_bs<1, 2, NR><<<grid, 256, 0, st>>>(b); break;
+                    case 0x1022: k_conv_bs<2, 2, NR><<<grid, 256, 0, st>>>(b); break;
+                    default: k_conv_bs<4, 2, NR><<<grid, 256, 0, st>>>(b); break;
+                }
+            };
+            if (narrow && a.Cg % 16 != 0)
+                go(std::true_type{});
+            else
+                go(std::false_type{});
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) {
                 set_hip_error("launch_conv_f64", e);

@@ -731,7 +731,8 @@ class DeviceExecutor:
                     info = dict(w=_dev(wf, dt), w_code=8, layout=wf.itemsize,
                                 kgp=ck.value, rows=rows.value, corr=None,
                                 boff=None, rowsum=0, wide=1)
-                    if dt == np.int16 and cg % 16 == 0:
+                    if dt == np.int16 and (cg % 16 == 0 or
+                                           (cg <= 4 and groups == 1)):
                         # the same weights as two int8 planes: the library
                         # may run the byte-split form on the int8 cores
                         kgp8, rows8 = _I64(0), _I64(0)

@@ -221,8 +221,9 @@ def test_int16_conv_on_fp64_matrix_cores(hip, tmp_path, monkeypatch, wtype,
                                          groups, size):
     """16-bit convolutions run on the FP64 MFMA path (w_code 8, weights
     packed as int16 or int32) or, for int16 weights and a multiple of 16
-    channels per group, by default in the byte-split form on the int8
-    matrix cores (tile codes 0x11000 | wm | tm << 4); under every tile code
+    channels per group (or at most 4 input channels, the stem), by default
+    in the byte-split form on the int8 matrix cores (tile codes 0x11000 |
+    wm | tm << 4); under every tile code
     every tensor equals the oracle's int64-accumulated one (inputs past the
     calibrated range saturate to the int16 extremes)."""
     from quantanything_amd import executor
@@ -242,7 +243,8 @@ def test_int16_conv_on_fp64_matrix_cores(hip, tmp_path, monkeypatch, wtype,
             if isinstance(d, ConvDesc)] == [(8, np.dtype(wtype).itemsize)]
     [(_, d, codes, _)] = ex.tunables
     assert len(codes) >= 4
-    split = wtype == "int16" and (cin // groups) % 16 == 0
+    split = wtype == "int16" and ((cin // groups) % 16 == 0 or
+                                  (cin <= 4 and groups == 1))
     assert bool(d.wsplit) == split
     assert any(c & 0x1000 for c in codes) == split
     for code in codes:
