@@ -173,8 +173,10 @@ __device__ __forceinline__ double clamp_d(double v, int64_t lo, int64_t hi) {
 // channels-last y / residual / copy): every value's table read and
 // residual read is issued before the first of them is used and before the
 // first store (one at a time they would each wait a memory round trip);
-// the multiplies in their float64 forms where those apply.
-template <int NV>
+// the multiplies in their float64 forms where those apply. RES / Y2: a
+// residual Add / a rescaled copy (compile-time, so that a launch without
+// them holds none of their constants).
+template <int NV, bool RES = true, bool Y2 = true>
 __device__ __forceinline__ void epi16_batch(const ConvArgs& a, int64_t co,
                                             const int64_t (&pp)[NV],
                                             const int64_t (&v)[NV],
@@ -210,13 +212,14 @@ __device__ __forceinline__ void epi16_batch(const ConvArgs& a, int64_t co,
         lv[j] = 0;
         rv[j] = 0;
         if (a.lut) lv[j] = a.lut[lut_index(a, q[j])];
-        if (a.res) rv[j] = ((const int16_t*)a.res)[p * a.res_pst + co];
+        if (RES && a.res)
+            rv[j] = ((const int16_t*)a.res)[p * a.res_pst + co];
     }
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         if (pp[j] >= a.M) continue;
         int64_t qq = a.lut ? (int64_t)lv[j] : q[j];
-        if (a.res) {
+        if (RES && a.res) {
             const int64_t r = (int64_t)rv[j] + a.res_so;
             if (rfast && qq > -B19 && qq < B19) {
                 const int64_t first = a.res_first ? r : qq;
@@ -232,7 +235,7 @@ __device__ __forceinline__ void epi16_batch(const ConvArgs& a, int64_t co,
             }
         }
         ((int16_t*)a.y)[pp[j] * a.y_pst + co] = (int16_t)(qq - a.y_so);
-        if (a.y2) {
+        if (Y2 && a.y2) {
             const int64_t c =
                 r2fast && qq > -B19 && qq < B19
                     ? (int64_t)clamp_d(round_d((double)(qq - a.r2_zp_in),
@@ -432,7 +435,10 @@ __global__ __launch_bounds__(256) void k_conv_f64(ConvArgs a) {
 // most 4 channels, stored 4 a pixel: the image stem): a lane loads its
 // pixel's 8 bytes and the group's other 12 positions hold 0 (their weights
 // are 0).
-template <int WM, int TM, bool NARROW>
+// EPI: 0 the general per-element epilogue (f64_store); else the int16 form
+// (mode EPI_QUANT, dense channels-last y), bit 1 with a residual Add, bit 2
+// with a rescaled copy.
+template <int WM, int TM, bool NARROW, int EPI>
 __global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -578,13 +584,14 @@ __global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
                                (int64_t)md[t][i][r] * 256 + ll[t][i][r] +
                                u * 128 + kc;
             }
-        if (q && a.fastio && a.y_code == 2) {
-            epi16_batch(a, co, pp, v, pre, m, sft);
-            continue;
-        }
+        if constexpr (EPI != 0) {
+            epi16_batch<TM * 4, (EPI & 2) != 0, (EPI & 4) != 0>(a, co, pp, v,
+                                                              pre, m, sft);
+        } else {
 #pragma unroll
-        for (int j = 0; j < TM * 4; ++j)
-            if (pp[j] < a.M) f64_store(a, co, pp[j], v[j], pre, m, sft);
+            for (int j = 0; j < TM * 4; ++j)
+                if (pp[j] < a.M) f64_store(a, co, pp[j], v[j], pre, m, sft);
+        }
     }
 }
 
@@ -678,6 +685,9 @@ bool launch_conv_f64(const ConvArgs& a, hipStream_t st) {
         a.x_add <= 32768) {
         int code = 0x1010 | (a.Cog >= 64 ? 4 : a.Cog >= 32 ? 2 : 1);
         if (a.tile_hint & TILE_VALID) code = a.tile_hint & 0xffff;
+        // the narrow form has one 16-channel block a wave
+        const bool nform = narrow && a.Cg % 16 != 0;
+        if (nform && (code & 0xff00) == 0x1000) code = (code & ~15) | 1;
         const int wm = code & 15, tm = (code >> 4) & 15;
         if ((code & 0xff00) == 0x1000 && (wm == 1 || wm == 2 || wm == 4) &&
             (tm == 1 || tm == 2)) {
@@ -688,21 +698,43 @@ bool launch_conv_f64(const ConvArgs& a, hipStream_t st) {
                 return false;
             }
             const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)a.G);
-            auto go = [&](auto nr) {
+            // the epilogue's form: general, or int16 with / without the
+            // residual Add and the rescaled copy
+            const int epi = (b.mode == EPI_QUANT && b.fastio && b.y_code == 2)
+                                ? 1 | (b.res ? 2 : 0) | (b.y2 ? 4 : 0)
+                                : 0;
+            using std::integral_constant;
+            auto tiles = [&](auto nr, auto ep) {
                 constexpr bool NR = decltype(nr)::value;
+                constexpr int EP = decltype(ep)::value;
                 switch (code) {
-                    case 0x1011: k_conv_bs<1, 1, NR><<<grid, 256, 0, st>>>(b); break;
-                    case 0x1012: k_conv_bs<2, 1, NR><<<grid, 256, 0, st>>>(b); break;
-                    case 0x1014: k_conv_bs<4, 1, NR><<<grid, 256, 0, st>>>(b); break;
-                    case 0x1021: k_conv_bs<1, 2, NR><<<grid, 256, 0, st>>>(b); break;
-                    case 0x1022: k_conv_bs<2, 2, NR><<<grid, 256, 0, st>>>(b); break;
-                    default: k_conv_bs<4, 2, NR><<<grid, 256, 0, st>>>(b); break;
+                    case 0x1011: k_conv_bs<1, 1, NR, EP><<<grid, 256, 0, st>>>(b); break;
+                    case 0x1021: k_conv_bs<1, 2, NR, EP><<<grid, 256, 0, st>>>(b); break;
+                    default:
+                        if constexpr (!NR) {
+                            switch (code) {
+                                case 0x1012: k_conv_bs<2, 1, false, EP><<<grid, 256, 0, st>>>(b); break;
+                                case 0x1014: k_conv_bs<4, 1, false, EP><<<grid, 256, 0, st>>>(b); break;
+                                case 0x1022: k_conv_bs<2, 2, false, EP><<<grid, 256, 0, st>>>(b); break;
+                                default: k_conv_bs<4, 2, false, EP><<<grid, 256, 0, st>>>(b); break;
+                            }
+                        }
+                        break;  // narrow: codes 0x1011 / 0x1021 only
                 }
             };
-            if (narrow && a.Cg % 16 != 0)
-                go(std::true_type{});
+            auto forms = [&](auto nr) {
+                switch (epi) {
+                    case 1: tiles(nr, integral_constant<int, 1>{}); break;
+                    case 3: tiles(nr, integral_constant<int, 3>{}); break;
+                    case 5: tiles(nr, integral_constant<int, 5>{}); break;
+                    case 7: tiles(nr, integral_constant<int, 7>{}); break;
+                    default: tiles(nr, integral_constant<int, 0>{}); break;
+                }
+            };
+            if (nform)
+                forms(std::true_type{});
             else
-                go(std::false_type{});
+                forms(std::false_type{});
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) {
                 set_hip_error("launch_conv_f64", e);
