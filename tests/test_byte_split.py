@@ -1,5 +1,6 @@
 """The byte-split form of 16-bit convolutions (int8 matrix cores): the
-weight packer and the decomposition the kernel sums, checked on the CPU.
+weight packer, the decomposition the kernel sums and the epilogue's float64
+requantization, checked on the CPU.
 
 A stored activation x (int16) is 256 xh + xl + 128 with xh = x >> 8 and
 xl = (x & 255) - 128, both int8; a centred weight w likewise. Over the
@@ -108,3 +109,69 @@ def test_decomposition_equals_the_direct_sum(seed):
     # the int8 sums stay inside int32 for K' < 2^16
     assert max(abs(hh), abs(mid), abs(lo)) < 2 ** 31
     assert ((xh >= -128) & (xh <= 127) & (xl >= -128) & (xl <= 127)).all()
+
+
+def _mbqm(x, m, s):
+    """The reference's fixed-point multiply (qa_kernels.cpp:188-205):
+    round half up of x m 2^-(31+s), exact in Python integers."""
+    ts = 31 + s
+    p = x * m
+    if ts > 0:
+        ts = min(ts, 120)
+        return (p + (1 << (ts - 1))) >> ts
+    return p << min(-ts, 60)
+
+
+def _fma_double(a, b, c):
+    """fma(a, b, c) on doubles: the exact a b + c rounded once to the
+    nearest double (Python's float() of a Fraction rounds correctly)."""
+    from fractions import Fraction
+    return float(Fraction(a) * Fraction(b) + Fraction(c))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_float64_requantize_form_is_exact(seed):
+    """The 16-bit epilogue's float64 requantization: y = fma(x, m 2^-ts,
+    1/2 + zp), floor(y) clipped, except where frac(y) lies within 2^-30 of
+    0 or 1 below |y| = 2^20 (those take the 128-bit form). Every value the
+    guard lets through equals the exact clip(mbqm(x) + zp); exact ties (x m
+    a multiple of 2^(ts-1)) are all flagged."""
+    import math
+    rng = np.random.default_rng(100 + seed)
+    flagged = 0
+    for _ in range(3000):
+        m = int(rng.integers(1 << 29, 1 << 31)) * int(rng.choice([1, -1]))
+        s = int(rng.integers(-30, 40))
+        ts = 31 + s
+        if not 1 <= ts <= 120:
+            continue
+        zp = int(rng.integers(-32768, 32768))
+        lo, hi = -32768, 32767
+        if rng.random() < 0.3:  # an exact tie: x m = (2k + 1) 2^(ts-1)
+            if ts - 1 > 62:
+                continue
+            # x = (2k + 1) 2^(ts-1) / m needs m | ...: use m a power of two
+            m = (1 << int(rng.integers(0, 31))) * int(rng.choice([1, -1]))
+            k = int(rng.integers(-4000, 4000))
+            num = (2 * k + 1) << (ts - 1)
+            if num % m:
+                continue
+            x = num // m
+        else:
+            x = int(rng.integers(-(1 << 45), 1 << 45))
+        if abs(x) >= 1 << 53:
+            continue
+        md = math.ldexp(float(m), -ts)  # exact: |m| < 2^31
+        y = _fma_double(float(x), md, 0.5 + zp)
+        f = math.floor(y)
+        fr = y - f
+        near = (fr < 2.0 ** -30 or fr > 1 - 2.0 ** -30) and abs(y) < 2.0 ** 20
+        want = min(max(_mbqm(x, m, s) + zp, lo), hi)
+        if near:
+            flagged += 1
+            continue
+        assert min(max(f, lo), hi) == want, (x, m, s, zp)
+        # an exact tie never passes the guard
+        assert (x * m) % (1 << (ts - 1)) or (x * m) % (1 << ts) == 0 \
+            or abs(y) >= 2.0 ** 20, (x, m, s)
+    assert flagged > 0
