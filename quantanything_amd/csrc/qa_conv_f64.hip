@@ -446,10 +446,26 @@ __global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
     const int g = blockIdx.z;
     const int co0 = blockIdx.y * WM * 16;
     const int64_t tile0 = ((int64_t)blockIdx.x * 4 + wave) * TM;
+    // per k-group, built once per work-group: the element offset of its
+    // 16 channels from the tap's input pixel (-1: no tap, the k-group pads
+    // K) and the tap's displacement dy << 16 | dx (the host keeps both
+    // below 2^31 and 2^15)
+    extern __shared__ int2 s_kt[];
+    for (int kg = threadIdx.x; kg < a.KGp; kg += 256) {
+        int2 e = {-1, 0};
+        if (kg < a.KG) {
+            const int tap = kg / a.CB, cb = kg - tap * a.CB;
+            const int ky = tap / a.KW, kx = tap - ky * a.KW;
+            e.x = (ky * a.DH * a.W + kx * a.DW) * (int)a.x_sp + 16 * cb;
+            e.y = (ky * a.DH) << 16 | (kx * a.DW);
+        }
+        s_kt[kg] = e;
+    }
+    __syncthreads();
     if (tile0 * 16 >= a.M) return;
     const int nsteps = a.KGp >> 2;
     const int16_t* xb[TM];
-    int iy0[TM], ix0[TM];
+    int iy0[TM], ix0[TM], pb[TM];
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
         const int64_t p = min((tile0 + t) * 16 + col, a.M - 1);
@@ -458,6 +474,7 @@ __global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
                 (int64_t)g * a.Cg;
         iy0[t] = pos.oy * a.SH - a.PH;
         ix0[t] = pos.ox * a.SW - a.PW;
+        pb[t] = (iy0[t] * a.W + ix0[t]) * (int)a.x_sp;  // may be < 0
     }
     // the lane's weight row (channel co0 + 16 i + col) in the high plane;
     // the low plane G groups further
@@ -477,20 +494,15 @@ __global__ __launch_bounds__(256) void k_conv_bs(ConvArgs a) {
     v4i whr[D][WM], wlr[D][WM];
     auto fetch = [&](int d, int s) {
         s = min(s, nsteps - 1);  // steps past the end: in bounds, unused
-        const int kg = 4 * s + kgl;
-        const int tap = (int)(((uint64_t)kg * a.mg_cb) >> 32);
-        const int cb = kg - tap * a.CB;
-        const int ky = (int)(((uint64_t)tap * a.mg_kw) >> 32);
-        const int kx = tap - ky * a.KW;
-        const bool kok = kg < a.KG;
+        const int2 e = s_kt[4 * s + kgl];
+        const int dy = e.y >> 16, dx = e.y & 0xffff;
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-            const int iy = iy0[t] + ky * a.DH, ix = ix0[t] + kx * a.DW;
-            const bool in = kok && (unsigned)iy < (unsigned)a.H &&
+            const int iy = iy0[t] + dy, ix = ix0[t] + dx;
+            const bool in = e.x >= 0 && (unsigned)iy < (unsigned)a.H &&
                             (unsigned)ix < (unsigned)a.W;
             // outside: the image's first pixel (in bounds, not used)
-            const int64_t off =
-                in ? ((int64_t)iy * a.W + ix) * a.x_sp + 16 * cb : 0;
+            const int off = in ? pb[t] + e.x : 0;
             if (NARROW) {
                 const int2 u = *(const int2*)(xb[t] + off);
                 xr[d][t][0] = int4{u.x, u.y, 0, 0};
@@ -682,7 +694,14 @@ bool launch_conv_f64(const ConvArgs& a, hipStream_t st) {
           xa % 16 == 0) ||
          narrow) &&
         a.KGp > 0 && a.KGp < 4096 && a.x_add >= -32767 &&
-        a.x_add <= 32768) {
+        a.x_add <= 32768 &&
+        // the k-group table's int32 offsets, displacements below 2^15 and
+        // every pixel base of the padded extent in int32
+        (int64_t)(a.H + a.PH + a.KH * a.DH + a.SH) *
+                (a.W + a.PW + a.KW * a.DW + a.SW) * a.x_sp +
+                16 * (int64_t)a.CB < ((int64_t)1 << 31) &&
+        (int64_t)(a.KH - 1) * a.DH < 32768 &&
+        (int64_t)(a.KW - 1) * a.DW < 32768) {
         int code = 0x1010 | (a.Cog >= 64 ? 4 : a.Cog >= 32 ? 2 : 1);
         if (a.tile_hint & TILE_VALID) code = a.tile_hint & 0xffff;
         // the narrow form has one 16-channel block a wave
@@ -704,19 +723,20 @@ bool launch_conv_f64(const ConvArgs& a, hipStream_t st) {
                                 ? 1 | (b.res ? 2 : 0) | (b.y2 ? 4 : 0)
                                 : 0;
             using std::integral_constant;
+            const size_t ktab = (size_t)a.KGp * sizeof(int2);  // k-groups
             auto tiles = [&](auto nr, auto ep) {
                 constexpr bool NR = decltype(nr)::value;
                 constexpr int EP = decltype(ep)::value;
                 switch (code) {
-                    case 0x1011: k_conv_bs<1, 1, NR, EP><<<grid, 256, 0, st>>>(b); break;
-                    case 0x1021: k_conv_bs<1, 2, NR, EP><<<grid, 256, 0, st>>>(b); break;
+                    case 0x1011: k_conv_bs<1, 1, NR, EP><<<grid, 256, ktab, st>>>(b); break;
+                    case 0x1021: k_conv_bs<1, 2, NR, EP><<<grid, 256, ktab, st>>>(b); break;
                     default:
                         if constexpr (!NR) {
                             switch (code) {
-                                case 0x1012: k_conv_bs<2, 1, false, EP><<<grid, 256, 0, st>>>(b); break;
-                                case 0x1014: k_conv_bs<4, 1, false, EP><<<grid, 256, 0, st>>>(b); break;
-                                case 0x1022: k_conv_bs<2, 2, false, EP><<<grid, 256, 0, st>>>(b); break;
-                                default: k_conv_bs<4, 2, false, EP><<<grid, 256, 0, st>>>(b); break;
+                                case 0x1012: k_conv_bs<2, 1, false, EP><<<grid, 256, ktab, st>>>(b); break;
+                                case 0x1014: k_conv_bs<4, 1, false, EP><<<grid, 256, ktab, st>>>(b); break;
+                                case 0x1022: k_conv_bs<2, 2, false, EP><<<grid, 256, ktab, st>>>(b); break;
+                                default: k_conv_bs<4, 2, false, EP><<<grid, 256, ktab, st>>>(b); break;
                             }
                         }
                         break;  // narrow: codes 0x1011 / 0x1021 only
