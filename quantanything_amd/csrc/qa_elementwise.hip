@@ -213,6 +213,60 @@ __global__ __launch_bounds__(kThreads) void k_add(
     }
 }
 
+// int8 -> int8 Add through two 256-entry tables built per work-group:
+// each operand's rescaled term depends on its stored byte alone (RA[u] =
+// mbqm(u + a_so - za, ma, sa), RB[u] = sign mbqm(u + b_so - zb, mb, sb), the
+// exact 128-bit form, kept as int64), so the result is clip(RA[a] + RB[b] +
+// zp_out), as k_add computes it. Four values a thread (word loads and
+// stores) when W4, else one.
+template <bool W4>
+__global__ __launch_bounds__(kThreads) void k_add_i8_tab(
+    const int8_t* __restrict__ a, int64_t as, const int8_t* __restrict__ b,
+    int64_t bs, int8_t* __restrict__ out, int64_t os, int64_t rows,
+    int64_t cols, int64_t za, int64_t ma, int64_t sa, int64_t zb, int64_t mb,
+    int64_t sb, int64_t sign, int64_t zp_out, int64_t qmin, int64_t qmax,
+    int64_t a_so, int64_t b_so, int64_t out_so) {
+    __shared__ int64_t ta[256], tb[256];
+    {
+        const int u = threadIdx.x;  // kThreads == 256
+        ta[u] = (int64_t)qa_clip128(
+            qa_mbqm_fast((int64_t)(u - 128) + a_so - za, ma, sa),
+            INT64_MIN / 4, INT64_MAX / 4);
+        tb[u] = (int64_t)qa_clip128(
+            (qa_i128)sign *
+                qa_mbqm_fast((int64_t)(u - 128) + b_so - zb, mb, sb),
+            INT64_MIN / 4, INT64_MAX / 4);
+    }
+    __syncthreads();
+    auto one = [&](int av, int bv) {
+        const int64_t v = ta[av + 128] + tb[bv + 128] + zp_out;
+        return (int)((v < qmin ? qmin : (v > qmax ? qmax : v)) - out_so);
+    };
+    if (W4) {
+        const int64_t cw = cols >> 2;  // words a row
+        const bool small = rows * cw < ((int64_t)1 << 32);
+        for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+             i < rows * cw; i += (int64_t)gridDim.x * kThreads) {
+            const int64_t r =
+                small ? (int64_t)((uint32_t)i / (uint32_t)cw) : i / cw;
+            const int64_t c = (i - r * cw) * 4;
+            const uint32_t wa = *(const uint32_t*)(a + r * as + c);
+            const uint32_t wb = *(const uint32_t*)(b + r * bs + c);
+            uint32_t w = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                w |= (uint32_t)(uint8_t)one((int8_t)(wa >> (8 * k)),
+                                            (int8_t)(wb >> (8 * k)))
+                     << (8 * k);
+            *(uint32_t*)(out + r * os + c) = w;
+        }
+    } else {
+        QA_ROW_LOOP {
+            out[r * os + i] = (int8_t)one(a[r * as + i], b[r * bs + i]);
+        }
+    }
+}
+
 template <class TIn, class TOut>
 __global__ __launch_bounds__(kThreads) void k_mul(
     const TIn* __restrict__ a, int64_t as, const TIn* __restrict__ b,
@@ -556,6 +610,34 @@ QA_API int qa_d_add(const void* a, int64_t a_rstride, const void* b,
     if (rows <= 0 || cols <= 0) return 0;
     hipStream_t st = pick(stream);
     const dim3 g = grid_rows(rows, cols);
+    // int8: the two operand tables, when every entry is an exact int64 far
+    // from overflow (|m| < 2^31 and a right shift: |entry| < 2^41)
+    auto small_mul = [](int64_t m, int64_t sh) {
+        return m > -((int64_t)1 << 31) && m < ((int64_t)1 << 31) &&
+               31 + sh >= 1 && 31 + sh <= 120;
+    };
+    if (in_code == 1 && out_code == 1 && qmin >= -(1 << 20) &&
+        qmax <= (1 << 20) && (sign == 1 || sign == -1) &&
+        small_mul(ma, sa) && small_mul(mb, sb) && za > -(1 << 20) &&
+        za < (1 << 20) && zb > -(1 << 20) && zb < (1 << 20) &&
+        a_so > -(1 << 20) && a_so < (1 << 20) && b_so > -(1 << 20) &&
+        b_so < (1 << 20)) {
+        const bool w4 = cols % 4 == 0 && a_rstride % 4 == 0 &&
+                        b_rstride % 4 == 0 && out_rstride % 4 == 0 &&
+                        (uintptr_t)a % 4 == 0 && (uintptr_t)b % 4 == 0 &&
+                        (uintptr_t)out % 4 == 0;
+        if (w4)
+            k_add_i8_tab<true><<<grid_rows(rows, cols / 4), kThreads, 0, st>>>(
+                (const int8_t*)a, a_rstride, (const int8_t*)b, b_rstride,
+                (int8_t*)out, out_rstride, rows, cols, za, ma, sa, zb, mb, sb,
+                sign, zp_out, qmin, qmax, a_so, b_so, out_so);
+        else
+            k_add_i8_tab<false><<<g, kThreads, 0, st>>>(
+                (const int8_t*)a, a_rstride, (const int8_t*)b, b_rstride,
+                (int8_t*)out, out_rstride, rows, cols, za, ma, sa, zb, mb, sb,
+                sign, zp_out, qmin, qmax, a_so, b_so, out_so);
+        return launched("qa_d_add") ? 0 : -1;
+    }
     QA_DISPATCH_STORAGE(in_code, TI,
         QA_DISPATCH_STORAGE(out_code, TO,
             k_add<TI, TO><<<g, kThreads, 0, st>>>(

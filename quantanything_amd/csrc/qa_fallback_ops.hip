@@ -30,16 +30,33 @@ __device__ __forceinline__ float dequant_f32(int64_t q, int64_t zp,
 }
 
 // ------------------------------------------------------------ N-D copy --
+// I32: the element count and every extent below 2^32, so that the index
+// decode divides in 32 bits (a 64-bit division is a long software
+// sequence per dimension and element).
+template <bool I32>
 __global__ __launch_bounds__(kThreads) void k_copy_nd(qa_nd_copy d,
                                                       int64_t total) {
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * kThreads) {
-        int64_t rem = i, xo = 0, yo = 0;
-        for (int k = (int)d.ndim - 1; k >= 0; --k) {
-            const int64_t c = rem % d.shape[k];
-            rem /= d.shape[k];
-            xo += c * d.xs[k];
-            yo += c * d.ys[k];
+        int64_t xo = 0, yo = 0;
+        if (I32) {
+            uint32_t rem = (uint32_t)i;
+            for (int k = (int)d.ndim - 1; k >= 0; --k) {
+                const uint32_t n = (uint32_t)d.shape[k];
+                const uint32_t q = rem / n;
+                const int64_t c = (int64_t)(rem - q * n);
+                rem = q;
+                xo += c * d.xs[k];
+                yo += c * d.ys[k];
+            }
+        } else {
+            int64_t rem = i;
+            for (int k = (int)d.ndim - 1; k >= 0; --k) {
+                const int64_t c = rem % d.shape[k];
+                rem /= d.shape[k];
+                xo += c * d.xs[k];
+                yo += c * d.ys[k];
+            }
         }
         int64_t q = load_any(d.x, (int)d.x_code, xo) + d.x_so;
         if (d.mode == 1)
@@ -449,8 +466,12 @@ QA_API int qa_d_copy_nd(const qa_nd_copy* d, void* stream) {
     }
     if (total == 0) return 0;
     const int64_t blocks = std::min<int64_t>(ceil_div(total, kThreads), 65535);
-    k_copy_nd<<<(unsigned)blocks, kThreads, 0, (hipStream_t)stream>>>(*d,
-                                                                      total);
+    if (total < ((int64_t)1 << 32))  // every extent divides in 32 bits
+        k_copy_nd<true><<<(unsigned)blocks, kThreads, 0,
+                          (hipStream_t)stream>>>(*d, total);
+    else
+        k_copy_nd<false><<<(unsigned)blocks, kThreads, 0,
+                           (hipStream_t)stream>>>(*d, total);
     return launched("qa_d_copy_nd") ? 0 : -1;
 }
 
