@@ -537,6 +537,21 @@ int qa_d_quantize_nhwc(const float* x, int64_t N, int64_t C, int64_t HW,
                        int64_t zp, int64_t qmin, int64_t qmax, int64_t so,
                        void* stream);
 
+/* Quantizes float32 NCHW input [N, C, H, W] (C <= 4) into the int8 rows of
+ * a convolution whose stride equals its kernel KH x KW (no padding; KW a
+ * multiple of 4, H and W multiples of the kernel; 16-byte aligned x and
+ * y): row (n, py, px) of KH*KW*4 bytes holds the patch's pixels kernel row
+ * by kernel row, 4 bytes a pixel, each the word qa_d_quantize_nhwc writes
+ * with y_sp = 4 (channel c in byte c, 0 above C). The reference quantizes
+ * the graph input (quant_container.py:150-155) and the convolution reads
+ * its im2col columns (qa_kernels.cpp:107-137, 141-175); for such a
+ * convolution those columns are these rows, so it runs as a 1x1
+ * convolution over N*OH*OW one-pixel images of KH*KW*4 channels. */
+int qa_d_quantize_patches(const float* x, int64_t N, int64_t C, int64_t H,
+                          int64_t W, int64_t KH, int64_t KW, void* y,
+                          double scale, int64_t zp, int64_t qmin,
+                          int64_t qmax, int64_t so, void* stream);
+
 /* Float fallback of Softmax over the last axis of [rows, cols]:
  * dequantize to float32, softmax in float64, float32, quantize
  * (quant_layers.py:195-205, float_ops.py:380-385). */

@@ -151,6 +151,45 @@ __global__ __launch_bounds__(kThreads) void k_quantize_cl4x4(
     }
 }
 
+// Graph input: float32 NCHW -> int8 in the row order of a convolution
+// whose stride is its kernel (KH x KW, no padding, H % KH == W % KW == 0):
+// row (n, py, px) holds the patch's kernel rows ky = 0..KH-1 of KW pixels,
+// 4 bytes a pixel (channel c in byte c, 0 above C), the bytes
+// k_quantize_cl4x4 writes for that pixel. A thread quantizes 4 pixels of
+// one image row (KW % 4 == 0: one patch) and stores their 16 bytes.
+__global__ __launch_bounds__(kThreads) void k_quantize_patches(
+    const float* __restrict__ x, int64_t N, int64_t C, int H, int W, int KH,
+    int KW, int8_t* __restrict__ y, double scale, double inv, int64_t zp,
+    int64_t qmin, int64_t qmax, int64_t so) {
+    const int64_t HW = (int64_t)H * W;
+    const int64_t groups = N * HW / 4;
+    const int OH = H / KH, OW = W / KW;
+    for (int64_t gi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+         gi < groups; gi += (int64_t)gridDim.x * kThreads) {
+        const int64_t i = gi * 4;  // first pixel
+        const int64_t n = i / HW;
+        const int p = (int)(i - n * HW);
+        const int iy = p / W, ix = p - iy * W;
+        const int py = iy / KH, ky = iy - py * KH;
+        const int px = ix / KW, kx = ix - px * KW;
+        uint32_t w[4] = {0, 0, 0, 0};
+        for (int64_t c = 0; c < C; ++c) {
+            const float4 v = *(const float4*)(x + (n * C + c) * HW + p);
+            const float f[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                w[k] |= (uint32_t)(uint8_t)(qa_quantize_one_fast(
+                                                f[k], scale, inv, zp, qmin,
+                                                qmax) -
+                                            so)
+                        << (8 * c);
+        }
+        const int64_t row = (n * OH + py) * OW + px;
+        *(uint4*)(y + ((row * KH + ky) * KW + kx) * 4) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 // Graph input: float32 NCHW -> quantized channels-last with pixel stride
 // y_sp >= C (padding channels written as 0), one thread per pixel.
 template <class TOut>
@@ -525,6 +564,29 @@ QA_API int qa_d_quantize_nhwc(const float* x, int64_t N, int64_t C,
         return -1;
     }
     return launched("qa_d_quantize_nhwc") ? 0 : -1;
+}
+
+QA_API int qa_d_quantize_patches(const float* x, int64_t N, int64_t C,
+                                 int64_t H, int64_t W, int64_t KH, int64_t KW,
+                                 void* y, double scale, int64_t zp,
+                                 int64_t qmin, int64_t qmax, int64_t so,
+                                 void* stream) {
+    if (N <= 0) return 0;
+    if (!x || !y || C < 1 || C > 4 || KH < 1 || KW < 4 || KW % 4 != 0 ||
+        H < KH || W < KW || H % KH != 0 || W % KW != 0 ||
+        H >= (1 << 15) || W >= (1 << 15) || (uintptr_t)x % 16 != 0 ||
+        (uintptr_t)y % 16 != 0 || !(scale > 0.0)) {
+        qa::set_error("qa_d_quantize_patches",
+                      "needs 1-4 channels, KW a multiple of 4, H and W "
+                      "multiples of the kernel (below 2^15), 16-byte aligned "
+                      "buffers and a positive scale");
+        return -1;
+    }
+    const unsigned g = qa::grid_1d(N * H * W / 4, kThreads, 2048);
+    k_quantize_patches<<<g, kThreads, 0, (hipStream_t)stream>>>(
+        x, N, C, (int)H, (int)W, (int)KH, (int)KW, (int8_t*)y, scale,
+        1.0 / scale, zp, qmin, qmax, so);
+    return launched("qa_d_quantize_patches") ? 0 : -1;
 }
 
 // Softmax over the last axis of a [rows, cols] device tensor through float:

@@ -628,6 +628,7 @@ class DeviceExecutor:
             for name, t in zip(layer.node.outputs, outs):
                 self.tensors[name] = t
         self._plan_epilogues()
+        self._fuse_patch_input(cons)
         self._fuse_input_quantization(cons)
         self._fuse_pools(cons)
         self._fuse_pairs(cons)
@@ -880,6 +881,90 @@ class DeviceExecutor:
                 dev = _dev(plan, np.uint8)
                 self.keep.append(dev)
                 d.epi_plan = dev.data_ptr()
+
+    def _fuse_patch_input(self, cons):
+        """A 4-D graph input read only by an int8 convolution whose stride
+        is its kernel (no padding, KW a multiple of 4, layout-1 weights: a
+        transformer's patch embedding) is quantized straight into that
+        convolution's im2col rows (``qa_d_quantize_patches``: the bytes of
+        the channels-last tensor, permuted), and the convolution runs as a
+        1x1 convolution over N*OH*OW one-pixel images of KH*KW*4 channels
+        (the large-GEMM kernels), its weights in the same order."""
+        for name, (xf, t, qp) in list(self.input_q.items()):
+            users = cons.get(name, [])
+            if name in self.graph.outputs or len(users) != 1 or \
+                    users[0].kind != "conv" or t.code != 1 or t.offset:
+                continue
+            ln = f"conv:{users[0].name}"
+            hits = [e for e in self.mfma_descs
+                    if e[0].x == t.ptr and e[3] == ln]
+            if len(hits) != 1:
+                continue
+            d, host, lut, _ = hits[0]
+            if not (d.w_layout == 1 and d.G == 1 and d.KH == d.SH and
+                    d.KW == d.SW and d.PH == 0 and d.PW == 0 and
+                    d.DH == 1 and d.DW == 1 and d.KW % 4 == 0 and
+                    d.H == d.OH * d.KH and d.W == d.OW * d.KW and
+                    1 <= d.C <= 4 and d.x_sp == 4 and d.x_sc == 1 and
+                    d.x_sn == d.H * d.W * 4 and d.y_sc == 1 and
+                    d.y_sn == d.OH * d.OW * d.y_sp and not d.res and
+                    d.y_code == 1 and d.epi_plan):
+                continue
+            layer = users[0]
+            n, c, h, w = t.shape
+            kh, kw = d.KH, d.KW
+            kc = kh * kw * 4
+            wc = np.asarray(layer.w_centered, np.int64)
+            cout = wc.shape[0]
+            # channel (ky * KW + kx) * 4 + ci of the 1x1 convolution
+            w2 = np.zeros((cout, kh, kw, 4), np.int32)
+            w2[..., :c] = wc.transpose(0, 2, 3, 1)
+            w2 = np.ascontiguousarray(w2.reshape(cout, kc, 1, 1))
+            kgp, rows = _I64(0), _I64(0)
+            size = self.lib.qa_pack_weights_i8_size(
+                cout, kc, 1, 1, 1, 0, ctypes.byref(kgp), ctypes.byref(rows))
+            wp = np.empty(size, np.int8)
+            corr = np.empty(cout, np.int64)
+            boff = np.empty(cout, np.int32)
+            need = ctypes.c_int32(0)
+            if self.lib.qa_pack_weights_i8(
+                    w2.ctypes.data, cout, kc, 1, 1, 1, int(d.x_add), 0,
+                    wp.ctypes.data, corr.ctypes.data, boff.ctypes.data,
+                    ctypes.byref(need)) != 0:
+                continue
+            dev = [_dev(wp, np.int8), _dev(corr, np.int64),
+                   _dev(boff, np.int32)]
+            self.keep.extend(dev)
+            pix = d.y_sp
+            (d.N, d.C, d.H, d.W, d.KH, d.KW, d.SH, d.SW, d.PH, d.PW, d.DH,
+             d.DW, d.OH, d.OW) = (n * d.OH * d.OW, kc, 1, 1, 1, 1, 1, 1, 0,
+                                  0, 1, 1, 1, 1)
+            d.x_sn, d.x_sc, d.x_sp = kc, 1, 0
+            d.y_sn, d.y_sc, d.y_sp = pix, 1, 0
+            d.w, d.w_layout = dev[0].data_ptr(), 0
+            d.w_kgp, d.w_rows = kgp.value, rows.value
+            d.corr, d.boff = dev[1].data_ptr(), dev[2].data_ptr()
+            d.needs_rowsum = need.value
+            d.tile = 0
+            plan = plan_epilogue(self.lib, d, *host, lut)
+            if plan is None:
+                raise RuntimeError(f"{ln}: no epilogue plan as a 1x1 "
+                                   "convolution")
+            pdev = _dev(plan, np.uint8)
+            self.keep.append(pdev)
+            d.epi_plan = pdev.data_ptr()
+            qname = f"quantize:{name}"
+
+            def fn(s, xf=xf, t=t, n=n, c=c, h=h, w=w, kh=kh, kw=kw, qp=qp):
+                _ok(self.lib.qa_d_quantize_patches(
+                    xf.data_ptr(), n, c, h, w, kh, kw, t.ptr, qp.scale,
+                    qp.zp, qp.qmin, qp.qmax, t.so, s),
+                    "qa_d_quantize_patches")
+
+            self.launches = [(f"patches:{name}", fn) if nm == qname
+                             else (nm, f) for nm, f in self.launches]
+            self.keep.append(t)
+            del self.tensors[name]  # holds the rows, not the image
 
     def _fuse_input_quantization(self, cons):
         """A 4-D graph input read only by a layout-1 (<= 4 channel) int8

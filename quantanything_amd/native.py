@@ -93,6 +93,8 @@ def _declare(lib):
         "qa_d_gap": (i32, [p, i32] + [i64] * 13 + [p, i32, i64, i64, p]),
         "qa_d_quantize_nhwc": (i32, [p, i64, i64, i64, p, i32, i64, f64, i64,
                                      i64, i64, i64, p]),
+        "qa_d_quantize_patches": (i32, [p] + [i64] * 6 + [p, f64] +
+                                  [i64] * 4 + [p]),
         "qa_d_softmax": (i32, [p, i32, i64, i64, f64, i64, i64, p, i32, f64]
                          + [i64] * 4 + [p]),
         "qa_d_softmax_table": (i32, [f64, i64, i64, p, p]),

@@ -303,7 +303,9 @@ def test_wide_kernel_rows_layout(hip, tmp_path, quant_type, cin, cout, k,
                                  stride, pad, size):
     """Convolutions of <= 4 channels with kernels wider than 4 columns use
     the row layout (ceil(KW/4) 16-byte groups per kernel row) and equal the
-    oracle for every tile code."""
+    oracle for every tile code. A patch embedding of the graph input
+    (stride = kernel, no padding) instead reads the input quantized into
+    its im2col rows, as a 1x1 convolution of KH*KW*4 channels."""
     b = G.GraphBuilder(13)
     y = b.conv("images", cin, cout, k, stride, pad=pad,
                w_scale=np.sqrt(1.0 / (cin * k * k)))
@@ -317,7 +319,9 @@ def test_wide_kernel_rows_layout(hip, tmp_path, quant_type, cin, cout, k,
     oracle.run(x, keep=True)
     ex = c.executor({"images": x.shape})
     convs = [t for t in ex.tunables if t[0].startswith("conv:")]
-    assert len(convs) == 1 and convs[0][1].w_layout == 1
+    patch = stride == k and pad == 0 and k % 4 == 0 and size % k == 0
+    assert len(convs) == 1 and convs[0][1].w_layout == (0 if patch else 1)
+    assert ("patches:images" in dict(ex.launches)) == patch
     _, d, codes, _ = convs[0]
     for code in codes:
         d.tile = code
