@@ -62,3 +62,40 @@ def test_patch_input_bit_exact(hip, tmp_path, quant_type, cin, cout, k, h, w,
                 got, oracle.env[name].reshape(got.shape), err_msg=name)
             checked += 1
     assert g.outputs[0] in ex.tensors and checked >= 1
+
+
+@pytest.mark.parametrize("n,c,h,w,kh,kw", [
+    (2, 3, 32, 48, 16, 16), (3, 1, 8, 24, 2, 8), (1, 4, 12, 12, 3, 4)])
+def test_patch_rows_are_the_channels_last_bytes_permuted(hip, n, c, h, w, kh,
+                                                         kw):
+    """qa_d_quantize_patches writes, for row (n, py, px), the 4-byte words
+    qa_d_quantize_nhwc writes for the patch's pixels, kernel row by kernel
+    row; bad geometries are refused with nothing launched."""
+    import torch
+    lib = hip.require()
+    rng = np.random.default_rng(n * 100 + kh)
+    x = (rng.standard_normal((n, c, h, w)) * 3).astype(np.float32)
+    x.flat[:3] = [1e9, -1e9, 0.5]
+    xd = torch.from_numpy(x).cuda()
+    scale, zp, qmin, qmax, so = 0.021, 3, -128, 127, 0
+    cl = torch.zeros(n * h * w * 4, dtype=torch.int8, device="cuda")
+    rows = torch.full((n * h * w * 4,), 77, dtype=torch.int8, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.qa_d_quantize_nhwc(xd.data_ptr(), n, c, h * w, cl.data_ptr(),
+                                  1, 4, scale, zp, qmin, qmax, so, s) == 0
+    assert lib.qa_d_quantize_patches(xd.data_ptr(), n, c, h, w, kh, kw,
+                                     rows.data_ptr(), scale, zp, qmin, qmax,
+                                     so, s) == 0
+    torch.cuda.synchronize()
+    want = cl.cpu().numpy().reshape(n, h // kh, kh, w // kw, kw, 4)
+    want = want.transpose(0, 1, 3, 2, 4, 5).reshape(-1)
+    np.testing.assert_array_equal(rows.cpu().numpy(), want)
+    # refused: kernel width not a multiple of 4, image not a multiple of
+    # the kernel, five channels
+    for args in [(n, c, h, w, kh, 6), (n, c, h + 1, w, kh, kw),
+                 (n, 5, h, w, kh, kw)]:
+        assert lib.qa_d_quantize_patches(xd.data_ptr(), *args,
+                                         rows.data_ptr(), scale, zp, qmin,
+                                         qmax, so, s) == -1
+        assert b"qa_d_quantize_patches" in lib.qa_last_error()
+        lib.qa_clear_error()
