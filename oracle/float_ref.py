@@ -77,11 +77,12 @@ def layer_norm(x, gamma, beta, axis, eps):
     return _f32(y + beta if beta is not None else y)
 
 
-def pool_pads(node, in_hw, kernel, strides, dilations):
-    """``(top, left, bottom, right)`` of a pooling window: ``auto_pad``
-    (SAME_UPPER / SAME_LOWER / VALID) or ``pads`` as the reference resolves
-    them (``float_ops.py:132-146``), then, under ``ceil_mode``, the end pads
-    grown so that the last partial window is included (``:518-531``)."""
+def conv_pads(node, in_hw, kernel, strides, dilations):
+    """``(top, left, bottom, right)`` of a convolution or pooling window:
+    ``auto_pad`` SAME_UPPER / SAME_LOWER (the output is ceil(size / stride)
+    and the padding that needs is split with the odd pixel at the end or at
+    the start), VALID (none) or the ``pads`` attribute
+    (``float_ops.py:132-146``)."""
     auto = node.attr("auto_pad", "NOTSET")
     if auto in ("SAME_UPPER", "SAME_LOWER"):
         lo, hi = [], []
@@ -91,11 +92,17 @@ def pool_pads(node, in_hw, kernel, strides, dilations):
             small, big = total // 2, total - total // 2
             lo.append(small if auto == "SAME_UPPER" else big)
             hi.append(big if auto == "SAME_UPPER" else small)
-        pads = [lo[0], lo[1], hi[0], hi[1]]
-    elif auto == "VALID":
-        pads = [0, 0, 0, 0]
-    else:
-        pads = list(node.attr("pads", [0, 0, 0, 0]))
+        return (lo[0], lo[1], hi[0], hi[1])
+    if auto == "VALID":
+        return (0, 0, 0, 0)
+    p = node.attr("pads", [0, 0, 0, 0])
+    return (p[0], p[1], p[2], p[3])
+
+
+def pool_pads(node, in_hw, kernel, strides, dilations):
+    """:func:`conv_pads`, then, under ``ceil_mode``, the end pads grown so
+    that the last partial window is included (``float_ops.py:518-531``)."""
+    pads = list(conv_pads(node, in_hw, kernel, strides, dilations))
     if node.attr("ceil_mode", 0):
         for ax in range(2):
             size = in_hw[ax] + pads[ax] + pads[ax + 2]
@@ -103,6 +110,21 @@ def pool_pads(node, in_hw, kernel, strides, dilations):
             out = -(-(size - ek) // strides[ax]) + 1
             pads[ax + 2] += max((out - 1) * strides[ax] + ek - size, 0)
     return tuple(pads)
+
+
+def _ints(args, index, node, attr, default=None):
+    """An integer list from input ``index`` when given (opset >= 10 / 13
+    form), else from attribute ``attr`` (``float_ops.py:125-129``)."""
+    if len(args) > index and args[index] is not None:
+        return np.asarray(args[index]).astype(np.int64).reshape(-1).tolist()
+    return node.attr(attr, default)
+
+
+# ONNX TensorProto element types of Cast's "to" and their NumPy types, as
+# onnx.helper.tensor_dtype_to_np_dtype maps them (float_ops.py:398-402)
+CAST_TYPES = {1: np.float32, 2: np.uint8, 3: np.int8, 4: np.uint16,
+              5: np.int16, 6: np.int32, 7: np.int64, 9: np.bool_,
+              10: np.float16, 11: np.float64}
 
 
 def eval_node(node, args, opset=13, pad_value=None):
@@ -150,8 +172,19 @@ def eval_node(node, args, opset=13, pad_value=None):
         shape = tuple(int(v) for v in np.asarray(args[1]).reshape(-1))
         return [np.broadcast_to(args[0], np.broadcast_shapes(
             args[0].shape, shape)).copy()]
-    if op == "Cast" and node.attr("to") == 1:  # float_ops.py:398-403
-        return [args[0].astype(np.float32)]
+    if op == "Cast":  # float_ops.py:398-402
+        return [args[0].astype(CAST_TYPES[node.attr("to")])]
+    if op == "Slice":  # float_ops.py:469-481: NumPy slicing, 2^62 = open
+        x = args[0]
+        starts = _ints(args, 1, node, "starts")
+        ends = _ints(args, 2, node, "ends")
+        axes = _ints(args, 3, node, "axes", list(range(len(starts))))
+        steps = _ints(args, 4, node, "steps", [1] * len(starts))
+        index = [slice(None)] * x.ndim
+        for b, e, a, st in zip(starts, ends, axes, steps):
+            index[a + x.ndim if a < 0 else a] = slice(
+                None if b >= 2**62 else b, None if abs(e) >= 2**62 else e, st)
+        return [x[tuple(index)]]
     if op == "AveragePool":  # float_ops.py:563-577
         x = args[0].astype(np.float32)
         k = tuple(node.attr("kernel_shape"))
@@ -223,15 +256,21 @@ def eval_node(node, args, opset=13, pad_value=None):
     if op == "GlobalAveragePool":
         x = args[0]
         return [_f32(x.mean(axis=tuple(range(2, x.ndim)), keepdims=True))]
-    if op == "Pad":
+    if op == "Pad":  # float_ops.py:499-513
         x = args[0]
-        pads = (np.asarray(args[1]).astype(np.int64).tolist()
-                if len(args) > 1 and args[1] is not None
-                else node.attr("pads"))
-        value = pad_value if pad_value is not None else node.attr("value", 0)
+        pads = _ints(args, 1, node, "pads")
+        value = pad_value
+        if value is None:
+            value = (np.asarray(args[2]).reshape(()).item()
+                     if len(args) > 2 and args[2] is not None
+                     else node.attr("value", 0))
         n = x.ndim
-        return [np.pad(x, [(pads[i], pads[i + n]) for i in range(n)],
-                       constant_values=value)]
+        width = [(pads[i], pads[i + n]) for i in range(n)]
+        mode = node.attr("mode", "constant")
+        if mode == "constant":
+            return [np.pad(x, width, constant_values=value)]
+        return [np.pad(x, width, mode={"reflect": "reflect",
+                                       "edge": "edge"}[mode])]
     if op == "MaxPool":
         # float_ops.py:518-560: pads from auto_pad / pads, the end pads
         # grown under ceil_mode, then the max over dilated windows

@@ -27,7 +27,7 @@ import json
 import numpy as np
 
 from oracle import abi
-from oracle.float_ref import UNARY, eval_node
+from oracle.float_ref import UNARY, conv_pads, eval_node
 
 INT32 = (-(2**31), 2**31 - 1)
 
@@ -128,8 +128,18 @@ class OraclePipeline:
         if op == "GlobalAveragePool":
             return "gap"
         if op in ("Reshape", "Flatten", "Squeeze", "Unsqueeze", "Transpose",
-                  "Split", "Slice", "Pad", "MaxPool", "GlobalMaxPool"):
-            return "shape"
+                  "Split", "Slice", "Pad", "MaxPool", "GlobalMaxPool") and \
+                all(const(i) for i in node.inputs[1:] if i):
+            # ShapingQuantize.supports (quant_layers.py:617-633): a Pad is
+            # scale-preserving only in constant mode with a zero pad value
+            if op != "Pad":
+                return "shape"
+            if node.attr("mode", "constant") == "constant":
+                value = (g.initializers[node.inputs[2]]
+                         if len(node.inputs) > 2 and node.inputs[2]
+                         else node.attr("value", 0))
+                if float(np.asarray(value)) == 0.0:
+                    return "shape"
         return "fallback"
 
     def _data_inputs(self, node, kind):
@@ -242,11 +252,8 @@ class OraclePipeline:
             x = args[0]
             zp = st["in_qp"][0][1]
             w = st["wc"]
-            strides = tuple(node.attr("strides", [1, 1]))
-            dil = tuple(node.attr("dilations", [1, 1]))
-            p = node.attr("pads", [0, 0, 0, 0])
-            acc = L.conv2d_int(x.astype(np.int64) - zp, w, strides,
-                               (p[0], p[1], p[2], p[3]), dil,
+            strides, p, dil = self._conv_geometry(node, x, w)
+            acc = L.conv2d_int(x.astype(np.int64) - zp, w, strides, p, dil,
                                node.attr("group", 1), st["wide"])
             n, co, oh, ow = acc.shape
             o = st["out_qp"][0]
@@ -325,7 +332,32 @@ class OraclePipeline:
             else:
                 full.append(self.g.initializers[n])
         outs = eval_node(node, full, self.g.opset)
-        return [L.quantize_f32(y, *q) for y, q in zip(outs, st["out_qp"])]
+        return [self._quantize(y, q) for y, q in zip(outs, st["out_qp"])]
+
+    def _quantize(self, y, qp):
+        """``utils.quantize`` (utils.py:97-114) of a fallback output: float32
+        and float64 values through the float32 ABI entry (the wrapper casts
+        them to float32 first), values of any other type (the integer, bool
+        and float16 results of a Cast) divided in float64 and rounded half
+        to even."""
+        s, z, lo, hi = qp
+        y = np.asarray(y)
+        if s == 0:
+            return np.full(y.shape, z, np.int32)
+        if y.dtype in (np.float32, np.float64):
+            return self.lib.quantize_f32(y, s, z, lo, hi)
+        q = np.round(y.astype(np.float64) / s) + z
+        return np.clip(q, lo, hi).astype(np.int32)
+
+    @staticmethod
+    def _conv_geometry(node, x, w):
+        """Strides, ``(top, left, bottom, right)`` pads with ``auto_pad``
+        resolved (``quant_layers.py:302-309`` through ``float_ops.py:132-146``)
+        and dilations of a convolution."""
+        strides = tuple(node.attr("strides", [1, 1]))
+        dil = tuple(node.attr("dilations", [1, 1]))
+        return strides, conv_pads(node, x.shape[2:], w.shape[2:], strides,
+                                  dil), dil
 
     def run(self, x, keep=False, overrides=None):
         """Returns ``{output name: int32 quantized array}`` and the
@@ -381,10 +413,8 @@ class OraclePipeline:
         xs = [self._fq(a, q) for a, q in zip(args, st["in_qp"])]
         if kind == "conv":
             x = xs[0]
-            strides = tuple(node.attr("strides", [1, 1]))
-            dil = tuple(node.attr("dilations", [1, 1]))
-            p = node.attr("pads", [0, 0, 0, 0])
-            y = self.lib.conv2d_f32(x, st["fake_w"], strides, tuple(p), dil,
+            strides, p, dil = self._conv_geometry(node, x, st["fake_w"])
+            y = self.lib.conv2d_f32(x, st["fake_w"], strides, p, dil,
                                     node.attr("group", 1))
             if st["fake_b"] is not None:
                 y = y + st["fake_b"].reshape(1, -1, 1, 1)

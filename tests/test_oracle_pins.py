@@ -1,0 +1,651 @@
+"""Pins of the oracle functions that no golden vector of the compiled
+reference covers: convolution padding from ``auto_pad``, the generic float
+fallbacks (AveragePool, ReduceMean, LogSoftmax, Pow, Div / Max / Min with
+broadcasting, Expand, Cast, Slice, Pad in every mode), the
+Abramowitz-Stegun ``erf`` and the erf Gelu, the lookup tables of Tanh, Elu,
+LeakyRelu, HardSigmoid, Softplus, Exp and Sqrt, and the fake-quantized pass.
+
+Every check is fixed by the mathematics or by hand-worked answers, not by
+retyping the oracle's formula: brute-force loops over tiny inputs, exact
+rational or decimal evaluation, closed forms (log-softmax of [0, ln 2]),
+symmetries (Tanh is odd) and saturated regions. The mistakes each group
+fails on are named in its docstring."""
+
+import decimal
+import math
+from decimal import Decimal
+from fractions import Fraction
+from itertools import product
+
+import numpy as np
+import pytest
+
+from oracle.float_ref import conv_pads, eval_node
+from oracle.pipeline import OraclePipeline, quant_type_info
+from quantanything_amd.graph import Graph, Node
+
+decimal.getcontext().prec = 60
+
+
+def _node(op, inputs=("a", "b", "c", "d", "e"), **attrs):
+    return Node("n", op, list(inputs), ["y"], attrs)
+
+
+def _qj(quant_type, qp, per_channel=True):
+    return {"quant_type": quant_type, "per_channel": per_channel,
+            "qparams": {k: dict(scale=s, zp=z, qmin=lo, qmax=hi)
+                        for k, (s, z, lo, hi) in qp.items()}}
+
+
+# ---------------------------------------------------- convolution pads --
+# (input size, kernel, stride, dilation) -> (SAME_UPPER head, tail),
+# worked by hand from the ONNX definition: the output has ceil(size /
+# stride) positions, the padding is whatever that needs, and its odd pixel
+# goes to the end (SAME_UPPER) or to the start (SAME_LOWER)
+SAME_KATS = [
+    ((5, 3, 2, 1), (1, 1)),   # 3 outputs: taps -1..5 -> 1 + 1
+    ((6, 3, 2, 1), (0, 1)),   # 3 outputs: taps 0..6 -> 0 + 1
+    ((4, 2, 1, 1), (0, 1)),   # 4 outputs of a 2-tap kernel
+    ((5, 3, 1, 2), (2, 2)),   # dilated 3-tap kernel spans 5
+    ((7, 1, 2, 1), (0, 0)),   # 1x1 stride 2: 4 outputs, no padding
+    ((8, 4, 3, 1), (1, 1)),   # 3 outputs: taps -1..8 -> 1 + 1
+    ((9, 4, 3, 1), (0, 1)),   # 3 outputs: taps 0..9 -> 0 + 1
+    ((10, 4, 3, 1), (1, 2)),  # 4 outputs: taps -1..11 -> 1 + 2
+]
+
+
+@pytest.mark.parametrize("geom, upper", SAME_KATS)
+def test_conv_pads_same_known_answers(geom, upper):
+    """SAME_UPPER puts the odd pixel at the end, SAME_LOWER at the start;
+    swapping them, or sizing the output as floor(size / stride), fails."""
+    size, k, s, d = geom
+    for auto, (head, tail) in (("SAME_UPPER", upper),
+                               ("SAME_LOWER", upper[::-1])):
+        node = _node("Conv", auto_pad=auto, pads=[9, 9, 9, 9])
+        p = conv_pads(node, (size, size + 1), (k, 1), (s, 1), (d, 1))
+        assert (p[0], p[2]) == (head, tail), (auto, geom)
+        assert (p[1], p[3]) == (0, 0)  # 1-tap stride-1 axis: no padding
+        out = (size + head + tail - d * (k - 1) - 1) // s + 1
+        assert out == -(-size // s)
+
+
+def test_conv_pads_valid_and_explicit():
+    assert conv_pads(_node("Conv", auto_pad="VALID", pads=[1, 2, 3, 4]),
+                     (5, 5), (3, 3), (1, 1), (1, 1)) == (0, 0, 0, 0)
+    assert conv_pads(_node("Conv", pads=[1, 2, 3, 4]), (5, 5), (3, 3),
+                     (1, 1), (1, 1)) == (1, 2, 3, 4)
+    assert conv_pads(_node("Conv"), (5, 5), (3, 3), (1, 1),
+                     (1, 1)) == (0, 0, 0, 0)
+
+
+def _direct_conv(x, w, stride, pads, zp):
+    """Python-integer convolution of a [1, C, H, W] input padded with zp,
+    window (oy * s - top + ky, ox * s - left + kx)."""
+    _, c, h, wd = x.shape
+    co, _, kh, kw = w.shape
+    t, l, b, r = pads
+    oh = (h + t + b - kh) // stride + 1
+    ow = (wd + l + r - kw) // stride + 1
+    y = np.zeros((1, co, oh, ow), np.int64)
+    for o, oy, ox in product(range(co), range(oh), range(ow)):
+        acc = 0
+        for ci, ky, kx in product(range(c), range(kh), range(kw)):
+            iy, ix = oy * stride - t + ky, ox * stride - l + kx
+            v = int(x[0, ci, iy, ix]) if 0 <= iy < h and 0 <= ix < wd \
+                else zp
+            acc += (v - zp) * int(w[o, ci, ky, kx])
+        y[0, o, oy, ox] = acc
+    return y
+
+
+@pytest.mark.parametrize("auto, stride, hw, pads", [
+    ("SAME_UPPER", 2, (6, 7), (0, 1, 1, 1)),
+    ("SAME_LOWER", 2, (6, 7), (1, 1, 0, 1)),
+    ("SAME_UPPER", 1, (5, 4), (1, 1, 1, 1)),
+    ("VALID", 2, (7, 6), (0, 0, 0, 0)),
+])
+def test_pipeline_conv_resolves_auto_pad(auto, stride, hw, pads):
+    """The oracle's integer convolution with ``auto_pad`` equals a direct
+    convolution at the hand-worked pads (an oracle that reads only
+    ``pads`` computes another shape); the fake-quantized convolution uses
+    the same geometry."""
+    rng = np.random.default_rng(3)
+    w = (rng.integers(-127, 128, size=(2, 3, 3, 3)) / 64.0).astype(np.float32)
+    w[:, 0, 0, 0] = 127 / 64.0  # per-channel scale exactly 1/64
+    node = Node("conv", "Conv", ["x", "w"], ["y"],
+                dict(auto_pad=auto, strides=[stride, stride],
+                     kernel_shape=[3, 3], pads=[3, 3, 3, 3]))
+    g = Graph([node], {"w": w}, {"x": [1, 3, *hw]}, ["y"])
+    # int8: symmetric weights (scale max|w| / 127 = 1/64); an input zero
+    # point of 9 so that padding must be the zero point, not 0
+    qj = _qj("int8", {"x": (0.25, 9, -128, 127), "y": (1.0, -20, -128, 127)})
+    pipe = OraclePipeline(g, qj)
+    q = rng.integers(-128, 128, size=(1, 3, *hw)).astype(np.int32)
+    ints, _ = pipe.run_integers({"x": q})
+    wq = np.round(w * 64).astype(np.int64)
+    acc = _direct_conv(q, wq, stride, pads, 9)
+    # y = acc * (0.25 / 64) / 1.0: an exact power of two, rounded half up
+    # by the fixed-point multiply (2^-8 * acc + 1/2, floored)
+    want = np.clip(np.floor(acc / 256.0 + 0.5) - 20, -128, 127)
+    np.testing.assert_array_equal(ints["y"], want)
+    fake = pipe.run_fake({"x": ((q - 9) * 0.25).astype(np.float32)})
+    assert fake["y"].shape == want.shape
+
+
+# -------------------------------------------------------- AveragePool --
+def _avgpool_brute(x, k, s, pads, include_pad):
+    n, c, h, w = x.shape
+    t, l, b, r = pads
+    oh = (h + t + b - k[0]) // s[0] + 1
+    ow = (w + l + r - k[1]) // s[1] + 1
+    y = np.zeros((n, c, oh, ow))
+    for i, j, oy, ox in product(range(n), range(c), range(oh), range(ow)):
+        tot, cnt = 0.0, 0
+        for ky, kx in product(range(k[0]), range(k[1])):
+            iy, ix = oy * s[0] - t + ky, ox * s[1] - l + kx
+            if 0 <= iy < h and 0 <= ix < w:
+                tot += float(x[i, j, iy, ix])
+                cnt += 1
+        y[i, j, oy, ox] = tot / (k[0] * k[1] if include_pad else cnt)
+    return y
+
+
+@pytest.mark.parametrize("attrs, pads", [
+    (dict(kernel_shape=[3, 3], strides=[1, 1], pads=[1, 1, 1, 1]),
+     (1, 1, 1, 1)),
+    (dict(kernel_shape=[3, 3], strides=[2, 2], pads=[1, 0, 1, 0]),
+     (1, 0, 1, 0)),
+    # ceil mode: 5 + 0 - 3 = 2 -> ceil(2 / 2) + 1 = 2 rows, no growth;
+    # width 6 - 3 = 3 -> ceil(3 / 2) + 1 = 3 columns, one extra end pixel
+    (dict(kernel_shape=[3, 3], strides=[2, 2], ceil_mode=1), (0, 0, 0, 1)),
+    (dict(kernel_shape=[2, 2], strides=[2, 2], auto_pad="SAME_UPPER"),
+     (0, 0, 1, 0)),
+    (dict(kernel_shape=[2, 3], strides=[1, 2], pads=[1, 1, 0, 1]),
+     (1, 1, 0, 1)),
+])
+@pytest.mark.parametrize("include_pad", [0, 1])
+def test_average_pool_brute_force(attrs, pads, include_pad):
+    """Window means with the padding excluded from the count, or counted
+    (count_include_pad = 1 divides by the window size); an inverted flag or
+    a window anchored at the wrong corner fails."""
+    x = np.random.default_rng(4).integers(-8, 9, size=(2, 2, 5, 6)).astype(
+        np.float32)
+    y = eval_node(_node("AveragePool", count_include_pad=include_pad,
+                        **attrs), [x])[0]
+    want = _avgpool_brute(x, attrs["kernel_shape"], attrs["strides"], pads,
+                          include_pad)
+    assert y.dtype == np.float32 and y.shape == want.shape
+    np.testing.assert_allclose(y, want, rtol=2**-23)
+
+
+def test_average_pool_of_a_constant_image():
+    """Padding excluded: every window mean of a constant image is the
+    constant; included: the border windows are scaled by their count."""
+    x = np.full((1, 1, 4, 4), 6.0, np.float32)
+    a = dict(kernel_shape=[3, 3], strides=[1, 1], pads=[1, 1, 1, 1])
+    np.testing.assert_array_equal(
+        eval_node(_node("AveragePool", **a), [x])[0], 6.0)
+    y = eval_node(_node("AveragePool", count_include_pad=1, **a), [x])[0]
+    assert y[0, 0, 0, 0] == np.float32(6.0 * 4 / 9)  # corner: 4 of 9 taps
+    assert y[0, 0, 1, 1] == 6.0
+
+
+# ---------------------------------------------------------- ReduceMean --
+@pytest.mark.parametrize("axes, keepdims", [
+    (None, 1), (None, 0), ([1], 1), ([-1], 0), ([0, -2], 1), ([2, 0], 0)])
+def test_reduce_mean_exact(axes, keepdims):
+    """Means of small integers against exact fractions; axes None reduces
+    every axis, negative axes count from the end, keepdims keeps 1s. A wrong
+    default for keepdims (it is 1) or axes (all) fails the shape check."""
+    x = np.random.default_rng(5).integers(-9, 10, size=(2, 3, 4)).astype(
+        np.float32)
+    args = [x] if axes is None else [x, np.array(axes, np.int64)]
+    attrs = {} if keepdims == 1 else dict(keepdims=0)
+    y = eval_node(_node("ReduceMean", **attrs), args)[0]
+    red = tuple(range(3)) if axes is None else \
+        tuple(sorted(a % 3 for a in axes))
+    keep = [d for d in range(3) if d not in red]
+    shape = tuple(1 if d in red else x.shape[d] for d in range(3)) \
+        if keepdims else tuple(x.shape[d] for d in keep)
+    assert y.shape == shape and y.dtype == np.float32
+    flat = y.reshape(-1)
+    for j, idx in enumerate(product(*[range(x.shape[d]) for d in keep])):
+        vals = []
+        for r in product(*[range(x.shape[d]) for d in red]):
+            full = [0, 0, 0]
+            for d, v in zip(keep, idx):
+                full[d] = v
+            for d, v in zip(red, r):
+                full[d] = v
+            vals.append(Fraction(int(x[tuple(full)])))
+        exact = sum(vals) / len(vals)
+        assert flat[j] == np.float32(float(exact))
+    # attribute form (opset < 18) selects the same axes
+    if axes is not None:
+        z = eval_node(_node("ReduceMean", axes=axes, **attrs), [x])[0]
+        np.testing.assert_array_equal(z, y)
+
+
+# ---------------------------------------------------------- LogSoftmax --
+def test_log_softmax_closed_form_and_default_axis():
+    """log-softmax of [0, ln 2] is [ln 1/3, ln 2/3]; every row's exponentials
+    sum to 1; the default axis is the last from opset 13 and axis 1 before."""
+    y = eval_node(_node("LogSoftmax", axis=1),
+                  [np.array([[0.0, np.log(2.0)]], np.float32)])[0]
+    np.testing.assert_allclose(y, [[np.log(1 / 3), np.log(2 / 3)]],
+                               rtol=1e-7)
+    x = np.random.default_rng(6).normal(size=(2, 3, 4)).astype(np.float32)
+    last = eval_node(_node("LogSoftmax"), [x], opset=13)[0]
+    np.testing.assert_allclose(np.exp(last.astype(np.float64)).sum(-1), 1.0,
+                               rtol=1e-6)
+    first = eval_node(_node("LogSoftmax"), [x], opset=11)[0]
+    np.testing.assert_allclose(np.exp(first.astype(np.float64)).sum(1), 1.0,
+                               rtol=1e-6)
+    # shift invariance along the reduced axis only
+    np.testing.assert_allclose(
+        eval_node(_node("LogSoftmax"), [x + np.float32(2.5)], opset=13)[0],
+        last, atol=2e-6)
+
+
+# -------------------------------------- Pow / Div / Max / Min / Expand --
+def test_pow_integer_exponents_by_repeated_multiplication():
+    """x^2 and x^3 of negative and positive bases equal repeated products
+    (exact here); a broadcast exponent row applies per column."""
+    x = np.array([[-2.0, -1.5, 0.0, 1.5, 3.0]], np.float32)
+    for e in (2.0, 3.0):
+        y = eval_node(_node("Pow"), [x, np.float32(e)])[0]
+        want = x * x if e == 2.0 else x * x * x
+        np.testing.assert_array_equal(y, want)
+    e = np.array([0.0, 1.0, 2.0, 3.0, 0.5], np.float32)
+    y = eval_node(_node("Pow"), [x, e])[0]
+    np.testing.assert_array_equal(
+        y, [[1.0, -1.5, 0.0, 1.5 ** 3, np.float32(np.sqrt(3.0))]])
+
+
+@pytest.mark.parametrize("op, fn", [
+    ("Div", lambda a, b: np.float32(a) / np.float32(b)),
+    ("Max", max), ("Min", min)])
+@pytest.mark.parametrize("sa, sb", [
+    ((2, 3, 4), (4,)), ((2, 1, 4), (3, 1)), ((1,), (2, 3, 1)),
+    ((3, 1), (1, 4))])
+def test_binary_broadcasting_brute_force(op, fn, sa, sb):
+    """NumPy broadcasting by explicit index arithmetic: axes right-aligned,
+    size-1 axes repeated. A transposed operand or left alignment fails."""
+    rng = np.random.default_rng(7)
+    a = rng.integers(-9, 10, size=sa).astype(np.float32)
+    b = rng.integers(1, 10, size=sb).astype(np.float32)
+    b *= np.where(rng.random(size=sb) < 0.5, -1, 1).astype(np.float32)
+    y = eval_node(_node(op), [a, b])[0]
+    nd = max(len(sa), len(sb))
+    pa, pb = (1,) * (nd - len(sa)) + sa, (1,) * (nd - len(sb)) + sb
+    out = tuple(max(u, v) for u, v in zip(pa, pb))
+    assert y.shape == out
+    ar, br = a.reshape(pa), b.reshape(pb)
+    for idx in product(*[range(n) for n in out]):
+        ia = tuple(i if n > 1 else 0 for i, n in zip(idx, pa))
+        ib = tuple(i if n > 1 else 0 for i, n in zip(idx, pb))
+        assert y[idx] == fn(ar[ia], br[ib]), idx
+
+
+def test_expand_shape_rule_and_values():
+    """Expand broadcasts the input against the shape operand both ways
+    (a 1 in the shape keeps the input's extent)."""
+    x = np.arange(3, dtype=np.float32).reshape(3, 1)
+    y = eval_node(_node("Expand"), [x, np.array([2, 1, 4], np.int64)])[0]
+    assert y.shape == (2, 3, 4)
+    for i, j, k in product(range(2), range(3), range(4)):
+        assert y[i, j, k] == j
+    z = eval_node(_node("Expand"), [x, np.array([1], np.int64)])[0]
+    np.testing.assert_array_equal(z, x)
+
+
+# ----------------------------------------------------------------- Cast --
+def test_cast_truncates_wraps_and_rounds():
+    """Float to integer truncates toward zero and wraps to the width; bool
+    is "non-zero"; float16 rounds to nearest even; float64 is exact."""
+    x = np.array([-3.7, 3.7, 200.5, -129.9, 0.0, 0.5], np.float32)
+    cast = lambda to: eval_node(_node("Cast", to=to), [x])[0]  # noqa: E731
+    np.testing.assert_array_equal(cast(6), [-3, 3, 200, -129, 0, 0])
+    assert cast(6).dtype == np.int32 and cast(7).dtype == np.int64
+    np.testing.assert_array_equal(cast(3), [-3, 3, 200 - 256, 127, 0, 0])
+    np.testing.assert_array_equal(cast(2), [253, 3, 200, 127, 0, 0])
+    np.testing.assert_array_equal(cast(9), [1, 1, 1, 1, 0, 1])
+    assert cast(10)[1] == np.float16(3.69921875)  # 3.7 -> nearest half
+    np.testing.assert_array_equal(cast(11), x.astype(np.float64))
+    np.testing.assert_array_equal(cast(1), x)
+
+
+# ---------------------------------------------------------------- Slice --
+@pytest.mark.parametrize("starts, ends, axes, steps, want", [
+    ([1], [3], [0], [1], lambda x: x[1:3]),
+    ([-1], [-(2**63)], [0], [-1], lambda x: x[::-1]),   # full reversal
+    ([4], [0], [0], [-2], lambda x: x[4:0:-2]),
+    ([2**62], [1], [1], [-1], lambda x: x[:, :1:-1]),   # open start
+    ([-100], [100], [-1], [2], lambda x: x[:, :, ::2]),  # clamped
+    ([1, 5], [2**62, -8], [2, 1], [1, -3], lambda x: x[:, 5:-8:-3, 1:]),
+])
+def test_slice_follows_python_slicing(starts, ends, axes, steps, want):
+    """Start / end / step as Python slices: negative indices count from the
+    end, out-of-range bounds clamp, 2^62 and beyond mean an open end, and a
+    negative step walks backwards (x[4:0:-2] takes 4 and 2)."""
+    x = np.arange(6 * 7 * 5).reshape(6, 7, 5)
+    args = [x, np.array(starts), np.array(ends), np.array(axes),
+            np.array(steps)]
+    y = eval_node(_node("Slice"), args)[0]
+    np.testing.assert_array_equal(y, want(x))
+    if starts == [4]:
+        np.testing.assert_array_equal(y[:, 0, 0], [4 * 35, 2 * 35])
+    # attribute form (opset < 10): axes default to 0..n-1, steps to 1
+    if steps == [1] * len(steps) and axes == list(range(len(axes))):
+        z = eval_node(_node("Slice", ["a"], starts=starts, ends=ends), [x])[0]
+        np.testing.assert_array_equal(z, y)
+
+
+# ------------------------------------------------------------------ Pad --
+def _pad_brute(x, lo, hi, mode, value):
+    out = tuple(n + a + b for n, a, b in zip(x.shape, lo, hi))
+    y = np.zeros(out, x.dtype)
+    for idx in product(*[range(n) for n in out]):
+        src, inside = [], True
+        for i, a, n in zip(idx, lo, x.shape):
+            j = i - a
+            if mode == "edge":
+                j = min(max(j, 0), n - 1)
+            elif mode == "reflect":
+                while j < 0 or j >= n:  # mirror at the end pixels
+                    j = -j if j < 0 else 2 * (n - 1) - j
+            inside &= 0 <= j < n
+            src.append(j)
+        y[idx] = x[tuple(src)] if inside else value
+    return y
+
+
+@pytest.mark.parametrize("mode", ["constant", "reflect", "edge"])
+def test_pad_modes_brute_force(mode):
+    """Constant padding with the value input (not the attribute), reflect
+    mirrors without repeating the edge (also past one period), edge repeats
+    the border."""
+    x = np.arange(2 * 3 * 4, dtype=np.float32).reshape(2, 3, 4) - 7
+    pads = np.array([0, 2, 5, 1, 1, 3], np.int64)  # begins, then ends
+    args = [x, pads, np.float32(0.5)]
+    y = eval_node(_node("Pad", mode=mode, value=9.0), args)[0]
+    want = _pad_brute(x, pads[:3], pads[3:], mode, 0.5)
+    np.testing.assert_array_equal(y, want)
+    if mode == "reflect":
+        # 1-D hand-worked: [a b c] padded by 3 each side
+        z = eval_node(_node("Pad", mode="reflect"),
+                      [np.array([1.0, 2.0, 3.0], np.float32),
+                       np.array([3, 3], np.int64)])[0]
+        np.testing.assert_array_equal(z, [2, 3, 2, 1, 2, 3, 2, 1, 2])
+    # the attribute value when no value input is given (opset < 11)
+    if mode == "constant":
+        z = eval_node(_node("Pad", ["a"], pads=pads.tolist(), value=9.0),
+                      [x])[0]
+        assert z[0, 0, 0] == 9.0
+
+
+def test_pipeline_pad_role_follows_shaping_rule():
+    """Only a constant-mode Pad with a zero value keeps its input's
+    parameters (padding with the zero point); reflect / edge and a non-zero
+    value are float fallbacks with their own output parameters."""
+    for attrs, value, kind in [({}, 0.0, "shape"),
+                               (dict(mode="reflect"), 0.0, "fallback"),
+                               (dict(mode="edge"), 0.0, "fallback"),
+                               ({}, 0.25, "fallback")]:
+        node = Node("p", "Pad", ["x", "pads", "v"], ["y"], attrs)
+        g = Graph([node], {"pads": np.array([0, 0, 1, 1, 0, 0, 1, 1],
+                                            np.int64),
+                           "v": np.float32(value)}, {"x": [1, 1, 2, 2]},
+                  ["y"])
+        qj = _qj("int8", {"x": (0.5, 0, -128, 127), "y": (0.25, 0, -128, 127),
+                          "pads": (1.0, 0, -128, 127),
+                          "v": (1.0, 0, -128, 127)})
+        (st,) = OraclePipeline(g, qj).plan
+        assert st["kind"] == kind
+        q = np.array([[[[1, -2], [3, 4]]]], np.int32)
+        ints, _ = OraclePipeline(g, qj).run_integers({"x": q})
+        if kind == "shape":  # values unchanged, zero point around
+            assert ints["y"][0, 0, 0, 0] == 0 and ints["y"][0, 0, 1, 1] == 1
+        elif value:  # 0.25 / 0.25 = 1 around; 0.5 q / 0.25 = 2 q inside
+            assert ints["y"][0, 0, 0, 0] == 1 and ints["y"][0, 0, 1, 1] == 2
+        else:  # reflect / edge of 2 q
+            assert ints["y"][0, 0, 1, 2] == -4 and \
+                ints["y"][0, 0, 2, 2] == 8
+
+
+# -------------------------------------------------------- erf and Gelu --
+def test_erf_within_abramowitz_stegun_bound():
+    """7.1.26 approximates erf within 1.5e-7 everywhere; erf is odd and
+    erf(0) = 0 (a sign dropped for negative inputs fails)."""
+    x = np.concatenate([np.linspace(-6, 6, 4001), [0.0, 1e-9, -1e-9]])
+    y = eval_node(_node("Erf"), [x.astype(np.float32)])[0].astype(np.float64)
+    exact = np.array([math.erf(float(np.float32(v))) for v in x])
+    assert np.max(np.abs(y - exact)) < 1.5e-7 + 2**-24
+    assert eval_node(_node("Erf"), [np.float32([0.0])])[0][0] == 0.0
+
+
+def test_erf_gelu_against_math_erf():
+    """Gelu(x) = x/2 (1 + erf(x / sqrt 2)) within the 7.1.26 bound; Gelu(0)
+    = 0, Gelu(x) -> x for large x and -> 0 for very negative x."""
+    x = np.linspace(-8, 8, 3201).astype(np.float32)
+    y = eval_node(_node("Gelu"), [x])[0].astype(np.float64)
+    xd = x.astype(np.float64)
+    exact = 0.5 * xd * (1 + np.array([math.erf(v / math.sqrt(2))
+                                      for v in xd]))
+    tol = 0.5 * np.abs(xd) * 1.5e-7 + np.abs(exact) * 2**-23 + 1e-12
+    assert np.all(np.abs(y - exact) <= tol)
+    assert y[1600] == 0.0 and y[-1] == np.float32(8.0) and abs(y[0]) < 1e-12
+
+
+# -------------------------------------------------- activation tables --
+def _one_ulp(v):
+    return np.spacing(np.float32(abs(v)))
+
+
+def _table(op, attrs, quant_type, inp, out):
+    node = Node("act", op, ["x"], ["y"], attrs)
+    g = Graph([node], {}, {"x": [1, 1, 4, 4]}, ["y"])
+    lo, hi = quant_type_info(quant_type)[2:]
+    qj = _qj(quant_type, {"x": (inp[0], inp[1], lo, hi),
+                          "y": (out[0], out[1], lo, hi)})
+    (st,) = OraclePipeline(g, qj).plan
+    assert st["kind"] == "lut" and st["offset"] == lo
+    return st["table"].astype(np.int64), lo, hi
+
+
+def _nearest_f32(v):
+    """The float32 nearest to the Decimal v, or None within 2^-40
+    (relative) of a midpoint between two float32 values."""
+    f = np.float32(float(v))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f,
+             np.nextafter(f, np.float32(np.inf))]
+    for a, b in zip(cands, cands[1:]):
+        mid = (Decimal(float(a)) + Decimal(float(b))) / 2
+        if abs(v - mid) <= Decimal(2) ** -40 * abs(v):
+            return None
+    return min(cands, key=lambda c: abs(Decimal(float(c)) - v))
+
+
+def _quantized_if_stable(y, ulps, s, z, lo, hi):
+    """round_half_even(f / s) + z clipped for every float32 f within
+    ``ulps`` units in the last place of the exact value y (a Decimal), or
+    None when they disagree (near a rounding tie); ``ulps`` = 0: f is the
+    correctly rounded float32 of y (None near a float32 midpoint)."""
+    if ulps == 0:
+        f = _nearest_f32(y)
+        if f is None:
+            return None
+        t = Decimal(float(f)) / Decimal(s)
+        frac = t - t.to_integral_value(rounding=decimal.ROUND_FLOOR)
+        if abs(frac - Decimal("0.5")) <= Decimal(2) ** -40 * max(abs(t), 1):
+            return None
+        q = int(t.to_integral_value(rounding=decimal.ROUND_HALF_EVEN)) + z
+        return min(max(q, lo), hi)
+    f = np.float32(float(y))
+    cands = [f]
+    for _ in range(ulps + 1):
+        cands.append(np.nextafter(cands[-1], np.float32(np.inf)))
+    g = f
+    for _ in range(ulps + 1):
+        g = np.nextafter(g, np.float32(-np.inf))
+        cands.append(g)
+    qs = set()
+    for c in cands:
+        t = Decimal(float(c)) / Decimal(s)
+        q = int(t.to_integral_value(rounding=decimal.ROUND_HALF_EVEN)) + z
+        qs.add(min(max(q, lo), hi))
+    return qs.pop() if len(qs) == 1 else None
+
+
+def _f32d(v):
+    return Decimal(float(np.float32(v)))
+
+
+def _exp(x):
+    return x.exp()
+
+
+TABLE_CASES = [
+    # op, attrs, exact f on the Decimal of the float32 input, ulps allowed
+    ("Tanh", {}, lambda x: ((2 * x).exp() - 1) / ((2 * x).exp() + 1), 2),
+    ("Elu", dict(alpha=1.5),
+     lambda x: x if x > 0 else _f32d(1.5) * _f32d(float(x.exp() - 1)), 2),
+    ("LeakyRelu", dict(alpha=0.1),
+     lambda x: x if x >= 0 else _f32d(0.1) * x, 1),
+    ("HardSigmoid", dict(alpha=0.3, beta=0.4),
+     lambda x: min(max(_f32d(float(_f32d(0.3) * x)) + _f32d(0.4), 0), 1), 1),
+    ("Softplus", {}, lambda x: (1 + x.exp()).ln(), 1),
+    ("Exp", {}, _exp, 1),
+]
+TYPES = [("int8", (0.045, 0), (0.011, 0)),
+         ("uint8", (0.03, 140), (0.021, 60))]
+
+
+@pytest.mark.parametrize("op, attrs, fn, ulps", TABLE_CASES)
+@pytest.mark.parametrize("quant_type, inp, out", TYPES)
+def test_activation_table_matches_exact_evaluation(op, attrs, fn, ulps,
+                                                   quant_type, inp, out):
+    """Every entry whose quantization is stable within a few float32 ulps
+    of the exact function equals it. A float32 exponential where the
+    reference uses float64, a LeakyRelu slope on the wrong side, or a
+    dropped HardSigmoid offset changes entries."""
+    if op == "Exp" and quant_type == "int8":
+        inp = (0.01, 0)  # exp of [-1.28, 1.27]: within the output range
+    table, lo, hi = _table(op, attrs, quant_type, inp, out)
+    checked = 0
+    for q in range(lo, hi + 1):
+        x32 = np.float32(float(q - inp[1]) * inp[0])
+        want = _quantized_if_stable(fn(Decimal(float(x32))), ulps, out[0],
+                                    out[1], lo, hi)
+        if want is None:
+            continue
+        assert table[q - lo] == want, (q, float(x32))
+        checked += 1
+    assert checked >= 0.97 * (hi - lo + 1)
+
+
+@pytest.mark.parametrize("op, fn, inp, out", [
+    ("Exp", _exp, (3.05e-5, 0), (9.0e-5, 0)),
+    ("Softplus", lambda x: (1 + x.exp()).ln(), (1.2e-4, 0), (1.3e-4, 0)),
+])
+def test_float64_tables_are_correctly_rounded(op, fn, inp, out):
+    """Exp and Softplus are evaluated in float64 and then rounded to
+    float32, i.e. correctly rounded here: every entry of a 16-bit table
+    equals the quantized correctly rounded value (away from ties). A
+    float32 evaluation, off by one ulp on a share of the inputs, changes a
+    few dozen of the 65,536 entries."""
+    table, lo, hi = _table(op, {}, "int16", inp, out)
+    checked = 0
+    for q in range(lo, hi + 1):
+        x32 = np.float32(float(q - inp[1]) * inp[0])
+        want = _quantized_if_stable(fn(Decimal(float(x32))), 0, out[0],
+                                    out[1], lo, hi)
+        if want is None:
+            continue
+        assert table[q - lo] == want, (q, float(x32))
+        checked += 1
+    assert checked >= 0.99 * (hi - lo + 1)
+
+
+def test_sqrt_table_of_unsigned_inputs():
+    """sqrt of the dequantized non-negative values, correctly rounded in
+    float32; exact squares land exactly."""
+    table, lo, hi = _table("Sqrt", {}, "uint8", (0.25, 0), (0.0625, 0))
+    for q in range(256):
+        r = Decimal(q * 0.25).sqrt()
+        want = _quantized_if_stable(r, 0, 0.0625, 0, 0, 255)
+        if want is not None:
+            assert table[q] == want
+    assert table[16] == 32 and table[64] == 64 and table[0] == 0
+
+
+@pytest.mark.parametrize("op, attrs", [
+    ("Tanh", {}), ("Elu", dict(alpha=1.5)), ("LeakyRelu", dict(alpha=0.1))])
+def test_tables_at_the_zero_point_and_tanh_symmetry(op, attrs):
+    """f(0) = 0 maps the input zero point to the output zero point; under
+    symmetric parameters the Tanh table is odd."""
+    for quant_type, inp, out in [("int8", (0.05, 0), (0.01, 0)),
+                                 ("uint8", (0.03, 131), (0.02, 17))]:
+        table, lo, hi = _table(op, attrs, quant_type, inp, out)
+        assert table[inp[1] - lo] == out[1]
+    table, lo, _ = _table("Tanh", {}, "int8", (0.05, 0), (1 / 127, 0))
+    for q in range(-127, 128):
+        assert table[q - lo] == -table[-q - lo]
+    assert table[127 - lo] == 127 or table[127 - lo] == 126
+
+
+def test_tables_in_their_saturated_regions():
+    """Tanh reaches +-1, HardSigmoid is 0 below -beta/alpha and 1 above
+    (1-beta)/alpha, LeakyRelu is the identity requantization for x >= 0,
+    Exp(0) is 1 and Softplus(0) is ln 2."""
+    t, lo, _ = _table("Tanh", {}, "int8", (0.1, 0), (1 / 100, 0))
+    assert all(t[q - lo] == 100 for q in range(100, 128))   # x >= 10
+    assert all(t[q - lo] == -100 for q in range(-128, -99))
+    h, lo, _ = _table("HardSigmoid", dict(alpha=0.3, beta=0.4), "int8",
+                      (0.05, 0), (1 / 127, 0))
+    for q in range(-128, 128):
+        x = q * 0.05
+        if x <= -0.4 / 0.3 - 1e-6:
+            assert h[q - lo] == 0
+        elif x >= 0.6 / 0.3 + 1e-6:
+            assert h[q - lo] == 127
+    lr, lo, _ = _table("LeakyRelu", dict(alpha=0.1), "int8", (0.04, 0),
+                       (0.02, 0))
+    for q in range(0, 64):
+        assert lr[q - lo] == 2 * q  # 0.04 q / 0.02
+    e, lo, _ = _table("Exp", {}, "int8", (0.01, 0), (0.02, 0))
+    assert e[0 - lo] == 50   # 1 / 0.02
+    sp, lo, _ = _table("Softplus", {}, "int8", (0.05, 0), (0.01, 0))
+    assert sp[0 - lo] == round(math.log(2) / 0.01)  # 69.31 -> 69
+
+
+# ---------------------------------------------------- fake quantization --
+def test_fake_quantized_conv_on_a_dyadic_grid():
+    """A conv whose input, weight and output scales are powers of two and
+    whose weights are small integers on that grid: every fake-quantized
+    value is exact, so the pass equals the hand-computed round_half_even of
+    the exact convolution of the quantized input (with the bias rounded to
+    the s_in * s_w grid). A dropped bias, an unquantized weight or a
+    truncating rounding fails."""
+    rng = np.random.default_rng(8)
+    wq = rng.integers(-127, 128, size=(3, 2, 3, 3))
+    wq[:, 0, 0, 0] = 127  # per-channel scale exactly 1/32
+    w = (wq / 32.0).astype(np.float32)
+    bias = np.array([0.3, -1.7, 2.0], np.float32)
+    node = Node("conv", "Conv", ["x", "w", "b"], ["y"],
+                dict(kernel_shape=[3, 3], pads=[1, 1, 1, 1]))
+    g = Graph([node], {"w": w, "b": bias}, {"x": [1, 2, 4, 5]}, ["y"])
+    qj = _qj("int8", {"x": (0.5, 0, -128, 127), "y": (2.0, 0, -128, 127),
+                      "w": (1.0, 0, -128, 127), "b": (1.0, 0, -128, 127)})
+    pipe = OraclePipeline(g, qj)
+    x = (rng.normal(size=(1, 2, 4, 5)) * 20).astype(np.float32)
+    got = pipe.run_fake({"x": x})["y"]
+    qx = np.clip(np.round(x.astype(np.float64) / 0.5), -128, 127)
+    # bias on the s_in * s_w = 1/64 grid, half to even
+    bq = [round(Fraction(float(b)) * 64) for b in bias]
+    acc = _direct_conv(qx.astype(np.int64), wq, 1, (1, 1, 1, 1), 0)
+    for o, oy, ox in product(range(3), range(4), range(5)):
+        exact = Fraction(int(acc[0, o, oy, ox]) + bq[o], 64)  # float value
+        q = round(exact / 2)  # Python's round: half to even
+        q = min(max(q, -128), 127)
+        assert got[0, o, oy, ox] == np.float32(q * 2.0), (o, oy, ox)
