@@ -680,6 +680,56 @@ typedef struct qa_fb_avgpool {
 } qa_fb_avgpool;
 int qa_d_fb_avgpool(const qa_fb_avgpool* d, void* stream);
 
+/* Pad that is not scale-preserving, so the reference runs it as a float
+ * fallback (quant_layers.py:617-633 declines it; :195-205): reflect or edge
+ * mode, or a non-zero constant (float_ops.py:499-513). Output element
+ * (i_0, .., i_{ndim-1}) of `shape` reads x at source index j_k = i_k - lo_k
+ * per axis: mode 0 (constant) takes `value` (the float32 pad value) when
+ * some j_k lies outside [0, xshape_k); mode 1 (reflect) mirrors j_k about
+ * the end elements without repeating them (period 2 (n - 1); n = 1 reads
+ * element 0); mode 2 (edge) clamps j_k to the axis. The value is then
+ * quantized with the output parameters. Element strides xs / ys. */
+typedef struct qa_fb_pad {
+    const void* x;
+    int64_t x_code, x_so, x_zp;
+    double x_scale;
+    void* y;
+    int64_t y_code, y_so;
+    int64_t ndim, shape[6], lo[6], xshape[6], xs[6], ys[6];
+    int64_t mode;
+    double value;
+    double out_scale;
+    int64_t out_zp, qmin, qmax;
+} qa_fb_pad;
+int qa_d_fb_pad(const qa_fb_pad* d, void* stream);
+
+/* Gather with an index array and Cast (float fallbacks, quant_layers.py:
+ * 195-205 over float_ops.py:490-496 and :398-402). Output element
+ * (i_0, .., i_{ndim-1}) of `shape` reads x at sum over k of c_k xs[k],
+ * where c_k = i_k except on axis `axis` (-1: none), where c_k =
+ * idx[i_k] (idx: nidx device int64 values in [0, extent), negative
+ * indices already wrapped); a Gather's index dimensions arrive collapsed
+ * into that one axis. The dequantized float32 value v is then cast to ONNX
+ * element type `cast_to` (1 float32 and 11 float64: v; 10 float16: v
+ * rounded to nearest even; 9 bool: v != 0; 6 int32 / 3 int8 / 2 uint8 /
+ * 5 int16 / 4 uint16: truncated toward zero, INT32_MIN when outside the
+ * int32 range, then wrapped to the width; 7 int64: truncated, INT64_MIN
+ * outside the int64 range), as NumPy's astype does on x86-64, and
+ * quantized: round_half_even((double)t / out_scale) + out_zp, clipped. */
+typedef struct qa_fb_gather {
+    const void* x;
+    int64_t x_code, x_so, x_zp;
+    double x_scale;
+    const int64_t* idx;
+    int64_t nidx, axis, cast_to;
+    void* y;
+    int64_t y_code, y_so;
+    int64_t ndim, shape[6], xs[6], ys[6];
+    double out_scale;
+    int64_t out_zp, qmin, qmax;
+} qa_fb_gather;
+int qa_d_fb_gather(const qa_fb_gather* d, void* stream);
+
 /* ---------------------------------------------- allocation-free GEMM --- */
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid

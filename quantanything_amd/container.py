@@ -82,7 +82,7 @@ class QuantContainer:
             print(f"Calibrated on {count} batch(es).")
 
     def _observe(self, batch):
-        env = dict(float_ops.normalize_feeds(self.graph, batch))
+        env = dict(float_ops.feed_dict(self.graph, batch))
         for name, v in env.items():
             lo, hi = float(v.min()), float(v.max())
             old = self.ranges.get(name, (lo, hi))
@@ -146,7 +146,7 @@ class QuantContainer:
             self._observe(x)
             return None
         self._require_calibration()
-        feeds = float_ops.normalize_feeds(self.graph, x)
+        feeds = float_ops.feed_dict(self.graph, x)
         if mode == "quantize":
             res = self._fake_pass(feeds)
         else:
@@ -185,7 +185,7 @@ class QuantContainer:
     def integer_outputs(self, x):
         """Runs the integer pass and returns the graph outputs as quantized
         integers (int32 arrays), before dequantization."""
-        feeds = float_ops.normalize_feeds(self.graph, x)
+        feeds = float_ops.feed_dict(self.graph, x)
         ex = self.executor({k: v.shape for k, v in feeds.items()})
         ex.run(feeds)
         return ex.integer_outputs()

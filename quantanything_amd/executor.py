@@ -307,6 +307,35 @@ class FbAvgPool(ctypes.Structure):
                 + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
 
 
+class FbPad(ctypes.Structure):
+    """``qa_fb_pad`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("x", _P)] + [(n, _I64) for n in ("x_code", "x_so", "x_zp")]
+                + [("x_scale", _D), ("y", _P)]
+                + [(n, _I64) for n in ("y_code", "y_so", "ndim")]
+                + [(n, _I64 * 6) for n in ("shape", "lo", "xshape", "xs",
+                                           "ys")]
+                + [("mode", _I64), ("value", _D), ("out_scale", _D)]
+                + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
+
+
+class FbGather(ctypes.Structure):
+    """``qa_fb_gather`` of ``include/qa_hip.h``."""
+
+    _fields_ = ([("x", _P)] + [(n, _I64) for n in ("x_code", "x_so", "x_zp")]
+                + [("x_scale", _D), ("idx", _P)]
+                + [(n, _I64) for n in ("nidx", "axis", "cast_to")]
+                + [("y", _P)]
+                + [(n, _I64) for n in ("y_code", "y_so", "ndim")]
+                + [(n, _I64 * 6) for n in ("shape", "xs", "ys")]
+                + [("out_scale", _D)]
+                + [(n, _I64) for n in ("out_zp", "qmin", "qmax")])
+
+
+# ONNX element types a Cast fallback handles on the device (qa_fb_gather)
+CAST_CODES = frozenset({1, 2, 3, 4, 5, 6, 7, 9, 10, 11})
+
+
 def _collapse(shape, strides, lo, hi):
     """The element stride of axes lo..hi-1 taken as one index (row-major
     order), or None when their strides do not allow it; 0 for no axes."""
@@ -797,8 +826,13 @@ class DeviceExecutor:
             # rows of the input as images of one pixel
             x = DeviceTensor(x.buf, x.offset, (m, k), xv[2], 1, 0, x.code,
                              x.so, x.qp)
-        if layer.kind == "conv" and not x.nhwc:
-            raise NotImplementedError("convolution of a strided view")
+        if layer.kind == "conv" and (not x.nhwc or x.sc != 1):
+            # rows and columns strided apart (a Slice with a step) or
+            # channels not contiguous (a dense copy): the view copied into
+            # a channels-last tensor, the layout the kernels read
+            xc = self._new(x.shape, x.qp)
+            self._copy(f"copy:{layer.name}", x, xc)
+            x = xc
         use_mfma = self._mfma_ok(layer, x, layout, groups, cg, cg * kh * kw)
         info = self._weights_dev(layer, x, layout, use_mfma)
         (d.N, d.C, d.H, d.W, d.Cout, d.KH, d.KW, d.SH, d.SW, d.PH, d.PW,
@@ -1203,6 +1237,8 @@ class DeviceExecutor:
         p = self._params(layer)
         if "lut" not in p:
             p["lut"] = _dev(layer.lut, np.int32)
+        if x.rows_view() is None:  # e.g. a Slice with a step: copy it dense
+            x = self._contiguous(f"copy:{layer.name}", x)
         y = self._new(x.shape, layer.out_qp[0], dense=x._strides is not None)
         xv, yv = x.rows_view(), y.rows_view()
         if xv is None or yv is None:
@@ -1256,6 +1292,8 @@ class DeviceExecutor:
             # the output is dense row-major: rows must be the leading axes
             want = (int(np.prod(a.shape[:-1], dtype=np.int64)), a.shape[-1])
             return tuple(av[:2]) == want and tuple(bv[:2]) == want
+        if not a.shape or not b.shape:  # a scalar: the broadcasting kernel
+            return False
         one, big = (b, a) if b.shape[0] == 1 else (a, b)
         return len(a.shape) == len(b.shape) and one.shape[0] == 1 and \
             one.shape[1:] == big.shape[1:] and one.row_major() and \
@@ -1491,20 +1529,39 @@ class DeviceExecutor:
                 [x.shape[ax] // len(node.outputs)] * len(node.outputs)
             return [x.derived(v) for v in torch.split(m, sizes, dim=ax)]
         if op == "Slice":
-            starts = self._const_list(node, 1, "starts")
-            ends = self._const_list(node, 2, "ends")
-            axes = self._const_list(node, 3, "axes") or \
-                list(range(len(starts)))
-            steps = self._const_list(node, 4, "steps") or [1] * len(starts)
-            index = [slice(None)] * nd
-            for st_, en, a, sp in zip(starts, ends, axes, steps):
-                if sp <= 0:
-                    raise NotImplementedError("Slice with a negative step")
-                index[a + nd if a < 0 else a] = slice(
-                    None if st_ >= 2**62 else st_,
-                    None if abs(en) >= 2**62 else en, sp)
-            return [x.derived(m[tuple(index)])]
+            return [self._slice_view(layer, x)]
         raise NotImplementedError(f"{op} on the device")
+
+    def _slice_view(self, layer, x):
+        """Slice as Python slicing (``float_ops.py:469-481``: bounds at or
+        beyond 2^62 open, others clamped, negative indices from the end):
+        per axis, offset += first * stride, stride *= step. A negative step
+        gives negative strides, which only the strided copy reads, so that
+        view is copied to a dense tensor."""
+        node = layer.node
+        nd = len(x.shape)
+        starts = self._const_list(node, 1, "starts")
+        ends = self._const_list(node, 2, "ends")
+        axes = self._const_list(node, 3, "axes") or list(range(len(starts)))
+        steps = self._const_list(node, 4, "steps") or [1] * len(starts)
+        shape, strides = list(x.shape), list(x.nd_strides)
+        offset = x.offset
+        for b, e, a, step in zip(starts, ends, axes, steps):
+            if step == 0:
+                raise ValueError(f"{layer.name}: Slice step 0")
+            a = a + nd if a < 0 else a
+            r = range(*slice(None if b >= 2**62 else b,
+                             None if abs(e) >= 2**62 else e,
+                             step).indices(shape[a]))
+            if len(r) == 0:
+                raise NotImplementedError(f"{layer.name}: empty Slice")
+            offset += r.start * strides[a]
+            shape[a], strides[a] = len(r), strides[a] * step
+        v = DeviceTensor.nd(x.buf, offset, shape, strides, x.code, x.so,
+                            x.qp)
+        if any(st < 0 for st in strides):
+            return self._contiguous(f"copy:{layer.name}", v)
+        return v
 
     def _plan_shape(self, layer, ins):
         x = ins[0]
@@ -1650,7 +1707,100 @@ class DeviceExecutor:
             return self._plan_fb_avgpool(layer, x)
         if op == "Expand" or (op == "Cast" and layer.node.attr("to") == 1):
             return self._plan_fb_copy(layer, x)
+        if op == "Cast":
+            return self._plan_fb_gather(layer, x, None, -1,
+                                        int(layer.node.attr("to")))
+        if op == "Pad":
+            return self._plan_fb_pad(layer, x)
         raise NotImplementedError(f"float fallback of {op} on the device")
+
+    def _plan_fb_pad(self, layer, x):
+        """Pad in reflect / edge mode or with a non-zero constant: the
+        float fallback, each output value requantized (the padding value
+        quantized from its float32 value)."""
+        node = layer.node
+        nd = len(x.shape)
+        pads = self._const_list(node, 1, "pads")
+        if pads is None or len(pads) != 2 * nd:
+            raise NotImplementedError("Pad without 2 * rank constant pads")
+        if min(pads) < 0:
+            raise NotImplementedError("Pad with negative pads (cropping)")
+        if not 1 <= nd <= 6:
+            raise NotImplementedError(f"Pad of rank {nd}")
+        mode = node.attr("mode", "constant")
+        if mode not in ("constant", "reflect", "edge"):
+            raise NotImplementedError(f"Pad mode {mode}")
+        value = 0.0
+        if mode == "constant":
+            init = self.graph.initializers
+            value = (np.asarray(init[node.inputs[2]]).reshape(()).item()
+                     if len(node.inputs) > 2 and node.inputs[2]
+                     else node.attr("value", 0.0))
+        shape = tuple(x.shape[k] + pads[k] + pads[k + nd] for k in range(nd))
+        o, iq = layer.out_qp[0], layer.in_qp[0]
+        y = self._new(shape, o, dense=nd not in (2, 4))
+        d = FbPad()
+        d.x, d.x_code, d.x_so = x.ptr, x.code, x.so
+        d.x_zp, d.x_scale = int(iq.zp), float(iq.scale)
+        d.y, d.y_code, d.y_so, d.ndim = y.ptr, y.code, y.so, nd
+        for k in range(nd):
+            d.shape[k], d.lo[k], d.xshape[k] = shape[k], pads[k], x.shape[k]
+            d.xs[k], d.ys[k] = x.nd_strides[k], y.nd_strides[k]
+        d.mode = ("constant", "reflect", "edge").index(mode)
+        d.value = float(np.float32(value))  # np.pad casts it to float32
+        d.out_scale, d.out_zp, d.qmin, d.qmax = self._qargs(o)
+        self.keep.extend([x.buf, y.buf, d])
+        self._add(f"fallback:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_fb_pad(ctypes.byref(d), s), "qa_d_fb_pad"))
+        return [y]
+
+    def _plan_fb_gather(self, layer, x, idx, axis, cast_to):
+        """Gather of an index array along ``axis`` (``idx``: the indices,
+        any shape) and / or Cast to ``cast_to``: the selected values
+        dequantized, cast, and requantized with the output parameters."""
+        if cast_to not in CAST_CODES:
+            raise NotImplementedError(f"Cast to element type {cast_to}")
+        nd = len(x.shape)
+        shape = list(x.shape)
+        out = tuple(x.shape)
+        if axis >= 0:
+            n = x.shape[axis]
+            idx = np.asarray(idx).astype(np.int64)
+            if idx.size == 0:
+                raise NotImplementedError("Gather of an empty index array")
+            if idx.min() < -n or idx.max() >= n:
+                raise IndexError(f"{layer.name}: Gather index out of range "
+                                 f"for an axis of {n}")
+            idx = np.where(idx < 0, idx + n, idx)
+            shape[axis] = idx.size
+            out = x.shape[:axis] + idx.shape + x.shape[axis + 1:]
+        if not 1 <= nd <= 6 or len(out) > 6:
+            raise NotImplementedError(f"{layer.node.op_type} of rank "
+                                      f"{len(out)}")
+        o, iq = layer.out_qp[0], layer.in_qp[0]
+        if len(out) == nd:  # coordinates map one to one: any layout
+            y = self._new(out, o, dense=nd not in (2, 4))
+            ys = list(y.nd_strides)
+        else:  # the index dimensions, dense in y, taken as one axis
+            y = self._new(out, o, dense=True)
+            ys = [int(np.prod(shape[k + 1:], dtype=np.int64))
+                  for k in range(nd)]
+        d = FbGather()
+        d.x, d.x_code, d.x_so = x.ptr, x.code, x.so
+        d.x_zp, d.x_scale = int(iq.zp), float(iq.scale)
+        if axis >= 0:
+            t = _dev(idx.reshape(-1), np.int64)
+            self.keep.append(t)
+            d.idx, d.nidx = t.data_ptr(), idx.size
+        d.axis, d.cast_to = axis, cast_to
+        d.y, d.y_code, d.y_so, d.ndim = y.ptr, y.code, y.so, nd
+        for k in range(nd):
+            d.shape[k], d.xs[k], d.ys[k] = shape[k], x.nd_strides[k], ys[k]
+        d.out_scale, d.out_zp, d.qmin, d.qmax = self._qargs(o)
+        self.keep.extend([x.buf, y.buf, d])
+        self._add(f"fallback:{layer.name}", lambda s: _ok(
+            self.lib.qa_d_fb_gather(ctypes.byref(d), s), "qa_d_fb_gather"))
+        return [y]
 
     @staticmethod
     def _qargs(qp):
@@ -1930,7 +2080,7 @@ class DeviceExecutor:
         if idx.ndim == 0:
             v = x.derived(m.select(ax, int(idx)))
         else:
-            raise NotImplementedError("Gather of an index array")
+            return self._plan_fb_gather(layer, x, idx, ax, 1)
         o, iq = layer.out_qp[0], layer.in_qp[0]
         y = self._new(v.shape, o, dense=True)
         self._copy(f"gather:{layer.name}", v, y, mode=2,

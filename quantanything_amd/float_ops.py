@@ -18,6 +18,8 @@ from numpy.lib.stride_tricks import sliding_window_view
 
 from quantanything_amd import native
 
+# op_type -> evaluator(node, inputs, opset, **kw) returning the list of the
+# node's outputs; UNARY: the element-wise ops that tabulate (f(node, x)).
 OPS = {}
 UNARY = {}
 
@@ -26,52 +28,63 @@ class UnsupportedOp(NotImplementedError):
     """An operator without a float implementation here."""
 
 
-def _reg(*names):
-    def deco(fn):
-        for n in names:
-            OPS[n] = fn
+def operator(*names, multi=False):
+    """Registers an evaluator under ONNX op names. Single-output evaluators
+    (``multi`` False) return one array, which is wrapped into the list that
+    every entry of :data:`OPS` returns."""
+    def register(fn):
+        entry = fn if multi else \
+            (lambda node, ins, opset, **kw: [fn(node, ins, opset, **kw)])
+        OPS.update(dict.fromkeys(names, entry))
         return fn
-    return deco
+    return register
 
 
-def _unary(name):
-    def deco(fn):
+def tabulated(name):
+    """Registers an element-wise ``f(node, x)`` that integer passes turn
+    into a lookup table over every quantized input value."""
+    def register(fn):
         UNARY[name] = fn
-        OPS[name] = lambda node, ins, opset, **kw: fn(node, ins[0])
+        OPS[name] = lambda node, ins, opset, **kw: [fn(node, ins[0])]
         return fn
-    return deco
+    return register
 
 
 def run_node(node, inputs, opset=13, **kw):
-    fn = OPS.get(node.op_type)
-    if fn is None:
+    """The node's outputs (a list) on float (or integer) NumPy inputs."""
+    try:
+        evaluate = OPS[node.op_type]
+    except KeyError:
         raise UnsupportedOp(f"operator {node.op_type} ({node.name}) has no "
-                            "float implementation")
-    out = fn(node, inputs, opset, **kw)
-    return list(out) if isinstance(out, (list, tuple)) else [out]
+                            "float implementation") from None
+    return evaluate(node, inputs, opset, **kw)
 
 
-def normalize_feeds(graph, feeds):
-    if not isinstance(feeds, dict):
-        names = graph.input_names
-        if len(names) != 1:
-            raise ValueError(f"model has {len(names)} inputs; pass a dict "
-                             f"keyed by {names}")
-        feeds = {names[0]: feeds}
-    return {k: np.asarray(v, dtype=np.float32) for k, v in feeds.items()}
+def feed_dict(graph, feeds):
+    """``{input name: float32 array}`` from a dict, or from one array when
+    the graph has a single input."""
+    names = graph.input_names
+    if isinstance(feeds, dict):
+        pairs = feeds.items()
+    elif len(names) == 1:
+        pairs = [(names[0], feeds)]
+    else:
+        raise ValueError(f"the graph has {len(names)} inputs "
+                         f"({', '.join(names)}): feed a dict of them")
+    return {name: np.asarray(v, dtype=np.float32) for name, v in pairs}
 
 
 def run_float(graph, feeds, keep_all=False):
-    env = dict(graph.initializers)
-    env.update(normalize_feeds(graph, feeds))
+    """The float32 pass: graph outputs (one array, or a list), or every
+    tensor of the pass with ``keep_all``."""
+    env = {**graph.initializers, **feed_dict(graph, feeds)}
     for node in graph.nodes:
-        outs = run_node(node, [env[i] if i else None for i in node.inputs],
-                        graph.opset)
-        env.update(zip(node.outputs, outs))
+        args = [env[i] if i else None for i in node.inputs]
+        env.update(zip(node.outputs, run_node(node, args, graph.opset)))
     if keep_all:
         return env
-    res = [env[o] for o in graph.outputs]
-    return res[0] if len(res) == 1 else res
+    outs = [env[o] for o in graph.outputs]
+    return outs if len(outs) > 1 else outs[0]
 
 
 def conv_pads(node, in_hw, kernel, strides, dilations):
@@ -100,7 +113,7 @@ def conv_geometry(node, x_shape, w_shape):
 
 
 # ------------------------------------------------------------- linear ----
-@_reg("Conv")
+@operator("Conv")
 def _conv(node, ins, opset, **kw):
     x, w = ins[0], ins[1]
     if x.ndim != 4:
@@ -111,7 +124,7 @@ def _conv(node, ins, opset, **kw):
     return y
 
 
-@_reg("Gemm")
+@operator("Gemm")
 def _gemm(node, ins, opset, **kw):
     a, b = ins[0], ins[1]
     if node.attr("transA", 0):
@@ -124,7 +137,7 @@ def _gemm(node, ins, opset, **kw):
     return y.astype(np.float32)
 
 
-@_reg("MatMul")
+@operator("MatMul")
 def _matmul(node, ins, opset, **kw):
     y = np.matmul(ins[0], ins[1]).astype(np.float32)
     if len(ins) > 2 and ins[2] is not None:
@@ -132,7 +145,7 @@ def _matmul(node, ins, opset, **kw):
     return y
 
 
-@_reg("FusedElementwise")
+@operator("FusedElementwise")
 def _fused(node, ins, opset, **kw):
     env = dict(node.attrs["consts"])
     env[node.inputs[0]] = ins[0]
@@ -142,7 +155,7 @@ def _fused(node, ins, opset, **kw):
     return env[node.outputs[0]]
 
 
-@_reg("BatchNormalization")
+@operator("BatchNormalization")
 def _bn(node, ins, opset, **kw):
     x, gamma, beta, mean, var = ins[:5]
     shape = [1, -1] + [1] * (x.ndim - 2)
@@ -152,73 +165,76 @@ def _bn(node, ins, opset, **kw):
 
 
 # ------------------------------------------------------- element-wise ----
-for _name, _fn in (("Add", np.add), ("Sub", np.subtract),
-                   ("Mul", np.multiply), ("Div", np.divide),
-                   ("Max", np.maximum), ("Min", np.minimum)):
-    OPS[_name] = (lambda f: lambda node, ins, opset, **kw: f(ins[0], ins[1]))(
-        _fn)
+def _binary(ufunc):
+    return lambda node, ins, opset, **kw: ufunc(ins[0], ins[1])
 
 
-@_unary("Sigmoid")
+for _op, _ufunc in {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply,
+                    "Div": np.divide, "Max": np.maximum,
+                    "Min": np.minimum}.items():
+    operator(_op)(_binary(_ufunc))
+
+
+@tabulated("Sigmoid")
 def _sigmoid(node, x):
     return (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
 
 
-@_unary("Relu")
+@tabulated("Relu")
 def _relu(node, x):
     return np.maximum(x, 0)
 
 
-@_unary("LeakyRelu")
+@tabulated("LeakyRelu")
 def _leaky(node, x):
     return np.where(x >= 0, x, node.attr("alpha", 0.01) * x).astype(
         np.float32)
 
 
-@_unary("Tanh")
+@tabulated("Tanh")
 def _tanh(node, x):
     return np.tanh(x).astype(np.float32)
 
 
-@_unary("HardSigmoid")
+@tabulated("HardSigmoid")
 def _hsig(node, x):
     a, b = node.attr("alpha", 0.2), node.attr("beta", 0.5)
     return np.clip(a * x + b, 0, 1).astype(np.float32)
 
 
-@_unary("HardSwish")
+@tabulated("HardSwish")
 def _hswish(node, x):
     return (x * np.clip(x / 6.0 + 0.5, 0, 1)).astype(np.float32)
 
 
-@_unary("Elu")
+@tabulated("Elu")
 def _elu(node, x):
     a = node.attr("alpha", 1.0)
     return np.where(x > 0, x, a * np.expm1(np.minimum(x, 0))).astype(
         np.float32)
 
 
-@_unary("Softplus")
+@tabulated("Softplus")
 def _softplus(node, x):
     return np.logaddexp(0, x.astype(np.float64)).astype(np.float32)
 
 
-@_unary("Abs")
+@tabulated("Abs")
 def _abs(node, x):
     return np.abs(x)
 
 
-@_unary("Neg")
+@tabulated("Neg")
 def _neg(node, x):
     return -x
 
 
-@_unary("Sqrt")
+@tabulated("Sqrt")
 def _sqrt(node, x):
     return np.sqrt(x).astype(np.float32)
 
 
-@_unary("Exp")
+@tabulated("Exp")
 def _exp(node, x):
     return np.exp(x.astype(np.float64)).astype(np.float32)
 
@@ -233,12 +249,12 @@ def erf(x):
     return np.sign(x) * (1.0 - poly * np.exp(-ax * ax))
 
 
-@_unary("Erf")
+@tabulated("Erf")
 def _erf(node, x):
     return erf(x).astype(np.float32)
 
 
-@_unary("Gelu")
+@tabulated("Gelu")
 def _gelu(node, x):
     x64 = x.astype(np.float64)
     if node.attr("approximate", "none") == "tanh":
@@ -247,13 +263,13 @@ def _gelu(node, x):
     return (0.5 * x64 * (1 + erf(x64 / np.sqrt(2)))).astype(np.float32)
 
 
-@_reg("Pow")
+@operator("Pow")
 def _pow(node, ins, opset, **kw):
     return np.power(ins[0].astype(np.float64),
                     np.asarray(ins[1]).astype(np.float64)).astype(np.float32)
 
 
-@_reg("Clip")
+@operator("Clip")
 def _clip(node, ins, opset, **kw):
     lo = ins[1] if len(ins) > 1 and ins[1] is not None else node.attr("min")
     hi = ins[2] if len(ins) > 2 and ins[2] is not None else node.attr("max")
@@ -264,7 +280,7 @@ def _axis(axis, ndim):
     return axis + ndim if axis < 0 else axis
 
 
-@_reg("Softmax")
+@operator("Softmax")
 def _softmax(node, ins, opset, **kw):
     x = ins[0].astype(np.float64)
     ax = _axis(node.attr("axis", -1 if opset >= 13 else 1), x.ndim)
@@ -272,7 +288,7 @@ def _softmax(node, ins, opset, **kw):
     return (e / e.sum(axis=ax, keepdims=True)).astype(np.float32)
 
 
-@_reg("LogSoftmax")
+@operator("LogSoftmax")
 def _log_softmax(node, ins, opset, **kw):
     x = ins[0].astype(np.float64)
     ax = _axis(node.attr("axis", -1 if opset >= 13 else 1), x.ndim)
@@ -281,7 +297,7 @@ def _log_softmax(node, ins, opset, **kw):
         np.float32)
 
 
-@_reg("LayerNormalization")
+@operator("LayerNormalization")
 def _layer_norm(node, ins, opset, **kw):
     x = ins[0].astype(np.float64)
     axes = tuple(range(_axis(node.attr("axis", -1), x.ndim), x.ndim))
@@ -294,19 +310,19 @@ def _layer_norm(node, ins, opset, **kw):
 
 
 # ------------------------------------------------------------- shapes ----
-@_reg("Identity", "Dropout")
+@operator("Identity", "Dropout")
 def _identity(node, ins, opset, **kw):
     return ins[0]
 
 
-@_reg("Flatten")
+@operator("Flatten")
 def _flatten(node, ins, opset, **kw):
     x = ins[0]
     ax = _axis(node.attr("axis", 1), x.ndim)
     return x.reshape(int(np.prod(x.shape[:ax])), -1)
 
 
-@_reg("Reshape")
+@operator("Reshape")
 def _reshape(node, ins, opset, **kw):
     x = ins[0]
     shape = [int(s) for s in np.asarray(ins[1]).reshape(-1)]
@@ -315,7 +331,7 @@ def _reshape(node, ins, opset, **kw):
     return x.reshape(shape)
 
 
-@_reg("Transpose")
+@operator("Transpose")
 def _transpose(node, ins, opset, **kw):
     perm = node.attr("perm")
     return np.transpose(ins[0], perm if perm else None)
@@ -328,7 +344,7 @@ def _axes(node, ins, index, attr):
     return None if v is None else [int(a) for a in v]
 
 
-@_reg("Squeeze")
+@operator("Squeeze")
 def _squeeze(node, ins, opset, **kw):
     axes = _axes(node, ins, 1, "axes")
     x = ins[0]
@@ -337,7 +353,7 @@ def _squeeze(node, ins, opset, **kw):
     return np.squeeze(x, axis=tuple(_axis(a, x.ndim) for a in axes))
 
 
-@_reg("Unsqueeze")
+@operator("Unsqueeze")
 def _unsqueeze(node, ins, opset, **kw):
     axes = _axes(node, ins, 1, "axes")
     x = ins[0]
@@ -347,13 +363,13 @@ def _unsqueeze(node, ins, opset, **kw):
     return x
 
 
-@_reg("Gather")
+@operator("Gather")
 def _gather(node, ins, opset, **kw):
     return np.take(ins[0], np.asarray(ins[1]).astype(np.int64),
                    axis=node.attr("axis", 0))
 
 
-@_reg("Slice")
+@operator("Slice")
 def _slice(node, ins, opset, **kw):
     x = ins[0]
     starts = _axes(node, ins, 1, "starts")
@@ -367,12 +383,12 @@ def _slice(node, ins, opset, **kw):
     return x[tuple(index)]
 
 
-@_reg("Concat")
+@operator("Concat")
 def _concat(node, ins, opset, **kw):
     return np.concatenate(ins, axis=node.attr("axis"))
 
 
-@_reg("Split")
+@operator("Split", multi=True)
 def _split(node, ins, opset, **kw):
     x = ins[0]
     ax = _axis(node.attr("axis", 0), x.ndim)
@@ -386,30 +402,38 @@ def _split(node, ins, opset, **kw):
     return list(np.split(x, np.cumsum(sizes)[:-1], axis=ax))
 
 
-@_reg("GlobalAveragePool")
+@operator("GlobalAveragePool")
 def _gap(node, ins, opset, **kw):
     x = ins[0]
     return x.mean(axis=tuple(range(2, x.ndim)), keepdims=True).astype(
         np.float32)
 
 
-@_reg("GlobalMaxPool")
+@operator("GlobalMaxPool")
 def _gmp(node, ins, opset, **kw):
     x = ins[0]
     return x.max(axis=tuple(range(2, x.ndim)), keepdims=True)
 
 
-@_reg("Pad")
+@operator("Pad")
 def _pad(node, ins, opset, pad_value=None, **kw):
+    """Constant padding with ``pad_value`` (the integer path's zero point),
+    else the value input or attribute; reflect (mirrored without repeating
+    the border) and edge (border repeated) modes (``float_ops.py:499-513``).
+    """
     x = ins[0]
     pads = (np.asarray(ins[1]).astype(np.int64).tolist()
             if len(ins) > 1 and ins[1] is not None else node.attr("pads"))
+    width = list(zip(pads[:x.ndim], pads[x.ndim:]))
+    mode = node.attr("mode", "constant")
+    if mode in ("reflect", "edge"):
+        return np.pad(x, width, mode=mode)
+    if mode != "constant":
+        raise UnsupportedOp(f"Pad mode {mode}")
     if pad_value is None:
         pad_value = (np.asarray(ins[2]).reshape(()).item()
                      if len(ins) > 2 and ins[2] is not None
                      else node.attr("value", 0))
-    n = x.ndim
-    width = [(pads[i], pads[i + n]) for i in range(n)]
     return np.pad(x, width, mode="constant", constant_values=pad_value)
 
 
@@ -431,7 +455,7 @@ def pool_geometry(node, in_hw):
     return kernel, strides, dil, tuple(pads)
 
 
-@_reg("MaxPool")
+@operator("MaxPool")
 def _maxpool(node, ins, opset, pad_value=None, **kw):
     x = ins[0]
     kernel, strides, dil, pads = pool_geometry(node, x.shape[2:])
@@ -447,28 +471,30 @@ def _maxpool(node, ins, opset, pad_value=None, **kw):
 
 
 # ------------------------------------------------- model-file operators ----
+# Constant's value fields and the NumPy type their value takes
+_CONSTANT_FIELDS = (("value", None), ("value_float", np.float32),
+                    ("value_int", np.int64), ("value_floats", None),
+                    ("value_ints", np.int64))
+
+
 def constant_value(node):
-    """The value of an ONNX ``Constant`` node (``float_ops.py:101-118``)."""
-    a = node.attrs
-    for key in ("value", "value_float", "value_int", "value_floats",
-                "value_ints"):
-        if key in a:
-            v = np.asarray(a[key])
-            if key == "value_float":
-                v = v.astype(np.float32)
-            elif key in ("value_int", "value_ints"):
-                v = v.astype(np.int64)
-            return v
-    raise UnsupportedOp(f"Constant node '{node.name}' has no supported "
-                        "value")
+    """The value of an ONNX ``Constant`` node (``float_ops.py:101-118``):
+    its tensor, or its scalar / list field as float32 / int64."""
+    field = next(((f, t) for f, t in _CONSTANT_FIELDS if f in node.attrs),
+                 None)
+    if field is None:
+        raise UnsupportedOp(f"Constant node '{node.name}' has no supported "
+                            "value")
+    v = np.asarray(node.attrs[field[0]])
+    return v if field[1] is None else v.astype(field[1])
 
 
-@_reg("Constant")
+@operator("Constant")
 def _constant(node, ins, opset, **kw):
     return constant_value(node)
 
 
-@_reg("Shape")
+@operator("Shape")
 def _shape(node, ins, opset, **kw):
     shape = np.array(np.shape(ins[0]), np.int64)
     return shape[node.attr("start", 0):node.attr("end", None)]
@@ -484,7 +510,7 @@ def _per_axis(v, x, axis):
     return v.reshape(shape)
 
 
-@_reg("QuantizeLinear")
+@operator("QuantizeLinear")
 def _quantize_linear(node, ins, opset, **kw):
     """y = saturate(round_half_even(x / scale) + zero_point) in the zero
     point's type (uint8 without one), float32 arithmetic."""
@@ -499,7 +525,7 @@ def _quantize_linear(node, ins, opset, **kw):
     return np.clip(y, info.min, info.max).astype(np.asarray(zp).dtype)
 
 
-@_reg("DequantizeLinear")
+@operator("DequantizeLinear")
 def _dequantize_linear(node, ins, opset, **kw):
     """x = (q - zero_point) * scale in float32."""
     q = np.asarray(ins[0])
@@ -510,7 +536,7 @@ def _dequantize_linear(node, ins, opset, **kw):
     return ((q.astype(np.float32) - zpf) * scale).astype(np.float32)
 
 
-@_reg("Expand")
+@operator("Expand")
 def _expand(node, ins, opset, **kw):
     shape = tuple(int(v) for v in np.asarray(ins[1]).reshape(-1))
     return np.broadcast_to(ins[0], np.broadcast_shapes(ins[0].shape,
@@ -523,7 +549,7 @@ CAST_TYPES = {1: np.float32, 2: np.uint8, 3: np.int8, 4: np.uint16,
               10: np.float16, 11: np.float64}
 
 
-@_reg("Cast")
+@operator("Cast")
 def _cast(node, ins, opset, **kw):
     to = node.attr("to")
     if to not in CAST_TYPES:
@@ -531,7 +557,7 @@ def _cast(node, ins, opset, **kw):
     return ins[0].astype(CAST_TYPES[to])
 
 
-@_reg("AveragePool")
+@operator("AveragePool")
 def _avgpool(node, ins, opset, **kw):
     """Window sums of the zero-padded input over the window's element count
     (or the whole window with count_include_pad), float32."""
@@ -548,7 +574,7 @@ def _avgpool(node, ins, opset, **kw):
     return (total / cnt).astype(np.float32)
 
 
-@_reg("ReduceMean")
+@operator("ReduceMean")
 def _reduce_mean(node, ins, opset, **kw):
     x = ins[0]
     axes = (np.asarray(ins[1]).astype(np.int64).tolist()

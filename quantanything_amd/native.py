@@ -112,6 +112,8 @@ def _declare(lib):
         "qa_d_fb_reduce_mean": (i32, [p, p]),
         "qa_d_fb_softmax": (i32, [p, p]),
         "qa_d_fb_avgpool": (i32, [p, p]),
+        "qa_d_fb_pad": (i32, [p, p]),
+        "qa_d_fb_gather": (i32, [p, p]),
         "qa_noalloc_scratch_bytes": (i64, []),
         "qa_gemm_i16_i32_noalloc_need": (i64, [i64] * 3),
         "qa_gemm_i16_i32_noalloc": (i32, [i64] * 3 + [p] * 4),
