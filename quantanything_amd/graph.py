@@ -362,6 +362,77 @@ def vit(seed=5, batch=32, size=224, patch=16, dim=384, depth=12, heads=6,
     return b.build("images", [batch, 3, size, size], y)
 
 
+def vit_export(seed=7, batch=2, size=32, patch=8, dim=32, depth=2, heads=4,
+               mlp=128, classes=10, gelu="tanh"):
+    """A ViT as a PyTorch-style export writes it, before any rewrite (the
+    reference tests' ``build_vit``, ``tests/models.py:125-246``): the class
+    token expanded over the batch by a ``Shape -> Gather -> Unsqueeze ->
+    Concat -> Expand`` chain, each LayerNorm written out (ReduceMean, Sub,
+    Pow, ReduceMean, Add epsilon, Sqrt, Div, Mul gain, Add bias; random gains
+    and biases), every Linear as MatMul + Add, the attention logits scaled
+    by an explicit ``Mul`` by 1/sqrt(hd), the class token gathered after the
+    final LayerNorm. ``gelu``: "tanh" for the Gelu operator (opset 20), or
+    "erf" for its decomposition Div, Erf, Add, Mul, Mul. Loading it applies
+    the reference's passes and gives :func:`vit`'s operator sequence."""
+    b = GraphBuilder(seed, opset=20)
+    hd = dim // heads
+    tokens = (size // patch) ** 2 + 1
+    f32, i64 = np.float32, np.int64
+    last = b.const(np.array([-1], i64))
+    axis0 = b.const(np.array([0], i64))
+
+    def ln(x):
+        g = b.const((1 + b.rng.normal((dim,), 0.1)).astype(f32), "ln_g")
+        beta = b.const(b.rng.normal((dim,), 0.1).astype(f32), "ln_b")
+        mean = b.op("ReduceMean", [x, last], keepdims=1)
+        d = b.op("Sub", [x, mean])
+        var = b.op("ReduceMean", [b.op("Pow", [d, b.const(f32(2.0))]), last],
+                   keepdims=1)
+        sd = b.op("Sqrt", [b.op("Add", [var, b.const(f32(1e-6))])])
+        return b.op("Add", [b.op("Mul", [b.op("Div", [d, sd]), g]), beta])
+
+    def linear(x, k, n):
+        y = b.op("MatMul", [x, b.weight(k, n, scale=np.sqrt(1.0 / k))])
+        return b.op("Add", [y, b.weight(n, scale=0.02, base="bias")])
+
+    def act(x):
+        if gelu == "tanh":
+            return b.op("Gelu", [x], approximate="tanh")
+        e = b.op("Erf", [b.op("Div", [x, b.const(f32(np.sqrt(2.0)))])])
+        return b.op("Mul", [b.op("Mul", [x, b.const(f32(0.5))]),
+                            b.op("Add", [e, b.const(f32(1.0))])])
+
+    x = b.conv("images", 3, dim, patch, patch, pad=0,
+               w_scale=np.sqrt(1.0 / (3 * patch * patch)), b_scale=0.02)
+    x = b.op("Reshape", [x, b.const(np.array([batch, dim, -1], i64))])
+    x = b.op("Transpose", [x], perm=[0, 2, 1])
+    n = b.op("Gather", [b.op("Shape", ["images"]), b.const(np.array(0, i64))],
+             axis=0)
+    shape = b.op("Concat", [b.op("Unsqueeze", [n, axis0]),
+                            b.const(np.array([1, dim], i64))], axis=0)
+    cls = b.weight(1, 1, dim, scale=0.02, base="cls")
+    x = b.op("Concat", [b.op("Expand", [cls, shape]), x], axis=1)
+    x = b.op("Add", [x, b.weight(1, tokens, dim, scale=0.02, base="pos")])
+    for _ in range(depth):
+        qkv = b.op("Reshape", [linear(ln(x), dim, 3 * dim), b.const(
+            np.array([batch, tokens, 3, heads, hd], i64))])
+        qkv = b.op("Transpose", [qkv], perm=[2, 0, 3, 1, 4])
+        q, k, v = [b.op("Squeeze", [t, axis0]) for t in
+                   b.op("Split", [qkv], n_out=3, axis=0, num_outputs=3)]
+        att = b.op("MatMul", [q, b.op("Transpose", [k], perm=[0, 1, 3, 2])])
+        att = b.op("Mul", [att, b.const(f32(hd ** -0.5))])
+        att = b.op("Softmax", [att], axis=-1)
+        o = b.op("Transpose", [b.op("MatMul", [att, v])], perm=[0, 2, 1, 3])
+        o = b.op("Reshape", [o, b.const(np.array([batch, tokens, dim], i64))])
+        x = b.op("Add", [x, linear(o, dim, dim)])
+        x = b.op("Add", [x, linear(act(linear(ln(x), dim, mlp)), mlp, dim)])
+    x = b.op("Gather", [ln(x), b.const(np.array(0, i64))], axis=1)
+    y = b.op("Gemm", [x, b.weight(classes, dim, scale=np.sqrt(1.0 / dim)),
+                      b.weight(classes, scale=0.01)], transB=1)
+    return Graph(b.nodes, b.inits, {"images": [batch, 3, size, size]}, [y],
+                 b.opset)
+
+
 def conv_silu(seed=2, cin=64, cout=64, size=56, k=3, stride=1):
     """One Conv -> SiLU layer (the single-conv workload as a graph)."""
     b = GraphBuilder(seed)

@@ -1,5 +1,10 @@
 """Model files on the device: a graph written to ONNX and read back
-calibrates to the same q.json and the same integer outputs; the QDQ export
+calibrates to the same q.json and the same integer outputs, and its integer
+pass equals the oracle pipeline's on the loaded graph; a PyTorch-style ViT
+export (decomposed LayerNorms, explicit attention scale, Shape-chain class
+token) loads through the reference's passes to the operator multiset of the
+post-pass builder and runs bit-exact against the oracle on its integer
+layers, within one step on its float fallbacks; the QDQ export
 of a calibrated container carries every q.json parameter and, run with the
 ONNX float semantics of QuantizeLinear / DequantizeLinear, reproduces the
 container's fake quantization (quant_container.py:150-160)."""
@@ -9,12 +14,14 @@ import json
 import numpy as np
 import pytest
 
+from oracle.pipeline import OraclePipeline
 from quantanything_amd import float_ops
 from quantanything_amd import graph as G
 from quantanything_amd import onnx_io
 from quantanything_amd.container import QuantContainer
 from quantanything_amd.synth import Stream
-from tests.test_onnx_io import PB
+from tests.test_gpu_vit import _check_against_oracle
+from tests.test_onnx_io import CFG, PB
 
 pytestmark = pytest.mark.gpu
 
@@ -46,6 +53,61 @@ def test_written_model_runs_identically(hip, tmp_path, model, quant_type):
     ia, ib = a.integer_outputs(calib[1]), b.integer_outputs(calib[1])
     for name in g.outputs:
         np.testing.assert_array_equal(ia[name], ib[name])
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8", "int16"])
+@pytest.mark.parametrize("model", sorted(MODELS))
+def test_loaded_model_matches_oracle(hip, tmp_path, model, quant_type):
+    """The loaded graph's integer pass against the oracle pipeline run on
+    the same loaded graph and q.json: every tensor bit-exact."""
+    print(f"case loaded {model} {quant_type}", flush=True)
+    g, shape = MODELS[model]()
+    h = onnx_io.load_onnx(onnx_io.save_onnx(g, tmp_path / "m.onnx"))
+    calib = _calib(shape)
+    c = QuantContainer(h, quant_type, True)
+    c.calibrate(calib)
+    ex = c.executor({h.input_names[0]: shape})
+    ex.run({h.input_names[0]: calib[1]})
+    c.save(tmp_path / "q.json")
+    o = OraclePipeline(h, tmp_path / "q.json")
+    o.run(calib[1], keep=True)
+    checked = 0
+    for n, t in ex.tensors.items():
+        if n in o.env:
+            got = t.to_host()
+            np.testing.assert_array_equal(got, o.env[n].reshape(got.shape),
+                                          err_msg=n)
+            checked += 1
+    assert checked >= 10
+
+
+@pytest.mark.parametrize("gelu", ["tanh", "erf"])
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+def test_loaded_vit_export_matches_oracle(hip, tmp_path, quant_type, gelu):
+    """A ViT export loaded through the reference's passes (LayerNorm fusion,
+    attention scale and LayerNorm affine folded, class-token Gather hoisted)
+    quantizes at the post-pass graph's points: its operators are those of
+    graph.vit, its integer layers are bit-exact against the oracle and its
+    float fallbacks (LayerNorm, Softmax, activation MatMuls, Gather) within
+    one step."""
+    from collections import Counter
+    print(f"case vit export {quant_type} {gelu}", flush=True)
+    raw = G.vit_export(gelu=gelu, **CFG)
+    h = onnx_io.load_onnx(onnx_io.save_onnx(raw, tmp_path / "vit.onnx"))
+    want = Counter(n.op_type for n in G.vit(seed=7, **CFG).nodes)
+    if gelu == "erf":
+        want["FusedElementwise"] += want.pop("Gelu")
+    assert Counter(n.op_type for n in h.nodes) == want
+    shape = (CFG["batch"], 3, CFG["size"], CFG["size"])
+    calib = _calib(shape, seed=90)
+    c = QuantContainer(h, quant_type, True)
+    c.calibrate(calib)
+    x = Stream(95).normal(shape, 1.0).astype(np.float32)
+    ex = c.executor({"images": x.shape}, fuse_attention=False)
+    ex.run({"images": x})
+    worst, exact, checked = _check_against_oracle(c, h, tmp_path, x, ex)
+    assert worst <= 1 and exact >= 0.99, (worst, exact)
+    assert checked >= 20
 
 
 def _grid_close(got, want, step, exact):

@@ -3,9 +3,13 @@ independent implementation of the same wire format: the protobuf runtime,
 given a descriptor of the ONNX schema subset written here from onnx.proto's
 field numbers. Models encoded by the runtime must decode to the same
 values, models this package writes must parse in the runtime to the same
-values, and the loader must apply the reference's constant folding,
-Identity removal, Conv + BatchNorm folding and MatMul + bias fusion
-(onnx_graph.py:177-235, graph_passes.py:66-101, :507-556)."""
+values, and the loader must apply the reference's constant folding (with
+static shapes from value infos or propagated from static inputs), Identity
+removal and graph passes: Conv + BatchNorm folding, MatMul + bias fusion,
+decomposed-LayerNorm fusion, the attention-scale fold, the Gather hoist and
+the LayerNorm-affine fold (onnx_graph.py:61-79, :177-235, graph_passes.py:
+66-204, :292-569); the rewritten graph must compute what the export
+computes."""
 
 import numpy as np
 import pytest
@@ -78,7 +82,8 @@ def _schema():
         ("name", 2, F.TYPE_STRING, O, None, False),
         ("initializer", 5, F.TYPE_MESSAGE, R, "TensorProto", False),
         ("input", 11, F.TYPE_MESSAGE, R, "ValueInfoProto", False),
-        ("output", 12, F.TYPE_MESSAGE, R, "ValueInfoProto", False)])
+        ("output", 12, F.TYPE_MESSAGE, R, "ValueInfoProto", False),
+        ("value_info", 13, F.TYPE_MESSAGE, R, "ValueInfoProto", False)])
     msg("OperatorSetIdProto", [("domain", 1, F.TYPE_STRING, O, None, False),
                                ("version", 2, F.TYPE_INT64, O, None,
                                 False)])
@@ -306,3 +311,166 @@ def test_rejects_truncated_and_external_data():
     ext = t.SerializeToString() + bytes([14 << 3, 1])  # data_location = 1
     with pytest.raises(ValueError, match="external data"):
         onnx_io.decode_tensor(ext)
+
+
+def _shape_chain_model(batch, value_info):
+    """Relu(x) -> r; Reshape(r, [N, -1]) with N read from Shape(r): folded
+    only when r's shape is known statically."""
+    m = PB["ModelProto"](ir_version=8)
+    m.opset_import.add(domain="", version=13)
+    g = m.graph
+    _pb_tensor(g.initializer.add(), "zero", np.array(0, np.int64), "list")
+    _pb_tensor(g.initializer.add(), "ax0", np.array([0], np.int64), "list")
+    _pb_tensor(g.initializer.add(), "rest", np.array([-1], np.int64), "list")
+    for op, ins, outs, attrs in [
+            ("Relu", ["x"], ["r"], {}), ("Shape", ["r"], ["s"], {}),
+            ("Gather", ["s", "zero"], ["n"], {"axis": 0}),
+            ("Unsqueeze", ["n", "ax0"], ["n1"], {}),
+            ("Concat", ["n1", "rest"], ["shape"], {"axis": 0}),
+            ("Reshape", ["r", "shape"], ["y"], {})]:
+        n = g.node.add(op_type=op)
+        n.input.extend(ins)
+        n.output.extend(outs)
+        for k, v in attrs.items():
+            n.attribute.add(name=k, type=onnx_io.A_INT, i=v)
+
+    def vi(where, name, dims):
+        t = where.add(name=name).type.tensor_type
+        t.elem_type = 1
+        for d in dims:
+            if isinstance(d, str):
+                t.shape.dim.add(dim_param=d)
+            else:
+                t.shape.dim.add(dim_value=d)
+    vi(g.input, "x", [batch, 3, 4])
+    vi(g.output, "y", [batch, 12])
+    if value_info:
+        vi(g.value_info, "r", [2, 3, 4])
+    return m.SerializeToString()
+
+
+def test_shape_of_an_intermediate_folds_from_value_info_or_static_inputs():
+    """A Shape node on an intermediate tensor folds when value_info
+    declares its shape, or when the graph inputs are static (shapes
+    propagated); with a symbolic input and no value_info it stays, as ONNX
+    shape inference would leave it."""
+    for batch, info, folded in [("N", True, True), (2, False, True),
+                                ("N", False, False)]:
+        h = onnx_io.load_onnx(_shape_chain_model(batch, info))
+        ops = [n.op_type for n in h.nodes]
+        if folded:
+            assert ops == ["Relu", "Reshape"], (batch, info, ops)
+            np.testing.assert_array_equal(
+                h.initializers[h.nodes[1].inputs[1]], [2, -1])
+        else:
+            assert "Shape" in ops, ops
+
+
+def _eval_cpu(g, x):
+    """Float pass on the CPU: convolutions through the oracle's C library,
+    the rest through the oracle's float operator semantics."""
+    from oracle import abi
+    from oracle.float_ref import conv_pads, eval_node
+    lib = abi.load("oracle")
+    env = {**g.initializers, g.input_names[0]: x}
+    for n in g.nodes:
+        a = [env[i] if i else None for i in n.inputs]
+        if n.op_type == "Conv":
+            s = tuple(n.attr("strides", [1, 1]))
+            p = conv_pads(n, a[0].shape[2:], a[1].shape[2:], s, (1, 1))
+            outs = [lib.conv2d_f32(a[0], a[1], s, p, (1, 1), 1) +
+                    a[2].reshape(1, -1, 1, 1)]
+        elif n.op_type == "Gemm":
+            w = a[1].T if n.attr("transB", 0) else a[1]
+            outs = [(a[0] @ w + a[2]).astype(np.float32)]
+        elif n.op_type == "Shape":
+            outs = [np.array(a[0].shape, np.int64)]
+        else:
+            outs = eval_node(n, a, g.opset)
+        env.update(zip(n.outputs, outs))
+    return env[g.outputs[0]]
+
+
+CFG = dict(batch=2, size=32, patch=8, dim=32, depth=2, heads=4, mlp=128,
+           classes=10)
+
+
+@pytest.mark.parametrize("gelu", ["tanh", "erf"])
+def test_vit_export_loads_to_the_reference_pass_sequence(gelu):
+    """A PyTorch-style ViT export (decomposed LayerNorms, MatMul + Add
+    linears, explicit attention-scale Mul, class token expanded by a Shape
+    chain and gathered after the final LayerNorm) loads to the operator
+    multiset of :func:`graph.vit` (the reference exporter's graph after its
+    passes): 5 LayerNorms fused, 8 MatMul + bias pairs, 2 attention scales
+    folded, 1 Gather hoisted, 5 LayerNorm affines folded."""
+    from collections import Counter
+    raw = G.vit_export(gelu=gelu, **CFG)
+    h = onnx_io.load_onnx(onnx_io.save_onnx(raw))
+    assert h.fusions == {"conv_bn": 0, "matmul_bias": 8, "layernorm": 5,
+                         "elementwise": 2 if gelu == "erf" else 0,
+                         "attention_scale": 2, "hoist_gather": 1,
+                         "layernorm_affine": 5}
+    ops = Counter(n.op_type for n in h.nodes)
+    want = Counter(n.op_type for n in G.vit(seed=7, **CFG).nodes)
+    if gelu == "erf":
+        want["FusedElementwise"] += want.pop("Gelu")
+    assert ops == want
+    assert not {"Shape", "Expand", "Unsqueeze", "ReduceMean", "Pow", "Sqrt",
+                "Div", "Erf"} & set(ops)
+    init = h.initializers
+    for n in h.nodes:
+        if n.op_type == "LayerNormalization":  # the affine moved out
+            assert np.all(init[n.inputs[1]] == 1) and \
+                np.all(init[n.inputs[2]] == 0)
+    # the class-token Gather now precedes the last LayerNorm
+    order = [n.op_type for n in h.nodes]
+    assert order[-3:] == ["Gather", "LayerNormalization", "Gemm"]
+
+
+@pytest.mark.parametrize("gelu", ["tanh", "erf"])
+def test_rewritten_vit_computes_the_export(gelu):
+    """The passes are exact algebra: the loaded graph's float pass equals
+    the raw export's within float32 rounding (LayerNorm in float64 against
+    its float32 decomposition, the scale and affine folded into the
+    weights)."""
+    raw = G.vit_export(gelu=gelu, **CFG)
+    h = onnx_io.load_onnx(onnx_io.save_onnx(raw))
+    x = np.random.default_rng(3).normal(size=(2, 3, 32, 32)).astype(
+        np.float32)
+    want = _eval_cpu(raw, x)
+    got = _eval_cpu(h, x)
+    assert got.shape == want.shape == (2, 10)
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=2e-5)
+    # without the rewrites the loaded graph is the export itself
+    plain = onnx_io.load_onnx(onnx_io.save_onnx(raw), optimize=False)
+    assert plain.fusions == {}
+    np.testing.assert_allclose(_eval_cpu(plain, x), want, rtol=1e-6,
+                               atol=1e-7)
+
+
+def test_passes_decline_near_misses():
+    """Conservative matching: a LayerNorm whose mean is over another axis,
+    a scale Mul whose MatMul output has a second reader, and a LayerNorm
+    read by a non-linear layer are left alone."""
+    b = G.GraphBuilder(0, opset=13)
+    x = "x"
+    mean = b.op("ReduceMean", [x], axes=[1], keepdims=1)   # not the last
+    d = b.op("Sub", [x, mean])
+    var = b.op("ReduceMean", [b.op("Pow", [d, b.const(np.float32(2.0))])],
+               axes=[1], keepdims=1)
+    sd = b.op("Sqrt", [b.op("Add", [var, b.const(np.float32(1e-6))])])
+    y = b.op("Add", [b.op("Mul", [b.op("Div", [d, sd]),
+                                  b.const(np.ones(8, np.float32))]),
+                     b.const(np.zeros(8, np.float32))])
+    g = G.Graph(b.nodes, b.inits, {"x": [2, 4, 8]}, [y], 13)
+    h = onnx_io.load_onnx(onnx_io.save_onnx(g))
+    assert h.fusions["layernorm"] == 0
+    assert "LayerNormalization" not in {n.op_type for n in h.nodes}
+    b = G.GraphBuilder(1, opset=17)
+    ln = b.op("LayerNormalization", ["x", b.const(np.full(8, 2, np.float32)),
+                                     b.const(np.ones(8, np.float32))],
+              axis=-1)
+    y = b.op("Relu", [ln])
+    g = G.Graph(b.nodes, b.inits, {"x": [2, 4, 8]}, [y], 17)
+    h = onnx_io.load_onnx(onnx_io.save_onnx(g))
+    assert h.fusions["layernorm_affine"] == 0
