@@ -24,7 +24,11 @@ The JSON line also carries
   adds the standalone GEMM and conv at the ABI level, the int16 and ViT-S
   passes on samples, and single-thread rows;
 * the standalone requantize and SiLU-table kernels over the conv's 6.42 M
-  outputs, in HBM GB/s.
+  outputs, in HBM GB/s;
+* ``h2d_d2h``: the same pass with the float batch copied in from pinned
+  host memory and the float outputs copied back inside every step, serial
+  and with the next batch's copy overlapping the current pass (reported
+  beside ``value``, which is the device-resident rate).
 
 Tile codes of the convolutions come from the committed
 ``profiles/yolov8n_cls_b64_int8_tiles.json`` (the set the committed counter
@@ -132,6 +136,69 @@ def roofline(ops, byts, ms):
     return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
             "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4),
             "traffic": None}
+
+
+def pcie_inclusive(ex, x, steps, torch):
+    """Images/s with the float batch copied from pinned host memory and the
+    float outputs copied back to pinned host memory inside every step
+    (the device-resident rate excludes both). ``serial``: copy in, pass,
+    copy out, one after the other on one stream. ``overlapped``: the next
+    batch's host-to-device copy runs on a second stream into one of two
+    staging buffers while the current pass runs; a device copy moves it
+    into the captured graph's input before its pass."""
+    inp = ex.inputs_f32["images"]
+    outs = list(ex.outputs_f32.values())
+    host_in = torch.empty(x.shape, dtype=torch.float32, pin_memory=True)
+    host_in.copy_(torch.from_numpy(np.ascontiguousarray(x, np.float32)))
+    host_out = [torch.empty(o.shape, dtype=o.dtype, pin_memory=True)
+                for o in outs]
+    main = torch.cuda.current_stream()
+
+    def serial_step():
+        inp.copy_(host_in, non_blocking=True)
+        ex.replay()
+        for o, h in zip(outs, host_out):
+            h.copy_(o, non_blocking=True)
+
+    stage = [torch.empty_like(inp) for _ in range(2)]
+    copier = torch.cuda.Stream()  # default priority
+    ready = [torch.cuda.Event() for _ in range(2)]
+    free = [torch.cuda.Event() for _ in range(2)]
+
+    def upload(i):
+        with torch.cuda.stream(copier):
+            copier.wait_event(free[i % 2])  # its last reader has copied it
+            stage[i % 2].copy_(host_in, non_blocking=True)
+            ready[i % 2].record(copier)
+
+    def overlapped(n):
+        upload(0)
+        for i in range(n):
+            main.wait_event(ready[i % 2])
+            inp.copy_(stage[i % 2], non_blocking=True)
+            free[i % 2].record(main)
+            if i + 1 < n:
+                upload(i + 1)
+            ex.replay()
+            for o, h in zip(outs, host_out):
+                h.copy_(o, non_blocking=True)
+
+    rec = {"h2d_bytes_per_step": int(inp.numel() * inp.element_size()),
+           "d2h_bytes_per_step": int(sum(o.numel() * o.element_size()
+                                         for o in outs)),
+           "steps": steps}
+    for label, run in (("serial", lambda n: [serial_step()
+                                            for _ in range(n)]),
+                       ("overlapped", overlapped)):
+        run(3)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run(steps)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        rec[label] = {"images_per_s": round(x.shape[0] / dt, 1),
+                      "ms_per_step": round(dt * 1e3, 4)}
+    return rec
 
 
 def measure_pass(name, g, quant_type, batch, steps, tune, torch):
@@ -356,6 +423,9 @@ def main():
     dt = time.perf_counter() - t0
     ms = dt * 1e3 / args.steps
     value = B * args.steps / dt
+    # the same pass with its float input and output crossing PCIe
+    pcie = None if args.eager else pcie_inclusive(
+        ex, x, max(5, min(args.steps, 50)), torch)
 
     # ---- per-launch durations (HIP events on the launch stream) ----------
     per = []
@@ -515,6 +585,7 @@ def main():
         "kernels": kernels,
         "other_configs": extra,
         "gate": gate,
+        "h2d_d2h": pcie,
         "calibration_s": round(calib_s, 3),
         "launches_per_step": len(ex.launches),
         "top_launches_ms": [[n, round(t, 5)] for t, n, _ in per[:6]],

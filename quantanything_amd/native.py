@@ -225,7 +225,8 @@ def mbqm_np(x, mult, shift):
 
 # ------------------------------------------------------------------ GEMM ----
 def gemm_f32(a, b):
-    """``a[M,K] @ b[K,N]`` in float32 on the GPU."""
+    """Float32 matrix product of host arrays, computed by the GPU
+    library (reference wrapper: ``native.py:207-217``)."""
     lib = library()
     a, b = _c(a, np.float32), _c(b, np.float32)
     out = np.empty((a.shape[0], b.shape[1]), dtype=np.float32)
@@ -236,7 +237,9 @@ def gemm_f32(a, b):
 
 
 def gemm_int(a, b, wide=False):
-    """Integer ``a[M,K] @ b[K,N]``; int32 accumulator, int64 when ``wide``."""
+    """Exact integer matrix product of host arrays: int16 operands summed
+    in int32, or int32 operands in int64 with ``wide``
+    (``native.py:219-235``)."""
     lib = library()
     m, k = a.shape
     n = b.shape[1]
@@ -254,7 +257,8 @@ def gemm_int(a, b, wide=False):
 
 # ----------------------------------------------------------- convolution ----
 def conv_output_size(size, k, stride, pad_begin, pad_end, dilation):
-    """Spatial output size of a convolution along one axis."""
+    """Output extent along H or W: (size + both pads - dilated kernel) //
+    stride + 1 (``native.py:239-241``)."""
     return (size + pad_begin + pad_end - dilation * (k - 1) - 1) // stride + 1
 
 
@@ -277,7 +281,8 @@ def conv_geometry(x_shape, w_shape, strides, pads, dilations, groups):
 
 def conv2d_f32(x, w, strides=(1, 1), pads=(0, 0, 0, 0), dilations=(1, 1),
                groups=1):
-    """Float32 NCHW convolution, weights ``[Cout, C/groups, KH, KW]``."""
+    """Float32 convolution of an NCHW host array with OIHW weights
+    (``[Cout, C / groups, KH, KW]``) on the GPU (``native.py:282-313``)."""
     lib = library()
     x, w = _c(x, np.float32), _c(w, np.float32)
     n, c, h, wd, cout, kh, kw, sh, sw, pt, pl, dh, dw, oh, ow = conv_geometry(
@@ -344,7 +349,8 @@ def requantize(acc, outer, channels, inner, mult, shift, zp, qmin, qmax,
 
 
 def rescale(x, zp_in, mult, shift, zp_out, qmin, qmax):
-    """``clip(mbqm(x - zp_in) + zp_out)`` element-wise."""
+    """Each value moved from the input grid to the output grid:
+    mbqm(x - zp_in) + zp_out, clipped (``native.py:444-462``)."""
     lib = library()
     x = _c(x, np.int32)
     out = np.empty_like(x)
@@ -355,7 +361,9 @@ def rescale(x, zp_in, mult, shift, zp_out, qmin, qmax):
 
 
 def add(a, b, za, ma, sa, zb, mb, sb, zp_out, qmin, qmax, sign=1):
-    """Rescale both operands to the output scale and add (or subtract)."""
+    """Integer Add / Sub: each operand brought to the output scale by its
+    own fixed-point multiplier, summed with the sign, offset by the output
+    zero point and clipped (``native.py:465-493``)."""
     lib = library()
     a, b = np.broadcast_arrays(a, b)
     a, b = _c(a, np.int32), _c(b, np.int32)
@@ -368,7 +376,8 @@ def add(a, b, za, ma, sa, zb, mb, sb, zp_out, qmin, qmax, sign=1):
 
 
 def mul(a, b, za, zb, mult, shift, zp_out, qmin, qmax):
-    """``clip(mbqm((a - za) * (b - zb)) + zp_out)`` element-wise."""
+    """Integer Mul: the centred product requantized by one fixed-point
+    multiplier, offset and clipped (``native.py:496-518``)."""
     lib = library()
     a, b = np.broadcast_arrays(a, b)
     a, b = _c(a, np.int32), _c(b, np.int32)
@@ -380,7 +389,8 @@ def mul(a, b, za, zb, mult, shift, zp_out, qmin, qmax):
 
 
 def lut(x, table, offset):
-    """``table[clip(x - offset, 0, len(table) - 1)]``."""
+    """Lookup-table activation: the entry at x - offset, the index held
+    inside the table (``native.py:521-532``)."""
     lib = library()
     table = _c(table, np.int32)
     x = _c(x, np.int32)
@@ -393,7 +403,8 @@ def lut(x, table, offset):
 
 # ------------------------------------------------- float <-> integer ----
 def quantize_f32(x, scale, zp, qmin, qmax):
-    """Per-tensor quantisation of float data to int32 (half-to-even)."""
+    """float32 -> int32 with one scale and zero point: the double quotient
+    rounded half to even, clipped (``native.py:536-546``)."""
     lib = library()
     x = _c(x, np.float32)
     out = np.empty(x.shape, dtype=np.int32)
@@ -404,7 +415,8 @@ def quantize_f32(x, scale, zp, qmin, qmax):
 
 
 def dequantize_f32(q, scale, zp):
-    """Per-tensor dequantisation of int32 data to float32."""
+    """int32 -> float32 with one scale and zero point, (q - zp) * scale in
+    double (``native.py:549-556``)."""
     lib = library()
     q = _c(q, np.int32)
     out = np.empty(q.shape, dtype=np.float32)

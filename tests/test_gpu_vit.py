@@ -117,7 +117,7 @@ def test_tiny_vit_matches_oracle(hip, tmp_path, quant_type):
     ex = c.executor({"images": x.shape}, fuse_attention=False)
     ex.run({"images": x})
     worst, exact, checked = _check_against_oracle(c, g, tmp_path, x, ex)
-    assert worst <= 1 and exact >= 0.98, (worst, exact)
+    assert worst <= 1 and exact >= 0.99, (worst, exact)
     assert checked >= 20
 
 

@@ -46,7 +46,7 @@ def test_vit_s16_full_size(hip, tmp_path, monkeypatch):
     worst, exact, checked = _check_against_oracle(c, g2, tmp_path, x2, ex)
     print(f"oracle checked {checked} tensors in {time.time() - t0:.1f}s: "
           f"fallbacks within {worst} step, {exact:.4f} exact", flush=True)
-    assert worst <= 1 and exact >= 0.98, (worst, exact)
+    assert worst <= 1 and exact >= 0.99, (worst, exact)
     assert checked >= 12 * 8
 
     # the fused attention launches give the same integer pass
