@@ -110,19 +110,31 @@ def layer_work(layer, x_shape, in_bytes=1):
     return ops, byts
 
 
-def time_launch(fn, reps, torch):
-    """Average duration (ms) of `fn` on torch's current stream (HIP events)."""
-    s = torch.cuda.current_stream()
-    fn(s.cuda_stream)
+def time_launch(fn, reps, torch, per_graph=20):
+    """Average duration (ms) of one launch of `fn`: ``per_graph`` launches
+    captured back to back in one HIP graph, replayed so that about ``reps``
+    launches run, timed with HIP events on the stream the graph replays on
+    (Python's own launch cost, several microseconds a call, would otherwise
+    be timed for kernels shorter than it)."""
+    fn(torch.cuda.current_stream().cuda_stream)  # warm-up, outside capture
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream().cuda_stream
+        for _ in range(per_graph):
+            fn(s)
+    g.replay()
+    torch.cuda.synchronize()
+    n = max(1, reps // per_graph)
     e0, e1 = torch.cuda.Event(enable_timing=True), \
         torch.cuda.Event(enable_timing=True)
-    e0.record(s)
-    for _ in range(reps):
-        fn(s.cuda_stream)
-    e1.record(s)
+    e0.record()
+    for _ in range(n):
+        g.replay()
+    e1.record()
     e1.synchronize()
-    return e0.elapsed_time(e1) / reps
+    del g
+    return e0.elapsed_time(e1) / (n * per_graph)
 
 
 def roofline(ops, byts, ms):
@@ -252,9 +264,11 @@ def kernel_rows(tune, torch, steps=50):
 
             wl.launch()
             times = {}
-            for c_ in DeviceExecutor.tile_candidates(wl.d):
-                wl.d.tile = c_
-                times[c_] = DeviceExecutor._time_launch(wl.launch, 8, 3)
+            for _ in range(2):  # two rounds: the first also warms clocks
+                for c_ in DeviceExecutor.tile_candidates(wl.d):
+                    wl.d.tile = c_
+                    t = time_launch(wl.launch, 40, torch)
+                    times[c_] = min(times.get(c_, t), t)
             code = min(times, key=times.get)
             wl.d.tile = code
         kms = time_launch(wl.launch, steps, torch)
@@ -433,7 +447,7 @@ def main():
     for name, t in ex.tensors.items():
         shapes[name] = t.shape
     for name, fn in ex.launches:
-        per.append((time_launch(fn, 20, torch), name, fn))
+        per.append((time_launch(fn, 40, torch), name, fn))
     layers = {l.name: l for l in c.layers}
     # a conv's fused residual Add reads, and its Concat copy writes, one
     # more output-sized tensor

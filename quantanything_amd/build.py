@@ -46,8 +46,10 @@ def build(verbose=True):
     with ThreadPoolExecutor(max_workers=workers) as ex:
         objs = list(ex.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")
+    # -z defs: an unresolved symbol (e.g. a kernel whose launch stub the
+    # host pass did not emit) fails the link instead of the first load
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC",
-           *map(str, objs), "-o", str(tmp)]
+           "-Wl,-z,defs", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError("link failed:\n" + proc.stderr)

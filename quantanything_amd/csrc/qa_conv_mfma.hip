@@ -83,6 +83,11 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
         for (int ww = a.Cog >= 64 ? 4 : a.Cog >= 32 ? 2 : 1; ww >= 1; ww >>= 1)
             if (conv_wr_applies(b, epi, ww)) return launch_conv_wr(b, ww, st);
     }
+    // narrow GEMMs / pointwise convolutions, one 16 x 16 block a wave with
+    // all of its operands in registers (tile hint bit 13)
+    if ((a.tile_hint & TILE_VALID) && ((a.tile_hint >> 13) & 1) &&
+        gemm_narrow_applies(b, epi))
+        return launch_gemm_narrow(b, st, a.tile_hint & 1);
     // large GEMMs: 128 x 128 blocks (tile hint bit 10 chooses; its low
     // bits 3 or 4 the direct-to-LDS pipeline with that many stages)
     if (gemm_big_applies(b, epi)) {

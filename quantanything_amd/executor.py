@@ -2097,7 +2097,8 @@ class DeviceExecutor:
         width up to the output channels per group, K-split (channel-blocked
         weight layout only) and weights in LDS (where 16 rows per channel
         group of K bytes fit in the 3 KiB-chunk staging budget; the library
-        re-checks the LDS size)."""
+        re-checks the LDS size), the large-GEMM kernel and the narrow-GEMM
+        kernel where their shapes apply."""
         cog = d.Cout // d.G
         if d.w_code == 8:  # FP64 path: wm | tm << 4 | split << 8
             wm_max = 1 if cog <= 16 else 2 if cog <= 32 else 4
@@ -2113,6 +2114,12 @@ class DeviceExecutor:
             # the large-GEMM kernel (128 x 128 blocks): K steps staged
             # through registers, or through 3 / 4 LDS stages of direct loads
             out += [0x10400, 0x10403, 0x10404]
+        if d.KH == d.KW == 1 and d.G == 1 and d.w_layout == 0 and \
+                d.Cout in (16, 32, 64) and d.C % 64 == 0 and d.C <= 576 and \
+                d.epi_plan and not d.res and not d.y2:
+            # narrow GEMM: a 16 x 16 block a wave, operands in registers
+            # (0x12001, Cout 64: the activation rows staged once in LDS)
+            out += [0x12000] + ([0x12001] if d.Cout == 64 else [])
         if d.w_layout == 0 and d.G == 1 and d.C % 16 == 0 and \
                 d.OW <= 256 and d.epi_plan and (d.H > 1 or d.W > 1):
             # bands of output rows, operands in LDS (the library checks the

@@ -43,29 +43,15 @@ def _direct(x, w, x_add, pre, mult, shift, zp, lo, hi):
     return y, acc
 
 
-@pytest.mark.parametrize("cin,cout", [(16, 16), (32, 48), (3, 16)])
-def test_byte_split_ties_against_direct_sum(hip, cin, cout):
+def _run_all_tiles(lib, xs, cin, w, x_add, pre, mult, shift, zp, lo, hi,
+                   want):
+    """qa_d_conv on stored int16 activations xs [N, H, W, Cs] with every
+    byte-split and FP64 tile code; each result must equal ``want``."""
     import torch
     from quantanything_amd.executor import F64_TILES, ConvDesc
 
-    lib = hip.require()
-    rng = np.random.default_rng(cin * 100 + cout)
-    n, h, w_ = 2, 7, 6
-    cs = 4 if cin <= 4 else cin  # stored channels a pixel
-    x = rng.integers(-40, 41, size=(n, h, w_, cin))
-    xs = np.zeros((n, h, w_, cs), np.int16)
-    xs[..., :cin] = x
-    w = rng.integers(-3, 4, size=(cout, cin, 3, 3)).astype(np.int32)
-    w[0, 0, 1, 1] = 32767  # an int16 extreme (its outputs saturate)
-    x_add, zp, lo, hi = 5, 7, -32768, 32767
-    pre = rng.integers(-50, 51, size=cout).astype(np.int64)
-    mult = np.full(cout, 1 << 30, np.int64)  # odd sums: exact ties
-    shift = np.zeros(cout, np.int64)
-    mult[1::3], shift[1::3] = 3 << 28, -1     # ties at every fourth sum
-    mult[2::3], shift[2::3] = 1518500250, 2   # an ordinary multiplier
-    want, acc = _direct(xs[..., :cin], w, x_add, pre, mult, shift, zp, lo, hi)
-    assert (acc % 2 == 1).any()
-
+    n, h, w_, cs = xs.shape
+    cout = w.shape[0]
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     ck, frows = ctypes.c_int64(0), ctypes.c_int64(0)
     nf = lib.qa_pack_weights_f64_size(cout, cin, 3, 3, 1, ctypes.byref(ck),
@@ -110,3 +96,56 @@ def test_byte_split_ties_against_direct_sum(hip, cin, cout):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(bufs["y"].cpu().numpy().astype(np.int64),
                                       want, err_msg=f"tile {code:#x}")
+
+
+@pytest.mark.parametrize("cin,cout", [(16, 16), (32, 48), (3, 16)])
+def test_byte_split_ties_against_direct_sum(hip, cin, cout):
+    lib = hip.require()
+    rng = np.random.default_rng(cin * 100 + cout)
+    n, h, w_ = 2, 7, 6
+    cs = 4 if cin <= 4 else cin  # stored channels a pixel
+    x = rng.integers(-40, 41, size=(n, h, w_, cin))
+    xs = np.zeros((n, h, w_, cs), np.int16)
+    xs[..., :cin] = x
+    w = rng.integers(-3, 4, size=(cout, cin, 3, 3)).astype(np.int32)
+    w[0, 0, 1, 1] = 32767  # an int16 extreme (its outputs saturate)
+    x_add, zp, lo, hi = 5, 7, -32768, 32767
+    pre = rng.integers(-50, 51, size=cout).astype(np.int64)
+    mult = np.full(cout, 1 << 30, np.int64)  # odd sums: exact ties
+    shift = np.zeros(cout, np.int64)
+    mult[1::3], shift[1::3] = 3 << 28, -1     # ties at every fourth sum
+    mult[2::3], shift[2::3] = 1518500250, 2   # an ordinary multiplier
+    want, acc = _direct(xs[..., :cin], w, x_add, pre, mult, shift, zp, lo, hi)
+    assert (acc % 2 == 1).any()
+    _run_all_tiles(lib, xs, cin, w, x_add, pre, mult, shift, zp, lo, hi,
+                   want)
+
+
+def test_byte_split_full_int16_range(hip):
+    """Activations over the whole int16 range (-32768 included) against
+    weights at -32768 and 32767, 256 input channels (K = 2304): the high
+    bytes reach -128 and 127, so the 65536 Hh and 256 (Hl + Lh) terms and
+    the int32 headroom of each int8 MFMA sum (|xh wh| <= 2^14, K' < 2^16)
+    are exercised. Multipliers of about 2^-27 keep most outputs inside the
+    clip bounds."""
+    lib = hip.require()
+    rng = np.random.default_rng(2304)
+    n, h, w_, cin, cout = 2, 5, 4, 256, 32
+    xs = rng.integers(-32768, 32768, size=(n, h, w_, cin)).astype(np.int16)
+    xs[0, :3, :3, :] = -32768  # a full window of the extremes
+    xs[1, -3:, -3:, :] = 32767
+    w = rng.integers(-32768, 32768, size=(cout, cin, 3, 3)).astype(np.int32)
+    w[0] = -32768
+    w[1] = 32767
+    w[2, ::2] = -32768
+    w[2, 1::2] = 32767
+    x_add, zp, lo, hi = -3, 11, -32768, 32767
+    pre = rng.integers(-(1 << 40), 1 << 40, size=cout).astype(np.int64)
+    mult = rng.integers(1 << 30, 1 << 31, size=cout).astype(np.int64)
+    shift = np.full(cout, 27, np.int64)
+    shift[:3] = 33  # the extreme rows sum to about 2^41
+    want, acc = _direct(xs, w, x_add, pre, mult, shift, zp, lo, hi)
+    assert np.abs(acc).max() > 1 << 40
+    assert ((want > lo) & (want < hi)).mean() > 0.5
+    _run_all_tiles(lib, xs, cin, w, x_add, pre, mult, shift, zp, lo, hi,
+                   want)
