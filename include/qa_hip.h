@@ -571,14 +571,19 @@ int qa_d_softmax(const void* x, int in_code, int64_t rows, int64_t cols,
  * float64) with exp(F(s) - F(m)) at 256 (m + 128) + s + 128 for stored
  * bytes s <= m, F(b) = float32((b + in_so - in_zp) * in_scale), once per
  * input quantization; qa_d_softmax_lut then reads a row's exponentials at
- * its largest byte (int8 input and output, cols <= 512). The reference
- * computes exp per element (float_ops.py:380-385). */
+ * its largest byte (int8 input and output, cols <= 1024). The reference
+ * computes exp per element (float_ops.py:380-385). qa_d_softmax_lut_f32
+ * also writes the dequantized result to out_f32, as qa_d_softmax_f32. */
 int qa_d_softmax_table(double in_scale, int64_t in_zp, int64_t in_so,
                        double* table, void* stream);
 int qa_d_softmax_lut(const void* x, int64_t rows, int64_t cols,
                      const double* table, void* out, double out_scale,
                      int64_t out_zp, int64_t qmin, int64_t qmax,
                      int64_t out_so, void* stream);
+int qa_d_softmax_lut_f32(const void* x, int64_t rows, int64_t cols,
+                         const double* table, void* out, double out_scale,
+                         int64_t out_zp, int64_t qmin, int64_t qmax,
+                         int64_t out_so, float* out_f32, void* stream);
 
 /* qa_d_softmax that also writes the dequantized result to out_f32
  * ([rows, cols] float32, (q - out_zp) * out_scale as qa_d_dequantize_f32

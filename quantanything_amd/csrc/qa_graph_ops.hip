@@ -388,12 +388,14 @@ __global__ __launch_bounds__(kThreads) void k_softmax_table(
 
 // k_softmax_rows for int8 input and output with the exponentials read from
 // k_softmax_table: the same float64 values, summed in the same order, so
-// the results are those of k_softmax_rows.
+// the results are those of k_softmax_rows. outf (optional): the dequantized
+// output, as k_softmax_rows writes it.
 template <int GS, int PER>
 __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
     const int8_t* __restrict__ x, int64_t rows, int64_t cols,
     const double* __restrict__ t, int8_t* __restrict__ out, double out_scale,
-    int64_t out_zp, int64_t qmin, int64_t qmax, int64_t out_so) {
+    int64_t out_zp, int64_t qmin, int64_t qmax, int64_t out_so,
+    float* __restrict__ outf) {
     constexpr int RPW = 64 / GS;  // rows per wave
     const int lane = threadIdx.x & 63;
     const int gl = lane % GS;
@@ -435,8 +437,37 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
             const int64_t q = qa_quantize_mixed(y, f32ok, invf, out_scale, inv,
                                                 out_zp, qmin, qmax);
             out[base + i] = (int8_t)(q - out_so);
+            if (outf) outf[base + i] = (float)((double)(q - out_zp) * out_scale);
         }
     }
+}
+
+// Rows of the table path: 16 lanes a row up to 256 columns, a wave a row up
+// to 512 (8 values a lane) or 1024 (16 a lane).
+bool softmax_lut_launch(const int8_t* x, int64_t rows, int64_t cols,
+                        const double* t, int8_t* out, double out_scale,
+                        int64_t out_zp, int64_t qmin, int64_t qmax,
+                        int64_t out_so, float* outf, hipStream_t st) {
+    if (cols <= 16 * 16) {
+        const int64_t blocks = std::min<int64_t>((rows + 15) / 16, 65535);
+        k_softmax_rows_lut<16, 16><<<(unsigned)blocks, kThreads, 0, st>>>(
+            x, rows, cols, t, out, out_scale, out_zp, qmin, qmax, out_so,
+            outf);
+        return true;
+    }
+    const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
+    if (cols <= 64 * SOFTMAX_PER)
+        k_softmax_rows_lut<64, SOFTMAX_PER><<<(unsigned)blocks, kThreads, 0,
+                                              st>>>(
+            x, rows, cols, t, out, out_scale, out_zp, qmin, qmax, out_so,
+            outf);
+    else if (cols <= 64 * 16)
+        k_softmax_rows_lut<64, 16><<<(unsigned)blocks, kThreads, 0, st>>>(
+            x, rows, cols, t, out, out_scale, out_zp, qmin, qmax, out_so,
+            outf);
+    else
+        return false;
+    return true;
 }
 
 bool softmax_launch(const void* x, int in_code, int64_t rows, int64_t cols,
@@ -453,16 +484,24 @@ bool softmax_launch(const void* x, int in_code, int64_t rows, int64_t cols,
                                              st>>>(
                 (const TI*)x, rows, cols, in_scale, in_zp, in_so, (TO*)out,
                 out_scale, out_zp, qmin, qmax, out_so, outf);
-        } else {
+        } else if (cols <= 64 * SOFTMAX_PER) {  // a wave a row
             const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
             k_softmax_rows<64, SOFTMAX_PER, TI, TO><<<(unsigned)blocks,
                                                       kThreads, 0, st>>>(
                 (const TI*)x, rows, cols, in_scale, in_zp, in_so, (TO*)out,
                 out_scale, out_zp, qmin, qmax, out_so, outf);
+        } else {  // a wave a row, 16 values a lane
+            const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
+            k_softmax_rows<64, 16, TI, TO><<<(unsigned)blocks, kThreads, 0,
+                                             st>>>(
+                (const TI*)x, rows, cols, in_scale, in_zp, in_so, (TO*)out,
+                out_scale, out_zp, qmin, qmax, out_so, outf);
         }
     };
+    // rows of at most 1024 values in registers (the table path,
+    // qa_d_softmax_lut, sums its exponentials in the same order)
     const bool same = in_code == out_code && (in_code == 1 || in_code == 2);
-    if (same && cols <= 64 * SOFTMAX_PER) {
+    if (same && cols <= 64 * 16) {
         if (in_code == 1)
             rows_kernel(int8_t{}, int8_t{});
         else
@@ -622,25 +661,34 @@ QA_API int qa_d_softmax_lut(const void* x, int64_t rows, int64_t cols,
                             int64_t out_zp, int64_t qmin, int64_t qmax,
                             int64_t out_so, void* stream) {
     if (rows <= 0 || cols <= 0) return 0;
-    if (!table || cols > 64 * SOFTMAX_PER) {
-        qa::set_error("qa_d_softmax_lut", "needs a table and at most 512 "
+    if (!table || !softmax_lut_launch((const int8_t*)x, rows, cols, table,
+                                      (int8_t*)out, out_scale, out_zp, qmin,
+                                      qmax, out_so, nullptr,
+                                      (hipStream_t)stream)) {
+        qa::set_error("qa_d_softmax_lut", "needs a table and at most 1024 "
                                           "columns");
         return -1;
     }
-    hipStream_t st = (hipStream_t)stream;
-    if (cols <= 16 * 16) {
-        const int64_t blocks = std::min<int64_t>((rows + 15) / 16, 65535);
-        k_softmax_rows_lut<16, 16><<<(unsigned)blocks, kThreads, 0, st>>>(
-            (const int8_t*)x, rows, cols, table, (int8_t*)out, out_scale,
-            out_zp, qmin, qmax, out_so);
-    } else {
-        const int64_t blocks = std::min<int64_t>((rows + 3) / 4, 65535);
-        k_softmax_rows_lut<64, SOFTMAX_PER><<<(unsigned)blocks, kThreads, 0,
-                                              st>>>(
-            (const int8_t*)x, rows, cols, table, (int8_t*)out, out_scale,
-            out_zp, qmin, qmax, out_so);
-    }
     return launched("qa_d_softmax_lut") ? 0 : -1;
+}
+
+// qa_d_softmax_lut that also writes the dequantized output (float32, same
+// [rows, cols] layout) for a graph output.
+QA_API int qa_d_softmax_lut_f32(const void* x, int64_t rows, int64_t cols,
+                                const double* table, void* out,
+                                double out_scale, int64_t out_zp,
+                                int64_t qmin, int64_t qmax, int64_t out_so,
+                                float* out_f32, void* stream) {
+    if (rows <= 0 || cols <= 0) return 0;
+    if (!table || !out_f32 ||
+        !softmax_lut_launch((const int8_t*)x, rows, cols, table,
+                            (int8_t*)out, out_scale, out_zp, qmin, qmax,
+                            out_so, out_f32, (hipStream_t)stream)) {
+        qa::set_error("qa_d_softmax_lut_f32", "needs a table, a float output "
+                                              "and at most 1024 columns");
+        return -1;
+    }
+    return launched("qa_d_softmax_lut_f32") ? 0 : -1;
 }
 
 // qa_d_softmax that also writes the dequantized output (float32, same

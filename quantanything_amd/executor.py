@@ -684,10 +684,8 @@ class DeviceExecutor:
             self.outputs_f32[name] = yf
             sm = self.softmax_of.get(name)
             if sm is not None:  # the Softmax writes the float copy too
-                lname, args = sm
-                fused = (lname, lambda s, args=args, yf=yf: _ok(
-                    self.lib.qa_d_softmax_f32(*args, yf.data_ptr(), s),
-                    "qa_d_softmax_f32"))
+                lname, with_f32 = sm
+                fused = (lname, lambda s, f=with_f32, yf=yf: f(s, yf))
                 self.launches = [fused if n == lname else (n, f)
                                  for n, f in self.launches]
                 continue
@@ -1671,8 +1669,11 @@ class DeviceExecutor:
             args = (x.ptr, x.code, rows, cols, iq.scale, iq.zp, x.so, y.ptr,
                     y.code, o.scale, o.zp, o.qmin, o.qmax, y.so)
             lname = f"softmax:{layer.name}"
-            self.softmax_of[layer.node.outputs[0]] = (lname, args)
-            if x.code == 1 and y.code == 1 and cols <= 512:
+            # for a graph output: the same launch writing the float copy too
+            self.softmax_of[layer.node.outputs[0]] = (
+                lname, lambda s, yf: _ok(self.lib.qa_d_softmax_f32(
+                    *args, yf.data_ptr(), s), "qa_d_softmax_f32"))
+            if x.code == 1 and y.code == 1 and cols <= 1024:
                 # int8: exponentials from a table built once per layer
                 tab = torch.empty(65536, dtype=torch.float64, device="cuda")
                 _ok(self.lib.qa_d_softmax_table(
@@ -1687,6 +1688,9 @@ class DeviceExecutor:
                     lname, layer.data_inputs[0], x.ptr, tab, o, y.so)
                 self._add(lname, lambda s: _ok(
                     self.lib.qa_d_softmax_lut(*largs, s), "qa_d_softmax_lut"))
+                self.softmax_of[layer.node.outputs[0]] = (
+                    lname, lambda s, yf: _ok(self.lib.qa_d_softmax_lut_f32(
+                        *largs, yf.data_ptr(), s), "qa_d_softmax_lut_f32"))
             else:
                 self._add(lname, lambda s: _ok(
                     self.lib.qa_d_softmax(*args, s), "qa_d_softmax"))

@@ -100,6 +100,8 @@ def _declare(lib):
         "qa_d_softmax_table": (i32, [f64, i64, i64, p, p]),
         "qa_d_softmax_lut": (i32, [p, i64, i64, p, p, f64, i64, i64, i64, i64,
                                    p]),
+        "qa_d_softmax_lut_f32": (i32, [p, i64, i64, p, p, f64, i64, i64, i64,
+                                       i64, p, p]),
         "qa_d_softmax_f32": (i32, [p, i32, i64, i64, f64, i64, i64, p, i32,
                                    f64] + [i64] * 4 + [p, p]),
         "qa_d_quantize_f32": (i32, [p, p, i32, i64, f64, i64, i64, i64, i64,

@@ -219,11 +219,13 @@ def test_large_gemm_kernel_bit_exact(hip, tmp_path, quant_type, m, k, n, act,
 
 
 @pytest.mark.parametrize("rows,cols", [(37, 17), (64, 197), (9, 256),
-                                       (12, 300), (5, 512)])
+                                       (12, 300), (5, 512), (64, 1000),
+                                       (3, 1024)])
 def test_softmax_table_equals_direct(hip, rows, cols):
     """The int8 Softmax through the table of exponentials stores exactly
     what the per-element float64 form stores (same exponentials, same
-    summation order), rows of mixed byte ranges included."""
+    summation order), rows of mixed byte ranges included; the forms that
+    also write the dequantized graph output agree on it."""
     import torch
     lib = hip.require()
     rng = np.random.default_rng(rows * 1000 + cols)
@@ -247,3 +249,17 @@ def test_softmax_table_equals_direct(hip, rows, cols):
                                 o_so, s) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(yb.cpu().numpy(), ya.cpu().numpy())
+    fa = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    fb = torch.empty_like(fa)
+    assert lib.qa_d_softmax_f32(xd.data_ptr(), 1, rows, cols, in_scale,
+                                in_zp, in_so, ya.data_ptr(), 1, o_scale, o_zp,
+                                -128, 127, o_so, fa.data_ptr(), s) == 0
+    assert lib.qa_d_softmax_lut_f32(xd.data_ptr(), rows, cols,
+                                    tab.data_ptr(), yb.data_ptr(), o_scale,
+                                    o_zp, -128, 127, o_so, fb.data_ptr(),
+                                    s) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(yb.cpu().numpy(), ya.cpu().numpy())
+    np.testing.assert_array_equal(fb.cpu().numpy(), fa.cpu().numpy())
+    want = (ya.cpu().numpy().astype(np.float64) - o_zp) * o_scale
+    np.testing.assert_array_equal(fa.cpu().numpy(), want.astype(np.float32))
