@@ -649,3 +649,153 @@ def test_fake_quantized_conv_on_a_dyadic_grid():
         q = round(exact / 2)  # Python's round: half to even
         q = min(max(q, -128), 127)
         assert got[0, o, oy, ox] == np.float32(q * 2.0), (o, oy, ox)
+
+
+# ------------------------------------- Add / Mul / Concat / Gemm steps --
+def _graph1(node, inits, shapes):
+    return Graph([node], inits, shapes, list(node.outputs))
+
+
+def test_add_sub_mul_concat_on_dyadic_scales():
+    """Each operand brought to the output scale by its own fixed-point
+    multiplier (AddQuantize: in_scale / out_scale, rounded half up per
+    operand, then the sign), Mul by (s_a s_b / s_out), Concat a plain copy
+    for equal parameters and a rescale otherwise, with zero points removed
+    and added back: hand-worked with power-of-two scales. Swapped
+    multipliers, a dropped zero point or a sign applied before the rounding
+    fail."""
+    a = np.array([[0, 1, 7, -9, 250]], np.int32)
+    b = np.array([[5, 3, -3, 4, 1]], np.int32)
+    qa_, qb_ = (0.5, 3, 0, 255), (0.25, -2, -128, 127)
+    for op, sign in (("Add", 1), ("Sub", -1)):
+        g = _graph1(Node("n", op, ["a", "b"], ["y"]), {},
+                    {"a": [1, 5], "b": [1, 5]})
+        qj = _qj("uint8", {"a": qa_, "b": qb_, "y": (0.5, 10, 0, 255)})
+        ints, _ = OraclePipeline(g, qj).run_integers({"a": a, "b": b})
+        want = [min(max((int(x) - 3) + sign * math.floor((int(y) + 2) / 2 +
+                                                         0.5) + 10, 0), 255)
+                for x, y in zip(a[0], b[0])]
+        np.testing.assert_array_equal(ints["y"][0], want)
+    g = _graph1(Node("n", "Mul", ["a", "b"], ["y"]), {},
+                {"a": [1, 5], "b": [1, 5]})
+    qj = _qj("uint8", {"a": qa_, "b": qb_, "y": (0.5, 10, 0, 255)})
+    ints, _ = OraclePipeline(g, qj).run_integers({"a": a, "b": b})
+    want = [min(max(math.floor((int(x) - 3) * (int(y) + 2) / 4 + 0.5) + 10,
+                    0), 255) for x, y in zip(a[0], b[0])]
+    np.testing.assert_array_equal(ints["y"][0], want)
+    # Concat: the first input shares the output's parameters (copied and
+    # clipped), the second is rescaled by 0.25 / 0.5
+    g = _graph1(Node("n", "Concat", ["a", "b"], ["y"], {"axis": 1}), {},
+                {"a": [1, 5], "b": [1, 5]})
+    qj = _qj("uint8", {"a": (0.5, 10, 0, 255), "b": qb_,
+                       "y": (0.5, 10, 0, 255)})
+    ints, _ = OraclePipeline(g, qj).run_integers({"a": a, "b": b})
+    want = [min(max(int(x), 0), 255) for x in a[0]] + \
+        [math.floor((int(y) + 2) / 2 + 0.5) + 10 for y in b[0]]
+    np.testing.assert_array_equal(ints["y"][0], want)
+
+
+def test_add_of_a_constant_operand():
+    """A constant operand of Add is quantized with its own q.json entry and
+    then added like an activation (quant_layers.py:476-513)."""
+    c = np.array([[1.0, -0.5, 2.25]], np.float32)
+    g = _graph1(Node("n", "Add", ["x", "c"], ["y"]), {"c": c},
+                {"x": [1, 3]})
+    qj = _qj("int8", {"x": (0.25, 0, -128, 127), "c": (0.25, 0, -128, 127),
+                      "y": (0.25, 0, -128, 127)})
+    ints, _ = OraclePipeline(g, qj).run_integers(
+        {"x": np.array([[4, 4, 4]], np.int32)})
+    np.testing.assert_array_equal(ints["y"][0], [4 + 4, 4 - 2, 4 + 9])
+
+
+def test_gemm_transb_alpha_beta_dyadic():
+    """Gemm with transB, alpha and beta: weights W^T * alpha quantized per
+    output column (scale 1/64 here), bias beta * C rounded half to even on
+    the s_in * s_w grid, the accumulator requantized by an exact power of
+    two: every output equals the Python-integer evaluation. A missing
+    transpose, alpha or beta fails."""
+    rng = np.random.default_rng(9)
+    n, k = 3, 8
+    wq = rng.integers(-127, 128, size=(n, k))
+    wq[:, 0] = 127  # per-column |max| = 127 -> scale 1/64 after alpha
+    w = (wq / 32.0).astype(np.float32)  # alpha 0.5 halves it
+    cb = np.array([0.3, -1.1, 4.0], np.float32)
+    node = Node("g", "Gemm", ["x", "w", "c"], ["y"],
+                {"transB": 1, "alpha": 0.5, "beta": 2.0})
+    g = _graph1(node, {"w": w, "c": cb}, {"x": [2, k]})
+    qj = _qj("int8", {"x": (0.5, 0, -128, 127), "y": (2.0, 0, -128, 127),
+                      "w": (1.0, 0, -128, 127), "c": (1.0, 0, -128, 127)})
+    x = rng.integers(-128, 128, size=(2, k)).astype(np.int32)
+    ints, _ = OraclePipeline(g, qj).run_integers({"x": x})
+    s = Fraction(1, 2) * Fraction(1, 64)  # s_in * s_w
+    for i in range(2):
+        for j in range(n):
+            acc = sum(int(x[i, kk]) * int(wq[j, kk]) for kk in range(k))
+            bq = round(Fraction(float(np.float32(cb[j] * np.float32(2.0))))
+                       / s)
+            y = (acc + bq) * s / 2  # the real output, exactly
+            want = min(max(math.floor(y + Fraction(1, 2)), -128), 127)
+            assert ints["y"][i, j] == want, (i, j)
+
+
+# ----------------------------------------- float shape operators etc. --
+def test_shape_operators_by_index_arithmetic():
+    """Split (sizes input, attribute, equal parts), Flatten (axis, negative
+    axis), Reshape (0 copies a dimension unless allowzero, -1 infers),
+    Transpose (a permutation, default reversal) and Concat along the last
+    axis, each checked by element index."""
+    x = np.arange(2 * 3 * 4).reshape(2, 3, 4)
+    a, b = eval_node(_node("Split", axis=1), [x, np.array([1, 2])])
+    assert a.shape == (2, 1, 4) and b.shape == (2, 2, 4)
+    assert b[1, 1, 3] == x[1, 2, 3]
+    parts = eval_node(Node("n", "Split", ["a"], ["p", "q"], {"axis": -1}),
+                      [x])
+    assert [p.shape for p in parts] == [(2, 3, 2)] * 2
+    assert parts[1][0, 2, 1] == x[0, 2, 3]
+    assert eval_node(_node("Flatten", axis=2), [x])[0].shape == (6, 4)
+    f = eval_node(_node("Flatten", axis=-1), [x])[0]
+    assert f.shape == (6, 4) and f[5, 3] == x[1, 2, 3]
+    r = eval_node(_node("Reshape"), [x, np.array([0, -1])])[0]
+    assert r.shape == (2, 12) and r[1, 11] == 23
+    z = eval_node(_node("Reshape", allowzero=1),
+                  [np.zeros((0, 3)), np.array([3, 0])])[0]
+    assert z.shape == (3, 0)
+    t = eval_node(_node("Transpose", perm=[2, 0, 1]), [x])[0]
+    assert t.shape == (4, 2, 3) and t[3, 1, 2] == x[1, 2, 3]
+    t = eval_node(_node("Transpose"), [x])[0]
+    assert t.shape == (4, 3, 2) and t[3, 2, 1] == x[1, 2, 3]
+    c = eval_node(_node("Concat", axis=-1), [x, 100 + x])[0]
+    assert c.shape == (2, 3, 8) and c[1, 2, 7] == 123 and c[1, 2, 3] == 23
+
+
+def test_clip_abs_neg_relu_gap_bn():
+    """Clip from attributes or inputs (an absent bound is open), Abs, Neg,
+    Relu, the float GlobalAveragePool as a mean over H and W, and the float
+    BatchNormalization as gamma (x - mean) / sqrt(var + eps) + beta."""
+    x = np.array([[-3.0, -0.5, 0.0, 0.5, 3.0]], np.float32)
+    np.testing.assert_array_equal(
+        eval_node(_node("Clip", min=-1.0, max=1.0), [x])[0],
+        [[-1, -0.5, 0, 0.5, 1]])
+    np.testing.assert_array_equal(
+        eval_node(_node("Clip"), [x, np.float32(0.0), None])[0],
+        [[0, 0, 0, 0.5, 3]])
+    np.testing.assert_array_equal(eval_node(_node("Abs"), [x])[0],
+                                  [[3, 0.5, 0, 0.5, 3]])
+    np.testing.assert_array_equal(eval_node(_node("Neg"), [x])[0], -x)
+    np.testing.assert_array_equal(eval_node(_node("Relu"), [x])[0],
+                                  [[0, 0, 0, 0.5, 3]])
+    img = np.arange(2 * 3 * 2 * 4, dtype=np.float32).reshape(2, 3, 2, 4)
+    gap = eval_node(_node("GlobalAveragePool"), [img])[0]
+    assert gap.shape == (2, 3, 1, 1) and gap[1, 2, 0, 0] == np.float32(
+        img[1, 2].sum() / 8)
+    g_, b_ = np.array([2.0, 0.5, 1.0], np.float32), np.array(
+        [1.0, 0.0, -1.0], np.float32)
+    m_, v_ = np.array([1.0, 2.0, 0.0], np.float32), np.array(
+        [3.0, 0.0, 1.0], np.float32)
+    y = eval_node(_node("BatchNormalization", epsilon=1.0),
+                  [img, g_, b_, m_, v_])[0]
+    # sqrt(var + 1) = 2, 1, sqrt(2): exact for the first two channels
+    np.testing.assert_array_equal(y[:, 0], (img[:, 0] - 1) * 1.0 + 1.0)
+    np.testing.assert_array_equal(y[:, 1], (img[:, 1] - 2) * 0.5)
+    np.testing.assert_allclose(y[:, 2], img[:, 2] / np.sqrt(2) - 1,
+                               rtol=1e-6)
