@@ -7,19 +7,28 @@
 //      float32 and quantized (qa_quantize_mixed) with S's parameters;
 //   P: exponentials from the qa_d_softmax_table table of S's quantization,
 //      summed per lane in column order (columns col + 16 nt of a row sit in
-//      lane col, nt = 0..15, exactly the 16-lanes-a-row layout of
+//      lane col, nt = 0, 1, .., exactly the 16-lanes-a-row layout of
 //      k_softmax_rows_lut<16, 16>), then across the row's 16 lanes by xor
 //      shuffles 8, 4, 2, 1, one float64 reciprocal a row;
 //   O: as S, from P and v.
 //
-// A work-group owns one (b0, b1) pair and a run of 16-row tiles of S / O:
-// it stages k (S's columns, as rows of depth K), v^T (O's columns, as rows
-// of depth N_S) and its q rows in LDS, zero-padded to the MFMA depth; each
-// wave takes tiles in turn. Per tile: S's 16 x N_S accumulators in
-// registers (MFMA C layout: lane col + 16 kg holds rows 4 kg + r, column
-// col + 16 nt), S quantized and the Softmax row by row in registers, P's
-// bytes to the wave's LDS tile (rows of N_S rounded up to 64, zero past
-// N_S), read back as the A operand of O = P v.
+// A work-group owns one (b0, b1) pair and 4 tiles of 16 query rows, one a
+// wave. It stages k (rows of depth K) and v^T (rows of depth N_S) in LDS,
+// zero-padded to the MFMA depth. S = q k^T leaves lane (col, kg) holding
+// rows 4 kg + r, column 16 nt + col of every 16-column block nt, so one
+// load of the exponential table serves 4 rows of the tile (4 table rows a
+// wave-wide gather: about half the address-unit time of 16). P's bytes go
+// to the wave's LDS tile row by row and come back as 16-byte fragments of
+// O^T = v^T P^T, whose lane holds 4 consecutive features of one row (one
+// word store).
+//
+// Per value: the float32 quantization (multiply, round, one fma for the
+// tie test, one med3 clip) and v_cvt_pk_u8_f32, which converts the clipped
+// value biased by 128 - so to its byte; a group of four whose tie test
+// fails in any lane is requantized by the double form. Every loop over the
+// 16-column blocks is branch-free (blocks past the launch's repeat the
+// last block's k rows and count as columns past N_S), so each phase has
+// all of its loads in flight at once.
 #include "../../include/qa_hip.h"
 #include "qa_conv_mfma.h"
 
@@ -29,7 +38,6 @@ namespace {
 typedef int v4a __attribute__((ext_vector_type(4)));
 
 constexpr int QA_ATT_KSQ = 2;  // q / k depth up to 128 bytes
-constexpr int QA_ATT_U = 8;    // staging chunks a thread has in flight
 
 struct AttnGeom {
     int NpS;       // S columns rounded up to 16 (at most 256)
@@ -38,15 +46,18 @@ struct AttnGeom {
     int NV;        // O columns rounded up to 16
     int RSK, RSV;  // LDS row strides (bytes) of depth KpQ / KpV rows
     int tiles;     // 16-row tiles of S and O per (b0, b1)
-    int tpw;       // tiles per work-group
+    int tpw;       // tiles per work-group (one a wave)
 };
 
 // One quantization's constants: qa_quantize_mixed's arguments and the
-// float32 form's threshold and bounds (qa_quantize_f32), precomputed.
+// float32 form's threshold (-1 where that form does not apply), and the
+// clip bounds and zero point biased by 128 - so (the stored byte + 128).
+// wrap: the clip range reaches past the int8 storage, whose bytes then
+// wrap around (the stored byte is q - so modulo 256).
 struct AttnQ {
     double scale, inv;
-    float invf, tie, zpf, qminf, qmaxf;
-    int zp, qmin, qmax, so, f32;
+    float invf, tie, cb, lob, hib;
+    int zp, qmin, qmax, so, wrap;
 };
 
 // The fused launch's operands and constants, compacted on the host.
@@ -59,38 +70,71 @@ struct AttnArgs {
     int64_t y_s0, y_s1, y_sm, y_sn;
     const double* table;
     int B1, M, Ns, Kq, No;
+    int oword;      // O rows stored a word (4 features) at a time
     double sS, sO;  // a_scale * b_scale of q k^T and of P v
     AttnQ S, P, O;
 };
 
-// qa_quantize_mixed with the constants precomputed, split: quant_fast is
-// the float32 form (qa_quantize_f32) and sets *slow where that form does not
-// decide (near-ties, NaN, or the scales outside the form); those values are
-// recomputed by quant_exact, the double form, called out of line so that
-// its registers stay out of the callers' loops. Together they return
-// qa_quantize_mixed's value.
+// qa_quantize_mixed's double form, out of line so that its registers stay
+// out of the callers' loops.
 __device__ __noinline__ int quant_exact(float y, double scale, double inv,
                                         int zp, int qmin, int qmax) {
     return (int)qa_quantize_one_fast(y, scale, inv, zp, qmin, qmax);
 }
 
-__device__ __forceinline__ int quant_fast(float y, const AttnQ& c,
-                                          bool* slow) {
+// quantize(y) + 128 - so by the float32 form (qa_quantize_f32, its clip on
+// the biased bounds); sets slow where that form does not decide.
+__device__ __forceinline__ float qb_fast(float y, const AttnQ& c, bool& slow) {
     const float r = rintf(y * c.invf);
     const float dd = fmaf(y, c.invf, -r);
-    *slow = !(c.f32 && fabsf(dd) < c.tie);
-    return (int)__builtin_amdgcn_fmed3f(r + c.zpf, c.qminf, c.qmaxf);
+    slow |= !(fabsf(dd) < c.tie);
+    return __builtin_amdgcn_fmed3f(r + c.cb, c.lob, c.hib);
 }
 
-__device__ __forceinline__ int quant_slow(float y, const AttnQ& c) {
-    return quant_exact(y, c.scale, c.inv, c.zp, c.qmin, c.qmax);
+__device__ __forceinline__ float qb_exact(float y, const AttnQ& c) {
+    return (float)(quant_exact(y, c.scale, c.inv, c.zp, c.qmin, c.qmax) -
+                   c.so + 128);
 }
 
-__global__ __launch_bounds__(256) void k_attention(AttnArgs d, AttnGeom g) {
+// biased values of a storage that wraps, taken modulo 256 (a branch that
+// is uniform: the flag is a kernel argument)
+__device__ __forceinline__ void wrap_u8(float (&b)[4], const AttnQ& c) {
+    if (c.wrap) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) b[r] = (float)((int)b[r] & 255);
+    }
+}
+
+// four biased values (integers in [0, 255]) as the bytes of one word
+__device__ __forceinline__ uint32_t pack_u8(const float (&b)[4]) {
+    uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(b[0], 0, 0u);
+    w = __builtin_amdgcn_cvt_pk_u8_f32(b[1], 1, w);
+    w = __builtin_amdgcn_cvt_pk_u8_f32(b[2], 2, w);
+    return __builtin_amdgcn_cvt_pk_u8_f32(b[3], 3, w);
+}
+
+// the 4 x 4 byte transpose of words a, b, c, d (rows) into o[0..3]
+// (columns): o[j] = a.j | b.j << 8 | c.j << 16 | d.j << 24
+__device__ __forceinline__ void transpose4(uint32_t a, uint32_t b, uint32_t c,
+                                           uint32_t d, uint32_t* o) {
+    const uint32_t ab0 = __builtin_amdgcn_perm(b, a, 0x05010400u);
+    const uint32_t ab1 = __builtin_amdgcn_perm(b, a, 0x07030602u);
+    const uint32_t cd0 = __builtin_amdgcn_perm(d, c, 0x05010400u);
+    const uint32_t cd1 = __builtin_amdgcn_perm(d, c, 0x07030602u);
+    o[0] = __builtin_amdgcn_perm(cd0, ab0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(cd0, ab0, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(cd1, ab1, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(cd1, ab1, 0x07060302u);
+}
+
+// NTS: 16-column blocks of S the kernel holds (>= the launch's NpS / 16);
+// KSQ: 64-byte K-steps of q k^T (>= KpQ / 64).
+template <int NTS, int KSQ>
+__global__ __launch_bounds__(256, 3) void k_attention(AttnArgs d, AttnGeom g) {
     extern __shared__ int4 lds4[];
-    int8_t* sk = (int8_t*)lds4;              // [NpS][RSK]  k rows
-    int8_t* sv = sk + g.NpS * g.RSK;          // [NV][RSV]   v^T rows
-    int8_t* sp = sv + g.NV * g.RSV;           // [4][16][RSV] S / P tiles
+    int8_t* sk = (int8_t*)lds4;       // [NpS][RSK]  k rows
+    int8_t* sv = sk + g.NpS * g.RSK;  // [NV][RSV]   v^T rows
+    int8_t* sp = sv + g.NV * g.RSV;   // [4][16][RSV] P tiles
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kg = lane >> 4;
@@ -99,253 +143,229 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs d, AttnGeom g) {
     const XcdBlock blk = xcd_block(false);
     const int64_t bz = blk.y;
     const int64_t b0 = bz / d.B1, b1 = bz - b0 * d.B1;
-    const int rt0 = (int)blk.x * g.tpw;
-    const int rt1 = min(rt0 + g.tpw, g.tiles);
+    const int rt = (int)blk.x * g.tpw + wave;  // the wave's tile
+    const int64_t m0 = (int64_t)rt * 16;
 
-    // the wave's q fragments of tile rt (rows past M read row M - 1,
-    // bytes past K are zero); the first tile's are requested before the
-    // staging below
-    const int8_t* qb = d.q + b0 * d.q_s0 + b1 * d.q_s1;
-    const int ksq = g.KpQ >> 6;
-    v4a fa[QA_ATT_KSQ];
-    auto load_q = [&](int rt) {
-        const int8_t* qr =
-            qb + min((int64_t)rt * 16 + col, (int64_t)d.M - 1) * d.q_sm;
+    // the lane's q fragments (row m0 + col, clamped; bytes past K are
+    // zero), requested before the staging
+    v4a fq[KSQ];
+    {
+        const int8_t* qr = d.q + b0 * d.q_s0 + b1 * d.q_s1 +
+                           min(m0 + col, (int64_t)d.M - 1) * d.q_sm;
 #pragma unroll
-        for (int ks = 0; ks < QA_ATT_KSQ; ++ks) {
+        for (int ks = 0; ks < KSQ; ++ks) {
             const int c = ks * 64 + kg * 16;
-            fa[ks] = v4a{0, 0, 0, 0};
-            if (ks < ksq && c < d.Kq) fa[ks] = *(const v4a*)(qr + c);
+            fq[ks] = v4a{0, 0, 0, 0};
+            if (c < d.Kq) fq[ks] = *(const v4a*)(qr + c);
         }
-    };
-    load_q(rt0 + wave);
+    }
 
-    // ---- staging: k rows (16-byte chunks along the depth) and v^T rows
-    // (16 consecutive v columns of one row per chunk, scattered to 16 LDS
-    // rows), zero past N_S and the depth; every load of the thread in
-    // flight before the first store ----
+    // ---- staging: k rows as 16-byte chunks; v^T 16 words a thread (4
+    // keys x 16 features, transposed in registers), keys past N_S zero;
+    // a round's loads all in flight before its stores ----
     {
         const int8_t* kb = d.k + b0 * d.k_s0 + b1 * d.k_s1;
         const int8_t* vb = d.v + b0 * d.v_s0 + b1 * d.v_s1;
         const int cpr = g.KpQ >> 4;        // k chunks per row
         const int nk = g.NpS * cpr;        // k chunks
-        const int nvr = g.NV >> 4;         // v^T row groups
-        const int nch = nk + nvr * g.KpV;  // all chunks
-        for (int e0 = tid; e0 < nch; e0 += QA_ATT_U * 256) {
-            v4a ch[QA_ATT_U];
+        const int nq = g.KpV >> 2;         // key quads
+        const int nvj = nq * (g.NV >> 4);  // v^T jobs (key quad, 16 features)
+        for (int e0 = tid, j = tid; e0 < nk || j < nvj;
+             e0 += 4 * 256, j += 256) {
+            v4a kc[4], vc[4];
 #pragma unroll
-            for (int u = 0; u < QA_ATT_U; ++u) {
+            for (int u = 0; u < 4; ++u) {
                 const int e = e0 + u * 256;
-                ch[u] = v4a{0, 0, 0, 0};
+                kc[u] = v4a{0, 0, 0, 0};
                 if (e < nk) {
                     const int r = e / cpr, c = (e - r * cpr) * 16;
                     if (r < d.Ns && c < d.Kq)
-                        ch[u] = *(const v4a*)(kb + (int64_t)r * d.k_sn + c);
-                } else if (e < nch) {
-                    const int f = e - nk;
-                    const int c = f / nvr, n = (f - c * nvr) * 16;
-                    if (c < d.Ns)
-                        ch[u] = *(const v4a*)(vb + (int64_t)c * d.v_sk + n);
+                        kc[u] = *(const v4a*)(kb + (int64_t)r * d.k_sn + c);
                 }
             }
+            const int n16 = j / nq, c4 = j - n16 * nq;
 #pragma unroll
-            for (int u = 0; u < QA_ATT_U; ++u) {
+            for (int i = 0; i < 4; ++i) {
+                const int key = 4 * c4 + i;
+                vc[i] = v4a{0, 0, 0, 0};
+                if (j < nvj && key < d.Ns)
+                    vc[i] = *(const v4a*)(vb + (int64_t)key * d.v_sk +
+                                          16 * n16);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
                 const int e = e0 + u * 256;
                 if (e < nk) {
                     const int r = e / cpr, c = (e - r * cpr) * 16;
-                    *(v4a*)(sk + r * g.RSK + c) = ch[u];
-                } else if (e < nch) {
-                    const int f = e - nk;
-                    const int c = f / nvr, n = (f - c * nvr) * 16;
-                    const int8_t* bt = (const int8_t*)&ch[u];
+                    *(v4a*)(sk + r * g.RSK + c) = kc[u];
+                }
+            }
+            if (j < nvj) {
+                int8_t* dst = sv + 16 * n16 * g.RSV + 4 * c4;
 #pragma unroll
-                    for (int j = 0; j < 16; ++j)
-                        sv[(n + j) * g.RSV + c] = bt[j];
+                for (int w = 0; w < 4; ++w) {
+                    uint32_t o[4];
+                    transpose4((uint32_t)vc[0][w], (uint32_t)vc[1][w],
+                               (uint32_t)vc[2][w], (uint32_t)vc[3][w], o);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        *(uint32_t*)(dst + (4 * w + b) * g.RSV) = o[b];
                 }
             }
         }
     }
     __syncthreads();
+    if (rt >= g.tiles) return;  // a wave past the last tile
 
-    // the wave's tile: S as columns of 16 row bytes (column n at 16 n, so a
-    // lane's 4 rows 4 kg + r of a column are one word), then P over it as
-    // rows of RSV bytes (P's columns past N_S meet v^T's zero rows)
-    int8_t* pw = sp + wave * 16 * g.RSV;
     const int nts = g.NpS >> 4;
-    const int ksv = g.KpV >> 6, dts = g.NV >> 4;
-    int8_t* const yb = d.y + b0 * d.y_s0 + b1 * d.y_s1;
-
-    for (int rt = rt0 + wave; rt < rt1; rt += 4) {
-        const int64_t m0 = (int64_t)rt * 16;  // the tile's first row
-        if (rt != rt0 + wave) load_q(rt);  // a later tile of the wave
-        // ---- S quantized a 16 x 16 block at a time: the stored bytes +
-        // 128 of the lane's 4 rows, one word a column ----
-        for (int nt0 = 0; nt0 < nts; nt0 += 4) {  // 4 blocks at a time
-            v4a acc[4];
+    const int ksq = g.KpQ >> 6;
+    // ---- S: the biased bytes of rows 4 kg + r, column 16 nt + col
+    // (byte r of sw[nt]); columns past N_S get byte 0 (outside the max) ----
+    v4a sacc[NTS];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                acc[u] = v4a{0, 0, 0, 0};
-                const int nt = min(nt0 + u, nts - 1);
+    for (int nt = 0; nt < NTS; ++nt) {
+        const int8_t* kr =
+            sk + (min(nt, nts - 1) * 16 + col) * g.RSK + kg * 16;
+        sacc[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+            fq[0], *(const v4a*)kr, v4a{0, 0, 0, 0}, 0, 0, 0);
+        if (KSQ > 1 && ksq > 1)
+            sacc[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                fq[KSQ - 1], *(const v4a*)(kr + 64), sacc[nt], 0, 0, 0);
+    }
+    uint32_t sw[NTS];
+    float mxf[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ks = 0; ks < QA_ATT_KSQ; ++ks)
-                    if (ks < ksq)
-                        acc[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                            fa[ks],
-                            *(const v4a*)(sk + (nt * 16 + col) * g.RSK +
-                                          ks * 64 + kg * 16),
-                            acc[u], 0, 0, 0);
-            }
-            float yf[4][4];
-            int qv[4][4];
-            uint32_t slow = 0;  // bit 4 u + r: the double form
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    bool sl;
-                    yf[u][r] = (float)((double)acc[u][r] * d.sS);
-                    qv[u][r] = quant_fast(yf[u][r], d.S, &sl);
-                    slow |= (uint32_t)sl << (4 * u + r);
-                }
-            if (slow) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if ((slow >> (4 * u + r)) & 1)
-                            qv[u][r] = quant_slow(yf[u][r], d.S);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int n = (nt0 + u) * 16 + col;
-                if (nt0 + u < nts && n < d.Ns) {
-                    uint32_t w = 0;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        w |= (uint32_t)((qv[u][r] - d.S.so + 128) & 255)
-                             << (8 * r);
-                    *(uint32_t*)(pw + n * 16 + 4 * kg) = w;
-                }
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        uint32_t sw[16];  // S words of the lane's columns (0: past N_S)
-        int mx[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int nt = 0; nt < 16; ++nt) {
-            const bool live = nt < nts && nt * 16 + col < d.Ns;
-            sw[nt] = live ? *(const uint32_t*)(pw + (nt * 16 + col) * 16 +
-                                               4 * kg)
-                          : 0u;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (live) mx[r] = max(mx[r], (int)((sw[nt] >> (8 * r)) & 255));
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    for (int nt = 0; nt < NTS; ++nt) {
+        float b[4];
+        bool slow = false;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
+            b[r] = qb_fast((float)((double)sacc[nt][r] * d.sS), d.S, slow);
+        if (slow) {
 #pragma unroll
-            for (int o = 8; o > 0; o >>= 1)
-                mx[r] = max(mx[r], __shfl_xor(mx[r], o));
-        // ---- the Softmax, two rows at a time (their table reads in
-        // flight together); P over the tile ----
-#pragma unroll 1
-        for (int r0 = 0; r0 < 4; r0 += 2) {
-            double e[2][16], sum[2] = {0.0, 0.0};
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int m = r0 + h == 0 ? mx[0] : r0 + h == 1 ? mx[1]
-                            : r0 + h == 2 ? mx[2] : mx[3];
-                const double* tr = d.table + 256 * m;
-#pragma unroll
-                for (int nt = 0; nt < 16; ++nt) {
-                    const bool live = nt < nts && nt * 16 + col < d.Ns;
-                    e[h][nt] = live ? tr[(sw[nt] >> (8 * (r0 + h))) & 255]
-                                    : 0.0;
-                }
-            }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int nt = 0; nt < 16; ++nt) sum[h] += e[h][nt];
-#pragma unroll
-                for (int o = 8; o > 0; o >>= 1)
-                    sum[h] += __shfl_xor(sum[h], o);
-                const double rsum = 1.0 / sum[h];  // one division a row
-                int8_t* prow = pw + (4 * kg + r0 + h) * g.RSV;
-                float yp[16];
-                int qp[16];
-                uint32_t slow = 0;
-#pragma unroll
-                for (int nt = 0; nt < 16; ++nt) {
-                    bool sl;
-                    yp[nt] = (float)(e[h][nt] * rsum);
-                    qp[nt] = quant_fast(yp[nt], d.P, &sl);
-                    slow |= (uint32_t)sl << nt;
-                }
-                if (slow) {
-#pragma unroll
-                    for (int nt = 0; nt < 16; ++nt)
-                        if ((slow >> nt) & 1) qp[nt] = quant_slow(yp[nt], d.P);
-                }
-#pragma unroll
-                for (int nt = 0; nt < 16; ++nt)
-                    if (nt < nts && nt * 16 + col < d.Ns)
-                        prow[nt * 16 + col] = (int8_t)(qp[nt] - d.P.so);
-            }
+            for (int r = 0; r < 4; ++r)
+                b[r] = qb_exact((float)((double)sacc[nt][r] * d.sS), d.S);
         }
-        // the wave's P bytes before its reads of them
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        // ---- O = P v: 16 rows x NV columns, 4 blocks at a time ----
-        for (int dt0 = 0; dt0 < dts; dt0 += 4) {
-            v4a acc2[4];
+        wrap_u8(b, d.S);
+        if (16 * nt + 16 > d.Ns && 16 * nt + col >= d.Ns) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                acc2[u] = v4a{0, 0, 0, 0};
-                const int dt = min(dt0 + u, dts - 1);
-                for (int ks = 0; ks < ksv; ++ks) {
-                    const int c = ks * 64 + kg * 16;
-                    acc2[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        *(const v4a*)(pw + col * g.RSV + c),
-                        *(const v4a*)(sv + (dt * 16 + col) * g.RSV + c),
-                        acc2[u], 0, 0, 0);
-                }
-            }
-            float yo[4][4];
-            int qo[4][4];
-            uint32_t slow = 0;
+            for (int r = 0; r < 4; ++r) b[r] = 0.f;
+        }
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+        for (int r = 0; r < 4; ++r) mxf[r] = fmaxf(mxf[r], b[r]);
+        sw[nt] = pack_u8(b);
+    }
+    // phase boundaries for the scheduler: each phase's values die in it
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t row[4];  // table offset of the row's maximum (a 16-bit index:
+                      // the loads take the table as a scalar base)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    bool sl;
-                    yo[u][r] = (float)((double)acc2[u][r] * d.sO);
-                    qo[u][r] = quant_fast(yo[u][r], d.O, &sl);
-                    slow |= (uint32_t)sl << (4 * u + r);
-                }
+    for (int r = 0; r < 4; ++r) {
+        int mx = (int)mxf[r];
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
+        row[r] = ((uint32_t)mx & 255u) << 8;
+    }
+
+    // ---- the Softmax of rows 4 kg + r ----
+    double e[NTS][4];
+#pragma unroll
+    for (int nt = 0; nt < NTS; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            e[nt][r] = d.table[row[r] | ((sw[nt] >> (8 * r)) & 255u)];
+#pragma unroll
+    for (int nt = 0; nt < NTS; ++nt)
+        if (16 * nt + 16 > d.Ns && 16 * nt + col >= d.Ns) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) e[nt][r] = 0.0;
+        }
+    double rs[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        double t = 0.0;
+#pragma unroll
+        for (int nt = 0; nt < NTS; ++nt) t += e[nt][r];
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) t += __shfl_xor(t, o);
+        rs[r] = 1.0 / t;  // one division a row
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // P's stored bytes to the wave's tile, rows of RSV bytes (columns past
+    // N_S meet v^T's zero rows)
+    int8_t* pw = sp + wave * 16 * g.RSV;
+#pragma unroll
+    for (int nt = 0; nt < NTS; ++nt) {
+        float b[4];
+        bool slow = false;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            b[r] = qb_fast((float)(e[nt][r] * rs[r]), d.P, slow);
+        if (slow) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                b[r] = qb_exact((float)(e[nt][r] * rs[r]), d.P);
+        }
+        wrap_u8(b, d.P);
+        const uint32_t w = pack_u8(b) ^ 0x80808080u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            pw[(4 * kg + r) * g.RSV + 16 * nt + col] = (int8_t)(w >> (8 * r));
+    }
+    // the wave's P bytes before its reads of them
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- O^T = v^T P^T, 4 blocks of 16 features at a time: lane (col,
+    // kg) holds row m0 + col, features 16 dt + 4 kg + r ----
+    constexpr int KSV = (NTS + 3) / 4;  // K-steps of P v
+    const int dts = g.NV >> 4, ksv = g.KpV >> 6;
+    v4a pf[KSV];  // the lane's P fragments: row col, bytes 64 ks + 16 kg
+#pragma unroll
+    for (int ks = 0; ks < KSV; ++ks)
+        pf[ks] = ks < ksv ? *(const v4a*)(pw + col * g.RSV + ks * 64 + kg * 16)
+                          : v4a{0, 0, 0, 0};
+    const int64_t m = m0 + col;
+    int8_t* const yr = d.y + b0 * d.y_s0 + b1 * d.y_s1 + m * d.y_sm;
+    for (int dt0 = 0; dt0 < dts; dt0 += 4) {
+        v4a acc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            acc[u] = v4a{0, 0, 0, 0};
+            if (dt0 + u >= dts) continue;
+            // K-steps past KpV repeat the last one against zero fragments
+#pragma unroll
+            for (int ks = 0; ks < KSV; ++ks)
+                acc[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    *(const v4a*)(sv + ((dt0 + u) * 16 + col) * g.RSV +
+                                  min(ks, ksv - 1) * 64 + kg * 16),
+                    pf[ks], acc[u], 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (dt0 + u >= dts) continue;
+            float b[4];
+            bool slow = false;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                b[r] = qb_fast((float)((double)acc[u][r] * d.sO), d.O, slow);
             if (slow) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if ((slow >> (4 * u + r)) & 1)
-                            qo[u][r] = quant_slow(yo[u][r], d.O);
+                for (int r = 0; r < 4; ++r)
+                    b[r] = qb_exact((float)((double)acc[u][r] * d.sO), d.O);
             }
+            wrap_u8(b, d.O);
+            if (m >= d.M) continue;
+            const int n = (dt0 + u) * 16 + 4 * kg;  // features n .. n + 3
+            const uint32_t w = pack_u8(b) ^ 0x80808080u;
+            if (d.oword) {
+                *(uint32_t*)(yr + n) = w;
+            } else {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int n = (dt0 + u) * 16 + col;
-                if (dt0 + u >= dts || n >= d.No) continue;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t m = m0 + 4 * kg + r;
-                    if (m < d.M)
-                        yb[m * d.y_sm + n * d.y_sn] =
-                            (int8_t)(qo[u][r] - d.O.so);
-                }
+                for (int r = 0; r < 4; ++r)
+                    yr[(int64_t)(n + r) * d.y_sn] = (int8_t)(w >> (8 * r));
             }
         }
-        // this tile's reads of P before the next tile's S words
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
 }
 
@@ -398,12 +418,10 @@ bool attn_geom(const qa_attention_desc* d, AttnGeom* g, int64_t* lds,
     g->RSK = g->KpQ + 16;
     g->RSV = g->KpV + 16;
     g->tiles = (int)ceil_div(qk.M, 16);
-    // one 16-row tile per wave
-    g->tpw = 4;
-    // k rows and v^T rows once per work-group, an S / P tile per wave (S
-    // as NpS columns of 16 bytes, or P as 16 rows of RSV bytes)
+    g->tpw = 4;  // one 16-row tile per wave
+    // k rows and v^T rows once per work-group, a P tile per wave
     *lds = (int64_t)g->NpS * g->RSK + (int64_t)g->NV * g->RSV +
-           4LL * std::max(16 * g->RSV, 16 * g->NpS);
+           4LL * 16 * g->RSV;
     if (*lds > 96 * 1024) {
         *why = "operands exceed the LDS budget";
         return false;
@@ -448,11 +466,14 @@ QA_API int qa_d_attention(const qa_attention_desc* d, void* stream) {
         c.qmin = (int)qmin;
         c.qmax = (int)qmax;
         c.so = (int)so;
-        c.f32 = qa_f32_form_ok(scale, zp, qmin, qmax) ? 1 : 0;
-        c.tie = qa_f32_tie(zp, qmin, qmax);
-        c.zpf = (float)zp;
-        c.qminf = (float)qmin;
-        c.qmaxf = (float)qmax;
+        // -1: every value takes the double form
+        c.tie = qa_f32_form_ok(scale, zp, qmin, qmax)
+                    ? qa_f32_tie(zp, qmin, qmax)
+                    : -1.0f;
+        c.cb = (float)(zp - so + 128);
+        c.lob = (float)(qmin - so + 128);
+        c.hib = (float)(qmax - so + 128);
+        c.wrap = qmin - so < -128 || qmax - so > 127;
         return c;
     };
     AttnArgs a;
@@ -470,6 +491,8 @@ QA_API int qa_d_attention(const qa_attention_desc* d, void* stream) {
     a.Ns = (int)qk.N;
     a.Kq = (int)qk.K;
     a.No = (int)av.N;
+    a.oword = av.y_sn == 1 && av.y_sm % 4 == 0 && av.y_s0 % 4 == 0 &&
+              av.y_s1 % 4 == 0 && (uintptr_t)av.y % 4 == 0;
     a.sS = qk.a_scale * qk.b_scale;
     a.sO = av.a_scale * av.b_scale;
     a.S = qc(qk.out_scale, qk.out_zp, qk.qmin, qk.qmax, qk.y_so);
@@ -477,7 +500,23 @@ QA_API int qa_d_attention(const qa_attention_desc* d, void* stream) {
     a.O = qc(av.out_scale, av.out_zp, av.qmin, av.qmax, av.y_so);
     const dim3 grid((unsigned)ceil_div(g.tiles, g.tpw),
                     (unsigned)(qk.B0 * qk.B1));
-    k_attention<<<grid, 256, (size_t)lds, (hipStream_t)stream>>>(a, g);
+    const int nts = g.NpS / 16, ksq = g.KpQ / 64;
+    hipStream_t st = (hipStream_t)stream;
+    auto go = [&](auto kern) {
+        kern<<<grid, 256, (size_t)lds, st>>>(a, g);
+    };
+    // the smallest instantiated block count >= nts
+    if (ksq == 1) {
+        if (nts <= 4) go(k_attention<4, 1>);
+        else if (nts <= 8) go(k_attention<8, 1>);
+        else if (nts <= 13) go(k_attention<13, 1>);
+        else go(k_attention<16, 1>);
+    } else {
+        if (nts <= 4) go(k_attention<4, 2>);
+        else if (nts <= 8) go(k_attention<8, 2>);
+        else if (nts <= 13) go(k_attention<13, 2>);
+        else go(k_attention<16, 2>);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("qa_d_attention", e);
