@@ -150,79 +150,142 @@ __global__ __launch_bounds__(kThreads) void k_layernorm(
     }
 }
 
+// The output quantization of the word kernel below, biased by 128 - so so
+// that a clipped value is its stored byte + 128: the float32 form of
+// qa_quantize_mixed (tie = -1 where that form does not apply, so every
+// value takes the double form), and wrap set where the clip range reaches
+// past the int8 storage (whose bytes then wrap around).
+struct LnQ {
+    double scale, inv;
+    float invf, tie, cb, lob, hib;
+    int zp, qmin, qmax, so, wrap;
+};
+
+__device__ __noinline__ int ln_quant_exact(float y, double scale, double inv,
+                                           int zp, int qmin, int qmax) {
+    return (int)qa_quantize_one_fast(y, scale, inv, zp, qmin, qmax);
+}
+
 // int8 rows of at most 512 values, a multiple of 4 (transformer widths):
 // 32 lanes a row (2 rows a wave), lane l holding the WPL 4-byte words
-// l, l + 32, ... of its row (coalesced word loads and stores). The same
-// float64 statistics as k_layernorm; each value is then scaled by the
-// row's reciprocal deviation (one division a row instead of one a value).
-template <int WPL>
-__global__ __launch_bounds__(kThreads) void k_layernorm_w(
+// l, l + 32, ... of its row (coalesced word loads and stores). The float64
+// steps of k_layernorm (mean, mean square deviation, then (v - mean) / sd
+// * gamma + beta, the division as one reciprocal a row) with per value:
+// the dequantized value from a 256-entry table in LDS (the reference's
+// float32 value of each stored byte, as a double), the affine step as one
+// multiply and one fma, and the float32 form of the output quantization
+// with v_cvt_pk_u8_f32 packing four values into their word (a word whose
+// tie test fails in any lane is requantized by the double form). Every
+// load of a row (its words, gamma and beta) is issued before the table is
+// built, so their latencies overlap. NW waves a work-group (16: the grid
+// is a quarter of the work-groups of 4-wave ones, which the dispatcher
+// starts at a few nanoseconds each).
+template <int WPL, int NW>
+__global__ __launch_bounds__(64 * NW) void k_layernorm_w(
     const int8_t* __restrict__ x, int64_t x_rs, int64_t rows, int64_t cols,
     double in_scale, int64_t in_zp, int64_t x_so,
     const float* __restrict__ gamma, const float* __restrict__ beta,
-    double eps, int8_t* __restrict__ y, int64_t y_rs, double out_scale,
-    int64_t out_zp, int64_t qmin, int64_t qmax, int64_t y_so) {
-    const int lane = threadIdx.x & 63;
+    double eps, int8_t* __restrict__ y, int64_t y_rs, LnQ o) {
+    __shared__ double s_dq[256];
+    const int tid = threadIdx.x, lane = tid & 63;
     const int gl = lane & 31;
-    const double inv = 1.0 / out_scale;
-    const bool f32ok = qa_f32_form_ok(out_scale, out_zp, qmin, qmax);
-    const float invf = (float)inv;
     const int words = (int)(cols >> 2);
     const int64_t first =
-        ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
-    for (int64_t r = first; r - (lane >> 5) < rows;
-         r += (int64_t)gridDim.x * 8) {
-        const bool live = r < rows;
-        const int64_t rr = live ? r : 0;
-        const uint32_t* xr = (const uint32_t*)(x + rr * x_rs);
-        double v[WPL][4];
-        double s = 0.0;
+        ((int64_t)blockIdx.x * NW + (tid >> 6)) * 2 + (lane >> 5);
+    const int64_t step = (int64_t)gridDim.x * 2 * NW;
+    uint32_t u[WPL];
+    float4 g4[WPL], b4[WPL];
+    auto load_row = [&](int64_t r) __attribute__((always_inline)) {
+        const uint32_t* xr = (const uint32_t*)(x + min(r, rows - 1) * x_rs);
 #pragma unroll
         for (int k = 0; k < WPL; ++k) {
-            const int w = gl + 32 * k;
-            const uint32_t u = w < words ? xr[w] : 0u;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                v[k][b] = w < words
-                              ? (double)dequant_f32(
-                                    (int64_t)(int8_t)(u >> (8 * b)) + x_so,
-                                    in_zp, in_scale)
-                              : 0.0;
-                s += v[k][b];
-            }
+            const int w = min(gl + 32 * k, words - 1);
+            u[k] = xr[w];
         }
-        const double mean = group_sum<32>(s) / (double)cols;
-        double q2 = 0.0;
+    };
+    load_row(first);
+    // beta's loads read gamma when there is no beta (no branch between
+    // the loads); its terms are then zero
+    const float* bsrc = beta ? beta : gamma;
+    const float bmul = beta ? 1.f : 0.f;
+#pragma unroll
+    for (int k = 0; k < WPL; ++k) {
+        const int w = min(gl + 32 * k, words - 1);
+        g4[k] = ((const float4*)gamma)[w];
+        b4[k] = ((const float4*)bsrc)[w];
+    }
+    if (tid < 256)
+        s_dq[tid] = (double)dequant_f32((int64_t)(tid - 128) + x_so, in_zp,
+                                        in_scale);
+    __syncthreads();
+    const double inv_cols = 1.0 / (double)cols;
+    for (int64_t r = first; r - (lane >> 5) < rows; r += step) {
+        if (r != first) load_row(r);
+        double v[WPL][4];
+        double s = 0.0;
+        // words past the row (a clamped re-read) count as zeros
 #pragma unroll
         for (int k = 0; k < WPL; ++k)
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const double t = v[k][b] - mean;
-                if (gl + 32 * k < words) q2 += t * t;
-            }
-        const double rsd = 1.0 / sqrt(group_sum<32>(q2) / (double)cols + eps);
-        if (!live) continue;
-        uint32_t* yr = (uint32_t*)(y + rr * y_rs);
+            for (int b = 0; b < 4; ++b)
+                v[k][b] = s_dq[((u[k] >> (8 * b)) & 255) ^ 128];
 #pragma unroll
         for (int k = 0; k < WPL; ++k) {
-            const int w = gl + 32 * k;
-            if (w >= words) continue;
-            const float4 g4 = ((const float4*)gamma)[w];
-            const float4 b4 = beta ? ((const float4*)beta)[w]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float gg[4] = {g4.x, g4.y, g4.z, g4.w};
-            const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
-            uint32_t out = 0;
+            const bool live = gl + 32 * k < words;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) s += live ? v[k][b] : 0.0;
+        }
+        const double mean = group_sum<32>(s) * inv_cols;
+        double q2 = 0.0;
+#pragma unroll
+        for (int k = 0; k < WPL; ++k) {
+            const bool live = gl + 32 * k < words;
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const double t =
-                    (v[k][b] - mean) * rsd * (double)gg[b] + (double)bb[b];
-                const int64_t q = qa_quantize_mixed((float)t, f32ok, invf,
-                                                    out_scale, inv, out_zp,
-                                                    qmin, qmax);
-                out |= (uint32_t)(uint8_t)(int8_t)(q - y_so) << (8 * b);
+                const double t = live ? v[k][b] - mean : 0.0;
+                q2 = fma(t, t, q2);
             }
-            yr[w] = out;
+        }
+        const double rsd =
+            1.0 / sqrt(group_sum<32>(q2) * inv_cols + eps);
+        if (r < rows) {
+            uint32_t* yr = (uint32_t*)(y + r * y_rs);
+#pragma unroll
+            for (int k = 0; k < WPL; ++k) {
+                const int w = gl + 32 * k;
+                if (w >= words) continue;
+                const float gg[4] = {g4[k].x, g4[k].y, g4[k].z, g4[k].w};
+                const float bb[4] = {b4[k].x * bmul, b4[k].y * bmul,
+                                     b4[k].z * bmul, b4[k].w * bmul};
+                float t[4], q[4];
+                bool slow = false;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    t[b] = (float)fma((v[k][b] - mean) * rsd, (double)gg[b],
+                                      (double)bb[b]);
+                    const float rr = rintf(t[b] * o.invf);
+                    const float dd = fmaf(t[b], o.invf, -rr);
+                    slow |= !(fabsf(dd) < o.tie);
+                    q[b] = __builtin_amdgcn_fmed3f(rr + o.cb, o.lob, o.hib);
+                }
+                if (__builtin_expect(slow, 0)) {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        q[b] = (float)(ln_quant_exact(t[b], o.scale, o.inv,
+                                                      o.zp, o.qmin, o.qmax) -
+                                       o.so + 128);
+                }
+                if (__builtin_expect(o.wrap, 0)) {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        q[b] = (float)((int)q[b] & 255);
+                }
+                uint32_t wv = __builtin_amdgcn_cvt_pk_u8_f32(q[0], 0, 0u);
+                wv = __builtin_amdgcn_cvt_pk_u8_f32(q[1], 1, wv);
+                wv = __builtin_amdgcn_cvt_pk_u8_f32(q[2], 2, wv);
+                wv = __builtin_amdgcn_cvt_pk_u8_f32(q[3], 3, wv);
+                yr[w] = wv ^ 0x80808080u;
+            }
         }
     }
 }
@@ -493,22 +556,38 @@ QA_API int qa_d_layernorm(const void* x, int x_code, int64_t x_rstride,
         x_rstride % 4 == 0 && y_rstride % 4 == 0 &&
         ((uintptr_t)x | (uintptr_t)y | (uintptr_t)gamma |
          (uintptr_t)(beta ? beta : gamma)) % 16 == 0) {
-        const int64_t blocks = std::min<int64_t>(ceil_div(rows, 8), 65535);
+        constexpr int NW = 16;  // waves a work-group, 2 rows each
+        const int64_t blocks =
+            std::min<int64_t>(ceil_div(rows, 2 * NW), 65535);
+        LnQ o;
+        o.scale = out_scale;
+        o.inv = 1.0 / out_scale;
+        o.invf = (float)o.inv;
+        o.tie = qa_f32_form_ok(out_scale, out_zp, qmin, qmax)
+                    ? qa_f32_tie(out_zp, qmin, qmax)
+                    : -1.0f;
+        o.cb = (float)(out_zp - y_so + 128);
+        o.lob = (float)(qmin - y_so + 128);
+        o.hib = (float)(qmax - y_so + 128);
+        o.zp = (int)out_zp;
+        o.qmin = (int)qmin;
+        o.qmax = (int)qmax;
+        o.so = (int)y_so;
+        o.wrap = qmin - y_so < -128 || qmax - y_so > 127;
         auto run = [&](auto kern) {
-            kern<<<(unsigned)blocks, kThreads, 0, st>>>(
+            kern<<<(unsigned)blocks, 64 * NW, 0, st>>>(
                 (const int8_t*)x, x_rstride, rows, cols, in_scale, in_zp, x_so,
-                gamma, beta, eps, (int8_t*)y, y_rstride, out_scale, out_zp,
-                qmin, qmax, y_so);
+                gamma, beta, eps, (int8_t*)y, y_rstride, o);
         };
         const int wpl = (int)ceil_div(cols / 4, 32);
         if (wpl <= 1)
-            run(k_layernorm_w<1>);
+            run(k_layernorm_w<1, NW>);
         else if (wpl <= 2)
-            run(k_layernorm_w<2>);
+            run(k_layernorm_w<2, NW>);
         else if (wpl == 3)
-            run(k_layernorm_w<3>);
+            run(k_layernorm_w<3, NW>);
         else
-            run(k_layernorm_w<4>);
+            run(k_layernorm_w<4, NW>);
         return launched("qa_d_layernorm") ? 0 : -1;
     }
     auto go = [&](auto ti, auto to) {
