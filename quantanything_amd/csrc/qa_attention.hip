@@ -219,8 +219,7 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs d, AttnGeom g) {
 
     const int nts = g.NpS >> 4;
     const int ksq = g.KpQ >> 6;
-    // ---- S: the biased bytes of rows 4 kg + r, column 16 nt + col
-    // (byte r of sw[nt]); columns past N_S get byte 0 (outside the max) ----
+    // ---- S's scores: rows 4 kg + r, column 16 nt + col in sacc[nt][r] ----
     v4a sacc[NTS];
 #pragma unroll
     for (int nt = 0; nt < NTS; ++nt) {
@@ -232,8 +231,44 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs d, AttnGeom g) {
             sacc[nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                 fq[KSQ - 1], *(const v4a*)(kr + 64), sacc[nt], 0, 0, 0);
     }
+    // The rows' maxima first: S's quantization is non-decreasing in the
+    // integer score (the float64 scaling, the float32 cast, the rounding
+    // and the clip all are; a storage that wraps is not supported here),
+    // so a row's largest byte is the quantization of its largest score
+    // over the columns before N_S. Then each block's bytes, whose table
+    // reads go out at once: they overlap the next blocks' quantization.
+    int amx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
+#pragma unroll
+    for (int nt = 0; nt < NTS; ++nt) {
+        const bool live = 16 * nt + 16 <= d.Ns || 16 * nt + col < d.Ns;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            amx[r] = max(amx[r], live ? sacc[nt][r] : INT_MIN);
+    }
+    uint32_t row[4];  // table offset of the row's maximum (a 16-bit index:
+                      // the loads take the table as a scalar base)
+    {
+        float bm[4];
+        bool slow = false;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1)
+                amx[r] = max(amx[r], __shfl_xor(amx[r], o));
+            bm[r] = qb_fast((float)((double)amx[r] * d.sS), d.S, slow);
+        }
+        if (slow) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                bm[r] = qb_exact((float)((double)amx[r] * d.sS), d.S);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) row[r] = ((uint32_t)bm[r] & 255u) << 8;
+    }
+
+    // ---- the Softmax of rows 4 kg + r ----
     uint32_t sw[NTS];
-    float mxf[4] = {0.f, 0.f, 0.f, 0.f};
+    double e[NTS][4];
 #pragma unroll
     for (int nt = 0; nt < NTS; ++nt) {
         float b[4];
@@ -246,34 +281,13 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs d, AttnGeom g) {
             for (int r = 0; r < 4; ++r)
                 b[r] = qb_exact((float)((double)sacc[nt][r] * d.sS), d.S);
         }
-        wrap_u8(b, d.S);
-        if (16 * nt + 16 > d.Ns && 16 * nt + col >= d.Ns) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) b[r] = 0.f;
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mxf[r] = fmaxf(mxf[r], b[r]);
         sw[nt] = pack_u8(b);
-    }
-    // phase boundaries for the scheduler: each phase's values die in it
-    __builtin_amdgcn_sched_barrier(0);
-    uint32_t row[4];  // table offset of the row's maximum (a 16-bit index:
-                      // the loads take the table as a scalar base)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        int mx = (int)mxf[r];
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
-        row[r] = ((uint32_t)mx & 255u) << 8;
-    }
-
-    // ---- the Softmax of rows 4 kg + r ----
-    double e[NTS][4];
-#pragma unroll
-    for (int nt = 0; nt < NTS; ++nt)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             e[nt][r] = d.table[row[r] | ((sw[nt] >> (8 * r)) & 255u)];
+    }
+    // phase boundaries for the scheduler: each phase's values die in it
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int nt = 0; nt < NTS; ++nt)
         if (16 * nt + 16 > d.Ns && 16 * nt + col >= d.Ns) {
@@ -409,6 +423,8 @@ bool attn_geom(const qa_attention_desc* d, AttnGeom* g, int64_t* lds,
     } else if (av.a_scale != d->p_scale || av.a_zp != d->p_zp ||
                av.a_so != d->p_so) {
         *why = "P's quantization differs between the Softmax and P v";
+    } else if (qk.qmin - qk.y_so < -128 || qk.qmax - qk.y_so > 127) {
+        *why = "needs S's clip range within its int8 storage";
     }
     if (*why) return false;
     g->NpS = (int)round_up(qk.N, 16);

@@ -48,7 +48,7 @@ def test_fused_attention_equals_three_launches(hip, B, H, T, hd):
     qf = (qkv[:, :, 0].astype(np.float64) - qs[1]) * qs[0]
     kf = (qkv[:, :, 1].astype(np.float64) - ks[1]) * ks[0]
     smax = np.abs(np.einsum("bthd,bshd->bhts", qf, kf)).max()
-    S = (smax / 110.0, 4, -128, 127, 4)      # scale, zp, qmin, qmax, so
+    S = (smax / 110.0, 4, -128, 127, 0)      # scale, zp, qmin, qmax, so
     P = (1.0 / 127.0, 0, -128, 127, 0)
     vmax = np.abs((qkv[:, :, 2].astype(np.float64) - vs[1]) * vs[0]).max()
     O = (vmax / 150.0, -3, -128, 127, -3)
