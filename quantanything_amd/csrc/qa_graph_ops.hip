@@ -390,6 +390,13 @@ __global__ __launch_bounds__(kThreads) void k_softmax_table(
 // k_softmax_table: the same float64 values, summed in the same order, so
 // the results are those of k_softmax_rows. outf (optional): the dequantized
 // output, as k_softmax_rows writes it.
+// qa_quantize_one_fast out of line (the callers' rare near-tie values)
+__device__ __noinline__ int softmax_quant_exact(float y, double scale,
+                                                double inv, int64_t zp,
+                                                int64_t qmin, int64_t qmax) {
+    return (int)qa_quantize_one_fast(y, scale, inv, zp, qmin, qmax);
+}
+
 template <int GS, int PER>
 __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
     const int8_t* __restrict__ x, int64_t rows, int64_t cols,
@@ -402,6 +409,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
     const double inv = 1.0 / out_scale;
     const bool f32ok = qa_f32_form_ok(out_scale, out_zp, qmin, qmax);
     const float invf = (float)inv;
+    const float tie = qa_f32_tie(out_zp, qmin, qmax);
     const int64_t first = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW +
                           lane / GS;
     for (int64_t r = first; r - lane / GS < rows;
@@ -429,15 +437,33 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
         for (int o = GS / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
         const double rsum = 1.0 / sum;  // one division a row
         if (!live) continue;
+        // the float32 form inline, the double form out of line for the
+        // values whose tie test fails (few instructions a value: the
+        // launch's code is fetched cold)
+        float y[PER];
+        int qv[PER];
+        uint32_t slow = 0;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            y[k] = (float)(e[k] * rsum);
+            bool sl = !f32ok;
+            qv[k] = qa_quantize_f32(y[k], invf, tie, (int)out_zp, (int)qmin,
+                                    (int)qmax, &sl);
+            slow |= (uint32_t)sl << k;
+        }
+        if (__builtin_expect(slow != 0, 0)) {
+            for (int k = 0; k < PER; ++k)
+                if ((slow >> k) & 1)
+                    qv[k] = softmax_quant_exact(y[k], out_scale, inv, out_zp,
+                                                qmin, qmax);
+        }
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int64_t i = gl + GS * k;
             if (i >= cols) continue;
-            const float y = (float)(e[k] * rsum);
-            const int64_t q = qa_quantize_mixed(y, f32ok, invf, out_scale, inv,
-                                                out_zp, qmin, qmax);
-            out[base + i] = (int8_t)(q - out_so);
-            if (outf) outf[base + i] = (float)((double)(q - out_zp) * out_scale);
+            out[base + i] = (int8_t)(qv[k] - out_so);
+            if (outf)
+                outf[base + i] = (float)((double)(qv[k] - out_zp) * out_scale);
         }
     }
 }
