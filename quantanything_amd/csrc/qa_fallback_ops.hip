@@ -69,6 +69,55 @@ __global__ __launch_bounds__(kThreads) void k_copy_nd(qa_nd_copy d,
     }
 }
 
+// Plain copies (same storage on both sides, values unchanged) whose
+// innermost axis is contiguous on both sides, in 16-byte chunks: chunk i is
+// part i % cpr of inner row i / cpr, whose index decodes over the other
+// axes in 32 bits (fewer than 2^32 chunks); strides in bytes.
+__global__ __launch_bounds__(kThreads) void k_copy_nd16(
+    const char* __restrict__ x, char* __restrict__ y, int ndim,
+    int64_t cpr, int64_t chunks, qa_nd_copy d, int es) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+         i < chunks; i += (int64_t)gridDim.x * kThreads) {
+        const uint32_t row = (uint32_t)i / (uint32_t)cpr;
+        const uint32_t part = (uint32_t)i - row * (uint32_t)cpr;
+        int64_t xo = (int64_t)part * 16, yo = xo;
+        uint32_t rem = row;
+        for (int k = ndim - 2; k >= 0; --k) {
+            const uint32_t n = (uint32_t)d.shape[k];
+            const uint32_t q = rem / n;
+            const int64_t c = (int64_t)(rem - q * n);
+            rem = q;
+            xo += c * d.xs[k] * es;
+            yo += c * d.ys[k] * es;
+        }
+        *(int4*)(y + yo) = *(const int4*)(x + xo);
+    }
+}
+
+// Whether a copy descriptor is a plain copy k_copy_nd16 can do.
+bool copy_nd16_applies(const qa_nd_copy& d, int64_t total) {
+    const int es = (int)d.x_code;
+    if (d.x_code != d.y_code || d.x_so != d.y_so || es > 4) return false;
+    const int64_t lo = es == 1 ? -128 : es == 2 ? -32768 : INT32_MIN;
+    const int64_t hi = es == 1 ? 127 : es == 2 ? 32767 : INT32_MAX;
+    // mode 1 with the identity multiplier, equal zero points and a clip
+    // range covering the storage changes no value
+    const bool same =
+        d.mode == 0 ||
+        (d.mode == 1 && d.m == ((int64_t)1 << 30) && d.s == -1 &&
+         d.zp_in == d.zp_out && d.qmin <= lo + d.x_so &&
+         d.qmax >= hi + d.x_so);
+    const int last = (int)d.ndim - 1;
+    if (!same || d.xs[last] != 1 || d.ys[last] != 1 ||
+        (d.shape[last] * es) % 16 != 0 || ((uintptr_t)d.x | (uintptr_t)d.y) % 16)
+        return false;
+    for (int k = 0; k < last; ++k)
+        if ((d.xs[k] * es) % 16 || (d.ys[k] * es) % 16 ||
+            d.shape[k] >= ((int64_t)1 << 32))
+            return false;
+    return total * es / 16 < ((int64_t)1 << 32);
+}
+
 // ----------------------------------------------------------- LayerNorm --
 // GS lanes per row (64 / GS rows per wave): rows of at most GS * PER values
 // are read once and held in registers; longer rows (GS = 64, PER = 0) are
@@ -528,6 +577,17 @@ QA_API int qa_d_copy_nd(const qa_nd_copy* d, void* stream) {
         total *= d->shape[k];
     }
     if (total == 0) return 0;
+    if (copy_nd16_applies(*d, total)) {
+        const int es = (int)d->x_code;
+        const int64_t cpr = d->shape[d->ndim - 1] * es / 16;
+        const int64_t chunks = total * es / 16;
+        const int64_t blocks =
+            std::min<int64_t>(ceil_div(chunks, kThreads), 65535);
+        k_copy_nd16<<<(unsigned)blocks, kThreads, 0, (hipStream_t)stream>>>(
+            (const char*)d->x, (char*)d->y, (int)d->ndim, cpr, chunks, *d,
+            es);
+        return launched("qa_d_copy_nd") ? 0 : -1;
+    }
     const int64_t blocks = std::min<int64_t>(ceil_div(total, kThreads), 65535);
     if (total < ((int64_t)1 << 32))  // every extent divides in 32 bits
         k_copy_nd<true><<<(unsigned)blocks, kThreads, 0,
