@@ -137,6 +137,53 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
                 w2[u] = *(const v4i*)(a2.wp + (ok ? r * rs2 + k * 16 : 0));
             }
         }
+        // TAIL: the first round of cv2's weight rows and of the band's
+        // prefix channels, cv2's table entry and constants, requested with
+        // the loads above (each later round would be one more memory
+        // round trip before the first MFMA); EARLY only for C = 16, where
+        // the registers holding them leave the occupancy unchanged
+        constexpr bool EARLY = TAIL && WM == 1;
+        const int kgp3 = TAIL ? 4 * g.KS3 : 0;
+        const int n3 = TAIL ? 16 * g.T3 * kgp3 : 0;
+        const int cpp3 = TAIL ? g.off_d >> 4 : 1;
+        const int np3 = TAIL ? R * OW * cpp3 : 0;
+        const int8_t* xp3 =
+            TAIL ? (const int8_t*)a3.x + ((int64_t)n * OH + oy0) * OW * a3.x_sp
+                 : nullptr;
+        v4i w3[4], pv3[4];
+        int a3w[4], ap3[4];
+        int tv3 = 0;
+        int4 pc3v = int4{0, 0, 0, 0};
+        uint32_t corr3v = 0;
+        auto load_w3 = [&](int e0) __attribute__((always_inline)) {
+            const int rs3 = (int)a3.wp_rstride;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = e0 + u * CP_NT;
+                const int r = cp_div(e, g.m_kgp3), k = e - r * kgp3;
+                const bool ok = e < n3;
+                a3w[u] = ok ? r * g.RSW3 + k * 16 : -1;
+                w3[u] = *(const v4i*)(a3.wp + (ok ? r * rs3 + k * 16 : 0));
+            }
+        };
+        auto load_pre = [&](int e0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = e0 + u * CP_NT;
+                const bool ok = e < np3;
+                const int px = ok ? e / cpp3 : 0, c = ok ? e - px * cpp3 : 0;
+                ap3[u] = ok ? px * g.RP + c * 16 : -1;
+                pv3[u] = *(const v4i*)(xp3 + (int64_t)px * a3.x_sp + c * 16);
+            }
+        };
+        if constexpr (EARLY) {
+            load_w3(tid);
+            load_pre(tid);
+            tv3 = ((const int*)((const char*)a3.plan + PLAN_E))[tid & 255];
+            const int cl = min(tid, a3.Cout - 1);
+            pc3v = ((const int4*)((const char*)a3.plan + PLAN_CH))[cl];
+            corr3v = a3.corr ? (uint32_t)a3.corr[cl] : 0u;
+        }
         // pad values: input band rows outside the image and its two pad
         // columns; intermediate rows outside the image and its pad columns
         for (int e = tid; e < BR * g.BW * WM; e += CP_NT) {
@@ -182,51 +229,30 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
                 *(v4i*)(s_w1 + aw[u]) = w1[u];
                 *(v4i*)(s_w2 + aw[u]) = w2[u];
             }
-        if (TAIL) {  // cv2's weight rows, table and per-channel constants
-            const int kgp3 = 4 * g.KS3;
-            const int n3 = 16 * g.T3 * kgp3;
-            const int rs3 = (int)a3.wp_rstride;
+        if constexpr (TAIL) {  // cv2's weights, table, constants
             for (int e0 = tid; e0 < n3; e0 += 4 * CP_NT) {
-                v4i w3[4];
-                int a3w[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int e = e0 + u * CP_NT;
-                    const int r = cp_div(e, g.m_kgp3), k = e - r * kgp3;
-                    const bool ok = e < n3;
-                    a3w[u] = ok ? r * g.RSW3 + k * 16 : -1;
-                    w3[u] = *(const v4i*)(a3.wp + (ok ? r * rs3 + k * 16 : 0));
-                }
+                if (!EARLY || e0 != tid) load_w3(e0);
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
                     if (a3w[u] >= 0) *(v4i*)(s_w3 + a3w[u]) = w3[u];
             }
             // the prefix channels of the band's output pixels
-            const int cpp = g.off_d >> 4;
-            const int np = R * OW * cpp;
-            const int8_t* xp = (const int8_t*)a3.x +
-                               ((int64_t)n * OH + oy0) * OW * a3.x_sp;
-            for (int e0 = tid; e0 < np; e0 += 4 * CP_NT) {
-                v4i pv[4];
-                int ap[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int e = e0 + u * CP_NT;
-                    const bool ok = e < np;
-                    const int px = ok ? e / cpp : 0, c = ok ? e - px * cpp : 0;
-                    ap[u] = ok ? px * g.RP + c * 16 : -1;
-                    pv[u] = *(const v4i*)(xp + (int64_t)px * a3.x_sp + c * 16);
-                }
+            for (int e0 = tid; e0 < np3; e0 += 4 * CP_NT) {
+                if (!EARLY || e0 != tid) load_pre(e0);
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
-                    if (ap[u] >= 0) *(v4i*)(s_pre + ap[u]) = pv[u];
+                    if (ap3[u] >= 0) *(v4i*)(s_pre + ap3[u]) = pv3[u];
             }
-            for (int i = tid; i < 256; i += CP_NT)
-                s_tab3[i] = ((const int*)((const char*)a3.plan + PLAN_E))[i];
-            for (int c = tid; c < 16 * g.T3; c += CP_NT) {
-                const int cl = min(c, a3.Cout - 1);
-                s_pc3[c] = ((const int4*)((const char*)a3.plan + PLAN_CH))[cl];
-                s_corr3[c] = a3.corr ? (uint32_t)a3.corr[cl] : 0u;
+            if (!EARLY) {
+                tv3 = ((const int*)((const char*)a3.plan + PLAN_E))[tid & 255];
+                const int cl = min(tid, a3.Cout - 1);
+                pc3v = ((const int4*)((const char*)a3.plan + PLAN_CH))[cl];
+                corr3v = a3.corr ? (uint32_t)a3.corr[cl] : 0u;
+            }
+            if (tid < 256) s_tab3[tid] = tv3;
+            if (tid < 16 * g.T3) {
+                s_pc3[tid] = pc3v;
+                s_corr3[tid] = corr3v;
             }
         }
     }
