@@ -140,9 +140,10 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
         // TAIL: the first round of cv2's weight rows and of the band's
         // prefix channels, cv2's table entry and constants, requested with
         // the loads above (each later round would be one more memory
-        // round trip before the first MFMA); EARLY only for C = 16, where
-        // the registers holding them leave the occupancy unchanged
-        constexpr bool EARLY = TAIL && WM == 1;
+        // round trip before the first MFMA); NE chunks a thread a round
+        // (C 32: one, to keep the registers within 4 waves a SIMD)
+        constexpr bool EARLY = TAIL && WM <= 2;
+        constexpr int NE = WM == 1 ? 4 : 1;
         const int kgp3 = TAIL ? 4 * g.KS3 : 0;
         const int n3 = TAIL ? 16 * g.T3 * kgp3 : 0;
         const int cpp3 = TAIL ? g.off_d >> 4 : 1;
@@ -150,15 +151,15 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
         const int8_t* xp3 =
             TAIL ? (const int8_t*)a3.x + ((int64_t)n * OH + oy0) * OW * a3.x_sp
                  : nullptr;
-        v4i w3[4], pv3[4];
-        int a3w[4], ap3[4];
+        v4i w3[NE], pv3[NE];
+        int a3w[NE], ap3[NE];
         int tv3 = 0;
         int4 pc3v = int4{0, 0, 0, 0};
         uint32_t corr3v = 0;
         auto load_w3 = [&](int e0) __attribute__((always_inline)) {
             const int rs3 = (int)a3.wp_rstride;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < NE; ++u) {
                 const int e = e0 + u * CP_NT;
                 const int r = cp_div(e, g.m_kgp3), k = e - r * kgp3;
                 const bool ok = e < n3;
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
         };
         auto load_pre = [&](int e0) __attribute__((always_inline)) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < NE; ++u) {
                 const int e = e0 + u * CP_NT;
                 const bool ok = e < np3;
                 const int px = ok ? e / cpp3 : 0, c = ok ? e - px * cpp3 : 0;
@@ -230,17 +231,17 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
                 *(v4i*)(s_w2 + aw[u]) = w2[u];
             }
         if constexpr (TAIL) {  // cv2's weights, table, constants
-            for (int e0 = tid; e0 < n3; e0 += 4 * CP_NT) {
+            for (int e0 = tid; e0 < n3; e0 += NE * CP_NT) {
                 if (!EARLY || e0 != tid) load_w3(e0);
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
+                for (int u = 0; u < NE; ++u)
                     if (a3w[u] >= 0) *(v4i*)(s_w3 + a3w[u]) = w3[u];
             }
             // the prefix channels of the band's output pixels
-            for (int e0 = tid; e0 < np3; e0 += 4 * CP_NT) {
+            for (int e0 = tid; e0 < np3; e0 += NE * CP_NT) {
                 if (!EARLY || e0 != tid) load_pre(e0);
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
+                for (int u = 0; u < NE; ++u)
                     if (ap3[u] >= 0) *(v4i*)(s_pre + ap3[u]) = pv3[u];
             }
             if (!EARLY) {
