@@ -419,6 +419,35 @@ typedef struct qa_pool_params {
 int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
                    void* stream);
 
+/* Packed int8 weights (qa_pack_weights_i8, layout 0: rows of kgp 16-byte
+ * K-groups, kgp a multiple of 4) rearranged in fragment order: the 1 KB
+ * matrix-core fragment of each 16-row tile and 64-byte K-step stored
+ * contiguously (chunk (j, s, l) at ((j * kgp / 4 + s) * 64 + l) * 16 is
+ * K-group 4 s + l / 16 of row 16 j + l % 16; zero past the last row).
+ * qa_fragments_i8_size gives the bytes (0 for invalid sizes);
+ * qa_d_pack_fragments_i8 writes them from device memory to device memory.
+ * No counterpart in the reference: a layout for qa_d_conv_pw_pool. */
+int64_t qa_fragments_i8_size(int64_t rows, int64_t kgp);
+int qa_d_pack_fragments_i8(const void* packed, int64_t rows, int64_t kgp,
+                           void* out, void* stream);
+
+/* qa_d_conv_pool with the convolution's producer in the same launch: d1
+ * and d2 are int8 1x1 stride-1 convolutions (packed layout 0, one group,
+ * table plans, no residual, rescaled copy or weight offsets), d2 reading
+ * d1's output (d2->x == d1->y, d2->C == d1->Cout <= 256), images of at
+ * most 64 pixels (d1->x dense channels-last, 16-byte aligned pixels);
+ * w1f / w2f hold d1's and d2's weights in fragment order
+ * (qa_d_pack_fragments_i8 of d->w, d->w_rows, d->w_kgp). The pooled result
+ * is what qa_d_conv(d1) then qa_d_conv_pool(d2, p) store; neither d1->y
+ * nor d2->y is written. Returns -1, launching nothing, for any other pair.
+ * The reference runs the three layers one after another
+ * (quant_layers.py:320-335 twice, then quant_layers.py:569-583).
+ * qa_conv_pw_pool_supported checks a pair without launching (1 or 0). */
+int qa_conv_pw_pool_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
+int qa_d_conv_pw_pool(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                      const qa_pool_params* p, const void* w1f,
+                      const void* w2f, void* stream);
+
 /* Two chained convolutions in one launch (the bottleneck of a C2f block):
  * d1 and d2 are int8 3x3 stride-1 pad-1 convolutions C -> C (C = 16, 32,
  * 64 or 128; packed layout 0, one group, epilogue plans, dense channels-last

@@ -249,5 +249,18 @@ struct PoolArgs {
     int64_t out_sn;
 };
 bool launch_conv_pool(const ConvArgs& a, const PoolArgs& p, hipStream_t st);
+// Two 1x1 convolutions, the second's output pooled, in one launch
+// (qa_conv_pw_pool.hip); arguments in launch form, b2 reading b1's output.
+bool conv_pw_pool_applies(const ConvArgs& b1, const ConvArgs& b2);
+// w1f / w2f: the weights in fragment order (launch_pack_fragments)
+bool launch_conv_pw_pool(const ConvArgs& b1, const ConvArgs& b2,
+                         const PoolArgs& p, const int8_t* w1f,
+                         const int8_t* w2f, hipStream_t st);
+// Packed layout-0 weight rows (rows x kgp 16-byte chunks) in fragment
+// order: the 1 KB MFMA fragment of each 16-row tile and 64-byte K-step
+// contiguous, lane l's 16 bytes at 16 l (fragments_bytes bytes).
+int64_t fragments_bytes(int64_t rows, int64_t kgp);
+bool launch_pack_fragments(const int8_t* src, int64_t rows, int64_t kgp,
+                           int8_t* dst, hipStream_t st);
 
 }  // namespace qa

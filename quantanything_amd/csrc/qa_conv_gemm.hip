@@ -887,6 +887,70 @@ QA_API int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
     return launch_conv_pool(a, pl, st) ? 0 : -1;
 }
 
+static bool pw_pool_args(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                         ConvArgs& b1, ConvArgs& b2, const char* who) {
+    ConvArgs a1, a2;
+    if (desc_args(d1, a1, who) != 1 || desc_args(d2, a2, who) != 1)
+        return false;
+    fast_io_args(a1, b1, -1);
+    fast_io_args(a2, b2, -1);
+    return conv_pw_pool_applies(b1, b2);
+}
+
+QA_API int qa_conv_pw_pool_supported(const qa_conv_desc* d1,
+                                     const qa_conv_desc* d2) {
+    ConvArgs b1, b2;
+    return pw_pool_args(d1, d2, b1, b2, "qa_conv_pw_pool_supported") ? 1 : 0;
+}
+
+QA_API int64_t qa_fragments_i8_size(int64_t rows, int64_t kgp) {
+    return rows > 0 && kgp > 0 && kgp % 4 == 0 ? fragments_bytes(rows, kgp)
+                                               : 0;
+}
+
+QA_API int qa_d_pack_fragments_i8(const void* packed, int64_t rows,
+                                  int64_t kgp, void* out, void* stream_) {
+    if (!packed || !out || qa_fragments_i8_size(rows, kgp) == 0) {
+        set_error("qa_d_pack_fragments_i8",
+                  "needs packed weights, rows > 0 and a multiple of 4 "
+                  "K-groups");
+        return -1;
+    }
+    return launch_pack_fragments((const int8_t*)packed, rows, kgp,
+                                 (int8_t*)out, (hipStream_t)stream_)
+               ? 0
+               : -1;
+}
+
+QA_API int qa_d_conv_pw_pool(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                             const qa_pool_params* p, const void* w1f,
+                             const void* w2f, void* stream_) {
+    ConvArgs b1, b2;
+    if (!p || !p->out || !w1f || !w2f ||
+        !pw_pool_args(d1, d2, b1, b2, "qa_d_conv_pw_pool")) {
+        set_error("qa_d_conv_pw_pool",
+                  "needs two int8 1x1 convolutions with table plans (no "
+                  "residual, second output or weight offsets), the second "
+                  "reading the first's output, images of at most 64 pixels, "
+                  "at most 256 channels between them, and a pool");
+        return -1;
+    }
+    PoolArgs pl;
+    pl.base = d2->OH * d2->OW * (d2->y_so - p->in_zp);
+    pl.mult = p->mult;
+    pl.shift = p->shift;
+    pl.zp = p->zp;
+    pl.qmin = p->qmin;
+    pl.qmax = p->qmax;
+    pl.out_so = p->out_so;
+    pl.out = (int8_t*)p->out;
+    pl.out_sn = p->out_sn;
+    return launch_conv_pw_pool(b1, b2, pl, (const int8_t*)w1f,
+                               (const int8_t*)w2f, (hipStream_t)stream_)
+               ? 0
+               : -1;
+}
+
 QA_API int qa_d_quantize_conv(const qa_conv_desc* d, const float* x,
                               double in_scale, int64_t in_zp, int64_t in_qmin,
                               int64_t in_qmax, void* stream_) {

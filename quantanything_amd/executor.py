@@ -481,6 +481,7 @@ class DeviceExecutor:
         self.softmax_lut = {}
         self.gap_info = {}  # pool launch -> layer, input, output, parameters
         self.pair_descs = {}  # fused pair launch -> (first, second desc)
+        self.pool_descs = {}  # fused conv + pool launch -> (desc, params)
         self.tunables = []  # (launch name, desc, tile codes, fn(stream))
         self.f64_descs = []  # (desc, None, None, launch name), FP64 path
         self.outputs_f32 = {}
@@ -660,6 +661,7 @@ class DeviceExecutor:
         self._fuse_patch_input(cons)
         self._fuse_input_quantization(cons)
         self._fuse_pools(cons)
+        self._fuse_pool_heads(cons)
         self._fuse_pairs(cons)
         self._fuse_pair_tails(cons)
         self._fuse_chains(cons)
@@ -1067,7 +1069,55 @@ class DeviceExecutor:
                              for n, f in self.launches if n != gname]
             codes = [0, 0x10001] + ([0x10002] if d.Cout > 64 else [])
             self.tunables.append((fused, d, codes, fn))
+            self.pool_descs[fused] = (d, pp)
             self.tensors.pop(xname, None)  # never materialized
+
+    def _fuse_pool_heads(self, cons):
+        """A 1x1 convolution whose output only feeds a pooled 1x1
+        convolution runs in the pool's launch (``qa_d_conv_pw_pool``): the
+        two layers of a classifier head before its pool in one launch, the
+        intermediate kept in LDS and never written."""
+        for fused, (d2, pp) in list(self.pool_descs.items()):
+            live = dict(self.launches)
+            if fused not in live:
+                continue
+            firsts = [(d, ln) for d, _, _, ln in self.mfma_descs
+                      if d.y == d2.x and ln in live]
+            if len(firsts) != 1:
+                continue
+            d1, ln1 = firsts[0]
+            mids = [n for n, t in self.tensors.items() if t.ptr == d1.y]
+            if len(mids) != 1 or mids[0] in self.graph.outputs or \
+                    [l.name for l in cons.get(mids[0], [])] != \
+                    [fused[len("convpool:"):]]:
+                continue
+            if not self.lib.qa_conv_pw_pool_supported(ctypes.byref(d1),
+                                                      ctypes.byref(d2)):
+                continue
+            name = f"convpool:{ln1[5:]}+{fused[len('convpool:'):]}"
+            # both weight sets in fragment order, made once here
+            frag = []
+            stream = torch.cuda.current_stream().cuda_stream
+            for d in (d1, d2):
+                size = self.lib.qa_fragments_i8_size(d.w_rows, d.w_kgp)
+                buf = torch.empty(max(size, 1), dtype=torch.int8,
+                                  device="cuda")
+                _ok(self.lib.qa_d_pack_fragments_i8(
+                    d.w, d.w_rows, d.w_kgp, buf.data_ptr(), stream),
+                    "qa_d_pack_fragments_i8")
+                self.keep.append(buf)
+                frag.append(buf.data_ptr())
+
+            def fn(s, d1=d1, d2=d2, pp=pp, f1=frag[0], f2=frag[1]):
+                _ok(self.lib.qa_d_conv_pw_pool(ctypes.byref(d1),
+                                               ctypes.byref(d2),
+                                               ctypes.byref(pp), f1, f2, s),
+                    "qa_d_conv_pw_pool")
+
+            self.launches = [(name, fn) if n == fused else (n, f)
+                             for n, f in self.launches if n != ln1]
+            self.tunables = [t for t in self.tunables if t[0] != fused]
+            self.tensors.pop(mids[0], None)  # never materialized
 
     def _fuse_attention(self, cons):
         """MatMul(q, k^T) -> Softmax over its rows -> MatMul(., v), int8,
