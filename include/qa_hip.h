@@ -247,6 +247,13 @@ typedef struct qa_conv_desc {
                                   the pixel sums, exact in int64 */
     const int64_t* wsplit_k;   /* with wsplit: per output channel
                                   (128 + x_add) * wsum[co] */
+    const void* w_frag;        /* w_code 1 only, optional: w in fragment
+                                  order (qa_d_pack_fragments_i8 of w, w_rows,
+                                  w_kgp); the narrow-GEMM kernel (tile
+                                  0x12000 / 0x12001) then loads each weight
+                                  fragment as one contiguous KB straight
+                                  into registers, and qa_d_conv_pw_pool
+                                  requires it. Results do not depend on it. */
 } qa_conv_desc;
 
 /* Host-side planner of the int8 table epilogue of qa_d_conv. From the
@@ -426,7 +433,7 @@ int qa_d_conv_pool(const qa_conv_desc* d, const qa_pool_params* p,
  * K-group 4 s + l / 16 of row 16 j + l % 16; zero past the last row).
  * qa_fragments_i8_size gives the bytes (0 for invalid sizes);
  * qa_d_pack_fragments_i8 writes them from device memory to device memory.
- * No counterpart in the reference: a layout for qa_d_conv_pw_pool. */
+ * No counterpart in the reference: the layout of qa_conv_desc.w_frag. */
 int64_t qa_fragments_i8_size(int64_t rows, int64_t kgp);
 int qa_d_pack_fragments_i8(const void* packed, int64_t rows, int64_t kgp,
                            void* out, void* stream);
@@ -435,9 +442,8 @@ int qa_d_pack_fragments_i8(const void* packed, int64_t rows, int64_t kgp,
  * and d2 are int8 1x1 stride-1 convolutions (packed layout 0, one group,
  * table plans, no residual, rescaled copy or weight offsets), d2 reading
  * d1's output (d2->x == d1->y, d2->C == d1->Cout <= 256), images of at
- * most 64 pixels (d1->x dense channels-last, 16-byte aligned pixels);
- * w1f / w2f hold d1's and d2's weights in fragment order
- * (qa_d_pack_fragments_i8 of d->w, d->w_rows, d->w_kgp). The pooled result
+ * most 64 pixels (d1->x dense channels-last, 16-byte aligned pixels), and
+ * both with their weights in fragment order (d->w_frag). The pooled result
  * is what qa_d_conv(d1) then qa_d_conv_pool(d2, p) store; neither d1->y
  * nor d2->y is written. Returns -1, launching nothing, for any other pair.
  * The reference runs the three layers one after another
@@ -445,8 +451,7 @@ int qa_d_pack_fragments_i8(const void* packed, int64_t rows, int64_t kgp,
  * qa_conv_pw_pool_supported checks a pair without launching (1 or 0). */
 int qa_conv_pw_pool_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
 int qa_d_conv_pw_pool(const qa_conv_desc* d1, const qa_conv_desc* d2,
-                      const qa_pool_params* p, const void* w1f,
-                      const void* w2f, void* stream);
+                      const qa_pool_params* p, void* stream);
 
 /* Two chained convolutions in one launch (the bottleneck of a C2f block):
  * d1 and d2 are int8 3x3 stride-1 pad-1 convolutions C -> C (C = 16, 32,

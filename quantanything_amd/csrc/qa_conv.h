@@ -50,6 +50,7 @@ struct ConvArgs {
     int64_t M;                      // N*OH*OW
     // ---- packed int8 weights (MFMA path) ----
     const int8_t* wp;
+    const int8_t* wfrag;            // the same in fragment order, or NULL
     int32_t layout;                 // 0 tap-major 16-channel groups, 1 stem
     int32_t CB, KG, KGp, Kreal;
     uint64_t mg_cb, mg_kw;          // ceil(2^32 / CB), ceil(2^32 / KW)
@@ -252,10 +253,9 @@ bool launch_conv_pool(const ConvArgs& a, const PoolArgs& p, hipStream_t st);
 // Two 1x1 convolutions, the second's output pooled, in one launch
 // (qa_conv_pw_pool.hip); arguments in launch form, b2 reading b1's output.
 bool conv_pw_pool_applies(const ConvArgs& b1, const ConvArgs& b2);
-// w1f / w2f: the weights in fragment order (launch_pack_fragments)
+// b1.wfrag / b2.wfrag: the weights in fragment order (required)
 bool launch_conv_pw_pool(const ConvArgs& b1, const ConvArgs& b2,
-                         const PoolArgs& p, const int8_t* w1f,
-                         const int8_t* w2f, hipStream_t st);
+                         const PoolArgs& p, hipStream_t st);
 // Packed layout-0 weight rows (rows x kgp 16-byte chunks) in fragment
 // order: the 1 KB MFMA fragment of each 16-row tile and 64-byte K-step
 // contiguous, lane l's 16 bytes at 16 l (fragments_bytes bytes).

@@ -698,6 +698,7 @@ int desc_args(const qa_conv_desc* d, ConvArgs& a, const char* who) {
             return -1;
         }
         a.wp = (const int8_t*)d->w;
+        a.wfrag = (const int8_t*)d->w_frag;
         a.layout = (int32_t)d->w_layout;
         a.CB = (int32_t)CB;
         a.KG = (int32_t)KG;
@@ -923,16 +924,15 @@ QA_API int qa_d_pack_fragments_i8(const void* packed, int64_t rows,
 }
 
 QA_API int qa_d_conv_pw_pool(const qa_conv_desc* d1, const qa_conv_desc* d2,
-                             const qa_pool_params* p, const void* w1f,
-                             const void* w2f, void* stream_) {
+                             const qa_pool_params* p, void* stream_) {
     ConvArgs b1, b2;
-    if (!p || !p->out || !w1f || !w2f ||
-        !pw_pool_args(d1, d2, b1, b2, "qa_d_conv_pw_pool")) {
+    if (!p || !p->out || !pw_pool_args(d1, d2, b1, b2, "qa_d_conv_pw_pool")) {
         set_error("qa_d_conv_pw_pool",
                   "needs two int8 1x1 convolutions with table plans (no "
                   "residual, second output or weight offsets), the second "
                   "reading the first's output, images of at most 64 pixels, "
-                  "at most 256 channels between them, and a pool");
+                  "at most 256 channels between them, weights in fragment "
+                  "order, and a pool");
         return -1;
     }
     PoolArgs pl;
@@ -945,10 +945,7 @@ QA_API int qa_d_conv_pw_pool(const qa_conv_desc* d1, const qa_conv_desc* d2,
     pl.out_so = p->out_so;
     pl.out = (int8_t*)p->out;
     pl.out_sn = p->out_sn;
-    return launch_conv_pw_pool(b1, b2, pl, (const int8_t*)w1f,
-                               (const int8_t*)w2f, (hipStream_t)stream_)
-               ? 0
-               : -1;
+    return launch_conv_pw_pool(b1, b2, pl, (hipStream_t)stream_) ? 0 : -1;
 }
 
 QA_API int qa_d_quantize_conv(const qa_conv_desc* d, const float* x,

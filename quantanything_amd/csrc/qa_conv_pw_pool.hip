@@ -15,7 +15,7 @@
 // VGPRs, loaded straight from global memory: every load of the launch
 // (tables, the image's pixels, per-channel constants, both weight sets) is
 // issued before the first use, so the work-group waits about one memory
-// round trip. The weights come in fragment order (qa_d_pack_fragments_i8:
+// round trip. The weights come in fragment order (ConvArgs.wfrag:
 // the 1 KB MFMA fragment of a 16-channel tile and K-step contiguous, lane
 // l's 16 bytes at 16 l), so each wave load is one contiguous KB, whole
 // cache lines; read from the packed rows (16 rows x 64 bytes a load, half
@@ -363,19 +363,19 @@ bool launch_pack_fragments(const int8_t* src, int64_t rows, int64_t kgp,
 }
 
 bool launch_conv_pw_pool(const ConvArgs& b1, const ConvArgs& b2,
-                         const PoolArgs& pl, const int8_t* w1f,
-                         const int8_t* w2f, hipStream_t st) {
+                         const PoolArgs& pl, hipStream_t st) {
     const int cblk = pp_cblk(b2);
     const PwPoolGeom g = pp_geom(b1, b2, cblk);
     const PpKern k = pp_kernel(b1.KGp / 4, b2.KGp / 4);
-    if (g.lds == 0 || !k || !pl.out || !w1f || !w2f) {
+    if (g.lds == 0 || !k || !pl.out || !b1.wfrag || !b2.wfrag) {
         set_error("launch_conv_pw_pool", "convolutions outside the kernel's "
-                                         "scope");
+                                         "scope, or weights not in fragment "
+                                         "order");
         return false;
     }
     const dim3 grid((unsigned)b1.N, (unsigned)ceil_div(b2.Cout, cblk));
     hipLaunchKernelGGL(k, grid, dim3(PP_NT), (size_t)g.lds, st, b1, b2, pl, g,
-                       w1f, w2f);
+                       b1.wfrag, b2.wfrag);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_hip_error("launch_conv_pw_pool", e);

@@ -13,16 +13,22 @@
 // one barrier, the MFMAs and the epilogue.
 //
 // A work-group of 4 waves covers 16 rows x 64 channels (Cout 64), 32 x 32
-// or 64 x 16; wave w owns one 16 x 16 block and holds all of its K-steps'
-// weight fragments in VGPRs. The MFMA takes the weights as its first
+// or 64 x 16; wave w owns one 16 x 16 block. With the weights in fragment
+// order (ConvArgs.wfrag) each wave loads its 16 x K block's fragments
+// straight into VGPRs, one contiguous KB a load. The activation rows (and
+// otherwise the weight rows, K bytes each) go to
+// LDS by direct global -> LDS loads in which each group of 4 lanes reads one
+// 64-byte K-step of one row: adjacent lanes, adjacent bytes, so a load
+// instruction is 16 requests of 64 bytes (a lane per row, as the MFMA
+// fragment layout would have it, makes 64 requests of 16 bytes, and the
+// 4096 x 576 x 64 GEMM took 3.2 instead of 2.95 us). In LDS the 64-byte
+// segment of (K-step s, row r) sits at (s R + r) 64 (R rows of the
+// operand), its 16-byte chunk k at position k ^ ((r >> 2) & 3), so that
+// the 16 lanes of a fragment read (rows 16 j .. 16 j + 15, one chunk) fall
+// in distinct bank groups. The MFMA takes the weights as its first
 // operand, so its result lane l holds channels 4 (l >> 4) + i of row
 // (l & 15): four consecutive bytes of one output row, stored as one word,
-// with no exchange between lanes. With ALDS (Cout 64: one row tile) the
-// work-group's 16 activation rows go once to LDS by direct global -> LDS
-// loads, a quarter of the L1 reads of loading them per wave; a direct load
-// of 64 lanes fills 1 KB of LDS in lane order, lane l taking row l & 15,
-// k-group l >> 4 of its K-step, which is the MFMA fragment layout, so each
-// fragment read is one contiguous KB. Epilogue per value: the plan's 64-bit
+// with no exchange between lanes. Epilogue per value: the plan's 64-bit
 // multiply-add and shift with the zero-point correction folded into its
 // constant, one med3 clip, then the table entry or, for an identity plan
 // (plain requantize), the byte offset.
@@ -38,6 +44,7 @@ constexpr int GN_DEVICES = 16;
 struct GnArgs {
     const int8_t* x;       // activation rows, xpst bytes apart
     const int8_t* wp;      // packed weight rows, 16 * KGp bytes apart
+    const int8_t* wf;      // the same in fragment order (WF)
     const char* plan;      // table epilogue plan
     const int64_t* corr;   // per-channel correction (zeros when none)
     const int32_t* boff;   // per-channel weight offsets (RS)
@@ -50,47 +57,52 @@ struct GnArgs {
 __device__ int64_t gn_zero_corr[64];
 
 // NB: 16-channel blocks (1, 2 or 4); the work-group's 4 waves cover 4 / NB
-// row tiles of 16. RS: pixel sums (weights with an offset). ALDS: the
-// activation rows staged once in LDS (NB = 4).
-template <int NB, bool RS, bool ALDS>
+// row tiles of 16. RS: pixel sums (weights with an offset). WF: the weights
+// in fragment order, each wave's fragments loaded straight into VGPRs (one
+// contiguous KB a load); otherwise staged in LDS like the activations.
+template <int NB, bool RS, bool WF>
 __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
-    static_assert(!ALDS || NB == 4, "one row tile per work-group");
     constexpr int RT = 4 / NB;
+    constexpr int RW = 16 * NB, RX = 16 * RT;  // weight / activation rows
     __shared__ int s_tab[256];
-    // ALDS: K-step s of row r, k-group g at 16 (64 s + 16 g + r). (A size
-    // that depends on ALDS makes hipcc's host pass drop the launch stubs
-    // when the direct-load builtin writes the array; unused, it takes no
-    // LDS.)
-    __shared__ __attribute__((aligned(16))) int8_t s_x[16 * 64 * GN_KMAX];
+    __shared__ __attribute__((aligned(16)))
+    int8_t s_w[WF ? 16 : RW * 64 * GN_KMAX];
+    __shared__ __attribute__((aligned(16))) int8_t s_x[RX * 64 * GN_KMAX];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kg = lane >> 4;
     const int c0 = (wave % NB) * 16;
-    const int64_t p0 = ((int64_t)blockIdx.x * RT + wave / NB) * 16;
+    const int64_t px = (int64_t)blockIdx.x * RX;  // the work-group's rows
+    const int64_t p0 = px + (wave / NB) * 16;     // this wave's
     const int nks = a.KGp >> 2;  // 64-byte K-steps, 1..GN_KMAX
-    const int8_t* xr = a.x + min(p0 + col, a.M - 1) * a.xpst + 16 * kg;
-    const int8_t* wr = a.wp + (c0 + col) * (16 * a.KGp) + 16 * kg;
 
-    // every request first, unconditionally
+    // every request first: the table entry, then the direct loads of both
+    // operands (instruction i of an operand: segments 16 i .. 16 i + 15 in
+    // (K-step, row) order, row fastest; lane l: segment 16 i + l / 4,
+    // position l % 4), then the constants
     const int tv = ((const int*)(a.plan + PLAN_E))[tid];
-    v4i fw[GN_KMAX], fx[GN_KMAX];
+    const int g = lane >> 2, q = lane & 3;
+    auto dloads = [&](const int8_t* base, int64_t rs, int R, int64_t rmax,
+                      int8_t* dst) __attribute__((always_inline)) {
+        const int n = R * nks / 16;  // instructions (R a multiple of 16)
+        for (int i = wave; i < n; i += 4) {
+            const int sg = 16 * i + g, st = sg / R, r = sg - st * R;
+            const int64_t row = min((int64_t)r, rmax);
+            __builtin_amdgcn_global_load_lds(
+                base + row * rs + 64 * st + 16 * (q ^ ((r >> 2) & 3)),
+                dst + 1024 * i, 16, 0, 0);
+        }
+    };
+    v4i fwr[GN_KMAX];
+    if (WF) {  // fragment (tile c0 / 16, K-step s) at 1024 (tile nks + s)
+        const int8_t* wr = a.wf + (int64_t)(c0 >> 4) * nks * 1024 + 16 * lane;
 #pragma unroll
-    for (int s = 0; s < GN_KMAX; ++s) {
-        const int o = min(s, nks - 1) * 64;  // past the last: re-read it
-        fw[s] = *(const v4i*)(wr + o);
-        if (!ALDS) fx[s] = *(const v4i*)(xr + o);
+        for (int s = 0; s < GN_KMAX; ++s)
+            fwr[s] = *(const v4i*)(wr + 1024 * min(s, nks - 1));
+    } else {
+        dloads(a.wp, 16 * a.KGp, RW, RW - 1, s_w);
     }
-    if (ALDS) {
-        // wave w: K-steps w, w + 4, ... (each LDS KB written once: the
-        // compiler would order two direct loads to one address by a wait)
-        auto dload = [&](int t) __attribute__((always_inline)) {
-            __builtin_amdgcn_global_load_lds(xr + t * 64, s_x + 1024 * t, 16,
-                                             0, 0);
-        };
-#pragma unroll
-        for (int s = 0; s < GN_KMAX; s += 4)
-            if (s + wave < nks) dload(s + wave);
-    }
+    dloads(a.x + px * a.xpst, a.xpst, RX, a.M - 1 - px, s_x);
     const int4 hdr = *(const int4*)a.plan;
     const int pD = ((const int*)a.plan)[4];
     int4 pc[4];
@@ -109,20 +121,19 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (ALDS) {
-#pragma unroll
-        for (int s = 0; s < GN_KMAX; ++s)
-            fx[s] = *(const v4i*)(s_x + 1024 * min(s, nks - 1) + 16 * lane);
-    }
-
+    // fragments: rows 16 j + col, chunk kg of K-step s
+    const int sw = 16 * (kg ^ ((col >> 2) & 3));
+    const int8_t* fw0 = s_w + (c0 + col) * 64 + sw;
+    const int8_t* fx0 = s_x + (int)(p0 - px + col) * 64 + sw;
     v4i acc = v4i{0, 0, 0, 0};
     int psum = 0;
 #pragma unroll
     for (int s = 0; s < GN_KMAX; ++s) {
         if (s < nks) {
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[s], fx[s], acc, 0,
-                                                        0, 0);
-            if (RS) psum += bytes_sum(fx[s], 16);
+            const v4i fw = WF ? fwr[s] : *(const v4i*)(fw0 + s * RW * 64);
+            const v4i fx = *(const v4i*)(fx0 + s * RX * 64);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw, fx, acc, 0, 0, 0);
+            if (RS) psum += bytes_sum(fx, 16);
         }
     }
     if (RS) {  // the row's byte sum over its 4 k-group lanes
@@ -192,6 +203,7 @@ bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, bool alds) {
     GnArgs g;
     g.x = (const int8_t*)b.x;
     g.wp = b.wp;
+    g.wf = b.wfrag;
     g.plan = (const char*)b.plan;
     g.corr = corr;
     g.boff = b.boff;
@@ -202,21 +214,17 @@ bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, bool alds) {
     g.KGp = b.KGp;
     g.pad = 0;
     const dim3 grid((unsigned)blocks);
-    if (nb == 4 && alds) {
-        if (b.rowsum)
-            k_gemm_narrow<4, true, true><<<grid, 256, 0, st>>>(g);
-        else
-            k_gemm_narrow<4, false, true><<<grid, 256, 0, st>>>(g);
-    } else {
-        switch (nb * 2 + (b.rowsum ? 1 : 0)) {
-#define QA_GN_CASE(NB, RS)                                          \
-    case NB * 2 + RS:                                               \
-        k_gemm_narrow<NB, RS != 0, false><<<grid, 256, 0, st>>>(g); \
+    (void)alds;  // both operands are always staged in LDS
+    switch (nb * 4 + (b.rowsum ? 2 : 0) + (b.wfrag ? 1 : 0)) {
+#define QA_GN_CASE(NB, RS, WF)                                             \
+    case NB * 4 + RS * 2 + WF:                                             \
+        k_gemm_narrow<NB, RS != 0, WF != 0><<<grid, 256, 0, st>>>(g);       \
         break;
-            QA_GN_CASE(1, 0) QA_GN_CASE(1, 1) QA_GN_CASE(2, 0)
-            QA_GN_CASE(2, 1) QA_GN_CASE(4, 0) QA_GN_CASE(4, 1)
+        QA_GN_CASE(1, 0, 0) QA_GN_CASE(1, 1, 0) QA_GN_CASE(2, 0, 0)
+        QA_GN_CASE(2, 1, 0) QA_GN_CASE(4, 0, 0) QA_GN_CASE(4, 1, 0)
+        QA_GN_CASE(1, 0, 1) QA_GN_CASE(1, 1, 1) QA_GN_CASE(2, 0, 1)
+        QA_GN_CASE(2, 1, 1) QA_GN_CASE(4, 0, 1) QA_GN_CASE(4, 1, 1)
 #undef QA_GN_CASE
-        }
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

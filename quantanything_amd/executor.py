@@ -63,7 +63,8 @@ class ConvDesc(ctypes.Structure):
                                              "r2_zp_in", "r2_m", "r2_s",
                                              "r2_zp_out", "r2_qmin",
                                              "r2_qmax")]
-        + [("tile", _I64), ("wsplit", _P), ("wsplit_k", _P)])
+        + [("tile", _I64), ("wsplit", _P), ("wsplit_k", _P),
+           ("w_frag", _P)])
 
 
 def storage_of(bits, signed):
@@ -667,6 +668,11 @@ class DeviceExecutor:
         self._fuse_chains(cons)
         if self.fuse_attention:
             self._fuse_attention(cons)
+        live = dict(self.launches)
+        for d, _, _, name in self.mfma_descs:
+            # the narrow-GEMM kernel's weights in fragment order
+            if name in live and self.narrow_ok(d):
+                self._frag_weights(d)
         for d, _, _, name in self.mfma_descs + self.f64_descs:
             if name in dict(self.launches):
                 self.tunables.append(
@@ -1072,6 +1078,22 @@ class DeviceExecutor:
             self.pool_descs[fused] = (d, pp)
             self.tensors.pop(xname, None)  # never materialized
 
+    def _frag_weights(self, d):
+        """Sets ``d.w_frag``: the descriptor's int8 weights in fragment order
+        (made once, on the current stream, kept with the plan)."""
+        if d.w_frag:
+            return
+        size = self.lib.qa_fragments_i8_size(d.w_rows, d.w_kgp)
+        if size <= 0:
+            return
+        buf = torch.empty(size, dtype=torch.int8, device="cuda")
+        _ok(self.lib.qa_d_pack_fragments_i8(
+            d.w, d.w_rows, d.w_kgp, buf.data_ptr(),
+            torch.cuda.current_stream().cuda_stream),
+            "qa_d_pack_fragments_i8")
+        self.keep.append(buf)
+        d.w_frag = buf.data_ptr()
+
     def _fuse_pool_heads(self, cons):
         """A 1x1 convolution whose output only feeds a pooled 1x1
         convolution runs in the pool's launch (``qa_d_conv_pw_pool``): the
@@ -1095,23 +1117,13 @@ class DeviceExecutor:
                                                       ctypes.byref(d2)):
                 continue
             name = f"convpool:{ln1[5:]}+{fused[len('convpool:'):]}"
-            # both weight sets in fragment order, made once here
-            frag = []
-            stream = torch.cuda.current_stream().cuda_stream
-            for d in (d1, d2):
-                size = self.lib.qa_fragments_i8_size(d.w_rows, d.w_kgp)
-                buf = torch.empty(max(size, 1), dtype=torch.int8,
-                                  device="cuda")
-                _ok(self.lib.qa_d_pack_fragments_i8(
-                    d.w, d.w_rows, d.w_kgp, buf.data_ptr(), stream),
-                    "qa_d_pack_fragments_i8")
-                self.keep.append(buf)
-                frag.append(buf.data_ptr())
+            for d in (d1, d2):  # both weight sets in fragment order
+                self._frag_weights(d)
 
-            def fn(s, d1=d1, d2=d2, pp=pp, f1=frag[0], f2=frag[1]):
+            def fn(s, d1=d1, d2=d2, pp=pp):
                 _ok(self.lib.qa_d_conv_pw_pool(ctypes.byref(d1),
                                                ctypes.byref(d2),
-                                               ctypes.byref(pp), f1, f2, s),
+                                               ctypes.byref(pp), s),
                     "qa_d_conv_pw_pool")
 
             self.launches = [(name, fn) if n == fused else (n, f)
@@ -2143,6 +2155,13 @@ class DeviceExecutor:
 
     # ------------------------------------------------------------ tiling --
     @staticmethod
+    def narrow_ok(d):
+        """Whether the narrow-GEMM kernel takes an int8 descriptor."""
+        return d.KH == d.KW == 1 and d.G == 1 and d.w_layout == 0 and \
+            d.Cout in (16, 32, 64) and d.C % 64 == 0 and d.C <= 576 and \
+            bool(d.epi_plan) and not d.res and not d.y2
+
+    @staticmethod
     def tile_candidates(d):
         """``qa_conv_desc.tile`` codes worth timing for one MFMA
         convolution. FP64 path: 0 (the library's choice), then each of its
@@ -2168,11 +2187,9 @@ class DeviceExecutor:
             # the large-GEMM kernel (128 x 128 blocks): K steps staged
             # through registers, or through 3 / 4 LDS stages of direct loads
             out += [0x10400, 0x10403, 0x10404]
-        if d.KH == d.KW == 1 and d.G == 1 and d.w_layout == 0 and \
-                d.Cout in (16, 32, 64) and d.C % 64 == 0 and d.C <= 576 and \
-                d.epi_plan and not d.res and not d.y2:
-            # narrow GEMM: a 16 x 16 block a wave, operands in registers
-            # (0x12001, Cout 64: the activation rows staged once in LDS)
+        if DeviceExecutor.narrow_ok(d):
+            # narrow GEMM: a 16 x 16 block a wave (0x12000; 0x12001 is the
+            # same kernel, kept for recorded tile sets)
             out += [0x12000] + ([0x12001] if d.Cout == 64 else [])
         if d.w_layout == 0 and d.G == 1 and d.C % 16 == 0 and \
                 d.OW <= 256 and d.epi_plan and (d.H > 1 or d.W > 1):

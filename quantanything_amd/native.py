@@ -69,7 +69,7 @@ def _declare(lib):
         "qa_d_quantize_conv": (i32, [p, p, f64, i64, i64, i64, p]),
         "qa_d_conv_pool": (i32, [p, p, p]),
         "qa_conv_pw_pool_supported": (i32, [p, p]),
-        "qa_d_conv_pw_pool": (i32, [p, p, p, p, p, p]),
+        "qa_d_conv_pw_pool": (i32, [p, p, p, p]),
         "qa_fragments_i8_size": (i64, [i64, i64]),
         "qa_d_pack_fragments_i8": (i32, [p, i64, i64, p, p]),
         "qa_conv_pair_supported": (i32, [p, p]),

@@ -55,6 +55,15 @@ class _Workload:
                                "epilogue")
         self.plan = _dev(plan, np.uint8)
         d.epi_plan = self.plan.data_ptr()
+        # the weights in fragment order too (the narrow-GEMM kernel's form)
+        size = self.lib.qa_fragments_i8_size(d.w_rows, d.w_kgp)
+        self.wfrag = torch.empty(max(size, 1), dtype=torch.int8,
+                                 device="cuda")
+        _ok(self.lib.qa_d_pack_fragments_i8(
+            d.w, d.w_rows, d.w_kgp, self.wfrag.data_ptr(),
+            torch.cuda.current_stream().cuda_stream),
+            "qa_d_pack_fragments_i8")
+        d.w_frag = self.wfrag.data_ptr()
         self.d = d
 
     def launch(self, stream=None):

@@ -528,3 +528,47 @@ def test_fused_conv_chain(hip, tmp_path, cin, c, k, stride, size, batch):
                 got, oracle.env[name].reshape(got.shape), err_msg=name)
             checked += 1
     assert checked >= 2
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+@pytest.mark.parametrize("cin,cout,size,batch", [
+    (64, 16, 9, 3),     # one channel block: 4 row tiles a work-group
+    (128, 32, 7, 2),    # two channel blocks, 98 rows (a partial work-group)
+    (576, 64, 5, 3),    # 9 K-steps, 75 rows
+    (192, 64, 16, 2),   # 3 K-steps, 512 rows
+])
+def test_narrow_gemm_kernel(hip, tmp_path, quant_type, cin, cout, size,
+                            batch):
+    """The narrow-GEMM kernel (tile codes 0x12000 / 0x12001: activations
+    staged in LDS by coalesced direct loads, swizzled; weights from their
+    fragment-order copy, or staged like the activations without one) equals
+    the oracle for 16, 32 and 64 output channels, ragged row counts and
+    weights with an offset (uint8: the row sums)."""
+    b = G.GraphBuilder(23)
+    y = b.silu(b.conv("images", cin, cout, 1, 1, pad=0,
+                      w_scale=np.sqrt(1.0 / cin), b_scale=0.05))
+    g = b.build("images", [None, cin, size, size], y)
+    calib = [Stream(130 + i).normal((batch, cin, size, size))
+             .astype(np.float32) for i in range(2)]
+    c = _calibrated(g, quant_type, True, calib)
+    x = Stream(140).normal((batch, cin, size, size)).astype(np.float32)
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    oracle.run(x, keep=True)
+    ex = c.executor({"images": x.shape})
+    assert len(ex.tunables) == 1
+    d, codes = ex.tunables[0][1], ex.tunables[0][2]
+    assert 0x12000 in codes and d.w_frag
+    frag = d.w_frag
+    for code, wf in [(c_, f) for c_ in codes if c_ & 0x12000 == 0x12000
+                     for f in (frag, None)]:
+        d.tile, d.w_frag = code, wf
+        ex.run({"images": x})
+        checked = 0
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, tile {code:#x}")
+                checked += 1
+        assert checked >= 1
