@@ -224,13 +224,16 @@ typedef struct qa_conv_desc {
                       held in registers (at most 36 / wm K-steps of 64
                       bytes), bands of R output rows (R 0: the library's
                       choice) in LDS (layout 0, one group, a table plan,
-                      int8 weights without a zero point); 0x12000: 1x1
-                      stride-1 convolutions and GEMMs of 16, 32 or 64
-                      output channels, C a multiple of 64 up to 576, a
-                      table plan without residual or second output: one
-                      16 x 16 block a wave with every operand in registers
-                      at once (0x12001, Cout 64: the activation rows staged
-                      once per work-group in LDS). FP64 path (w_code
+                      int8 weights without a zero point); 0x12000 |
+                      (T - 1) << 4 (T 1..4): 1x1 stride-1 convolutions and
+                      GEMMs of 16, 32 or 64 output channels or a multiple
+                      of 4 above 64 (in blocks of 64), C a multiple of 64
+                      up to 576 (up to 1280 with Cout >= 64 and w_frag), a
+                      table plan without residual (a rescaled copy
+                      allowed): one 16 x 16 block a wave with its weight
+                      fragments in registers, T row tiles of 16 a wave, the
+                      activation rows staged in LDS (0x12001 is 0x12000).
+                      FP64 path (w_code
                       8): 0x10000 | wm | tm << 4
                       | split << 8 with (wm, tm, split) one of (1,1,0),
                       (2,1,0), (1,4,0), (1,1,1), (2,1,1), (4,1,1); tm =

@@ -195,12 +195,13 @@ bool gemm_big_applies(const ConvArgs& b, int epi);
 // stages 3 or 4: the K loop through that many LDS stages filled by direct
 // loads; otherwise the register-staged two-buffer loop
 bool launch_gemm_big(const ConvArgs& b, hipStream_t st, int stages = 0);
-// Narrow GEMMs / pointwise convolutions (Cout 16, 32 or 64, K a multiple of
-// 64 up to 576, table plan without residual or copy): every operand of a
-// 16 x 16 block in registers at once (qa_gemm_narrow.hip).
+// Narrow GEMMs / pointwise convolutions (Cout 16, 32, 64 or blocks of 64,
+// K a multiple of 64 up to 576, or 1280 with fragment-order weights, table
+// plan without residual; a rescaled copy allowed): a 16 x 16 block a wave
+// with its weight fragments in VGPRs (qa_gemm_narrow.hip).
 bool gemm_narrow_applies(const ConvArgs& b, int epi);
-// alds: the activation rows staged once per work-group in LDS (Cout 64)
-bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, bool alds);
+// rtl: row tiles each wave computes (1..4) with the same weights
+bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, int rtl);
 // int8 convolutions over bands of output rows with the input band and the
 // weights in LDS (qa_conv_band.hip); wm = 16-channel groups per work-group.
 bool conv_band_applies(const ConvArgs& b, int epi, int wm);

@@ -87,7 +87,7 @@ bool launch_conv_mfma(const ConvArgs& a, hipStream_t st) {
     // all of its operands in registers (tile hint bit 13)
     if ((a.tile_hint & TILE_VALID) && ((a.tile_hint >> 13) & 1) &&
         gemm_narrow_applies(b, epi))
-        return launch_gemm_narrow(b, st, a.tile_hint & 1);
+        return launch_gemm_narrow(b, st, 1 + ((a.tile_hint >> 4) & 3));
     // large GEMMs: 128 x 128 blocks (tile hint bit 10 chooses; its low
     // bits 3 or 4 the direct-to-LDS pipeline with that many stages)
     if (gemm_big_applies(b, epi)) {

@@ -1,7 +1,9 @@
 // Narrow int8 GEMMs and pointwise convolutions with the table epilogue:
-// 16, 32 or 64 output channels, K a multiple of 64 up to 576, any number of
-// rows M (the standalone 4096 x 576 x 64 GEMM, the 1x1 convolutions of 16 -
-// 64 channels over 64 to 576 input channels).
+// 16, 32 or 64 output channels, or any multiple of 4 in blocks of 64; K a
+// multiple of 64 up to 576 (1280 in 64-channel blocks with the weights in
+// fragment order); any number of rows M (the standalone 4096 x 576 x 64
+// GEMM, the 1x1 convolutions of a classifier's late stages, its
+// 1280 -> 1000 head).
 //
 // Such a launch moves a few MB and does well under a microsecond of matrix
 // work, so its time is its chain of dependent steps, not arithmetic. The
@@ -37,8 +39,7 @@
 namespace qa {
 namespace {
 
-constexpr int GN_KMAX = 9;  // K-steps of 64 bytes held in registers
-constexpr int GN_DEVICES = 16;
+constexpr int GN_KMAX = 20;  // K-steps of 64 bytes (K up to 1280)
 
 // The kernel's arguments, read in one scalar round.
 struct GnArgs {
@@ -46,35 +47,40 @@ struct GnArgs {
     const int8_t* wp;      // packed weight rows, 16 * KGp bytes apart
     const int8_t* wf;      // the same in fragment order (WF)
     const char* plan;      // table epilogue plan
-    const int64_t* corr;   // per-channel correction (zeros when none)
+    const int64_t* corr;   // per-channel correction (NULL: none)
     const int32_t* boff;   // per-channel weight offsets (RS)
     int8_t* y;             // output rows, ypst bytes apart
-    int64_t xpst, ypst, M;
-    int32_t KGp, pad;
+    int8_t* y2;            // the rescaled copy (NULL: none), y2pst apart
+    int64_t xpst, ypst, y2pst, M;
+    int32_t KGp, Cout, RTL, pad;
 };
 
-// The correction read by plans without one (zero-initialized; read only).
-__device__ int64_t gn_zero_corr[64];
-
-// NB: 16-channel blocks (1, 2 or 4); the work-group's 4 waves cover 4 / NB
-// row tiles of 16. RS: pixel sums (weights with an offset). WF: the weights
-// in fragment order, each wave's fragments loaded straight into VGPRs (one
-// contiguous KB a load); otherwise staged in LDS like the activations.
-template <int NB, bool RS, bool WF>
+// NB: 16-channel blocks (1, 2 or 4) a work-group; blockIdx.y selects the
+// work-group's block of 16 NB channels (NB = 4 past 64 output channels).
+// Its 4 waves cover 4 / NB row tiles of 16 at a time, RTL times (each
+// wave's weight fragments stay in VGPRs over its RTL row tiles, which
+// the work-group stages together). RS: pixel sums (weights with an
+// offset). WF: the weights in fragment order, each wave's fragments loaded
+// straight into VGPRs (one contiguous KB a load); otherwise staged in LDS
+// like the activations. KM: K-steps held (9; 20 with NB = 4 and WF).
+// Dynamic LDS: the activation rows (16 (4 / NB) RTL of them), then (not
+// WF) the weight rows.
+template <int NB, bool RS, bool WF, int KM>
 __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     constexpr int RT = 4 / NB;
-    constexpr int RW = 16 * NB, RX = 16 * RT;  // weight / activation rows
+    constexpr int RW = 16 * NB;  // weight rows
+    extern __shared__ int4 gn_dyn[];
     __shared__ int s_tab[256];
-    __shared__ __attribute__((aligned(16)))
-    int8_t s_w[WF ? 16 : RW * 64 * GN_KMAX];
-    __shared__ __attribute__((aligned(16))) int8_t s_x[RX * 64 * GN_KMAX];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kg = lane >> 4;
-    const int c0 = (wave % NB) * 16;
+    const int nks = a.KGp >> 2;  // 64-byte K-steps, 1..KM
+    const int RX = 16 * RT * a.RTL;               // the work-group's rows
+    int8_t* const s_x = (int8_t*)gn_dyn;
+    int8_t* const s_w = s_x + RX * nks * 64;
+    const int cw = (int)blockIdx.y * RW;          // the work-group's channels
+    const int c0 = cw + (wave % NB) * 16;         // this wave's
     const int64_t px = (int64_t)blockIdx.x * RX;  // the work-group's rows
-    const int64_t p0 = px + (wave / NB) * 16;     // this wave's
-    const int nks = a.KGp >> 2;  // 64-byte K-steps, 1..GN_KMAX
 
     // every request first: the table entry, then the direct loads of both
     // operands (instruction i of an operand: segments 16 i .. 16 i + 15 in
@@ -93,25 +99,25 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
                 dst + 1024 * i, 16, 0, 0);
         }
     };
-    v4i fwr[GN_KMAX];
+    v4i fwr[KM];
     if (WF) {  // fragment (tile c0 / 16, K-step s) at 1024 (tile nks + s)
         const int8_t* wr = a.wf + (int64_t)(c0 >> 4) * nks * 1024 + 16 * lane;
 #pragma unroll
-        for (int s = 0; s < GN_KMAX; ++s)
+        for (int s = 0; s < KM; ++s)
             fwr[s] = *(const v4i*)(wr + 1024 * min(s, nks - 1));
-    } else {
-        dloads(a.wp, 16 * a.KGp, RW, RW - 1, s_w);
     }
     dloads(a.x + px * a.xpst, a.xpst, RX, a.M - 1 - px, s_x);
+    if (!WF)  // weight rows cw .. cw + RW - 1 (packed rows padded to 128)
+        dloads(a.wp + (int64_t)cw * 16 * a.KGp, 16 * a.KGp, RW, RW - 1, s_w);
     const int4 hdr = *(const int4*)a.plan;
     const int pD = ((const int*)a.plan)[4];
     int4 pc[4];
     uint32_t crr[4], cbo[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const int c = c0 + 4 * kg + r;
+        const int c = min(c0 + 4 * kg + r, a.Cout - 1);
         pc[r] = ((const int4*)(a.plan + PLAN_CH))[c];
-        crr[r] = (uint32_t)a.corr[c];
+        crr[r] = a.corr ? (uint32_t)a.corr[c] : 0u;
         cbo[r] = RS ? (uint32_t)a.boff[c] : 0u;
     }
     // every load done (the direct ones among them), the table to LDS, then
@@ -121,43 +127,59 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    // fragments: rows 16 j + col, chunk kg of K-step s
-    const int sw = 16 * (kg ^ ((col >> 2) & 3));
-    const int8_t* fw0 = s_w + (c0 + col) * 64 + sw;
-    const int8_t* fx0 = s_x + (int)(p0 - px + col) * 64 + sw;
-    v4i acc = v4i{0, 0, 0, 0};
-    int psum = 0;
+    if (!WF) {
+        const int8_t* fw0 =
+            s_w + (c0 - cw + col) * 64 + 16 * (kg ^ ((col >> 2) & 3));
 #pragma unroll
-    for (int s = 0; s < GN_KMAX; ++s) {
-        if (s < nks) {
-            const v4i fw = WF ? fwr[s] : *(const v4i*)(fw0 + s * RW * 64);
-            const v4i fx = *(const v4i*)(fx0 + s * RX * 64);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw, fx, acc, 0, 0, 0);
-            if (RS) psum += bytes_sum(fx, 16);
-        }
+        for (int s = 0; s < KM; ++s)
+            fwr[s] = *(const v4i*)(fw0 + min(s, nks - 1) * RW * 64);
     }
-    if (RS) {  // the row's byte sum over its 4 k-group lanes
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
-    }
-
+    int64_t cc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        cc[r] = plan_fold((int64_t)(((uint64_t)(uint32_t)pc[r].w << 32) |
+                                    (uint32_t)pc[r].z),
+                          crr[r], pc[r].x);
     const int pA = hdr.x, pB = hdr.y;
     const bool idt = hdr.w & PLAN_IDENT;
-    int e[4];
+    const int cs = c0 + 4 * kg;  // the lane's 4 channels (Cout % 4 == 0)
+    // row tile j = wave / NB + RT t of the work-group: rows 16 j + col,
+    // chunk kg of K-step s
+    for (int t = 0; t < a.RTL; ++t) {
+        const int j = wave / NB + RT * t;
+        const int8_t* fx0 =
+            s_x + (16 * j + col) * 64 + 16 * (kg ^ ((col >> 2) & 3));
+        v4i acc = v4i{0, 0, 0, 0};
+        int psum = 0;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        int w = acc[r];
-        if (RS) w += (int)(cbo[r] * (uint32_t)psum);
-        const int64_t cc = plan_fold(
-            (int64_t)(((uint64_t)(uint32_t)pc[r].w << 32) |
-                      (uint32_t)pc[r].z),
-            crr[r], pc[r].x);
-        const int v = med3_i32(plan_q0(w, pc[r].x, cc, pc[r].y), pA, pB);
-        e[r] = idt ? v + pD : s_tab[v - pA];
+        for (int s = 0; s < KM; ++s) {
+            if (s < nks) {
+                const v4i fx = *(const v4i*)(fx0 + s * RX * 64);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fwr[s], fx, acc,
+                                                           0, 0, 0);
+                if (RS) psum += bytes_sum(fx, 16);
+            }
+        }
+        if (RS) {  // the row's byte sum over its 4 k-group lanes
+            psum += __shfl_xor(psum, 16);
+            psum += __shfl_xor(psum, 32);
+        }
+        int e[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            int w = acc[r];
+            if (RS) w += (int)(cbo[r] * (uint32_t)psum);
+            const int v = med3_i32(plan_q0(w, pc[r].x, cc[r], pc[r].y), pA,
+                                   pB);
+            e[r] = idt ? v + pD : s_tab[v - pA];
+        }
+        const int64_t p = px + 16 * j + col;
+        if (p < a.M && cs < a.Cout) {
+            *(uint32_t*)(a.y + p * a.ypst + cs) = pack_entries(e, 0);
+            if (a.y2)
+                *(uint32_t*)(a.y2 + p * a.y2pst + cs) = pack_entries(e, 1);
+        }
     }
-    const int64_t p = p0 + col;
-    if (p < a.M)
-        *(uint32_t*)(a.y + p * a.ypst + c0 + 4 * kg) = pack_entries(e, 0);
 }
 
 }  // namespace
@@ -169,62 +191,83 @@ bool gemm_narrow_applies(const ConvArgs& b, int epi) {
     // dense channels-last tensor
     const int64_t xpst = hw == 1 ? b.x_sn : b.x_sp;
     return epi == Q8_TABLE && b.mode == EPI_QUANT && b.fastio && b.plan &&
-           !b.res && !b.y2 && b.G == 1 && b.layout == 0 && b.KH == 1 &&
+           !b.res && b.G == 1 && b.layout == 0 && b.KH == 1 &&
            b.KW == 1 && b.SH == 1 && b.SW == 1 && b.PH == 0 && b.PW == 0 &&
            b.OH == b.H && b.OW == b.W && (hw == 1 || b.x_sn == hw * b.x_sp) &&
            b.x_code == 1 && b.x_sc == 1 && xpst % 16 == 0 && xa % 16 == 0 &&
-           (b.Cout == 16 || b.Cout == 32 || b.Cout == 64) &&
-           b.Cg % 64 == 0 && b.KGp * 16 == b.Cg && b.KGp <= 4 * GN_KMAX &&
+           b.Cout >= 16 && b.Cout % 4 == 0 &&
+           (b.Cout <= 64 ? b.Cout % 16 == 0 : b.Cout <= 64 * 65535) &&
+           b.Cg % 64 == 0 && b.KGp * 16 == b.Cg &&
+           (b.KGp <= 36 ||
+            (b.KGp <= 4 * GN_KMAX && b.Cout >= 64 && b.wfrag)) &&
            b.wp_rstride == (int64_t)b.KGp * 16 && b.y_code == 1 &&
            b.M < ((int64_t)1 << 31);
 }
 
-bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, bool alds) {
-    const int nb = b.Cout / 16;
-    const int64_t blocks = ceil_div(b.M, 16 * (4 / nb));
-    if (blocks >= ((int64_t)1 << 31)) {
+bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, int rtl) {
+    // Cout 16 / 32 / 64: one channel block of Cout; beyond, blocks of 64
+    const int nb = b.Cout <= 64 ? b.Cout / 16 : 4;
+    // row tiles a wave: 1..4, fewer where the rows would not fit in 64 KB
+    // of LDS (results do not depend on it)
+    const int64_t per = (int64_t)(b.KGp / 4) * 64 * 16 * (4 / nb);
+    const int64_t wrows = b.wfrag ? 0 : (int64_t)(b.KGp / 4) * 64 * 16 * nb;
+    rtl = std::max(1, std::min(rtl, 4));
+    while (rtl > 1 && per * rtl + wrows > 64 * 1024) --rtl;
+    const int rx = 16 * (4 / nb) * rtl;  // rows a work-group
+    const int64_t blocks = ceil_div(b.M, rx);
+    const int64_t cblocks = ceil_div(b.Cout, 16 * nb);
+    if (blocks >= ((int64_t)1 << 31) || cblocks > 65535) {
         set_error("launch_gemm_narrow", "grid too large");
         return false;
-    }
-    const int64_t* corr = b.corr;
-    if (!corr) {  // gn_zero_corr's address on the current device
-        static int64_t* zeros[GN_DEVICES] = {};
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || dev < 0 ||
-            dev >= GN_DEVICES ||
-            (!zeros[dev] &&
-             hipGetSymbolAddress((void**)&zeros[dev],
-                                 HIP_SYMBOL(gn_zero_corr)) != hipSuccess)) {
-            set_error("launch_gemm_narrow", "no zero correction array");
-            return false;
-        }
-        corr = zeros[dev];
     }
     GnArgs g;
     g.x = (const int8_t*)b.x;
     g.wp = b.wp;
     g.wf = b.wfrag;
     g.plan = (const char*)b.plan;
-    g.corr = corr;
+    g.corr = b.corr;
     g.boff = b.boff;
     g.y = (int8_t*)b.y;
+    g.y2 = (int8_t*)b.y2;
     g.xpst = (int64_t)b.H * b.W == 1 ? b.x_sn : b.x_sp;
     g.ypst = b.y_pst;
+    g.y2pst = b.y2_pst;
     g.M = b.M;
     g.KGp = b.KGp;
+    g.Cout = b.Cout;
+    g.RTL = rtl;
     g.pad = 0;
-    const dim3 grid((unsigned)blocks);
-    (void)alds;  // both operands are always staged in LDS
-    switch (nb * 4 + (b.rowsum ? 2 : 0) + (b.wfrag ? 1 : 0)) {
-#define QA_GN_CASE(NB, RS, WF)                                             \
-    case NB * 4 + RS * 2 + WF:                                             \
-        k_gemm_narrow<NB, RS != 0, WF != 0><<<grid, 256, 0, st>>>(g);       \
+    const dim3 grid((unsigned)blocks, (unsigned)cblocks);
+    // activation rows, then (without fragment order) the weight rows
+    const size_t lds = (size_t)(b.KGp / 4) * 64 *
+                       (rx + (b.wfrag ? 0 : 16 * nb));
+    if (lds > 64 * 1024) {
+        set_error("launch_gemm_narrow", "rows do not fit in LDS");
+        return false;
+    }
+    if (b.KGp > 36) {  // 10..20 K-steps: 64-channel blocks, fragment order
+        if (nb != 4 || !b.wfrag) {
+            set_error("launch_gemm_narrow", "K past 576 needs 64-channel "
+                                            "blocks and fragment-order "
+                                            "weights");
+            return false;
+        }
+        if (b.rowsum)
+            k_gemm_narrow<4, true, true, GN_KMAX><<<grid, 256, lds, st>>>(g);
+        else
+            k_gemm_narrow<4, false, true, GN_KMAX><<<grid, 256, lds, st>>>(g);
+    } else {
+        switch (nb * 4 + (b.rowsum ? 2 : 0) + (b.wfrag ? 1 : 0)) {
+#define QA_GN_CASE(NB, RS, WF)                                            \
+    case NB * 4 + RS * 2 + WF:                                            \
+        k_gemm_narrow<NB, RS != 0, WF != 0, 9><<<grid, 256, lds, st>>>(g); \
         break;
-        QA_GN_CASE(1, 0, 0) QA_GN_CASE(1, 1, 0) QA_GN_CASE(2, 0, 0)
-        QA_GN_CASE(2, 1, 0) QA_GN_CASE(4, 0, 0) QA_GN_CASE(4, 1, 0)
-        QA_GN_CASE(1, 0, 1) QA_GN_CASE(1, 1, 1) QA_GN_CASE(2, 0, 1)
-        QA_GN_CASE(2, 1, 1) QA_GN_CASE(4, 0, 1) QA_GN_CASE(4, 1, 1)
+            QA_GN_CASE(1, 0, 0) QA_GN_CASE(1, 1, 0) QA_GN_CASE(2, 0, 0)
+            QA_GN_CASE(2, 1, 0) QA_GN_CASE(4, 0, 0) QA_GN_CASE(4, 1, 0)
+            QA_GN_CASE(1, 0, 1) QA_GN_CASE(1, 1, 1) QA_GN_CASE(2, 0, 1)
+            QA_GN_CASE(2, 1, 1) QA_GN_CASE(4, 0, 1) QA_GN_CASE(4, 1, 1)
 #undef QA_GN_CASE
+        }
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

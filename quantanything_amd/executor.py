@@ -2158,8 +2158,10 @@ class DeviceExecutor:
     def narrow_ok(d):
         """Whether the narrow-GEMM kernel takes an int8 descriptor."""
         return d.KH == d.KW == 1 and d.G == 1 and d.w_layout == 0 and \
-            d.Cout in (16, 32, 64) and d.C % 64 == 0 and d.C <= 576 and \
-            bool(d.epi_plan) and not d.res and not d.y2
+            d.Cout >= 16 and d.Cout % 4 == 0 and \
+            (d.Cout > 64 or d.Cout % 16 == 0) and d.C % 64 == 0 and \
+            (d.C <= 576 or (d.C <= 1280 and d.Cout >= 64)) and \
+            bool(d.epi_plan) and not d.res
 
     @staticmethod
     def tile_candidates(d):
@@ -2188,9 +2190,9 @@ class DeviceExecutor:
             # through registers, or through 3 / 4 LDS stages of direct loads
             out += [0x10400, 0x10403, 0x10404]
         if DeviceExecutor.narrow_ok(d):
-            # narrow GEMM: a 16 x 16 block a wave (0x12000; 0x12001 is the
-            # same kernel, kept for recorded tile sets)
-            out += [0x12000] + ([0x12001] if d.Cout == 64 else [])
+            # narrow GEMM: a 16 x 16 block a wave, 1, 2 or 4 row tiles a
+            # wave with the same weights
+            out += [0x12000, 0x12010, 0x12030]
         if d.w_layout == 0 and d.G == 1 and d.C % 16 == 0 and \
                 d.OW <= 256 and d.epi_plan and (d.H > 1 or d.W > 1):
             # bands of output rows, operands in LDS (the library checks the

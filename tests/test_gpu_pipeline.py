@@ -536,17 +536,29 @@ def test_fused_conv_chain(hip, tmp_path, cin, c, k, stride, size, batch):
     (128, 32, 7, 2),    # two channel blocks, 98 rows (a partial work-group)
     (576, 64, 5, 3),    # 9 K-steps, 75 rows
     (192, 64, 16, 2),   # 3 K-steps, 512 rows
+    (256, 256, 7, 4),   # 4 channel blocks of 64
+    (128, 200, 6, 3),   # a partial last channel block (200 = 3 x 64 + 8)
+    (1280, 1000, 1, 64),  # a classifier head: 20 K-steps, one pixel an image
+    (128, 128, 9, 2),   # with a rescaled copy (a C2f's Split / Concat)
 ])
 def test_narrow_gemm_kernel(hip, tmp_path, quant_type, cin, cout, size,
                             batch):
     """The narrow-GEMM kernel (tile codes 0x12000 / 0x12001: activations
     staged in LDS by coalesced direct loads, swizzled; weights from their
     fragment-order copy, or staged like the activations without one) equals
-    the oracle for 16, 32 and 64 output channels, ragged row counts and
-    weights with an offset (uint8: the row sums)."""
+    the oracle for 16, 32 and 64 output channels, blocks of 64 channels
+    (a partial last one), K up to 1280, ragged row counts and weights with
+    an offset (uint8: the row sums)."""
     b = G.GraphBuilder(23)
     y = b.silu(b.conv("images", cin, cout, 1, 1, pad=0,
                       w_scale=np.sqrt(1.0 / cin), b_scale=0.05))
+    if cin == cout == 128:  # a C2f-style Split / Concat: the copy y2
+        h1, h2 = b.op("Split", [y, b.const(np.array([64, 64], np.int64))],
+                      n_out=2, axis=1)
+        # both halves first, as a C2f concatenates them, and a wider range
+        # in the Concat, so that they are copied rescaled by the 1x1 conv
+        y = b.op("Concat", [h1, h2, b.conv(h2, 64, 64, 3, 1, w_scale=1.0)],
+                 axis=1)
     g = b.build("images", [None, cin, size, size], y)
     calib = [Stream(130 + i).normal((batch, cin, size, size))
              .astype(np.float32) for i in range(2)]
@@ -555,12 +567,16 @@ def test_narrow_gemm_kernel(hip, tmp_path, quant_type, cin, cout, size,
     oracle = OraclePipeline(g, _qjson(c, tmp_path))
     oracle.run(x, keep=True)
     ex = c.executor({"images": x.shape})
-    assert len(ex.tunables) == 1
-    d, codes = ex.tunables[0][1], ex.tunables[0][2]
+    first = [t for t in ex.tunables if t[1].KH == 1]
+    assert len(first) == 1
+    d, codes = first[0][1], first[0][2]
     assert 0x12000 in codes and d.w_frag
+    assert bool(d.y2) == (cin == cout == 128)
     frag = d.w_frag
+    # past 9 K-steps only the fragment-order weights are taken
+    forms = (frag, None) if cin <= 576 else (frag,)
     for code, wf in [(c_, f) for c_ in codes if c_ & 0x12000 == 0x12000
-                     for f in (frag, None)]:
+                     for f in forms]:
         d.tile, d.w_frag = code, wf
         ex.run({"images": x})
         checked = 0
