@@ -418,10 +418,13 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
         const int64_t base = (live ? r : 0) * cols;
         int sv[PER];
         int mx = 0;
+        // every load unconditional (clamped into the row), so that all of
+        // them are in flight at once
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int64_t i = gl + GS * k;
-            sv[k] = live && i < cols ? (int)x[base + i] + 128 : -1;
+            const int v = (int)x[base + min(i, cols - 1)];
+            sv[k] = live && i < cols ? v + 128 : -1;
             mx = max(mx, sv[k]);
         }
 #pragma unroll
@@ -430,7 +433,8 @@ __global__ __launch_bounds__(kThreads) void k_softmax_rows_lut(
         double e[PER], sum = 0.0;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            e[k] = sv[k] >= 0 ? tr[sv[k]] : 0.0;
+            const double tv = tr[max(sv[k], 0)];
+            e[k] = sv[k] >= 0 ? tv : 0.0;
             sum += e[k];
         }
 #pragma unroll
