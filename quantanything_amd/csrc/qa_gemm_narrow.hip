@@ -53,6 +53,11 @@ struct GnArgs {
     int8_t* y2;            // the rescaled copy (NULL: none), y2pst apart
     int64_t xpst, ypst, y2pst, M;
     int32_t KGp, Cout, RTL, pad;
+    // CV (a k x k convolution, Cg a multiple of 64): the image geometry;
+    // row p is output pixel p of the batch, K-step s covers tap s / CBK,
+    // input channels 64 (s % CBK) ..; x_sn / xpst: image / pixel strides
+    int64_t x_sn;
+    int32_t H, W, OH, OW, SH, SW, PH, PW, DH, DW, KW, CBK, padv, pad2;
 };
 
 // NB: 16-channel blocks (1, 2 or 4) a work-group; blockIdx.y selects the
@@ -65,7 +70,11 @@ struct GnArgs {
 // like the activations. KM: K-steps held (9; 20 with NB = 4 and WF).
 // Dynamic LDS: the activation rows (16 (4 / NB) RTL of them), then (not
 // WF) the weight rows.
-template <int NB, bool RS, bool WF, int KM>
+// CV: the activation rows are the im2col rows of a convolution (each
+// 64-byte K-step one tap's 64 channels of one input pixel, loaded like a
+// GEMM row's); a tap outside the image loads pixel (0, 0) and then has
+// its LDS bytes overwritten with the pad value.
+template <int NB, bool RS, bool WF, int KM, bool CV = false>
 __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     constexpr int RT = 4 / NB;
     constexpr int RW = 16 * NB;  // weight rows
@@ -106,7 +115,32 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
         for (int s = 0; s < KM; ++s)
             fwr[s] = *(const v4i*)(wr + 1024 * min(s, nks - 1));
     }
-    dloads(a.x + px * a.xpst, a.xpst, RX, a.M - 1 - px, s_x);
+    uint32_t fix = 0;  // CV: this lane's padding chunks (instruction bits)
+    if (CV) {
+        const int n = RX * nks / 16;
+        const int ohw = a.OH * a.OW;
+        int k = 0;
+        for (int i = wave; i < n; i += 4, ++k) {
+            const int sg = 16 * i + g, st = sg / RX, r = sg - st * RX;
+            const int64_t p = min(px + r, a.M - 1);
+            const int nimg = (int)(p / ohw);
+            const int rem = (int)(p - (int64_t)nimg * ohw);
+            const int oy = rem / a.OW, ox = rem - oy * a.OW;
+            const int tap = st / a.CBK, cpart = st - tap * a.CBK;
+            const int ky = tap / a.KW, kx = tap - ky * a.KW;
+            const int iy = oy * a.SH - a.PH + ky * a.DH;
+            const int ix = ox * a.SW - a.PW + kx * a.DW;
+            const bool in = iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
+            fix |= (in ? 0u : 1u) << k;
+            __builtin_amdgcn_global_load_lds(
+                a.x + (int64_t)nimg * a.x_sn +
+                    ((int64_t)(in ? iy : 0) * a.W + (in ? ix : 0)) * a.xpst +
+                    64 * cpart + 16 * (q ^ ((r >> 2) & 3)),
+                s_x + 1024 * i, 16, 0, 0);
+        }
+    } else {
+        dloads(a.x + px * a.xpst, a.xpst, RX, a.M - 1 - px, s_x);
+    }
     if (!WF)  // weight rows cw .. cw + RW - 1 (packed rows padded to 128)
         dloads(a.wp + (int64_t)cw * 16 * a.KGp, 16 * a.KGp, RW, RW - 1, s_w);
     const int4 hdr = *(const int4*)a.plan;
@@ -124,6 +158,14 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     // one bare barrier (the empty asm keeps LDS accesses on their side)
     __builtin_amdgcn_s_waitcnt(0x0f70);
     s_tab[tid] = tv;
+    if (CV && fix) {  // padding taps: the pad value over what was loaded
+        const int pv = (int)((uint32_t)(uint8_t)a.padv * 0x01010101u);
+        const int n = RX * nks / 16;
+        int k = 0;
+        for (int i = wave; i < n; i += 4, ++k)
+            if ((fix >> k) & 1)
+                *(v4i*)(s_x + 1024 * i + 16 * lane) = v4i{pv, pv, pv, pv};
+    }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -184,7 +226,28 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
 
 }  // namespace
 
+// A k x k convolution the narrow kernel takes as a GEMM over im2col rows
+// (tile codes with the weights in fragment order).
+bool narrow_conv_applies(const ConvArgs& b, int epi) {
+    const uintptr_t xa = (uintptr_t)b.x;
+    return epi == Q8_TABLE && b.mode == EPI_QUANT && b.fastio && b.plan &&
+           !b.res && b.G == 1 && b.layout == 0 && b.wfrag &&
+           (b.KH > 1 || b.KW > 1 || b.SH > 1 || b.SW > 1 || b.PH > 0 ||
+            b.PW > 0 || b.OH != b.H || b.OW != b.W) &&
+           b.x_code == 1 && b.x_sc == 1 && b.Cg % 64 == 0 &&
+           b.x_sp % 16 == 0 && b.x_sn % 16 == 0 && xa % 16 == 0 &&
+           b.KGp * 16 == b.Cg * b.KH * b.KW &&
+           b.Cout >= 16 && b.Cout % 4 == 0 &&
+           (b.Cout <= 64 ? b.Cout % 16 == 0 : b.Cout <= 64 * 65535) &&
+           (b.KGp <= 36 || (b.KGp <= 4 * GN_KMAX && b.Cout >= 64)) &&
+           b.wp_rstride == (int64_t)b.KGp * 16 && b.y_code == 1 &&
+           b.M < ((int64_t)1 << 31) &&
+           (int64_t)b.OH * b.OW < ((int64_t)1 << 31) &&
+           (int64_t)b.H * b.W * b.x_sp < ((int64_t)1 << 31);
+}
+
 bool gemm_narrow_applies(const ConvArgs& b, int epi) {
+    if (narrow_conv_applies(b, epi)) return true;
     const uintptr_t xa = (uintptr_t)b.x;
     const int64_t hw = (int64_t)b.H * b.W;
     // a row's stride: the GEMM's row stride, or the pixel stride of a
@@ -237,6 +300,24 @@ bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, int rtl) {
     g.Cout = b.Cout;
     g.RTL = rtl;
     g.pad = 0;
+    const bool cv = narrow_conv_applies(b, Q8_TABLE);
+    if (cv) {
+        g.xpst = b.x_sp;
+        g.x_sn = b.x_sn;
+        g.H = b.H;
+        g.W = b.W;
+        g.OH = b.OH;
+        g.OW = b.OW;
+        g.SH = b.SH;
+        g.SW = b.SW;
+        g.PH = b.PH;
+        g.PW = b.PW;
+        g.DH = b.DH;
+        g.DW = b.DW;
+        g.KW = b.KW;
+        g.CBK = b.Cg / 64;
+        g.padv = b.pad_value;
+    }
     const dim3 grid((unsigned)blocks, (unsigned)cblocks);
     // activation rows, then (without fragment order) the weight rows
     const size_t lds = (size_t)(b.KGp / 4) * 64 *
@@ -245,7 +326,19 @@ bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, int rtl) {
         set_error("launch_gemm_narrow", "rows do not fit in LDS");
         return false;
     }
-    if (b.KGp > 36) {  // 10..20 K-steps: 64-channel blocks, fragment order
+    if (cv) {  // im2col rows, fragment-order weights
+        const int kcase = (b.KGp > 36 ? 0 : nb) * 2 + (b.rowsum ? 1 : 0);
+        switch (kcase) {
+#define QA_GN_CV(NB, RS, KM)                                                  \
+    case (KM == 9 ? NB : 0) * 2 + RS:                                        \
+        k_gemm_narrow<NB, RS != 0, true, KM, true><<<grid, 256, lds, st>>>(g); \
+        break;
+            QA_GN_CV(1, 0, 9) QA_GN_CV(1, 1, 9) QA_GN_CV(2, 0, 9)
+            QA_GN_CV(2, 1, 9) QA_GN_CV(4, 0, 9) QA_GN_CV(4, 1, 9)
+            QA_GN_CV(4, 0, GN_KMAX) QA_GN_CV(4, 1, GN_KMAX)
+#undef QA_GN_CV
+        }
+    } else if (b.KGp > 36) {  // 10..20 K-steps: 64-channel blocks
         if (nb != 4 || !b.wfrag) {
             set_error("launch_gemm_narrow", "K past 576 needs 64-channel "
                                             "blocks and fragment-order "

@@ -2156,12 +2156,14 @@ class DeviceExecutor:
     # ------------------------------------------------------------ tiling --
     @staticmethod
     def narrow_ok(d):
-        """Whether the narrow-GEMM kernel takes an int8 descriptor."""
-        return d.KH == d.KW == 1 and d.G == 1 and d.w_layout == 0 and \
-            d.Cout >= 16 and d.Cout % 4 == 0 and \
-            (d.Cout > 64 or d.Cout % 16 == 0) and d.C % 64 == 0 and \
-            (d.C <= 576 or (d.C <= 1280 and d.Cout >= 64)) and \
-            bool(d.epi_plan) and not d.res
+        """Whether the narrow-GEMM kernel takes an int8 descriptor (a 1x1
+        convolution or GEMM, or a k x k convolution as a GEMM over its
+        im2col rows)."""
+        k = d.C * d.KH * d.KW  # K of the GEMM (of the im2col rows)
+        return d.G == 1 and d.w_layout == 0 and d.Cout >= 16 and \
+            d.Cout % 4 == 0 and (d.Cout > 64 or d.Cout % 16 == 0) and \
+            d.C % 64 == 0 and (k <= 576 or (k <= 1280 and d.Cout >= 64)) \
+            and bool(d.epi_plan) and not d.res
 
     @staticmethod
     def tile_candidates(d):

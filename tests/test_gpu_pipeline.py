@@ -588,3 +588,45 @@ def test_narrow_gemm_kernel(hip, tmp_path, quant_type, cin, cout, size,
                     err_msg=f"{name}, tile {code:#x}")
                 checked += 1
         assert checked >= 1
+
+
+@pytest.mark.parametrize("quant_type", ["int8", "uint8"])
+@pytest.mark.parametrize("cin,cout,k,stride,pad,dil,size,batch", [
+    (64, 64, 3, 1, 1, 1, 13, 2),     # the 3x3 64 -> 64 layer form
+    (128, 256, 3, 2, 1, 1, 14, 2),   # stride 2, 18 K-steps
+    (64, 128, 3, 2, 1, 1, 15, 3),    # stride 2, odd size
+    (64, 32, 3, 1, 2, 2, 11, 2),     # dilation 2
+    (64, 16, 2, 2, 0, 1, 9, 2),      # 2x2, no padding
+])
+def test_narrow_kernel_on_convolutions(hip, tmp_path, quant_type, cin, cout,
+                                       k, stride, pad, dil, size, batch):
+    """The narrow-GEMM kernel over a convolution's im2col rows (taps
+    outside the image get the pad value in LDS) equals the oracle for every
+    row-tile code, strides, dilation and weights with an offset."""
+    b = G.GraphBuilder(27)
+    y = b.silu(b.conv("images", cin, cout, k, stride, pad=pad, dilation=dil,
+                      w_scale=np.sqrt(1.0 / (cin * k * k)), b_scale=0.05))
+    g = b.build("images", [None, cin, size, size], y)
+    calib = [Stream(150 + i).normal((batch, cin, size, size))
+             .astype(np.float32) for i in range(2)]
+    c = _calibrated(g, quant_type, True, calib)
+    x = Stream(160).normal((batch, cin, size, size)).astype(np.float32)
+    oracle = OraclePipeline(g, _qjson(c, tmp_path))
+    oracle.run(x, keep=True)
+    ex = c.executor({"images": x.shape})
+    assert len(ex.tunables) == 1
+    d, codes = ex.tunables[0][1], ex.tunables[0][2]
+    narrow = [c_ for c_ in codes if c_ & 0x12000 == 0x12000]
+    assert narrow and d.w_frag
+    for code in narrow:
+        d.tile = code
+        ex.run({"images": x})
+        checked = 0
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, tile {code:#x}")
+                checked += 1
+        assert checked >= 1
