@@ -230,6 +230,14 @@ bool launch_conv_pair(const ConvArgs& b1, const ConvArgs& b2, hipStream_t st,
 bool conv_chain_applies(const ConvArgs& b1, int epi1, const ConvArgs& b2,
                         int epi2);
 bool launch_conv_chain(const ConvArgs& b1, const ConvArgs& b2, hipStream_t st);
+// The same pair as two GEMMs over the same rows (qa_narrow_chain.hip): b1
+// a 1x1 or k x k convolution of a multiple of 64 input channels and up to
+// 256 output channels, b2 a 1x1 convolution of up to 256 reading its
+// output, both with fragment-order weights; rtl row tiles of 16 a
+// work-group.
+bool narrow_chain_applies(const ConvArgs& b1, const ConvArgs& b2);
+bool launch_narrow_chain(const ConvArgs& b1, const ConvArgs& b2, int rtl,
+                         hipStream_t st);
 // 16-bit operands on the FP64 matrix cores (qa_conv_f64.hip), exact.
 bool launch_conv_f64(const ConvArgs& a, hipStream_t st);
 

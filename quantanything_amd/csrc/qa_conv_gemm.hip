@@ -833,14 +833,17 @@ QA_API int qa_d_conv_pair_tail(const qa_conv_desc* d1,
     return launch_conv_pair(b1, b2, (hipStream_t)stream_, &b3) ? 0 : -1;
 }
 
-static bool chain_args(const qa_conv_desc* d1, const qa_conv_desc* d2,
-                       ConvArgs& b1, ConvArgs& b2, const char* who) {
+// 0: no chain kernel takes the pair; 1: the weights-in-registers chain
+// (and maybe the narrow one); 2: the narrow chain only
+static int chain_args(const qa_conv_desc* d1, const qa_conv_desc* d2,
+                      ConvArgs& b1, ConvArgs& b2, const char* who) {
     ConvArgs a1, a2;
     if (desc_args(d1, a1, who) != 1 || desc_args(d2, a2, who) != 1)
-        return false;
+        return 0;
     const int e1 = fast_io_args(a1, b1, -1);  // Q8_TABLE or -1
     const int e2 = fast_io_args(a2, b2, -1);
-    return conv_chain_applies(b1, e1, b2, e2);
+    if (conv_chain_applies(b1, e1, b2, e2)) return 1;
+    return e1 != -1 && e2 != -1 && narrow_chain_applies(b1, b2) ? 2 : 0;
 }
 
 QA_API int qa_conv_chain_supported(const qa_conv_desc* d1,
@@ -852,14 +855,28 @@ QA_API int qa_conv_chain_supported(const qa_conv_desc* d1,
 QA_API int qa_d_conv_chain(const qa_conv_desc* d1, const qa_conv_desc* d2,
                            void* stream_) {
     ConvArgs b1, b2;
-    if (!chain_args(d1, d2, b1, b2, "qa_d_conv_chain")) {
+    const int k = chain_args(d1, d2, b1, b2, "qa_d_conv_chain");
+    if (!k) {
         set_error("qa_d_conv_chain",
                   "needs an int8 convolution of 16, 32 or 64 output channels "
                   "(weights-in-registers form, no residual) and a 1x1 "
                   "convolution of the same width reading its output, both "
-                  "with table plans");
+                  "with table plans; or, with the weights in fragment order, "
+                  "a 1x1 or k x k convolution of a multiple of 64 input "
+                  "channels and up to 256 output channels and a 1x1 "
+                  "convolution of up to 256 reading its output");
         return -1;
     }
+    // d2->tile 0x12000 | (T - 1) << 4: the narrow chain, T row tiles a
+    // work-group; the narrow chain also where the other does not apply
+    const int64_t t = d2->tile;
+    const bool narrow_hint = (t & TILE_VALID) && ((t >> 13) & 1);
+    if (k == 2 || (narrow_hint && narrow_chain_applies(b1, b2)))
+        return launch_narrow_chain(b1, b2,
+                                   narrow_hint ? 1 + (int)((t >> 4) & 3) : 1,
+                                   (hipStream_t)stream_)
+                   ? 0
+                   : -1;
     return launch_conv_chain(b1, b2, (hipStream_t)stream_) ? 0 : -1;
 }
 

@@ -1275,11 +1275,20 @@ class DeviceExecutor:
             if len(mids) != 1 or mids[0] in self.graph.outputs or \
                     [l.name for l in cons.get(mids[0], [])] != [ln2[5:]]:
                 continue
+            # the narrow chain kernel reads both weight sets in fragment
+            # order
+            narrow = self.narrow_ok(d1) and d1.Cout <= 256 and \
+                d2.Cout <= 256 and self.code == 1
+            if narrow:
+                self._frag_weights(d1)
+                self._frag_weights(d2)
             if not self.lib.qa_conv_chain_supported(ctypes.byref(d1),
                                                     ctypes.byref(d2)):
                 continue
             fused = f"chain:{ln1[5:]}+{ln2[5:]}"
             rows = [0] + [0x10000 | r for r in BAND_ROWS if r <= d1.OH]
+            if narrow:  # the narrow chain, 1, 2 or 4 row tiles a group
+                rows += [0x12000, 0x12010, 0x12030]
 
             def fn(s, d1=d1, d2=d2):
                 _ok(self.lib.qa_d_conv_chain(ctypes.byref(d1),

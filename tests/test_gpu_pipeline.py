@@ -492,12 +492,16 @@ def test_fused_conv_pair(hip, tmp_path, c, size, batch, residual):
     (32, 64, 3, 2, 15, 3),
     (16, 16, 3, 1, 20, 2),
     (64, 64, 1, 1, 9, 3),    # 1x1 then 1x1
+    (64, 128, 3, 2, 15, 2),  # the narrow chain: im2col rows, 128 channels
+    (128, 256, 3, 2, 14, 2),  # 18 K-steps, 256 channels
+    (128, 128, 1, 1, 7, 3),  # the narrow chain over GEMM rows
 ])
 def test_fused_conv_chain(hip, tmp_path, cin, c, k, stride, size, batch):
     """A convolution whose output only feeds a 1x1 convolution of the same
     width runs with it as one launch (the intermediate kept in LDS) and the
-    result equals the oracle bit for bit; the intermediate tensor is never
-    materialized."""
+    result equals the oracle bit for bit for every tile code of the fused
+    launch (band heights of the weights-in-registers chain, row tiles of
+    the narrow chain); the intermediate tensor is never materialized."""
     b = G.GraphBuilder(29)
     t = b.silu(b.conv("images", cin, c, k, stride,
                       w_scale=np.sqrt(1.0 / (k * k * cin)), b_scale=0.05))
@@ -519,15 +523,23 @@ def test_fused_conv_chain(hip, tmp_path, cin, c, k, stride, size, batch):
     ex = cq.executor({"images": x.shape})
     assert [n for n, _ in ex.launches if n.startswith("chain:")], \
         [n for n, _ in ex.launches]
-    ex.run({"images": x})
-    checked = 0
-    for name, tt in ex.tensors.items():
-        if name in oracle.env:
-            got = tt.to_host()
-            np.testing.assert_array_equal(
-                got, oracle.env[name].reshape(got.shape), err_msg=name)
-            checked += 1
-    assert checked >= 2
+    chain = [t for t in ex.tunables if t[0].startswith("chain:")]
+    assert len(chain) == 1
+    d2, codes = chain[0][1], chain[0][2]
+    if cin % 64 == 0:
+        assert 0x12000 in codes
+    for code in codes:
+        d2.tile = code
+        ex.run({"images": x})
+        checked = 0
+        for name, tt in ex.tensors.items():
+            if name in oracle.env:
+                got = tt.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, tile {code:#x}")
+                checked += 1
+        assert checked >= 2
 
 
 @pytest.mark.parametrize("quant_type", ["int8", "uint8"])
