@@ -13,9 +13,9 @@
 // pixel; taps outside the image get the pad value afterwards), conv 1's
 // weight fragments (fragment order, one contiguous KB a load) go straight
 // into the VGPRs of the wave that owns their channel tile (tile j to wave
-// j % 8), conv 2's whole weight set goes to LDS in fragment order by
-// direct loads, and both tables and every channel's plan constants to
-// LDS. MFMA v_mfma_i32_16x16x64_i8 with the weights as the first operand,
+// j % 8), requested last so that its MFMAs start as they arrive; conv 2's
+// whole weight set, both tables and every channel's plan constants go to
+// LDS by direct loads. MFMA v_mfma_i32_16x16x64_i8 with the weights as the first operand,
 // so the result lane l holds channels 4 (l >> 4) + r of row (l & 15): the
 // 4 stored bytes are one word, into the LDS tile (conv 1) or to HBM (conv
 // 2, with the rescaled copy of a Concat). Epilogues: the table plan of
@@ -49,39 +49,82 @@ struct NcArgs {
         lds_w2;
 };
 
-// KM1: K-steps of conv 1 held (>= ks1); CT1 / CT2: channel tiles a wave
-// owns at most in each conv; CV1: conv 1 is a k x k convolution.
-template <int KM1, int CT1, int CT2, bool CV1>
+// KM1: K-steps of conv 1 (exactly: its MFMA sequence has no branches,
+// so each MFMA waits for its own weight fragment only); CT1 / CT2: channel
+// tiles a wave owns at most in each conv; CV1: conv 1 is a k x k
+// convolution.
+// NW2: conv 2's fragment loads a wave (2 or 8; a fixed count, so that the
+// waits for conv 1's weights, requested before them, count exactly).
+// s_waitcnt vmcnt(n) for a count known after unrolling (n < 64)
+__device__ __forceinline__ void wait_vm(int n) {
+#define QA_VM(N) \
+    case N:      \
+        __builtin_amdgcn_s_waitcnt(0x0f70 | ((N) & 15) | (((N) >> 4) << 14)); \
+        break;
+#define QA_VM4(N) QA_VM(N) QA_VM(N + 1) QA_VM(N + 2) QA_VM(N + 3)
+#define QA_VM16(N) QA_VM4(N) QA_VM4(N + 4) QA_VM4(N + 8) QA_VM4(N + 12)
+    switch (n) {
+        QA_VM16(0) QA_VM16(16) QA_VM16(32) QA_VM16(48)
+        default: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+    }
+#undef QA_VM16
+#undef QA_VM4
+#undef QA_VM
+}
+
+template <int KM1, int CT1, int CT2, bool CV1, int NW2>
 __global__ __launch_bounds__(NC_NT) void k_narrow_chain(NcArgs a) {
     extern __shared__ int4 nc_dyn[];
     int8_t* const s_x = (int8_t*)nc_dyn;   // conv 1's rows
     int8_t* const s_m = s_x + a.lds_m;     // conv 1's output tile
     int8_t* const s_w2 = s_x + a.lds_w2;   // conv 2's weights
-    __shared__ int s_tab1[256], s_tab2[256];
+    __shared__ __attribute__((aligned(16))) int s_tab1[256], s_tab2[256];
     __shared__ int4 s_pc[2][NC_CMAX];
-    __shared__ uint32_t s_cr[2][NC_CMAX];
+    __shared__ __attribute__((aligned(16))) int64_t s_cr[2][NC_CMAX];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kg = lane >> 4;
     const int g = lane >> 2, q = lane & 3;
     const int RX = 16 * a.RTL;
     const int64_t px = (int64_t)blockIdx.x * RX;
-    const int ks1 = a.ks1, ks2 = a.ks2;
+    constexpr int ks1 = KM1;
+    const int ks2 = a.ks2;
     const int T1 = a.C1 >> 4, T2 = a.C2 >> 4;
 
-    // ---- every request first
-    const int tv = tid < 256 ? ((const int*)(a.plan1 + PLAN_E))[tid]
-                             : ((const int*)(a.plan2 + PLAN_E))[tid - 256];
-    int4 pcv[2];
-    uint32_t crv[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {  // thread t: channel t % 256 of conv h
-        const int c = tid & 255;
-        const char* plan = h ? a.plan2 : a.plan1;
-        const int cmax = (h ? a.C2 : a.C1) - 1;
-        const int64_t* corr = h ? a.corr2 : a.corr1;
-        pcv[h] = ((const int4*)(plan + PLAN_CH))[min(c, cmax)];
-        crv[h] = corr ? (uint32_t)corr[min(c, cmax)] : 0u;
+    const int4 hdr1 = *(const int4*)a.plan1;
+    const int4 hdr2 = *(const int4*)a.plan2;
+
+    // ---- every request first: the tables, the plans' per-channel
+    // constants and the corrections by direct global -> LDS loads (16
+    // bytes a lane; channels past the last read the last one), the waves
+    // taking turns
+    {
+        const int n1 = (a.C1 + 63) >> 6, n2 = (a.C2 + 63) >> 6;
+        const int m1 = a.corr1 ? (a.C1 + 127) >> 7 : 0;
+        const int m2 = a.corr2 ? (a.C2 + 127) >> 7 : 0;
+        const int items = 2 + n1 + n2 + m1 + m2;
+        for (int it = wave; it < items; it += NC_NW) {
+            const int8_t* src;
+            int8_t* dst;
+            if (it < 2) {
+                src = (const int8_t*)(it ? a.plan2 : a.plan1) + PLAN_E +
+                      16 * lane;
+                dst = (int8_t*)(it ? s_tab2 : s_tab1);
+            } else if (it < 2 + n1 + n2) {
+                const int h = it >= 2 + n1, i = it - 2 - (h ? n1 : 0);
+                const int c = min(64 * i + lane, (h ? a.C2 : a.C1) - 1);
+                src = (const int8_t*)(h ? a.plan2 : a.plan1) + PLAN_CH +
+                      16 * c;
+                dst = (int8_t*)&s_pc[h][64 * i];
+            } else {
+                const int h = it >= 2 + n1 + n2 + m1;
+                const int i = it - 2 - n1 - n2 - (h ? m1 : 0);
+                const int c = min(128 * i + 2 * lane, (h ? a.C2 : a.C1) - 2);
+                src = (const int8_t*)((h ? a.corr2 : a.corr1) + c);
+                dst = (int8_t*)&s_cr[h][128 * i];
+            }
+            __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+        }
     }
     // conv 1's rows: instruction i covers segments 16 i .. 16 i + 15 in
     // (K-step, row) order, row fastest; lane l: segment 16 i + l / 4,
@@ -116,37 +159,39 @@ __global__ __launch_bounds__(NC_NT) void k_narrow_chain(NcArgs a) {
             __builtin_amdgcn_global_load_lds(src, s_x + 1024 * i, 16, 0, 0);
         }
     }
-    // conv 2's weights, fragment order, to LDS
-    for (int i = wave; i < T2 * ks2; i += NC_NW)
+    asm volatile("" ::: "memory");  // the weights' loads stay after these
+    // conv 1's weight fragments of the wave's tiles (a tile past the last
+    // reads the last one and is not stored), requested last: the barrier
+    // below waits for everything before them only, and conv 1's MFMAs
+    // start as its fragments arrive
+    v4i w1[CT1][KM1];
+    const int8_t* wr[CT1];
+#pragma unroll
+    for (int i = 0; i < CT1; ++i)
+        wr[i] = a.wf1 + (int64_t)min(wave + NC_NW * i, T1 - 1) * ks1 * 1024 +
+                16 * lane;
+#pragma unroll
+    for (int s = 0; s < KM1; ++s) {  // in the order the MFMAs use them
+#pragma unroll
+        for (int i = 0; i < CT1; ++i)
+            w1[i][s] = *(const v4i*)(wr[i] + 1024 * s);
+        asm volatile("" ::: "memory");  // (kept in that order)
+    }
+    // conv 2's weights, fragment order, to LDS (needed after conv 1 only);
+    // slots past the last fragment load the last one again into its own
+    // place (the same bytes)
+#pragma unroll
+    for (int k = 0; k < NW2; ++k) {
+        const int i = min(wave + NC_NW * k, T2 * ks2 - 1);
         __builtin_amdgcn_global_load_lds(a.wf2 + 1024 * i + 16 * lane,
                                          s_w2 + 1024 * i, 16, 0, 0);
-    // conv 1's weight fragments of the wave's tiles (a tile past the last
-    // reads the last one and is not stored)
-    v4i w1[CT1][KM1];
-#pragma unroll
-    for (int i = 0; i < CT1; ++i) {
-        const int j = min(wave + NC_NW * i, T1 - 1);
-        const int8_t* wr = a.wf1 + (int64_t)j * ks1 * 1024 + 16 * lane;
-#pragma unroll
-        for (int s = 0; s < KM1; ++s)
-            w1[i][s] = *(const v4i*)(wr + 1024 * min(s, ks1 - 1));
     }
-    const int4 hdr1 = *(const int4*)a.plan1;
-    const int4 hdr2 = *(const int4*)a.plan2;
 
-    // every load done (the direct ones among them); tables, constants and
-    // the padding taps' pad value to LDS; one bare barrier
-    __builtin_amdgcn_s_waitcnt(0x0f70);
-    if (tid < 256)
-        s_tab1[tid] = tv;
-    else
-        s_tab2[tid - 256] = tv;
-    if (tid < 256) {
-        s_pc[0][tid] = pcv[0];
-        s_cr[0][tid] = crv[0];
-        s_pc[1][tid] = pcv[1];
-        s_cr[1][tid] = crv[1];
-    }
+    // the tables, constants and rows landed (loads complete in issue
+    // order: conv 1's weights and conv 2's follow them); the padding taps'
+    // pad value; one bare barrier
+    constexpr int NW = CT1 * KM1 + NW2;  // loads after the rows (<= 44)
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (NW & 15) | ((NW >> 4) << 14));
     if (CV1 && fix) {
         const int pv = (int)((uint32_t)(uint8_t)a.padv * 0x01010101u);
         const int n = RX * ks1 / 16;
@@ -164,33 +209,36 @@ __global__ __launch_bounds__(NC_NT) void k_narrow_chain(NcArgs a) {
                    const int* tab, int (&e)[4])
                    __attribute__((always_inline)) {
         const int* tabE = tab - hdr.x;
+        const bool corr = h ? a.corr2 != nullptr : a.corr1 != nullptr;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int4 pc = s_pc[h][c + r];
             const int64_t cc = plan_fold(
                 (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z),
-                s_cr[h][c + r], pc.x);
+                corr ? (uint32_t)s_cr[h][c + r] : 0u, pc.x);
             e[r] = tabE[med3_i32(plan_q0(acc[r], pc.x, cc, pc.y), hdr.x,
                                  hdr.y)];
         }
     };
     const int sw = 16 * (kg ^ ((col >> 2) & 3));
     // ---- conv 1: row tiles t, the wave's channel tiles; stored bytes to
-    // the LDS tile (rows of RSM bytes)
-    for (int t = 0; t < a.RTL; ++t) {
+    // the LDS tile (rows of RSM bytes). The first row tile is peeled off
+    // the loop, so that its MFMAs wait for each weight fragment in turn
+    // (a loop over them would wait for all of them first).
+    auto conv1_tile = [&](int t, auto first) __attribute__((always_inline)) {
+        constexpr bool FIRST = decltype(first)::value;
         const int8_t* fx0 = s_x + (16 * t + col) * 64 + sw;
         v4i acc[CT1];
 #pragma unroll
         for (int i = 0; i < CT1; ++i) acc[i] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < KM1; ++s) {
-            if (s < ks1) {
-                const v4i fx = *(const v4i*)(fx0 + s * RX * 64);
+            if (FIRST) wait_vm(NW - CT1 * (s + 1));
+            const v4i fx = *(const v4i*)(fx0 + s * RX * 64);
 #pragma unroll
-                for (int i = 0; i < CT1; ++i)
-                    acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        w1[i][s], fx, acc[i], 0, 0, 0);
-            }
+            for (int i = 0; i < CT1; ++i)
+                acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    w1[i][s], fx, acc[i], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < CT1; ++i) {
@@ -202,7 +250,11 @@ __global__ __launch_bounds__(NC_NT) void k_narrow_chain(NcArgs a) {
                     pack_entries(e, 0);
             }
         }
-    }
+    };
+    conv1_tile(0, std::true_type{});
+    for (int t = 1; t < a.RTL; ++t) conv1_tile(t, std::false_type{});
+    // conv 2's weights landed too; the tile written
+    __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
 
     // ---- conv 2 over the LDS tile: the wave's channel tiles j2, stored
@@ -245,18 +297,38 @@ __global__ __launch_bounds__(NC_NT) void k_narrow_chain(NcArgs a) {
 
 using NcKern = void (*)(NcArgs);
 
-template <bool CV1>
-NcKern nc_kernel(int km1, int ct1, int ct2) {
-    if (km1 == 9) {
-        if (ct1 == 1) return ct2 == 1 ? &k_narrow_chain<9, 1, 1, CV1>
-                                      : &k_narrow_chain<9, 1, 2, CV1>;
-        return ct2 == 1 ? &k_narrow_chain<9, 2, 1, CV1>
-                        : &k_narrow_chain<9, 2, 2, CV1>;
+template <int KM1, bool CV1>
+NcKern nc_kernel_ct(int ct1, int ct2, int nw2) {
+    if (nw2 <= 2) {
+        if (ct1 == 1)
+            return ct2 == 1 ? &k_narrow_chain<KM1, 1, 1, CV1, 2>
+                            : &k_narrow_chain<KM1, 1, 2, CV1, 2>;
+        return ct2 == 1 ? &k_narrow_chain<KM1, 2, 1, CV1, 2>
+                        : &k_narrow_chain<KM1, 2, 2, CV1, 2>;
     }
-    if (ct1 == 1) return ct2 == 1 ? &k_narrow_chain<20, 1, 1, CV1>
-                                  : &k_narrow_chain<20, 1, 2, CV1>;
-    return ct2 == 1 ? &k_narrow_chain<20, 2, 1, CV1>
-                    : &k_narrow_chain<20, 2, 2, CV1>;
+    if (ct1 == 1)
+        return ct2 == 1 ? &k_narrow_chain<KM1, 1, 1, CV1, 8>
+                        : &k_narrow_chain<KM1, 1, 2, CV1, 8>;
+    return ct2 == 1 ? &k_narrow_chain<KM1, 2, 1, CV1, 8>
+                    : &k_narrow_chain<KM1, 2, 2, CV1, 8>;
+}
+
+// The instantiated K-step counts of conv 1: 2 and 4 (1x1 over 128 or 256
+// channels), 9 (3x3 over 64, or 1x1 over 576), 18 (3x3 over 128).
+NcKern nc_kernel(bool cv, int ks1, int ct1, int ct2, int nw2) {
+    if (cv) {
+        switch (ks1) {
+            case 9: return nc_kernel_ct<9, true>(ct1, ct2, nw2);
+            case 18: return nc_kernel_ct<18, true>(ct1, ct2, nw2);
+            default: return nullptr;
+        }
+    }
+    switch (ks1) {
+        case 2: return nc_kernel_ct<2, false>(ct1, ct2, nw2);
+        case 4: return nc_kernel_ct<4, false>(ct1, ct2, nw2);
+        case 9: return nc_kernel_ct<9, false>(ct1, ct2, nw2);
+        default: return nullptr;
+    }
 }
 
 // conv 1 as rows of a GEMM (1x1, stride 1, no padding) or not
@@ -308,6 +380,8 @@ bool narrow_chain_applies(const ConvArgs& b1, const ConvArgs& b2) {
             ((uintptr_t)b2.y2 % 4 == 0 && b2.y2_pst % 4 == 0)) &&
            b1.M < ((int64_t)1 << 31) &&
            (int64_t)b1.H * b1.W * b1.x_sp < ((int64_t)1 << 31) &&
+           nc_kernel(!rows1, b1.KGp / 4, 1, 1, 1) != nullptr &&
+           (b2.Cout / 16) * (b2.KGp / 4) <= 8 * NC_NW &&
            nc_lds(b1, b2, 1, &om, &ow, &rs) > 0;
 }
 
@@ -325,10 +399,10 @@ bool launch_narrow_chain(const ConvArgs& b1, const ConvArgs& b2, int rtl,
     const int lds = nc_lds(b1, b2, rtl, &om, &ow, &rsm);
     const int T1 = b1.Cout / 16, T2 = b2.Cout / 16;
     const int ct1 = T1 > NC_NW ? 2 : 1, ct2 = T2 > NC_NW ? 2 : 1;
-    const int km1 = b1.KGp <= 36 ? 9 : 20;
     const bool cv = !nc_gemm_rows(b1);
-    const NcKern k = cv ? nc_kernel<true>(km1, ct1, ct2)
-                        : nc_kernel<false>(km1, ct1, ct2);
+    // conv 2's fragment loads a wave
+    const int nw2 = (int)ceil_div((int64_t)T2 * (b2.KGp / 4), NC_NW);
+    const NcKern k = nc_kernel(cv, b1.KGp / 4, ct1, ct2, nw2);
     NcArgs a;
     a.x = (const int8_t*)b1.x;
     a.xpst = (int64_t)b1.H * b1.W == 1 && !cv ? b1.x_sn : b1.x_sp;
