@@ -501,9 +501,18 @@ int qa_d_conv_pair_tail(const qa_conv_desc* d1, const qa_conv_desc* d2,
  * d2->y (and d2->y2); d1->y is not
  * written. Returns -1, launching nothing, for any other pair; the
  * reference runs the two convolutions one after the other
- * (quant_layers.py:320-335 twice). qa_conv_chain_supported checks a pair
- * without launching (1 or 0). d2->tile: 0, or 0x10000 | R for bands of R
- * output rows a work-group (ignored where they do not fit). */
+ * (quant_layers.py:320-335 twice). A second form takes wider pairs when
+ * both descriptors carry fragment-order weights (w_frag): d1 a 1x1 or
+ * k x k convolution of a multiple of 64 input channels (K up to 1280
+ * bytes, one group) and 16..256 output channels (a multiple of 16, no
+ * rescaled copy), d2 a 1x1 convolution of 16..256 output channels reading
+ * all of them; d1's stored bytes then pass through LDS only (the
+ * late-stage C2f inputs of a classifier: Conv_126+Conv_134,
+ * Conv_192+Conv_200 of YOLOv8n-cls). qa_conv_chain_supported checks a
+ * pair without launching (1 or 0). d2->tile: 0, 0x10000 | R for bands of
+ * R output rows a work-group (ignored where they do not fit), or
+ * 0x12000 | (T - 1) << 4 for the second form with T row tiles of 16 a
+ * work-group (T 1..4, fewer where LDS runs out). */
 int qa_conv_chain_supported(const qa_conv_desc* d1, const qa_conv_desc* d2);
 int qa_d_conv_chain(const qa_conv_desc* d1, const qa_conv_desc* d2,
                     void* stream);
