@@ -5,6 +5,11 @@ already resident in HBM: input quantization, 26 fused conv kernels (int8
 MFMA, bias + requantize + SiLU table + residual Add in the epilogue), C2f
 concatenations, GlobalAveragePool, the 1280->1000 Gemm, the Softmax float
 fallback and output dequantization, replayed as one captured HIP graph.
+By default two batches are in flight (``--in-flight``): two executors, each
+with its own input, buffers and full pass, captured as two parallel branches
+of one graph, so one replay runs two steps and the GPU overlaps one batch's
+launches with the other's launch gaps and idle CUs; K steps are K / 2 such
+replays. ``single_batch`` in the line is the same K steps one pass a replay.
 Weights are random from a seed (2.72 M parameters); the model is calibrated
 on 32 seeded N(0,1) images; inputs are seeded N(0,1) images (synthetic data).
 
@@ -84,6 +89,10 @@ def parse():
                         "standalone GEMM / conv / requantize / table "
                         "kernels) and print its records, e.g. under a "
                         "profiler")
+    p.add_argument("--in-flight", type=int, default=2, metavar="N",
+                   help="batches in flight: N executors (own inputs and "
+                        "buffers) as parallel branches of one HIP graph; "
+                        "1: one pass a replay")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="finish with one device copy of MIB MiB (a plain "
                         "copy kernel that calibrates byte counters)")
@@ -423,20 +432,73 @@ def main():
             cpu_rows += cpu_baseline.conv_rows(synth.conv_workload(),
                                                [cores, 1])
 
+    # ---- further batches in flight: their own executors, inputs and
+    # buffers; each must give the first one's outputs for the same images
+    nf = 1 if args.eager else max(1, args.in_flight)
+    flight = None
+    if nf > 1:
+        from quantanything_amd.executor import DeviceExecutor, InFlight
+
+        exs = [ex]
+        first = ex.tensors[g.outputs[0]].to_host()
+        same = True
+        for k in range(1, nf):
+            shift = k * B // nf
+            e = DeviceExecutor(c, {"images": x.shape})
+            e.inputs_f32["images"].copy_(
+                torch.from_numpy(np.ascontiguousarray(np.roll(x, shift, 0))))
+            for (n0, d0, _, _), (n1, d1, _, _) in zip(ex.tunables,
+                                                      e.tunables):
+                if n0 != n1:
+                    raise RuntimeError("executors planned differently")
+                d1.tile = d0.tile
+            e.launch()
+            torch.cuda.synchronize()
+            same &= bool(np.array_equal(e.tensors[g.outputs[0]].to_host(),
+                                        np.roll(first, shift, 0)))
+            exs.append(e)
+        if gate is not None:
+            gate["in_flight_batches_equal"] = same
+        if not same:
+            print(json.dumps({"error": "a batch in flight differs from the "
+                                       "first executor's pass"}))
+            return 1
+        flight = InFlight(exs)
+
     # ---- timed region: captured graph replays ----------------------------
     step = ex.launch if args.eager else ex.replay
     if not args.eager:
         ex.capture()
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
+
+    def timed(inflight):
+        if inflight is None:
+            for _ in range(args.warmup):
+                step()
+        else:
+            for _ in range(max(1, args.warmup // nf)):
+                inflight.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        if inflight is None:
+            for _ in range(args.steps):
+                step()
+        else:  # K steps: K // N replays of N batches, the rest one by one
+            reps, rest = divmod(args.steps, nf)
+            for _ in range(reps):
+                inflight.replay()
+            for _ in range(rest):
+                step()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    dt = timed(flight)
     ms = dt * 1e3 / args.steps
     value = B * args.steps / dt
+    single = None
+    if flight is not None:
+        dt1 = timed(None)
+        single = {"images_per_s": round(B * args.steps / dt1, 1),
+                  "ms_per_step": round(dt1 * 1e3 / args.steps, 4)}
     # the same pass with its float input and output crossing PCIe
     pcie = None if args.eager else pcie_inclusive(
         ex, x, max(5, min(args.steps, 50)), torch)
@@ -592,7 +654,8 @@ def main():
         "config": {"workload": "YOLOv8n-cls int8 integer-only inference",
                    "global_batch": B, "image": 224, "quant_type": "int8",
                    "per_channel": True, "params": g.num_params(),
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU", "batches_in_flight": nf},
+        "single_batch": single,
         "roofline": roof,
         "cpu_baseline": cpu,
         "cpu_baselines": cpu_rows,

@@ -2300,3 +2300,42 @@ class DeviceExecutor:
 
     def integer_outputs(self):
         return {k: self.tensors[k].to_host() for k in self.graph.outputs}
+
+
+class InFlight:
+    """Several batches in flight: the passes of ``executors`` (one per
+    batch, each with its own buffers, e.g. consecutive batches of a stream
+    of requests) captured as parallel branches of ONE HIP graph, forked from
+    and joined to the replaying stream. The GPU then runs one batch's
+    launches while another's wait on a launch gap or leave CUs idle: a
+    late-stage launch of a classifier covers a few hundred work-groups and
+    runs for a few microseconds, so a single pass leaves most of the chip
+    idle most of the time. Graphs replayed from two streams did not overlap
+    here; branches of one graph do. Each executor's results are those of
+    its own pass (``DeviceExecutor.replay``): the branches share no memory.
+    ``replay()`` runs every batch once."""
+
+    def __init__(self, executors):
+        if not executors:
+            raise ValueError("InFlight needs at least one executor")
+        self.executors = list(executors)
+        for ex in self.executors:  # warm-up outside capture
+            ex.launch()
+        torch.cuda.synchronize()
+        # one side stream a branch past the first, default priority
+        self.streams = [torch.cuda.Stream() for _ in self.executors[1:]]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cur = torch.cuda.current_stream()
+            for s in self.streams:
+                s.wait_stream(cur)
+            self.executors[0].launch(cur.cuda_stream)
+            for ex, s in zip(self.executors[1:], self.streams):
+                with torch.cuda.stream(s):
+                    ex.launch(s.cuda_stream)
+            for s in self.streams:
+                cur.wait_stream(s)
+        self.cuda_graph = g
+
+    def replay(self):
+        self.cuda_graph.replay()

@@ -373,6 +373,35 @@ def test_batch_size_can_change_after_calibration(hip):
     np.testing.assert_array_equal(one, many[:1])
 
 
+def test_batches_in_flight_match_their_own_passes(hip):
+    """Two executors (own inputs and buffers) as parallel branches of one
+    graph: every replay gives each executor its own eager result, with eager
+    work and synchronisation between the replays, and the second batch
+    (the first one's images rolled) the first one's outputs rolled."""
+    import torch
+
+    from quantanything_amd.executor import DeviceExecutor, InFlight
+
+    g = G.yolov8n_cls(seed=3)
+    calib = [Stream(40 + i).normal((2, 3, 224, 224)).astype(np.float32)
+             for i in range(2)]
+    c = _calibrated(g, "int8", True, calib)
+    x = Stream(51).normal((2, 3, 224, 224)).astype(np.float32)
+    exs = [DeviceExecutor(c, {"images": x.shape}) for _ in range(2)]
+    eager = [exs[0].run({"images": x}),
+             exs[1].run({"images": np.roll(x, 1, 0)})]
+    for k in eager[0]:
+        np.testing.assert_array_equal(eager[1][k], np.roll(eager[0][k], 1, 0))
+    fl = InFlight(exs)
+    for _ in range(3):
+        fl.replay()
+        torch.cuda.synchronize()
+        for ex, want in zip(exs, eager):
+            for k, v in ex.outputs_f32.items():
+                np.testing.assert_array_equal(v.cpu().numpy(), want[k])
+        torch.zeros(1024, device="cuda").sum().item()
+
+
 def test_graph_replay_matches_eager(hip):
     """A captured HIP graph replayed several times (with eager work and
     synchronisation in between) gives the eager result every time."""
