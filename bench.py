@@ -222,7 +222,37 @@ def pcie_inclusive(ex, x, steps, torch):
     return rec
 
 
-def measure_pass(name, g, quant_type, batch, steps, tune, torch):
+def in_flight(c, ex, x, out_name, nf, torch):
+    """``nf`` batches in flight: ``ex`` and nf - 1 more executors of
+    container ``c`` (own buffers, ``ex``'s tiles), batch k holding ``x``
+    rolled by k B / nf images, as one graph of parallel branches
+    (``executor.InFlight``). Returns it and whether every extra batch's
+    output ``out_name`` equals ``ex``'s (which holds its pass over ``x``),
+    rolled the same way, bit for bit."""
+    from quantanything_amd.executor import DeviceExecutor, InFlight
+
+    B = x.shape[0]
+    exs = [ex]
+    first = ex.tensors[out_name].to_host()
+    same = True
+    for k in range(1, nf):
+        shift = k * B // nf
+        e = DeviceExecutor(c, {"images": x.shape})
+        e.inputs_f32["images"].copy_(
+            torch.from_numpy(np.ascontiguousarray(np.roll(x, shift, 0))))
+        for (n0, d0, _, _), (n1, d1, _, _) in zip(ex.tunables, e.tunables):
+            if n0 != n1:
+                raise RuntimeError("executors planned differently")
+            d1.tile = d0.tile
+        e.launch()
+        torch.cuda.synchronize()
+        same &= bool(np.array_equal(e.tensors[out_name].to_host(),
+                                    np.roll(first, shift, 0)))
+        exs.append(e)
+    return InFlight(exs), same
+
+
+def measure_pass(name, g, quant_type, batch, steps, tune, torch, nf=1):
     """Images/s of one captured integer pass of graph ``g`` (calibrated on
     32 seeded N(0, 1) images, tiles tuned as for the headline pass)."""
     from quantanything_amd.container import QuantContainer
@@ -238,20 +268,34 @@ def measure_pass(name, g, quant_type, batch, steps, tune, torch):
     torch.cuda.synchronize()
     if tune:
         ex.tune()
+    ex.launch()
+    torch.cuda.synchronize()
     ex.capture()
-    for _ in range(3):
-        ex.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        ex.replay()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
-    return {"workload": name, "quant_type": quant_type, "global_batch": batch,
-            "images_per_s": round(batch / dt, 1),
-            "ms_per_step": round(dt * 1e3, 4), "steps": steps,
-            "launches_per_step": len(ex.launches),
-            "params": g.num_params()}, c
+
+    def timed(step, k):
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(k):
+            step()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    dt = timed(ex.replay, steps) / steps
+    rec = {"workload": name, "quant_type": quant_type, "global_batch": batch,
+           "images_per_s": round(batch / dt, 1),
+           "ms_per_step": round(dt * 1e3, 4), "steps": steps,
+           "launches_per_step": len(ex.launches),
+           "params": g.num_params()}
+    if nf > 1:  # the same steps with nf batches in flight
+        fl, same = in_flight(c, ex, x, g.outputs[0], nf, torch)
+        reps = max(1, steps // nf)
+        dtf = timed(fl.replay, reps) / (reps * nf)
+        rec["in_flight"] = {"batches": nf, "outputs_equal": same,
+                            "images_per_s": round(batch / dtf, 1),
+                            "ms_per_step": round(dtf * 1e3, 4)}
+    return rec, c
 
 
 def kernel_rows(tune, torch, steps=50):
@@ -345,7 +389,8 @@ def main():
         if args.only == "vit":
             rec, _ = measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",
                                   G.vit(seed=5, batch=32), "int8", 32,
-                                  args.steps, not args.no_tune, torch)
+                                  args.steps, not args.no_tune, torch,
+                                  max(1, args.in_flight))
         else:
             rec, _ = measure_pass("YOLOv8n-cls int16 (wide accumulation)",
                                   G.yolov8n_cls(seed=3), "int16", B,
@@ -437,33 +482,13 @@ def main():
     nf = 1 if args.eager else max(1, args.in_flight)
     flight = None
     if nf > 1:
-        from quantanything_amd.executor import DeviceExecutor, InFlight
-
-        exs = [ex]
-        first = ex.tensors[g.outputs[0]].to_host()
-        same = True
-        for k in range(1, nf):
-            shift = k * B // nf
-            e = DeviceExecutor(c, {"images": x.shape})
-            e.inputs_f32["images"].copy_(
-                torch.from_numpy(np.ascontiguousarray(np.roll(x, shift, 0))))
-            for (n0, d0, _, _), (n1, d1, _, _) in zip(ex.tunables,
-                                                      e.tunables):
-                if n0 != n1:
-                    raise RuntimeError("executors planned differently")
-                d1.tile = d0.tile
-            e.launch()
-            torch.cuda.synchronize()
-            same &= bool(np.array_equal(e.tensors[g.outputs[0]].to_host(),
-                                        np.roll(first, shift, 0)))
-            exs.append(e)
+        flight, same = in_flight(c, ex, x, g.outputs[0], nf, torch)
         if gate is not None:
             gate["in_flight_batches_equal"] = same
         if not same:
             print(json.dumps({"error": "a batch in flight differs from the "
                                        "first executor's pass"}))
             return 1
-        flight = InFlight(exs)
 
     # ---- timed region: captured graph replays ----------------------------
     step = ex.launch if args.eager else ex.replay
@@ -615,7 +640,7 @@ def main():
         steps = max(5, min(args.steps, 50))
         rec, cv = measure_pass("ViT-S/16 (12 blocks, 197 tokens) int8",
                                G.vit(seed=5, batch=32), "int8", 32, steps,
-                               not args.no_tune, torch)
+                               not args.no_tune, torch, nf)
         extra.append(rec)
         rec, c16 = measure_pass("YOLOv8n-cls int16 (wide accumulation)",
                                 G.yolov8n_cls(seed=3), "int16", B, steps,
