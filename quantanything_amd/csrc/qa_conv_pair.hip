@@ -62,9 +62,11 @@ __device__ __forceinline__ int cp_div(int n, uint32_t m) {
     return (int)__umulhi((uint32_t)n, m);
 }
 
+// WM <= 2: at most 128 VGPRs, so that two work-groups share a CU
 template <int WM, bool RES, bool TAIL>
-__global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
-                                                     PairGeom g, ConvArgs a3) {
+__global__ __launch_bounds__(CP_NT)
+__attribute__((amdgpu_waves_per_eu(WM <= 2 ? 4 : 1))) void k_conv_pair(
+    ConvArgs a1, ConvArgs a2, PairGeom g, ConvArgs a3) {
     constexpr int C = 16 * WM;          // channels of every tensor
     constexpr int KS = (9 * WM + 3) / 4;  // K-steps: KGp = round_up(9 WM, 4)
     constexpr int LCPP = WM == 1 ? 0 : WM == 2 ? 1 : 2;  // log2 chunks/pixel
@@ -80,7 +82,6 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
     __shared__ uint32_t s_corr[2][C];
     __shared__ int s_tab3[TAIL ? 256 : 1];
     __shared__ int4 s_pc3[TAIL ? 128 : 1];
-    __shared__ uint32_t s_corr3[TAIL ? 128 : 1];
     int8_t* s_w3 = (int8_t*)lds4 + g.t_w3;    // TAIL: cv2's weights
     int8_t* s_t = (int8_t*)lds4 + g.t_tile;   // TAIL: per-wave tiles
     int8_t* s_pre = (int8_t*)lds4 + g.t_pre;  // TAIL: the band's prefix
@@ -251,9 +252,13 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
                 corr3v = a3.corr ? (uint32_t)a3.corr[cl] : 0u;
             }
             if (tid < 256) s_tab3[tid] = tv3;
-            if (tid < 16 * g.T3) {
-                s_pc3[tid] = pc3v;
-                s_corr3[tid] = corr3v;
+            if (tid < 16 * g.T3) {  // the correction folded in (plan_q0)
+                const uint64_t cf = (uint64_t)plan_fold(
+                    (int64_t)(((uint64_t)(uint32_t)pc3v.w << 32) |
+                              (uint32_t)pc3v.z),
+                    corr3v, pc3v.x);
+                s_pc3[tid] = int4{pc3v.x, pc3v.y, (int)(uint32_t)cf,
+                                  (int)(uint32_t)(cf >> 32)};
             }
         }
     }
@@ -268,8 +273,7 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
     for (int s = 0; s < KS; ++s) kt[s] = s_kt[4 * s + kgl];
     v4i wb[KS][WM];
     int cm[WM], ct[WM];
-    int64_t cc[WM];
-    uint32_t ccorr[WM];
+    int64_t cc[WM];  // the plan constant with the correction folded in
     auto load_conv = [&](const int8_t* s_w, int which) {
 #pragma unroll
         for (int s = 0; s < KS; ++s)
@@ -282,9 +286,12 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
             const int4 pc = s_pc[which][16 * i + col];
             cm[i] = pc.x;
             ct[i] = pc.y;
-            cc[i] = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
-                              (uint32_t)pc.z);
-            ccorr[i] = s_corr[which][16 * i + col];
+            cc[i] = plan_fold((int64_t)(((uint64_t)(uint32_t)pc.w << 32) |
+                                        (uint32_t)pc.z),
+                              s_corr[which][16 * i + col], pc.x);
+            // opaque, so that each value is one 32x32 -> 64 multiply-add
+            // instead of a re-associated 64-bit product
+            asm volatile("" : "+v"(cc[i]));
         }
     };
     // accumulators of the 16 pixels whose band base offsets are xb
@@ -324,12 +331,11 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
             for (int i = 0; i < WM; ++i) {
                 int e[4];
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const uint32_t wu = (uint32_t)acc[i][rr] + ccorr[i];
-                    const int q0 =
-                        (int)(((int64_t)(int)wu * cm[i] + cc[i]) >> ct[i]);
-                    e[rr] = s_tab1[min(max(q0, h1.x), h1.y) - h1.x];
-                }
+                for (int rr = 0; rr < 4; ++rr)
+                    e[rr] = s_tab1[med3_i32(plan_q0(acc[i][rr], cm[i], cc[i],
+                                                    ct[i]),
+                                            h1.x, h1.y) -
+                                   h1.x];
                 const uint32_t wy =
                     quad_transpose(pack_entries(e, 0), sel1, sel2);
                 if (pok) *(uint32_t*)(dst + 16 * i) = wy;
@@ -366,19 +372,17 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
             for (int i = 0; i < WM; ++i) {
                 int e[4];
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const uint32_t wu = (uint32_t)acc[i][rr] + ccorr[i];
-                    const int q0 =
-                        (int)(((int64_t)(int)wu * cm[i] + cc[i]) >> ct[i]);
-                    e[rr] = min(max(q0, pA), pB) - pA;
-                }
+                for (int rr = 0; rr < 4; ++rr)
+                    e[rr] = med3_i32(plan_q0(acc[i][rr], cm[i], cc[i], ct[i]),
+                                     pA, pB) -
+                            pA;
                 if (RES) {
                     const uint32_t rv = quad_transpose(rw[i], sel1, sel2);
 #pragma unroll
                     for (int rr = 0; rr < 4; ++rr) {
                         const int v = s_tab2[256 + e[rr]] +
                                       s_tab2[512 + ((rv >> (8 * rr)) & 255)];
-                        e[rr] = min(max(v, 0), pSH);
+                        e[rr] = med3_i32(v, 0, pSH);
                     }
                 }
 #pragma unroll
@@ -409,15 +413,16 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
 #pragma unroll
                     for (int s3 = 0; s3 < 4; ++s3) {
                         if (s3 >= g.KS3) continue;
-                        // row col of the tile: pixel qp of the band
+                        // row col of the tile: pixel qp of the band; past
+                        // the Concat's channels the weights are zero and
+                        // any bytes do (the tile's last chunk is read)
                         const int c16 = (4 * s3 + kgl) * 16;
-                        const v4i fa3 =
+                        const int8_t* src3 =
                             c16 < g.off_d
-                                ? *(const v4i*)(s_pre + qp * g.RP + c16)
-                                : c16 < g.Ctot
-                                      ? *(const v4i*)(tw + col * g.RT + c16 -
-                                                      g.off_d)
-                                      : v4i{0, 0, 0, 0};
+                                ? s_pre + qp * g.RP + c16
+                                : tw + col * g.RT +
+                                      min(c16, g.Ctot - 16) - g.off_d;
+                        const v4i fa3 = *(const v4i*)src3;
 #pragma unroll
                         for (int j = 0; j < TJ; ++j)
                             if (j0 + j < g.T3)
@@ -434,10 +439,9 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair(ConvArgs a1, ConvArgs a2,
                         const int c3 = 16 * (j0 + j) + cq;
                         if (j0 + j >= g.T3) continue;
                         const int4 pc3 = s_pc3[16 * (j0 + j) + col];
-                        const int64_t cc3 = plan_fold(
+                        const int64_t cc3 =
                             (int64_t)(((uint64_t)(uint32_t)pc3.w << 32) |
-                                      (uint32_t)pc3.z),
-                            s_corr3[16 * (j0 + j) + col], pc3.x);
+                                      (uint32_t)pc3.z);
                         int e3[4];
 #pragma unroll
                         for (int rr = 0; rr < 4; ++rr)
@@ -567,8 +571,12 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair_cs(ConvArgs a1,
         const int4 pc = s_pc[which][co];
         cm = pc.x;
         ct = pc.y;
-        cc = (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
         cr = s_corr[which][co];
+        // the correction folded into the constant (plan_q0)
+        cc = plan_fold(
+            (int64_t)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z), cr,
+            pc.x);
+        asm volatile("" : "+v"(cc));  // one multiply-add a value (above)
     };
     auto tile_acc = [&](const int8_t* xb, const v4i (&w)[KS]) {
         v4i fa[KS];
@@ -606,11 +614,10 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair_cs(ConvArgs a1,
             const int sr = cp_div(sq, g.m_w), sc = sq - sr * OW;
             int e[4];
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const uint32_t wu = (uint32_t)acc[rr] + cr;
-                const int q0 = (int)(((int64_t)(int)wu * cm + cc) >> ct);
-                e[rr] = s_tab1[min(max(q0, h1.x), h1.y) - h1.x];
-            }
+            for (int rr = 0; rr < 4; ++rr)
+                e[rr] = s_tab1[med3_i32(plan_q0(acc[rr], cm, cc, ct), h1.x,
+                                        h1.y) -
+                               h1.x];
             const uint32_t wy = quad_transpose(pack_entries(e, 0), sel1, sel2);
             if (pq < npix)
                 *(uint32_t*)(s_m + (sr * g.BW + sc + 1) * g.PS + 16 * wave +
@@ -644,18 +651,15 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair_cs(ConvArgs a1,
             const v4i acc = tile_acc(s_m + (r * g.BW + ox) * g.PS, wb2);
             int e[4];
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const uint32_t wu = (uint32_t)acc[rr] + cr;
-                const int q0 = (int)(((int64_t)(int)wu * cm + cc) >> ct);
-                e[rr] = min(max(q0, pA), pB) - pA;
-            }
+            for (int rr = 0; rr < 4; ++rr)
+                e[rr] = med3_i32(plan_q0(acc[rr], cm, cc, ct), pA, pB) - pA;
             if (RES) {
                 const uint32_t rv = quad_transpose(rw, sel1, sel2);
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int v = s_tab2[256 + e[rr]] +
                                   s_tab2[512 + ((rv >> (8 * rr)) & 255)];
-                    e[rr] = min(max(v, 0), pSH);
+                    e[rr] = med3_i32(v, 0, pSH);
                 }
             }
 #pragma unroll
