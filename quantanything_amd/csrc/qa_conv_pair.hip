@@ -500,11 +500,20 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair_cs(ConvArgs a1,
     const v4i pad1 = {pv1, pv1, pv1, pv1}, pad2 = {pv2, pv2, pv2, pv2};
     const int co = 16 * wave + col;  // this lane's weight row (both convs)
     // conv 1's weight fragments, in flight with the band's loads
+    // a weight fragment: one contiguous KB a wave load from the
+    // fragment-order copy (ConvArgs.wfrag; the wave's tile, K-step s at
+    // 1 KB s), else 16 rows x 64 bytes of the packed rows (half lines:
+    // their loads arrive about 2.5x slower)
+    auto wfrag = [&](const ConvArgs& a, int& st) {
+        st = a.wfrag ? 1024 : 64;
+        return a.wfrag ? a.wfrag + (int64_t)wave * KS * 1024 + 16 * lane
+                       : a.wp + (int64_t)co * a.wp_rstride + 16 * kgl;
+    };
+    int wst1;
+    const int8_t* wp1 = wfrag(a1, wst1);
     v4i wb[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-        wb[s] = *(const v4i*)(a1.wp + (int64_t)co * a1.wp_rstride + 64 * s +
-                              16 * kgl);
+    for (int s = 0; s < KS; ++s) wb[s] = *(const v4i*)(wp1 + wst1 * s);
     const int r_lo = max(0, -iy0), r_hi = min(BR, a1.H - iy0);
     const int nreal = max(r_hi - r_lo, 0) * W * WM;
     {
@@ -591,11 +600,11 @@ __global__ __launch_bounds__(CP_NT) void k_conv_pair_cs(ConvArgs a1,
     };
 
     // ---- phase 1 (conv 2's weights in flight) ----
+    int wst2;
+    const int8_t* wp2 = wfrag(a2, wst2);
     v4i wb2[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-        wb2[s] = *(const v4i*)(a2.wp + (int64_t)co * a2.wp_rstride + 64 * s +
-                               16 * kgl);
+    for (int s = 0; s < KS; ++s) wb2[s] = *(const v4i*)(wp2 + wst2 * s);
     {
         int cm, ct;
         int64_t cc;

@@ -1200,6 +1200,9 @@ class DeviceExecutor:
                                             ctypes.byref(d2), s),
                     "qa_d_conv_pair")
 
+            if d2.Cout == 128:  # the channel-split form loads fragments
+                self._frag_weights(d1)
+                self._frag_weights(d2)
             self.launches = [(fused, fn) if n == ln2 else (n, f)
                              for n, f in self.launches if n != ln1]
             # band heights to time (0: the library's cost model)
