@@ -189,16 +189,21 @@ def test_stem_quantization_edge_values(hip, tmp_path, quant_type):
     oracle = OraclePipeline(g, _qjson(c, tmp_path))
     oracle.run(x, keep=True)
     ex = c.executor({"images": x.shape})
-    assert any(t[0].startswith("qconv:") for t in ex.tunables)
-    ex.run({"images": x})
-    checked = 0
-    for name, t in ex.tensors.items():
-        if name in oracle.env:
-            got = t.to_host()
-            np.testing.assert_array_equal(
-                got, oracle.env[name].reshape(got.shape), err_msg=name)
-            checked += 1
-    assert checked >= 2
+    fused = [t for t in ex.tunables if t[0].startswith("qconv:")]
+    assert len(fused) == 1
+    _, d, codes, _ = fused[0]
+    for code in codes:  # every band height and bands-a-work-group form
+        d.tile = code
+        ex.run({"images": x})
+        checked = 0
+        for name, t in ex.tensors.items():
+            if name in oracle.env:
+                got = t.to_host()
+                np.testing.assert_array_equal(
+                    got, oracle.env[name].reshape(got.shape),
+                    err_msg=f"{name}, band code {code:#x}")
+                checked += 1
+        assert checked >= 2
 
 
 def _conv_graph(cin, cout, k, stride, pad, dil, groups, size):
