@@ -22,7 +22,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 # Packed FP32 VALU instructions are disabled for every HIP source.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Leading scalar kernel arguments (up to 16 dwords) arrive preloaded in
+# SGPRs: a kernel can issue its first loads without a scalar load round
+# trip of its arguments.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                "-mllvm", "-amdgpu-kernarg-preload-count=16"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
           f"--offload-arch={ARCH}", "-Wno-unused-command-line-argument"]
 

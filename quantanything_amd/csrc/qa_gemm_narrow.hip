@@ -41,7 +41,9 @@ namespace {
 
 constexpr int GN_KMAX = 20;  // K-steps of 64 bytes (K up to 1280)
 
-// The kernel's arguments, read in one scalar round.
+// The kernel's arguments, read in one scalar round; the ones its first
+// loads need also go as leading scalar arguments, which the dispatch
+// preloads into SGPRs (no scalar load before the first vector load).
 struct GnArgs {
     const int8_t* x;       // activation rows, xpst bytes apart
     const int8_t* wp;      // packed weight rows, 16 * KGp bytes apart
@@ -74,8 +76,12 @@ struct GnArgs {
 // 64-byte K-step one tap's 64 channels of one input pixel, loaded like a
 // GEMM row's); a tap outside the image loads pixel (0, 0) and then has
 // its LDS bytes overwritten with the pad value.
+#define GN_ARGS(g) \
+    (g).x, (g).wf, (g).plan, (g).xpst, (g).M, (g).KGp, (g).RTL, (g)
 template <int NB, bool RS, bool WF, int KM, bool CV = false>
-__global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
+__global__ __launch_bounds__(256) void k_gemm_narrow(
+    const int8_t* x, const int8_t* wf, const char* plan, int64_t xpst,
+    int64_t M, int32_t KGp, int32_t RTL, GnArgs a) {
     constexpr int RT = 4 / NB;
     constexpr int RW = 16 * NB;  // weight rows
     extern __shared__ int4 gn_dyn[];
@@ -83,8 +89,8 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kg = lane >> 4;
-    const int nks = a.KGp >> 2;  // 64-byte K-steps, 1..KM
-    const int RX = 16 * RT * a.RTL;               // the work-group's rows
+    const int nks = KGp >> 2;  // 64-byte K-steps, 1..KM
+    const int RX = 16 * RT * RTL;               // the work-group's rows
     int8_t* const s_x = (int8_t*)gn_dyn;
     int8_t* const s_w = s_x + RX * nks * 64;
     const int cw = (int)blockIdx.y * RW;          // the work-group's channels
@@ -95,7 +101,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     // operands (instruction i of an operand: segments 16 i .. 16 i + 15 in
     // (K-step, row) order, row fastest; lane l: segment 16 i + l / 4,
     // position l % 4), then the constants
-    const int tv = ((const int*)(a.plan + PLAN_E))[tid];
+    const int tv = ((const int*)(plan + PLAN_E))[tid];
     const int g = lane >> 2, q = lane & 3;
     auto dloads = [&](const int8_t* base, int64_t rs, int R, int64_t rmax,
                       int8_t* dst) __attribute__((always_inline)) {
@@ -110,7 +116,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     };
     v4i fwr[KM];
     if (WF) {  // fragment (tile c0 / 16, K-step s) at 1024 (tile nks + s)
-        const int8_t* wr = a.wf + (int64_t)(c0 >> 4) * nks * 1024 + 16 * lane;
+        const int8_t* wr = wf + (int64_t)(c0 >> 4) * nks * 1024 + 16 * lane;
 #pragma unroll
         for (int s = 0; s < KM; ++s)
             fwr[s] = *(const v4i*)(wr + 1024 * min(s, nks - 1));
@@ -122,7 +128,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
         int k = 0;
         for (int i = wave; i < n; i += 4, ++k) {
             const int sg = 16 * i + g, st = sg / RX, r = sg - st * RX;
-            const int64_t p = min(px + r, a.M - 1);
+            const int64_t p = min(px + r, M - 1);
             const int nimg = (int)(p / ohw);
             const int rem = (int)(p - (int64_t)nimg * ohw);
             const int oy = rem / a.OW, ox = rem - oy * a.OW;
@@ -133,24 +139,24 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
             const bool in = iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
             fix |= (in ? 0u : 1u) << k;
             __builtin_amdgcn_global_load_lds(
-                a.x + (int64_t)nimg * a.x_sn +
-                    ((int64_t)(in ? iy : 0) * a.W + (in ? ix : 0)) * a.xpst +
+                x + (int64_t)nimg * a.x_sn +
+                    ((int64_t)(in ? iy : 0) * a.W + (in ? ix : 0)) * xpst +
                     64 * cpart + 16 * (q ^ ((r >> 2) & 3)),
                 s_x + 1024 * i, 16, 0, 0);
         }
     } else {
-        dloads(a.x + px * a.xpst, a.xpst, RX, a.M - 1 - px, s_x);
+        dloads(x + px * xpst, xpst, RX, M - 1 - px, s_x);
     }
     if (!WF)  // weight rows cw .. cw + RW - 1 (packed rows padded to 128)
-        dloads(a.wp + (int64_t)cw * 16 * a.KGp, 16 * a.KGp, RW, RW - 1, s_w);
-    const int4 hdr = *(const int4*)a.plan;
-    const int pD = ((const int*)a.plan)[4];
+        dloads(a.wp + (int64_t)cw * 16 * KGp, 16 * KGp, RW, RW - 1, s_w);
+    const int4 hdr = *(const int4*)plan;
+    const int pD = ((const int*)plan)[4];
     int4 pc[4];
     uint32_t crr[4], cbo[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int c = min(c0 + 4 * kg + r, a.Cout - 1);
-        pc[r] = ((const int4*)(a.plan + PLAN_CH))[c];
+        pc[r] = ((const int4*)(plan + PLAN_CH))[c];
         crr[r] = a.corr ? (uint32_t)a.corr[c] : 0u;
         cbo[r] = RS ? (uint32_t)a.boff[c] : 0u;
     }
@@ -187,7 +193,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
     const int cs = c0 + 4 * kg;  // the lane's 4 channels (Cout % 4 == 0)
     // row tile j = wave / NB + RT t of the work-group: rows 16 j + col,
     // chunk kg of K-step s
-    for (int t = 0; t < a.RTL; ++t) {
+    for (int t = 0; t < RTL; ++t) {
         const int j = wave / NB + RT * t;
         const int8_t* fx0 =
             s_x + (16 * j + col) * 64 + 16 * (kg ^ ((col >> 2) & 3));
@@ -216,7 +222,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(GnArgs a) {
             e[r] = idt ? v + pD : s_tab[v - pA];
         }
         const int64_t p = px + 16 * j + col;
-        if (p < a.M && cs < a.Cout) {
+        if (p < M && cs < a.Cout) {
             *(uint32_t*)(a.y + p * a.ypst + cs) = pack_entries(e, 0);
             if (a.y2)
                 *(uint32_t*)(a.y2 + p * a.y2pst + cs) = pack_entries(e, 1);
@@ -331,7 +337,7 @@ bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, int rtl) {
         switch (kcase) {
 #define QA_GN_CV(NB, RS, KM)                                                  \
     case (KM == 9 ? NB : 0) * 2 + RS:                                        \
-        k_gemm_narrow<NB, RS != 0, true, KM, true><<<grid, 256, lds, st>>>(g); \
+        k_gemm_narrow<NB, RS != 0, true, KM, true><<<grid, 256, lds, st>>>(GN_ARGS(g)); \
         break;
             QA_GN_CV(1, 0, 9) QA_GN_CV(1, 1, 9) QA_GN_CV(2, 0, 9)
             QA_GN_CV(2, 1, 9) QA_GN_CV(4, 0, 9) QA_GN_CV(4, 1, 9)
@@ -346,14 +352,14 @@ bool launch_gemm_narrow(const ConvArgs& b, hipStream_t st, int rtl) {
             return false;
         }
         if (b.rowsum)
-            k_gemm_narrow<4, true, true, GN_KMAX><<<grid, 256, lds, st>>>(g);
+            k_gemm_narrow<4, true, true, GN_KMAX><<<grid, 256, lds, st>>>(GN_ARGS(g));
         else
-            k_gemm_narrow<4, false, true, GN_KMAX><<<grid, 256, lds, st>>>(g);
+            k_gemm_narrow<4, false, true, GN_KMAX><<<grid, 256, lds, st>>>(GN_ARGS(g));
     } else {
         switch (nb * 4 + (b.rowsum ? 2 : 0) + (b.wfrag ? 1 : 0)) {
 #define QA_GN_CASE(NB, RS, WF)                                            \
     case NB * 4 + RS * 2 + WF:                                            \
-        k_gemm_narrow<NB, RS != 0, WF != 0, 9><<<grid, 256, lds, st>>>(g); \
+        k_gemm_narrow<NB, RS != 0, WF != 0, 9><<<grid, 256, lds, st>>>(GN_ARGS(g)); \
         break;
             QA_GN_CASE(1, 0, 0) QA_GN_CASE(1, 1, 0) QA_GN_CASE(2, 0, 0)
             QA_GN_CASE(2, 1, 0) QA_GN_CASE(4, 0, 0) QA_GN_CASE(4, 1, 0)
