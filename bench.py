@@ -80,7 +80,8 @@ def parse():
                         "(default: the committed set, when present)")
     p.add_argument("--retune", action="store_true",
                    help="time the tile variants of every convolution "
-                        "instead of using the committed set")
+                        "instead of using the committed set (alone, then "
+                        "with the batches in flight)")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the ViT-S and int16 YOLOv8n-cls passes")
     p.add_argument("--only", choices=("vit", "int16", "gemm", "kernels"),
@@ -483,6 +484,20 @@ def main():
     flight = None
     if nf > 1:
         flight, same = in_flight(c, ex, x, g.outputs[0], nf, torch)
+        if args.retune:  # the codes again, with the batches in flight
+            from quantanything_amd.executor import InFlight, tune_in_flight
+
+            # the launch slowest alone keeps its fastest code alone (the
+            # roofline kernel)
+            slowest = max(tiles, key=lambda n: tiles[n][1]) if tiles else None
+            chosen = tune_in_flight(flight.executors,
+                                    keep=() if slowest is None else (slowest,))
+            for n, code in chosen.items():
+                if n in tiles and code != tiles[n][0]:
+                    tiles[n] = (code, float("nan"), tiles[n][2])
+            ex.launch()
+            torch.cuda.synchronize()
+            flight = InFlight(flight.executors)
         if gate is not None:
             gate["in_flight_batches_equal"] = same
         if not same:

@@ -2342,3 +2342,49 @@ class InFlight:
 
     def replay(self):
         self.cuda_graph.replay()
+
+
+def tune_in_flight(executors, sweeps=2, reps=60, rounds=3, keep=()):
+    """Chooses each launch's tile code with the batches of ``executors``
+    in flight (``InFlight``; the executors of one graph and input shape,
+    planned alike): for every tunable launch in turn, every code is set on
+    all executors and the two-branch graph is captured and timed (best of
+    ``rounds`` runs of ``reps`` replays); a code replaces the current one
+    when it is at least 0.5% faster. ``sweeps`` passes over the launches;
+    launches named in ``keep`` stay as they are. With the GPU shared, bands
+    of more rows (fewer work-groups, less halo work) tend to win over the
+    fastest code of a launch timed alone. Returns ``{launch name: code}``;
+    results do not depend on the codes."""
+    import time
+
+    def setcode(i, code):
+        for e in executors:
+            e.tunables[i][1].tile = code
+
+    def rate():
+        fl = InFlight(executors)
+        for _ in range(5):
+            fl.replay()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(rounds):
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fl.replay()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        return reps / best
+
+    for _ in range(sweeps):
+        for i, (name, d, codes, _) in enumerate(executors[0].tunables):
+            if name in keep:
+                continue
+            cur = d.tile
+            res = {}
+            for code in codes:
+                setcode(i, code)
+                res[code] = rate()
+            best = max(res, key=res.get)
+            setcode(i, best if res[best] > res[cur] * 1.005 else cur)
+    return {name: d.tile for name, d, _, _ in executors[0].tunables}
