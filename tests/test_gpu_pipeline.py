@@ -385,7 +385,8 @@ def test_batches_in_flight_match_their_own_passes(hip):
     (the first one's images rolled) the first one's outputs rolled."""
     import torch
 
-    from quantanything_amd.executor import DeviceExecutor, InFlight
+    from quantanything_amd.executor import (DeviceExecutor, InFlight,
+                                            tune_in_flight)
 
     g = G.yolov8n_cls(seed=3)
     calib = [Stream(40 + i).normal((2, 3, 224, 224)).astype(np.float32)
@@ -405,6 +406,18 @@ def test_batches_in_flight_match_their_own_passes(hip):
             for k, v in ex.outputs_f32.items():
                 np.testing.assert_array_equal(v.cpu().numpy(), want[k])
         torch.zeros(1024, device="cuda").sum().item()
+    # tile choice in flight: every launch gets one of its own codes, and the
+    # results stay the same
+    keep = exs[0].tunables[0][0]
+    chosen = tune_in_flight(exs, sweeps=1, reps=2, rounds=1, keep=(keep,))
+    for name, d, codes, _ in exs[0].tunables:
+        assert chosen[name] in codes and (name != keep or chosen[name] == 0)
+    fl = InFlight(exs)
+    fl.replay()
+    torch.cuda.synchronize()
+    for ex, want in zip(exs, eager):
+        for k, v in ex.outputs_f32.items():
+            np.testing.assert_array_equal(v.cpu().numpy(), want[k])
 
 
 def test_graph_replay_matches_eager(hip):
